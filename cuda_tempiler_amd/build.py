@@ -1,0 +1,89 @@
+"""Build libtempo_gfx950.so in-tree (hipcc, gfx950 only).
+
+    python3 -m cuda_tempiler_amd.build
+
+Translation units: the two shipped deliveries' launch.hip (each instantiates its own ladder),
+the FMHA unit and the C-ABI shim.  They compile in parallel, then link into one shared object
+next to this file.  Before compiling, the shipped kernel.hip files are re-frozen from the
+plugin skeletons and the dispatch tables regenerated from select.py, so a build always ships
+what the skeletons and the ladders say.
+"""
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+OUT = os.path.join(HERE, "libtempo_gfx950.so")
+BUILD = os.path.join(HERE, "_build")
+SHIPPED = os.path.join(ROOT, "kernels", "shipped")
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+# -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 anywhere (their results are not trusted on this pool)
+FLAGS = [
+    "-O3", "-std=c++17", "--offload-arch=%s" % ARCH, "-fPIC",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wno-unused-result",
+]
+INCLUDES = [
+    "-I", os.path.join(ROOT, "include"),
+    "-I", SHIPPED,
+    "-I", os.path.join(ROOT, "kernels"),
+    "-I", os.path.join(HERE, "csrc"),
+    "-I", os.path.join(ROOT, "tempo", "plugins", "gfx950", "skeletons"),
+]
+UNITS = [
+    os.path.join(SHIPPED, "gemm_fp16", "gfx950", "launch.hip"),
+    os.path.join(SHIPPED, "gemm_w8a16", "gfx950", "launch.hip"),
+    os.path.join(HERE, "csrc", "fmha.hip"),
+    os.path.join(HERE, "csrc", "capi.hip"),
+]
+
+
+def regenerate() -> None:
+    """Freeze skeletons into the shipped kernel.hip files; regenerate dispatch.inc tables."""
+    sys.path.insert(0, ROOT)
+    from tempo.plugins.gfx950 import ship
+
+    ship.write_all()
+    for op in ("gemm_fp16", "gemm_w8a16"):
+        d = os.path.join(SHIPPED, op, "gfx950")
+        text = subprocess.run([sys.executable, os.path.join(d, "gen_dispatch.py")],
+                              check=True, capture_output=True, text=True).stdout
+        path = os.path.join(d, "dispatch.inc")
+        if not os.path.exists(path) or open(path).read() != text:
+            with open(path, "w") as f:
+                f.write(text)
+
+
+def _compile(src: str) -> str:
+    name = os.path.relpath(src, ROOT).replace(os.sep, "_").replace(".hip", ".o")
+    obj = os.path.join(BUILD, name)
+    cmd = [HIPCC] + FLAGS + INCLUDES + ["-c", src, "-o", obj]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("hipcc failed on %s:\n%s\n%s" % (src, " ".join(cmd), r.stderr[-6000:]))
+    return obj
+
+
+def build(verbose: bool = False) -> str:
+    os.makedirs(BUILD, exist_ok=True)
+    regenerate()
+    with cf.ThreadPoolExecutor(max_workers=len(UNITS)) as ex:
+        objs = list(ex.map(_compile, UNITS))
+    cmd = [HIPCC, "--offload-arch=%s" % ARCH, "-shared", "-fPIC", "-o", OUT + ".tmp"] + objs
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("link failed:\n%s" % r.stderr[-4000:])
+    os.replace(OUT + ".tmp", OUT)
+    if verbose:
+        print(OUT)
+    return OUT
+
+
+if __name__ == "__main__":
+    build(verbose=True)

@@ -1,0 +1,215 @@
+"""ctypes binding of libtempo_gfx950.so (C ABI: include/tempo_gfx950.h).
+
+This is the binding a Python host tree would add (the reference's hot path crosses into native
+code through a POD launcher, kernels/shipped/gemm_fp16/sm_70/launch.cuh:20-75; its host binding
+is a template in INTEGRATION.md:83-97).  Device memory and streams come from PyTorch-ROCm
+tensors; only raw pointers cross the boundary.
+
+There is no CPU fallback anywhere in this module: if the library is missing, lib() raises.
+"""
+from __future__ import annotations
+
+import ctypes as ct
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libtempo_gfx950.so")
+HEADER = os.path.join(os.path.dirname(HERE), "include", "tempo_gfx950.h")
+
+TEMPO_OK = 0
+TEMPO_FALLBACK = 9  # hipErrorInvalidConfiguration: "not covered, take your own path"
+W8_SYM_I8 = 1
+W8_ASYM_U8 = 2
+
+_p = ct.c_void_p
+_i = ct.c_int
+_l = ct.c_long
+
+
+class TempoGemmParams(ct.Structure):
+    _fields_ = [("A", _p), ("B", _p), ("C", _p), ("M", _i), ("N", _i), ("K", _i),
+                ("lda", _i), ("ldb", _i), ("ldc", _i)]
+
+
+class TempoW8A16Params(ct.Structure):
+    _fields_ = [("A", _p), ("Wq", _p), ("scale", _p), ("zero", _p), ("C", _p),
+                ("M", _i), ("N", _i), ("K", _i), ("lda", _i), ("ldw", _i), ("ldc", _i),
+                ("group", _i), ("fmt", _i)]
+
+
+class TempoFmhaParams(ct.Structure):
+    _fields_ = [("Q", _p), ("K", _p), ("V", _p), ("O", _p), ("LSE", _p),
+                ("B", _i), ("H", _i), ("Hkv", _i), ("Sq", _i), ("Sk", _i), ("D", _i),
+                ("scale", ct.c_float), ("causal", _i)] + [
+                   (n, _l) for n in ("q_sb", "q_ss", "q_sh", "k_sb", "k_ss", "k_sh",
+                                     "v_sb", "v_ss", "v_sh", "o_sb", "o_ss", "o_sh")]
+
+
+class TempoError(RuntimeError):
+    def __init__(self, code: int, what: str):
+        super().__init__("%s failed with hipError %d" % (what, code))
+        self.code = code
+
+
+class NotCovered(TempoError):
+    """The shipped ladder does not cover this shape: the caller takes its own path."""
+
+
+_LIB = None
+
+EXPORTS = {
+    "tempo_abi_version": ([], _i),
+    "tempo_gemm_fp16_applicable": ([ct.POINTER(TempoGemmParams)], _i),
+    "tempo_gemm_fp16_launch": ([ct.POINTER(TempoGemmParams), _p], _i),
+    "tempo_gemm_w8a16_applicable": ([ct.POINTER(TempoW8A16Params)], _i),
+    "tempo_gemm_w8a16_launch": ([ct.POINTER(TempoW8A16Params), _p], _i),
+    "tempo_dequant_tile": ([ct.POINTER(TempoW8A16Params), _i, _i, _i, _i, _p, _p], _i),
+    "tempo_fmha_fwd_applicable": ([ct.POINTER(TempoFmhaParams)], _i),
+    "tempo_fmha_fwd_launch": ([ct.POINTER(TempoFmhaParams), _p], _i),
+    "tempo_naive_gemm_fp16_launch": ([_p, _p, _p, _i, _i, _i, _p], _i),
+    "tempo_probe_mfma_layout": ([_i, _p, _p], _i),
+    "tempo_route": ([_i, _i, _i, _i, ct.c_char_p, _i], _i),
+}
+
+
+def lib():
+    """Load the library; raises if it was not built (the product path has no fallback)."""
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                "libtempo_gfx950.so is not built (%s); run `python3 -m cuda_tempiler_amd.build`"
+                % LIB_PATH)
+        L = ct.CDLL(LIB_PATH)
+        for name, (args, res) in EXPORTS.items():
+            f = getattr(L, name)
+            f.argtypes = args
+            f.restype = res
+        _LIB = L
+    return _LIB
+
+
+def _check(rc: int, what: str) -> None:
+    if rc == TEMPO_FALLBACK:
+        raise NotCovered(rc, what)
+    if rc != TEMPO_OK:
+        raise TempoError(rc, what)
+
+
+def _stream(stream):
+    if stream is None:
+        import torch
+
+        return _p(torch.cuda.current_stream().cuda_stream)
+    if isinstance(stream, int):
+        return _p(stream)
+    return _p(stream.cuda_stream)
+
+
+def route(op: int, M: int, N: int, K: int) -> str:
+    """Host-only: ladder row the shipped dispatcher picks ('' = not covered)."""
+    buf = ct.create_string_buffer(64)
+    lib().tempo_route(op, M, N, K, buf, 64)
+    return buf.value.decode()
+
+
+# ---- torch-facing helpers (torch is plumbing: device memory and streams) ------------------
+def _ptr(t):
+    return _p(t.data_ptr()) if t is not None else None
+
+
+def gemm_fp16(A, B, C=None, stream=None):
+    """C[M,N] = A[M,K] . B[N,K]^T on the shipped gfx950 ladder.  Raises NotCovered."""
+    import torch
+
+    M, K = A.shape
+    N = B.shape[0]
+    if C is None:
+        C = torch.empty((M, N), dtype=torch.float16, device=A.device)
+    p = TempoGemmParams(_ptr(A), _ptr(B), _ptr(C), M, N, K, A.stride(0), B.stride(0), C.stride(0))
+    _check(lib().tempo_gemm_fp16_launch(p, _stream(stream)),
+           "tempo_gemm_fp16_launch")
+    return C
+
+
+def w8a16_params(A, Wq, scale, zero, C, fmt: int, group: int = 128) -> TempoW8A16Params:
+    M, K = A.shape
+    N = Wq.shape[0]
+    return TempoW8A16Params(_ptr(A), _ptr(Wq), _ptr(scale), _ptr(zero), _ptr(C), M, N, K,
+                            A.stride(0), Wq.stride(0), C.stride(0) if C is not None else N,
+                            group if fmt == W8_ASYM_U8 else 0, fmt)
+
+
+def gemm_w8a16(A, Wq, scale, zero=None, fmt: int = W8_SYM_I8, group: int = 128, C=None,
+               stream=None):
+    import torch
+
+    M = A.shape[0]
+    N = Wq.shape[0]
+    if C is None:
+        C = torch.empty((M, N), dtype=torch.float16, device=A.device)
+    p = w8a16_params(A, Wq, scale, zero, C, fmt, group)
+    _check(lib().tempo_gemm_w8a16_launch(p, _stream(stream)), "tempo_gemm_w8a16_launch")
+    return C
+
+
+def dequant_tile(Wq, scale, zero, fmt, n0, k0, rows, cols, group=128, stream=None):
+    import torch
+
+    N, K = Wq.shape
+    dummyA = torch.empty((1, K), dtype=torch.float16, device=Wq.device)
+    out = torch.empty((rows, cols), dtype=torch.float16, device=Wq.device)
+    p = w8a16_params(dummyA, Wq, scale, zero, out, fmt, group)
+    p.C = _ptr(out)
+    p.ldc = max(N, 8)
+    _check(lib().tempo_dequant_tile(p, n0, k0, rows, cols, _ptr(out), _stream(stream)),
+           "tempo_dequant_tile")
+    return out
+
+
+def fmha_params(Q, K, V, O, LSE, scale: float, causal: bool = True) -> TempoFmhaParams:
+    """Q/O [B,Sq,H,D], K/V [B,Sk,Hkv,D] tensors (any strides with d contiguous)."""
+    B, Sq, H, D = Q.shape
+    _, Sk, Hkv, _ = K.shape
+    return TempoFmhaParams(
+        _ptr(Q), _ptr(K), _ptr(V), _ptr(O), _ptr(LSE), B, H, Hkv, Sq, Sk, D, float(scale),
+        int(bool(causal)),
+        Q.stride(0), Q.stride(1), Q.stride(2), K.stride(0), K.stride(1), K.stride(2),
+        V.stride(0), V.stride(1), V.stride(2), O.stride(0), O.stride(1), O.stride(2))
+
+
+def fmha_fwd(Q, K, V, scale: float, causal: bool = True, O=None, LSE=None, stream=None):
+    import torch
+
+    B, Sq, H, D = Q.shape
+    if O is None:
+        O = torch.empty_like(Q)
+    if LSE is None:
+        LSE = torch.empty((B, H, Sq), dtype=torch.float32, device=Q.device)
+    p = fmha_params(Q, K, V, O, LSE, scale, causal)
+    _check(lib().tempo_fmha_fwd_launch(p, _stream(stream)), "tempo_fmha_fwd_launch")
+    return O, LSE
+
+
+def naive_gemm_fp16(A, B, C=None, stream=None):
+    import torch
+
+    M, K = A.shape
+    N = B.shape[0]
+    if C is None:
+        C = torch.empty((M, N), dtype=torch.float16, device=A.device)
+    _check(lib().tempo_naive_gemm_fp16_launch(_ptr(A), _ptr(B), _ptr(C), M, N, K,
+                                               _stream(stream)), "tempo_naive_gemm_fp16_launch")
+    return C
+
+
+def probe_mfma_layout(ms: int, device="cuda"):
+    """Returns (rows, cols) int arrays [64][nacc] of the MFMA result map, measured on the GPU."""
+    import torch
+
+    nacc = 16 if ms == 32 else 4
+    out = torch.zeros((2, 64, nacc), dtype=torch.float32, device=device)
+    _check(lib().tempo_probe_mfma_layout(ms, _ptr(out), _stream(None)), "tempo_probe_mfma_layout")
+    torch.cuda.synchronize()
+    o = out.cpu().numpy()
+    return o[0].astype(int) - 1, o[1].astype(int) - 1

@@ -1,0 +1,163 @@
+// capi.hip -- extern "C" boundary of libtempo_gfx950.so (declarations: include/tempo_gfx950.h).
+//
+// Thin by design: it converts the C structs into the shipped deliveries' POD parameters and
+// calls their launch(); every kernel decision lives in the deliveries (kernels/shipped/...) and
+// the FMHA skeleton.  No framework type crosses this file.
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+
+#include "tempo_gfx950.h"
+#include "gemm_fp16/gfx950/launch.h"
+#include "gemm_w8a16/gfx950/launch.h"
+#include "naive/gemm_fp16.hip"
+#include "fmha_api.h"
+
+namespace {
+
+using tempo::gen::Mfma;
+using tempo::gen::f16x8;
+
+template <int MS>
+__global__ void k_probe_layout(float* out) {
+  const int l = threadIdx.x;
+  constexpr int NACC = Mfma<MS>::NACC;
+  for (int pass = 0; pass < 2; ++pass) {
+    typename Mfma<MS>::acc_t acc;
+    for (int v = 0; v < NACC; ++v) acc[v] = 0.f;
+    f16x8 a, b;
+    for (int e = 0; e < 8; ++e) {
+      a[e] = (_Float16)0.f;
+      b[e] = (_Float16)0.f;
+    }
+    if (l / MS == 0) {  // one k slot (k-group 0, element 0) carries a rank-1 product
+      a[0] = (_Float16)(pass == 0 ? (float)(l % MS + 1) : 1.f);
+      b[0] = (_Float16)(pass == 0 ? 1.f : (float)(l % MS + 1));
+    }
+    acc = Mfma<MS>::run(a, b, acc);
+    for (int v = 0; v < NACC; ++v) out[(pass * 64 + l) * NACC + v] = acc[v];
+  }
+}
+
+tempo::gen::GemmParams to_pod(const TempoGemmParams* p) {
+  tempo::gen::GemmParams g;
+  g.A = static_cast<const _Float16*>(p->A);
+  g.B = static_cast<const _Float16*>(p->B);
+  g.C = static_cast<_Float16*>(p->C);
+  g.M = p->M;
+  g.N = p->N;
+  g.K = p->K;
+  g.lda = p->lda;
+  g.ldb = p->ldb;
+  g.ldc = p->ldc;
+  return g;
+}
+
+tempo::gen8::W8A16Params to_pod(const TempoW8A16Params* p) {
+  tempo::gen8::W8A16Params g;
+  g.A = static_cast<const _Float16*>(p->A);
+  g.Wq = p->Wq;
+  g.scale = static_cast<const _Float16*>(p->scale);
+  g.zero = static_cast<const uint8_t*>(p->zero);
+  g.C = static_cast<_Float16*>(p->C);
+  g.M = p->M;
+  g.N = p->N;
+  g.K = p->K;
+  g.lda = p->lda;
+  g.ldw = p->ldw;
+  g.ldc = p->ldc;
+  g.group = p->group;
+  g.fmt = p->fmt;
+  return g;
+}
+
+int copy_tag(const char* t, char* tag, int tag_len) {
+  if (tag && tag_len > 0) {
+    const char* s = t ? t : "";
+    std::strncpy(tag, s, (size_t)tag_len - 1);
+    tag[tag_len - 1] = '\0';
+  }
+  return t ? 1 : 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tempo_abi_version(void) { return 1; }
+
+int tempo_gemm_fp16_applicable(const TempoGemmParams* p) {
+  if (!p) return 0;
+  return tempo::gen::route(to_pod(p)) != nullptr;
+}
+
+int tempo_gemm_fp16_launch(const TempoGemmParams* p, tempo_stream_t stream) {
+  if (!p) return (int)hipErrorInvalidValue;
+  return (int)tempo::gen::launch(to_pod(p), static_cast<hipStream_t>(stream));
+}
+
+int tempo_gemm_w8a16_applicable(const TempoW8A16Params* p) {
+  if (!p) return 0;
+  return tempo::gen8::route(to_pod(p)) != nullptr;
+}
+
+int tempo_gemm_w8a16_launch(const TempoW8A16Params* p, tempo_stream_t stream) {
+  if (!p) return (int)hipErrorInvalidValue;
+  return (int)tempo::gen8::launch(to_pod(p), static_cast<hipStream_t>(stream));
+}
+
+int tempo_dequant_tile(const TempoW8A16Params* p, int n0, int k0, int rows, int cols, void* out,
+                       tempo_stream_t stream) {
+  if (!p || !out) return (int)hipErrorInvalidValue;
+  return (int)tempo::gen8::dequant_tile(to_pod(p), n0, k0, rows, cols,
+                                        static_cast<_Float16*>(out),
+                                        static_cast<hipStream_t>(stream));
+}
+
+int tempo_fmha_fwd_applicable(const TempoFmhaParams* p) {
+  if (!p) return 0;
+  return tempo_fmha::applicable(*p) ? 1 : 0;
+}
+
+int tempo_fmha_fwd_launch(const TempoFmhaParams* p, tempo_stream_t stream) {
+  if (!p) return (int)hipErrorInvalidValue;
+  return (int)tempo_fmha::launch(*p, static_cast<hipStream_t>(stream));
+}
+
+int tempo_naive_gemm_fp16_launch(const void* A, const void* B, void* C, int M, int N, int K,
+                                 tempo_stream_t stream) {
+  if (!A || !B || !C || M <= 0 || N <= 0 || K <= 0) return (int)hipErrorInvalidValue;
+  return (int)naive_gemm_fp16_launch(static_cast<const _Float16*>(A),
+                                     static_cast<const _Float16*>(B), static_cast<_Float16*>(C),
+                                     M, N, K, static_cast<hipStream_t>(stream));
+}
+
+int tempo_probe_mfma_layout(int ms, float* out, tempo_stream_t stream) {
+  if (!out) return (int)hipErrorInvalidValue;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (ms == 32)
+    hipLaunchKernelGGL(k_probe_layout<32>, dim3(1), dim3(64), 0, s, out);
+  else if (ms == 16)
+    hipLaunchKernelGGL(k_probe_layout<16>, dim3(1), dim3(64), 0, s, out);
+  else
+    return (int)hipErrorInvalidValue;
+  return (int)hipGetLastError();
+}
+
+int tempo_route(int op, int M, int N, int K, char* tag, int tag_len) {
+  // Host-only: dummy 16-byte-aligned addresses stand in for device pointers (never touched).
+  const uintptr_t fake = 0x1000;
+  if (op == 0) {
+    TempoGemmParams p = {(const void*)fake, (const void*)fake, (void*)fake, M, N, K, K, K, N};
+    return copy_tag(tempo::gen::route(to_pod(&p)), tag, tag_len);
+  }
+  if (op == 1 || op == 2) {
+    TempoW8A16Params p = {(const void*)fake, (const void*)fake, (const void*)fake,
+                          op == 2 ? (const void*)fake : nullptr, (void*)fake, M, N, K, K, K, N,
+                          op == 2 ? 128 : 0, op};
+    return copy_tag(tempo::gen8::route(to_pod(&p)), tag, tag_len);
+  }
+  return copy_tag(nullptr, tag, tag_len);
+}
+
+}  // extern "C"

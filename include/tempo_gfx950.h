@@ -1,0 +1,142 @@
+/*
+ * tempo_gfx950.h -- C ABI of the MI355X (gfx950) kernels behind the Tempolator plugin
+ * `tempo/plugins/gfx950` and the shipped deliveries kernels/shipped/{gemm_fp16,gemm_w8a16}/gfx950.
+ *
+ * Library: cuda_tempiler_amd/libtempo_gfx950.so (built by cuda_tempiler_amd/build.py).
+ *
+ * Conventions (all entry points):
+ *   - plain pointers and sizes; no framework types.  Device pointers are HIP device memory.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the null stream).  Every launch is
+ *     asynchronous on that stream and never synchronises; the caller owns every buffer.
+ *   - the int returned is a hipError_t value: 0 = success; TEMPO_FALLBACK (9, the value of
+ *     hipErrorInvalidConfiguration) = "shape not covered, take your own path" -- a legal
+ *     answer, not a failure (reference kernels/shipped/gemm_fp16/sm_70/dispatch.inc:12-13,26).
+ *     Other values propagate from the HIP runtime.
+ *   - fp16 data is IEEE binary16; results round to nearest even.
+ */
+#ifndef TEMPO_GFX950_H
+#define TEMPO_GFX950_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* tempo_stream_t;
+
+#define TEMPO_OK 0
+#define TEMPO_FALLBACK 9
+
+/* ------------------------------------------------------------------------------------------
+ * gemm_fp16:  C[M][N] = fp16_rn( sum_k A[m][k] * B[n][k] ), fp32 accumulation.
+ * Replaces the reference's shipped launcher tempo::gen::GemmParams / applicable() / launch()
+ * (kernels/shipped/gemm_fp16/sm_70/launch.cuh:20-26, :59-67, :75; launch.cu:20-22).  Same
+ * fields, same meaning (strides in elements, k contiguous).
+ * ------------------------------------------------------------------------------------------ */
+typedef struct TempoGemmParams {
+  const void* A; /* fp16 [M][lda] */
+  const void* B; /* fp16 [N][ldb] */
+  void* C;       /* fp16 [M][ldc] */
+  int M, N, K;
+  int lda, ldb, ldc;
+} TempoGemmParams;
+
+/* 1 = covered (launch will run a kernel), 0 = not covered (caller takes its own path).
+ * Reference: launch.cuh:59-67 applicable() plus the ladder coverage of dispatch.inc. */
+int tempo_gemm_fp16_applicable(const TempoGemmParams* p);
+/* Reference: launch.cu:20-22 tempo::gen::launch(const GemmParams&, cudaStream_t). */
+int tempo_gemm_fp16_launch(const TempoGemmParams* p, tempo_stream_t stream);
+
+/* ------------------------------------------------------------------------------------------
+ * gemm_w8a16:  C = fp16_rn( A . deq(Wq)^T ), fp32 accumulation, weights dequantised in
+ * registers bit-exactly:
+ *   fmt 1 (TEMPO_W8_SYM_I8):   Wq int8  [N][ldw], scale fp16 [N]          W = fp16_rn(q * s[n])
+ *   fmt 2 (TEMPO_W8_ASYM_U8):  Wq uint8 [N][ldw], scale fp16 [N][K/group], zero uint8 [N][K/group]
+ *                              W = fp16_rn((q - z[n][k/group]) * s[n][k/group])
+ * Replaces the reference's W8A16 skeleton launch (tempo/plugins/sm70/skeletons/gemm_w8a16/
+ * harness.cu:88-94, k_gemm8 in kernel.cuh:226-296), which is symmetric and scale-free; the
+ * scaled formats extend it as declared in the north star (GPTQ formula of
+ * bench/gemm_baseline.py:229, stored [N][K]).
+ * ------------------------------------------------------------------------------------------ */
+#define TEMPO_W8_SYM_I8 1
+#define TEMPO_W8_ASYM_U8 2
+
+typedef struct TempoW8A16Params {
+  const void* A;     /* fp16 [M][lda] */
+  const void* Wq;    /* int8 or uint8 [N][ldw] */
+  const void* scale; /* fp16, [N] (fmt 1) or [N][K/group] (fmt 2) */
+  const void* zero;  /* NULL (fmt 1) or uint8 [N][K/group] (fmt 2) */
+  void* C;           /* fp16 [M][ldc] */
+  int M, N, K;
+  int lda, ldw, ldc;
+  int group; /* fmt 2: k per scale group (multiple of 64, divides K); fmt 1: ignored */
+  int fmt;
+} TempoW8A16Params;
+
+int tempo_gemm_w8a16_applicable(const TempoW8A16Params* p);
+int tempo_gemm_w8a16_launch(const TempoW8A16Params* p, tempo_stream_t stream);
+
+/* Debug/verification: dequantise rows [n0, n0+rows) x cols [k0, k0+cols) of Wq into fp16
+ * out[rows][cols] with the same device functions the GEMM feeds use (cols % 8 == 0, k0 % 8 == 0).
+ * No reference counterpart: the reference's skeleton has no scale, so its dequantisation is the
+ * identity (harness.cu:39-46); this entry is what makes "bit-exact dequant" testable. */
+int tempo_dequant_tile(const TempoW8A16Params* p, int n0, int k0, int rows, int cols, void* out,
+                       tempo_stream_t stream);
+
+/* ------------------------------------------------------------------------------------------
+ * fmha_fwd: O = softmax(scale * Q K^T + causal mask) V, fp32 softmax, fp16 O, fp32 LSE
+ * (natural log).  GQA: query head h reads KV head h / (H / Hkv).  Causal mask is bottom-right:
+ * row i sees keys j <= i + (Sk - Sq).  Strides in elements; Q/O addressed as
+ * b*sb + i*ss + h*sh + d, K/V likewise with the KV head.  LSE may be NULL, else [B][H][Sq].
+ * Replaces the forward signature of the reference's profiled FMHA (profiled/fwd_ws/fa2_sm70/
+ * csrc/volta_fwd_ws.cuh:276-283; attn_fwd_cutlass.cu:137,193,660-666).  The reference ships no
+ * FMHA skeleton (tempo/plugins/sm70/__init__.py:57).
+ * ------------------------------------------------------------------------------------------ */
+typedef struct TempoFmhaParams {
+  const void* Q;
+  const void* K;
+  const void* V;
+  void* O;
+  float* LSE;
+  int B, H, Hkv, Sq, Sk, D;
+  float scale;
+  int causal;
+  long q_sb, q_ss, q_sh;
+  long k_sb, k_ss, k_sh;
+  long v_sb, v_ss, v_sh;
+  long o_sb, o_ss, o_sh;
+} TempoFmhaParams;
+
+int tempo_fmha_fwd_applicable(const TempoFmhaParams* p);
+int tempo_fmha_fwd_launch(const TempoFmhaParams* p, tempo_stream_t stream);
+
+/* ------------------------------------------------------------------------------------------
+ * The naive input kernel (kernels/naive/gemm_fp16.hip): one thread per output, sequential k.
+ * The "vs input" bar; reference kernels/naive/gemm_fp16.cu:60-76.
+ * ------------------------------------------------------------------------------------------ */
+int tempo_naive_gemm_fp16_launch(const void* A, const void* B, void* C, int M, int N, int K,
+                                 tempo_stream_t stream);
+
+/* ------------------------------------------------------------------------------------------
+ * Plugin support (no reference counterpart in the C ABI; the sm70 plugin does these checks
+ * from Python, tempo/plugins/sm70/tensor.py:72-86).
+ * ------------------------------------------------------------------------------------------ */
+/* MFMA result-layout probe: runs one MFMA of shape ms (32 or 16) with rank-1 operands that encode
+ * row and column indices, writing out[2][64][nacc] floats (row+1, then col+1, per lane and
+ * result register).  nacc = 16 for ms 32, 4 for ms 16.  `out` is device memory. */
+int tempo_probe_mfma_layout(int ms, float* out, tempo_stream_t stream);
+
+/* Name of the shipped ladder row a shape dispatches to ("" when not covered).  op 0 = gemm_fp16,
+ * op 1 = gemm_w8a16 (fmt 1), op 2 = gemm_w8a16 (fmt 2).  Host-only; no GPU needed. */
+int tempo_route(int op, int M, int N, int K, char* tag, int tag_len);
+
+/* ABI version of this header (bumped on any struct change). */
+int tempo_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TEMPO_GFX950_H */

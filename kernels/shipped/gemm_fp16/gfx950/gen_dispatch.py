@@ -1,0 +1,69 @@
+#!/usr/bin/env python3
+"""Generates dispatch.inc from select.py: one source of the ladder, two consumers.
+
+    python3 gen_dispatch.py > dispatch.inc
+
+The Python predicate is what a host tree calls once at load time; the instantiation table is
+what the compiler needs.  The second is generated from the first so they cannot drift
+(reference: kernels/shipped/gemm_fp16/sm_70/gen_dispatch.py:6-13).
+"""
+from __future__ import annotations
+
+import importlib.util
+import os
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+def _select():
+    spec = importlib.util.spec_from_file_location("tempo_select_fp16_gfx950",
+                                                  os.path.join(HERE, "select.py"))
+    m = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(m)
+    return m
+
+
+HEAD = """// GENERATED from select.py -- do not edit.  Regenerate with:
+//   python3 kernels/shipped/gemm_fp16/gfx950/gen_dispatch.py > dispatch.inc
+//
+// M-band ladder, one TEMPO_ROW(band, fit, launcher, tag) per row; launch.hip expands it twice
+// (launch and route).  First band that holds M decides; if its kernel does not fit the shape,
+// or no band holds M, the answer is hipErrorInvalidConfiguration: the caller's own path takes
+// over (TEMPO_FALLBACK) -- a legal answer, not a failure.
+"""
+
+
+def instantiation(kind, p):
+    if kind == "stream":
+        return "launch_stream<%d,%d,%d>" % (p["MB"], p["R"], p["U"])
+    return "launch_mfma<%d,%d,%d,%d,%d,%d,%d,%d,%d>" % (
+        p["BM"], p["BN"], p["BK"], p["WM"], p["WN"], p["MS"], p["SWZ"], p["GROUP"], p["XCD"])
+
+
+def condition(sel, kind, p, m_max):
+    if kind == "stream":
+        fit = "(p.N %% %d) == 0 && (p.K %% %d) == 0" % (sel.STREAM_N_ROWS * p["R"],
+                                                          sel.STREAM_K_STEP)
+    else:
+        fit = "(p.N %% %d) == 0 && (p.K %% %d) == 0" % (p["BN"], p["BK"])
+    return "p.M <= %d" % m_max, fit
+
+
+def render() -> str:
+    sel = _select()
+    out = [HEAD]
+    for m_max, tag, kind, p in sel.LADDER:
+        band, fit = condition(sel, kind, p, m_max)
+        out.append("TEMPO_ROW(%s, %s,\n          (%s), \"%s\")" % (band, fit, instantiation(kind, p), tag))
+    out.append("TEMPO_FALLBACK_ROW")
+    return "\n".join(out) + "\n"
+
+
+def main():
+    sys.stdout.write(render())
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,143 @@
+// launch.h -- kernel/framework boundary of the shipped gemm_w8a16 for gfx950.
+//
+// POD + pointers only (same discipline as the reference's kernels/shipped/gemm_fp16/sm_70/
+// launch.cuh:5-8).  C = fp16_rn(A . deq(Wq)^T) with fp32 accumulation; the weights are
+// dequantised in registers, bit-exactly:
+//   fmt 1: Wq int8 [N][ldw], scale fp16 [N]                  W = fp16_rn(q * s[n])
+//   fmt 2: Wq uint8 [N][ldw], scale fp16 [N][K/group], zero uint8 [N][K/group]
+//          W = fp16_rn((q - z) * s)
+// Asynchronous on the given stream, never synchronises, caller owns every buffer.  Not covered
+// -> hipErrorInvalidConfiguration (take your own path).  The only state is the split-K
+// workspace of the streaming kernel (one per device, allocated on first need, kept); calls that
+// overlap on one device must not both take the split-K route.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "kernel.hip"
+
+namespace tempo {
+namespace gen8 {
+
+struct W8A16Params {
+  const _Float16* A;      // [M][lda]
+  const void* Wq;         // int8 / uint8 [N][ldw]
+  const _Float16* scale;  // [N] or [N][K/group]
+  const uint8_t* zero;    // nullptr or [N][K/group]
+  _Float16* C;            // [M][ldc]
+  int M, N, K;
+  int lda, ldw, ldc;
+  int group;
+  int fmt;  // 1 int8 symmetric per-channel, 2 uint8 asymmetric group-wise
+};
+
+constexpr size_t kWsPartialBytes = size_t(32) << 20;
+constexpr size_t kWsCounterCount = size_t(1) << 16;
+hipError_t workspace(float** partials, unsigned** counters);  // defined in launch.hip
+
+inline void stream_split(int M, int N, int K, int R, int U, int* S_out, int* chunk_out) {
+  const int slabs = N / (16 * R);
+  const int step = 64 * U;
+  int S = (2048 + slabs - 1) / slabs;
+  const int smax_k = K / 256 > 0 ? K / 256 : 1;
+  if (S > smax_k) S = smax_k;
+  if (S < 1) S = 1;
+  while (S > 1 && (size_t)S * M * N * 4 > kWsPartialBytes) --S;
+  int chunk = (K + S - 1) / S;
+  chunk = (chunk + step - 1) / step * step;
+  S = (K + chunk - 1) / chunk;
+  *S_out = S;
+  *chunk_out = chunk;
+}
+
+inline StreamArgs stream_args(const W8A16Params& p) {
+  StreamArgs a;
+  a.A = p.A;
+  a.B = p.Wq;
+  a.scale = p.scale;
+  a.zero = p.zero;
+  a.C = p.C;
+  a.ws = nullptr;
+  a.counters = nullptr;
+  a.M = p.M;
+  a.N = p.N;
+  a.K = p.K;
+  a.lda = p.lda;
+  a.ldb = p.ldw;
+  a.ldc = p.ldc;
+  a.S = 1;
+  a.chunk = p.K;
+  a.group = p.fmt == 2 ? p.group : 0;
+  return a;
+}
+
+template <int MB, int R, int U>
+inline hipError_t launch_stream(const W8A16Params& p, hipStream_t s) {
+  StreamArgs a = stream_args(p);
+  stream_split(p.M, p.N, p.K, R, U, &a.S, &a.chunk);
+  if (a.S > 1) {
+    if ((size_t)(p.N / (16 * R)) > kWsCounterCount) return hipErrorInvalidConfiguration;
+    const hipError_t e = workspace(&a.ws, &a.counters);
+    if (e != hipSuccess) return e;
+  }
+  const int units = (p.N / (16 * R)) * a.S;
+  const dim3 grid((units + 3) / 4), blk(256);
+  if (p.fmt == 1)
+    hipLaunchKernelGGL((k_stream<MB, R, U, 1>), grid, blk, 0, s, a);
+  else
+    hipLaunchKernelGGL((k_stream<MB, R, U, 2>), grid, blk, 0, s, a);
+  return hipGetLastError();
+}
+
+template <int BM, int BN, int BK, int WM, int WN, int MS, int SWZ, int GROUP, int XCD>
+inline hipError_t launch_mfma(const W8A16Params& p, hipStream_t s) {
+  const int nm = (p.M + BM - 1) / BM;
+  const int nn = p.N / BN;
+  const dim3 grid(nm * nn), blk(WM * WN * 64);
+  if (p.fmt == 1)
+    hipLaunchKernelGGL((k_gemm<BM, BN, BK, WM, WN, MS, SWZ, GROUP, XCD, 1>), grid, blk, 0, s,
+                       p.A, p.Wq, p.scale, p.zero, p.C, p.M, p.N, p.K, p.lda, p.ldw, p.ldc, 0);
+  else
+    hipLaunchKernelGGL((k_gemm<BM, BN, BK, WM, WN, MS, SWZ, GROUP, XCD, 2>), grid, blk, 0, s,
+                       p.A, p.Wq, p.scale, p.zero, p.C, p.M, p.N, p.K, p.lda, p.ldw, p.ldc,
+                       p.group);
+  return hipGetLastError();
+}
+
+inline bool applicable(const W8A16Params& p) {
+  if (p.M <= 0 || p.N <= 0 || p.K <= 0) return false;
+  if (p.fmt != 1 && p.fmt != 2) return false;
+  if (!p.A || !p.Wq || !p.scale || !p.C) return false;
+  if (p.fmt == 2 && (!p.zero || p.group <= 0 || (p.group % 64) != 0 || (p.K % p.group) != 0))
+    return false;
+  if (p.lda < p.K || p.ldw < p.K || p.ldc < p.N) return false;
+  if ((p.K % 8) != 0 || (p.N % 8) != 0) return false;
+  if ((p.lda % 8) != 0 || (p.ldw % 16) != 0 || (p.ldc % 4) != 0) return false;
+  if ((reinterpret_cast<uintptr_t>(p.A) % 16) != 0) return false;
+  if ((reinterpret_cast<uintptr_t>(p.Wq) % 16) != 0) return false;
+  if ((reinterpret_cast<uintptr_t>(p.C) % 8) != 0) return false;
+  return true;
+}
+
+hipError_t launch(const W8A16Params& p, hipStream_t s);
+const char* route(const W8A16Params& p);
+
+// Dequantise a [rows][cols] tile of the weights with the GEMM feeds' own device functions.
+inline hipError_t dequant_tile(const W8A16Params& p, int n0, int k0, int rows, int cols,
+                               _Float16* out, hipStream_t s) {
+  if (!applicable(p) || rows <= 0 || cols <= 0 || (cols % 8) != 0 || (k0 % 8) != 0 || n0 < 0 ||
+      k0 < 0 || n0 + rows > p.N || k0 + cols > p.K)
+    return hipErrorInvalidValue;
+  const StreamArgs a = stream_args(p);
+  const int work = rows * (cols / 8);
+  const dim3 grid((work + 255) / 256), blk(256);
+  if (p.fmt == 1)
+    hipLaunchKernelGGL((k_dequant_tile<1>), grid, blk, 0, s, a, n0, k0, rows, cols, out);
+  else
+    hipLaunchKernelGGL((k_dequant_tile<2>), grid, blk, 0, s, a, n0, k0, rows, cols, out);
+  return hipGetLastError();
+}
+
+}  // namespace gen8
+}  // namespace tempo

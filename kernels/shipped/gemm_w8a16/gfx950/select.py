@@ -1,0 +1,48 @@
+"""Shipped dispatcher for gemm_w8a16 on gfx950: (op, M, N, K, fmt, group) -> kernel id or None.
+
+Same contract as kernels/shipped/gemm_fp16/gfx950/select.py (reference pattern:
+kernels/shipped/gemm_fp16/sm_70/select.py:23-58).  The weight formats:
+  fmt 1  int8 symmetric, fp16 scale per output channel
+  fmt 2  uint8 asymmetric, fp16 scale + uint8 zero-point per (row, group of `group` k)
+Every row of the ladder is instantiated for both formats; dispatch.inc is generated from this
+file by gen_dispatch.py.
+"""
+
+ARCH = "gfx950"
+FORMATS = (1, 2)
+
+# (M_max, tag, kind, template params).  First band that holds M decides.
+LADDER = [
+    (16, "s16r1u4", "stream", dict(MB=1, R=1, U=4)),
+    (32, "s32r1u4", "stream", dict(MB=2, R=1, U=4)),
+    (256, "m128x128k64", "mfma",
+     dict(BM=128, BN=128, BK=64, WM=2, WN=2, MS=32, SWZ=1, GROUP=8, XCD=1)),
+    (1 << 30, "m256x256k64", "mfma",
+     dict(BM=256, BN=256, BK=64, WM=2, WN=2, MS=32, SWZ=1, GROUP=8, XCD=1)),
+]
+
+STREAM_K_STEP = 64
+STREAM_N_ROWS = 16
+
+
+def _fits(kind, p, M, N, K):
+    if kind == "stream":
+        return N % (STREAM_N_ROWS * p["R"]) == 0 and K % STREAM_K_STEP == 0
+    return N % p["BN"] == 0 and K % p["BK"] == 0
+
+
+def select(op, M, N, K, fmt=1, group=128, dtype_a="fp16", dtype_c="fp16", arch=ARCH):
+    if op != "gemm_w8a16" or arch != ARCH:
+        return None
+    if (dtype_a, dtype_c) != ("fp16", "fp16") or fmt not in FORMATS:
+        return None
+    if M <= 0 or N <= 0 or K <= 0 or N % 8 or K % 8:
+        return None
+    if fmt == 2 and (group <= 0 or group % 64 or K % group):
+        return None
+    for m_max, tag, kind, p in LADDER:
+        if M <= m_max:
+            if not _fits(kind, p, M, N, K):
+                return None
+            return dict(tag=tag, kind=kind, fmt=fmt, **p)
+    return None

@@ -1,0 +1,245 @@
+// gemm_mfma -- tiled C[M,N] = A[M,K] . B[N,K]^T on CDNA4 matrix cores (gfx950).
+//
+// Semantics follow the reference's naive kernel (kernels/naive/gemm_fp16.cu:60-68): fp16
+// operands, fp32 accumulation, one RNE rounding to fp16 per output.  The order of the k
+// summation differs (MFMA dot products), which is why parity is a relL2 gate, not bit equality.
+//
+// Template axes (the plugin's search space, tempo/plugins/gfx950/space.py):
+//   BM, BN   macro tile of C per workgroup
+//   BK       k extent of one LDS stage (the LDS holds two stages: double buffer)
+//   WM, WN   waves along M and N (workgroup = WM*WN*64 lanes); wave tile (BM/WM) x (BN/WN)
+//   MS       MFMA shape: 32 -> v_mfma_f32_32x32x16_f16, 16 -> v_mfma_f32_16x16x32_f16
+//   SWZ      LDS chunk swizzle: 0 none, 1 chunk ^ (row % CPR), 2 chunk ^ ((row/2) % CPR)
+//   GROUP    raster group height in tiles (L2 reuse); 0 = row-major tile order
+//   XCD      1 = remap block ids so each of the 8 XCDs owns a contiguous run of tiles
+//   BFMT     B operand format: 0 fp16, 1 int8 + per-row fp16 scale, 2 uint8 + per-(row,group)
+//            fp16 scale and uint8 zero-point.  Formats 1 and 2 dequantise while staging the
+//            B tile into LDS (once per workgroup, not once per wave), bit-exact with the
+//            closed forms in cdna4.h.
+//
+// Layout in registers: the MFMA "A" operand is fed from B rows (n) and the "B" operand from A
+// rows (m), so each lane's result values are 4 consecutive n of one m -- the epilogue writes
+// 8-byte runs of C instead of 2-byte scatters.
+//
+// LDS layout: per stage, A tile [BM][BK] and B tile [BN][BK] fp16, k contiguous, 16-byte chunks
+// swizzled by row so the 16-byte MFMA feed reads (one row per lane) spread over the banks.
+//
+// Requirements checked by the launcher (applicable()): N % BN == 0, K % BK == 0, 16-byte
+// aligned rows; M is predicated (rows past M are loaded from row M-1 and never stored).
+
+template <int BK, int SWZ>
+__device__ __forceinline__ int lds_chunk(int row, int chunk) {
+  constexpr int CPR = BK / 8;  // 16-byte chunks per row
+  if constexpr (SWZ == 1) return chunk ^ (row & (CPR - 1));
+  else if constexpr (SWZ == 2) return chunk ^ ((row >> 1) & (CPR - 1));
+  else return chunk;
+}
+
+// Tile order: block id -> (tile_m, tile_n).
+template <int GROUP, int XCD>
+__device__ __forceinline__ void tile_of(int bid, int nm, int nn, int& tm, int& tn) {
+  const int total = nm * nn;
+  if constexpr (XCD) {
+    // Workgroups are handed to the 8 XCDs round-robin (bid % 8).  Give XCD x the contiguous
+    // run [x*total/8, (x+1)*total/8) of the tile order so its concurrent tiles share panels in
+    // that XCD's own L2.
+    if ((total & 7) == 0) bid = (bid & 7) * (total >> 3) + (bid >> 3);
+  }
+  if constexpr (GROUP > 0) {
+    const int per = GROUP * nn;
+    const int g = bid / per;
+    const int first = g * GROUP;
+    const int gs = min(GROUP, nm - first);
+    const int r = bid - g * per;
+    tm = first + r % gs;
+    tn = r / gs;
+  } else {
+    tm = bid / nn;
+    tn = bid - tm * nn;
+  }
+}
+
+template <int BM, int BN, int BK, int WM, int WN, int MS, int SWZ, int GROUP, int XCD, int BFMT>
+struct GemmCfg {
+  static constexpr int THREADS = WM * WN * 64;
+  static constexpr int CPR = BK / 8;
+  static constexpr int WTM = BM / WM;  // wave tile rows (m)
+  static constexpr int WTN = BN / WN;  // wave tile cols (n)
+  static constexpr int TM = WTM / MS;  // MFMA blocks per wave along m
+  static constexpr int TN = WTN / MS;
+  static constexpr int KS = BK / Mfma<MS>::KSTEP;  // MFMA k-steps per stage
+  static constexpr int A_IT = BM * CPR / THREADS;  // 16-byte A chunks per thread per stage
+  static constexpr int B_IT = BN * CPR / THREADS;
+  static constexpr int LDS_BYTES = 2 * (BM + BN) * BK * 2;
+  static_assert(BK % Mfma<MS>::KSTEP == 0, "BK must hold whole MFMA k-steps");
+  static_assert(WTM % MS == 0 && WTN % MS == 0, "wave tile must hold whole MFMA blocks");
+  static_assert((BM * CPR) % THREADS == 0 && (BN * CPR) % THREADS == 0, "tile/thread split");
+  static_assert(CPR == 4 || CPR == 8, "BK of 32 or 64");
+};
+
+// Raw B chunk as loaded from global memory: 16 bytes of fp16, or 8 bytes of int8/uint8.
+template <int BFMT>
+struct BRaw;
+template <>
+struct BRaw<0> { u32x4 v; };
+template <>
+struct BRaw<1> { u32x2 v; };
+template <>
+struct BRaw<2> { u32x2 v; };
+
+template <int BM, int BN, int BK, int WM, int WN, int MS, int SWZ, int GROUP, int XCD, int BFMT>
+__global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm(
+    const _Float16* __restrict__ A, const void* __restrict__ Bv,
+    const _Float16* __restrict__ scale, const uint8_t* __restrict__ zero,
+    _Float16* __restrict__ C, int M, int N, int K, int lda, int ldb, int ldc, int group) {
+  using Cfg = GemmCfg<BM, BN, BK, WM, WN, MS, SWZ, GROUP, XCD, BFMT>;
+  using MF = Mfma<MS>;
+  constexpr int T = Cfg::THREADS, CPR = Cfg::CPR;
+  constexpr int TM = Cfg::TM, TN = Cfg::TN;
+
+  __shared__ __attribute__((aligned(16))) _Float16 smem[2 * (BM + BN) * BK];
+  _Float16* const sA = smem;                 // [2][BM][BK]
+  _Float16* const sB = smem + 2 * BM * BK;   // [2][BN][BK]
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+
+  const int nm = (M + BM - 1) / BM, nn = N / BN;
+  int tmi, tni;
+  tile_of<GROUP, XCD>(blockIdx.x, nm, nn, tmi, tni);
+  const int m0 = tmi * BM, n0 = tni * BN;
+
+  // ---- global -> register staging -------------------------------------------------------
+  const u32x4* gA[Cfg::A_IT];
+  int sAoff[Cfg::A_IT];
+#pragma unroll
+  for (int i = 0; i < Cfg::A_IT; ++i) {
+    const int q = tid + i * T, r = q / CPR, c = q % CPR;
+    const int gm = min(m0 + r, M - 1);
+    gA[i] = reinterpret_cast<const u32x4*>(A + (long)gm * lda + c * 8);
+    sAoff[i] = r * BK + lds_chunk<BK, SWZ>(r, c) * 8;
+  }
+  int sBoff[Cfg::B_IT];
+  long gBoff[Cfg::B_IT];  // element offset of the chunk's row start + k
+  int bRow[Cfg::B_IT], bC[Cfg::B_IT];
+#pragma unroll
+  for (int i = 0; i < Cfg::B_IT; ++i) {
+    const int q = tid + i * T, r = q / CPR, c = q % CPR;
+    bRow[i] = n0 + r;
+    bC[i] = c;
+    gBoff[i] = (long)(n0 + r) * ldb + c * 8;
+    sBoff[i] = r * BK + lds_chunk<BK, SWZ>(r, c) * 8;
+  }
+  _Float16 rowScale[Cfg::B_IT];
+  if constexpr (BFMT == 1) {
+#pragma unroll
+    for (int i = 0; i < Cfg::B_IT; ++i) rowScale[i] = scale[bRow[i]];
+  }
+
+  u32x4 ra[Cfg::A_IT];
+  BRaw<BFMT> rb[Cfg::B_IT];
+
+  auto load_stage = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < Cfg::A_IT; ++i) ra[i] = gA[i][k0 / 8];
+#pragma unroll
+    for (int i = 0; i < Cfg::B_IT; ++i) {
+      if constexpr (BFMT == 0)
+        rb[i].v = *reinterpret_cast<const u32x4*>(
+            reinterpret_cast<const _Float16*>(Bv) + gBoff[i] + k0);
+      else
+        rb[i].v = *reinterpret_cast<const u32x2*>(
+            reinterpret_cast<const uint8_t*>(Bv) + gBoff[i] + k0);
+    }
+  };
+  auto store_stage = [&](int buf, int k0) {
+    _Float16* a = sA + buf * BM * BK;
+    _Float16* b = sB + buf * BN * BK;
+#pragma unroll
+    for (int i = 0; i < Cfg::A_IT; ++i) *reinterpret_cast<u32x4*>(a + sAoff[i]) = ra[i];
+#pragma unroll
+    for (int i = 0; i < Cfg::B_IT; ++i) {
+      u32x4 v;
+      if constexpr (BFMT == 0) {
+        v = rb[i].v;
+      } else if constexpr (BFMT == 1) {
+        v = as_u32x4(dequant8_i8(rb[i].v[0], rb[i].v[1], rowScale[i]));
+      } else {
+        const int k = k0 + bC[i] * 8;
+        const long gi = (long)bRow[i] * (K / group) + k / group;
+        v = as_u32x4(dequant8_u8(rb[i].v[0], rb[i].v[1], zero[gi], scale[gi]));
+      }
+      *reinterpret_cast<u32x4*>(b + sBoff[i]) = v;
+    }
+  };
+
+  typename MF::acc_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v = 0; v < MF::NACC; ++v) acc[i][j][v] = 0.f;
+
+  // fragment read offsets (row part) inside one stage
+  const int fr = lane % MS;
+  const int fk = lane / MS;  // k-group of this lane
+  int aRow[TM], bRowF[TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) aRow[i] = wm * Cfg::WTM + i * MS + fr;
+#pragma unroll
+  for (int j = 0; j < TN; ++j) bRowF[j] = wn * Cfg::WTN + j * MS + fr;
+
+  const int NT = K / BK;
+  load_stage(0);
+  store_stage(0, 0);
+  __syncthreads();
+
+  for (int kt = 0; kt < NT; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < NT) load_stage((kt + 1) * BK);
+    const _Float16* a = sA + cur * BM * BK;
+    const _Float16* b = sB + cur * BN * BK;
+#pragma unroll
+    for (int ks = 0; ks < Cfg::KS; ++ks) {
+      const int chunk = ks * (64 / MS) + fk;
+      f16x8 fa[TM], fb[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+        fa[i] = *reinterpret_cast<const f16x8*>(a + aRow[i] * BK +
+                                                lds_chunk<BK, SWZ>(aRow[i], chunk) * 8);
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        fb[j] = *reinterpret_cast<const f16x8*>(b + bRowF[j] * BK +
+                                                lds_chunk<BK, SWZ>(bRowF[j], chunk) * 8);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = MF::run(fb[j], fa[i], acc[i][j]);
+    }
+    if (kt + 1 < NT) store_stage(cur ^ 1, (kt + 1) * BK);
+    __syncthreads();
+  }
+
+  // ---- epilogue: each lane owns 4 consecutive n of one m per result group ----------------
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int m = m0 + wm * Cfg::WTM + i * MS + (lane % MS);
+    if (m >= M) continue;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+#pragma unroll
+      for (int g = 0; g < MF::GROUPS; ++g) {
+        const int n = n0 + wn * Cfg::WTN + j * MS + mfma_out_row<MS>(lane, g, 0);
+        f16x4 o;
+        o[0] = (_Float16)acc[i][j][4 * g + 0];
+        o[1] = (_Float16)acc[i][j][4 * g + 1];
+        o[2] = (_Float16)acc[i][j][4 * g + 2];
+        o[3] = (_Float16)acc[i][j][4 * g + 3];
+        *reinterpret_cast<f16x4*>(C + (long)m * ldc + n) = o;
+      }
+    }
+  }
+}

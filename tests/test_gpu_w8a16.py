@@ -1,0 +1,134 @@
+"""GPU parity of the shipped gemm_w8a16 (both weight formats) against the CPU oracle.
+
+Dequantisation must be bit-exact (tempo_dequant_tile runs the GEMM feeds' own device functions);
+the GEMM output must match the oracle (dequantise, then the naive fp16 GEMM) within relL2 3e-3,
+and bit-exactly on inputs whose arithmetic is exact.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from tests.gpu_util import dev, host, poisoned, say
+
+pytestmark = pytest.mark.gpu
+
+SHAPES_NK = [(7168, 5120), (5120, 6144), (34816, 5120), (5120, 17408), (1024, 5120), (5120, 5120)]
+
+
+def make_weights(N, K, fmt, seed, G=128):
+    g = np.random.Generator(np.random.PCG64(seed))
+    if fmt == 1:
+        q = g.integers(-127, 128, (N, K), dtype=np.int16).astype(np.int8)
+        s = O.f2h(g.uniform(0.5, 1.5, N).astype(np.float32) / 127)
+        return q, s, None
+    q = g.integers(0, 256, (N, K), dtype=np.int16).astype(np.uint8)
+    s = O.f2h(g.uniform(0.5, 1.5, (N, K // G)).astype(np.float32) / 255)
+    z = g.integers(100, 157, (N, K // G), dtype=np.int16).astype(np.uint8)
+    return q, s, z
+
+
+def _run(A, q, s, z, fmt, device, G=128):
+    import torch
+    from cuda_tempiler_amd import capi
+
+    M, K = A.shape
+    N = q.shape[0]
+    dC = poisoned((M, N), device)
+    capi.gemm_w8a16(dev(A, device), dev(q, device), dev(s, device),
+                    dev(z, device) if z is not None else None, fmt=fmt, group=G, C=dC)
+    torch.cuda.synchronize()
+    return host(dC)
+
+
+@pytest.mark.parametrize("fmt", [1, 2])
+def test_dequant_tile_bit_exact(gpu, fmt):
+    import torch
+    from cuda_tempiler_amd import capi
+
+    N, K = 512, 1024
+    q, s, z = make_weights(N, K, fmt, 5)
+    ref = O.dequant_sym(q, s) if fmt == 1 else O.dequant_asym(q, s, z, 128)
+    dq, ds = dev(q, gpu), dev(s, gpu)
+    dz = dev(z, gpu) if z is not None else None
+    full = capi.dequant_tile(dq, ds, dz, fmt, 0, 0, N, K)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(full).view(np.uint16), ref.view(np.uint16))
+    part = capi.dequant_tile(dq, ds, dz, fmt, 100, 264, 37, 136)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(part).view(np.uint16), ref[100:137, 264:400].view(np.uint16))
+
+
+@pytest.mark.parametrize("fmt", [1, 2])
+def test_dequant_covers_every_byte_and_zero_point(gpu, fmt):
+    """All 256 weight bytes against every zero-point (fmt 2) / many scales (fmt 1)."""
+    import torch
+    from cuda_tempiler_amd import capi
+
+    N, K = 256, 256
+    q = np.tile(np.arange(256, dtype=np.uint8), (N, 1))
+    if fmt == 1:
+        q = q.view(np.int8)
+        s = O.f2h(np.linspace(1e-4, 60.0, N).astype(np.float32))
+        z = None
+        ref = O.dequant_sym(q, s)
+    else:
+        s = O.f2h(np.linspace(1e-3, 3.0, N * 2).astype(np.float32).reshape(N, 2))
+        z = np.repeat(np.arange(256, dtype=np.uint8)[:, None], 2, axis=1)
+        ref = O.dequant_asym(q, s, z, 128)
+    out = capi.dequant_tile(dev(q, gpu), dev(s, gpu), dev(z, gpu) if z is not None else None,
+                            fmt, 0, 0, N, K)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(out).view(np.uint16), ref.view(np.uint16))
+
+
+@pytest.mark.parametrize("fmt", [1, 2])
+@pytest.mark.parametrize("M", [1, 16, 32, 128])
+def test_w8a16_parity_small_m(gpu, fmt, M):
+    for N, K in SHAPES_NK:
+        say("w8a16 fmt", fmt, "M", M, "N", N, "K", K)
+        A = O.randn_f16((M, K), 11, K ** -0.5)
+        q, s, z = make_weights(N, K, fmt, 77)
+        C = _run(A, q, s, z, fmt, gpu)
+        assert O.count_poison(C) == 0
+        ref = O.gemm_w8a16(A, q, s, z, 128, fmt)
+        rel = O.rel_l2(C, ref)
+        say("  relL2 %.3e" % rel)
+        assert rel <= 3e-3
+
+
+@pytest.mark.parametrize("fmt", [1, 2])
+def test_w8a16_parity_prefill(gpu, fmt):
+    """M = 2048 on two of the dense shapes; oracle on sampled rows."""
+    for N, K in [(5120, 6144), (7168, 5120)]:
+        M = 2048
+        say("w8a16 prefill fmt", fmt, M, N, K)
+        A = O.randn_f16((M, K), 11, K ** -0.5)
+        q, s, z = make_weights(N, K, fmt, 77)
+        C = _run(A, q, s, z, fmt, gpu)
+        assert O.count_poison(C) == 0
+        rows = np.r_[0:64, 1000:1064, M - 64:M]
+        ref = O.gemm_w8a16(A[rows], q, s, z, 128, fmt)
+        rel = O.rel_l2(np.ascontiguousarray(C[rows]), ref)
+        say("  relL2 %.3e" % rel)
+        assert rel <= 3e-3
+
+
+@pytest.mark.parametrize("fmt", [1, 2])
+@pytest.mark.parametrize("M", [1, 32, 300])
+def test_w8a16_exact_regime_bit_exact(gpu, fmt, M):
+    """Scales that are powers of two and activations on a 1/8 grid make every product and
+    partial sum exact in fp32, so the result is order-independent: bits must equal the oracle."""
+    N, K = 1024, 2048
+    g = np.random.Generator(np.random.PCG64(31))
+    A = (g.integers(-4, 5, (M, K)).astype(np.float32) / 8).astype(np.float16)
+    if fmt == 1:
+        q = g.integers(-127, 128, (N, K), dtype=np.int16).astype(np.int8)
+        s = np.full(N, np.float16(2.0 ** -7))
+        z = None
+    else:
+        q = g.integers(0, 256, (N, K), dtype=np.int16).astype(np.uint8)
+        s = np.full((N, K // 128), np.float16(2.0 ** -8))
+        z = g.integers(100, 157, (N, K // 128), dtype=np.int16).astype(np.uint8)
+    C = _run(A, q, s, z, fmt, gpu)
+    ref = O.gemm_w8a16(A, q, s, z, 128, fmt)
+    assert np.array_equal(C.view(np.uint16), ref.view(np.uint16))
