@@ -71,7 +71,7 @@ typedef struct TempoW8A16Params {
   void* C;           /* fp16 [M][ldc] */
   int M, N, K;
   int lda, ldw, ldc;
-  int group; /* fmt 2: k per scale group (multiple of 64, divides K); fmt 1: ignored */
+  int group; /* fmt 2: k per scale group (128; divides K); fmt 1: ignored */
   int fmt;
 } TempoW8A16Params;
 

@@ -37,6 +37,10 @@ HEAD = """// GENERATED from select.py -- do not edit.  Regenerate with:
 def instantiation(kind, p):
     if kind == "stream":
         return "launch_stream<%d,%d,%d>" % (p["MB"], p["R"], p["U"])
+    if kind == "dma":
+        return "launch_dma<%d,%d,%d,%d,%d,%d,%d,%d,%d>" % (
+            p["BM"], p["BN"], p["BK"], p["WM"], p["WN"], p["STAGES"], p["SWZ"], p["GROUP"],
+            p["XCD"])
     return "launch_mfma<%d,%d,%d,%d,%d,%d,%d,%d,%d>" % (
         p["BM"], p["BN"], p["BK"], p["WM"], p["WN"], p["MS"], p["SWZ"], p["GROUP"], p["XCD"])
 
@@ -44,7 +48,7 @@ def instantiation(kind, p):
 def condition(sel, kind, p, m_max):
     if kind == "stream":
         fit = "(p.N %% %d) == 0 && (p.K %% %d) == 0" % (sel.STREAM_N_ROWS * p["R"],
-                                                          sel.STREAM_K_STEP)
+                                                          sel.STREAM_K_STEP * p["U"])
     else:
         fit = "(p.N %% %d) == 0 && (p.K %% %d) == 0" % (p["BN"], p["BK"])
     return "p.M <= %d" % m_max, fit

@@ -5,10 +5,8 @@
 // given stream, never synchronises, and the caller owns every buffer.  A shape the ladder
 // does not cover returns hipErrorInvalidConfiguration: "take your own path" (dispatch.inc).
 //
-// The only state is the split-K workspace of the streaming (decode) kernel: one buffer per
-// device, allocated on the first call that needs it and kept for the life of the process.
-// Calls that overlap on one device (different streams, same time) must not both take the
-// split-K route; calls serialised on one stream are safe.
+// The launcher keeps no state and allocates nothing: concurrent calls on different streams are
+// independent.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -27,26 +25,20 @@ struct GemmParams {
   int lda, ldb, ldc;  // row strides in elements
 };
 
-// ---- split-K workspace (streaming kernel only) ---------------------------------------------
-constexpr size_t kWsPartialBytes = size_t(32) << 20;  // fp32 partials, S*M*N*4 <= this
-constexpr size_t kWsCounterCount = size_t(1) << 16;   // per-slab arrival counters
-hipError_t workspace(float** partials, unsigned** counters);  // defined in launch.hip
-
-// Choose the k split for the streaming kernel: enough waves to cover the machine (about 8
-// per CU of 256 CUs), chunks of whole pipeline stages, workspace within its fixed size.
-inline void stream_split(int M, int N, int K, int R, int U, int* S_out, int* chunk_out) {
+// k split of the streaming kernel: waves per workgroup (each takes one contiguous k chunk, the
+// workgroup reduces through LDS).  Aim for about 8 waves per CU over the machine's 256 CUs,
+// at most 8 waves per workgroup, every chunk a whole number of pipeline stages.
+inline void stream_split(int N, int K, int R, int U, int* S_out, int* chunk_out) {
   const int slabs = N / (16 * R);
-  const int step = 64 * U;
+  const int stages = K / (64 * U);
   int S = (2048 + slabs - 1) / slabs;
-  const int smax_k = K / 256 > 0 ? K / 256 : 1;  // keep chunks >= 256 k
-  if (S > smax_k) S = smax_k;
+  if (S > 8) S = 8;
+  if (S > stages) S = stages;
   if (S < 1) S = 1;
-  while (S > 1 && (size_t)S * M * N * 4 > kWsPartialBytes) --S;
-  int chunk = (K + S - 1) / S;
-  chunk = (chunk + step - 1) / step * step;
-  S = (K + chunk - 1) / chunk;
+  const int per = (stages + S - 1) / S;  // stages per wave
+  S = (stages + per - 1) / per;
   *S_out = S;
-  *chunk_out = chunk;
+  *chunk_out = per * 64 * U;
 }
 
 template <int MB, int R, int U>
@@ -57,8 +49,6 @@ inline hipError_t launch_stream(const GemmParams& p, hipStream_t s) {
   a.scale = nullptr;
   a.zero = nullptr;
   a.C = p.C;
-  a.ws = nullptr;
-  a.counters = nullptr;
   a.M = p.M;
   a.N = p.N;
   a.K = p.K;
@@ -66,15 +56,10 @@ inline hipError_t launch_stream(const GemmParams& p, hipStream_t s) {
   a.ldb = p.ldb;
   a.ldc = p.ldc;
   a.group = 0;
-  stream_split(p.M, p.N, p.K, R, U, &a.S, &a.chunk);
-  if (a.S > 1) {
-    if ((size_t)(p.N / (16 * R)) > kWsCounterCount) return hipErrorInvalidConfiguration;
-    const hipError_t e = workspace(&a.ws, &a.counters);
-    if (e != hipSuccess) return e;
-  }
-  const int units = (p.N / (16 * R)) * a.S;
-  const dim3 grid((units + 3) / 4), blk(256);
-  hipLaunchKernelGGL((k_stream<MB, R, U, 0>), grid, blk, 0, s, a);
+  stream_split(p.N, p.K, R, U, &a.S, &a.chunk);
+  const dim3 grid(p.N / (16 * R)), blk(64 * a.S);
+  const size_t lds = a.S > 1 ? (size_t)a.S * R * MB * 64 * 16 : 0;
+  hipLaunchKernelGGL((k_stream<MB, R, U, 0>), grid, blk, lds, s, a);
   return hipGetLastError();
 }
 
@@ -87,6 +72,16 @@ inline hipError_t launch_mfma(const GemmParams& p, hipStream_t s) {
                      p.A, static_cast<const void*>(p.B), static_cast<const _Float16*>(nullptr),
                      static_cast<const uint8_t*>(nullptr), p.C, p.M, p.N, p.K, p.lda, p.ldb,
                      p.ldc, 0);
+  return hipGetLastError();
+}
+
+template <int BM, int BN, int BK, int WM, int WN, int STAGES, int SWZ, int GROUP, int XCD>
+inline hipError_t launch_dma(const GemmParams& p, hipStream_t s) {
+  const int nm = (p.M + BM - 1) / BM;
+  const int nn = p.N / BN;
+  const dim3 grid(nm * nn), blk(WM * WN * 64);
+  hipLaunchKernelGGL((k_gemm_dma<BM, BN, BK, WM, WN, STAGES, SWZ, GROUP, XCD>), grid, blk, 0, s,
+                     p.A, p.B, p.C, p.M, p.N, p.K, p.lda, p.ldb, p.ldc);
   return hipGetLastError();
 }
 

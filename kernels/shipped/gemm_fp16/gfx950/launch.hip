@@ -4,39 +4,10 @@
 //
 // Build (host tree): hipcc -O3 -std=c++17 --offload-arch=gfx950
 //                    -Xclang -target-feature -Xclang -packed-fp32-ops -c launch.hip
-#include <mutex>
-
 #include "launch.h"
 
 namespace tempo {
 namespace gen {
-
-hipError_t workspace(float** partials, unsigned** counters) {
-  static std::mutex mu;
-  static void* ws[64] = {};
-  int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) return e;
-  if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
-  std::lock_guard<std::mutex> lock(mu);
-  if (!ws[dev]) {
-    const size_t bytes = kWsPartialBytes + kWsCounterCount * sizeof(unsigned);
-    void* p = nullptr;
-    e = hipMalloc(&p, bytes);
-    if (e != hipSuccess) return e;
-    // counters must start at zero; every completed call leaves them at zero again
-    e = hipMemset(static_cast<char*>(p) + kWsPartialBytes, 0, kWsCounterCount * sizeof(unsigned));
-    if (e == hipSuccess) e = hipDeviceSynchronize();
-    if (e != hipSuccess) {
-      (void)hipFree(p);
-      return e;
-    }
-    ws[dev] = p;
-  }
-  *partials = static_cast<float*>(ws[dev]);
-  *counters = reinterpret_cast<unsigned*>(static_cast<char*>(ws[dev]) + kWsPartialBytes);
-  return hipSuccess;
-}
 
 hipError_t launch(const GemmParams& p, hipStream_t s) {
   if (!applicable(p)) return hipErrorInvalidConfiguration;

@@ -6,7 +6,7 @@ ladder -- dispatch.inc is generated from it by gen_dispatch.py and a test checks
 
 Bands (M is the only runtime-varying extent in serving):
   * M <= 32   stream: the weight-streaming decode kernel (HBM-bound; one pass over B).
-  * M >  32   mfma: the LDS-tiled MFMA kernel, macro tile chosen by M.
+  * M >  32   mfma / dma: LDS-tiled MFMA kernels (dma = LDS-DMA copies), tile chosen by M.
 """
 
 ARCH = "gfx950"
@@ -17,8 +17,8 @@ LADDER = [
     (32, "s32r1u4", "stream", dict(MB=2, R=1, U=4)),
     (256, "m128x128k64", "mfma",
      dict(BM=128, BN=128, BK=64, WM=2, WN=2, MS=32, SWZ=1, GROUP=8, XCD=1)),
-    (1 << 30, "m256x256k64", "mfma",
-     dict(BM=256, BN=256, BK=64, WM=2, WN=2, MS=32, SWZ=1, GROUP=8, XCD=1)),
+    (1 << 30, "d256x256k64s2", "dma",
+     dict(BM=256, BN=256, BK=64, WM=2, WN=2, STAGES=2, SWZ=2, GROUP=8, XCD=1)),
 ]
 
 # Divisibility each kind needs (checked at run time by dispatch.inc, mirrored here).
@@ -28,7 +28,7 @@ STREAM_N_ROWS = 16  # weight rows per MFMA row group (times R)
 
 def _fits(kind, p, M, N, K):
     if kind == "stream":
-        return N % (STREAM_N_ROWS * p["R"]) == 0 and K % STREAM_K_STEP == 0
+        return N % (STREAM_N_ROWS * p["R"]) == 0 and K % (STREAM_K_STEP * p["U"]) == 0
     return N % p["BN"] == 0 and K % p["BK"] == 0
 
 

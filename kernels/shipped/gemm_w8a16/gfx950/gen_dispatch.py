@@ -44,7 +44,7 @@ def instantiation(kind, p):
 def condition(sel, kind, p, m_max):
     if kind == "stream":
         fit = "(p.N %% %d) == 0 && (p.K %% %d) == 0" % (sel.STREAM_N_ROWS * p["R"],
-                                                          sel.STREAM_K_STEP)
+                                                          sel.STREAM_K_STEP * p["U"])
     else:
         fit = "(p.N %% %d) == 0 && (p.K %% %d) == 0" % (p["BN"], p["BK"])
     return "p.M <= %d" % m_max, fit

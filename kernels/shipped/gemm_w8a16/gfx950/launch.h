@@ -7,9 +7,8 @@
 //   fmt 2: Wq uint8 [N][ldw], scale fp16 [N][K/group], zero uint8 [N][K/group]
 //          W = fp16_rn((q - z) * s)
 // Asynchronous on the given stream, never synchronises, caller owns every buffer.  Not covered
-// -> hipErrorInvalidConfiguration (take your own path).  The only state is the split-K
-// workspace of the streaming kernel (one per device, allocated on first need, kept); calls that
-// overlap on one device must not both take the split-K route.
+// -> hipErrorInvalidConfiguration (take your own path).  The launcher keeps no state and
+// allocates nothing.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -32,23 +31,20 @@ struct W8A16Params {
   int fmt;  // 1 int8 symmetric per-channel, 2 uint8 asymmetric group-wise
 };
 
-constexpr size_t kWsPartialBytes = size_t(32) << 20;
-constexpr size_t kWsCounterCount = size_t(1) << 16;
-hipError_t workspace(float** partials, unsigned** counters);  // defined in launch.hip
-
-inline void stream_split(int M, int N, int K, int R, int U, int* S_out, int* chunk_out) {
+// k split of the streaming kernel: waves per workgroup (each takes one contiguous k chunk, the
+// workgroup reduces through LDS).  Aim for about 8 waves per CU over the machine's 256 CUs,
+// at most 8 waves per workgroup, every chunk a whole number of pipeline stages.
+inline void stream_split(int N, int K, int R, int U, int* S_out, int* chunk_out) {
   const int slabs = N / (16 * R);
-  const int step = 64 * U;
+  const int stages = K / (64 * U);
   int S = (2048 + slabs - 1) / slabs;
-  const int smax_k = K / 256 > 0 ? K / 256 : 1;
-  if (S > smax_k) S = smax_k;
+  if (S > 8) S = 8;
+  if (S > stages) S = stages;
   if (S < 1) S = 1;
-  while (S > 1 && (size_t)S * M * N * 4 > kWsPartialBytes) --S;
-  int chunk = (K + S - 1) / S;
-  chunk = (chunk + step - 1) / step * step;
-  S = (K + chunk - 1) / chunk;
+  const int per = (stages + S - 1) / S;  // stages per wave
+  S = (stages + per - 1) / per;
   *S_out = S;
-  *chunk_out = chunk;
+  *chunk_out = per * 64 * U;
 }
 
 inline StreamArgs stream_args(const W8A16Params& p) {
@@ -58,8 +54,6 @@ inline StreamArgs stream_args(const W8A16Params& p) {
   a.scale = p.scale;
   a.zero = p.zero;
   a.C = p.C;
-  a.ws = nullptr;
-  a.counters = nullptr;
   a.M = p.M;
   a.N = p.N;
   a.K = p.K;
@@ -75,18 +69,13 @@ inline StreamArgs stream_args(const W8A16Params& p) {
 template <int MB, int R, int U>
 inline hipError_t launch_stream(const W8A16Params& p, hipStream_t s) {
   StreamArgs a = stream_args(p);
-  stream_split(p.M, p.N, p.K, R, U, &a.S, &a.chunk);
-  if (a.S > 1) {
-    if ((size_t)(p.N / (16 * R)) > kWsCounterCount) return hipErrorInvalidConfiguration;
-    const hipError_t e = workspace(&a.ws, &a.counters);
-    if (e != hipSuccess) return e;
-  }
-  const int units = (p.N / (16 * R)) * a.S;
-  const dim3 grid((units + 3) / 4), blk(256);
+  stream_split(p.N, p.K, R, U, &a.S, &a.chunk);
+  const dim3 grid(p.N / (16 * R)), blk(64 * a.S);
+  const size_t lds = a.S > 1 ? (size_t)a.S * R * MB * 64 * 16 : 0;
   if (p.fmt == 1)
-    hipLaunchKernelGGL((k_stream<MB, R, U, 1>), grid, blk, 0, s, a);
+    hipLaunchKernelGGL((k_stream<MB, R, U, 1>), grid, blk, lds, s, a);
   else
-    hipLaunchKernelGGL((k_stream<MB, R, U, 2>), grid, blk, 0, s, a);
+    hipLaunchKernelGGL((k_stream<MB, R, U, 2>), grid, blk, lds, s, a);
   return hipGetLastError();
 }
 
@@ -109,8 +98,7 @@ inline bool applicable(const W8A16Params& p) {
   if (p.M <= 0 || p.N <= 0 || p.K <= 0) return false;
   if (p.fmt != 1 && p.fmt != 2) return false;
   if (!p.A || !p.Wq || !p.scale || !p.C) return false;
-  if (p.fmt == 2 && (!p.zero || p.group <= 0 || (p.group % 64) != 0 || (p.K % p.group) != 0))
-    return false;
+  if (p.fmt == 2 && (!p.zero || p.group != 128 || (p.K % p.group) != 0)) return false;
   if (p.lda < p.K || p.ldw < p.K || p.ldc < p.N) return false;
   if ((p.K % 8) != 0 || (p.N % 8) != 0) return false;
   if ((p.lda % 8) != 0 || (p.ldw % 16) != 0 || (p.ldc % 4) != 0) return false;

@@ -27,7 +27,7 @@ STREAM_N_ROWS = 16
 
 def _fits(kind, p, M, N, K):
     if kind == "stream":
-        return N % (STREAM_N_ROWS * p["R"]) == 0 and K % STREAM_K_STEP == 0
+        return N % (STREAM_N_ROWS * p["R"]) == 0 and K % (STREAM_K_STEP * p["U"]) == 0
     return N % p["BN"] == 0 and K % p["BK"] == 0
 
 
@@ -38,7 +38,7 @@ def select(op, M, N, K, fmt=1, group=128, dtype_a="fp16", dtype_c="fp16", arch=A
         return None
     if M <= 0 or N <= 0 or K <= 0 or N % 8 or K % 8:
         return None
-    if fmt == 2 and (group <= 0 or group % 64 or K % group):
+    if fmt == 2 and (group != 128 or K % group):
         return None
     for m_max, tag, kind, p in LADDER:
         if M <= m_max:

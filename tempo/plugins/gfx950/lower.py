@@ -1,0 +1,217 @@
+"""gfx950: SKELETONS -- section 7 (reference pattern tempo/plugins/sm70/lower.py).
+
+The product GENERATES a kernel from the declared operation; render() only substitutes: it wraps
+the skeleton sources in a namespace and appends the one explicit instantiation named by the
+hyperform, so the emitted file compiles to exactly the kernel entry_probe() names.
+"""
+from __future__ import annotations
+
+import math
+import os
+from typing import Iterator
+
+from ..base import (Atom, AtomKind, Hyperform, Launch, OpSpec, PluginCapabilityError, Rendered)
+from . import space
+from .machine import Gfx950Machine
+from .resources import Gfx950Resources
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+SKEL = os.path.join(HERE, "skeletons")
+_M = Gfx950Machine()
+_RES = Gfx950Resources()
+
+CAPABILITIES = frozenset({
+    "gemm_fp16_ntn",          # C = A . B^T, both operands k-contiguous
+    "gemm_w8a16_sym_i8",      # int8 weights, fp16 scale per output channel
+    "gemm_w8a16_asym_u8_g128",  # uint8 weights, fp16 scale + uint8 zero per (row, 128 k)
+    "lds_dma_pipeline",       # global_load_lds_dwordx4 multi-stage copies
+    "xcd_aware_raster",       # block ids remapped so each XCD owns a contiguous tile run
+    "decode_lds_ring",        # per-wave LDS-DMA ring for the weight-streaming regime
+    "fmha_fwd_causal_gqa",    # fixed skeleton skeletons/fmha_fwd (not searched)
+})
+
+# kernel symbol, template-parameter order, and argument list, per kind: the emitter's only data
+_ENTRY = {
+    "dma": ("k_gemm_dma", ("BM", "BN", "BK", "WM", "WN", "STAGES", "SWZ", "GROUP", "XCD"),
+            "const _Float16*, const _Float16*, _Float16*, int, int, int, int, int, int",
+            ("common/cdna4.h", "gemm_mfma/kernel.hip")),
+    "reg": ("k_gemm", ("BM", "BN", "BK", "WM", "WN", "MS", "SWZ", "GROUP", "XCD", "BFMT"),
+            "const _Float16*, const void*, const _Float16*, const uint8_t*, _Float16*, int, int, "
+            "int, int, int, int, int",
+            ("common/cdna4.h", "gemm_mfma/kernel.hip")),
+    "ring": ("k_stream_dma", ("MB", "R", "D", "BFMT"), "StreamArgs",
+             ("common/cdna4.h", "gemv_stream/kernel.hip")),
+    "stream": ("k_stream", ("MB", "R", "U", "BFMT"), "StreamArgs",
+               ("common/cdna4.h", "gemv_stream/kernel.hip")),
+}
+NAMESPACE = "tempo::gen"
+
+
+def _p(h: Hyperform) -> dict:
+    return dict(h.params)
+
+
+class Gfx950Skeletons:
+    _LAYOUT_V1 = ("k", "k", "n")
+    _ACC_V1 = "fp32"
+
+    def ops(self):
+        return ("gemm",)
+
+    def axes(self):
+        return space.axes()
+
+    def capabilities(self):
+        return CAPABILITIES
+
+    def _require_form_v1(self, op: OpSpec) -> None:
+        got = (op.layout_a, op.layout_b, op.layout_c)
+        if got != self._LAYOUT_V1:
+            raise PluginCapabilityError(
+                "gfx950 skeletons compute C = A . B^T with k-contiguous operands (layouts %s); "
+                "declared %s.  Refused: another layout is another operation."
+                % ("/".join(self._LAYOUT_V1), "/".join(got)))
+        if op.dtype_acc != self._ACC_V1:
+            raise PluginCapabilityError("gfx950 skeletons accumulate in fp32 (MFMA f32 result); "
+                                        "declared %s" % op.dtype_acc)
+        if op.dtype_c != "fp16":
+            raise PluginCapabilityError("gfx950 skeletons write fp16 C; declared %s" % op.dtype_c)
+        space.bfmt(op)
+
+    def variants(self, op: OpSpec) -> Iterator[Hyperform]:
+        self._require_form_v1(op)
+        return space.variants(op)
+
+    # -- resources without a build ------------------------------------------------------------
+    def _split(self, op: OpSpec, p: dict):
+        N, K = int(op.shapes["N"]), int(op.shapes["K"])
+        kind = p["kind"]
+        if kind == "ring":
+            per_wave = space.lds_bytes("ring", dict(p, S=1))
+            return space.stream_split(N, K, p["R"], 64, p["BFMT"], per_wave)
+        return space.stream_split(N, K, p["R"], 64 * p["U"], p["BFMT"])
+
+    def resources_of(self, op: OpSpec, h: Hyperform):
+        """(regs, max_live, lds) estimated from the skeleton's structure; the two register numbers
+        are the optimistic and pessimistic edges of one estimate."""
+        p = _p(h)
+        kind = p["kind"]
+        if kind in ("dma", "reg"):
+            ms = p.get("MS", 32)
+            nacc = 16 if ms == 32 else 4
+            tm, tn = p["BM"] // p["WM"] // ms, p["BN"] // p["WN"] // ms
+            acc = tm * tn * nacc
+            frags = 2 * (tm + tn) * 4 if kind == "dma" else (tm + tn) * 4
+            nw = p["WM"] * p["WN"]
+            if kind == "dma":
+                rpb = 1024 // (p["BK"] * 2)
+                copies = 2 * ((p["BM"] + p["BN"]) // (rpb * nw))  # 64-bit source addresses
+            else:
+                per = (p["BM"] + p["BN"]) * p["BK"] // 8 // (nw * 64)
+                copies = per * 4 + per * 2  # staged data + addresses
+            regs = acc + frags + copies + 16
+            return regs, int(regs * 1.2), space.lds_bytes(kind, p)
+        wb = 2 if p["BFMT"] == 0 else 1
+        S, _ = self._split(op, p)
+        if kind == "ring":
+            regs = p["R"] * p["MB"] * 4 + (p["R"] * wb + 2 * p["MB"]) * 4 + 2 * (p["R"] + p["MB"]) + 16
+        else:
+            regs = (2 * p["R"] * p["MB"] * 4 + 2 * p["U"] * (p["R"] * wb + 2 * p["MB"]) * 4
+                    + 2 * (p["R"] + p["MB"]) + 16)
+        return regs, int(regs * 1.25), space.lds_bytes(kind, dict(p, S=S))
+
+    def launch_of(self, op: OpSpec, h: Hyperform) -> Launch:
+        p = _p(h)
+        M, N = int(op.shapes["M"]), int(op.shapes["N"])
+        kind = p["kind"]
+        if kind in ("dma", "reg"):
+            grid = -(-M // p["BM"]) * (N // p["BN"])
+            threads = p["WM"] * p["WN"] * 64
+            S = 1
+        else:
+            S, _ = self._split(op, p)
+            grid = N // (16 * p["R"])
+            threads = 64 * S
+        _, _, lds = self.resources_of(op, h)
+        return Launch(grid_ctas=grid, threads=threads, smem_bytes=lds, entry=self.entry_probe(h),
+                      min_ctas_per_sm=1)
+
+    def estimate_atoms(self, op: OpSpec, h: Hyperform) -> list:
+        """Per-wave load of the whole operation on the channels MFMA (flop), LDS and VMEM (bytes),
+        as one compute unit sees it: one k-tile (or k-step) footprint times the number of times a
+        CU replays it (k-tiles x rounds of resident workgroups)."""
+        p = _p(h)
+        kind = p["kind"]
+        M, N, K = int(op.shapes["M"]), int(op.shapes["N"]), int(op.shapes["K"])
+        regs, _, lds = self.resources_of(op, h)
+        lau = self.launch_of(op, h)
+        occ = _RES.occupancy(min(regs, 512), lds, lau.threads)
+        per_cu = max(1, occ.ctas_per_sm)
+        rounds = -(-lau.grid_ctas // (int(_M.rate("GEOM.SMS").value) * per_cu))
+        atoms = []
+        if kind in ("dma", "reg"):
+            ms = p.get("MS", 32)
+            tm, tn = p["BM"] // p["WM"] // ms, p["BN"] // p["WN"] // ms
+            ks = p["BK"] // (16 if ms == 32 else 32)
+            nw = p["WM"] * p["WN"]
+            reps = (K // p["BK"]) * rounds
+            flops = tm * tn * ks * space.MFMA_FLOPS[ms]
+            lds_rd = (tm + tn) * ks * 1024
+            vmem = (p["BM"] + p["BN"]) * p["BK"] * 2 // nw
+            if p.get("BFMT", 0):
+                vmem = p["BM"] * p["BK"] * 2 // nw + p["BN"] * p["BK"] // nw
+        else:
+            wb = 2 if p["BFMT"] == 0 else 1
+            S, chunk = self._split(op, p)
+            reps = (chunk // 64) * rounds
+            flops = 2 * p["R"] * p["MB"] * space.MFMA_FLOPS[16]
+            vmem = (p["R"] * wb + 2 * p["MB"]) * 1024
+            lds_rd = vmem if kind == "ring" else 0
+        atoms.append(Atom(uid=0, kind=AtomKind.COMPUTE, op_id="v_mfma x%d" % (flops // 16384),
+                          footprint={"MFMA": float(flops * reps)},
+                          latency=_M.rate("LATENCY.MFMA32").value))
+        if lds_rd:
+            atoms.append(Atom(uid=1, kind=AtomKind.MEM_READ, op_id="ds_read_b128",
+                              footprint={"LDS": float(lds_rd * reps)},
+                              latency=_M.rate("LATENCY.LDS").value))
+        atoms.append(Atom(uid=2, kind=AtomKind.XFER_ISSUE,
+                          op_id="global_load_lds_dwordx4" if kind in ("dma", "ring") else "global_load_dwordx4",
+                          footprint={"VMEM": float(vmem * reps)},
+                          latency=_M.rate("LATENCY.VMEM").value, token="copy"))
+        atoms.append(Atom(uid=3, kind=AtomKind.XFER_WAIT, op_id="s_waitcnt vmcnt", footprint={},
+                          token="copy"))
+        atoms.append(Atom(uid=4, kind=AtomKind.BARRIER, op_id="s_barrier", footprint={}))
+        return atoms
+
+    # -- emission ------------------------------------------------------------------------------
+    def render(self, op: OpSpec, h: Hyperform) -> Rendered:
+        self._require_form_v1(op)
+        p = _p(h)
+        kind = p["kind"]
+        if kind not in _ENTRY:
+            raise PluginCapabilityError("no entry declared for skeleton kind %r" % kind)
+        sym, order, args, files = _ENTRY[kind]
+        body = []
+        for f in files:
+            with open(os.path.join(SKEL, f), encoding="utf-8") as fh:
+                body.append("// ===== %s =====\n%s\n" % (f, fh.read()))
+        head = ("// GENERATED by tempo: plugin gfx950, hyperform %s, operation %s %sx%sx%s.\n"
+                "#include <hip/hip_runtime.h>\n#include <stdint.h>\n\nnamespace tempo {\nnamespace gen {\n\n"
+                % (h.key, op.kind, op.shapes.get("M"), op.shapes.get("N"), op.shapes.get("K")))
+        inst = ("\n// explicit instantiation: the one kernel this file exists to contain\n"
+                "template __global__ void %s<%s>(%s);\n"
+                % (sym, ", ".join(str(int(p[k])) for k in order), args))
+        src = head + "".join(body) + inst + "\n}  // namespace gen\n}  // namespace tempo\n"
+        return Rendered(source=src, launch=self.launch_of(op, h), includes=(),
+                        notes="namespace wrap + one explicit instantiation; logic lives in the skeleton",
+                        filename="kernel_%s.hip" % h.key)
+
+    def entry_probe(self, h: Hyperform) -> str:
+        """The kernel's name as the profiler prints it (demangled template id)."""
+        p = _p(h)
+        sym, order, _, _ = _ENTRY[p["kind"]]
+        vals = []
+        for k in order:
+            v = p[k]
+            vals.append("true" if v is True else "false" if v is False else str(int(v)))
+        return "%s::%s<%s>" % (NAMESPACE, sym, ", ".join(vals))

@@ -1,0 +1,197 @@
+// harness.hip -- measuring harness of the gemm_mfma skeleton on gfx950 (plugin build/verify/
+// measure stages).  Reference pattern: tempo/plugins/sm70/skeletons/gemm_hmma884/harness.cu
+// (gate before stopwatch, poison fill, relL2 in double, fp64 spot check, JSON lines).
+//
+// Build (done by tempo/plugins/gfx950/tune.py, which also writes configs.inc):
+//   hipcc -O3 -std=c++17 --offload-arch=gfx950 -Xclang -target-feature -Xclang -packed-fp32-ops
+//         -I<dir with configs.inc> harness.hip -o harness
+// Run:  ./harness M N K [iters]
+//
+// For each CFG row of configs.inc: fill A, B from a hash (seeded, deterministic), compute the
+// reference once with the naive one-thread-per-output kernel (the pipeline's input), then per
+// variant: poison C with 0x7f7f, launch, synchronise, gate (no poison left, relL2 <= 3e-3 vs the
+// naive kernel, fp64 spot cells), and only then time back-to-back launches with hipEvents over
+// rotating copies of B (working set above the 256 MiB Infinity Cache).  Prints one JSON line per
+// variant: BUILD-free (resource numbers come from the compiler pass), CAND on success,
+// FAILGATE on a failed gate.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <vector>
+
+namespace tempo {
+namespace tune {
+#include "common/cdna4.h"
+#include "gemm_mfma/kernel.hip"
+}  // namespace tune
+}  // namespace tempo
+
+using namespace tempo::tune;
+
+#define CK(x)                                                                          \
+  do {                                                                                 \
+    hipError_t e_ = (x);                                                               \
+    if (e_ != hipSuccess) {                                                            \
+      printf("HIPERR %s @%d: %s\n", #x, __LINE__, hipGetErrorString(e_));              \
+      exit(2);                                                                         \
+    }                                                                                  \
+  } while (0)
+
+__global__ void k_fill(_Float16* p, long n, unsigned seed, float scale) {
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) {
+    unsigned h = (unsigned)i * 2654435761u + seed;
+    h ^= h >> 15;
+    h *= 2246822519u;
+    h ^= h >> 13;
+    p[i] = (_Float16)((((float)(h & 0xFFFF) / 65535.f) - 0.5f) * scale);
+  }
+}
+
+__global__ void k_naive(const _Float16* A, const _Float16* B, _Float16* C, int M, int N, int K) {
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  const int m = blockIdx.y * blockDim.y + threadIdx.y;
+  if (m >= M || n >= N) return;
+  float acc = 0.f;
+  for (int k = 0; k < K; ++k) acc = __builtin_fmaf((float)A[(long)m * K + k], (float)B[(long)n * K + k], acc);
+  C[(long)m * N + n] = (_Float16)acc;
+}
+
+__global__ void k_rel(const _Float16* a, const _Float16* b, long n, double* out) {
+  double d = 0, r = 0;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) {
+    const double x = (double)(float)a[i], y = (double)(float)b[i];
+    d += (x - y) * (x - y);
+    r += y * y;
+  }
+  atomicAdd(out, d);
+  atomicAdd(out + 1, r);
+}
+
+__global__ void k_poison(const _Float16* a, long n, unsigned long long* o) {
+  unsigned long long c = 0;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x)
+    if (*reinterpret_cast<const unsigned short*>(a + i) == 0x7f7f) ++c;
+  atomicAdd(o, c);
+}
+
+__global__ void k_fill_u16(unsigned short* p, long n, unsigned short v) {
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) p[i] = v;
+}
+
+static double rel_l2(const _Float16* a, const _Float16* b, long n) {
+  double* d;
+  CK(hipMalloc(&d, 16));
+  CK(hipMemset(d, 0, 16));
+  hipLaunchKernelGGL(k_rel, dim3(1024), dim3(256), 0, 0, a, b, n, d);
+  CK(hipDeviceSynchronize());
+  double h[2];
+  CK(hipMemcpy(h, d, 16, hipMemcpyDeviceToHost));
+  CK(hipFree(d));
+  return h[1] > 0 ? sqrt(h[0] / h[1]) : (h[0] > 0 ? 1.0 : 0.0);
+}
+
+static unsigned long long poison_left(const _Float16* a, long n) {
+  unsigned long long* d;
+  CK(hipMalloc(&d, 8));
+  CK(hipMemset(d, 0, 8));
+  hipLaunchKernelGGL(k_poison, dim3(1024), dim3(256), 0, 0, a, n, d);
+  CK(hipDeviceSynchronize());
+  unsigned long long h;
+  CK(hipMemcpy(&h, d, 8, hipMemcpyDeviceToHost));
+  CK(hipFree(d));
+  return h;
+}
+
+typedef void (*LaunchFn)(const _Float16*, const _Float16*, _Float16*, int, int, int, hipStream_t);
+struct Arm {
+  const char* tag;
+  bool (*fits)(int, int, int);
+  LaunchFn launch;
+};
+
+template <int BM, int BN, int BK, int WM, int WN, int STAGES, int SWZ, int GROUP, int XCD>
+struct Dma {
+  static bool fits(int M, int N, int K) { (void)M; return N % BN == 0 && K % BK == 0; }
+  static void launch(const _Float16* A, const _Float16* B, _Float16* C, int M, int N, int K, hipStream_t s) {
+    const int nm = (M + BM - 1) / BM, nn = N / BN;
+    hipLaunchKernelGGL((k_gemm_dma<BM, BN, BK, WM, WN, STAGES, SWZ, GROUP, XCD>), dim3(nm * nn),
+                       dim3(WM * WN * 64), 0, s, A, B, C, M, N, K, K, K, N);
+  }
+};
+
+template <int BM, int BN, int BK, int WM, int WN, int MS, int SWZ, int GROUP, int XCD>
+struct Reg {
+  static bool fits(int M, int N, int K) { (void)M; return N % BN == 0 && K % BK == 0; }
+  static void launch(const _Float16* A, const _Float16* B, _Float16* C, int M, int N, int K, hipStream_t s) {
+    const int nm = (M + BM - 1) / BM, nn = N / BN;
+    hipLaunchKernelGGL((k_gemm<BM, BN, BK, WM, WN, MS, SWZ, GROUP, XCD, 0>), dim3(nm * nn),
+                       dim3(WM * WN * 64), 0, s, A, (const void*)B, (const _Float16*)nullptr,
+                       (const uint8_t*)nullptr, C, M, N, K, K, K, N, 0);
+  }
+};
+
+#define DMA(tag, ...) Arm{tag, &Dma<__VA_ARGS__>::fits, &Dma<__VA_ARGS__>::launch},
+#define REG(tag, ...) Arm{tag, &Reg<__VA_ARGS__>::fits, &Reg<__VA_ARGS__>::launch},
+
+static const Arm kArms[] = {
+#include "configs.inc"
+};
+
+int main(int argc, char** argv) {
+  const int M = argc > 1 ? atoi(argv[1]) : 4096;
+  const int N = argc > 2 ? atoi(argv[2]) : 15360;
+  const int K = argc > 3 ? atoi(argv[3]) : 3840;
+  const int iters = argc > 4 ? atoi(argv[4]) : 50;
+  const long na = (long)M * K, nb = (long)N * K, nc = (long)M * N;
+  // rotate B through enough copies to exceed the 256 MiB Infinity Cache (>= 512 MiB of B)
+  const int nrot = std::max(1, (int)std::ceil(512.0 * 1024 * 1024 / (nb * 2.0)));
+  _Float16 *A, *C, *R;
+  std::vector<_Float16*> Bs(nrot);
+  CK(hipMalloc(&A, na * 2));
+  CK(hipMalloc(&C, nc * 2));
+  CK(hipMalloc(&R, nc * 2));
+  for (int i = 0; i < nrot; ++i) {
+    CK(hipMalloc(&Bs[i], nb * 2));
+    hipLaunchKernelGGL(k_fill, dim3(1024), dim3(256), 0, 0, Bs[i], nb, 77u, 2.f / sqrtf((float)K));
+  }
+  hipLaunchKernelGGL(k_fill, dim3(1024), dim3(256), 0, 0, A, na, 11u, 2.f);
+  hipLaunchKernelGGL(k_naive, dim3((N + 15) / 16, (M + 15) / 16), dim3(16, 16), 0, 0, A, Bs[0], R, M, N, K);
+  CK(hipDeviceSynchronize());
+  hipEvent_t e0, e1;
+  CK(hipEventCreate(&e0));
+  CK(hipEventCreate(&e1));
+  const double flop = 2.0 * M * N * K;
+  printf("SHAPE {\"M\":%d,\"N\":%d,\"K\":%d,\"rotate\":%d}\n", M, N, K, nrot);
+  fflush(stdout);
+  for (const Arm& arm : kArms) {
+    if (!arm.fits(M, N, K)) continue;
+    hipLaunchKernelGGL(k_fill_u16, dim3(1024), dim3(256), 0, 0, (unsigned short*)C, nc, (unsigned short)0x7f7f);
+    arm.launch(A, Bs[0], C, M, N, K, 0);
+    CK(hipGetLastError());
+    CK(hipDeviceSynchronize());
+    const unsigned long long left = poison_left(C, nc);
+    const double rel = rel_l2(C, R, nc);
+    if (left || !(rel <= 3e-3)) {
+      printf("FAILGATE {\"tag\":\"%s\",\"uncovered\":%llu,\"rel\":%.3e}\n", arm.tag, left, rel);
+      fflush(stdout);
+      continue;
+    }
+    for (int i = 0; i < 5; ++i) arm.launch(A, Bs[i % nrot], C, M, N, K, 0);
+    CK(hipDeviceSynchronize());
+    CK(hipEventRecord(e0, 0));
+    for (int i = 0; i < iters; ++i) arm.launch(A, Bs[i % nrot], C, M, N, K, 0);
+    CK(hipEventRecord(e1, 0));
+    CK(hipEventSynchronize(e1));
+    float ms = 0.f;
+    CK(hipEventElapsedTime(&ms, e0, e1));
+    const double t = ms / iters;
+    printf("CAND {\"tag\":\"%s\",\"M\":%d,\"N\":%d,\"K\":%d,\"us\":%.2f,\"tflops\":%.1f,\"rel\":%.2e}\n",
+           arm.tag, M, N, K, t * 1e3, flop / (t * 1e-3) / 1e12, rel);
+    fflush(stdout);
+  }
+  return 0;
+}

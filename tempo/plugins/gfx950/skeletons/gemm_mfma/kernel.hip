@@ -27,12 +27,22 @@
 // Requirements checked by the launcher (applicable()): N % BN == 0, K % BK == 0, 16-byte
 // aligned rows; M is predicated (rows past M are loaded from row M-1 and never stored).
 
+// LDS chunk swizzle: the 16-byte chunk c of tile row `row` is stored at chunk c ^ f(row).
+// SWZ 1: f = (row / rows-per-128B) % CPR -- spreads 8 consecutive rows over 32 banks.
+// SWZ 2: f = (row / rows-per-256B) % CPR -- spreads 16 consecutive rows over 64 banks.
 template <int BK, int SWZ>
 __device__ __forceinline__ int lds_chunk(int row, int chunk) {
   constexpr int CPR = BK / 8;  // 16-byte chunks per row
-  if constexpr (SWZ == 1) return chunk ^ (row & (CPR - 1));
-  else if constexpr (SWZ == 2) return chunk ^ ((row >> 1) & (CPR - 1));
-  else return chunk;
+  constexpr int ROW_BYTES = BK * 2;
+  if constexpr (SWZ == 1) {
+    constexpr int R128 = ROW_BYTES >= 128 ? 1 : 128 / ROW_BYTES;
+    return chunk ^ ((row / R128) & (CPR - 1));
+  } else if constexpr (SWZ == 2) {
+    constexpr int R256 = ROW_BYTES >= 256 ? 1 : 256 / ROW_BYTES;
+    return chunk ^ ((row / R256) & (CPR - 1));
+  } else {
+    return chunk;
+  }
 }
 
 // Tile order: block id -> (tile_m, tile_n).
@@ -233,6 +243,181 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm(
 #pragma unroll
       for (int g = 0; g < MF::GROUPS; ++g) {
         const int n = n0 + wn * Cfg::WTN + j * MS + mfma_out_row<MS>(lane, g, 0);
+        f16x4 o;
+        o[0] = (_Float16)acc[i][j][4 * g + 0];
+        o[1] = (_Float16)acc[i][j][4 * g + 1];
+        o[2] = (_Float16)acc[i][j][4 * g + 2];
+        o[3] = (_Float16)acc[i][j][4 * g + 3];
+        *reinterpret_cast<f16x4*>(C + (long)m * ldc + n) = o;
+      }
+    }
+  }
+}
+
+// ============================================================================================
+// k_gemm_dma -- fp16 B only.  Same tile, swizzle and epilogue as k_gemm, but the global -> LDS
+// copy is the gfx950 LDS-DMA load (global_load_lds_dwordx4): data goes straight from L2 into
+// LDS without passing through registers, the copy costs one instruction per 1 KiB per wave, and
+// STAGES-1 k-tiles are in flight while one is computed.
+//
+// One DMA instruction fills a contiguous 1 KiB of LDS, lane l writing bytes [16l, 16l+16).  The
+// swizzle is therefore applied on the GLOBAL side: lane l fetches the chunk that belongs at LDS
+// slot l.  Waits are explicit (s_waitcnt vmcnt(N) for this wave's own copies, then s_barrier
+// for everyone's); the compiler does not order LDS reads after LDS-DMA writes by itself.
+// ============================================================================================
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// s_waitcnt vmcnt(N) lgkmcnt(0).  gfx9 encoding: vmcnt[3:0] bits 3:0, expcnt bits 6:4,
+// lgkmcnt bits 11:8, vmcnt[5:4] bits 15:14.
+template <int N>
+__device__ __forceinline__ void s_wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0x0 << 8));
+}
+
+template <int BM, int BN, int BK, int WM, int WN, int STAGES, int SWZ, int GROUP, int XCD>
+__global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_dma(
+    const _Float16* __restrict__ A, const _Float16* __restrict__ B, _Float16* __restrict__ C,
+    int M, int N, int K, int lda, int ldb, int ldc) {
+  constexpr int MS = 32;
+  using MF = Mfma<MS>;
+  constexpr int NW = WM * WN;
+  constexpr int CPR = BK / 8;
+  constexpr int RPB = 1024 / (BK * 2);  // tile rows per 1 KiB DMA block
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int TM = WTM / MS, TN = WTN / MS;
+  constexpr int KS = BK / MF::KSTEP;
+  constexpr int A_BLK = BM / RPB / NW;  // DMA instructions per wave per stage
+  constexpr int B_BLK = BN / RPB / NW;
+  constexpr int L = A_BLK + B_BLK;
+  constexpr int STAGE_ELEMS = (BM + BN) * BK;
+  static_assert(BM % (RPB * NW) == 0 && BN % (RPB * NW) == 0, "DMA blocks per wave");
+  static_assert(STAGES >= 2 && (STAGES - 2) * L < 64, "stages / vmcnt range");
+  static_assert(WTM % MS == 0 && WTN % MS == 0 && BK % MF::KSTEP == 0, "tile shape");
+
+  __shared__ __attribute__((aligned(1024))) _Float16 smem[STAGES * STAGE_ELEMS];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+
+  const int nm = (M + BM - 1) / BM, nn = N / BN;
+  int tmi, tni;
+  tile_of<GROUP, XCD>(blockIdx.x, nm, nn, tmi, tni);
+  const int m0 = tmi * BM, n0 = tni * BN;
+
+  // per-lane global sources: DMA block i of this wave = tile block (i*NW + wave)
+  const _Float16* srcA[A_BLK];
+  const _Float16* srcB[B_BLK];
+  {
+    const int rin = lane / CPR, phys = lane % CPR;
+#pragma unroll
+    for (int i = 0; i < A_BLK; ++i) {
+      const int row = (i * NW + wave) * RPB + rin;
+      const int c = lds_chunk<BK, SWZ>(row, phys);  // involution: logical chunk of slot `phys`
+      srcA[i] = A + (long)min(m0 + row, M - 1) * lda + c * 8;
+    }
+#pragma unroll
+    for (int i = 0; i < B_BLK; ++i) {
+      const int row = (i * NW + wave) * RPB + rin;
+      const int c = lds_chunk<BK, SWZ>(row, phys);
+      srcB[i] = B + (long)(n0 + row) * ldb + c * 8;
+    }
+  }
+  auto issue = [&](int kt) {
+    const int st = kt % STAGES;
+    _Float16* sa = smem + st * STAGE_ELEMS;
+    _Float16* sb = sa + BM * BK;
+    const int k0 = kt * BK;
+#pragma unroll
+    for (int i = 0; i < A_BLK; ++i)
+      __builtin_amdgcn_global_load_lds((void*)(srcA[i] + k0),
+                                       (lds_void_t*)(sa + (i * NW + wave) * RPB * BK), 16, 0, 0);
+#pragma unroll
+    for (int i = 0; i < B_BLK; ++i)
+      __builtin_amdgcn_global_load_lds((void*)(srcB[i] + k0),
+                                       (lds_void_t*)(sb + (i * NW + wave) * RPB * BK), 16, 0, 0);
+  };
+
+  typename MF::acc_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v = 0; v < MF::NACC; ++v) acc[i][j][v] = 0.f;
+
+  const int fr = lane % MS, fk = lane / MS;
+  int aOff[TM], bOff[TN];  // row offsets (elements) of this lane's fragment rows
+#pragma unroll
+  for (int i = 0; i < TM; ++i) aOff[i] = (wm * WTM + i * MS + fr);
+#pragma unroll
+  for (int j = 0; j < TN; ++j) bOff[j] = (wn * WTN + j * MS + fr);
+
+  const int NT = K / BK;
+#pragma unroll
+  for (int s = 0; s < STAGES - 1; ++s)
+    if (s < NT) issue(s);
+
+  for (int kt = 0; kt < NT; ++kt) {
+    // this wave's copies of tile kt have landed (later tiles may still be in flight) ...
+    asm volatile("" ::: "memory");  // compiler-only fence: no LDS access crosses the barrier
+    if (kt + STAGES - 2 < NT) s_wait_vm<(STAGES - 2) * L>();
+    else s_wait_vm<0>();
+    // ... and everyone's have; everyone is also done reading the buffer about to be refilled
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (kt + STAGES - 1 < NT) issue(kt + STAGES - 1);
+
+    const _Float16* a = smem + (kt % STAGES) * STAGE_ELEMS;
+    const _Float16* b = a + BM * BK;
+    f16x8 fa[2][TM], fb[2][TN];
+    auto read = [&](auto bufc, int ks) {
+      constexpr int bb = decltype(bufc)::value;
+      const int chunk = ks * (64 / MS) + fk;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+        fa[bb][i] = *reinterpret_cast<const f16x8*>(a + aOff[i] * BK +
+                                                    lds_chunk<BK, SWZ>(aOff[i], chunk) * 8);
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        fb[bb][j] = *reinterpret_cast<const f16x8*>(b + bOff[j] * BK +
+                                                    lds_chunk<BK, SWZ>(bOff[j], chunk) * 8);
+    };
+    auto mma = [&](auto bufc) {
+      constexpr int bb = decltype(bufc)::value;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = MF::run(fb[bb][j], fa[bb][i], acc[i][j]);
+    };
+    // Fragment double buffer: the reads of step ks+1 are issued before the 16 MFMAs of step ks
+    // and the scheduler is not allowed to sink them (sched_barrier), so LDS latency hides
+    // under the matrix-core work instead of stalling every few MFMAs.
+    read(IC<0>{}, 0);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int ks = 0; ks < KS; ks += 2) {
+      if (ks + 1 < KS) read(IC<1>{}, ks + 1);
+      mma(IC<0>{});
+      __builtin_amdgcn_sched_barrier(0);
+      if (ks + 2 < KS) read(IC<0>{}, ks + 2);
+      if (ks + 1 < KS) mma(IC<1>{});
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  // ---- epilogue: each lane owns 4 consecutive n of one m per result group ----------------
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int m = m0 + wm * WTM + i * MS + (lane % MS);
+    if (m >= M) continue;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+#pragma unroll
+      for (int g = 0; g < MF::GROUPS; ++g) {
+        const int n = n0 + wn * WTN + j * MS + mfma_out_row<MS>(lane, g, 0);
         f16x4 o;
         o[0] = (_Float16)acc[i][j][4 * g + 0];
         o[1] = (_Float16)acc[i][j][4 * g + 1];

@@ -8,15 +8,17 @@
 // cores are >20x over-provisioned here; what they save is the VALU time a dot-product path
 // would spend on 2MNK multiply-adds, leaving the VALU to the dequantisation alone.
 //
-// Work unit = one wave: R groups of 16 weight rows x one K chunk.  A workgroup holds 4 units.
-// With S > 1 chunks per row slab the units write fp32 partials to a workspace and the last
-// unit to finish a slab (counted with an atomic per slab) sums the S partials in chunk order
-// 0..S-1 -- so the result does not depend on arrival order -- writes fp16 C and re-arms the
-// counter to zero for the next call.
+// One workgroup = one slab of 16*R weight rows; its S waves split K into S contiguous chunks
+// (S = blockDim.x / 64).  At the end the waves add their partial sums through LDS in wave order
+// 0..S-1 (deterministic) and wave 0 writes fp16 C.  No global workspace and no cross-workgroup
+// synchronisation: on this part an agent-scope fence is an L2 write-back + invalidate of the
+// whole XCD, which per-wave split-K reductions through global memory would pay every time.
 //
-// Template axes: MB (16-column blocks of M: M <= 16*MB), R (row groups per wave), U (k-steps
-// of 64 loaded per pipeline stage), BFMT (0 fp16, 1 int8 + row scale, 2 uint8 + group scale
-// and zero-point, group 128).
+// Template axes: MB (16-column blocks of M: M <= 16*MB), R (row groups per wave; each activation
+// fragment feeds R row groups, so activation traffic is 1/R of the one-group-per-wave form), U
+// (k-steps of 64 per pipeline stage), BFMT (0 fp16, 1 int8 + row scale, 2 uint8 + group scale
+// and zero-point with group 128: the stage's scales and zero-points for its 64*U/128 groups
+// arrive with one small load each, in flight together with the weights).
 //
 // k order inside one 64-step: lane (row r = l%16, kgroup g = l/16) owns the 16 consecutive
 // k-values [16g, 16g+16) of its row; the first MFMA takes elements 0..7, the second 8..15.
@@ -28,13 +30,49 @@ struct StreamArgs {
   const _Float16* scale;
   const uint8_t* zero;
   _Float16* C;         // [M][ldc]
-  float* ws;           // [S][M][N] fp32 partials (S > 1 only)
-  unsigned* counters;  // [N / (16R)] arrival counters, zero between calls (S > 1 only)
   int M, N, K, lda, ldb, ldc;
-  int S;               // k chunks per slab
-  int chunk;           // k per chunk (multiple of 64*U, except the last chunk)
+  int S;               // waves per workgroup = k chunks per slab
+  int chunk;           // k per chunk (multiple of 64*U; K is a multiple of 64*U too)
   int group;           // k per scale group (fmt 2)
 };
+
+// Group-wise metadata of one stage for one lane's row (fmt 2, group 128): GPS = 64*U/128 groups.
+template <int GPS>
+struct GMeta;
+template <>
+struct GMeta<1> { uint8_t z; uint16_t s; };
+template <>
+struct GMeta<2> { uint16_t z; uint32_t s; };
+template <>
+struct GMeta<4> { uint32_t z; u32x2 s; };
+
+template <int GPS>
+__device__ __forceinline__ void gmeta_load(GMeta<GPS>& g, const uint8_t* z, const _Float16* s) {
+  if constexpr (GPS == 1) {
+    g.z = *z;
+    g.s = *reinterpret_cast<const uint16_t*>(s);
+  } else if constexpr (GPS == 2) {
+    g.z = *reinterpret_cast<const uint16_t*>(z);
+    g.s = *reinterpret_cast<const uint32_t*>(s);
+  } else {
+    g.z = *reinterpret_cast<const uint32_t*>(z);
+    g.s = *reinterpret_cast<const u32x2*>(s);
+  }
+}
+
+template <int GPS>
+__device__ __forceinline__ void gmeta_get(const GMeta<GPS>& g, int i, uint8_t& z, _Float16& s) {
+  if constexpr (GPS == 1) {
+    z = g.z;
+    s = __builtin_bit_cast(_Float16, g.s);
+  } else if constexpr (GPS == 2) {
+    z = (uint8_t)(g.z >> (8 * i));
+    s = __builtin_bit_cast(_Float16, (uint16_t)(g.s >> (16 * i)));
+  } else {
+    z = (uint8_t)(g.z >> (8 * i));
+    s = __builtin_bit_cast(_Float16, (uint16_t)(g.s[i >> 1] >> (16 * (i & 1))));
+  }
+}
 
 template <int BFMT>
 struct WRaw;  // per lane, per row group, per 64-step: the 16 k-values of its row
@@ -45,15 +83,21 @@ struct WRaw<1> { u32x4 v; };     // 16 bytes int8
 template <>
 struct WRaw<2> { u32x4 v; };     // 16 bytes uint8
 
-template <int MB, int R, int U, int BFMT>
-__global__ __launch_bounds__(256) void k_stream(StreamArgs p) {
+// ALDS = 1: the workgroup first copies A[0..M)[0..K) into LDS (row stride 2K+16 bytes, so the 16
+// rows of one fragment read land in 16 distinct bank groups) and the k-loop reads activation
+// fragments from there -- one weight load per k-step instead of one weight + two activation
+// loads, and for M = 1 the 16 lanes of a k-group read one address (an LDS broadcast).  Chosen by
+// the launcher when M*(2K+16) bytes fit its LDS budget.
+template <int MB, int R, int U, int BFMT, int ALDS = 0>
+__global__ __launch_bounds__(512) void k_stream(StreamArgs p) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t dsm_s[];
+  const long arow_bytes = 2L * p.K + 16;
+  const long act_bytes = ALDS ? (long)p.M * arow_bytes : 0;
+  f32x4* red = reinterpret_cast<f32x4*>(dsm_s + act_bytes);  // [S][R*MB][64] partials
   const int lane = threadIdx.x & 63;
-  const int unit = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int slabs = p.N / (16 * R);
-  if (unit >= slabs * p.S) return;  // whole-wave exit: no barrier in this kernel
-  const int slab = unit / p.S;
-  const int split = unit - slab * p.S;
-  const int kbeg = split * p.chunk;
+  const int split = threadIdx.x >> 6;
+  const int slab = blockIdx.x;
+  const int kbeg = min(p.K, split * p.chunk);
   const int kend = min(p.K, kbeg + p.chunk);
 
   const int r16 = lane & 15;  // row within a 16-row group / column within a 16-col block
@@ -72,51 +116,81 @@ __global__ __launch_bounds__(256) void k_stream(StreamArgs p) {
   }
   // activation row pointers (rows past M read row M-1; their results are never stored)
   const _Float16* arow[MB];
+  const uint8_t* alds[MB];
 #pragma unroll
   for (int b = 0; b < MB; ++b) {
     const int m = min(b * 16 + r16, p.M - 1);
     arow[b] = p.A + (long)m * p.lda + 16 * kg;
+    alds[b] = dsm_s + m * arow_bytes + 32 * kg;
+  }
+  if constexpr (ALDS) {
+    const int cpr = p.K / 8;  // 16-byte chunks per activation row
+    for (int i = threadIdx.x; i < p.M * cpr; i += blockDim.x) {
+      const int m = i / cpr, c = i - m * cpr;
+      *reinterpret_cast<u32x4*>(dsm_s + m * arow_bytes + c * 16) =
+          *reinterpret_cast<const u32x4*>(p.A + (long)m * p.lda + c * 8);
+    }
+    __syncthreads();
   }
 
-  f32x4 acc[R][MB];
+  f32x4 acc[R][MB], acc2[R][MB];
 #pragma unroll
   for (int r = 0; r < R; ++r)
 #pragma unroll
-    for (int b = 0; b < MB; ++b) acc[r][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int b = 0; b < MB; ++b) {
+      acc[r][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+      acc2[r][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
 
   WRaw<BFMT> w[2][U][R];
-  u32x4 a[2][U][MB][2];
+  u32x4 a[2][U][MB][ALDS ? 1 : 2];
+  constexpr int GPS = (64 * U) / 128 > 0 ? (64 * U) / 128 : 1;  // groups per stage (fmt 2)
+  GMeta<GPS> gm[2][R];
+  const long gstride = BFMT == 2 ? (long)(p.K / 128) : 0;  // groups per weight row
 
+  // Every stage is whole: K and the chunk are multiples of 64*U (checked by the launcher), so
+  // the loads carry no predicate and the compiler can wait for exactly the stage it consumes.
   auto issue = [&](auto bufc, int k0) {
     constexpr int buf = decltype(bufc)::value;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int k = k0 + 64 * u;
-      const bool live = k < kend;
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         if constexpr (BFMT == 0) {
           const u32x4* q = reinterpret_cast<const u32x4*>(wrow[r] + (long)k * 2);
-          if (live) { w[buf][u][r].v[0] = q[0]; w[buf][u][r].v[1] = q[1]; }
+          w[buf][u][r].v[0] = q[0];
+          w[buf][u][r].v[1] = q[1];
         } else {
-          const u32x4* q = reinterpret_cast<const u32x4*>(wrow[r] + k);
-          if (live) w[buf][u][r].v = q[0];
+          w[buf][u][r].v = *reinterpret_cast<const u32x4*>(wrow[r] + k);
         }
       }
+      if constexpr (BFMT == 2) {
+        if (u == 0) {
 #pragma unroll
-      for (int b = 0; b < MB; ++b) {
-        const u32x4* q = reinterpret_cast<const u32x4*>(arow[b] + k);
-        if (live) { a[buf][u][b][0] = q[0]; a[buf][u][b][1] = q[1]; }
+          for (int r = 0; r < R; ++r) {
+            const long gi = (long)(nbase + r * 16 + r16) * gstride + k0 / 128;
+            gmeta_load<GPS>(gm[buf][r], p.zero + gi, p.scale + gi);
+          }
+        }
+      }
+      if constexpr (!ALDS) {
+#pragma unroll
+        for (int b = 0; b < MB; ++b) {
+          const u32x4* q = reinterpret_cast<const u32x4*>(arow[b] + k);
+          a[buf][u][b][0] = q[0];
+          a[buf][u][b][1] = q[1];
+        }
       }
     }
   };
 
+  // two independent accumulator chains per (row group, column block): consecutive MFMAs never
+  // wait on each other's result
   auto compute = [&](auto bufc, int k0) {
     constexpr int buf = decltype(bufc)::value;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int k = k0 + 64 * u;
-      if (k >= kend) break;
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         f16x8 w0, w1;
@@ -129,60 +203,79 @@ __global__ __launch_bounds__(256) void k_stream(StreamArgs p) {
           w1 = dequant8_i8(q[2], q[3], rscale[r]);
         } else {
           const u32x4 q = w[buf][u][r].v;
-          const long n = nbase + r * 16 + r16;
-          const long gi = n * (p.K / p.group) + (k + 16 * kg) / p.group;
-          const uint8_t z = p.zero[gi];
-          const _Float16 s = p.scale[gi];
+          uint8_t z;
+          _Float16 s;
+          gmeta_get<GPS>(gm[buf][r], (64 * u) / 128, z, s);
           w0 = dequant8_u8(q[0], q[1], z, s);
           w1 = dequant8_u8(q[2], q[3], z, s);
         }
 #pragma unroll
         for (int b = 0; b < MB; ++b) {
-          acc[r][b] = Mfma<16>::run(w0, as_f16x8(a[buf][u][b][0]), acc[r][b]);
-          acc[r][b] = Mfma<16>::run(w1, as_f16x8(a[buf][u][b][1]), acc[r][b]);
+          u32x4 a0, a1;
+          if constexpr (ALDS) {
+            const uint8_t* q = alds[b] + (long)(k0 + 64 * u) * 2;
+            a0 = *reinterpret_cast<const u32x4*>(q);
+            a1 = *reinterpret_cast<const u32x4*>(q + 16);
+          } else {
+            a0 = a[buf][u][b][0];
+            a1 = a[buf][u][b][1];
+          }
+          acc[r][b] = Mfma<16>::run(w0, as_f16x8(a0), acc[r][b]);
+          acc2[r][b] = Mfma<16>::run(w1, as_f16x8(a1), acc2[r][b]);
         }
       }
     }
   };
 
   // two-stage register pipeline: loads of stage s+1 are in flight while stage s computes.
-  // The loop is unrolled by two so every register-array index is a compile-time constant.
+  // Unrolled by two so every register-array index is a compile-time constant, and the steady
+  // state always issues before it computes (tail peeled), so the wait before each compute is
+  // "all but the stage just issued" on every path into it.
   constexpr int STEP = 64 * U;
   int k0 = kbeg;
-  issue(IC<0>{}, k0);
-  while (true) {
-    if (k0 + STEP < kend) issue(IC<1>{}, k0 + STEP);
+  int n = (kend - kbeg) / STEP;  // whole stages in this chunk (0 for a wave past K)
+  if (n > 0) issue(IC<0>{}, k0);
+  while (n >= 3) {
+    issue(IC<1>{}, k0 + STEP);
     compute(IC<0>{}, k0);
-    k0 += STEP;
-    if (k0 >= kend) break;
-    if (k0 + STEP < kend) issue(IC<0>{}, k0 + STEP);
-    compute(IC<1>{}, k0);
-    k0 += STEP;
-    if (k0 >= kend) break;
+    issue(IC<0>{}, k0 + 2 * STEP);
+    compute(IC<1>{}, k0 + STEP);
+    k0 += 2 * STEP;
+    n -= 2;
   }
+  if (n == 2) {
+    issue(IC<1>{}, k0 + STEP);
+    compute(IC<0>{}, k0);
+    compute(IC<1>{}, k0 + STEP);
+  } else if (n == 1) {
+    compute(IC<0>{}, k0);
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int b = 0; b < MB; ++b) acc[r][b] += acc2[r][b];
 
   // ---- result: lane holds C[m = b*16 + r16][n = nbase + r*16 + 4*kg + v], v = 0..3 ----------
-  if (p.S == 1) {
+  if (p.S > 1) {
+    // partials of every wave through LDS; summed in wave order by wave 0
 #pragma unroll
-    for (int b = 0; b < MB; ++b) {
-      const int m = b * 16 + r16;
-      if (m >= p.M) continue;
+    for (int r = 0; r < R; ++r)
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const int n = nbase + r * 16 + 4 * kg;
-        f16x4 o;
-        o[0] = (_Float16)acc[r][b][0];
-        o[1] = (_Float16)acc[r][b][1];
-        o[2] = (_Float16)acc[r][b][2];
-        o[3] = (_Float16)acc[r][b][3];
-        *reinterpret_cast<f16x4*>(p.C + (long)m * p.ldc + n) = o;
+      for (int b = 0; b < MB; ++b) red[(split * R * MB + r * MB + b) * 64 + lane] = acc[r][b];
+    __syncthreads();
+    if (split != 0) return;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int b = 0; b < MB; ++b) {
+        f32x4 t = red[(r * MB + b) * 64 + lane];
+        for (int w = 1; w < p.S; ++w) {
+          const f32x4 v = red[(w * R * MB + r * MB + b) * 64 + lane];
+          t[0] += v[0]; t[1] += v[1]; t[2] += v[2]; t[3] += v[3];
+        }
+        acc[r][b] = t;
       }
-    }
-    return;
   }
-
-  // split-K: publish this chunk's partial, then the last arrival reduces the slab.
-  const long plane = (long)p.M * p.N;
 #pragma unroll
   for (int b = 0; b < MB; ++b) {
     const int m = b * 16 + r16;
@@ -190,36 +283,14 @@ __global__ __launch_bounds__(256) void k_stream(StreamArgs p) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int n = nbase + r * 16 + 4 * kg;
-      *reinterpret_cast<f32x4*>(p.ws + split * plane + (long)m * p.N + n) = acc[r][b];
-    }
-  }
-  __threadfence();
-  unsigned prev = 0;
-  if (lane == 0) prev = atomicAdd(p.counters + slab, 1u);
-  prev = __shfl(prev, 0);
-  if (prev != (unsigned)(p.S - 1)) return;
-  __threadfence();
-#pragma unroll
-  for (int b = 0; b < MB; ++b) {
-    const int m = b * 16 + r16;
-    if (m >= p.M) continue;
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int n = nbase + r * 16 + 4 * kg;
-      f32x4 s = {0.f, 0.f, 0.f, 0.f};
-      for (int sp = 0; sp < p.S; ++sp) {
-        const f32x4 v = *reinterpret_cast<const f32x4*>(p.ws + sp * plane + (long)m * p.N + n);
-        s[0] += v[0]; s[1] += v[1]; s[2] += v[2]; s[3] += v[3];
-      }
       f16x4 o;
-      o[0] = (_Float16)s[0];
-      o[1] = (_Float16)s[1];
-      o[2] = (_Float16)s[2];
-      o[3] = (_Float16)s[3];
+      o[0] = (_Float16)acc[r][b][0];
+      o[1] = (_Float16)acc[r][b][1];
+      o[2] = (_Float16)acc[r][b][2];
+      o[3] = (_Float16)acc[r][b][3];
       *reinterpret_cast<f16x4*>(p.C + (long)m * p.ldc + n) = o;
     }
   }
-  if (lane == 0) p.counters[slab] = 0u;  // re-arm for the next call on this workspace
 }
 
 // Debug/verification entry: dequantise a [rows x cols] tile of B starting at (n0, k0) with the
@@ -244,4 +315,242 @@ __global__ void k_dequant_tile(StreamArgs p, int n0, int k0, int rows, int cols,
     v = dequant8_u8(q[0], q[1], p.zero[gi], p.scale[gi]);
   }
   *reinterpret_cast<f16x8*>(out + (long)r * cols + c8 * 8) = v;
+}
+
+// ============================================================================================
+// k_stream_dma -- same operation, work split and reduction as k_stream, but everything a k-step
+// consumes travels HBM/L2 -> LDS with the gfx950 LDS-DMA load (global_load_lds_dwordx4) into a
+// PRIVATE ring of D k-steps per wave: R*(1|2) KiB of weights and 2*MB KiB of activation
+// fragments per step.  Bytes in flight cost no registers, and because every k-step issues the
+// same instructions, one constant wait -- s_waitcnt vmcnt((D-1) * per-step count) -- is exactly
+// "step j has landed" (vmcnt retires in issue order, so a shorter-distance load of any kind
+// would cap the depth of the weight prefetch; that is why the activations ride the ring too).
+//
+// Per wave, iteration j:  wait for step j;  ds_read slot j % D -> registers;  lgkmcnt(0);
+// DMA step j+D into slot j % D (past the chunk's end the index clamps to the last step: a
+// redundant L2 hit that keeps the count constant);  dequantise + MFMA.
+//
+// DMA lane map: lane l fetches the 16 bytes of the operand fragment it will consume (row
+// l % 16, k-group l / 16), LDS-DMA stores lane l's 16 bytes at byte 16*l of the 1 KiB block,
+// and lane l reads back exactly those bytes: the ring is a latency buffer, not a shuffle.
+// fmt 2 scale/zero-points of the wave's whole chunk are staged in LDS once, before the loop.
+// ============================================================================================
+typedef __attribute__((address_space(3))) void lds_void_stream_t;
+
+template <int N>
+__device__ __forceinline__ void s_wait_vm_stream() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+template <int MB, int R, int D, int BFMT>
+struct StreamDma {
+  static constexpr int WB = BFMT == 0 ? 2 : 1;  // weight bytes per element
+  static constexpr int LD = R * WB;              // weight DMA instructions (1 KiB) per step
+  static constexpr int LA = 2 * MB;              // activation DMA instructions per step
+  static constexpr int SLOT = (LD + LA) * 1024;  // ring slot bytes
+  static constexpr int WAIT = (D - 1) * (LD + LA);
+  static constexpr int META_GROUPS = 64;         // fmt 2: groups staged per wave (chunk <= 8192 k)
+  static constexpr int META = BFMT == 2 ? R * 16 * META_GROUPS * 3 : 0;  // z (1 B) + s (2 B)
+  static constexpr int WAVE_BYTES = D * SLOT + META;
+  static_assert(WAIT < 64, "ring too deep for vmcnt");
+  static constexpr size_t lds(int S) {
+    return (size_t)S * WAVE_BYTES + (S > 1 ? (size_t)S * R * MB * 64 * 16 : 0);
+  }
+};
+
+template <int MB, int R, int D, int BFMT>
+__global__ __launch_bounds__(512) void k_stream_dma(StreamArgs p) {
+  using SD = StreamDma<MB, R, D, BFMT>;
+  constexpr int WB = SD::WB, LD = SD::LD, SLOT = SD::SLOT;
+  extern __shared__ __attribute__((aligned(1024))) uint8_t dsm[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int slab = blockIdx.x;
+  uint8_t* ring = dsm + (size_t)wave * SD::WAVE_BYTES;
+  uint8_t* meta = ring + D * SLOT;  // fmt 2: [R*16 rows][64 groups] z, then s
+  f32x4* red = reinterpret_cast<f32x4*>(dsm + (size_t)p.S * SD::WAVE_BYTES);
+
+  const int kbeg = min(p.K, wave * p.chunk);
+  const int kend = min(p.K, kbeg + p.chunk);
+  const int n = (kend - kbeg) / 64;  // k-steps of this wave (>= 1 by construction of S)
+  const int r16 = lane & 15, kg = lane >> 4;
+  const int nbase = slab * 16 * R;
+
+  const uint8_t* wsrc[R];
+  _Float16 rscale[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const long row = nbase + r * 16 + r16;
+    wsrc[r] = reinterpret_cast<const uint8_t*>(p.B) + (row * p.ldb + kbeg + 16 * kg) * WB;
+    if constexpr (BFMT == 1) rscale[r] = p.scale[row];
+  }
+  const _Float16* asrc[MB];
+#pragma unroll
+  for (int b = 0; b < MB; ++b) asrc[b] = p.A + (long)min(b * 16 + r16, p.M - 1) * p.lda + kbeg + 16 * kg;
+
+  if constexpr (BFMT == 2) {
+    // stage this wave's scale/zero-points: R*16 rows x G groups (G = chunk/128 <= 64)
+    const int g0 = kbeg / 128, G = (kend - 1) / 128 - g0 + 1;  // groups the chunk touches
+    const long gstride = p.K / 128;
+    for (int i = lane; i < R * 16 * G; i += 64) {
+      const int row = i / G, g = i - row * G;
+      const long gi = (long)(nbase + row) * gstride + g0 + g;
+      meta[row * SD::META_GROUPS + g] = p.zero[gi];
+      reinterpret_cast<_Float16*>(meta + R * 16 * SD::META_GROUPS)[row * SD::META_GROUPS + g] = p.scale[gi];
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // staged before any DMA is counted
+  }
+
+  f32x4 acc[R][MB];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int b = 0; b < MB; ++b) acc[r][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto dma = [&](int j) {  // step j (clamped) -> ring slot j % D
+    const int jj = min(j, n - 1);
+    uint8_t* slot = ring + (j % D) * SLOT;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int h = 0; h < WB; ++h)
+        __builtin_amdgcn_global_load_lds((void*)(wsrc[r] + (long)jj * 64 * WB + 16 * h),
+                                         (lds_void_stream_t*)(slot + (r * WB + h) * 1024), 16, 0, 0);
+#pragma unroll
+    for (int b = 0; b < MB; ++b)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        __builtin_amdgcn_global_load_lds((void*)(asrc[b] + jj * 64 + 8 * h),
+                                         (lds_void_stream_t*)(slot + (LD + 2 * b + h) * 1024), 16, 0, 0);
+  };
+
+  for (int j = 0; j < D; ++j) dma(j);
+  for (int j = 0; j < n; ++j) {
+    asm volatile("" ::: "memory");
+    s_wait_vm_stream<SD::WAIT>();  // step j has landed
+    asm volatile("" ::: "memory");
+    const uint8_t* slot = ring + (j % D) * SLOT;
+    u32x4 w[R][WB], av[MB][2];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int h = 0; h < WB; ++h)
+        w[r][h] = *reinterpret_cast<const u32x4*>(slot + (r * WB + h) * 1024 + 16 * lane);
+#pragma unroll
+    for (int b = 0; b < MB; ++b)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        av[b][h] = *reinterpret_cast<const u32x4*>(slot + (LD + 2 * b + h) * 1024 + 16 * lane);
+    uint8_t zc[R];
+    _Float16 sc[R];
+    if constexpr (BFMT == 2) {
+      const int g = (kbeg + j * 64) / 128 - kbeg / 128;  // group of this step in the stage
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        zc[r] = meta[(r * 16 + r16) * SD::META_GROUPS + g];
+        sc[r] = reinterpret_cast<const _Float16*>(meta + R * 16 * SD::META_GROUPS)[(r * 16 + r16) * SD::META_GROUPS + g];
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): operands are in registers, slot is free
+    asm volatile("" ::: "memory");
+    dma(j + D);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      f16x8 w0, w1;
+      if constexpr (BFMT == 0) {
+        w0 = as_f16x8(w[r][0]);
+        w1 = as_f16x8(w[r][1]);
+      } else if constexpr (BFMT == 1) {
+        w0 = dequant8_i8(w[r][0][0], w[r][0][1], rscale[r]);
+        w1 = dequant8_i8(w[r][0][2], w[r][0][3], rscale[r]);
+      } else {
+        w0 = dequant8_u8(w[r][0][0], w[r][0][1], zc[r], sc[r]);
+        w1 = dequant8_u8(w[r][0][2], w[r][0][3], zc[r], sc[r]);
+      }
+#pragma unroll
+      for (int b = 0; b < MB; ++b) {
+        acc[r][b] = Mfma<16>::run(w0, as_f16x8(av[b][0]), acc[r][b]);
+        acc[r][b] = Mfma<16>::run(w1, as_f16x8(av[b][1]), acc[r][b]);
+      }
+    }
+    (void)zc;
+    (void)sc;
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // no LDS-DMA write may outlive this workgroup's LDS
+  asm volatile("" ::: "memory");
+
+  if (p.S > 1) {
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int b = 0; b < MB; ++b) red[(wave * R * MB + r * MB + b) * 64 + lane] = acc[r][b];
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int b = 0; b < MB; ++b) {
+        f32x4 t = red[(r * MB + b) * 64 + lane];
+        for (int w = 1; w < p.S; ++w) {
+          const f32x4 v = red[(w * R * MB + r * MB + b) * 64 + lane];
+          t[0] += v[0]; t[1] += v[1]; t[2] += v[2]; t[3] += v[3];
+        }
+        acc[r][b] = t;
+      }
+  }
+#pragma unroll
+  for (int b = 0; b < MB; ++b) {
+    const int m = b * 16 + r16;
+    if (m >= p.M) continue;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int nn = nbase + r * 16 + 4 * kg;
+      f16x4 o;
+      o[0] = (_Float16)acc[r][b][0];
+      o[1] = (_Float16)acc[r][b][1];
+      o[2] = (_Float16)acc[r][b][2];
+      o[3] = (_Float16)acc[r][b][3];
+      *reinterpret_cast<f16x4*>(p.C + (long)m * p.ldc + nn) = o;
+    }
+  }
+}
+
+template <int MB, int R, int D, int BFMT>
+constexpr size_t stream_dma_lds(int S) {
+  return StreamDma<MB, R, D, BFMT>::lds(S);
+}
+
+// Streaming-read probe: each wave streams its share of `bytes` through a private LDS-DMA ring
+// of D KiB (no compute) and folds one dword per step into an output, so nothing is optimised
+// away.  Measures the read bandwidth this part sustains with the ring discipline.
+template <int D>
+__global__ __launch_bounds__(256) void k_read_probe(const uint8_t* src, long bytes_per_wave,
+                                                    unsigned* out) {
+  __shared__ __attribute__((aligned(1024))) uint8_t ring_all[4 * D * 1024];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const long gw = (long)blockIdx.x * 4 + wave;
+  uint8_t* ring = ring_all + wave * D * 1024;
+  const uint8_t* base = src + gw * bytes_per_wave + 16 * lane;
+  const int n = (int)(bytes_per_wave / 1024);
+  unsigned accum = 0;
+  auto dma = [&](int j) {
+    const int jj = min(j, n - 1);
+    __builtin_amdgcn_global_load_lds((void*)(base + (long)jj * 1024),
+                                     (lds_void_stream_t*)(ring + (j % D) * 1024), 16, 0, 0);
+  };
+  for (int j = 0; j < D; ++j) dma(j);
+  for (int j = 0; j < n; ++j) {
+    asm volatile("" ::: "memory");
+    s_wait_vm_stream<D - 1>();
+    asm volatile("" ::: "memory");
+    accum += *reinterpret_cast<const unsigned*>(ring + (j % D) * 1024 + 16 * lane);
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    asm volatile("" ::: "memory");
+    dma(j + D);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  asm volatile("" ::: "memory");
+  if (accum == 0x9e3779b9u) out[0] = accum;  // practically never; keeps the reads alive
 }

@@ -1,0 +1,183 @@
+"""gfx950: SEARCH SPACE -- axes and legal hyperforms (reference pattern tempo/plugins/sm70/space.py).
+
+Four skeleton kinds, each a kernel family of tempo/plugins/gfx950/skeletons:
+  dma     gemm_mfma/k_gemm_dma      fp16 x fp16, LDS-DMA multi-stage pipeline (prefill, M > 32)
+  reg     gemm_mfma/k_gemm          any weight format, register-staged copy that can dequantise
+                                    on the way into LDS (W8A16 prefill, fp16 fallback)
+  ring    gemv_stream/k_stream_dma  decode (M <= 32): per-wave LDS-DMA ring of k-steps
+  stream  gemv_stream/k_stream      decode, register-staged prefetch (kept as a measured arm)
+
+Legality here means "compiles and launches": LDS within 160 KiB, tiles divide the shape, the
+vmcnt-counted depth fits the 6-bit counter.  Register pressure is NOT legality -- it is the
+resource verdict's business (tempo/plugins/gfx950/resources.py).
+"""
+from __future__ import annotations
+
+from typing import Iterator
+
+from ..base import Axis, Hyperform, OpSpec, PluginCapabilityError
+
+LDS_MAX = 160 * 1024
+MFMA_FLOPS = {32: 32 * 32 * 16 * 2, 16: 16 * 16 * 32 * 2}
+
+AXES = (
+    Axis("kind", frozenset({"LDS", "VMEM", "regs"})),
+    Axis("block_tile", frozenset({"LDS", "VMEM", "hbm", "waves"})),
+    Axis("wave_tile", frozenset({"LDS", "regs"})),
+    Axis("bk", frozenset({"LDS", "barriers"})),
+    Axis("stages", frozenset({"LDS", "latency"})),
+    Axis("swizzle", frozenset({"LDS"})),
+    Axis("group", frozenset({"l2", "hbm"})),
+    Axis("xcd", frozenset({"l2"})),
+    Axis("mfma_shape", frozenset({"MFMA", "regs"})),
+    Axis("rows_per_wave", frozenset({"VMEM", "regs"})),
+    Axis("ring_depth", frozenset({"LDS", "latency", "hbm"})),
+)
+
+DOMAINS = {
+    "dma": dict(BM=(128, 256), BN=(128, 192, 256), BK=(32, 64), STAGES=(2, 3, 4), SWZ=(0, 1, 2),
+                GROUP=(4, 8, 16), XCD=(0, 1)),
+    "reg": dict(BM=(64, 128, 256), BN=(128, 256), BK=(64,), MS=(16, 32), SWZ=(1, 2), GROUP=(8,),
+                XCD=(1,)),
+    "ring": dict(R=(1, 2, 4), D=(4, 5, 6, 8, 10, 12, 14, 16)),
+    "stream": dict(R=(1, 2, 4), U=(2, 4, 8)),
+}
+
+BFMT_OF = {("fp16", "fp16"): 0, ("fp16", "int8"): 1, ("fp16", "uint8"): 2}
+
+
+def bfmt(op: OpSpec) -> int:
+    key = (op.dtype_a, op.dtype_b)
+    if key not in BFMT_OF:
+        raise PluginCapabilityError("gfx950 skeletons take A fp16 with B fp16|int8|uint8; got %s x %s"
+                                    % key)
+    return BFMT_OF[key]
+
+
+def lds_bytes(kind: str, p: dict) -> int:
+    if kind == "dma":
+        return p["STAGES"] * (p["BM"] + p["BN"]) * p["BK"] * 2
+    if kind == "reg":
+        return 2 * (p["BM"] + p["BN"]) * p["BK"] * 2
+    if kind == "ring":
+        wb = 2 if p["BFMT"] == 0 else 1
+        per_wave = p["D"] * (p["R"] * wb + 2 * p["MB"]) * 1024 + (p["R"] * 16 * 64 * 3 if p["BFMT"] == 2 else 0)
+        return p.get("S", 1) * per_wave + (p.get("S", 1) * p["R"] * p["MB"] * 1024 if p.get("S", 1) > 1 else 0)
+    if kind == "stream":
+        return p.get("S", 1) * p["R"] * p["MB"] * 1024 if p.get("S", 1) > 1 else 0
+    raise KeyError(kind)
+
+
+def stream_split(N: int, K: int, R: int, step_k: int, bfmt_: int = 0, per_wave_lds: int = 0):
+    """Waves per workgroup S and k chunk, as the shipped launchers compute them."""
+    slabs = N // (16 * R)
+    steps = K // step_k
+    S = min(8, max(1, -(-2048 // max(1, slabs))), steps)
+    while bfmt_ == 2 and -(-K // S) > 8192 and S < 8:
+        S += 1
+
+    def fix(s_):
+        per = -(-steps // s_)
+        return -(-steps // per), per * step_k
+
+    S, chunk = fix(S)
+    while per_wave_lds and S > 1 and S * per_wave_lds > LDS_MAX:
+        S, chunk = fix(S - 1)
+    return S, chunk
+
+
+def tag(kind: str, p: dict) -> str:
+    if kind == "dma":
+        return "dma_m%dn%dk%d_w%dx%d_s%d_z%d_g%d_x%d" % (p["BM"], p["BN"], p["BK"], p["WM"], p["WN"],
+                                                      p["STAGES"], p["SWZ"], p["GROUP"], p["XCD"])
+    if kind == "reg":
+        return "reg_m%dn%dk%d_w%dx%d_f%d_z%d_b%d" % (p["BM"], p["BN"], p["BK"], p["WM"], p["WN"],
+                                                   p["MS"], p["SWZ"], p["BFMT"])
+    if kind == "ring":
+        return "ring_mb%d_r%d_d%d_b%d" % (p["MB"], p["R"], p["D"], p["BFMT"])
+    return "stream_mb%d_r%d_u%d_b%d" % (p["MB"], p["R"], p["U"], p["BFMT"])
+
+
+def legal(kind: str, p: dict, M: int, N: int, K: int):
+    """None when the hyperform compiles and launches for this shape, else the reason."""
+    if kind in ("dma", "reg"):
+        BM, BN, BK = p["BM"], p["BN"], p["BK"]
+        if N % BN or K % BK:
+            return "tile %dx%d does not divide N=%d / K=%d" % (BN, BK, N, K)
+        WM, WN = p["WM"], p["WN"]
+        ms = p.get("MS", 32)
+        if (BM // WM) % ms or (BN // WN) % ms:
+            return "wave tile not a multiple of the MFMA shape"
+        if kind == "dma":
+            rpb = 1024 // (BK * 2)
+            nw = WM * WN
+            if BM % (rpb * nw) or BN % (rpb * nw):
+                return "DMA blocks do not divide among waves"
+            L = (BM + BN) // (rpb * nw)
+            if (p["STAGES"] - 2) * L >= 64:
+                return "vmcnt depth"
+        if lds_bytes(kind, p) > LDS_MAX:
+            return "LDS %d B > 160 KiB" % lds_bytes(kind, p)
+        return None
+    R = p["R"]
+    if N % (16 * R):
+        return "N %% %d" % (16 * R)
+    if M > 16 * p["MB"]:
+        return "M > 16*MB"
+    if kind == "ring":
+        wb = 2 if p["BFMT"] == 0 else 1
+        if K % 64:
+            return "K % 64"
+        if (p["D"] - 1) * (R * wb + 2 * p["MB"]) >= 64:
+            return "vmcnt depth"
+        if p["D"] < 3:
+            return "ring depth < 3"
+        if lds_bytes(kind, dict(p, S=1)) > LDS_MAX:
+            return "LDS"
+        return None
+    if K % (64 * p["U"]):
+        return "K %% %d" % (64 * p["U"])
+    return None
+
+
+def variants(op: OpSpec) -> Iterator[Hyperform]:
+    if op.kind != "gemm":
+        raise PluginCapabilityError("gfx950 skeletons take 'gemm' in the pipeline; FMHA is a "
+                                    "fixed skeleton (skeletons/fmha_fwd), not a searched one")
+    M, N, K = int(op.shapes["M"]), int(op.shapes["N"]), int(op.shapes["K"])
+    b = bfmt(op)
+    out = []
+    if M <= 32:
+        MB = 1 if M <= 16 else 2
+        for R in DOMAINS["ring"]["R"]:
+            for D in DOMAINS["ring"]["D"]:
+                out.append(("ring", dict(MB=MB, R=R, D=D, BFMT=b)))
+        for R in DOMAINS["stream"]["R"]:
+            for U in DOMAINS["stream"]["U"]:
+                out.append(("stream", dict(MB=MB, R=R, U=U, BFMT=b)))
+    if b == 0:
+        d = DOMAINS["dma"]
+        for BM in d["BM"]:
+            for BN in d["BN"]:
+                for BK in d["BK"]:
+                    for ST in d["STAGES"]:
+                        for SW in d["SWZ"]:
+                            for G in d["GROUP"]:
+                                for X in d["XCD"]:
+                                    out.append(("dma", dict(BM=BM, BN=BN, BK=BK, WM=2, WN=2,
+                                                            STAGES=ST, SWZ=SW, GROUP=G, XCD=X)))
+    d = DOMAINS["reg"]
+    for BM in d["BM"]:
+        for BN in d["BN"]:
+            for MS in d["MS"]:
+                for SW in d["SWZ"]:
+                    out.append(("reg", dict(BM=BM, BN=BN, BK=64, WM=2, WN=2, MS=MS, SWZ=SW,
+                                            GROUP=8, XCD=1, BFMT=b)))
+    for kind, p in out:
+        if legal(kind, p, M, N, K) is None:
+            params = dict(p, kind=kind)
+            yield Hyperform(plugin="gfx950", params=params, key=tag(kind, p))
+
+
+def axes():
+    return AXES
