@@ -1,0 +1,286 @@
+#!/usr/bin/env python3
+"""Benchmark of the shipped gfx950 GEMM path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode]
+
+One step is one launch of the shipped gemm_fp16 (kernels/shipped/gemm_fp16/gfx950, reached
+through the C-ABI libtempo_gfx950.so) over configuration C1: C[4096,15360] = A[4096,3840] .
+B[15360,3840]^T, fp16 inputs N(0,1)/sqrt(K) from PCG64 seeds 11 / 77, fp32 accumulation, fp16
+output; inputs are resident in HBM before the timed region.  `value` is that kernel's TFLOP/s
+(2MNK flops per step).  Before timing, the output passes a correctness gate (no 0x7f7f poison
+left, fp64 dot products on 256 sampled cells within |got-ref|/(|ref|+1e-3) <= 3e-3, the rule of
+the reference's kernels/shipped/gemm_fp16/sm_70/ship_probe.cu:70-79).
+
+Extra fields of the one JSON line:
+  roofline      the C1 kernel against the fp16 dense MFMA peak; `achieved` from HIP events on
+                the launch stream; `traffic` (HBM bytes per launch) from the committed rocprofv3
+                --pmc summary profiles/gemm_fp16_c1_traffic.txt when present, else null.
+  cpu_baseline  the CPU restatement of the reference's naive kernel (oracle/, fp32 sequential-k
+                FMA per output, OpenMP) timed on this host over a bounded row sample of C1.
+  decode        HBM GB/s of the decode regime (M <= 32): gemm_w8a16 on both weight formats and
+                gemm_fp16 on the two C2 shapes, weights rotated through > 512 MiB so no launch
+                finds its weights in the 256 MiB Infinity Cache.
+  fmha          the causal FMHA forward at configuration C5, TFLOP/s.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, HERE)
+
+METRIC = ("GEMM TFLOP/s & % fp16 MFMA peak (prefill); HBM GB/s & % peak (decode M≤32)")
+PEAK_FP16_TFLOPS = 2516.6   # 256 CUs x 2.4 GHz x 4096 flop/clk (AMD dense fp16 figure)
+PEAK_HBM_GBPS = 8000.0      # MI355X HBM3E
+TRAFFIC_FILE = os.path.join(HERE, "profiles", "gemm_fp16_c1_traffic.txt")
+
+C1 = dict(M=4096, N=15360, K=3840)
+SEED_A, SEED_B = 11, 77
+
+
+def randn_f16(shape, seed, scale):
+    g = np.random.Generator(np.random.PCG64(seed))
+    return (g.standard_normal(shape, dtype=np.float32) * np.float32(scale)).astype(np.float16)
+
+
+def to_dev(x):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(x)).to("cuda:0")
+
+
+def time_launches(fn, steps, warmup, stream):
+    """Average ms per launch of fn(i) on `stream`, HIP events recorded on that same stream."""
+    import torch
+
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(steps):
+        fn(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def gate_c1(A, B, C):
+    """fp64 spot check of 256 sampled cells plus the poison count (numpy, independent of the
+    kernel and of the CPU oracle)."""
+    M, K = A.shape
+    N = B.shape[0]
+    Ch = C.view(np.uint16)
+    poison = int(np.count_nonzero(Ch == 0x7f7f))
+    t = np.arange(256)
+    m, n = (t * 37) % M, (t * 53) % N
+    ref = np.einsum("ik,ik->i", A[m].astype(np.float64), B[n].astype(np.float64))
+    got = C[m, n].astype(np.float64)
+    rel = np.abs(got - ref) / (np.abs(ref) + 1e-3)
+    return {"poison": poison, "spot_cells": 256, "spot_max": float(rel.max()),
+            "ok": bool(poison == 0 and rel.max() <= 3e-3)}
+
+
+def read_traffic():
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary, or None."""
+    if not os.path.exists(TRAFFIC_FILE):
+        return None
+    with open(TRAFFIC_FILE, encoding="utf-8") as f:
+        for line in f:
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(float(line.split(":", 1)[1]))
+    return None
+
+
+def cpu_baseline(A, B, budget_s=12.0):
+    """The oracle's fp32 sequential-k GEMM over C1 rows, repeated until about `budget_s` of
+    CPU work (a bounded sample of the workload)."""
+    from oracle import oracle as O
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or len(os.sched_getaffinity(0))
+    threads = min(threads, len(os.sched_getaffinity(0)))
+    N, K = B.shape
+    O.gemm_f16(A[:64], B, threads=threads)  # thread pool and page warm-up, not timed
+    t = time.perf_counter()
+    O.gemm_f16(A[:256], B, threads=threads)
+    rate = 2 * 256 * N * K / (time.perf_counter() - t)
+    rows = int(min(A.shape[0], max(256, budget_s * rate / (2 * N * K))))
+    rows -= rows % 8
+    reps = max(1, int(round(budget_s * rate / (2 * rows * N * K))))
+    t = time.perf_counter()
+    for _ in range(reps):
+        O.gemm_f16(A[:rows], B, threads=threads)
+    dt = time.perf_counter() - t
+    return {"value": round(2 * reps * rows * N * K / dt / 1e12, 5), "unit": "TFLOP/s",
+            "cores": threads, "kind": "port",
+            "sample": "C1 rows 0..%d (%dx%dx%d) x %d passes, %.1f s: oracle_gemm_f16, the C "
+                      "restatement of kernels/naive/gemm_fp16.cu:60-68 (fp32 sequential-k FMA "
+                      "per output, OpenMP over %d threads)" % (rows - 1, rows, N, K, reps, dt,
+                                                               threads)}
+
+
+def decode_lines(steps):
+    import torch
+    from cuda_tempiler_amd import capi
+
+    out = []
+    stream = torch.cuda.current_stream()
+    g = np.random.Generator(np.random.PCG64(3))
+
+    def rotate(nbytes):
+        return max(2, -(-(512 << 20) // nbytes) + 1)
+
+    # W8A16, both formats, shape (34816, 5120) and (5120, 17408)
+    for (N, K) in ((34816, 5120), (5120, 17408)):
+        for fmt in (1, 2):
+            G = 128
+            nb = N * K + (2 * N if fmt == 1 else 3 * N * K // G)
+            copies = rotate(nb)
+            W, S, Z = [], [], []
+            for c in range(copies):
+                if fmt == 1:
+                    W.append(torch.randint(-127, 128, (N, K), dtype=torch.int8, device="cuda:0"))
+                    S.append(torch.empty(N, dtype=torch.float16, device="cuda:0").uniform_(0.5, 1.5) / 127)
+                    Z.append(None)
+                else:
+                    W.append(torch.randint(0, 256, (N, K), dtype=torch.uint8, device="cuda:0"))
+                    S.append(torch.empty((N, K // G), dtype=torch.float16, device="cuda:0").uniform_(0.5, 1.5) / 255)
+                    Z.append(torch.randint(100, 157, (N, K // G), dtype=torch.uint8, device="cuda:0"))
+            for M in (1, 16, 32):
+                A = to_dev((g.standard_normal((M, K), dtype=np.float32) / np.sqrt(K)).astype(np.float16))
+                C = torch.empty((M, N), dtype=torch.float16, device="cuda:0")
+                fn = lambda i: capi.gemm_w8a16(A, W[i % copies], S[i % copies], Z[i % copies],
+                                               fmt=fmt, group=G, C=C, stream=stream)
+                ms = time_launches(fn, steps, max(10, steps // 5), stream)
+                byts = nb + 2 * M * K + 2 * M * N
+                gbps = byts / (ms * 1e-3) / 1e9
+                out.append({"op": "gemm_w8a16", "fmt": "sym_i8" if fmt == 1 else "asym_u8_g128",
+                            "M": M, "N": N, "K": K, "us": round(ms * 1e3, 2),
+                            "GBps": round(gbps, 1), "hbm_frac": round(gbps / PEAK_HBM_GBPS, 4),
+                            "route": capi.route(1 if fmt == 1 else 2, M, N, K)})
+            del W, S, Z
+    # fp16 decode (C2 shapes)
+    for (N, K) in ((15360, 3840), (3840, 15360)):
+        nb = 2 * N * K
+        copies = rotate(nb)
+        Bs = [torch.randn((N, K), dtype=torch.float16, device="cuda:0") for _ in range(copies)]
+        for M in (1, 8, 16, 32):
+            A = torch.randn((M, K), dtype=torch.float16, device="cuda:0")
+            C = torch.empty((M, N), dtype=torch.float16, device="cuda:0")
+            fn = lambda i: capi.gemm_fp16(A, Bs[i % copies], C, stream=stream)
+            ms = time_launches(fn, steps, max(10, steps // 5), stream)
+            byts = nb + 2 * M * K + 2 * M * N
+            gbps = byts / (ms * 1e-3) / 1e9
+            out.append({"op": "gemm_fp16", "M": M, "N": N, "K": K, "us": round(ms * 1e3, 2),
+                        "GBps": round(gbps, 1), "hbm_frac": round(gbps / PEAK_HBM_GBPS, 4),
+                        "route": capi.route(0, M, N, K)})
+        del Bs
+    return out
+
+
+def fmha_line(steps):
+    import torch
+    from cuda_tempiler_amd import capi
+
+    B, S, H, Hkv, D = 1, 4096, 16, 8, 256
+    Q = torch.randn((B, S, H, D), dtype=torch.float16, device="cuda:0")
+    K = torch.randn((B, S, Hkv, D), dtype=torch.float16, device="cuda:0")
+    V = torch.randn((B, S, Hkv, D), dtype=torch.float16, device="cuda:0")
+    O = torch.empty_like(Q)
+    L = torch.empty((B, H, S), dtype=torch.float32, device="cuda:0")
+    stream = torch.cuda.current_stream()
+    fn = lambda i: capi.fmha_fwd(Q, K, V, 1.0 / 16, True, O=O, LSE=L, stream=stream)
+    ms = time_launches(fn, steps, max(5, steps // 5), stream)
+    flops = 4 * D * B * H * S * (S + 1) // 2
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"op": "fmha_fwd", "config": "B=1 H=16 Hkv=8 S=4096 D=256 causal", "us": round(ms * 1e3, 1),
+            "TFLOPs": round(tf, 1), "mfma_frac": round(tf / PEAK_FP16_TFLOPS, 4)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-decode", action="store_true", help="skip the decode and FMHA lines")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="after the timed region, run a plain 1 GiB device copy three times (the "
+                         "known-size kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path (the GEMMs would "
+              "shard by N with no exchange; see the sharding notes of the design document). "
+              "Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import torch
+    from cuda_tempiler_amd import capi
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    capi.lib()  # loud failure if the HIP library is not built
+    M, N, K = C1["M"], C1["N"], C1["K"]
+    Ah = randn_f16((M, K), SEED_A, 1.0 / np.sqrt(K))
+    Bh = randn_f16((N, K), SEED_B, 1.0 / np.sqrt(K))
+    A, B = to_dev(Ah), to_dev(Bh)
+    C = torch.empty((M, N), dtype=torch.int16, device="cuda:0").fill_(0x7f7f).view(torch.float16)
+    stream = torch.cuda.Stream()  # default priority
+    with torch.cuda.stream(stream):
+        capi.gemm_fp16(A, B, C, stream=stream)
+    torch.cuda.synchronize()
+    gate = gate_c1(Ah, Bh, C.cpu().numpy())
+    if not gate["ok"]:
+        print(json.dumps({"error": "correctness gate failed", "gate": gate}), file=sys.stderr)
+        return 1
+
+    fn = lambda i: capi.gemm_fp16(A, B, C, stream=stream)
+    torch.cuda.synchronize()
+    ms = time_launches(fn, args.steps, args.warmup, stream)
+    flops = 2 * M * N * K
+    tflops = flops / (ms * 1e-3) / 1e12
+    traffic = read_traffic()
+    line = {
+        "metric": METRIC, "value": round(tflops, 1), "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
+        "data": "synthetic: A,B ~ N(0,1)/sqrt(K) fp16 from numpy PCG64 seeds 11/77",
+        "config": {"workload": "C1 dense fp16 GEMM C=A.B^T M=4096 N=15360 K=3840, fp32 accumulate",
+                   "kernel_row": capi.route(0, M, N, K), "parallelism": "single GPU"},
+        "gate": gate,
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": PEAK_FP16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / PEAK_FP16_TFLOPS, 4),
+                     "traffic": traffic,
+                     "algorithmic_bytes": 2 * (M * K + N * K + M * N)},
+    }
+    del C
+    if args.copy_calibration:
+        src = torch.empty(1 << 29, dtype=torch.float16, device="cuda:0").fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        line["copy_calibration_bytes"] = src.numel() * 2
+        del src, dst
+    if not args.no_decode:
+        torch.cuda.empty_cache()
+        line["decode"] = decode_lines(max(50, args.steps))
+        torch.cuda.empty_cache()
+        line["fmha"] = fmha_line(max(10, args.steps // 10))
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(Ah, Bh)
+    else:
+        line["cpu_baseline"] = None
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

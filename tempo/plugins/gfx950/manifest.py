@@ -1,0 +1,156 @@
+"""manifest.json of a shipped delivery (schema tempo/shipped/1, the reference's
+kernels/shipped/gemm_fp16/sm_70/manifest.json fields, written for gfx950).
+
+    python3 -m tempo.plugins.gfx950.manifest [--rows gpurun_out/rows_<op>.json ...]
+
+Static part, derived here on the CPU: the op, layout and predicate; the dispatch ladder (read
+from the delivery's own select.py); per ladder row the build numbers of OUR compile (VGPRs,
+AGPRs, spills, scratch, LDS from hipcc's resource remarks, MFMA count and LDS-DMA use from
+llvm-objdump), obtained by rendering the row's hyperform through the plugin and compiling it;
+and an md5 over EVERY file of the delivery (kernel.hip, launch.h, launch.hip, dispatch.inc,
+select.py), so no file ships unsigned.  Measured part: the rows written by
+tempo.plugins.gfx950.measure_shipped on an MI355X, with the card state before and after.
+"""
+from __future__ import annotations
+
+import argparse
+import hashlib
+import importlib.util
+import json
+import os
+import sys
+import tempfile
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.abspath(os.path.join(HERE, "..", "..", ".."))
+SHIPPED = os.path.join(ROOT, "kernels", "shipped")
+SIGNED = ("kernel.hip", "launch.h", "launch.hip", "dispatch.inc", "select.py")
+
+OPS = {
+    "gemm_fp16": dict(dtype="fp16 x fp16 -> fp16, fp32 accumulate",
+                      dtypes=("fp16", "fp16"), fmts=(0,)),
+    "gemm_w8a16": dict(dtype="fp16 x (int8 sym per-channel | uint8 asym group-128) -> fp16, "
+                             "dequantised to fp16 on the way into the MFMA feed, fp32 accumulate",
+                       dtypes=("fp16", "int8"), fmts=(1, 2)),
+}
+
+
+def _select(op):
+    path = os.path.join(SHIPPED, op, "gfx950", "select.py")
+    spec = importlib.util.spec_from_file_location("sel_" + op, path)
+    m = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(m)
+    return m
+
+
+def md5_of(op):
+    d = os.path.join(SHIPPED, op, "gfx950")
+    h = hashlib.md5()
+    for f in SIGNED:
+        with open(os.path.join(d, f), "rb") as fh:
+            h.update(f.encode() + b"\0" + fh.read())
+    return h.hexdigest()
+
+
+def build_numbers(op):
+    """Compile each ladder row's kernel alone (rendered by the plugin) and read our numbers."""
+    sys.path.insert(0, ROOT)
+    from tempo.plugins.base import Hyperform, OpSpec
+    from tempo.plugins.gfx950 import load
+    from tempo.plugins.gfx950.toolchain import isa_summary
+    from tempo.plugins.gfx950.classifier import parse_disasm
+
+    plug = load()
+    sel = _select(op)
+    out = {}
+    for fmt in OPS[op]["fmts"]:
+        db = {0: "fp16", 1: "int8", 2: "uint8"}[fmt]
+        spec = OpSpec(kind="gemm", dtype_a="fp16", dtype_b=db, dtype_c="fp16", dtype_acc="fp32",
+                      layout_a="k", layout_b="k", layout_c="n",
+                      shapes={"M": 4096, "N": 15360, "K": 3840})
+        for m_max, tag, kind, p in sel.LADDER:
+            pk = {"stream": "stream", "mfma": "reg", "dma": "dma"}[kind]
+            params = dict(p, kind=pk)
+            if pk != "dma":
+                params["BFMT"] = fmt
+            h = Hyperform(plugin="gfx950", params=params, key="%s_f%d" % (tag, fmt))
+            r = plug.skeletons.render(spec, h)
+            with tempfile.TemporaryDirectory() as td:
+                src = os.path.join(td, r.filename)
+                with open(src, "w") as f:
+                    f.write(r.source)
+                obj = os.path.join(td, "k.o")
+                b = plug.toolchain.compile(src, obj, mode="device")
+                if not b.ok:
+                    raise RuntimeError("row %s does not compile:\n%s" % (tag, b.log[-3000:]))
+                isa = isa_summary(sum(parse_disasm(plug.toolchain.disasm(obj)).values(), []))
+            key = tag if len(OPS[op]["fmts"]) == 1 else "%s/fmt%d" % (tag, fmt)
+            out[key] = dict(tag=tag, kind=kind, regs=b.regs, vgpr_spill=b.spill_st,
+                            sgpr_spill=b.spill_ld, scratch_bytes_per_lane=b.stack_frame,
+                            lds_static=b.smem_static, mfma=isa["mfma"], lds_dma=isa["lds_dma"],
+                            ds_read_b128=isa["ds_read_b128"], scratch_insts=isa["scratch"])
+    return out
+
+
+def make(op, rows_files=()):
+    sel = _select(op)
+    d = os.path.join(SHIPPED, op, "gfx950")
+    path = os.path.join(d, "manifest.json")
+    old = {}
+    if os.path.exists(path):
+        with open(path) as f:
+            old = json.load(f)
+    man = {
+        "schema": "tempo/shipped/1",
+        "op": "gemm" if op == "gemm_fp16" else "gemm_w8a16",
+        "arch": "gfx950",
+        "dtype": OPS[op]["dtype"],
+        "layout": "C = A . B^T, both operands k-contiguous (row-major [M,K] and [N,K]), C [M,N]",
+        "predicate": {
+            "alignment": "A, B 16 B; C 8 B; lda, ldb multiples of 8 elements, ldc of 4",
+            "M": "any (rows beyond M are predicated in the tiled kernels)",
+            "per_row_fit": "see dispatch[].fit",
+            "fallback": "hipErrorInvalidConfiguration (TEMPO_FALLBACK): the caller's own path",
+        },
+        "dispatch": [],
+        "build": build_numbers(op),
+        "source_md5": md5_of(op),
+        "source_md5_of": list(SIGNED),
+        "rows": old.get("rows", []),
+        "card": old.get("card", None),
+    }
+    for m_max, tag, kind, p in sel.LADDER:
+        if kind == "stream":
+            fit = "N %% %d == 0 and K %% %d == 0" % (sel.STREAM_N_ROWS * p["R"],
+                                                    sel.STREAM_K_STEP * p["U"])
+        else:
+            fit = "N %% %d == 0 and K %% %d == 0" % (p["BN"], p["BK"])
+        man["dispatch"].append(dict(M_max=m_max, tag=tag, kind=kind, params=p, fit=fit))
+    if op == "gemm_w8a16":
+        man["predicate"]["formats"] = {"1": "int8 weights, fp16 scale per output channel",
+                                       "2": "uint8 weights, fp16 scale + uint8 zero per (row, 128 k)"}
+    for rf in rows_files:
+        with open(rf) as f:
+            got = json.load(f)
+        if got.get("op") != op:
+            continue
+        man["rows"] = got["rows"]
+        man["card"] = {"before": got.get("card_before"), "after": got.get("card_after")}
+        man["rows_source_md5"] = md5_of(op)
+    with open(path, "w") as f:
+        json.dump(man, f, indent=1)
+        f.write("\n")
+    return path
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--rows", nargs="*", default=[])
+    ap.add_argument("--op", nargs="*", default=list(OPS))
+    a = ap.parse_args()
+    for op in a.op:
+        print(make(op, a.rows))
+
+
+if __name__ == "__main__":
+    main()

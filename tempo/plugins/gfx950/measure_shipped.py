@@ -1,0 +1,228 @@
+"""Measure stage of the shipped deliveries on one MI355X: gate first, then paired timing.
+
+    python3 -m tempo.plugins.gfx950.measure_shipped [gemm_fp16|gemm_w8a16] [--out DIR] [--quick]
+
+For every configuration shape of the op (C1/C2 for gemm_fp16; C3/C4 for gemm_w8a16) it
+  1. runs the shipped launcher once into a 0x7f7f-poisoned output and gates it (reference
+     tempo/core/measure/correctness.py:21-27): no poison left, relL2 <= 3e-3 against the
+     reference semantics computed on the GPU by the naive kernel (kernels/naive/gemm_fp16.hip,
+     bit-identical to the CPU oracle's fp32 sequential-k FMA; for W8A16 the weights are first
+     dequantised by tempo_dequant_tile, bit-exact), and fp64 spot cells within
+     |got-ref|/(|ref|+1e-3) <= 3e-3 (kernels/shipped/gemm_fp16/sm_70/ship_probe.cu:70-79);
+  2. times the shipped kernel, the library bar (torch.matmul = hipBLASLt, fp16 weights) and the
+     naive kernel with HIP events, in paired rounds with the arms interleaved and the weights
+     rotated through > 512 MiB, and reports the median of the per-round ratios (reference
+     tempo/core/measure/ratio.py:63-73).
+Rows go to DIR/rows_<op>.json; tempo.plugins.gfx950.manifest folds them into manifest.json.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+import numpy as np
+
+PEAK_TF = 2516.6
+PEAK_GBPS = 8000.0
+ROUNDS = 5
+
+SHAPES_FP16 = [(4096, 15360, 3840)] + [(M, N, K) for (N, K) in ((15360, 3840), (3840, 15360))
+                                        for M in (1, 8, 16, 32, 64, 128, 256)]
+NK_W8 = [(7168, 5120), (5120, 6144), (34816, 5120), (5120, 17408), (1024, 5120), (5120, 5120)]
+SHAPES_W8 = [(M, N, K) for (N, K) in NK_W8 for M in (1, 16, 128, 2048)]
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+def _events_ms(fn, iters, stream):
+    import torch
+
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(iters):
+        fn(i)
+    e1.record(stream)
+    e1.synchronize()
+    return e0.elapsed_time(e1) / iters
+
+
+def _spot(A, Wf, C, cells=256):
+    """fp64 dot products on sampled cells: A [M,K] fp16, Wf [N,K] fp16, C [M,N] fp16 (torch)."""
+    M, N = C.shape
+    t = np.arange(cells)
+    m, n = (t * 37) % M, (t * 53) % N
+    a = A.cpu().numpy().astype(np.float64)[m]
+    w = Wf[n.tolist()].cpu().numpy().astype(np.float64)
+    ref = np.einsum("ik,ik->i", a, w)
+    got = C.cpu().numpy().astype(np.float64)[m, n]
+    return float(np.max(np.abs(got - ref) / (np.abs(ref) + 1e-3)))
+
+
+def _rel_l2(got, ref):
+    import torch
+
+    g, r = got.double(), ref.double()
+    den = torch.sum(r * r).item()
+    return float(torch.sqrt(torch.sum((g - r) ** 2) / den).item()) if den > 0 else 0.0
+
+
+def measure(op: str, quick: bool = False):
+    import torch
+
+    from cuda_tempiler_amd import capi
+
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    gen = torch.Generator(device=dev)
+    rows = []
+    if op == "gemm_fp16":
+        cases = [(M, N, K, 0) for (M, N, K) in SHAPES_FP16]
+    else:
+        cases = [(M, N, K, f) for f in (1, 2) for (M, N, K) in SHAPES_W8]
+    if quick:
+        cases = cases[::4]
+    for (M, N, K, fmt) in cases:
+        _say("measure %s fmt=%d M=%d N=%d K=%d" % (op, fmt, M, N, K))
+        gen.manual_seed(1000 * M + N + K + fmt)
+        A = (torch.randn((M, K), generator=gen, device=dev) / K ** 0.5).half()
+        wbytes = 2 * N * K if fmt == 0 else N * K + (2 * N if fmt == 1 else 3 * N * K // 128)
+        copies = max(2, -(-(512 << 20) // wbytes) + 1)
+        Ws, Ss, Zs, Fs = [], [], [], []
+        for c in range(copies):
+            if fmt == 0:
+                Ws.append((torch.randn((N, K), generator=gen, device=dev) / K ** 0.5).half())
+                Ss.append(None)
+                Zs.append(None)
+            elif fmt == 1:
+                Ws.append(torch.randint(-127, 128, (N, K), generator=gen, device=dev,
+                                        dtype=torch.int8))
+                Ss.append((torch.rand(N, generator=gen, device=dev) + 0.5).div(127).half())
+                Zs.append(None)
+            else:
+                Ws.append(torch.randint(0, 256, (N, K), generator=gen, device=dev,
+                                        dtype=torch.uint8))
+                Ss.append((torch.rand((N, K // 128), generator=gen, device=dev) + 0.5)
+                          .div(255).half())
+                Zs.append(torch.randint(100, 157, (N, K // 128), generator=gen, device=dev,
+                                        dtype=torch.uint8))
+        # dequantised fp16 copy of the first weight set (bit-exact dequant) for gate and library bar
+        if fmt == 0:
+            F0 = Ws[0]
+        else:
+            F0 = capi.dequant_tile(Ws[0], Ss[0], Zs[0], fmt, 0, 0, N, K)
+        Fb = [F0] + [F0.clone() for _ in range(max(1, -(-(512 << 20) // (2 * N * K))))]
+        C = torch.empty((M, N), dtype=torch.int16, device=dev).fill_(0x7f7f).view(torch.float16)
+
+        def ours(i, C=C):
+            if fmt == 0:
+                capi.gemm_fp16(A, Ws[i % copies], C)
+            else:
+                capi.gemm_w8a16(A, Ws[i % copies], Ss[i % copies], Zs[i % copies], fmt=fmt, C=C)
+
+        try:
+            ours(0)
+        except capi.NotCovered:
+            rows.append(dict(M=M, N=N, K=K, fmt=fmt, winner=None, note="not covered: fallback"))
+            continue
+        torch.cuda.synchronize()
+        poison = int((C.view(torch.int16) == 0x7f7f).sum().item())
+        ref = capi.naive_gemm_fp16(A, F0)
+        torch.cuda.synchronize()
+        rel = _rel_l2(C, ref)
+        spot = _spot(A, F0, C)
+        ok = poison == 0 and rel <= 3e-3 and spot <= 3e-3
+        row = dict(M=M, N=N, K=K, fmt=fmt, winner=capi.route(fmt, M, N, K), poison=poison,
+                   rel_l2=rel, spot_rel=spot, gate="pass" if ok else "FAIL")
+        if not ok:
+            rows.append(row)
+            _say("  GATE FAIL", row)
+            continue
+        Cl = torch.empty((M, N), dtype=torch.float16, device=dev)
+
+        def lib_bar(i):
+            torch.matmul(A, Fb[i % len(Fb)].t(), out=Cl)
+
+        def naive(i):
+            capi.naive_gemm_fp16(A, F0, Cl)
+
+        # iteration count: ~0.3 s per arm per round (reference harness: it = clamp(300/ms, 3, 2000))
+        for f in (ours, lib_bar):
+            for i in range(3):
+                f(i)
+        torch.cuda.synchronize()
+        t0 = _events_ms(ours, 3, stream)
+        it = int(min(2000, max(3, 300.0 / max(t0, 1e-3) / 10)))
+        ratios, t_ours, t_lib = [], [], []
+        for r in range(ROUNDS):
+            a = _events_ms(ours, it, stream)
+            b = _events_ms(lib_bar, it, stream)
+            t_ours.append(a)
+            t_lib.append(b)
+            ratios.append(b / a)
+        tn = _events_ms(naive, 1 if M * N * K > 1e10 else 3, stream)
+        ms = statistics.median(t_ours)
+        flops = 2.0 * M * N * K
+        byts = wbytes + 2 * M * K + 2 * M * N
+        row.update(ms=ms, tflops=flops / ms / 1e9, GBps=byts / ms / 1e6,
+                   mfma_frac=flops / ms / 1e9 / PEAK_TF, hbm_frac=byts / ms / 1e6 / PEAK_GBPS,
+                   ratio_vs_hipblaslt=statistics.median(ratios), ratio_min=min(ratios),
+                   ratio_max=max(ratios), hipblaslt_tflops=flops / statistics.median(t_lib) / 1e9,
+                   naive_tflops=flops / tn / 1e9, ratio_vs_naive=tn / ms, iters=it, rounds=ROUNDS)
+        rows.append(row)
+        _say("  %s" % json.dumps(row))
+        del Ws, Ss, Zs, Fb, F0
+        torch.cuda.empty_cache()
+    return rows
+
+
+def card_state():
+    import subprocess
+
+    out = {"time": time.strftime("%Y-%m-%dT%H:%M:%S")}
+    try:
+        import torch
+
+        out["name"] = torch.cuda.get_device_name(0)
+        p = torch.cuda.get_device_properties(0)
+        out["gcn_arch"] = getattr(p, "gcnArchName", "")
+        out["cus"] = p.multi_processor_count
+    except Exception as e:  # recorded, not fatal
+        out["name_error"] = str(e)
+    for cmd in (["amd-smi", "metric", "--clock", "--json"], ["rocm-smi", "--showclocks", "--json"]):
+        try:
+            r = subprocess.run(cmd, capture_output=True, text=True, timeout=30)
+            if r.returncode == 0:
+                out[cmd[0]] = r.stdout[-4000:]
+                break
+        except Exception:
+            continue
+    return out
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("op", nargs="?", default="gemm_fp16", choices=("gemm_fp16", "gemm_w8a16"))
+    ap.add_argument("--out", default="gpurun_out")
+    ap.add_argument("--quick", action="store_true")
+    a = ap.parse_args()
+    os.makedirs(a.out, exist_ok=True)
+    before = card_state()
+    rows = measure(a.op, a.quick)
+    after = card_state()
+    path = os.path.join(a.out, "rows_%s.json" % a.op)
+    with open(path, "w") as f:
+        json.dump({"op": a.op, "card_before": before, "card_after": after, "rows": rows}, f,
+                  indent=1)
+    bad = [r for r in rows if r.get("gate") == "FAIL"]
+    _say("wrote %s: %d rows, %d gate failures" % (path, len(rows), len(bad)))
+    return 1 if bad else 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

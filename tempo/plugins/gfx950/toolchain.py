@@ -81,7 +81,7 @@ class Gfx950Toolchain:
         out.parent.mkdir(parents=True, exist_ok=True)
         cmd = [HIPCC] + FLAGS + ["-Rpass-analysis=kernel-resource-usage"] + list(extra)
         if mode == "device":
-            cmd += ["--cuda-device-only", "-c"]
+            cmd += ["--cuda-device-only", "--no-gpu-bundle-output", "-c"]
         elif mode == "obj":
             cmd += ["-c"]
         elif mode != "exe":

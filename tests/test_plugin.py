@@ -1,0 +1,246 @@
+"""CPU gates of the gfx950 plugin against the tempo/arch/1 contract, and the core drivers.
+
+Patterns of the reference's tests/test_gates.py (G1 loader, G2 refusals are contract errors and
+never AttributeError, G4 closed rate table, G5 self-test) and tests/test_pipeline.py (oracle
+gate, coverage, registry), restated for the gfx950 plugin.
+"""
+import os
+
+import pytest
+
+from tempo.plugins import base, registry
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+NAIVE = os.path.join(ROOT, "kernels", "naive", "gemm_fp16.hip")
+C1 = {"M": 4096, "N": 15360, "K": 3840}
+
+
+@pytest.fixture(scope="module")
+def plug():
+    return registry.load("gfx950")
+
+
+def _op(**kw):
+    d = dict(kind="gemm", dtype_a="fp16", dtype_b="fp16", dtype_c="fp16", dtype_acc="fp32",
+             layout_a="k", layout_b="k", layout_c="n", shapes=dict(C1), tol_rel_l2=3e-3)
+    d.update(kw)
+    return base.OpSpec(**d)
+
+
+# ---- G1: loader ------------------------------------------------------------------------------
+def test_g1_registry_loads_gfx950(plug):
+    assert "gfx950" in registry.available()
+    assert plug.id == "gfx950"
+    assert plug.contract.split("/")[0:2] == ["tempo", "arch"]
+    for section in ("machine", "memory", "tensor", "resources", "sync", "classifier",
+                    "skeletons", "toolchain", "meters"):
+        assert hasattr(plug, section), section
+    assert isinstance(plug.declared_stubs(), tuple)
+
+
+def test_g1_every_rate_is_a_rate(plug):
+    for sym, r in plug.machine.symbols().items():
+        assert isinstance(r, base.Rate), sym
+        assert r.status in base.STATUS
+
+
+# ---- G2: refusals are contract errors --------------------------------------------------------
+def test_g2_unknown_symbol(plug):
+    with pytest.raises(base.UnknownSymbol):
+        plug.machine.rate("CAP.NOT_A_RATE")
+
+
+def test_g2_layout_refused_structurally(plug):
+    with pytest.raises(base.PluginCapabilityError):
+        list(plug.skeletons.variants(_op(layout_b="n")))
+    with pytest.raises(base.PluginCapabilityError):
+        list(plug.skeletons.variants(_op(dtype_acc="fp16")))
+    with pytest.raises(base.PluginCapabilityError):
+        list(plug.skeletons.variants(_op(dtype_b="fp8")))
+
+
+def test_g2_clock_lock_not_supported(plug):
+    with pytest.raises(base.NotSupported):
+        with plug.meters.clock_lock(0, 2400):
+            pass
+
+
+# ---- G4: closed rate table, SPEC never a time bound ------------------------------------------
+def test_g4_spec_is_not_a_channel_capacity(plug):
+    for name, ch in plug.machine.channels().items():
+        assert ch.capacity.status != "SPEC", name
+
+
+def test_g4_spec_refused_in_time_bound():
+    r = base.Rate("PEAK.X", 1.0, "x", "SPEC")
+    with pytest.raises(base.ContractError):
+        base.spec_forbidden_in_time_bound(r)
+
+
+# ---- G5: self-test -----------------------------------------------------------------------------
+def test_g5_selftest_green(plug):
+    rep = plug.selftest()
+    assert rep.green, rep.render()
+
+
+# ---- resources -------------------------------------------------------------------------------
+def test_resource_verdicts(plug):
+    R = plug.resources
+    assert R.verdict(256, 300, 200 * 1024, 256).code == "WALL_SMEM"
+    assert R.verdict(600, 600, 64 * 1024, 256).code == "NO_BUDGET"
+    assert R.verdict(400, 600, 64 * 1024, 256).code == "WALL_REG"
+    assert R.verdict(128, 200, 64 * 1024, 512, 2).code == "SPILL"
+    v = R.verdict(128, 128, 64 * 1024, 256)
+    assert v.code == "FITS" and v.ok
+    # 256 threads at 128 registers: 4 waves per SIMD fit by registers, LDS 64 KiB -> 2 per CU
+    assert R.occupancy(128, 64 * 1024, 256).ctas_per_sm == 2
+    assert R.reg_budget(4) == 512 and R.reg_budget(16) == 128
+
+
+# ---- space / prune / bound -------------------------------------------------------------------
+def test_space_is_legal_and_injective(plug):
+    from tempo.plugins.gfx950 import space
+
+    hs = list(plug.skeletons.variants(_op()))
+    assert len(hs) > 100
+    assert len({h.key for h in hs}) == len(hs)
+    for h in hs:
+        p = dict(h.params)
+        assert space.legal(p["kind"], p, 4096, 15360, 3840) is None
+        assert space.lds_bytes(p["kind"], p) <= space.LDS_MAX
+
+
+def test_decode_space_has_stream_kinds(plug):
+    hs = list(plug.skeletons.variants(_op(dtype_b="int8", shapes={"M": 1, "N": 7168, "K": 5120})))
+    kinds = {dict(h.params)["kind"] for h in hs}
+    assert {"ring", "stream", "reg"} <= kinds and "dma" not in kinds
+
+
+def test_prune_cuts_only_hard_codes(plug):
+    from tempo.core.search import prune as P
+
+    op = _op()
+    hs = list(plug.skeletons.variants(op))
+    cands = P.prune(plug, op, hs)
+    assert len(cands) == len(hs)
+    for c in cands:
+        if not c.kept and c.verdict is not None and not c.verdict.ok:
+            assert c.verdict.code in P.HARD_CODES
+    kept = P.kept(cands)
+    assert kept
+    # the C1 winner's family is kept and its bound is MFMA-bound, not silent
+    dma = [c for c in kept if c.hyper.key.startswith("dma_m256n256k64")]
+    assert dma and all(c.bound is not None and not c.bound.silent for c in dma)
+    assert all(c.bound.binding == "MFMA" for c in dma)
+
+
+def test_bound_is_a_lower_bound_on_flops(plug):
+    """T >= flops per CU / MFMA capacity: the C1 bound can never beat the MFMA peak."""
+    from tempo.core.model.bound import bound
+
+    op = _op()
+    h = next(h for h in plug.skeletons.variants(op) if h.key.startswith("dma_m256n256k64"))
+    atoms = plug.skeletons.estimate_atoms(op, h)
+    regs, max_live, lds = plug.skeletons.resources_of(op, h)
+    lau = plug.skeletons.launch_of(op, h)
+    occ = plug.resources.occupancy(regs, lds, lau.threads)
+    b = bound(atoms, plug.machine.channels(), warps_per_sm=occ.warps_per_sm)
+    cap = plug.machine.rate("CAP.MFMA_F16").value
+    per_cu_flops = 2 * 4096 * 15360 * 3840 / 256
+    assert b.T >= per_cu_flops / cap * 0.999
+
+
+# ---- emit + build (hipcc, CPU only) -----------------------------------------------------------
+def test_render_and_build_one_hyperform(plug, tmp_path):
+    from tempo.core.emit import render as R
+    from tempo.plugins.gfx950.classifier import parse_disasm
+    from tempo.plugins.gfx950.toolchain import isa_summary
+
+    op = _op()
+    h = next(h for h in plug.skeletons.variants(op) if h.key == "dma_m256n256k64_w2x2_s2_z2_g8_x1")
+    path = R.emit(plug, op, h, str(tmp_path))
+    assert os.path.exists(path)
+    obj = tmp_path / "k.o"
+    b = plug.toolchain.compile(path, obj, mode="device")
+    assert b.ok, b.log[-2000:]
+    assert b.spill_st == 0 and b.stack_frame == 0
+    assert b.smem_static == 2 * (256 + 256) * 64 * 2
+    isa = isa_summary(sum(parse_disasm(plug.toolchain.disasm(obj)).values(), []))
+    assert isa["mfma"] >= 64 and isa["lds_dma"] > 0 and isa["scratch"] == 0
+    assert isa["ds_read_b128"] > 0
+    assert plug.skeletons.entry_probe(h).startswith("tempo::gen::k_gemm_dma<256, 256, 64")
+
+
+# ---- recognize ---------------------------------------------------------------------------------
+def test_recognize_naive_input():
+    from tempo.core.op import recognize
+
+    op = recognize.from_file(NAIVE, C1)
+    assert (op.kind, op.dtype_a, op.dtype_b, op.dtype_c, op.dtype_acc) == \
+        ("gemm", "fp16", "fp16", "fp16", "fp32")
+    assert (op.layout_a, op.layout_b, op.layout_c) == ("k", "k", "n")
+    assert op.tol_rel_l2 == pytest.approx(3e-3)
+
+
+def test_recognize_refuses_mismatched_signature(tmp_path):
+    from tempo.core.op import recognize
+
+    text = open(NAIVE, encoding="utf-8").read().replace("naive_gemm_fp16(", "other_name(", 1)
+    p = tmp_path / "bad.hip"
+    p.write_text(text)
+    with pytest.raises(recognize.NotRecognised):
+        recognize.from_file(str(p), C1)
+
+
+# ---- core oracle gate / coverage / ratio ------------------------------------------------------
+def test_oracle_gate_needs_named_independent_path():
+    from tempo.core.op.oracle import OracleResult
+
+    r = OracleResult(rel_l2=1e-4, tol=3e-3, independent_rel_l2=2e-4, independent_path="")
+    assert r.necessary_ok and not r.ok
+    r.independent_path = "fp64 dot products on 2048 sampled cells"
+    assert r.ok
+    r.independent_rel_l2 = 1e-2
+    assert not r.ok
+
+
+def test_coverage_from_poison():
+    import numpy as np
+
+    from tempo.core.op.coverage import from_poison
+
+    cells = np.zeros(100, np.uint16)
+    assert from_poison(cells).ok
+    cells[17] = 0x7f7f
+    assert not from_poison(cells).ok
+
+
+def test_median_ratio():
+    from tempo.core.measure.ratio import median_ratio
+
+    r = median_ratio([(1.0, 2.0), (1.0, 2.2), (1.0, 1.8)])
+    assert r == pytest.approx(2.0, rel=1e-6) or r == pytest.approx(0.5, rel=1e-6)
+
+
+# ---- toolchain remark parsing -----------------------------------------------------------------
+def test_parse_resource_remarks():
+    from tempo.plugins.gfx950.toolchain import parse_resource_remarks
+
+    text = """k.hip:3:1: remark: k.hip:3:0: Function Name: _Z1kPf [-Rpass-analysis=kernel-resource-usage]
+k.hip:3:1: remark: k.hip:3:0:     TotalSGPRs: 18 [-Rpass-analysis=kernel-resource-usage]
+k.hip:3:1: remark: k.hip:3:0:     VGPRs: 130 [-Rpass-analysis=kernel-resource-usage]
+k.hip:3:1: remark: k.hip:3:0:     AGPRs: 64 [-Rpass-analysis=kernel-resource-usage]
+k.hip:3:1: remark: k.hip:3:0:     ScratchSize [bytes/lane]: 0 [-Rpass-analysis=kernel-resource-usage]
+k.hip:3:1: remark: k.hip:3:0:     LDS Size [bytes/block]: 65536 [-Rpass-analysis=kernel-resource-usage]
+"""
+    r = parse_resource_remarks(text)
+    assert r["_Z1kPf"]["VGPRs"] == 130 and r["_Z1kPf"]["AGPRs"] == 64
+    assert r["_Z1kPf"]["LDS Size [bytes/block]"] == 65536
+
+
+def test_tensor_result_maps_are_bijections(plug):
+    from tempo.plugins.gfx950.tensor import result_map
+
+    for ms in (32, 16):
+        rows, cols = result_map(ms)
+        assert len({(a, b) for a, b in zip(rows.ravel(), cols.ravel())}) == ms * ms

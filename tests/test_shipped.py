@@ -1,0 +1,106 @@
+"""CPU checks of the shipped deliveries and the C-ABI library (no GPU calls).
+
+"One source, two consumers" (reference kernels/shipped/gemm_fp16/sm_70/test_gate.py:102-146):
+select.py is the ladder, dispatch.inc is generated from it, and the compiled dispatcher must
+pick the same row as select.py for every shape.  The library must export every symbol that
+include/tempo_gfx950.h declares.
+"""
+import importlib.util
+import os
+import re
+import subprocess
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+SHIPPED = os.path.join(ROOT, "kernels", "shipped")
+HEADER = os.path.join(ROOT, "include", "tempo_gfx950.h")
+OPS = ("gemm_fp16", "gemm_w8a16")
+
+
+def _select(op):
+    path = os.path.join(SHIPPED, op, "gfx950", "select.py")
+    spec = importlib.util.spec_from_file_location("select_%s" % op, path)
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+@pytest.mark.parametrize("op", OPS)
+def test_dispatch_inc_is_generated_from_select(op):
+    d = os.path.join(SHIPPED, op, "gfx950")
+    text = subprocess.run([sys.executable, os.path.join(d, "gen_dispatch.py")], check=True,
+                          capture_output=True, text=True).stdout
+    with open(os.path.join(d, "dispatch.inc"), encoding="utf-8") as f:
+        assert f.read() == text, "dispatch.inc is stale: re-run the build"
+
+
+def test_frozen_kernels_match_skeletons():
+    from tempo.plugins.gfx950 import ship
+
+    assert ship.stale() == []
+
+
+def test_delivery_layout():
+    for op in OPS:
+        d = os.path.join(SHIPPED, op, "gfx950")
+        for f in ("kernel.hip", "launch.h", "launch.hip", "dispatch.inc", "select.py",
+                  "gen_dispatch.py", "manifest.json"):
+            assert os.path.exists(os.path.join(d, f)), "%s/%s missing" % (op, f)
+
+
+def _declared():
+    with open(HEADER, encoding="utf-8") as f:
+        text = f.read()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(tempo_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    from cuda_tempiler_amd import capi
+
+    declared = _declared()
+    assert len(declared) >= 10
+    L = capi.lib()
+    missing = [s for s in declared if not hasattr(L, s)]
+    assert not missing
+    assert set(declared) == set(capi.EXPORTS), "ctypes table and header disagree"
+
+
+def test_abi_version():
+    from cuda_tempiler_amd import capi
+
+    assert capi.lib().tempo_abi_version() >= 1
+
+
+SWEEP_M = (1, 2, 8, 16, 17, 31, 32, 33, 64, 128, 255, 256, 257, 1000, 2048, 4096)
+SWEEP_NK = ((15360, 3840), (3840, 15360), (7168, 5120), (5120, 6144), (34816, 5120),
+            (5120, 17408), (1024, 5120), (5120, 5120), (512, 384), (520, 384), (384, 100),
+            (4096, 192), (4096, 320))
+
+
+def test_compiled_route_agrees_with_select_fp16():
+    from cuda_tempiler_amd import capi
+
+    sel = _select("gemm_fp16")
+    for (N, K) in SWEEP_NK:
+        for M in SWEEP_M:
+            r = sel.select("gemm", M, N, K)
+            assert capi.route(0, M, N, K) == (r["tag"] if r else ""), (M, N, K)
+
+
+@pytest.mark.parametrize("fmt", [1, 2])
+def test_compiled_route_agrees_with_select_w8a16(fmt):
+    from cuda_tempiler_amd import capi
+
+    sel = _select("gemm_w8a16")
+    for (N, K) in SWEEP_NK:
+        for M in SWEEP_M:
+            r = sel.select("gemm_w8a16", M, N, K, fmt=fmt, group=128)
+            assert capi.route(fmt, M, N, K) == (r["tag"] if r else ""), (M, N, K, fmt)
+
+
+def test_route_unknown_op_is_empty():
+    from cuda_tempiler_amd import capi
+
+    assert capi.route(7, 64, 64, 64) == ""
