@@ -41,7 +41,10 @@ inline void stream_split(int N, int K, int R, int U, int* S_out, int* chunk_out)
   *chunk_out = per * 64 * U;
 }
 
-template <int MB, int R, int U>
+// Activations staged in LDS (ALDS rows) only while M*(2K+16) bytes stay within this budget.
+constexpr size_t kStreamActLds = 96 * 1024;
+
+template <int MB, int R, int U, int ALDS>
 inline hipError_t launch_stream(const GemmParams& p, hipStream_t s) {
   StreamArgs a;
   a.A = p.A;
@@ -58,8 +61,12 @@ inline hipError_t launch_stream(const GemmParams& p, hipStream_t s) {
   a.group = 0;
   stream_split(p.N, p.K, R, U, &a.S, &a.chunk);
   const dim3 grid(p.N / (16 * R)), blk(64 * a.S);
-  const size_t lds = a.S > 1 ? (size_t)a.S * R * MB * 64 * 16 : 0;
-  hipLaunchKernelGGL((k_stream<MB, R, U, 0>), grid, blk, lds, s, a);
+  const size_t red = a.S > 1 ? (size_t)a.S * R * MB * 64 * 16 : 0;
+  const size_t act = (size_t)p.M * (2 * (size_t)p.K + 16);
+  if (ALDS && act <= kStreamActLds)
+    hipLaunchKernelGGL((k_stream<MB, R, U, 0, 1>), grid, blk, act + red, s, a);
+  else
+    hipLaunchKernelGGL((k_stream<MB, R, U, 0, 0>), grid, blk, red, s, a);
   return hipGetLastError();
 }
 

@@ -4,21 +4,29 @@ None means "caller's own path" (the fallback).  Same contract as the reference's
 kernels/shipped/gemm_fp16/sm_70/select.py:23-58; this file is the ONE source of the M-band
 ladder -- dispatch.inc is generated from it by gen_dispatch.py and a test checks they agree.
 
-Bands (M is the only runtime-varying extent in serving):
-  * M <= 32   stream: the weight-streaming decode kernel (HBM-bound; one pass over B).
+Rows are tried in order; the first row whose band holds (M, N) -- M <= M_max and N >= N_min --
+AND whose kernel fits the shape (divisibility) is taken.  No such row: None, the caller's own
+path.  (The reference stops at the first band that holds M; here a row that does not fit falls
+through to the next one, so a narrower row can sit in front of a general one.)
+  * M <= 32   stream: the weight-streaming decode kernel (HBM-bound; one pass over B).  A = 1
+              stages the activations in LDS once per workgroup (M = 1).  Wide N takes four
+              row groups per wave (R = 4): fewer activation re-reads, still >= 192 slabs.
   * M >  32   mfma / dma: LDS-tiled MFMA kernels (dma = LDS-DMA copies), tile chosen by M.
 """
 
 ARCH = "gfx950"
 
-# (M_max, tag, kind, template params).  First matching row wins.
+# (M_max, N_min, tag, kind, template params).  First row that holds (M, N) and fits wins.
 LADDER = [
-    (16, "s16r1u4", "stream", dict(MB=1, R=1, U=4)),
-    (32, "s32r1u4", "stream", dict(MB=2, R=1, U=4)),
-    (256, "m128x128k64", "mfma",
+    (1, 0, "s1a_r1u4", "stream", dict(MB=1, R=1, U=4, A=1)),
+    (16, 12288, "s16r4u2", "stream", dict(MB=1, R=4, U=2, A=0)),
+    (16, 0, "s16r1u4", "stream", dict(MB=1, R=1, U=4, A=0)),
+    (32, 12288, "s32r4u2", "stream", dict(MB=2, R=4, U=2, A=0)),
+    (32, 0, "s32r1u4", "stream", dict(MB=2, R=1, U=4, A=0)),
+    (256, 0, "m128x128k64", "mfma",
      dict(BM=128, BN=128, BK=64, WM=2, WN=2, MS=32, SWZ=1, GROUP=8, XCD=1)),
-    (1 << 30, "d256x256k64s2", "dma",
-     dict(BM=256, BN=256, BK=64, WM=2, WN=2, STAGES=2, SWZ=2, GROUP=8, XCD=1)),
+    (1 << 30, 0, "d256x256k64w8", "dma",
+     dict(BM=256, BN=256, BK=64, WM=2, WN=4, STAGES=2, SWZ=2, GROUP=8, XCD=1)),
 ]
 
 # Divisibility each kind needs (checked at run time by dispatch.inc, mirrored here).
@@ -39,9 +47,7 @@ def select(op, M, N, K, dtype_a="fp16", dtype_b="fp16", dtype_c="fp16", arch=ARC
         return None
     if M <= 0 or N <= 0 or K <= 0 or N % 8 or K % 8:
         return None
-    for m_max, tag, kind, p in LADDER:
-        if M <= m_max:
-            if not _fits(kind, p, M, N, K):
-                return None  # the band's kernel does not cover this shape: fallback
+    for m_max, n_min, tag, kind, p in LADDER:
+        if M <= m_max and N >= n_min and _fits(kind, p, M, N, K):
             return dict(tag=tag, kind=kind, **p)
     return None

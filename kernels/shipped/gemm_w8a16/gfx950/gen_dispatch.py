@@ -27,34 +27,37 @@ def _select():
 HEAD = """// GENERATED from select.py -- do not edit.  Regenerate with:
 //   python3 kernels/shipped/gemm_w8a16/gfx950/gen_dispatch.py > dispatch.inc
 //
-// M-band ladder, one TEMPO_ROW(band, fit, launcher, tag) per row; launch.hip expands it twice
-// (launch and route).  First band that holds M decides; if its kernel does not fit the shape,
-// or no band holds M, the answer is hipErrorInvalidConfiguration: the caller's own path takes
-// over (TEMPO_FALLBACK) -- a legal answer, not a failure.
+// Ladder, one TEMPO_ROW(band, fit, launcher, tag) per row; launch.hip expands it twice (launch
+// and route).  The first row whose band holds (M, N) and whose kernel fits the shape runs; if
+// none does, the answer is hipErrorInvalidConfiguration: the caller's own path takes over
+// (TEMPO_FALLBACK) -- a legal answer, not a failure.
 """
 
 
 def instantiation(kind, p):
     if kind == "stream":
-        return "launch_stream<%d,%d,%d>" % (p["MB"], p["R"], p["U"])
+        return "launch_stream<%d,%d,%d,%d>" % (p["MB"], p["R"], p["U"], p.get("A", 0))
     return "launch_mfma<%d,%d,%d,%d,%d,%d,%d,%d,%d>" % (
         p["BM"], p["BN"], p["BK"], p["WM"], p["WN"], p["MS"], p["SWZ"], p["GROUP"], p["XCD"])
 
 
-def condition(sel, kind, p, m_max):
+def condition(sel, kind, p, m_max, n_min=0):
     if kind == "stream":
         fit = "(p.N %% %d) == 0 && (p.K %% %d) == 0" % (sel.STREAM_N_ROWS * p["R"],
                                                           sel.STREAM_K_STEP * p["U"])
     else:
         fit = "(p.N %% %d) == 0 && (p.K %% %d) == 0" % (p["BN"], p["BK"])
-    return "p.M <= %d" % m_max, fit
+    band = "p.M <= %d" % m_max
+    if n_min:
+        band += " && p.N >= %d" % n_min
+    return band, fit
 
 
 def render() -> str:
     sel = _select()
     out = [HEAD]
-    for m_max, tag, kind, p in sel.LADDER:
-        band, fit = condition(sel, kind, p, m_max)
+    for m_max, n_min, tag, kind, p in sel.LADDER:
+        band, fit = condition(sel, kind, p, m_max, n_min)
         out.append("TEMPO_ROW(%s, %s,\n          (%s), \"%s\")" % (band, fit, instantiation(kind, p), tag))
     out.append("TEMPO_FALLBACK_ROW")
     return "\n".join(out) + "\n"

@@ -66,16 +66,28 @@ inline StreamArgs stream_args(const W8A16Params& p) {
   return a;
 }
 
-template <int MB, int R, int U>
+// Activations staged in LDS (ALDS rows) only while M*(2K+16) bytes stay within this budget.
+constexpr size_t kStreamActLds = 96 * 1024;
+
+template <int MB, int R, int U, int ALDS>
 inline hipError_t launch_stream(const W8A16Params& p, hipStream_t s) {
   StreamArgs a = stream_args(p);
   stream_split(p.N, p.K, R, U, &a.S, &a.chunk);
   const dim3 grid(p.N / (16 * R)), blk(64 * a.S);
-  const size_t lds = a.S > 1 ? (size_t)a.S * R * MB * 64 * 16 : 0;
-  if (p.fmt == 1)
-    hipLaunchKernelGGL((k_stream<MB, R, U, 1>), grid, blk, lds, s, a);
-  else
-    hipLaunchKernelGGL((k_stream<MB, R, U, 2>), grid, blk, lds, s, a);
+  const size_t red = a.S > 1 ? (size_t)a.S * R * MB * 64 * 16 : 0;
+  const size_t act = (size_t)p.M * (2 * (size_t)p.K + 16);
+  const bool alds = ALDS && act <= kStreamActLds;
+  if (p.fmt == 1) {
+    if (alds)
+      hipLaunchKernelGGL((k_stream<MB, R, U, 1, 1>), grid, blk, act + red, s, a);
+    else
+      hipLaunchKernelGGL((k_stream<MB, R, U, 1, 0>), grid, blk, red, s, a);
+  } else {
+    if (alds)
+      hipLaunchKernelGGL((k_stream<MB, R, U, 2, 1>), grid, blk, act + red, s, a);
+    else
+      hipLaunchKernelGGL((k_stream<MB, R, U, 2, 0>), grid, blk, red, s, a);
+  }
   return hipGetLastError();
 }
 

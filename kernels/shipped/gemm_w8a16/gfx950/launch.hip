@@ -12,7 +12,7 @@ namespace gen8 {
 hipError_t launch(const W8A16Params& p, hipStream_t s) {
   if (!applicable(p)) return hipErrorInvalidConfiguration;
 #define TEMPO_ROW(band, fit, fn, tag) \
-  if (band) return (fit) ? fn(p, s) : hipErrorInvalidConfiguration;
+  if ((band) && (fit)) return fn(p, s);
 #define TEMPO_FALLBACK_ROW return hipErrorInvalidConfiguration;
 #include "dispatch.inc"
 #undef TEMPO_ROW
@@ -22,7 +22,7 @@ hipError_t launch(const W8A16Params& p, hipStream_t s) {
 const char* route(const W8A16Params& p) {
   if (!applicable(p)) return nullptr;
 #define TEMPO_ROW(band, fit, fn, tag) \
-  if (band) return (fit) ? tag : nullptr;
+  if ((band) && (fit)) return tag;
 #define TEMPO_FALLBACK_ROW return nullptr;
 #include "dispatch.inc"
 #undef TEMPO_ROW

@@ -11,13 +11,18 @@ file by gen_dispatch.py.
 ARCH = "gfx950"
 FORMATS = (1, 2)
 
-# (M_max, tag, kind, template params).  First band that holds M decides.
+# (M_max, N_min, tag, kind, template params).  Rows are tried in order; the first row whose band
+# holds (M, N) -- M <= M_max and N >= N_min -- and whose kernel fits the shape is taken.
 LADDER = [
-    (16, "s16r1u4", "stream", dict(MB=1, R=1, U=4)),
-    (32, "s32r1u4", "stream", dict(MB=2, R=1, U=4)),
-    (256, "m128x128k64", "mfma",
+    (1, 0, "s1a_r1u8", "stream", dict(MB=1, R=1, U=8, A=1)),
+    (1, 0, "s1a_r1u4", "stream", dict(MB=1, R=1, U=4, A=1)),
+    (16, 4096, "s16r2u4", "stream", dict(MB=1, R=2, U=4, A=0)),
+    (16, 0, "s16r1u4", "stream", dict(MB=1, R=1, U=4, A=0)),
+    (32, 16384, "s32r4u2", "stream", dict(MB=2, R=4, U=2, A=0)),
+    (32, 0, "s32r2u4", "stream", dict(MB=2, R=2, U=4, A=0)),
+    (256, 0, "m128x128k64", "mfma",
      dict(BM=128, BN=128, BK=64, WM=2, WN=2, MS=32, SWZ=1, GROUP=8, XCD=1)),
-    (1 << 30, "m256x256k64", "mfma",
+    (1 << 30, 0, "m256x256k64", "mfma",
      dict(BM=256, BN=256, BK=64, WM=2, WN=2, MS=32, SWZ=1, GROUP=8, XCD=1)),
 ]
 
@@ -40,9 +45,7 @@ def select(op, M, N, K, fmt=1, group=128, dtype_a="fp16", dtype_c="fp16", arch=A
         return None
     if fmt == 2 and (group != 128 or K % group):
         return None
-    for m_max, tag, kind, p in LADDER:
-        if M <= m_max:
-            if not _fits(kind, p, M, N, K):
-                return None
+    for m_max, n_min, tag, kind, p in LADDER:
+        if M <= m_max and N >= n_min and _fits(kind, p, M, N, K):
             return dict(tag=tag, kind=kind, fmt=fmt, **p)
     return None

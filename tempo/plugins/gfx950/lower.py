@@ -41,7 +41,7 @@ _ENTRY = {
             ("common/cdna4.h", "gemm_mfma/kernel.hip")),
     "ring": ("k_stream_dma", ("MB", "R", "D", "BFMT"), "StreamArgs",
              ("common/cdna4.h", "gemv_stream/kernel.hip")),
-    "stream": ("k_stream", ("MB", "R", "U", "BFMT"), "StreamArgs",
+    "stream": ("k_stream", ("MB", "R", "U", "BFMT", "ALDS"), "StreamArgs",
                ("common/cdna4.h", "gemv_stream/kernel.hip")),
 }
 NAMESPACE = "tempo::gen"
@@ -116,9 +116,13 @@ class Gfx950Skeletons:
         if kind == "ring":
             regs = p["R"] * p["MB"] * 4 + (p["R"] * wb + 2 * p["MB"]) * 4 + 2 * (p["R"] + p["MB"]) + 16
         else:
-            regs = (2 * p["R"] * p["MB"] * 4 + 2 * p["U"] * (p["R"] * wb + 2 * p["MB"]) * 4
+            act_regs = 0 if p.get("ALDS", 0) else 2 * p["MB"]
+            regs = (2 * p["R"] * p["MB"] * 4 + 2 * p["U"] * (p["R"] * wb + act_regs) * 4
                     + 2 * (p["R"] + p["MB"]) + 16)
-        return regs, int(regs * 1.25), space.lds_bytes(kind, dict(p, S=S))
+        lds = space.lds_bytes(kind, dict(p, S=S))
+        if kind == "stream" and p.get("ALDS", 0):
+            lds += int(op.shapes["M"]) * (2 * int(op.shapes["K"]) + 16)
+        return regs, int(regs * 1.25), lds
 
     def launch_of(self, op: OpSpec, h: Hyperform) -> Launch:
         p = _p(h)

@@ -68,11 +68,13 @@ def build_numbers(op):
         spec = OpSpec(kind="gemm", dtype_a="fp16", dtype_b=db, dtype_c="fp16", dtype_acc="fp32",
                       layout_a="k", layout_b="k", layout_c="n",
                       shapes={"M": 4096, "N": 15360, "K": 3840})
-        for m_max, tag, kind, p in sel.LADDER:
+        for m_max, n_min, tag, kind, p in sel.LADDER:
             pk = {"stream": "stream", "mfma": "reg", "dma": "dma"}[kind]
             params = dict(p, kind=pk)
             if pk != "dma":
                 params["BFMT"] = fmt
+            if pk == "stream":
+                params["ALDS"] = params.pop("A", 0)
             h = Hyperform(plugin="gfx950", params=params, key="%s_f%d" % (tag, fmt))
             r = plug.skeletons.render(spec, h)
             with tempfile.TemporaryDirectory() as td:
@@ -112,6 +114,8 @@ def make(op, rows_files=()):
             "per_row_fit": "see dispatch[].fit",
             "fallback": "hipErrorInvalidConfiguration (TEMPO_FALLBACK): the caller's own path",
         },
+        "dispatch_rule": "rows in order; the first whose band holds (M, N) and whose kernel fits "
+                         "the shape runs; none -> fallback",
         "dispatch": [],
         "build": build_numbers(op),
         "source_md5": md5_of(op),
@@ -119,13 +123,14 @@ def make(op, rows_files=()):
         "rows": old.get("rows", []),
         "card": old.get("card", None),
     }
-    for m_max, tag, kind, p in sel.LADDER:
+    for m_max, n_min, tag, kind, p in sel.LADDER:
         if kind == "stream":
             fit = "N %% %d == 0 and K %% %d == 0" % (sel.STREAM_N_ROWS * p["R"],
                                                     sel.STREAM_K_STEP * p["U"])
         else:
             fit = "N %% %d == 0 and K %% %d == 0" % (p["BN"], p["BK"])
-        man["dispatch"].append(dict(M_max=m_max, tag=tag, kind=kind, params=p, fit=fit))
+        man["dispatch"].append(dict(M_max=m_max, N_min=n_min, tag=tag, kind=kind, params=p,
+                                    fit=fit))
     if op == "gemm_w8a16":
         man["predicate"]["formats"] = {"1": "int8 weights, fp16 scale per output channel",
                                        "2": "uint8 weights, fp16 scale + uint8 zero per (row, 128 k)"}

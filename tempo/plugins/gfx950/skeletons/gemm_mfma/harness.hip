@@ -6,6 +6,8 @@
 //   hipcc -O3 -std=c++17 --offload-arch=gfx950 -Xclang -target-feature -Xclang -packed-fp32-ops
 //         -I<dir with configs.inc> harness.hip -o harness
 // Run:  ./harness M N K [iters]
+//       ./harness peak        -- MFMA-only throughput probe (no memory traffic): the ceiling the
+//                                matrix cores reach at the clock the part sustains under load
 //
 // For each CFG row of configs.inc: fill A, B from a hash (seeded, deterministic), compute the
 // reference once with the naive one-thread-per-output kernel (the pipeline's input), then per
@@ -21,6 +23,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
+#include <string>
 #include <vector>
 
 namespace tempo {
@@ -106,6 +109,61 @@ static unsigned long long poison_left(const _Float16* a, long n) {
   return h;
 }
 
+// MFMA-only probe: CHAINS independent 32x32x16 accumulators per wave, ITERS rounds, operands in
+// registers.  The result is stored (one value per lane) so the work cannot be removed.
+template <int CHAINS>
+__global__ __launch_bounds__(256) void k_mfma_peak(float* out, int iters, float seed) {
+  f32x16 acc[CHAINS];
+#pragma unroll
+  for (int c = 0; c < CHAINS; ++c)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[c][v] = 0.f;
+  f16x8 a, b;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    a[i] = (_Float16)(seed * (float)(threadIdx.x + i));
+    b[i] = (_Float16)(seed * (float)(i - (int)threadIdx.x));
+  }
+  for (int it = 0; it < iters; ++it)
+#pragma unroll
+    for (int c = 0; c < CHAINS; ++c) acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[c], 0, 0, 0);
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < CHAINS; ++c)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) s += acc[c][v];
+  out[(long)blockIdx.x * blockDim.x + threadIdx.x] = s;
+}
+
+static int peak_probe() {
+  const int iters = 4000;
+  hipEvent_t e0, e1;
+  CK(hipEventCreate(&e0));
+  CK(hipEventCreate(&e1));
+  for (int wg_per_cu : {1, 2}) {
+    const int grid = 256 * wg_per_cu * 4;  // 4 rounds of the part
+    float* out;
+    CK(hipMalloc(&out, (size_t)grid * 256 * sizeof(float)));
+    for (int rep = 0; rep < 2; ++rep) {
+      hipLaunchKernelGGL(k_mfma_peak<4>, dim3(grid), dim3(256), 0, 0, out, iters, 1e-3f);
+      CK(hipGetLastError());
+      CK(hipDeviceSynchronize());
+      CK(hipEventRecord(e0, 0));
+      hipLaunchKernelGGL(k_mfma_peak<4>, dim3(grid), dim3(256), 0, 0, out, iters, 1e-3f);
+      CK(hipEventRecord(e1, 0));
+      CK(hipEventSynchronize(e1));
+      float ms = 0.f;
+      CK(hipEventElapsedTime(&ms, e0, e1));
+      const double flop = 2.0 * 32 * 32 * 16 * 4.0 * iters * (double)grid * 4;  // 4 waves per WG
+      printf("PEAK {\"waves_per_simd\":%d,\"us\":%.1f,\"tflops\":%.1f}\n", wg_per_cu, ms * 1e3,
+             flop / (ms * 1e-3) / 1e12);
+      fflush(stdout);
+    }
+    CK(hipFree(out));
+  }
+  return 0;
+}
+
 typedef void (*LaunchFn)(const _Float16*, const _Float16*, _Float16*, int, int, int, hipStream_t);
 struct Arm {
   const char* tag;
@@ -113,12 +171,13 @@ struct Arm {
   LaunchFn launch;
 };
 
-template <int BM, int BN, int BK, int WM, int WN, int STAGES, int SWZ, int GROUP, int XCD>
+template <int BM, int BN, int BK, int WM, int WN, int STAGES, int SWZ, int GROUP, int XCD, int XT = 0,
+          int MINB = 1>
 struct Dma {
   static bool fits(int M, int N, int K) { (void)M; return N % BN == 0 && K % BK == 0; }
   static void launch(const _Float16* A, const _Float16* B, _Float16* C, int M, int N, int K, hipStream_t s) {
     const int nm = (M + BM - 1) / BM, nn = N / BN;
-    hipLaunchKernelGGL((k_gemm_dma<BM, BN, BK, WM, WN, STAGES, SWZ, GROUP, XCD>), dim3(nm * nn),
+    hipLaunchKernelGGL((k_gemm_dma<BM, BN, BK, WM, WN, STAGES, SWZ, GROUP, XCD, XT, MINB>), dim3(nm * nn),
                        dim3(WM * WN * 64), 0, s, A, B, C, M, N, K, K, K, N);
   }
 };
@@ -142,6 +201,7 @@ static const Arm kArms[] = {
 };
 
 int main(int argc, char** argv) {
+  if (argc > 1 && std::string(argv[1]) == "peak") return peak_probe();
   const int M = argc > 1 ? atoi(argv[1]) : 4096;
   const int N = argc > 2 ? atoi(argv[2]) : 15360;
   const int K = argc > 3 ? atoi(argv[3]) : 3840;

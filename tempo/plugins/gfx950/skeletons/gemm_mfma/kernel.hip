@@ -275,8 +275,15 @@ __device__ __forceinline__ void s_wait_vm() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0x0 << 8));
 }
 
-template <int BM, int BN, int BK, int WM, int WN, int STAGES, int SWZ, int GROUP, int XCD>
-__global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_dma(
+// XT = 1 pipelines across k-tile boundaries: the wait + barrier for tile kt+1, the DMA issue of
+// tile kt+STAGES and the first fragment reads of tile kt+1 all happen BEFORE the last MFMA group
+// of tile kt, so the matrix cores have work while the workgroup synchronises.  The prologue then
+// fills all STAGES buffers.  XT = 0 keeps the plain loop (wait + barrier at the top of a tile).
+// MINB = workgroups the compiler must leave room for on one CU (register budget 512 / waves per
+// SIMD); 2 lets two small-tile workgroups share a CU, so one computes while the other waits.
+template <int BM, int BN, int BK, int WM, int WN, int STAGES, int SWZ, int GROUP, int XCD,
+          int XT = 0, int MINB = 1>
+__global__ __launch_bounds__(WM * WN * 64, MINB) void k_gemm_dma(
     const _Float16* __restrict__ A, const _Float16* __restrict__ B, _Float16* __restrict__ C,
     int M, int N, int K, int lda, int ldb, int ldc) {
   constexpr int MS = 32;
@@ -292,7 +299,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_dma(
   constexpr int L = A_BLK + B_BLK;
   constexpr int STAGE_ELEMS = (BM + BN) * BK;
   static_assert(BM % (RPB * NW) == 0 && BN % (RPB * NW) == 0, "DMA blocks per wave");
-  static_assert(STAGES >= 2 && (STAGES - 2) * L < 64, "stages / vmcnt range");
+  static_assert(STAGES >= 2 && (STAGES - 2 + XT) * L < 64, "stages / vmcnt range");
   static_assert(WTM % MS == 0 && WTN % MS == 0 && BK % MF::KSTEP == 0, "tile shape");
 
   __shared__ __attribute__((aligned(1024))) _Float16 smem[STAGES * STAGE_ELEMS];
@@ -356,6 +363,70 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_dma(
   for (int j = 0; j < TN; ++j) bOff[j] = (wn * WTN + j * MS + fr);
 
   const int NT = K / BK;
+  if constexpr (XT) {
+    f16x8 fa[2][TM], fb[2][TN];
+    auto read = [&](auto bufc, const _Float16* a, int ks) {
+      constexpr int bb = decltype(bufc)::value;
+      const _Float16* b = a + BM * BK;
+      const int chunk = ks * (64 / MS) + fk;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+        fa[bb][i] = *reinterpret_cast<const f16x8*>(a + aOff[i] * BK +
+                                                    lds_chunk<BK, SWZ>(aOff[i], chunk) * 8);
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        fb[bb][j] = *reinterpret_cast<const f16x8*>(b + bOff[j] * BK +
+                                                    lds_chunk<BK, SWZ>(bOff[j], chunk) * 8);
+    };
+    auto mma = [&](auto bufc) {
+      constexpr int bb = decltype(bufc)::value;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = MF::run(fb[bb][j], fa[bb][i], acc[i][j]);
+    };
+    static_assert(KS % 2 == 0, "fragment buffers alternate; a tile holds an even k-step count");
+    // prologue: every buffer gets a tile; wait for tile 0 (tiles 1..STAGES-1 stay in flight)
+#pragma unroll
+    for (int s = 0; s < STAGES; ++s)
+      if (s < NT) issue(s);
+    asm volatile("" ::: "memory");
+    if (NT >= STAGES) s_wait_vm<(STAGES - 1) * L>();
+    else s_wait_vm<0>();
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    read(IC<0>{}, smem, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    for (int kt = 0; kt < NT; ++kt) {
+      const _Float16* a = smem + (kt % STAGES) * STAGE_ELEMS;
+#pragma unroll
+      for (int ks = 0; ks < KS - 2; ks += 2) {
+        read(IC<1>{}, a, ks + 1);
+        mma(IC<0>{});
+        __builtin_amdgcn_sched_barrier(0);
+        read(IC<0>{}, a, ks + 2);
+        mma(IC<1>{});
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      read(IC<1>{}, a, KS - 1);
+      mma(IC<0>{});
+      __builtin_amdgcn_sched_barrier(0);
+      if (kt + 1 < NT) {
+        // Tile kt+1 has landed for this wave (tiles up to kt+STAGES-1 may still be in flight)
+        // and this wave's reads of tile kt are complete (lgkmcnt 0) ...
+        asm volatile("" ::: "memory");
+        if (kt + STAGES < NT) s_wait_vm<(STAGES - 2) * L>();
+        else s_wait_vm<0>();
+        // ... and everyone's: tile kt+1 is readable and buffer kt % STAGES is free.
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (kt + STAGES < NT) issue(kt + STAGES);
+        read(IC<0>{}, smem + ((kt + 1) % STAGES) * STAGE_ELEMS, 0);
+      }
+      mma(IC<1>{});
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  } else {
 #pragma unroll
   for (int s = 0; s < STAGES - 1; ++s)
     if (s < NT) issue(s);
@@ -406,6 +477,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_dma(
       if (ks + 1 < KS) mma(IC<1>{});
       __builtin_amdgcn_sched_barrier(0);
     }
+  }
   }
 
   // ---- epilogue: each lane owns 4 consecutive n of one m per result group ----------------

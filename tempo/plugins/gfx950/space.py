@@ -40,7 +40,7 @@ DOMAINS = {
     "reg": dict(BM=(64, 128, 256), BN=(128, 256), BK=(64,), MS=(16, 32), SWZ=(1, 2), GROUP=(8,),
                 XCD=(1,)),
     "ring": dict(R=(1, 2, 4), D=(4, 5, 6, 8, 10, 12, 14, 16)),
-    "stream": dict(R=(1, 2, 4), U=(2, 4, 8)),
+    "stream": dict(R=(1, 2, 4), U=(2, 4, 8), ALDS=(0, 1)),
 }
 
 BFMT_OF = {("fp16", "fp16"): 0, ("fp16", "int8"): 1, ("fp16", "uint8"): 2}
@@ -95,7 +95,7 @@ def tag(kind: str, p: dict) -> str:
                                                    p["MS"], p["SWZ"], p["BFMT"])
     if kind == "ring":
         return "ring_mb%d_r%d_d%d_b%d" % (p["MB"], p["R"], p["D"], p["BFMT"])
-    return "stream_mb%d_r%d_u%d_b%d" % (p["MB"], p["R"], p["U"], p["BFMT"])
+    return "stream_mb%d_r%d_u%d_b%d_a%d" % (p["MB"], p["R"], p["U"], p["BFMT"], p.get("ALDS", 0))
 
 
 def legal(kind: str, p: dict, M: int, N: int, K: int):
@@ -137,6 +137,8 @@ def legal(kind: str, p: dict, M: int, N: int, K: int):
         return None
     if K % (64 * p["U"]):
         return "K %% %d" % (64 * p["U"])
+    if p.get("ALDS", 0) and M * (2 * K + 16) > 96 * 1024:
+        return "activations do not fit the LDS budget"
     return None
 
 
@@ -154,7 +156,8 @@ def variants(op: OpSpec) -> Iterator[Hyperform]:
                 out.append(("ring", dict(MB=MB, R=R, D=D, BFMT=b)))
         for R in DOMAINS["stream"]["R"]:
             for U in DOMAINS["stream"]["U"]:
-                out.append(("stream", dict(MB=MB, R=R, U=U, BFMT=b)))
+                for AL in DOMAINS["stream"]["ALDS"]:
+                    out.append(("stream", dict(MB=MB, R=R, U=U, BFMT=b, ALDS=AL)))
     if b == 0:
         d = DOMAINS["dma"]
         for BM in d["BM"]:

@@ -70,9 +70,12 @@ def test_shipped_known_answers_bit_exact(gpu):
             assert int(C.view(np.uint16)[m, n]) == bits, (M, N, K, m, n)
 
 
-SHAPES = [(1, 15360, 3840), (8, 15360, 3840), (16, 3840, 15360), (17, 4096, 3840),
-          (32, 3840, 15360), (64, 15360, 3840), (128, 3840, 15360), (200, 4096, 3840),
-          (256, 15360, 3840), (512, 4096, 3840)]
+# one shape per ladder row at least (route named in the test id), plus ragged M and a shape whose
+# first matching row does not fit (N = 12304: N % 64 != 0, falls through to the next row)
+SHAPES = [(1, 15360, 3840), (1, 3840, 15360), (8, 15360, 3840), (8, 12304, 3840),
+          (16, 3840, 15360), (17, 4096, 3840), (24, 15360, 3840), (32, 3840, 15360),
+          (64, 15360, 3840), (128, 3840, 15360), (200, 4096, 3840), (256, 15360, 3840),
+          (512, 4096, 3840), (300, 15360, 3840)]
 
 
 @pytest.mark.parametrize("M,N,K", SHAPES)
