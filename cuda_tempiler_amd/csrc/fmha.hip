@@ -22,18 +22,24 @@ bool applicable(const TempoFmhaParams& p) {
   for (uintptr_t x : ptrs)
     if (x % 16 != 0) return false;
   if ((long)p.Sq * p.q_ss > (1L << 40)) return false;
+  if ((long)((p.Sq + 127) / 128) * p.H * p.B >= (1L << 31)) return false;
+  // key/value rows of one block are addressed with 32-bit byte offsets from the block's first row
+  if (p.k_ss > (1L << 24) || p.v_ss > (1L << 24)) return false;
   return true;
 }
 
 template <int D, bool CAUSAL>
 static hipError_t run(const TempoFmhaParams& p, hipStream_t s) {
-  const dim3 grid((p.Sq + fmha::BQ - 1) / fmha::BQ, p.H, p.B), blk(256);
+  // one workgroup per (query block, head, batch); the kernel numbers them heaviest causal
+  // query block first across all heads and batches
+  const int nqb = (p.Sq + fmha::BQ - 1) / fmha::BQ;
+  const dim3 grid((unsigned)nqb * p.H * p.B), blk(256);
   const float scale_log2 = p.scale * 1.4426950408889634f;
-  hipLaunchKernelGGL((fmha::k_fmha_fwd<D, CAUSAL>), grid, blk, 0, s,
+  hipLaunchKernelGGL((fmha::k_fmha_fwd2<D, CAUSAL, 64, 1, 4>), grid, blk, 0, s,
                      static_cast<const _Float16*>(p.Q), static_cast<const _Float16*>(p.K),
-                     static_cast<const _Float16*>(p.V), static_cast<_Float16*>(p.O), p.LSE, p.H,
-                     p.Hkv, p.Sq, p.Sk, scale_log2, p.q_sb, p.q_ss, p.q_sh, p.k_sb, p.k_ss, p.k_sh,
-                     p.v_sb, p.v_ss, p.v_sh, p.o_sb, p.o_ss, p.o_sh);
+                     static_cast<const _Float16*>(p.V), static_cast<_Float16*>(p.O), p.LSE, p.B,
+                     p.H, p.Hkv, p.Sq, p.Sk, scale_log2, p.q_sb, p.q_ss, p.q_sh, p.k_sb, p.k_ss,
+                     p.k_sh, p.v_sb, p.v_ss, p.v_sh, p.o_sb, p.o_ss, p.o_sh);
   return hipGetLastError();
 }
 

@@ -253,4 +253,279 @@ __global__ __launch_bounds__(256, 1) void k_fmha_fwd(
   }
 }
 
+// ============================================================================================
+// k_fmha_fwd2 -- the DMA form.  Same semantics and the same MFMA formulation (S^T = K.Q^T, each
+// lane owns one query row; O^T += V^T.P^T with P^T taken from the S^T accumulators), changed in
+// how the key/value blocks reach the matrix cores and in the softmax bookkeeping:
+//   * K and V blocks of BKV keys are copied global -> LDS with LDS-DMA (global_load_lds_dwordx4),
+//     no register staging.  Both are stored in their natural [key][d] order with the 16-byte
+//     chunk index XOR-ed by fmha_swz(key % 16), a bit swap of the 4-bit row index chosen so that
+//     both read patterns are free of bank conflicts on the 64-bank LDS: the K read (16 rows, one
+//     chunk) and the transposed V read (4 rows x 4 consecutive chunks) each land on 16 distinct
+//     16-byte slots of a 256-byte bank window.  The swizzle is applied on the global side (lane l
+//     of a DMA instruction writes bytes [16l, 16l+16) of a 1 KiB block and fetches the chunk
+//     that belongs there).
+//   * The V^T operand (8 keys of one d per lane) is read with ds_read_b64_tr_b16: within each
+//     group of 16 lanes, lane j supplies the address of 4 consecutive d of key row (base + j/4),
+//     and lane i receives, for e = 0..3, element i%4 of the row supplied by lane 4e + i/4 --
+//     i.e. key base+e at d = d0 + i.  Two such reads give the 8 keys of one MFMA k-group.
+//   * All LDS read addresses are a per-lane offset (computed once) plus a compile-time constant,
+//     and all DMA sources a per-lane 32-bit offset from a wave-uniform block base.
+//   * Rescale threshold: the running max used for the exponentials only moves when some lane's
+//     block max exceeds it by more than TAU (base-2 units).  Any reference value gives the same
+//     softmax (the numerator and l use the same one), exp2 arguments stay <= TAU, and the O
+//     rescale -- 128 AGPR read/multiply/write triples per lane -- is almost never paid.
+//   * Blocks are numbered heaviest query block first over ALL heads and batches.
+// ============================================================================================
+typedef __attribute__((address_space(3))) void fmha_lds_void_t;
+typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 fmha_h4;
+typedef __attribute__((address_space(3))) fmha_h4 fmha_lds_h4;
+
+template <int N>
+__device__ __forceinline__ void fmha_wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0x0 << 8));
+}
+
+__device__ __forceinline__ u32x2 fmha_tr_read(const char* p) {
+  const fmha_h4 v = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+      (fmha_lds_h4*)((__attribute__((address_space(3))) const char*)(p)));
+  return __builtin_bit_cast(u32x2, v);
+}
+
+constexpr float FMHA_TAU = 8.f;  // log2 of the largest unnormalised probability allowed
+
+// swizzle key of a key row (only its low 4 bits matter): swap the two 2-bit halves
+__device__ __forceinline__ int fmha_swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+
+// WAVES = 4 or 8 waves per workgroup, 32 query rows each (the query block is 32*WAVES rows).
+template <int D, bool CAUSAL, int BKV2, int MINB, int WAVES = 4>
+__global__ __launch_bounds__(64 * WAVES, MINB) void k_fmha_fwd2(
+    const _Float16* __restrict__ Q, const _Float16* __restrict__ Kg,
+    const _Float16* __restrict__ Vg, _Float16* __restrict__ O, float* __restrict__ LSE, int B,
+    int H, int Hkv, int Sq, int Sk, float scale_log2, long q_sb, long q_ss, long q_sh, long k_sb,
+    long k_ss, long k_sh, long v_sb, long v_ss, long v_sh, long o_sb, long o_ss, long o_sh) {
+  static_assert(D == 128 || D == 256, "head dim 128 or 256");
+  static_assert(BKV2 == 32 || BKV2 == 64, "key block 32 or 64");
+  constexpr int NJ = BKV2 / 32;              // 32-key MFMA blocks of S per key block
+  constexpr int DCH = D / 8;                 // 16-byte chunks per key row
+  constexpr int DS = D / 16;                 // MFMA k-steps over d for S
+  constexpr int DB = D / 32;                 // 32-wide d blocks of O^T
+  constexpr int RB = D * 2;                  // bytes per key row in LDS
+  constexpr int ROWS_PER_KB = 1024 / RB;     // key rows per 1 KiB DMA block
+  constexpr int BLK = BKV2 / ROWS_PER_KB;    // DMA blocks per operand per KV block
+  constexpr int BLK_W = BLK / WAVES;         // ... per wave
+  constexpr int BQW = 32 * WAVES;            // query rows per workgroup
+  constexpr int TILE_B = BKV2 * RB;          // bytes of one K (or V) block
+  static_assert(BLK % WAVES == 0, "DMA blocks split over the waves");
+
+  __shared__ __attribute__((aligned(1024))) char smem[2 * 2 * TILE_B];  // [stage][K,V][BKV][D]
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int hl = lane >> 5;
+  const int l32 = lane & 31;
+
+  // heaviest query block first over all (b, h)
+  const int nqb = (Sq + BQW - 1) / BQW;
+  const int bid = blockIdx.x;
+  const int per_qb = H * B;
+  const int qb = CAUSAL ? (nqb - 1 - bid / per_qb) : bid / per_qb;
+  const int hb = bid % per_qb;
+  const int h = hb % H, b = hb / H;
+  const int hk = h / (H / Hkv);
+  const int off = Sk - Sq;
+  const int q0 = qb * BQW;
+  const int qi = q0 + wave * 32 + l32;
+  const int qrow = min(qi, Sq - 1);
+
+  const _Float16* Qp = Q + b * q_sb + (long)h * q_sh;
+  const char* Kp = reinterpret_cast<const char*>(Kg + b * k_sb + (long)hk * k_sh);
+  const char* Vp = reinterpret_cast<const char*>(Vg + b * v_sb + (long)hk * v_sh);
+
+  f16x8 qf[DS];
+#pragma unroll
+  for (int st = 0; st < DS; ++st)
+    qf[st] = *reinterpret_cast<const f16x8*>(Qp + (long)qrow * q_ss + 16 * st + 8 * hl);
+
+  int kend = Sk;
+  if (CAUSAL) {
+    const int last = min(q0 + BQW, Sq) - 1 + off;
+    kend = last + 1 < Sk ? last + 1 : Sk;
+    if (kend < 0) kend = 0;
+  }
+  const int nkb = (kend + BKV2 - 1) / BKV2;
+
+  // ---- DMA: block i of this wave = operand block (i*WAVES + wave); lane -> (row, phys chunk) ---
+  const int rin = lane / DCH, phys = lane % DCH;
+  unsigned ksrc[BLK_W], vsrc[BLK_W];  // byte offsets from the key block's first row
+  int drow[BLK_W];
+#pragma unroll
+  for (int i = 0; i < BLK_W; ++i) {
+    const int r = (i * WAVES + wave) * ROWS_PER_KB + rin;
+    const int c = phys ^ fmha_swz(r);  // logical chunk stored at slot `phys`
+    drow[i] = r;
+    ksrc[i] = (unsigned)(r * k_ss * 2 + c * 16);
+    vsrc[i] = (unsigned)(r * v_ss * 2 + c * 16);
+  }
+  auto issue = [&](int kb) {
+    char* sk = smem + (kb & 1) * 2 * TILE_B;
+    char* sv = sk + TILE_B;
+    const int j0 = kb * BKV2;
+    const char* kblk = Kp + (long)j0 * k_ss * 2;
+    const char* vblk = Vp + (long)j0 * v_ss * 2;
+    if (j0 + BKV2 <= Sk) {
+#pragma unroll
+      for (int i = 0; i < BLK_W; ++i) {
+        __builtin_amdgcn_global_load_lds((void*)(kblk + ksrc[i]),
+                                         (fmha_lds_void_t*)(sk + (i * WAVES + wave) * 1024), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((void*)(vblk + vsrc[i]),
+                                         (fmha_lds_void_t*)(sv + (i * WAVES + wave) * 1024), 16, 0, 0);
+      }
+    } else {  // ragged key tail: rows past Sk re-read row Sk-1 (masked out of the softmax)
+#pragma unroll
+      for (int i = 0; i < BLK_W; ++i) {
+        const long back = (long)max(0, j0 + drow[i] - (Sk - 1));
+        __builtin_amdgcn_global_load_lds((void*)(kblk + ksrc[i] - back * k_ss * 2),
+                                         (fmha_lds_void_t*)(sk + (i * WAVES + wave) * 1024), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((void*)(vblk + vsrc[i] - back * v_ss * 2),
+                                         (fmha_lds_void_t*)(sv + (i * WAVES + wave) * 1024), 16, 0, 0);
+      }
+    }
+  };
+
+  // ---- LDS read offsets (bytes within a stage's K or V tile) ------------------------------------
+  // K (S^T operand): row kr = 32*jb + l32, logical chunk 2*st + hl, swizzle key fmha_swz(l32)
+  // (same for every jb).  (2st + hl) ^ key only touches bits 0..3, i.e. st & 7: eight offsets.
+  const int kkey = fmha_swz(l32);
+  int koff[8];
+#pragma unroll
+  for (int s7 = 0; s7 < 8; ++s7) koff[s7] = l32 * RB + (((2 * s7) | hl) ^ kkey) * 16;
+  // V^T (transposed reads): lane (group tg, index tj) addresses key row R(t) + tk (+8 for the
+  // second read; R(t) is a multiple of 16, so the row's swizzle key is fmha_swz(tk) or
+  // fmha_swz(tk + 8)) at d = 32*db + 16*(tg&1) + 4*(tj&3): logical chunk 4*db + cd, byte 8*(tj&1).
+  const int tg = lane >> 4, tj = lane & 15;
+  const int tk = 4 * (tg >> 1) + (tj >> 2);          // 0..7: the swizzle key of the first read
+  const int cd = 2 * (tg & 1) + ((tj & 3) >> 1);     // 0..3
+  const int half = 8 * (tj & 1);
+  // (4db + cd) ^ key touches bits 0..3 only: four lane offsets per read, by db & 3
+  int voff0[4], voff1[4];
+#pragma unroll
+  for (int p4 = 0; p4 < 4; ++p4) {
+    voff0[p4] = tk * RB + (((p4 << 2) | cd) ^ fmha_swz(tk)) * 16 + half;
+    voff1[p4] = (tk + 8) * RB + (((p4 << 2) | cd) ^ fmha_swz(tk + 8)) * 16 + half;
+  }
+
+  f32x16 acc_o[DB];
+#pragma unroll
+  for (int i = 0; i < DB; ++i)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc_o[i][v] = 0.f;
+  float m_run = -__builtin_inff();  // reference value of the exponentials (base 2, scaled)
+  float l_run = 0.f;
+
+  if (nkb > 0) issue(0);
+
+  for (int kb = 0; kb < nkb; ++kb) {
+    asm volatile("" ::: "memory");
+    fmha_wait_vm<0>();
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (kb + 1 < nkb) issue(kb + 1);
+    const char* k = smem + (kb & 1) * 2 * TILE_B;
+    const char* v = k + TILE_B;
+    const int j0 = kb * BKV2;
+
+    // S^T in 32-key blocks: lane holds keys j0 + 32*jb + 8*(r>>2) + 4*hl + (r&3) of row qi
+    f32x16 s[NJ];
+#pragma unroll
+    for (int jb = 0; jb < NJ; ++jb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[jb][r] = 0.f;
+#pragma unroll
+      for (int st = 0; st < DS; ++st) {
+        const f16x8 kf = *reinterpret_cast<const f16x8*>(k + koff[st & 7] + (st >> 3) * 256 +
+                                                         jb * 32 * RB);
+        s[jb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[st], s[jb], 0, 0, 0);
+      }
+    }
+
+    // masked raw-score max (scale > 0, so the max commutes with the scaling)
+    const bool need_mask = (j0 + BKV2 > Sk) || (CAUSAL && j0 + BKV2 - 1 > q0 + off);
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int jb = 0; jb < NJ; ++jb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float x = s[jb][r];
+        if (need_mask) {
+          const int j = j0 + 32 * jb + 8 * (r >> 2) + 4 * hl + (r & 3);
+          const bool hide = (j >= Sk) || (CAUSAL && j > qi + off);
+          x = hide ? -__builtin_inff() : x;
+        }
+        s[jb][r] = x;
+        mx = fmaxf(mx, x);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 32)) * scale_log2;
+    // move the reference only when some lane's max overtook it by more than TAU (or it was unset)
+    const bool move = !(mx - m_run <= FMHA_TAU);  // true for m_run = -inf and a finite mx
+    if (__builtin_amdgcn_ballot_w64(move) != 0) {
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha = (m_new == -__builtin_inff()) ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
+      l_run *= alpha;
+      m_run = m_new;
+#pragma unroll
+      for (int i = 0; i < DB; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc_o[i][r] *= alpha;
+    }
+    const float m_use = (m_run == -__builtin_inff()) ? 0.f : m_run;
+    float psum = 0.f;
+    f16x8 pf[2 * NJ];
+#pragma unroll
+    for (int jb = 0; jb < NJ; ++jb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[jb][r], scale_log2, -m_use));
+        psum += p;
+        pf[2 * jb + (r >> 3)][r & 7] = (_Float16)p;
+      }
+    psum += __shfl_xor(psum, 32);
+    l_run += psum;
+
+    // O^T += V^T . P^T in MFMA k-steps of 16 keys; step t, element e <-> key
+    // 32(t/2) + 16(t%2) + 8(e/4) + 4*hl + e%4, matching pf[t][e] above
+#pragma unroll
+    for (int t = 0; t < 2 * NJ; ++t) {
+      const int rt = 32 * (t >> 1) + 16 * (t & 1);
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const u32x2 v0 = fmha_tr_read(v + voff0[db & 3] + rt * RB + (db >> 2) * 256);
+        const u32x2 v1 = fmha_tr_read(v + voff1[db & 3] + rt * RB + (db >> 2) * 256);
+        const u32x4 vv = {v0[0], v0[1], v1[0], v1[1]};
+        acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(vv), pf[t], acc_o[db], 0, 0, 0);
+      }
+    }
+  }
+
+  if (qi < Sq) {
+    const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+    _Float16* Op = O + b * o_sb + (long)qi * o_ss + (long)h * o_sh;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        f16x4 o;
+        o[0] = (_Float16)(acc_o[db][4 * g + 0] * inv);
+        o[1] = (_Float16)(acc_o[db][4 * g + 1] * inv);
+        o[2] = (_Float16)(acc_o[db][4 * g + 2] * inv);
+        o[3] = (_Float16)(acc_o[db][4 * g + 3] * inv);
+        *reinterpret_cast<f16x4*>(Op + db * 32 + 8 * g + 4 * hl) = o;
+      }
+    if (LSE && hl == 0)
+      LSE[((long)b * H + h) * Sq + qi] =
+          l_run > 0.f ? m_run * 0.6931471805599453f + __logf(l_run) : -__builtin_inff();
+  }
+}
+
 }  // namespace fmha

@@ -61,7 +61,42 @@ def test_fmha_parity_small(gpu, case):
     r = O.rel_l2(got, ref)
     say("  relL2 %.3e" % r)
     assert r <= TOL
-    assert np.max(np.abs(lse - lref)) <= LSE_TOL
+    assert _lse_close(lse, lref)
+
+
+def _lse_close(lse, lref):
+    inf = np.isneginf(lref)
+    assert np.array_equal(np.isneginf(lse), inf)
+    return np.max(np.abs(lse[~inf] - lref[~inf]), initial=0.0) <= LSE_TOL
+
+
+def test_fmha_rows_without_keys(gpu):
+    """Causal with Sq > Sk: off = Sk - Sq < 0, the first Sq - Sk rows see no key at all; their
+    output is 0 and their LSE -inf, as in the oracle."""
+    B, Sq, Sk, H, Hkv, D = 1, 300, 130, 2, 1, 128
+    Q, K, V = _inputs(B, Sq, Sk, H, Hkv, D, seed=21)
+    got, lse = _run(Q, K, V, 1.0 / np.sqrt(D), True, gpu)
+    ref, lref = O.fmha_fwd(Q, K, V, 1.0 / np.sqrt(D), True)
+    assert O.count_poison(got) == 0
+    assert not np.any(got[:, : Sq - Sk].astype(np.float32))
+    assert O.rel_l2(got, ref) <= TOL
+    assert _lse_close(lse, lref)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_fmha_growing_scores_rescale(gpu, causal):
+    """Key rows scaled up along the sequence: every block's max overtakes the running one by a
+    wide margin, so the running-max rescale of the output is taken again and again."""
+    B, S, H, Hkv, D = 1, 512, 2, 2, 128
+    Q, K, V = _inputs(B, S, S, H, Hkv, D, seed=33)
+    grow = (1.0 + np.arange(S, dtype=np.float32) / 24.0)[None, :, None, None]
+    K = O.f2h(K.astype(np.float32) * grow)
+    got, lse = _run(Q, K, V, 1.0 / np.sqrt(D), causal, gpu)
+    ref, lref = O.fmha_fwd(Q, K, V, 1.0 / np.sqrt(D), causal)
+    r = O.rel_l2(got, ref)
+    say("growing scores relL2 %.3e" % r)
+    assert r <= TOL
+    assert _lse_close(lse, lref)
 
 
 def test_fmha_strided_bhsd(gpu):
