@@ -38,9 +38,9 @@ def instantiation(kind, p):
     if kind == "stream":
         return "launch_stream<%d,%d,%d,%d>" % (p["MB"], p["R"], p["U"], p.get("A", 0))
     if kind == "dma":
-        return "launch_dma<%d,%d,%d,%d,%d,%d,%d,%d,%d>" % (
+        return "launch_dma<%d,%d,%d,%d,%d,%d,%d,%d,%d,%d>" % (
             p["BM"], p["BN"], p["BK"], p["WM"], p["WN"], p["STAGES"], p["SWZ"], p["GROUP"],
-            p["XCD"])
+            p["XCD"], p.get("MS", 32))
     return "launch_mfma<%d,%d,%d,%d,%d,%d,%d,%d,%d>" % (
         p["BM"], p["BN"], p["BK"], p["WM"], p["WN"], p["MS"], p["SWZ"], p["GROUP"], p["XCD"])
 

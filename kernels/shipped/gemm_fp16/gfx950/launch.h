@@ -82,12 +82,13 @@ inline hipError_t launch_mfma(const GemmParams& p, hipStream_t s) {
   return hipGetLastError();
 }
 
-template <int BM, int BN, int BK, int WM, int WN, int STAGES, int SWZ, int GROUP, int XCD>
+template <int BM, int BN, int BK, int WM, int WN, int STAGES, int SWZ, int GROUP, int XCD, int MS>
 inline hipError_t launch_dma(const GemmParams& p, hipStream_t s) {
   const int nm = (p.M + BM - 1) / BM;
   const int nn = p.N / BN;
   const dim3 grid(nm * nn), blk(WM * WN * 64);
-  hipLaunchKernelGGL((k_gemm_dma<BM, BN, BK, WM, WN, STAGES, SWZ, GROUP, XCD>), grid, blk, 0, s,
+  hipLaunchKernelGGL((k_gemm_dma<BM, BN, BK, WM, WN, STAGES, SWZ, GROUP, XCD, 0, 1, MS>), grid, blk,
+                     0, s,
                      p.A, p.B, p.C, p.M, p.N, p.K, p.lda, p.ldb, p.ldc);
   return hipGetLastError();
 }

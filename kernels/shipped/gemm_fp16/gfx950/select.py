@@ -25,8 +25,8 @@ LADDER = [
     (32, 0, "s32r1u4", "stream", dict(MB=2, R=1, U=4, A=0)),
     (256, 0, "m128x128k64", "mfma",
      dict(BM=128, BN=128, BK=64, WM=2, WN=2, MS=32, SWZ=1, GROUP=8, XCD=1)),
-    (1 << 30, 0, "d256x256k64w8", "dma",
-     dict(BM=256, BN=256, BK=64, WM=2, WN=4, STAGES=2, SWZ=2, GROUP=8, XCD=1)),
+    (1 << 30, 0, "d256x256k64w16m16", "dma",
+     dict(BM=256, BN=256, BK=64, WM=4, WN=4, STAGES=2, SWZ=2, GROUP=8, XCD=1, MS=16)),
 ]
 
 # Divisibility each kind needs (checked at run time by dispatch.inc, mirrored here).

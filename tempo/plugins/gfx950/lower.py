@@ -32,7 +32,8 @@ CAPABILITIES = frozenset({
 
 # kernel symbol, template-parameter order, and argument list, per kind: the emitter's only data
 _ENTRY = {
-    "dma": ("k_gemm_dma", ("BM", "BN", "BK", "WM", "WN", "STAGES", "SWZ", "GROUP", "XCD"),
+    "dma": ("k_gemm_dma", ("BM", "BN", "BK", "WM", "WN", "STAGES", "SWZ", "GROUP", "XCD", "XT",
+                           "MINB", "MS"),
             "const _Float16*, const _Float16*, _Float16*, int, int, int, int, int, int",
             ("common/cdna4.h", "gemm_mfma/kernel.hip")),
     "reg": ("k_gemm", ("BM", "BN", "BK", "WM", "WN", "MS", "SWZ", "GROUP", "XCD", "BFMT"),

@@ -75,6 +75,10 @@ def build_numbers(op):
                 params["BFMT"] = fmt
             if pk == "stream":
                 params["ALDS"] = params.pop("A", 0)
+            if pk == "dma":
+                params.setdefault("XT", 0)
+                params.setdefault("MINB", 1)
+                params.setdefault("MS", 32)
             h = Hyperform(plugin="gfx950", params=params, key="%s_f%d" % (tag, fmt))
             r = plug.skeletons.render(spec, h)
             with tempfile.TemporaryDirectory() as td:

@@ -172,12 +172,12 @@ struct Arm {
 };
 
 template <int BM, int BN, int BK, int WM, int WN, int STAGES, int SWZ, int GROUP, int XCD, int XT = 0,
-          int MINB = 1>
+          int MINB = 1, int MS = 32>
 struct Dma {
   static bool fits(int M, int N, int K) { (void)M; return N % BN == 0 && K % BK == 0; }
   static void launch(const _Float16* A, const _Float16* B, _Float16* C, int M, int N, int K, hipStream_t s) {
     const int nm = (M + BM - 1) / BM, nn = N / BN;
-    hipLaunchKernelGGL((k_gemm_dma<BM, BN, BK, WM, WN, STAGES, SWZ, GROUP, XCD, XT, MINB>), dim3(nm * nn),
+    hipLaunchKernelGGL((k_gemm_dma<BM, BN, BK, WM, WN, STAGES, SWZ, GROUP, XCD, XT, MINB, MS>), dim3(nm * nn),
                        dim3(WM * WN * 64), 0, s, A, B, C, M, N, K, K, K, N);
   }
 };

@@ -281,12 +281,12 @@ __device__ __forceinline__ void s_wait_vm() {
 // fills all STAGES buffers.  XT = 0 keeps the plain loop (wait + barrier at the top of a tile).
 // MINB = workgroups the compiler must leave room for on one CU (register budget 512 / waves per
 // SIMD); 2 lets two small-tile workgroups share a CU, so one computes while the other waits.
+// MS = MFMA shape (32: v_mfma_f32_32x32x16_f16, 16: v_mfma_f32_16x16x32_f16).
 template <int BM, int BN, int BK, int WM, int WN, int STAGES, int SWZ, int GROUP, int XCD,
-          int XT = 0, int MINB = 1>
+          int XT = 0, int MINB = 1, int MS = 32>
 __global__ __launch_bounds__(WM * WN * 64, MINB) void k_gemm_dma(
     const _Float16* __restrict__ A, const _Float16* __restrict__ B, _Float16* __restrict__ C,
     int M, int N, int K, int lda, int ldb, int ldc) {
-  constexpr int MS = 32;
   using MF = Mfma<MS>;
   constexpr int NW = WM * WN;
   constexpr int CPR = BK / 8;

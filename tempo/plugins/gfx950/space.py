@@ -36,7 +36,7 @@ AXES = (
 
 DOMAINS = {
     "dma": dict(BM=(128, 256), BN=(128, 192, 256), BK=(32, 64), STAGES=(2, 3, 4), SWZ=(0, 1, 2),
-                GROUP=(4, 8, 16), XCD=(0, 1)),
+                GROUP=(4, 8, 16), XCD=(0, 1), WAVES=((2, 2), (2, 4), (4, 2), (4, 4)), MS=(16, 32)),
     "reg": dict(BM=(64, 128, 256), BN=(128, 256), BK=(64,), MS=(16, 32), SWZ=(1, 2), GROUP=(8,),
                 XCD=(1,)),
     "ring": dict(R=(1, 2, 4), D=(4, 5, 6, 8, 10, 12, 14, 16)),
@@ -88,8 +88,9 @@ def stream_split(N: int, K: int, R: int, step_k: int, bfmt_: int = 0, per_wave_l
 
 def tag(kind: str, p: dict) -> str:
     if kind == "dma":
-        return "dma_m%dn%dk%d_w%dx%d_s%d_z%d_g%d_x%d" % (p["BM"], p["BN"], p["BK"], p["WM"], p["WN"],
-                                                      p["STAGES"], p["SWZ"], p["GROUP"], p["XCD"])
+        return "dma_m%dn%dk%d_w%dx%d_s%d_z%d_g%d_x%d_f%d" % (
+            p["BM"], p["BN"], p["BK"], p["WM"], p["WN"], p["STAGES"], p["SWZ"], p["GROUP"], p["XCD"],
+            p.get("MS", 32))
     if kind == "reg":
         return "reg_m%dn%dk%d_w%dx%d_f%d_z%d_b%d" % (p["BM"], p["BN"], p["BK"], p["WM"], p["WN"],
                                                    p["MS"], p["SWZ"], p["BFMT"])
@@ -114,8 +115,10 @@ def legal(kind: str, p: dict, M: int, N: int, K: int):
             if BM % (rpb * nw) or BN % (rpb * nw):
                 return "DMA blocks do not divide among waves"
             L = (BM + BN) // (rpb * nw)
-            if (p["STAGES"] - 2) * L >= 64:
+            if (p["STAGES"] - 2 + p.get("XT", 0)) * L >= 64:
                 return "vmcnt depth"
+            if nw * 64 > 1024:
+                return "more than 1024 lanes"
         if lds_bytes(kind, p) > LDS_MAX:
             return "LDS %d B > 160 KiB" % lds_bytes(kind, p)
         return None
@@ -167,8 +170,11 @@ def variants(op: OpSpec) -> Iterator[Hyperform]:
                         for SW in d["SWZ"]:
                             for G in d["GROUP"]:
                                 for X in d["XCD"]:
-                                    out.append(("dma", dict(BM=BM, BN=BN, BK=BK, WM=2, WN=2,
-                                                            STAGES=ST, SWZ=SW, GROUP=G, XCD=X)))
+                                    for (WM, WN) in d["WAVES"]:
+                                        for MS in d["MS"]:
+                                            out.append(("dma", dict(
+                                                BM=BM, BN=BN, BK=BK, WM=WM, WN=WN, STAGES=ST,
+                                                SWZ=SW, GROUP=G, XCD=X, XT=0, MINB=1, MS=MS)))
     d = DOMAINS["reg"]
     for BM in d["BM"]:
         for BN in d["BN"]:

@@ -157,7 +157,8 @@ def test_render_and_build_one_hyperform(plug, tmp_path):
     from tempo.plugins.gfx950.toolchain import isa_summary
 
     op = _op()
-    h = next(h for h in plug.skeletons.variants(op) if h.key == "dma_m256n256k64_w2x2_s2_z2_g8_x1")
+    h = next(h for h in plug.skeletons.variants(op)
+             if h.key == "dma_m256n256k64_w4x4_s2_z2_g8_x1_f16")
     path = R.emit(plug, op, h, str(tmp_path))
     assert os.path.exists(path)
     obj = tmp_path / "k.o"
@@ -166,7 +167,7 @@ def test_render_and_build_one_hyperform(plug, tmp_path):
     assert b.spill_st == 0 and b.stack_frame == 0
     assert b.smem_static == 2 * (256 + 256) * 64 * 2
     isa = isa_summary(sum(parse_disasm(plug.toolchain.disasm(obj)).values(), []))
-    assert isa["mfma"] >= 64 and isa["lds_dma"] > 0 and isa["scratch"] == 0
+    assert isa["mfma"] >= 32 and isa["lds_dma"] > 0 and isa["scratch"] == 0
     assert isa["ds_read_b128"] > 0
     assert plug.skeletons.entry_probe(h).startswith("tempo::gen::k_gemm_dma<256, 256, 64")
 

@@ -114,4 +114,4 @@ def test_rows_fall_through_when_the_first_row_does_not_fit():
     assert capi.route(0, 1, 15360, 3840) == "s1a_r1u4"
     assert capi.route(1, 1, 5120, 5120) == "s1a_r1u8"
     assert capi.route(1, 1, 5120, 5376) == "s1a_r1u4"   # K % 512 != 0, K % 256 == 0
-    assert capi.route(0, 4096, 15360, 3840) == "d256x256k64w8"
+    assert capi.route(0, 4096, 15360, 3840) == "d256x256k64w16m16"
