@@ -35,6 +35,9 @@ HEAD = """// GENERATED from select.py -- do not edit.  Regenerate with:
 
 
 def instantiation(kind, p):
+    if kind == "shared":
+        return "launch_shared<%d,%d,%d,%d,%d>" % (p["MB"], p["R"], p["U"], p["SN"],
+                                                  p.get("TPB", 1024))
     if kind == "stream":
         return "launch_stream<%d,%d,%d,%d>" % (p["MB"], p["R"], p["U"], p.get("A", 0))
     if kind == "dma":
@@ -48,6 +51,9 @@ def instantiation(kind, p):
 def condition(sel, kind, p, m_max, n_min=0):
     if kind == "stream":
         fit = "(p.N %% %d) == 0 && (p.K %% %d) == 0" % (sel.STREAM_N_ROWS * p["R"],
+                                                          sel.STREAM_K_STEP * p["U"])
+    elif kind == "shared":
+        fit = "(p.N %% %d) == 0 && (p.K %% %d) == 0" % (sel.STREAM_N_ROWS * p["R"] * p["SN"],
                                                           sel.STREAM_K_STEP * p["U"])
     else:
         fit = "(p.N %% %d) == 0 && (p.K %% %d) == 0" % (p["BN"], p["BK"])

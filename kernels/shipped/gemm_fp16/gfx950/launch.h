@@ -70,6 +70,48 @@ inline hipError_t launch_stream(const GemmParams& p, hipStream_t s) {
   return hipGetLastError();
 }
 
+// k-chunks of the shared-activation kernel: about 2048 waves over the part, at most TPB/64 waves
+// per workgroup (TPB = the kernel's launch bound), the stage count divisible by the chunk count, and the activation rings of every
+// chunk plus the reduction within the 160 KiB of LDS.
+inline void shared_split(int N, int K, int MB, int R, int U, int SN, int TPB, int* SK_out,
+                         int* chunk_out, size_t* lds_out) {
+  const int stages = K / (64 * U);
+  const int wgs = N / (16 * R * SN);
+  int SK = (2048 + wgs * SN - 1) / (wgs * SN);
+  if (SK > TPB / 64 / SN) SK = TPB / 64 / SN;
+  if (SK < 1) SK = 1;
+  const size_t stage = (size_t)16 * MB * 128 * U;
+  auto lds = [&](int sk) {
+    return (size_t)sk * 2 * stage + (sk > 1 ? (size_t)SN * sk * R * MB * 1024 : 0);
+  };
+  while (SK > 1 && (stages % SK != 0 || lds(SK) > 160 * 1024)) --SK;
+  *SK_out = SK;
+  *chunk_out = stages / SK * 64 * U;
+  *lds_out = lds(SK);
+}
+
+template <int MB, int R, int U, int SN, int TPB>
+inline hipError_t launch_shared(const GemmParams& p, hipStream_t s) {
+  StreamArgs a;
+  a.A = p.A;
+  a.B = p.B;
+  a.scale = nullptr;
+  a.zero = nullptr;
+  a.C = p.C;
+  a.M = p.M;
+  a.N = p.N;
+  a.K = p.K;
+  a.lda = p.lda;
+  a.ldb = p.ldb;
+  a.ldc = p.ldc;
+  a.group = 0;
+  size_t lds = 0;
+  shared_split(p.N, p.K, MB, R, U, SN, TPB, &a.S, &a.chunk, &lds);
+  const dim3 grid(p.N / (16 * R * SN)), blk(64 * SN * a.S);
+  hipLaunchKernelGGL((k_stream_sh<MB, R, U, 0, SN, TPB>), grid, blk, lds, s, a);
+  return hipGetLastError();
+}
+
 template <int BM, int BN, int BK, int WM, int WN, int MS, int SWZ, int GROUP, int XCD>
 inline hipError_t launch_mfma(const GemmParams& p, hipStream_t s) {
   const int nm = (p.M + BM - 1) / BM;

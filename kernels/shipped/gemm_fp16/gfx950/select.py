@@ -8,9 +8,10 @@ Rows are tried in order; the first row whose band holds (M, N) -- M <= M_max and
 AND whose kernel fits the shape (divisibility) is taken.  No such row: None, the caller's own
 path.  (The reference stops at the first band that holds M; here a row that does not fit falls
 through to the next one, so a narrower row can sit in front of a general one.)
-  * M <= 32   stream: the weight-streaming decode kernel (HBM-bound; one pass over B).  A = 1
-              stages the activations in LDS once per workgroup (M = 1).  Wide N takes four
-              row groups per wave (R = 4): fewer activation re-reads, still >= 192 slabs.
+  * M <= 32   stream / shared: the weight-streaming decode kernels (HBM-bound; one pass over
+              B).  A = 1 stages the activations in LDS once per workgroup (M = 1).  "shared"
+              (k_stream_sh) lets SN slab waves share one LDS copy of each activation stage, which
+              pays where N leaves enough slabs to fill the part (wide N).
   * M >  32   mfma / dma: LDS-tiled MFMA kernels (dma = LDS-DMA copies), tile chosen by M.
 """
 
@@ -19,9 +20,9 @@ ARCH = "gfx950"
 # (M_max, N_min, tag, kind, template params).  First row that holds (M, N) and fits wins.
 LADDER = [
     (1, 0, "s1a_r1u4", "stream", dict(MB=1, R=1, U=4, A=1)),
-    (16, 12288, "s16r4u2", "stream", dict(MB=1, R=4, U=2, A=0)),
+    (16, 12288, "h16r1u4n4", "shared", dict(MB=1, R=1, U=4, SN=4)),
     (16, 0, "s16r1u4", "stream", dict(MB=1, R=1, U=4, A=0)),
-    (32, 12288, "s32r4u2", "stream", dict(MB=2, R=4, U=2, A=0)),
+    (32, 12288, "h32r1u4n4", "shared", dict(MB=2, R=1, U=4, SN=4)),
     (32, 0, "s32r1u4", "stream", dict(MB=2, R=1, U=4, A=0)),
     (256, 0, "m128x128k64", "mfma",
      dict(BM=128, BN=128, BK=64, WM=2, WN=2, MS=32, SWZ=1, GROUP=8, XCD=1)),
@@ -37,6 +38,9 @@ STREAM_N_ROWS = 16  # weight rows per MFMA row group (times R)
 def _fits(kind, p, M, N, K):
     if kind == "stream":
         return N % (STREAM_N_ROWS * p["R"]) == 0 and K % (STREAM_K_STEP * p["U"]) == 0
+    if kind == "shared":
+        return (N % (STREAM_N_ROWS * p["R"] * p["SN"]) == 0
+                and K % (STREAM_K_STEP * p["U"]) == 0)
     return N % p["BN"] == 0 and K % p["BK"] == 0
 
 

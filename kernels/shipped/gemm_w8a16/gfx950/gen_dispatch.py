@@ -35,6 +35,9 @@ HEAD = """// GENERATED from select.py -- do not edit.  Regenerate with:
 
 
 def instantiation(kind, p):
+    if kind == "shared":
+        return "launch_shared<%d,%d,%d,%d,%d>" % (p["MB"], p["R"], p["U"], p["SN"],
+                                                  p.get("TPB", 1024))
     if kind == "stream":
         return "launch_stream<%d,%d,%d,%d>" % (p["MB"], p["R"], p["U"], p.get("A", 0))
     return "launch_mfma<%d,%d,%d,%d,%d,%d,%d,%d,%d>" % (
@@ -45,11 +48,16 @@ def condition(sel, kind, p, m_max, n_min=0):
     if kind == "stream":
         fit = "(p.N %% %d) == 0 && (p.K %% %d) == 0" % (sel.STREAM_N_ROWS * p["R"],
                                                           sel.STREAM_K_STEP * p["U"])
+    elif kind == "shared":
+        fit = "(p.N %% %d) == 0 && (p.K %% %d) == 0" % (sel.STREAM_N_ROWS * p["R"] * p["SN"],
+                                                          sel.STREAM_K_STEP * p["U"])
     else:
         fit = "(p.N %% %d) == 0 && (p.K %% %d) == 0" % (p["BN"], p["BK"])
     band = "p.M <= %d" % m_max
     if n_min:
         band += " && p.N >= %d" % n_min
+    if "fmts" in p:
+        band += " && (%s)" % " || ".join("p.fmt == %d" % f for f in p["fmts"])
     return band, fit
 
 

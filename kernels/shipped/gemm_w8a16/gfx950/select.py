@@ -12,13 +12,20 @@ ARCH = "gfx950"
 FORMATS = (1, 2)
 
 # (M_max, N_min, tag, kind, template params).  Rows are tried in order; the first row whose band
-# holds (M, N) -- M <= M_max and N >= N_min -- and whose kernel fits the shape is taken.
+# holds (M, N) -- M <= M_max and N >= N_min -- whose weight format is listed (params "fmts";
+# absent = both) and whose kernel fits the shape is taken.
 LADDER = [
     (1, 0, "s1a_r1u8", "stream", dict(MB=1, R=1, U=8, A=1)),
     (1, 0, "s1a_r1u4", "stream", dict(MB=1, R=1, U=4, A=1)),
-    (16, 4096, "s16r2u4", "stream", dict(MB=1, R=2, U=4, A=0)),
+    (8, 16384, "h8r1u2n2", "shared", dict(MB=1, R=1, U=2, SN=2, fmts=(1,))),
+    (8, 16384, "h8r1u4n2", "shared", dict(MB=1, R=1, U=4, SN=2)),
+    (8, 0, "s8r2u4", "stream", dict(MB=1, R=2, U=4, A=0)),
+    (16, 16384, "h16r1u2n2", "shared", dict(MB=1, R=1, U=2, SN=2, fmts=(1,))),
+    (16, 0, "h16r1u4n2", "shared", dict(MB=1, R=1, U=4, SN=2)),
     (16, 0, "s16r1u4", "stream", dict(MB=1, R=1, U=4, A=0)),
-    (32, 16384, "s32r4u2", "stream", dict(MB=2, R=4, U=2, A=0)),
+    (32, 16384, "h32r1u2n4", "shared", dict(MB=2, R=1, U=2, SN=4, fmts=(1,))),
+    (32, 16384, "h32r1u4n4", "shared", dict(MB=2, R=1, U=4, SN=4)),
+    (32, 0, "h32r1u4n2", "shared", dict(MB=2, R=1, U=4, SN=2, TPB=512)),
     (32, 0, "s32r2u4", "stream", dict(MB=2, R=2, U=4, A=0)),
     (256, 0, "m128x128k64", "mfma",
      dict(BM=128, BN=128, BK=64, WM=2, WN=2, MS=32, SWZ=1, GROUP=8, XCD=1)),
@@ -33,6 +40,9 @@ STREAM_N_ROWS = 16
 def _fits(kind, p, M, N, K):
     if kind == "stream":
         return N % (STREAM_N_ROWS * p["R"]) == 0 and K % (STREAM_K_STEP * p["U"]) == 0
+    if kind == "shared":
+        return (N % (STREAM_N_ROWS * p["R"] * p["SN"]) == 0
+                and K % (STREAM_K_STEP * p["U"]) == 0)
     return N % p["BN"] == 0 and K % p["BK"] == 0
 
 
@@ -46,6 +56,9 @@ def select(op, M, N, K, fmt=1, group=128, dtype_a="fp16", dtype_c="fp16", arch=A
     if fmt == 2 and (group != 128 or K % group):
         return None
     for m_max, n_min, tag, kind, p in LADDER:
+        if fmt not in p.get("fmts", FORMATS):
+            continue
         if M <= m_max and N >= n_min and _fits(kind, p, M, N, K):
-            return dict(tag=tag, kind=kind, fmt=fmt, **p)
+            q = {k: v for k, v in p.items() if k != "fmts"}
+            return dict(tag=tag, kind=kind, fmt=fmt, **q)
     return None

@@ -44,6 +44,8 @@ _ENTRY = {
              ("common/cdna4.h", "gemv_stream/kernel.hip")),
     "stream": ("k_stream", ("MB", "R", "U", "BFMT", "ALDS"), "StreamArgs",
                ("common/cdna4.h", "gemv_stream/kernel.hip")),
+    "shared": ("k_stream_sh", ("MB", "R", "U", "BFMT", "SN", "TPB"), "StreamArgs",
+               ("common/cdna4.h", "gemv_stream/kernel.hip")),
 }
 NAMESPACE = "tempo::gen"
 
@@ -87,6 +89,8 @@ class Gfx950Skeletons:
     def _split(self, op: OpSpec, p: dict):
         N, K = int(op.shapes["N"]), int(op.shapes["K"])
         kind = p["kind"]
+        if kind == "shared":
+            return space.shared_split(N, K, p["MB"], p["R"], p["U"], p["SN"], p["TPB"])[:2]
         if kind == "ring":
             per_wave = space.lds_bytes("ring", dict(p, S=1))
             return space.stream_split(N, K, p["R"], 64, p["BFMT"], per_wave)
@@ -114,6 +118,12 @@ class Gfx950Skeletons:
             return regs, int(regs * 1.2), space.lds_bytes(kind, p)
         wb = 2 if p["BFMT"] == 0 else 1
         S, _ = self._split(op, p)
+        if kind == "shared":
+            regs = (2 * p["R"] * p["MB"] * 4 + 2 * p["U"] * p["R"] * wb * 4 + 8 * p["MB"]
+                    + 2 * (p["R"] + p["MB"]) + 16)
+            lds = space.shared_split(int(op.shapes["N"]), int(op.shapes["K"]), p["MB"], p["R"],
+                                     p["U"], p["SN"], p["TPB"])[2]
+            return regs, int(regs * 1.25), lds
         if kind == "ring":
             regs = p["R"] * p["MB"] * 4 + (p["R"] * wb + 2 * p["MB"]) * 4 + 2 * (p["R"] + p["MB"]) + 16
         else:
@@ -133,6 +143,10 @@ class Gfx950Skeletons:
             grid = -(-M // p["BM"]) * (N // p["BN"])
             threads = p["WM"] * p["WN"] * 64
             S = 1
+        elif kind == "shared":
+            S, _ = self._split(op, p)
+            grid = N // (16 * p["R"] * p["SN"])
+            threads = 64 * p["SN"] * S
         else:
             S, _ = self._split(op, p)
             grid = N // (16 * p["R"])

@@ -69,8 +69,13 @@ def build_numbers(op):
                       layout_a="k", layout_b="k", layout_c="n",
                       shapes={"M": 4096, "N": 15360, "K": 3840})
         for m_max, n_min, tag, kind, p in sel.LADDER:
-            pk = {"stream": "stream", "mfma": "reg", "dma": "dma"}[kind]
-            params = dict(p, kind=pk)
+            if fmt not in p.get("fmts", (fmt,)):
+                continue
+            pk = {"stream": "stream", "mfma": "reg", "dma": "dma", "shared": "shared"}[kind]
+            params = {k: v for k, v in p.items() if k != "fmts"}
+            params["kind"] = pk
+            if pk == "shared":
+                params.setdefault("TPB", 1024)
             if pk != "dma":
                 params["BFMT"] = fmt
             if pk == "stream":
@@ -131,10 +136,14 @@ def make(op, rows_files=()):
         if kind == "stream":
             fit = "N %% %d == 0 and K %% %d == 0" % (sel.STREAM_N_ROWS * p["R"],
                                                     sel.STREAM_K_STEP * p["U"])
+        elif kind == "shared":
+            fit = "N %% %d == 0 and K %% %d == 0" % (sel.STREAM_N_ROWS * p["R"] * p["SN"],
+                                                    sel.STREAM_K_STEP * p["U"])
         else:
             fit = "N %% %d == 0 and K %% %d == 0" % (p["BN"], p["BK"])
-        man["dispatch"].append(dict(M_max=m_max, N_min=n_min, tag=tag, kind=kind, params=p,
-                                    fit=fit))
+        man["dispatch"].append(dict(M_max=m_max, N_min=n_min, tag=tag, kind=kind,
+                                    params={k: v for k, v in p.items() if k != "fmts"},
+                                    fmts=list(p.get("fmts", OPS[op]["fmts"])), fit=fit))
     if op == "gemm_w8a16":
         man["predicate"]["formats"] = {"1": "int8 weights, fp16 scale per output channel",
                                        "2": "uint8 weights, fp16 scale + uint8 zero per (row, 128 k)"}

@@ -117,6 +117,8 @@ struct Arm {
   int MB, R, U, BFMT;  // U = k-steps per stage (register kernel) or 1 (ring kernel)
   int D;               // ring depth (LDS-DMA kernel), 0 for the register kernel
   LaunchFn launch;
+  int SN = 0;          // shared-activation kernel: slab waves per workgroup (0: other kernels)
+  int TPB = 512;       // shared-activation kernel: launch bound
 };
 template <int MB, int R, int U, int BFMT, int ALDS = 0>
 static void launch_arm(StreamArgs a, hipStream_t s) {
@@ -131,6 +133,26 @@ static void launch_arm_dma(StreamArgs a, hipStream_t s) {
   const size_t lds = stream_dma_lds<MB, R, D, BFMT>(a.S);
   hipLaunchKernelGGL((k_stream_dma<MB, R, D, BFMT>), grid, blk, lds, s, a);
 }
+template <int MB, int R, int U, int BFMT, int SN, int TPB>
+static void launch_arm_sh(StreamArgs a, hipStream_t s) {
+  const dim3 grid(a.N / (16 * R * SN)), blk(64 * SN * a.S);
+  const size_t lds = StreamSh<MB, U>::lds(SN, a.S, R);
+  hipLaunchKernelGGL((k_stream_sh<MB, R, U, BFMT, SN, TPB>), grid, blk, lds, s, a);
+}
+// k-chunks of the shared kernel: about 2048 waves over the part, at most 8 waves per
+// workgroup, the stage count divisible by the chunk count
+static void sh_split(int N, int K, int R, int U, int SN, int TPB, int* SK_out, int* chunk_out) {
+  const int stages = K / (64 * U);
+  const int wgs = N / (16 * R * SN);
+  int SK = (2048 + wgs * SN - 1) / (wgs * SN);
+  if (SK > TPB / 64 / SN) SK = TPB / 64 / SN;
+  if (SK < 1) SK = 1;
+  while (stages % SK) --SK;
+  *SK_out = SK;
+  *chunk_out = stages / SK * 64 * U;
+}
+#define STREAMS(tag, MB, R, U, F, SN, TPB) \
+  Arm{tag, MB, R, U, F, 0, &launch_arm_sh<MB, R, U, F, SN, TPB>, SN, TPB},
 #define STREAM(tag, MB, R, U, F) Arm{tag, MB, R, U, F, 0, &launch_arm<MB, R, U, F>},
 #define STREAMA(tag, MB, R, U, F) Arm{tag, MB, R, U, F, -1, &launch_arm<MB, R, U, F, 1>},
 #define STREAMD(tag, MB, R, D, F) Arm{tag, MB, R, 1, F, D, &launch_arm_dma<MB, R, D, F>},
@@ -239,6 +261,20 @@ int main(int argc, char** argv) {
     a.ldc = N;
     a.group = 128;
     split_rule(N, K, arm.R, arm.U, &a.S, &a.chunk, force_s);
+    if (arm.SN > 0) {
+      if (N % (16 * arm.R * arm.SN)) continue;
+      sh_split(N, K, arm.R, arm.U, arm.SN, arm.TPB, &a.S, &a.chunk);
+      // activation rings of every k-chunk + the reduction must fit the 160 KiB of LDS
+      const size_t stage = (size_t)16 * arm.MB * 128 * arm.U;
+      while (a.S > 1 && (size_t)a.S * 2 * stage + (size_t)arm.SN * a.S * arm.R * arm.MB * 1024 >
+                            160 * 1024) {
+        const int stages = K / (64 * arm.U);
+        int sk = a.S - 1;
+        while (stages % sk) --sk;
+        a.S = sk;
+        a.chunk = stages / sk * 64 * arm.U;
+      }
+    }
     if (arm.D < 0 && (size_t)M * (2 * (size_t)K + 16) > 96 * 1024) continue;  // LDS activations
     if (arm.D > 0) {  // ring kernel: LDS of S waves within 160 KiB; fmt 2 chunk <= 8192 k
       const size_t per_wave = (size_t)arm.D * (arm.R * eb + 2 * arm.MB) * 1024 +

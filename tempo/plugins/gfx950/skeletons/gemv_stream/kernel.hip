@@ -554,3 +554,245 @@ __global__ __launch_bounds__(256) void k_read_probe(const uint8_t* src, long byt
   asm volatile("" ::: "memory");
   if (accum == 0x9e3779b9u) out[0] = accum;  // practically never; keeps the reads alive
 }
+
+// ============================================================================================
+// k_stream_sh -- the decode kernel with the activations SHARED between waves.
+//
+// k_stream re-reads the whole activation block A[0..M)[k-chunk] from L2 in every workgroup (one
+// workgroup = one slab of 16R weight rows), so at M = 16..32 the activation traffic equals or
+// exceeds the weight traffic and, measured, caps the kernel well below the M = 1 rate (the same
+// kernel with all activation rows aliased to one reaches the M = 1 rate).  Here one workgroup
+// holds SN slabs x SK k-chunks of waves (wave w: slab group w % SN, k-chunk w / SN).  The SN waves
+// of one k-chunk walk the same k-steps, so each stage of activations (16*MB rows x 64U k) is
+// brought global -> LDS ONCE by LDS-DMA (the SN waves split the copy) into a two-slot ring of that
+// k-chunk, and read from there by all SN waves: activation traffic drops by SN.  Weights stay in
+// the register pipeline of k_stream (stage s+1 in flight while stage s computes), dequantised in
+// registers, MFMA 16x16x32 as before; the SK partial sums of a slab are added through LDS in
+// k-chunk order (deterministic) and written by the chunk-0 wave.
+//
+// Per iteration s (all waves of the workgroup in step): wait until this wave's copies for stage s
+// have landed and its LDS reads of stage s-1 are done; s_barrier (everyone's copies for stage s
+// landed, everyone done with slot (s+1) % 2); issue the weight loads of stage s+1 and the
+// activation copy of stage s+1 into slot (s+1) % 2; compute stage s.
+//
+// LDS activation stage: [16*MB rows][64U k] fp16, 16-byte chunk c of row r stored at chunk
+// c ^ (r % 16), so the 16 rows of one fragment read hit 16 distinct bank groups.  Rows >= M are
+// copies of row M-1 (never stored to C).
+// Requirements (launcher): N % (16*R*SN) == 0, the stage count K / (64U) divisible by SK, and
+// (2*MB*U) % SN == 0 (whole 1 KiB copy blocks per wave).
+// ============================================================================================
+template <int N>
+__device__ __forceinline__ void s_wait_vm_lgkm0() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0x0 << 8));
+}
+
+template <int MB, int U>
+struct StreamSh {
+  static constexpr int RB = 128 * U;                // bytes per activation row per stage
+  static constexpr int STAGE = 16 * MB * RB;        // bytes per activation stage
+  static constexpr int NBLK = STAGE / 1024;         // 1 KiB copy blocks per stage
+  static constexpr size_t lds(int SN, int SK, int R) {
+    return (size_t)SK * 2 * STAGE + (SK > 1 ? (size_t)SN * SK * R * MB * 64 * 16 : 0);
+  }
+};
+
+// TPB: the launch bound (512 or 1024 lanes; 1024 caps a lane at 128 registers)
+template <int MB, int R, int U, int BFMT, int SN, int TPB = 512>
+__global__ __launch_bounds__(TPB) void k_stream_sh(StreamArgs p) {
+  using SS = StreamSh<MB, U>;
+  constexpr int RB = SS::RB, STAGE = SS::STAGE, NBLK = SS::NBLK;
+  static_assert(NBLK % SN == 0, "activation copy blocks split evenly over the slab waves");
+  static_assert(U >= 2, "a stage row must hold at least 16 chunks for the swizzle");
+  constexpr int BW = NBLK / SN;  // copy blocks per wave per stage
+  extern __shared__ __attribute__((aligned(1024))) uint8_t dsh[];
+  const int SK = p.S;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int ng = wave % SN, kgrp = wave / SN;
+  uint8_t* ring = dsh + (size_t)kgrp * 2 * STAGE;
+  f32x4* red = reinterpret_cast<f32x4*>(dsh + (size_t)SK * 2 * STAGE);
+
+  const int r16 = lane & 15;
+  const int kg = lane >> 4;
+  const int slab = blockIdx.x * SN + ng;
+  const int nbase = slab * 16 * R;
+  const int kbeg = kgrp * p.chunk;
+  constexpr int STEP = 64 * U;
+  const int nst = p.chunk / STEP;  // identical for every k-chunk (launcher)
+
+  const uint8_t* wrow[R];
+  _Float16 rscale[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const long n = nbase + r * 16 + r16;
+    constexpr int EB = BFMT == 0 ? 2 : 1;
+    wrow[r] = reinterpret_cast<const uint8_t*>(p.B) + (n * p.ldb + 16 * kg) * EB;
+    if constexpr (BFMT == 1) rscale[r] = p.scale[n];
+  }
+
+  // activation copy: block i of this wave = stage block (i*SN + ng); lane -> (row, phys chunk)
+  long asrc[BW];
+#pragma unroll
+  for (int i = 0; i < BW; ++i) {
+    const int off = (i * SN + ng) * 1024 + 16 * lane;
+    const int row = off / RB, phys = (off % RB) / 16;
+    const int logical = phys ^ (row & 15);
+    asrc[i] = (long)min(row, p.M - 1) * p.lda + 8 * logical;
+  }
+  auto copy_act = [&](int s) {
+    uint8_t* dst = ring + (s & 1) * STAGE;
+    const _Float16* base = p.A + kbeg + s * STEP;
+#pragma unroll
+    for (int i = 0; i < BW; ++i)
+      __builtin_amdgcn_global_load_lds((void*)(base + asrc[i]),
+                                       (lds_void_stream_t*)(dst + (i * SN + ng) * 1024), 16, 0, 0);
+  };
+  // fragment read offsets: row b*16 + r16, chunks 8u + 2kg (+1) XOR r16; (8u + 2kg) ^ r16 only
+  // touches bits 0..3, so two variants by u & 1, plus 16 chunks per two k-steps
+  int aoff0[2], aoff1[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    aoff0[q] = r16 * RB + ((8 * q + 2 * kg) ^ r16) * 16;
+    aoff1[q] = r16 * RB + ((8 * q + 2 * kg + 1) ^ r16) * 16;
+  }
+
+  f32x4 acc[R][MB], acc2[R][MB];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int b = 0; b < MB; ++b) {
+      acc[r][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+      acc2[r][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+  WRaw<BFMT> w[2][U][R];
+  constexpr int GPS = (64 * U) / 128 > 0 ? (64 * U) / 128 : 1;
+  GMeta<GPS> gm[2][R];
+  const long gstride = BFMT == 2 ? (long)(p.K / 128) : 0;
+
+  auto issue_w = [&](auto bufc, int k0) {
+    constexpr int buf = decltype(bufc)::value;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int k = k0 + 64 * u;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        if constexpr (BFMT == 0) {
+          const u32x4* q = reinterpret_cast<const u32x4*>(wrow[r] + (long)k * 2);
+          w[buf][u][r].v[0] = q[0];
+          w[buf][u][r].v[1] = q[1];
+        } else {
+          w[buf][u][r].v = *reinterpret_cast<const u32x4*>(wrow[r] + k);
+        }
+      }
+    }
+    if constexpr (BFMT == 2) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const long gi = (long)(nbase + r * 16 + r16) * gstride + k0 / 128;
+        gmeta_load<GPS>(gm[buf][r], p.zero + gi, p.scale + gi);
+      }
+    }
+  };
+
+  auto compute = [&](auto bufc, int s) {
+    constexpr int buf = decltype(bufc)::value;
+    const uint8_t* a = ring + (s & 1) * STAGE;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        f16x8 w0, w1;
+        if constexpr (BFMT == 0) {
+          w0 = as_f16x8(w[buf][u][r].v[0]);
+          w1 = as_f16x8(w[buf][u][r].v[1]);
+        } else if constexpr (BFMT == 1) {
+          const u32x4 q = w[buf][u][r].v;
+          w0 = dequant8_i8(q[0], q[1], rscale[r]);
+          w1 = dequant8_i8(q[2], q[3], rscale[r]);
+        } else {
+          const u32x4 q = w[buf][u][r].v;
+          uint8_t z;
+          _Float16 sc;
+          gmeta_get<GPS>(gm[buf][r], (64 * u) / 128, z, sc);
+          w0 = dequant8_u8(q[0], q[1], z, sc);
+          w1 = dequant8_u8(q[2], q[3], z, sc);
+        }
+#pragma unroll
+        for (int b = 0; b < MB; ++b) {
+          const uint8_t* rowp = a + b * 16 * RB + (u >> 1) * 256;
+          const u32x4 a0 = *reinterpret_cast<const u32x4*>(rowp + aoff0[u & 1]);
+          const u32x4 a1 = *reinterpret_cast<const u32x4*>(rowp + aoff1[u & 1]);
+          acc[r][b] = Mfma<16>::run(w0, as_f16x8(a0), acc[r][b]);
+          acc2[r][b] = Mfma<16>::run(w1, as_f16x8(a1), acc2[r][b]);
+        }
+      }
+    }
+  };
+
+  // one pipeline step: (top) stage s landed for everyone; issue stage s+1; compute stage s
+  auto step = [&](auto bufc, int s) {
+    constexpr int buf = decltype(bufc)::value;
+    asm volatile("" ::: "memory");
+    s_wait_vm_lgkm0<0>();
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (s + 1 < nst) {
+      issue_w(IC<buf ^ 1>{}, kbeg + (s + 1) * STEP);
+      copy_act(s + 1);
+    }
+    compute(bufc, s);
+  };
+
+  if (nst > 0) {
+    issue_w(IC<0>{}, kbeg);
+    copy_act(0);
+  }
+  int s = 0;
+  for (; s + 1 < nst; s += 2) {
+    step(IC<0>{}, s);
+    step(IC<1>{}, s + 1);
+  }
+  if (s < nst) step(IC<0>{}, s);
+
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int b = 0; b < MB; ++b) acc[r][b] += acc2[r][b];
+
+  if (SK > 1) {
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int b = 0; b < MB; ++b) red[(wave * R * MB + r * MB + b) * 64 + lane] = acc[r][b];
+    __syncthreads();
+    if (kgrp != 0) return;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int b = 0; b < MB; ++b) {
+        f32x4 t = acc[r][b];
+        for (int g = 1; g < SK; ++g) {
+          const f32x4 v = red[((g * SN + ng) * R * MB + r * MB + b) * 64 + lane];
+          t[0] += v[0]; t[1] += v[1]; t[2] += v[2]; t[3] += v[3];
+        }
+        acc[r][b] = t;
+      }
+  }
+#pragma unroll
+  for (int b = 0; b < MB; ++b) {
+    const int m = b * 16 + r16;
+    if (m >= p.M) continue;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int n = nbase + r * 16 + 4 * kg;
+      f16x4 o;
+      o[0] = (_Float16)acc[r][b][0];
+      o[1] = (_Float16)acc[r][b][1];
+      o[2] = (_Float16)acc[r][b][2];
+      o[3] = (_Float16)acc[r][b][3];
+      *reinterpret_cast<f16x4*>(p.C + (long)m * p.ldc + n) = o;
+    }
+  }
+}

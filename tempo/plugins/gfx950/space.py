@@ -41,6 +41,7 @@ DOMAINS = {
                 XCD=(1,)),
     "ring": dict(R=(1, 2, 4), D=(4, 5, 6, 8, 10, 12, 14, 16)),
     "stream": dict(R=(1, 2, 4), U=(2, 4, 8), ALDS=(0, 1)),
+    "shared": dict(R=(1, 2), U=(2, 4), SN=(2, 4, 8)),
 }
 
 BFMT_OF = {("fp16", "fp16"): 0, ("fp16", "int8"): 1, ("fp16", "uint8"): 2}
@@ -65,6 +66,10 @@ def lds_bytes(kind: str, p: dict) -> int:
         return p.get("S", 1) * per_wave + (p.get("S", 1) * p["R"] * p["MB"] * 1024 if p.get("S", 1) > 1 else 0)
     if kind == "stream":
         return p.get("S", 1) * p["R"] * p["MB"] * 1024 if p.get("S", 1) > 1 else 0
+    if kind == "shared":
+        sk = p.get("S", 1)
+        return sk * 2 * 16 * p["MB"] * 128 * p["U"] + (p["SN"] * sk * p["R"] * p["MB"] * 1024
+                                                       if sk > 1 else 0)
     raise KeyError(kind)
 
 
@@ -86,6 +91,21 @@ def stream_split(N: int, K: int, R: int, step_k: int, bfmt_: int = 0, per_wave_l
     return S, chunk
 
 
+def shared_split(N: int, K: int, MB: int, R: int, U: int, SN: int, TPB: int = 1024):
+    """(SK, chunk, lds bytes) of the shared-activation kernel, as the shipped launchers compute."""
+    stages = K // (64 * U)
+    wgs = max(1, N // (16 * R * SN))
+    SK = min(TPB // 64 // SN, max(1, -(-2048 // (wgs * SN))))
+    stage = 16 * MB * 128 * U
+
+    def lds(sk):
+        return sk * 2 * stage + (SN * sk * R * MB * 1024 if sk > 1 else 0)
+
+    while SK > 1 and (stages % SK or lds(SK) > LDS_MAX):
+        SK -= 1
+    return SK, stages // SK * 64 * U, lds(SK)
+
+
 def tag(kind: str, p: dict) -> str:
     if kind == "dma":
         return "dma_m%dn%dk%d_w%dx%d_s%d_z%d_g%d_x%d_f%d" % (
@@ -96,6 +116,8 @@ def tag(kind: str, p: dict) -> str:
                                                    p["MS"], p["SWZ"], p["BFMT"])
     if kind == "ring":
         return "ring_mb%d_r%d_d%d_b%d" % (p["MB"], p["R"], p["D"], p["BFMT"])
+    if kind == "shared":
+        return "shared_mb%d_r%d_u%d_b%d_n%d" % (p["MB"], p["R"], p["U"], p["BFMT"], p["SN"])
     return "stream_mb%d_r%d_u%d_b%d_a%d" % (p["MB"], p["R"], p["U"], p["BFMT"], p.get("ALDS", 0))
 
 
@@ -127,6 +149,12 @@ def legal(kind: str, p: dict, M: int, N: int, K: int):
         return "N %% %d" % (16 * R)
     if M > 16 * p["MB"]:
         return "M > 16*MB"
+    if kind == "shared":
+        if N % (16 * R * p["SN"]) or K % (64 * p["U"]) or p["U"] < 2:
+            return "shape does not divide into slab groups / stages"
+        if (2 * p["MB"] * p["U"]) % p["SN"]:
+            return "activation copy blocks do not split over the slab waves"
+        return None
     if kind == "ring":
         wb = 2 if p["BFMT"] == 0 else 1
         if K % 64:
@@ -161,6 +189,10 @@ def variants(op: OpSpec) -> Iterator[Hyperform]:
             for U in DOMAINS["stream"]["U"]:
                 for AL in DOMAINS["stream"]["ALDS"]:
                     out.append(("stream", dict(MB=MB, R=R, U=U, BFMT=b, ALDS=AL)))
+        for R in DOMAINS["shared"]["R"]:
+            for U in DOMAINS["shared"]["U"]:
+                for SN in DOMAINS["shared"]["SN"]:
+                    out.append(("shared", dict(MB=MB, R=R, U=U, BFMT=b, SN=SN, TPB=1024)))
     if b == 0:
         d = DOMAINS["dma"]
         for BM in d["BM"]:

@@ -27,6 +27,12 @@ def make_weights(N, K, fmt, seed, G=128):
     return q, s, z
 
 
+def _route(fmt, M, N, K):
+    from cuda_tempiler_amd import capi
+
+    return capi.route(fmt, M, N, K)
+
+
 def _run(A, q, s, z, fmt, device, G=128):
     import torch
     from cuda_tempiler_amd import capi
@@ -82,10 +88,10 @@ def test_dequant_covers_every_byte_and_zero_point(gpu, fmt):
 
 
 @pytest.mark.parametrize("fmt", [1, 2])
-@pytest.mark.parametrize("M", [1, 16, 32, 128])
+@pytest.mark.parametrize("M", [1, 5, 8, 16, 27, 32, 128])
 def test_w8a16_parity_small_m(gpu, fmt, M):
     for N, K in SHAPES_NK:
-        say("w8a16 fmt", fmt, "M", M, "N", N, "K", K)
+        say("w8a16 fmt", fmt, "M", M, "N", N, "K", K, "route", _route(fmt, M, N, K))
         A = O.randn_f16((M, K), 11, K ** -0.5)
         q, s, z = make_weights(N, K, fmt, 77)
         C = _run(A, q, s, z, fmt, gpu)
@@ -114,11 +120,14 @@ def test_w8a16_parity_prefill(gpu, fmt):
 
 
 @pytest.mark.parametrize("fmt", [1, 2])
-@pytest.mark.parametrize("M", [1, 32, 300])
-def test_w8a16_exact_regime_bit_exact(gpu, fmt, M):
+@pytest.mark.parametrize("M", [1, 8, 16, 32, 300])
+@pytest.mark.parametrize("N", [1024, 17408])
+def test_w8a16_exact_regime_bit_exact(gpu, fmt, M, N):
     """Scales that are powers of two and activations on a 1/8 grid make every product and
-    partial sum exact in fp32, so the result is order-independent: bits must equal the oracle."""
-    N, K = 1024, 2048
+    partial sum exact in fp32, so the result is order-independent: bits must equal the oracle.
+    N = 17408 reaches the wide-N ladder rows (shared activations, k-chunk reduction)."""
+    K = 2048
+    say("exact regime fmt", fmt, "M", M, "N", N, "route", _route(fmt, M, N, K))
     g = np.random.Generator(np.random.PCG64(31))
     A = (g.integers(-4, 5, (M, K)).astype(np.float32) / 8).astype(np.float16)
     if fmt == 1:

@@ -109,8 +109,10 @@ def test_route_unknown_op_is_empty():
 def test_rows_fall_through_when_the_first_row_does_not_fit():
     from cuda_tempiler_amd import capi
 
-    assert capi.route(0, 8, 15360, 3840) == "s16r4u2"
+    assert capi.route(0, 8, 15360, 3840) == "h16r1u4n4"
     assert capi.route(0, 8, 12304, 3840) == "s16r1u4"   # N % 64 != 0
+    assert capi.route(1, 16, 34816, 5120) == "h16r1u2n2"  # int8 only
+    assert capi.route(2, 16, 34816, 5120) == "h16r1u4n2"
     assert capi.route(0, 1, 15360, 3840) == "s1a_r1u4"
     assert capi.route(1, 1, 5120, 5120) == "s1a_r1u8"
     assert capi.route(1, 1, 5120, 5376) == "s1a_r1u4"   # K % 512 != 0, K % 256 == 0
