@@ -528,4 +528,280 @@ __global__ __launch_bounds__(64 * WAVES, MINB) void k_fmha_fwd2(
   }
 }
 
+// ============================================================================================
+// k_fmha_fwd3 -- k_fmha_fwd2 with the score MFMAs of the NEXT key block overlapping the softmax
+// of the current one.  Iteration kb computes S(kb+1) = K(kb+1).Q^T on the matrix cores while the
+// VALU turns S(kb) into P(kb) (max, exponentials, sums), then O^T += V(kb)^T . P(kb)^T.  K runs
+// one block ahead of V: K(kb+2) and V(kb+1) are copied during iteration kb into the slots that
+// K(kb) and V(kb-1) left, so the LDS footprint is the same two K and two V blocks as before.
+// sched_group_barrier hints interleave one MFMA with a few VALU/LDS instructions so the wave
+// keeps issuing softmax work while each MFMA occupies the matrix core.
+// ============================================================================================
+// SG = 1 adds sched_group_barrier hints that interleave MFMAs with LDS reads and VALU work.
+template <int D, bool CAUSAL, int BKV2, int SG = 0>
+__global__ __launch_bounds__(256, 1) void k_fmha_fwd3(
+    const _Float16* __restrict__ Q, const _Float16* __restrict__ Kg,
+    const _Float16* __restrict__ Vg, _Float16* __restrict__ O, float* __restrict__ LSE, int B,
+    int H, int Hkv, int Sq, int Sk, float scale_log2, long q_sb, long q_ss, long q_sh, long k_sb,
+    long k_ss, long k_sh, long v_sb, long v_ss, long v_sh, long o_sb, long o_ss, long o_sh) {
+  static_assert(D == 128 || D == 256, "head dim 128 or 256");
+  static_assert(BKV2 == 32 || BKV2 == 64, "key block 32 or 64");
+  constexpr int WAVES = 4;
+  constexpr int NJ = BKV2 / 32;
+  constexpr int DCH = D / 8;
+  constexpr int DS = D / 16;
+  constexpr int DB = D / 32;
+  constexpr int RB = D * 2;
+  constexpr int ROWS_PER_KB = 1024 / RB;
+  constexpr int BLK = BKV2 / ROWS_PER_KB;
+  constexpr int BLK_W = BLK / WAVES;
+  constexpr int BQW = 32 * WAVES;
+  constexpr int TILE_B = BKV2 * RB;
+  static_assert(BLK % WAVES == 0, "DMA blocks split over the waves");
+
+  __shared__ __attribute__((aligned(1024))) char smem[4 * TILE_B];  // K[2] then V[2]
+  char* const kbuf = smem;
+  char* const vbuf = smem + 2 * TILE_B;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int hl = lane >> 5;
+  const int l32 = lane & 31;
+
+  const int nqb = (Sq + BQW - 1) / BQW;
+  const int bid = blockIdx.x;
+  const int per_qb = H * B;
+  const int qb = CAUSAL ? (nqb - 1 - bid / per_qb) : bid / per_qb;
+  const int hb = bid % per_qb;
+  const int h = hb % H, b = hb / H;
+  const int hk = h / (H / Hkv);
+  const int off = Sk - Sq;
+  const int q0 = qb * BQW;
+  const int qi = q0 + wave * 32 + l32;
+  const int qrow = min(qi, Sq - 1);
+
+  const _Float16* Qp = Q + b * q_sb + (long)h * q_sh;
+  const char* Kp = reinterpret_cast<const char*>(Kg + b * k_sb + (long)hk * k_sh);
+  const char* Vp = reinterpret_cast<const char*>(Vg + b * v_sb + (long)hk * v_sh);
+
+  f16x8 qf[DS];
+#pragma unroll
+  for (int st = 0; st < DS; ++st)
+    qf[st] = *reinterpret_cast<const f16x8*>(Qp + (long)qrow * q_ss + 16 * st + 8 * hl);
+
+  int kend = Sk;
+  if (CAUSAL) {
+    const int last = min(q0 + BQW, Sq) - 1 + off;
+    kend = last + 1 < Sk ? last + 1 : Sk;
+    if (kend < 0) kend = 0;
+  }
+  const int nkb = (kend + BKV2 - 1) / BKV2;
+
+  const int rin = lane / DCH, phys = lane % DCH;
+  unsigned ksrc[BLK_W], vsrc[BLK_W];
+  int drow[BLK_W];
+#pragma unroll
+  for (int i = 0; i < BLK_W; ++i) {
+    const int r = (i * WAVES + wave) * ROWS_PER_KB + rin;
+    const int c = phys ^ fmha_swz(r);
+    drow[i] = r;
+    ksrc[i] = (unsigned)(r * k_ss * 2 + c * 16);
+    vsrc[i] = (unsigned)(r * v_ss * 2 + c * 16);
+  }
+  // one operand block j (K or V) -> its slot j & 1; rows past Sk re-read row Sk-1
+  auto copy_block = [&](const char* base, long ss, const unsigned* src, char* slots, int j) {
+    char* dst = slots + (j & 1) * TILE_B;
+    const int j0 = j * BKV2;
+    const char* blk = base + (long)j0 * ss * 2;
+    if (j0 + BKV2 <= Sk) {
+#pragma unroll
+      for (int i = 0; i < BLK_W; ++i)
+        __builtin_amdgcn_global_load_lds((void*)(blk + src[i]),
+                                         (fmha_lds_void_t*)(dst + (i * WAVES + wave) * 1024), 16,
+                                         0, 0);
+    } else {
+#pragma unroll
+      for (int i = 0; i < BLK_W; ++i) {
+        const long back = (long)max(0, j0 + drow[i] - (Sk - 1));
+        __builtin_amdgcn_global_load_lds((void*)(blk + src[i] - back * ss * 2),
+                                         (fmha_lds_void_t*)(dst + (i * WAVES + wave) * 1024), 16,
+                                         0, 0);
+      }
+    }
+  };
+
+  const int kkey = fmha_swz(l32);
+  int koff[8];
+#pragma unroll
+  for (int s7 = 0; s7 < 8; ++s7) koff[s7] = l32 * RB + (((2 * s7) | hl) ^ kkey) * 16;
+  const int tg = lane >> 4, tj = lane & 15;
+  const int tk = 4 * (tg >> 1) + (tj >> 2);
+  const int cd = 2 * (tg & 1) + ((tj & 3) >> 1);
+  const int half = 8 * (tj & 1);
+  int voff0[4], voff1[4];
+#pragma unroll
+  for (int p4 = 0; p4 < 4; ++p4) {
+    voff0[p4] = tk * RB + (((p4 << 2) | cd) ^ fmha_swz(tk)) * 16 + half;
+    voff1[p4] = (tk + 8) * RB + (((p4 << 2) | cd) ^ fmha_swz(tk + 8)) * 16 + half;
+  }
+
+  f32x16 acc_o[DB];
+#pragma unroll
+  for (int i = 0; i < DB; ++i)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc_o[i][v] = 0.f;
+  float m_run = -__builtin_inff();
+  float l_run = 0.f;
+
+  // S^T of block j from K slot j & 1 into s (NJ 32-key blocks)
+  auto scores = [&](f32x16* s, int j) {
+    const char* k = kbuf + (j & 1) * TILE_B;
+#pragma unroll
+    for (int jb = 0; jb < NJ; ++jb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[jb][r] = 0.f;
+#pragma unroll
+      for (int st = 0; st < DS; ++st) {
+        const f16x8 kf = *reinterpret_cast<const f16x8*>(k + koff[st & 7] + (st >> 3) * 256 +
+                                                         jb * 32 * RB);
+        s[jb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[st], s[jb], 0, 0, 0);
+      }
+    }
+  };
+  // softmax, part 1: masked row max of block j (scale > 0 commutes with the max)
+  auto softmax_max = [&](f32x16* s, int j) {
+    const int j0 = j * BKV2;
+    const bool need_mask = (j0 + BKV2 > Sk) || (CAUSAL && j0 + BKV2 - 1 > q0 + off);
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int jb = 0; jb < NJ; ++jb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float x = s[jb][r];
+        if (need_mask) {
+          const int jj = j0 + 32 * jb + 8 * (r >> 2) + 4 * hl + (r & 3);
+          const bool hide = (jj >= Sk) || (CAUSAL && jj > qi + off);
+          x = hide ? -__builtin_inff() : x;
+        }
+        s[jb][r] = x;
+        mx = fmaxf(mx, x);
+      }
+    return fmaxf(mx, __shfl_xor(mx, 32)) * scale_log2;
+  };
+  // the (rare) move of the reference value, with the O rescale it implies
+  auto move_ref = [&](float mx) {
+    const bool move = !(mx - m_run <= FMHA_TAU);
+    if (__builtin_amdgcn_ballot_w64(move) != 0) {
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha =
+          (m_new == -__builtin_inff()) ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
+      l_run *= alpha;
+      m_run = m_new;
+#pragma unroll
+      for (int i = 0; i < DB; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc_o[i][r] *= alpha;
+    }
+  };
+  // softmax, part 2 fused with O^T += V^T . P^T: the 8 probabilities of MFMA k-step t are made
+  // right before the step's MFMAs, so the exponentials of step t+1 overlap the MFMAs of step t.
+  // Step t, element e <-> key 32(t/2) + 16(t%2) + 8(e/4) + 4*hl + e%4 = S register 8(t%2) + e of
+  // 32-key block t/2.
+  auto exp_pv = [&](const f32x16* s, int j) {
+    const char* v = vbuf + (j & 1) * TILE_B;
+    const float m_use = (m_run == -__builtin_inff()) ? 0.f : m_run;
+    float psum = 0.f;
+#pragma unroll
+    for (int t = 0; t < 2 * NJ; ++t) {
+      f16x8 pt;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float pv = __builtin_amdgcn_exp2f(
+            __builtin_fmaf(s[t >> 1][8 * (t & 1) + e], scale_log2, -m_use));
+        psum += pv;
+        pt[e] = (_Float16)pv;
+      }
+      const int rt = 32 * (t >> 1) + 16 * (t & 1);
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const u32x2 v0 = fmha_tr_read(v + voff0[db & 3] + rt * RB + (db >> 2) * 256);
+        const u32x2 v1 = fmha_tr_read(v + voff1[db & 3] + rt * RB + (db >> 2) * 256);
+        const u32x4 vv = {v0[0], v0[1], v1[0], v1[1]};
+        acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(vv), pt, acc_o[db], 0, 0, 0);
+      }
+    }
+    psum += __shfl_xor(psum, 32);
+    l_run += psum;
+  };
+  auto sync_top = [&]() {
+    asm volatile("" ::: "memory");
+    fmha_wait_vm<0>();
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+
+  f32x16 sa[NJ], sb[NJ];
+  if (nkb > 0) {
+    copy_block(Kp, k_ss, ksrc, kbuf, 0);
+    copy_block(Vp, v_ss, vsrc, vbuf, 0);
+    if (nkb > 1) copy_block(Kp, k_ss, ksrc, kbuf, 1);
+    sync_top();
+    scores(sa, 0);
+  }
+  // iteration kb: K(kb+1), V(kb) resident; copy K(kb+2), V(kb+1); S(kb+1) || max(kb); exp + PV(kb).
+  // The scores of a block past the end read a stale K slot and are never used (unconditional so
+  // the MFMAs and the max share one scheduling region).
+  auto iter = [&](f32x16* cur, f32x16* nxt, int kb) {
+    sync_top();
+    if (kb + 2 < nkb) copy_block(Kp, k_ss, ksrc, kbuf, kb + 2);
+    if (kb + 1 < nkb) copy_block(Vp, v_ss, vsrc, vbuf, kb + 1);
+    scores(nxt, kb + 1);
+    const float mx = softmax_max(cur, kb);
+    if constexpr (SG) {
+#pragma unroll
+      for (int i = 0; i < NJ * DS; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0);  // LDS read
+        __builtin_amdgcn_sched_group_barrier(0x0002, 2, 0);  // VALU
+      }
+    }
+    move_ref(mx);
+    exp_pv(cur, kb);
+    if constexpr (SG) {
+#pragma unroll
+      for (int i = 0; i < 2 * NJ * DB; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x0100, 2, 0);  // LDS read
+        __builtin_amdgcn_sched_group_barrier(0x0002, 3, 0);  // VALU
+        __builtin_amdgcn_sched_group_barrier(0x0400, 1, 0);  // transcendental
+      }
+    }
+  };
+  int kb = 0;
+  for (; kb + 1 < nkb; kb += 2) {
+    iter(sa, sb, kb);
+    iter(sb, sa, kb + 1);
+  }
+  if (kb < nkb) iter(sa, sb, kb);
+
+  if (qi < Sq) {
+    const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+    _Float16* Op = O + b * o_sb + (long)qi * o_ss + (long)h * o_sh;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        f16x4 o;
+        o[0] = (_Float16)(acc_o[db][4 * g + 0] * inv);
+        o[1] = (_Float16)(acc_o[db][4 * g + 1] * inv);
+        o[2] = (_Float16)(acc_o[db][4 * g + 2] * inv);
+        o[3] = (_Float16)(acc_o[db][4 * g + 3] * inv);
+        *reinterpret_cast<f16x4*>(Op + db * 32 + 8 * g + 4 * hl) = o;
+      }
+    if (LSE && hl == 0)
+      LSE[((long)b * H + h) * Sq + qi] =
+          l_run > 0.f ? m_run * 0.6931471805599453f + __logf(l_run) : -__builtin_inff();
+  }
+}
+
 }  // namespace fmha
