@@ -184,6 +184,35 @@ def decode_lines(steps):
     return out
 
 
+def gptq_lines(steps):
+    """Load-time GPTQ repack (checkpoint [K/4,N] int32 -> [N,K] bytes) on the model's two
+    largest layers; algorithmic bytes = the checkpoint read once plus the repack written once."""
+    import torch
+    from cuda_tempiler_amd import capi
+
+    out = []
+    stream = torch.cuda.current_stream()
+    for (K, N) in ((5120, 34816), (17408, 5120)):
+        G = 128
+        qw = torch.randint(-(2**31), 2**31 - 1, (K // 4, N), dtype=torch.int32, device="cuda:0")
+        qz = torch.randint(-(2**31), 2**31 - 1, (K // G, N // 4), dtype=torch.int32, device="cuda:0")
+        sc = torch.empty((K // G, N), dtype=torch.float16, device="cuda:0").uniform_(0.001, 0.021)
+        wq = torch.empty((N, K), dtype=torch.uint8, device="cuda:0")
+        so = torch.empty((N, K // G), dtype=torch.float16, device="cuda:0")
+        zo = torch.empty((N, K // G), dtype=torch.uint8, device="cuda:0")
+        lib = capi.lib()
+        args = (capi._ptr(qw), capi._ptr(qz), capi._ptr(sc), K, N, G, capi._ptr(wq),
+                capi._ptr(so), capi._ptr(zo), capi._stream(stream))
+        fn = lambda i: capi._check(lib.tempo_gptq_repack_u8(*args), "tempo_gptq_repack_u8")
+        ms = time_launches(fn, steps, max(5, steps // 5), stream)
+        byts = 2 * (K * N + 3 * (K // G) * N)
+        gbps = byts / (ms * 1e-3) / 1e9
+        out.append({"op": "gptq_repack_u8", "K": K, "N": N, "us": round(ms * 1e3, 2),
+                    "GBps": round(gbps, 1), "hbm_frac": round(gbps / PEAK_HBM_GBPS, 4)})
+        del qw, qz, sc, wq, so, zo
+    return out
+
+
 def fmha_line(steps):
     import torch
     from cuda_tempiler_amd import capi
@@ -274,6 +303,8 @@ def main():
         line["decode"] = decode_lines(max(50, args.steps))
         torch.cuda.empty_cache()
         line["fmha"] = fmha_line(max(10, args.steps // 10))
+        torch.cuda.empty_cache()
+        line["gptq_repack"] = gptq_lines(max(20, args.steps // 4))
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(Ah, Bh)
     else:

@@ -40,6 +40,7 @@ UNITS = [
     os.path.join(SHIPPED, "gemm_fp16", "gfx950", "launch.hip"),
     os.path.join(SHIPPED, "gemm_w8a16", "gfx950", "launch.hip"),
     os.path.join(HERE, "csrc", "fmha.hip"),
+    os.path.join(HERE, "csrc", "gptq.hip"),
     os.path.join(HERE, "csrc", "capi.hip"),
 ]
 

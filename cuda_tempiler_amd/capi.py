@@ -69,6 +69,7 @@ EXPORTS = {
     "tempo_naive_gemm_fp16_launch": ([_p, _p, _p, _i, _i, _i, _p], _i),
     "tempo_probe_mfma_layout": ([_i, _p, _p], _i),
     "tempo_route": ([_i, _i, _i, _i, ct.c_char_p, _i], _i),
+    "tempo_gptq_repack_u8": ([_p, _p, _p, _i, _i, _i, _p, _p, _p, _p], _i),
 }
 
 
@@ -201,6 +202,23 @@ def naive_gemm_fp16(A, B, C=None, stream=None):
     _check(lib().tempo_naive_gemm_fp16_launch(_ptr(A), _ptr(B), _ptr(C), M, N, K,
                                                _stream(stream)), "tempo_naive_gemm_fp16_launch")
     return C
+
+
+def gptq_repack(qweight, qzeros, scales, group: int = 128, stream=None):
+    """GPTQ int8 checkpoint tensors (qweight int32 [K/4,N], qzeros int32 [K/G,N/4], scales fp16
+    [K/G,N]) -> (wq uint8 [N,K], scale fp16 [N,K/G], zero uint8 [N,K/G]) for gemm_w8a16 fmt 2."""
+    import torch
+
+    K = qweight.shape[0] * 4
+    N = qweight.shape[1]
+    dev = qweight.device
+    wq = torch.empty((N, K), dtype=torch.uint8, device=dev)
+    sc = torch.empty((N, K // group), dtype=torch.float16, device=dev)
+    zr = torch.empty((N, K // group), dtype=torch.uint8, device=dev)
+    _check(lib().tempo_gptq_repack_u8(_ptr(qweight), _ptr(qzeros), _ptr(scales), K, N, group,
+                                      _ptr(wq), _ptr(sc), _ptr(zr), _stream(stream)),
+           "tempo_gptq_repack_u8")
+    return wq, sc, zr
 
 
 def probe_mfma_layout(ms: int, device="cuda"):

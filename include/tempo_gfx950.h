@@ -86,6 +86,19 @@ int tempo_dequant_tile(const TempoW8A16Params* p, int n0, int k0, int rows, int 
                        tempo_stream_t stream);
 
 /* ------------------------------------------------------------------------------------------
+ * GPTQ int8 repack (one-time, at load): checkpoint layout -> the fmt 2 layout of gemm_w8a16.
+ *   in:  qweight int32 [K/4][N] (byte k%4 of qweight[k/4][n] = q[k][n]), qzeros int32
+ *        [K/group][N/4] (byte n%4 = z[g][n]), scales fp16 [K/group][N]
+ *   out: wq uint8 [N][K], scale_out fp16 [N][K/group], zero_out uint8 [N][K/group]
+ * A byte permutation (bit-exact).  Requires K % 128 == 0, N % 64 == 0, group == 128, 16-byte
+ * aligned qweight and wq; otherwise TEMPO_FALLBACK.  The checkpoint format is the reference's
+ * make_gptq_int8 (bench/gemm_baseline.py:214-232, dequantised by the formula of :229).
+ * ------------------------------------------------------------------------------------------ */
+int tempo_gptq_repack_u8(const void* qweight, const void* qzeros, const void* scales, int K, int N,
+                         int group, void* wq, void* scale_out, void* zero_out,
+                         tempo_stream_t stream);
+
+/* ------------------------------------------------------------------------------------------
  * fmha_fwd: O = softmax(scale * Q K^T + causal mask) V, fp32 softmax, fp16 O, fp32 LSE
  * (natural log).  GQA: query head h reads KV head h / (H / Hkv).  Causal mask is bottom-right:
  * row i sees keys j <= i + (Sk - Sq).  Strides in elements; Q/O addressed as

@@ -200,3 +200,26 @@ def ship_probe_inputs(M: int, N: int, K: int):
     A = (((ia % 7) - 3).astype(np.float32) * np.float32(0.125)).astype(np.float16).reshape(M, K)
     B = (((ib % 5) - 2).astype(np.float32) * np.float32(0.125)).astype(np.float16).reshape(N, K)
     return A, B
+
+
+def gptq_unpack(qweight, qzeros, scales, G: int = 128):
+    """GPTQ int8 checkpoint (bench/gemm_baseline.py:214-232): qweight int32 [K/4,N], qzeros int32
+    [K/G,N/4], scales fp16 [K/G,N] -> q uint8 [K,N], z uint8 [K/G,N], s fp16 [K/G,N]."""
+    qw = np.ascontiguousarray(qweight).view(np.uint32)
+    qz = np.ascontiguousarray(qzeros).view(np.uint32)
+    K4, N = qw.shape
+    q = np.stack([(qw >> (8 * b)) & 0xFF for b in range(4)], axis=1).reshape(K4 * 4, N)
+    z = np.stack([(qz >> (8 * b)) & 0xFF for b in range(4)], axis=2).reshape(qz.shape[0], N)
+    return q.astype(np.uint8), z.astype(np.uint8), np.ascontiguousarray(scales).view(np.float16)
+
+
+def gptq_to_nk(qweight, qzeros, scales, G: int = 128):
+    """The fmt 2 operands of gemm_w8a16 for a GPTQ checkpoint: (wq [N,K], s [N,K/G], z [N,K/G])."""
+    q, z, s = gptq_unpack(qweight, qzeros, scales, G)
+    return (np.ascontiguousarray(q.T), np.ascontiguousarray(s.T), np.ascontiguousarray(z.T))
+
+
+def gptq_dense(qweight, qzeros, scales, G: int = 128):
+    """W [K,N] fp16 = fp16_rn((q - z[k/G]) * s[k/G]) -- gemm_baseline.py:229."""
+    wq, s, z = gptq_to_nk(qweight, qzeros, scales, G)
+    return np.ascontiguousarray(dequant_asym(wq, s, z, G).T)

@@ -141,3 +141,61 @@ def test_w8a16_exact_regime_bit_exact(gpu, fmt, M, N):
     C = _run(A, q, s, z, fmt, gpu)
     ref = O.gemm_w8a16(A, q, s, z, 128, fmt)
     assert np.array_equal(C.view(np.uint16), ref.view(np.uint16))
+
+
+def _gptq_checkpoint(K, N, G, seed):
+    """GPTQ int8 tensors over the full int32 range (bench/gemm_baseline.py:219-223)."""
+    g = np.random.Generator(np.random.PCG64(seed))
+    qw = g.integers(-(2**31), 2**31 - 1, (K // 4, N), dtype=np.int64).astype(np.int32)
+    qz = g.integers(-(2**31), 2**31 - 1, (K // G, N // 4), dtype=np.int64).astype(np.int32)
+    sc = O.f2h(g.uniform(0.001, 0.021, (K // G, N)).astype(np.float32))
+    return qw, qz, sc
+
+
+@pytest.mark.parametrize("KN", [(128, 64), (256, 192), (5120, 6144), (5120, 34816), (17408, 5120)],
+                         ids=lambda kn: "k%d_n%d" % kn)
+def test_gptq_repack_bit_exact(gpu, KN):
+    """The device repack of a GPTQ checkpoint equals the oracle's byte for byte (weights, scales
+    and zero-points), at the model's full layer shapes included."""
+    import torch
+    from cuda_tempiler_amd import capi
+
+    K, N = KN
+    say("gptq repack", KN)
+    qw, qz, sc = _gptq_checkpoint(K, N, 128, K + N)
+    wq, s, z = capi.gptq_repack(dev(qw, gpu), dev(qz, gpu), dev(sc, gpu))
+    torch.cuda.synchronize()
+    rw, rs, rz = O.gptq_to_nk(qw, qz, sc)
+    assert np.array_equal(host(wq), rw)
+    assert np.array_equal(host(s).view(np.uint16), rs.view(np.uint16))
+    assert np.array_equal(host(z), rz)
+
+
+@pytest.mark.parametrize("M", [1, 16, 200])
+def test_gptq_checkpoint_to_gemm(gpu, M):
+    """GPTQ checkpoint -> device repack -> fmt 2 GEMM: matches the oracle built on the reference's
+    dense formula (gemm_baseline.py:229) within relL2 3e-3, and bit-for-bit the same GEMM fed
+    with the oracle's repack."""
+    import torch
+    from cuda_tempiler_amd import capi
+
+    K, N = 5120, 6144
+    say("gptq gemm M=%d" % M, _route(2, M, N, K))
+    qw, qz, sc = _gptq_checkpoint(K, N, 128, 77)
+    wq, s, z = capi.gptq_repack(dev(qw, gpu), dev(qz, gpu), dev(sc, gpu))
+    g = np.random.Generator(np.random.PCG64(M))
+    A = O.f2h(g.standard_normal((M, K), dtype=np.float32))
+    dA = dev(A, gpu)
+    C = capi.gemm_w8a16(dA, wq, s, z, fmt=2, group=128, C=poisoned((M, N), gpu))
+    rw, rs, rz = O.gptq_to_nk(qw, qz, sc)
+    C2 = capi.gemm_w8a16(dA, dev(rw, gpu), dev(rs, gpu), dev(rz, gpu), fmt=2, group=128,
+                         C=poisoned((M, N), gpu))
+    torch.cuda.synchronize()
+    got = host(C)
+    assert O.count_poison(got) == 0
+    assert np.array_equal(got.view(np.uint16), host(C2).view(np.uint16))
+    W = O.gptq_dense(qw, qz, sc)
+    ref = O.gemm_f16(A, np.ascontiguousarray(W.T))
+    r = O.rel_l2(got, ref)
+    say("  relL2 %.3e" % r)
+    assert r <= 3e-3

@@ -192,3 +192,61 @@ def test_poison_and_spot():
     Cm2[0, 0] = np.float16(float(Cm2[0, 0]) + 1.0)  # one wrong cell is seen by the spot check
     worst2, bad2 = O.spot_fp64(A, B, Cm2, cells=64)
     assert bad2 >= 1
+
+
+def _gptq_checkpoint(K, N, G, seed):
+    """Random GPTQ int8 tensors over the full int32 range, as bench/gemm_baseline.py:219-223."""
+    g = np.random.Generator(np.random.PCG64(seed))
+    qw = g.integers(-(2**31), 2**31 - 1, (K // 4, N), dtype=np.int64).astype(np.int32)
+    qz = g.integers(-(2**31), 2**31 - 1, (K // G, N // 4), dtype=np.int64).astype(np.int32)
+    sc = O.f2h(g.uniform(0.001, 0.021, (K // G, N)).astype(np.float32))
+    return qw, qz, sc
+
+
+def test_gptq_unpack_against_python_brute_force():
+    """Byte k%4 of qweight[k/4][n] and byte n%4 of qzeros[g][n/4], read with Python's arbitrary
+    precision ints (arithmetic shift of the signed word, then & 0xFF, as the reference's torch
+    expression does on int32)."""
+    K, N, G = 256, 12, 128
+    qw, qz, sc = _gptq_checkpoint(K, N, G, 3)
+    q, z, s = O.gptq_unpack(qw, qz, sc, G)
+    for k in range(K):
+        for n in range(N):
+            assert q[k, n] == (int(qw[k // 4, n]) >> (8 * (k % 4))) & 0xFF
+    for gi in range(K // G):
+        for n in range(N):
+            assert z[gi, n] == (int(qz[gi, n // 4]) >> (8 * (n % 4))) & 0xFF
+    assert np.array_equal(s.view(np.uint16), sc.view(np.uint16))
+
+
+def test_gptq_pack_unpack_round_trip():
+    """An independent packer (little-endian bytes via numpy views) inverts the unpack."""
+    K, N, G = 512, 64, 128
+    g = np.random.Generator(np.random.PCG64(8))
+    q = g.integers(0, 256, (K, N), dtype=np.int16).astype(np.uint8)
+    z = g.integers(0, 256, (K // G, N), dtype=np.int16).astype(np.uint8)
+    qw = np.ascontiguousarray(q.reshape(K // 4, 4, N).transpose(0, 2, 1)).view("<i4")[..., 0]
+    qz = np.ascontiguousarray(z.reshape(K // G, N // 4, 4)).view("<i4")[..., 0]
+    sc = O.f2h(np.full((K // G, N), 0.01, np.float32))
+    q2, z2, _ = O.gptq_unpack(qw, qz, sc, G)
+    assert np.array_equal(q2, q) and np.array_equal(z2, z)
+    wq, s_nk, z_nk = O.gptq_to_nk(qw, qz, sc, G)
+    assert wq.shape == (N, K) and np.array_equal(wq, q.T)
+    assert s_nk.shape == (N, K // G) and np.array_equal(z_nk, z.T)
+
+
+def test_gptq_dense_against_reference_formula():
+    """W[k][n] = half((q - z[k/G]) * s[k/G]) (gemm_baseline.py:229); (q - z) * s has at most
+    9 + 11 significant bits, so the fp64 product is exact and one rounding to fp16 is the whole
+    answer."""
+    K, N, G = 384, 16, 128
+    qw, qz, sc = _gptq_checkpoint(K, N, G, 11)
+    W = O.gptq_dense(qw, qz, sc, G)
+    assert W.shape == (K, N)
+    ref = np.empty((K, N), np.float16)
+    for k in range(K):
+        for n in range(N):
+            q = (int(qw[k // 4, n]) >> (8 * (k % 4))) & 0xFF
+            z = (int(qz[k // G, n // 4]) >> (8 * (n % 4))) & 0xFF
+            ref[k, n] = np.float16(float(q - z) * float(sc[k // G, n]))
+    assert np.array_equal(W.view(np.uint16), ref.view(np.uint16))

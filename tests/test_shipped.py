@@ -117,3 +117,17 @@ def test_rows_fall_through_when_the_first_row_does_not_fit():
     assert capi.route(1, 1, 5120, 5120) == "s1a_r1u8"
     assert capi.route(1, 1, 5120, 5376) == "s1a_r1u4"   # K % 512 != 0, K % 256 == 0
     assert capi.route(0, 4096, 15360, 3840) == "d256x256k64w16m16"
+
+
+def test_gptq_repack_refuses_before_any_launch():
+    """Shapes and groups the repack does not cover are refused on the host (no GPU touched)."""
+    from cuda_tempiler_amd import capi
+
+    L = capi.lib()
+    p = capi._p(4096)  # never dereferenced: every case below is refused before a launch
+    s = capi._p(0)
+    assert L.tempo_gptq_repack_u8(p, p, p, 5120, 6144, 64, p, p, p, s) == capi.TEMPO_FALLBACK
+    assert L.tempo_gptq_repack_u8(p, p, p, 5120 + 32, 6144, 128, p, p, p, s) == capi.TEMPO_FALLBACK
+    assert L.tempo_gptq_repack_u8(p, p, p, 5120, 6144 + 4, 128, p, p, p, s) == capi.TEMPO_FALLBACK
+    assert L.tempo_gptq_repack_u8(p, p, p, 0, 6144, 128, p, p, p, s) == capi.TEMPO_FALLBACK
+    assert L.tempo_gptq_repack_u8(None, p, p, 5120, 6144, 128, p, p, p, s) != 0
