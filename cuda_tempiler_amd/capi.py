@@ -69,6 +69,7 @@ EXPORTS = {
     "tempo_naive_gemm_fp16_launch": ([_p, _p, _p, _i, _i, _i, _p], _i),
     "tempo_probe_mfma_layout": ([_i, _p, _p], _i),
     "tempo_route": ([_i, _i, _i, _i, ct.c_char_p, _i], _i),
+    "tempo_naive_gemm_w8a16_launch": ([ct.POINTER(TempoW8A16Params), _p], _i),
     "tempo_gptq_repack_u8": ([_p, _p, _p, _i, _i, _i, _p, _p, _p, _p], _i),
 }
 
@@ -201,6 +202,20 @@ def naive_gemm_fp16(A, B, C=None, stream=None):
         C = torch.empty((M, N), dtype=torch.float16, device=A.device)
     _check(lib().tempo_naive_gemm_fp16_launch(_ptr(A), _ptr(B), _ptr(C), M, N, K,
                                                _stream(stream)), "tempo_naive_gemm_fp16_launch")
+    return C
+
+
+def naive_gemm_w8a16(A, Wq, scale, zero=None, fmt: int = W8_SYM_I8, group: int = 128, C=None,
+                     stream=None):
+    """The naive W8A16 input kernel (one thread per output): the "vs input" bar."""
+    import torch
+
+    M = A.shape[0]
+    N = Wq.shape[0]
+    if C is None:
+        C = torch.empty((M, N), dtype=torch.float16, device=A.device)
+    p = w8a16_params(A, Wq, scale, zero, C, fmt, group)
+    _check(lib().tempo_naive_gemm_w8a16_launch(p, _stream(stream)), "tempo_naive_gemm_w8a16_launch")
     return C
 
 

@@ -11,6 +11,7 @@
 #include "gemm_fp16/gfx950/launch.h"
 #include "gemm_w8a16/gfx950/launch.h"
 #include "naive/gemm_fp16.hip"
+#include "naive/gemm_w8a16.hip"
 #include "fmha_api.h"
 
 namespace {
@@ -130,6 +131,21 @@ int tempo_naive_gemm_fp16_launch(const void* A, const void* B, void* C, int M, i
   return (int)naive_gemm_fp16_launch(static_cast<const _Float16*>(A),
                                      static_cast<const _Float16*>(B), static_cast<_Float16*>(C),
                                      M, N, K, static_cast<hipStream_t>(stream));
+}
+
+int tempo_naive_gemm_w8a16_launch(const TempoW8A16Params* p, tempo_stream_t stream) {
+  if (!p || !p->A || !p->Wq || !p->scale || !p->C || p->M <= 0 || p->N <= 0 || p->K <= 0)
+    return (int)hipErrorInvalidValue;
+  if (p->lda != p->K || p->ldw != p->K || p->ldc != p->N) return (int)hipErrorInvalidValue;
+  if (p->fmt == TEMPO_W8_ASYM_U8) {
+    if (!p->zero || p->group <= 0 || p->K % p->group != 0) return (int)hipErrorInvalidValue;
+  } else if (p->fmt != TEMPO_W8_SYM_I8) {
+    return (int)hipErrorInvalidValue;
+  }
+  return (int)naive_gemm_w8a16_launch(
+      static_cast<const _Float16*>(p->A), p->Wq, static_cast<const _Float16*>(p->scale),
+      static_cast<const uint8_t*>(p->zero), static_cast<_Float16*>(p->C), p->M, p->N, p->K,
+      p->fmt == TEMPO_W8_ASYM_U8 ? p->group : 0, p->fmt, static_cast<hipStream_t>(stream));
 }
 
 int tempo_probe_mfma_layout(int ms, float* out, tempo_stream_t stream) {

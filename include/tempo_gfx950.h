@@ -132,6 +132,12 @@ int tempo_fmha_fwd_launch(const TempoFmhaParams* p, tempo_stream_t stream);
 int tempo_naive_gemm_fp16_launch(const void* A, const void* B, void* C, int M, int N, int K,
                                  tempo_stream_t stream);
 
+/* The naive W8A16 input kernel (kernels/naive/gemm_w8a16.hip): dequantise each weight once to
+ * fp16_rn((q - z) * s), then the naive fp16 accumulation above.  Dense operands only (lda = ldw
+ * = K, ldc = N).  The reference ships no naive W8A16 input; its dense formula is
+ * bench/gemm_baseline.py:229. */
+int tempo_naive_gemm_w8a16_launch(const TempoW8A16Params* p, tempo_stream_t stream);
+
 /* ------------------------------------------------------------------------------------------
  * Plugin support (no reference counterpart in the C ABI; the sm70 plugin does these checks
  * from Python, tempo/plugins/sm70/tensor.py:72-86).

@@ -33,7 +33,8 @@ def prune(plugin, op, hyperforms, keep_silent: bool = True, bound_slack: float =
         try:
             regs, max_live, smem = plugin.skeletons.resources_of(op, h)
             lau = plugin.skeletons.launch_of(op, h)
-            v = plugin.resources.verdict(regs, max_live, smem, lau.threads, lau.min_ctas_per_sm)
+            v = plugin.resources.verdict(regs, max_live, smem, lau.threads, lau.min_ctas_per_sm,
+                                         bound_threads=getattr(lau, "bound_threads", 0))
         except Exception as e:
             out.append(Candidate(h, None, None, False, "no resource verdict: %s" % e))
             continue

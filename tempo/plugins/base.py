@@ -301,7 +301,7 @@ class Resources(Protocol):
     # regs: the optimistic edge of the register estimate (residency, time bound);
     # max_live: the pessimistic edge (the "will it spill" question).
     def verdict(self, regs: int, max_live: int, smem_bytes: int, threads: int,
-                min_ctas_per_sm: int = 1) -> ResourceVerdict: ...
+                min_ctas_per_sm: int = 1, bound_threads: int = 0) -> ResourceVerdict: ...
     def wave_quantum(self, occ: Occupancy) -> int: ...
     def declared_bounds_required(self) -> bool: ...
 
@@ -378,6 +378,9 @@ class Launch:
     # residency the skeleton declares to the compiler (__launch_bounds__ minimum); it sets the
     # register budget, so it crosses the boundary instead of being inferred by the core
     min_ctas_per_sm: int = 1
+    # the thread count named in __launch_bounds__ when the launched block can be smaller (a
+    # wave count chosen at launch time); 0 = `threads`.  It sets the budget the same way.
+    bound_threads: int = 0
 
 
 @dataclass(frozen=True)

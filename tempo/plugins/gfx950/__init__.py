@@ -88,7 +88,7 @@ class Gfx950Plugin:
         R = self.resources
         codes = {
             R.verdict(256, 300, 200 * 1024, 256).code,       # LDS beyond 160 KiB
-            R.verdict(600, 600, 64 * 1024, 256).code,        # no workgroup fits at all
+            R.verdict(128, 128, 64 * 1024, 40 * 64).code,    # more waves than a CU's slots
             R.verdict(400, 600, 64 * 1024, 256).code,        # max_live beyond 512
             R.verdict(128, 200, 64 * 1024, 512, 2).code,     # declared residency leaves 128
             R.verdict(128, 128, 64 * 1024, 256).code,

@@ -115,19 +115,27 @@ class Gfx950Skeletons:
                 per = (p["BM"] + p["BN"]) * p["BK"] // 8 // (nw * 64)
                 copies = per * 4 + per * 2  # staged data + addresses
             regs = acc + frags + copies + 16
-            return regs, int(regs * 1.2), space.lds_bytes(kind, p)
+            # pessimistic edge: the epilogue reads every accumulator out of the AGPRs before the
+            # fp16 conversion, so when the budget allows it the compiler holds acc twice
+            return regs, max(int(regs * 1.2), 2 * acc + 16), space.lds_bytes(kind, p)
         wb = 2 if p["BFMT"] == 0 else 1
         S, _ = self._split(op, p)
         if kind == "shared":
-            regs = (2 * p["R"] * p["MB"] * 4 + 2 * p["U"] * p["R"] * wb * 4 + 8 * p["MB"]
-                    + 2 * (p["R"] + p["MB"]) + 16)
+            # weights double-buffered (U steps x R slabs x 4*wb VGPRs), the activation fragments
+            # of U steps (8 per step per MB), accumulators (8 per R x MB), the fp16 expansion of
+            # 8-bit weights (4 per step per slab) plus scale/zero for fmt 2, addresses
+            U, R, MB, bf = p["U"], p["R"], p["MB"], p["BFMT"]
+            regs = (2 * U * R * wb * 4 + 8 * U * MB + 8 * R * MB + (4 * U * R if bf else 0)
+                    + (3 * U * R if bf == 2 else 0) + 14)
             lds = space.shared_split(int(op.shapes["N"]), int(op.shapes["K"]), p["MB"], p["R"],
                                      p["U"], p["SN"], p["TPB"])[2]
             return regs, int(regs * 1.25), lds
         if kind == "ring":
             regs = p["R"] * p["MB"] * 4 + (p["R"] * wb + 2 * p["MB"]) * 4 + 2 * (p["R"] + p["MB"]) + 16
         else:
-            act_regs = 0 if p.get("ALDS", 0) else 2 * p["MB"]
+            # activations: register-staged per step (2*MB per step), or read from the LDS copy
+            # just before each MFMA (still MB per step in flight)
+            act_regs = p["MB"] if p.get("ALDS", 0) else 2 * p["MB"]
             regs = (2 * p["R"] * p["MB"] * 4 + 2 * p["U"] * (p["R"] * wb + act_regs) * 4
                     + 2 * (p["R"] + p["MB"]) + 16)
         lds = space.lds_bytes(kind, dict(p, S=S))
@@ -139,21 +147,24 @@ class Gfx950Skeletons:
         p = _p(h)
         M, N = int(op.shapes["M"]), int(op.shapes["N"])
         kind = p["kind"]
+        minb, bound = 1, 0
         if kind in ("dma", "reg"):
             grid = -(-M // p["BM"]) * (N // p["BN"])
             threads = p["WM"] * p["WN"] * 64
-            S = 1
+            minb = p.get("MINB", 1) if kind == "dma" else 1
         elif kind == "shared":
             S, _ = self._split(op, p)
             grid = N // (16 * p["R"] * p["SN"])
             threads = 64 * p["SN"] * S
+            bound = p["TPB"]  # __launch_bounds__(TPB)
         else:
             S, _ = self._split(op, p)
             grid = N // (16 * p["R"])
             threads = 64 * S
+            bound = 512  # k_stream / k_stream_dma: __launch_bounds__(512)
         _, _, lds = self.resources_of(op, h)
         return Launch(grid_ctas=grid, threads=threads, smem_bytes=lds, entry=self.entry_probe(h),
-                      min_ctas_per_sm=1)
+                      min_ctas_per_sm=minb, bound_threads=bound)
 
     def estimate_atoms(self, op: OpSpec, h: Hyperform) -> list:
         """Per-wave load of the whole operation on the channels MFMA (flop), LDS and VMEM (bytes),
@@ -164,7 +175,8 @@ class Gfx950Skeletons:
         M, N, K = int(op.shapes["M"]), int(op.shapes["N"]), int(op.shapes["K"])
         regs, _, lds = self.resources_of(op, h)
         lau = self.launch_of(op, h)
-        occ = _RES.occupancy(min(regs, 512), lds, lau.threads)
+        occ = _RES.occupancy(min(regs, _RES.declared_budget(lau.threads, lau.min_ctas_per_sm,
+                                                            lau.bound_threads)), lds, lau.threads)
         per_cu = max(1, occ.ctas_per_sm)
         rounds = -(-lau.grid_ctas // (int(_M.rate("GEOM.SMS").value) * per_cu))
         atoms = []

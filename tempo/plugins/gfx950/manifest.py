@@ -18,8 +18,10 @@ import hashlib
 import importlib.util
 import json
 import os
+import random
 import sys
 import tempfile
+from concurrent.futures import ProcessPoolExecutor
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.abspath(os.path.join(HERE, "..", "..", ".."))
@@ -52,6 +54,102 @@ def md5_of(op):
     return h.hexdigest()
 
 
+def hyper_params(kind, p, fmt):
+    """A ladder row of select.py (kind, template params) -> the plugin's hyperform params: the
+    same kernel, named the way space.variants() names it."""
+    pk = {"stream": "stream", "mfma": "reg", "dma": "dma", "shared": "shared"}[kind]
+    params = {k: v for k, v in p.items() if k != "fmts"}
+    params["kind"] = pk
+    if pk == "shared":
+        params.setdefault("TPB", 1024)
+    if pk != "dma":
+        params["BFMT"] = fmt
+    if pk == "stream":
+        params["ALDS"] = params.pop("A", 0)
+    if pk == "dma":
+        params.setdefault("XT", 0)
+        params.setdefault("MINB", 1)
+        params.setdefault("MS", 32)
+    return params
+
+
+# The register gate's fixture (tests/test_prune_acceptance.py): bodies of the plugin's own
+# skeletons, compiled here, whose compiler numbers the pruner's pre-build estimate is held to.  A
+# seeded sample of every kind over the op's canonical shapes, plus bodies heavy enough to spill,
+# so that "a spilled body is never called FITS" is tested on real spills.
+GATE_SHAPES = {0: ((4096, 15360, 3840), (16, 15360, 3840), (1, 3840, 15360)),
+               1: ((16, 34816, 5120), (1, 5120, 17408)),
+               2: ((16, 34816, 5120), (1, 5120, 17408))}
+GATE_HEAVY = (dict(kind="stream", MB=1, R=4, U=8, ALDS=0), dict(kind="stream", MB=2, R=4, U=4, ALDS=0),
+              dict(kind="stream", MB=1, R=4, U=4, ALDS=0),
+              dict(kind="shared", MB=2, R=2, U=4, SN=2, TPB=1024),
+              dict(kind="shared", MB=1, R=2, U=4, SN=2, TPB=1024))
+GATE_PER_KIND = 6
+
+
+def _spec(fmt, shape):
+    from tempo.plugins.base import OpSpec
+
+    M, N, K = shape
+    return OpSpec(kind="gemm", dtype_a="fp16", dtype_b={0: "fp16", 1: "int8", 2: "uint8"}[fmt],
+                  dtype_c="fp16", dtype_acc="fp32", layout_a="k", layout_b="k", layout_c="n",
+                  shapes={"M": M, "N": N, "K": K})
+
+
+def gate_bodies(op):
+    """[(fmt, shape, params)]: deterministic (seeded) per op."""
+    sys.path.insert(0, ROOT)
+    from tempo.plugins.gfx950 import load
+
+    plug = load()
+    out, seen = [], set()
+    for fmt in OPS[op]["fmts"]:
+        rng = random.Random(950 + fmt)
+        for shape in GATE_SHAPES[fmt]:
+            by = {}
+            for h in plug.skeletons.variants(_spec(fmt, shape)):
+                by.setdefault(h.params["kind"], []).append(dict(h.params))
+            for kind in sorted(by):
+                pool = sorted(by[kind], key=lambda p: json.dumps(sorted(p.items())))
+                for p in rng.sample(pool, min(len(pool), GATE_PER_KIND)):
+                    k = json.dumps(sorted(p.items()))
+                    if k not in seen:
+                        seen.add(k)
+                        out.append((fmt, shape, p))
+        for hv in GATE_HEAVY:
+            p = dict(hv, BFMT=fmt)
+            k = json.dumps(sorted(p.items()))
+            if k not in seen:
+                seen.add(k)
+                out.append((fmt, GATE_SHAPES[fmt][0], p))
+    return out
+
+
+def _compile_body(job):
+    fmt, shape, params = job
+    sys.path.insert(0, ROOT)
+    from tempo.plugins.base import Hyperform
+    from tempo.plugins.gfx950 import load
+
+    plug = load()
+    spec = _spec(fmt, shape)
+    r = plug.skeletons.render(spec, Hyperform(plugin="gfx950", params=params, key="gate"))
+    with tempfile.TemporaryDirectory() as td:
+        src = os.path.join(td, r.filename)
+        with open(src, "w") as f:
+            f.write(r.source)
+        b = plug.toolchain.compile(src, os.path.join(td, "k.o"), mode="device")
+    if not b.ok:
+        raise RuntimeError("gate body %s does not compile:\n%s" % (params, b.log[-2000:]))
+    return dict(fmt=fmt, shape=list(shape), params=params, regs=b.regs, vgpr_spill=b.spill_st,
+                scratch_bytes_per_lane=b.stack_frame)
+
+
+def gate_numbers(op, jobs=8):
+    with ProcessPoolExecutor(jobs) as ex:
+        return list(ex.map(_compile_body, gate_bodies(op)))
+
+
 def build_numbers(op):
     """Compile each ladder row's kernel alone (rendered by the plugin) and read our numbers."""
     sys.path.insert(0, ROOT)
@@ -71,19 +169,7 @@ def build_numbers(op):
         for m_max, n_min, tag, kind, p in sel.LADDER:
             if fmt not in p.get("fmts", (fmt,)):
                 continue
-            pk = {"stream": "stream", "mfma": "reg", "dma": "dma", "shared": "shared"}[kind]
-            params = {k: v for k, v in p.items() if k != "fmts"}
-            params["kind"] = pk
-            if pk == "shared":
-                params.setdefault("TPB", 1024)
-            if pk != "dma":
-                params["BFMT"] = fmt
-            if pk == "stream":
-                params["ALDS"] = params.pop("A", 0)
-            if pk == "dma":
-                params.setdefault("XT", 0)
-                params.setdefault("MINB", 1)
-                params.setdefault("MS", 32)
+            params = hyper_params(kind, p, fmt)
             h = Hyperform(plugin="gfx950", params=params, key="%s_f%d" % (tag, fmt))
             r = plug.skeletons.render(spec, h)
             with tempfile.TemporaryDirectory() as td:
@@ -127,11 +213,14 @@ def make(op, rows_files=()):
                          "the shape runs; none -> fallback",
         "dispatch": [],
         "build": build_numbers(op),
+        "gate": gate_numbers(op),
         "source_md5": md5_of(op),
         "source_md5_of": list(SIGNED),
         "rows": old.get("rows", []),
         "card": old.get("card", None),
     }
+    if "rows_source_md5" in old:
+        man["rows_source_md5"] = old["rows_source_md5"]
     for m_max, n_min, tag, kind, p in sel.LADDER:
         if kind == "stream":
             fit = "N %% %d == 0 and K %% %d == 0" % (sel.STREAM_N_ROWS * p["R"],

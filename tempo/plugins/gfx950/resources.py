@@ -52,7 +52,9 @@ class Gfx950Resources:
         return max(gran, int(math.ceil(regs / gran)) * gran)
 
     def occupancy(self, regs: int, smem_bytes: int, threads: int) -> Occupancy:
-        """Resident waves per CU: registers per SIMD, wave slots, LDS per workgroup."""
+        """Resident waves per CU: registers per SIMD, wave slots, LDS per workgroup.  `regs` is
+        what one wave holds; callers that start from an estimate clamp it to the declared budget
+        first (the compiler never allocates beyond it: it spills instead)."""
         tpw = _i("GEOM.THREADS_PER_WARP")
         simds = _i("GEOM.SCHEDULERS_PER_SM")
         isa = _i("GEOM.REG_ISA_LIMIT")
@@ -71,20 +73,28 @@ class Gfx950Resources:
         return Occupancy(warps_per_sm=int(ctas * waves_wg), ctas_per_sm=int(ctas),
                          regs_per_thread=int(regs), limiter=limiter)
 
+    def declared_budget(self, threads: int, min_ctas_per_sm: int = 1, bound_threads: int = 0) -> int:
+        """The register budget __launch_bounds__(max(threads, bound_threads), min_ctas_per_sm)
+        gives the compiler."""
+        tpw = _i("GEOM.THREADS_PER_WARP")
+        waves = max(1, math.ceil(max(threads, bound_threads) / tpw)) * max(1, int(min_ctas_per_sm))
+        return self.reg_budget(waves)
+
     def verdict(self, regs: int, max_live: int, smem_bytes: int, threads: int,
-                min_ctas_per_sm: int = 1) -> ResourceVerdict:
+                min_ctas_per_sm: int = 1, bound_threads: int = 0) -> ResourceVerdict:
         isa = _i("GEOM.REG_ISA_LIMIT")
         lds_max = _i("GEOM.SMEM_PER_CTA_MAX")
-        tpw = _i("GEOM.THREADS_PER_WARP")
-        occ = self.occupancy(regs, smem_bytes, threads)
+        budget = self.declared_budget(threads, min_ctas_per_sm, bound_threads)
+        # the compiler holds a wave to the declared budget (spilling the rest), so residency is
+        # computed from min(estimate, budget): an estimate above the budget is a spill question,
+        # never a "cannot launch" one
+        occ = self.occupancy(min(regs, budget), smem_bytes, threads)
         if smem_bytes > lds_max:
             return ResourceVerdict(False, "WALL_SMEM", occ,
                                    "LDS %d B > %d B per workgroup" % (smem_bytes, lds_max))
         if occ.ctas_per_sm <= 0:
             return ResourceVerdict(False, "NO_BUDGET", occ, "no workgroup is resident on a CU")
         need = self.spill_threshold(max_live)
-        declared_waves = max(1, math.ceil(threads / tpw)) * max(1, int(min_ctas_per_sm))
-        budget = self.reg_budget(declared_waves)
         if need > isa:
             return ResourceVerdict(False, "WALL_REG", occ,
                                    "max_live %d + overhead = %d > %d registers per lane (advisory: "
@@ -92,10 +102,8 @@ class Gfx950Resources:
         if need > budget:
             over = need - budget
             return ResourceVerdict(over <= self.free_spills(), "SPILL", occ,
-                                   "needs %d registers, declared budget %d at %d waves per "
-                                   "workgroup-set: %d values to scratch, cost x%.1f"
-                                   % (need, budget, declared_waves, over,
-                                      self.spill_cost(over).value))
+                                   "needs %d registers, declared budget %d: %d values to scratch, "
+                                   "cost x%.1f" % (need, budget, over, self.spill_cost(over).value))
         return ResourceVerdict(True, "FITS", occ,
                                "needs %d registers even at the pessimistic edge; budget %d; %d "
                                "workgroup(s) per CU, limited by %s"

@@ -87,7 +87,17 @@ def test_g5_selftest_green(plug):
 def test_resource_verdicts(plug):
     R = plug.resources
     assert R.verdict(256, 300, 200 * 1024, 256).code == "WALL_SMEM"
-    assert R.verdict(600, 600, 64 * 1024, 256).code == "NO_BUDGET"
+    assert R.verdict(128, 128, 64 * 1024, 40 * 64).code == "NO_BUDGET"  # > 32 wave slots
+    # an estimate above the declared budget is a spill question, never "cannot launch": the
+    # compiler holds the wave to the budget
+    v = R.verdict(600, 600, 64 * 1024, 1024)
+    assert v.code == "WALL_REG" and v.occ.ctas_per_sm == 1
+    v = R.verdict(152, 182, 128 * 1024, 1024)
+    assert v.code == "SPILL" and v.occ.ctas_per_sm == 1
+    # __launch_bounds__(512) on a kernel launched with 4 waves: the budget is the bound's
+    assert R.declared_budget(256) == 512 and R.declared_budget(256, 1, 512) == 256
+    assert R.verdict(100, 300, 0, 256, 1, 512).code == "SPILL"
+    assert R.verdict(100, 300, 0, 256).code == "FITS"
     assert R.verdict(400, 600, 64 * 1024, 256).code == "WALL_REG"
     assert R.verdict(128, 200, 64 * 1024, 512, 2).code == "SPILL"
     v = R.verdict(128, 128, 64 * 1024, 256)
