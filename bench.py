@@ -184,6 +184,67 @@ def decode_lines(steps):
     return out
 
 
+def gate_up_lines(steps):
+    """The fused gate/up epilogue on the production gate_up shape (2N = 34816, K = 5120; both
+    W8A16 formats and fp16 weights) against the unfused chain on the same stream: the plain
+    shipped GEMM into [M, 2N], then torch's silu and product."""
+    import torch
+    import torch.nn.functional as F
+    from cuda_tempiler_amd import capi
+
+    out = []
+    stream = torch.cuda.current_stream()
+    N, K, G = 17408, 5120, 128
+    for fmt in (1, 2, 0):
+        wb = 2 if fmt == 0 else 1
+        nb = 2 * N * K * wb + (4 * N if fmt == 1 else (6 * N * K // G if fmt == 2 else 0))
+        copies = max(2, -(-(512 << 20) // nb) + 1)
+        W, S, Z = [], [], []
+        for c in range(copies):
+            if fmt == 0:
+                W.append(torch.randn((2 * N, K), dtype=torch.float16, device="cuda:0") / K ** 0.5)
+                S.append(None)
+                Z.append(None)
+            elif fmt == 1:
+                W.append(torch.randint(-127, 128, (2 * N, K), dtype=torch.int8, device="cuda:0"))
+                S.append(torch.empty(2 * N, dtype=torch.float16, device="cuda:0").uniform_(0.5, 1.5) / 127)
+                Z.append(None)
+            else:
+                W.append(torch.randint(0, 256, (2 * N, K), dtype=torch.uint8, device="cuda:0"))
+                S.append(torch.empty((2 * N, K // G), dtype=torch.float16, device="cuda:0").uniform_(0.5, 1.5) / 255)
+                Z.append(torch.randint(100, 157, (2 * N, K // G), dtype=torch.uint8, device="cuda:0"))
+        for M in (1, 16, 32):
+            A = torch.randn((M, K), dtype=torch.float16, device="cuda:0") / K ** 0.5
+            C = torch.empty((M, N), dtype=torch.float16, device="cuda:0")
+            T = torch.empty((M, 2 * N), dtype=torch.float16, device="cuda:0")
+            if fmt == 0:
+                fused = lambda i: capi.gemm_fp16_gate_up(A, W[i % copies], C, stream=stream)
+                plain = lambda i: capi.gemm_fp16(A, W[i % copies], T, stream=stream)
+            else:
+                fused = lambda i: capi.gemm_w8a16_gate_up(A, W[i % copies], S[i % copies],
+                                                          Z[i % copies], fmt=fmt, group=G, C=C,
+                                                          stream=stream)
+                plain = lambda i: capi.gemm_w8a16(A, W[i % copies], S[i % copies], Z[i % copies],
+                                                  fmt=fmt, group=G, C=T, stream=stream)
+
+            def unfused(i):
+                plain(i)
+                g, u = T.chunk(2, dim=-1)
+                return F.silu(g) * u
+
+            ms_f = time_launches(fused, steps, max(10, steps // 5), stream)
+            ms_u = time_launches(unfused, steps, max(10, steps // 5), stream)
+            byts = nb + 2 * M * K + 2 * M * N
+            gbps = byts / (ms_f * 1e-3) / 1e9
+            out.append({"op": "gate_up", "fmt": ["fp16", "sym_i8", "asym_u8_g128"][fmt],
+                        "M": M, "N": N, "K": K, "us": round(ms_f * 1e3, 2),
+                        "unfused_us": round(ms_u * 1e3, 2), "speedup": round(ms_u / ms_f, 3),
+                        "GBps": round(gbps, 1), "hbm_frac": round(gbps / PEAK_HBM_GBPS, 4),
+                        "route": capi.route(3 + fmt, M, N, K)})
+        del W, S, Z
+    return out
+
+
 def gptq_lines(steps):
     """Load-time GPTQ repack (checkpoint [K/4,N] int32 -> [N,K] bytes) on the model's two
     largest layers; algorithmic bytes = the checkpoint read once plus the repack written once."""
@@ -305,6 +366,8 @@ def main():
         line["fmha"] = fmha_line(max(10, args.steps // 10))
         torch.cuda.empty_cache()
         line["gptq_repack"] = gptq_lines(max(20, args.steps // 4))
+        torch.cuda.empty_cache()
+        line["gate_up"] = gate_up_lines(max(50, args.steps // 2))
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(Ah, Bh)
     else:

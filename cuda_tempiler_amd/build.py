@@ -53,12 +53,13 @@ def regenerate() -> None:
     ship.write_all()
     for op in ("gemm_fp16", "gemm_w8a16"):
         d = os.path.join(SHIPPED, op, "gfx950")
-        text = subprocess.run([sys.executable, os.path.join(d, "gen_dispatch.py")],
-                              check=True, capture_output=True, text=True).stdout
-        path = os.path.join(d, "dispatch.inc")
-        if not os.path.exists(path) or open(path).read() != text:
-            with open(path, "w") as f:
-                f.write(text)
+        for name, args in (("dispatch.inc", []), ("dispatch_gate_up.inc", ["--gate-up"])):
+            text = subprocess.run([sys.executable, os.path.join(d, "gen_dispatch.py")] + args,
+                                  check=True, capture_output=True, text=True).stdout
+            path = os.path.join(d, name)
+            if not os.path.exists(path) or open(path).read() != text:
+                with open(path, "w") as f:
+                    f.write(text)
 
 
 def _compile(src: str) -> str:

@@ -69,6 +69,8 @@ EXPORTS = {
     "tempo_naive_gemm_fp16_launch": ([_p, _p, _p, _i, _i, _i, _p], _i),
     "tempo_probe_mfma_layout": ([_i, _p, _p], _i),
     "tempo_route": ([_i, _i, _i, _i, ct.c_char_p, _i], _i),
+    "tempo_gemm_fp16_gate_up_launch": ([ct.POINTER(TempoGemmParams), _p], _i),
+    "tempo_gemm_w8a16_gate_up_launch": ([ct.POINTER(TempoW8A16Params), _p], _i),
     "tempo_naive_gemm_w8a16_launch": ([ct.POINTER(TempoW8A16Params), _p], _i),
     "tempo_gptq_repack_u8": ([_p, _p, _p, _i, _i, _i, _p, _p, _p, _p], _i),
 }
@@ -131,6 +133,36 @@ def gemm_fp16(A, B, C=None, stream=None):
     p = TempoGemmParams(_ptr(A), _ptr(B), _ptr(C), M, N, K, A.stride(0), B.stride(0), C.stride(0))
     _check(lib().tempo_gemm_fp16_launch(p, _stream(stream)),
            "tempo_gemm_fp16_launch")
+    return C
+
+
+def gemm_fp16_gate_up(A, B, C=None, stream=None):
+    """C[M,N] = silu(A.B[:N]^T) * (A.B[N:]^T) for B [2N, K] (gate rows, then up rows)."""
+    import torch
+
+    M, K = A.shape
+    N = B.shape[0] // 2
+    if C is None:
+        C = torch.empty((M, N), dtype=torch.float16, device=A.device)
+    p = TempoGemmParams(_ptr(A), _ptr(B), _ptr(C), M, N, K, A.stride(0), B.stride(0), C.stride(0))
+    _check(lib().tempo_gemm_fp16_gate_up_launch(p, _stream(stream)),
+           "tempo_gemm_fp16_gate_up_launch")
+    return C
+
+
+def gemm_w8a16_gate_up(A, Wq, scale, zero=None, fmt: int = W8_SYM_I8, group: int = 128, C=None,
+                       stream=None):
+    """The fused gate/up GEMM on 8-bit weights: Wq [2N, K] (and its scale / zero rows)."""
+    import torch
+
+    M = A.shape[0]
+    N = Wq.shape[0] // 2
+    if C is None:
+        C = torch.empty((M, N), dtype=torch.float16, device=A.device)
+    p = w8a16_params(A, Wq, scale, zero, C, fmt, group)
+    p.N = N
+    _check(lib().tempo_gemm_w8a16_gate_up_launch(p, _stream(stream)),
+           "tempo_gemm_w8a16_gate_up_launch")
     return C
 
 

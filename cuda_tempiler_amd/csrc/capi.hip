@@ -107,6 +107,16 @@ int tempo_gemm_w8a16_launch(const TempoW8A16Params* p, tempo_stream_t stream) {
   return (int)tempo::gen8::launch(to_pod(p), static_cast<hipStream_t>(stream));
 }
 
+int tempo_gemm_fp16_gate_up_launch(const TempoGemmParams* p, tempo_stream_t stream) {
+  if (!p) return (int)hipErrorInvalidValue;
+  return (int)tempo::gen::launch_gate_up(to_pod(p), static_cast<hipStream_t>(stream));
+}
+
+int tempo_gemm_w8a16_gate_up_launch(const TempoW8A16Params* p, tempo_stream_t stream) {
+  if (!p) return (int)hipErrorInvalidValue;
+  return (int)tempo::gen8::launch_gate_up(to_pod(p), static_cast<hipStream_t>(stream));
+}
+
 int tempo_dequant_tile(const TempoW8A16Params* p, int n0, int k0, int rows, int cols, void* out,
                        tempo_stream_t stream) {
   if (!p || !out) return (int)hipErrorInvalidValue;
@@ -163,15 +173,19 @@ int tempo_probe_mfma_layout(int ms, float* out, tempo_stream_t stream) {
 int tempo_route(int op, int M, int N, int K, char* tag, int tag_len) {
   // Host-only: dummy 16-byte-aligned addresses stand in for device pointers (never touched).
   const uintptr_t fake = 0x1000;
-  if (op == 0) {
+  const bool gu = op >= 3 && op <= 5;  // fused gate/up variants of ops 0..2
+  const int base = gu ? op - 3 : op;
+  if (base == 0) {
     TempoGemmParams p = {(const void*)fake, (const void*)fake, (void*)fake, M, N, K, K, K, N};
-    return copy_tag(tempo::gen::route(to_pod(&p)), tag, tag_len);
+    return copy_tag(gu ? tempo::gen::route_gate_up(to_pod(&p)) : tempo::gen::route(to_pod(&p)),
+                    tag, tag_len);
   }
-  if (op == 1 || op == 2) {
+  if (base == 1 || base == 2) {
     TempoW8A16Params p = {(const void*)fake, (const void*)fake, (const void*)fake,
-                          op == 2 ? (const void*)fake : nullptr, (void*)fake, M, N, K, K, K, N,
-                          op == 2 ? 128 : 0, op};
-    return copy_tag(tempo::gen8::route(to_pod(&p)), tag, tag_len);
+                          base == 2 ? (const void*)fake : nullptr, (void*)fake, M, N, K, K, K, N,
+                          base == 2 ? 128 : 0, base};
+    return copy_tag(gu ? tempo::gen8::route_gate_up(to_pod(&p)) : tempo::gen8::route(to_pod(&p)),
+                    tag, tag_len);
   }
   return copy_tag(nullptr, tag, tag_len);
 }

@@ -18,6 +18,7 @@ route around libtempo_gfx950.so.
     import cuda_tempiler_amd.torch_ops as tops
     y = torch.ops.tempo.linear_fp16(x, w)              # x [..., K] fp16, w [N, K] fp16
     y = torch.ops.tempo.linear_w8a16(x, wq, s, z, 2, 128)
+    h = torch.ops.tempo.linear_gate_up_fp16(x, w_gate_up)   # silu(x.Wg^T) * (x.Wu^T), fused
     tops.counters()                                     # {"d256x256k64w16m16": 3, "off": 1, ...}
 """
 from __future__ import annotations
@@ -161,6 +162,80 @@ def linear_w8a16(x: torch.Tensor, wq: torch.Tensor, scale: torch.Tensor,
 @linear_w8a16.register_fake
 def _(x, wq, scale, zero, fmt, group):
     return x.new_empty((*x.shape[:-1], wq.shape[0]))
+
+
+# ------------------------------------------------------------------------------ fused gate/up
+
+
+def _silu_mul_own(y: torch.Tensor) -> torch.Tensor:
+    g, u = y.chunk(2, dim=-1)
+    return F.silu(g) * u
+
+
+def _gate_up_impl(x, run_kernel, own_path, op_code, N, K):
+    if not enabled():
+        _count("off")
+        return own_path()
+    x2 = _rows(x)
+    M = x2.shape[0]
+    tag = capi.route(op_code, M, N, K)
+    y = torch.empty((M, N), dtype=torch.float16, device=x.device)
+    try:
+        run_kernel(x2, y)
+    except capi.NotCovered:
+        _count("fallback")
+        return own_path()
+    _count(tag)
+    return y.view(*x.shape[:-1], N)
+
+
+@torch.library.custom_op("tempo::linear_gate_up_fp16", mutates_args=())
+def linear_gate_up_fp16(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """silu(x . w[:N]^T) * (x . w[N:]^T) for the merged gate_up weight w [2N, K] (gate rows, then
+    up rows): the MLP's first projection with its activation fused into the GEMM epilogue."""
+    N, K = w.shape[0] // 2, w.shape[1]
+
+    def own_path():
+        return _silu_mul_own(F.linear(x, w))
+
+    if (x.dtype != torch.float16 or w.dtype != torch.float16 or w.dim() != 2 or w.shape[0] % 2
+            or w.stride(1) != 1 or not _covered_device(x, w) or x.shape[-1] != K):
+        if enabled():
+            _count("fallback")
+            return own_path()
+    return _gate_up_impl(x, lambda x2, y: capi.gemm_fp16_gate_up(x2, w, y), own_path, 3, N, K)
+
+
+@linear_gate_up_fp16.register_fake
+def _(x, w):
+    return x.new_empty((*x.shape[:-1], w.shape[0] // 2))
+
+
+@torch.library.custom_op("tempo::linear_gate_up_w8a16", mutates_args=())
+def linear_gate_up_w8a16(x: torch.Tensor, wq: torch.Tensor, scale: torch.Tensor,
+                         zero: Optional[torch.Tensor], fmt: int, group: int) -> torch.Tensor:
+    """The fused gate/up projection on 8-bit weights wq [2N, K] (scale / zero rows follow)."""
+    N, K = wq.shape[0] // 2, wq.shape[1]
+
+    def own_path():
+        return _silu_mul_own(F.linear(x, dequantize(wq, scale, zero, fmt, group).to(x.device)))
+
+    if (x.dtype != torch.float16 or wq.dim() != 2 or wq.shape[0] % 2 or wq.stride(1) != 1
+            or not _covered_device(x, wq, scale, zero) or x.shape[-1] != K
+            or fmt not in (capi.W8_SYM_I8, capi.W8_ASYM_U8)):
+        if enabled():
+            _count("fallback")
+            return own_path()
+    return _gate_up_impl(
+        x, lambda x2, y: capi.gemm_w8a16_gate_up(x2, wq, scale.contiguous(),
+                                                 zero.contiguous() if zero is not None else None,
+                                                 fmt=fmt, group=group, C=y),
+        own_path, 3 + fmt, N, K)
+
+
+@linear_gate_up_w8a16.register_fake
+def _(x, wq, scale, zero, fmt, group):
+    return x.new_empty((*x.shape[:-1], wq.shape[0] // 2))
 
 
 # ------------------------------------------------------------------------------ modules

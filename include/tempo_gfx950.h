@@ -78,6 +78,20 @@ typedef struct TempoW8A16Params {
 int tempo_gemm_w8a16_applicable(const TempoW8A16Params* p);
 int tempo_gemm_w8a16_launch(const TempoW8A16Params* p, tempo_stream_t stream);
 
+/* ------------------------------------------------------------------------------------------
+ * Fused gate/up epilogue (the MLP's first projection):
+ *   C[m][n] = silu(G[m][n]) * U[m][n],  G = A . B[0..N)^T,  U = A . B[N..2N)^T
+ * with N the OUTPUT width: B (fp16) or Wq / scale / zero (W8A16) hold 2N rows, the gate rows
+ * then the up rows (the merged gate_up layout; the production shape S1 of
+ * bench/shapes/qwen36_27b_int8.json is this GEMM at 2N = 34816).  G and U are rounded to fp16
+ * before the epilogue, so the result is the unfused chain's up to the last bit of silu.  The
+ * reference names this fusion and its price and does not ship it (docs/NOT_YET.md:141-146,
+ * kernels/shipped/gemm_fp16/sm_70/INTEGRATION.md:21).  Decode shapes (M <= 32) are covered;
+ * others return TEMPO_FALLBACK (run the plain GEMM and the elementwise step).
+ * ------------------------------------------------------------------------------------------ */
+int tempo_gemm_fp16_gate_up_launch(const TempoGemmParams* p, tempo_stream_t stream);
+int tempo_gemm_w8a16_gate_up_launch(const TempoW8A16Params* p, tempo_stream_t stream);
+
 /* Debug/verification: dequantise rows [n0, n0+rows) x cols [k0, k0+cols) of Wq into fp16
  * out[rows][cols] with the same device functions the GEMM feeds use (cols % 8 == 0, k0 % 8 == 0).
  * No reference counterpart: the reference's skeleton has no scale, so its dequantisation is the
@@ -147,7 +161,8 @@ int tempo_naive_gemm_w8a16_launch(const TempoW8A16Params* p, tempo_stream_t stre
  * result register).  nacc = 16 for ms 32, 4 for ms 16.  `out` is device memory. */
 int tempo_probe_mfma_layout(int ms, float* out, tempo_stream_t stream);
 
-/* Name of the shipped ladder row a shape dispatches to ("" when not covered).  op 0 = gemm_fp16,
+/* Name of the shipped ladder row a shape dispatches to ("" when not covered).  ops 3, 4, 5 are the
+ * fused gate/up variants of ops 0, 1, 2 (N = output width).  op 0 = gemm_fp16,
  * op 1 = gemm_w8a16 (fmt 1), op 2 = gemm_w8a16 (fmt 2).  Host-only; no GPU needed. */
 int tempo_route(int op, int M, int N, int K, char* tag, int tag_len);
 

@@ -44,8 +44,11 @@ inline void stream_split(int N, int K, int R, int U, int* S_out, int* chunk_out)
 // Activations staged in LDS (ALDS rows) only while M*(2K+16) bytes stay within this budget.
 constexpr size_t kStreamActLds = 96 * 1024;
 
-template <int MB, int R, int U, int ALDS>
+// EPI = 1: fused gate/up epilogue -- p.N is the output width, B holds 2N rows (gate, then up)
+// and C = silu(A.B[0..N)^T) * (A.B[N..2N)^T); each wave carries 2R row groups.
+template <int MB, int R, int U, int ALDS, int EPI = 0>
 inline hipError_t launch_stream(const GemmParams& p, hipStream_t s) {
+  constexpr int RR = EPI ? 2 * R : R;
   StreamArgs a;
   a.A = p.A;
   a.B = p.B;
@@ -59,22 +62,25 @@ inline hipError_t launch_stream(const GemmParams& p, hipStream_t s) {
   a.ldb = p.ldb;
   a.ldc = p.ldc;
   a.group = 0;
+  a.up = EPI ? p.N : 0;
   stream_split(p.N, p.K, R, U, &a.S, &a.chunk);
   const dim3 grid(p.N / (16 * R)), blk(64 * a.S);
-  const size_t red = a.S > 1 ? (size_t)a.S * R * MB * 64 * 16 : 0;
+  const size_t red = a.S > 1 ? (size_t)a.S * RR * MB * 64 * 16 : 0;
   const size_t act = (size_t)p.M * (2 * (size_t)p.K + 16);
   if (ALDS && act <= kStreamActLds)
-    hipLaunchKernelGGL((k_stream<MB, R, U, 0, 1>), grid, blk, act + red, s, a);
+    hipLaunchKernelGGL((k_stream<MB, R, U, 0, 1, EPI>), grid, blk, act + red, s, a);
   else
-    hipLaunchKernelGGL((k_stream<MB, R, U, 0, 0>), grid, blk, red, s, a);
+    hipLaunchKernelGGL((k_stream<MB, R, U, 0, 0, EPI>), grid, blk, red, s, a);
   return hipGetLastError();
 }
 
 // k-chunks of the shared-activation kernel: about 2048 waves over the part, at most TPB/64 waves
 // per workgroup (TPB = the kernel's launch bound), the stage count divisible by the chunk count, and the activation rings of every
 // chunk plus the reduction within the 160 KiB of LDS.
+// RR: row groups per wave (2R with the fused gate/up epilogue; 0 = R).
 inline void shared_split(int N, int K, int MB, int R, int U, int SN, int TPB, int* SK_out,
-                         int* chunk_out, size_t* lds_out) {
+                         int* chunk_out, size_t* lds_out, int RR = 0) {
+  if (RR == 0) RR = R;
   const int stages = K / (64 * U);
   const int wgs = N / (16 * R * SN);
   int SK = (2048 + wgs * SN - 1) / (wgs * SN);
@@ -82,7 +88,7 @@ inline void shared_split(int N, int K, int MB, int R, int U, int SN, int TPB, in
   if (SK < 1) SK = 1;
   const size_t stage = (size_t)16 * MB * 128 * U;
   auto lds = [&](int sk) {
-    return (size_t)sk * 2 * stage + (sk > 1 ? (size_t)SN * sk * R * MB * 1024 : 0);
+    return (size_t)sk * 2 * stage + (sk > 1 ? (size_t)SN * sk * RR * MB * 1024 : 0);
   };
   while (SK > 1 && (stages % SK != 0 || lds(SK) > 160 * 1024)) --SK;
   *SK_out = SK;
@@ -90,7 +96,7 @@ inline void shared_split(int N, int K, int MB, int R, int U, int SN, int TPB, in
   *lds_out = lds(SK);
 }
 
-template <int MB, int R, int U, int SN, int TPB>
+template <int MB, int R, int U, int SN, int TPB, int EPI = 0>
 inline hipError_t launch_shared(const GemmParams& p, hipStream_t s) {
   StreamArgs a;
   a.A = p.A;
@@ -105,10 +111,13 @@ inline hipError_t launch_shared(const GemmParams& p, hipStream_t s) {
   a.ldb = p.ldb;
   a.ldc = p.ldc;
   a.group = 0;
+  a.up = EPI ? p.N : 0;
   size_t lds = 0;
-  shared_split(p.N, p.K, MB, R, U, SN, TPB, &a.S, &a.chunk, &lds);
-  const dim3 grid(p.N / (16 * R * SN)), blk(64 * SN * a.S);
-  hipLaunchKernelGGL((k_stream_sh<MB, R, U, 0, SN, TPB>), grid, blk, lds, s, a);
+  // EPI: the slab waves pair up (gate, up), so the work is that of the plain kernel over 2N rows
+  const int rows = EPI ? 2 * p.N : p.N;
+  shared_split(rows, p.K, MB, R, U, SN, TPB, &a.S, &a.chunk, &lds);
+  const dim3 grid(rows / (16 * R * SN)), blk(64 * SN * a.S);
+  hipLaunchKernelGGL((k_stream_sh<MB, R, U, 0, SN, TPB, EPI>), grid, blk, lds, s, a);
   return hipGetLastError();
 }
 
@@ -155,6 +164,12 @@ hipError_t launch(const GemmParams& p, hipStream_t s);
 
 // Host-only: tag of the ladder row launch() would run, nullptr when not covered.
 const char* route(const GemmParams& p);
+
+// Fused gate/up: C[M][N] = silu(A . B[0..N)^T) * (A . B[N..2N)^T), B with 2N rows of stride ldb
+// (the gate rows, then the up rows).  Its own ladder (dispatch_gate_up.inc); not covered ->
+// hipErrorInvalidConfiguration, the caller runs the plain GEMM and its own elementwise step.
+hipError_t launch_gate_up(const GemmParams& p, hipStream_t s);
+const char* route_gate_up(const GemmParams& p);
 
 }  // namespace gen
 }  // namespace tempo

@@ -30,9 +30,30 @@ LADDER = [
      dict(BM=256, BN=256, BK=64, WM=4, WN=4, STAGES=2, SWZ=2, GROUP=8, XCD=1, MS=16)),
 ]
 
+# Fused gate/up ladder (C = silu(A.B[0..N)^T) * (A.B[N..2N)^T), N = output width): the decode
+# kernels with EPI = 1 (shared: the slab waves pair up, gate and up; stream: each wave carries
+# the gate and the up row groups of its slab).  Rows measured on (N, K) = (17408, 5120) and
+# (7680, 3840) against the plain GEMM + a separate silu*mul kernel.  M > 32 is not covered: the
+# caller runs the plain GEMM and its own elementwise step.
+LADDER_GATE_UP = [
+    (1, 0, "gh1r1u2n2", "shared", dict(MB=1, R=1, U=2, SN=2, TPB=512)),
+    (16, 0, "gh16r1u4n2", "shared", dict(MB=1, R=1, U=4, SN=2, TPB=512)),
+    (16, 0, "g16r1u4", "stream", dict(MB=1, R=1, U=4, A=0)),
+    (32, 0, "gh32r1u4n4", "shared", dict(MB=2, R=1, U=4, SN=4, TPB=1024)),
+    (32, 0, "g32r1u4", "stream", dict(MB=2, R=1, U=4, A=0)),
+]
+
 # Divisibility each kind needs (checked at run time by dispatch.inc, mirrored here).
 STREAM_K_STEP = 64  # k per pipeline step of the stream kernel
 STREAM_N_ROWS = 16  # weight rows per MFMA row group (times R)
+
+
+def _fits_gate_up(kind, p, M, N, K):
+    # N is the output width; the shared kernel's SN slab waves pair up (SN/2 output slabs)
+    if kind == "shared":
+        return (p["SN"] % 2 == 0 and N % (STREAM_N_ROWS * p["R"] * p["SN"] // 2) == 0
+                and K % (STREAM_K_STEP * p["U"]) == 0)
+    return _fits(kind, p, M, N, K)
 
 
 def _fits(kind, p, M, N, K):
@@ -51,7 +72,22 @@ def select(op, M, N, K, dtype_a="fp16", dtype_b="fp16", dtype_c="fp16", arch=ARC
         return None
     if M <= 0 or N <= 0 or K <= 0 or N % 8 or K % 8:
         return None
-    for m_max, n_min, tag, kind, p in LADDER:
-        if M <= m_max and N >= n_min and _fits(kind, p, M, N, K):
+    return _first(LADDER, M, N, K)
+
+
+def _first(ladder, M, N, K, fits=_fits):
+    for m_max, n_min, tag, kind, p in ladder:
+        if M <= m_max and N >= n_min and fits(kind, p, M, N, K):
             return dict(tag=tag, kind=kind, **p)
     return None
+
+
+def select_gate_up(op, M, N, K, dtype_a="fp16", dtype_b="fp16", dtype_c="fp16", arch=ARCH):
+    """The fused gate/up row for output width N (B has 2N rows), or None."""
+    if op != "gemm_gate_up" or arch != ARCH:
+        return None
+    if (dtype_a, dtype_b, dtype_c) != ("fp16", "fp16", "fp16"):
+        return None
+    if M <= 0 or N <= 0 or K <= 0 or N % 8 or K % 8:
+        return None
+    return _first(LADDER_GATE_UP, M, N, K, _fits_gate_up)

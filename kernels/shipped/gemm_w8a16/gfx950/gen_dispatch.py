@@ -34,22 +34,26 @@ HEAD = """// GENERATED from select.py -- do not edit.  Regenerate with:
 """
 
 
-def instantiation(kind, p):
+def instantiation(kind, p, epi=0):
+    tail = ",%d" % epi if epi else ""
     if kind == "shared":
-        return "launch_shared<%d,%d,%d,%d,%d>" % (p["MB"], p["R"], p["U"], p["SN"],
-                                                  p.get("TPB", 1024))
+        return "launch_shared<%d,%d,%d,%d,%d%s>" % (p["MB"], p["R"], p["U"], p["SN"],
+                                                    p.get("TPB", 1024), tail)
     if kind == "stream":
-        return "launch_stream<%d,%d,%d,%d>" % (p["MB"], p["R"], p["U"], p.get("A", 0))
+        return "launch_stream<%d,%d,%d,%d%s>" % (p["MB"], p["R"], p["U"], p.get("A", 0), tail)
+    if epi:
+        raise ValueError("the fused gate/up epilogue exists for the stream kernels only")
     return "launch_mfma<%d,%d,%d,%d,%d,%d,%d,%d,%d>" % (
         p["BM"], p["BN"], p["BK"], p["WM"], p["WN"], p["MS"], p["SWZ"], p["GROUP"], p["XCD"])
 
 
-def condition(sel, kind, p, m_max, n_min=0):
+def condition(sel, kind, p, m_max, n_min=0, gate_up=False):
     if kind == "stream":
         fit = "(p.N %% %d) == 0 && (p.K %% %d) == 0" % (sel.STREAM_N_ROWS * p["R"],
                                                           sel.STREAM_K_STEP * p["U"])
     elif kind == "shared":
-        fit = "(p.N %% %d) == 0 && (p.K %% %d) == 0" % (sel.STREAM_N_ROWS * p["R"] * p["SN"],
+        spw = p["SN"] // 2 if gate_up else p["SN"]  # gate/up: the slab waves pair up
+        fit = "(p.N %% %d) == 0 && (p.K %% %d) == 0" % (sel.STREAM_N_ROWS * p["R"] * spw,
                                                           sel.STREAM_K_STEP * p["U"])
     else:
         fit = "(p.N %% %d) == 0 && (p.K %% %d) == 0" % (p["BN"], p["BK"])
@@ -61,18 +65,27 @@ def condition(sel, kind, p, m_max, n_min=0):
     return band, fit
 
 
-def render() -> str:
+HEAD_GATE_UP = """// GENERATED from select.py (LADDER_GATE_UP) -- do not edit.  Regenerate with:
+//   python3 kernels/shipped/gemm_w8a16/gfx950/gen_dispatch.py --gate-up > dispatch_gate_up.inc
+//
+// Fused gate/up ladder: p.N is the output width, the weights hold 2N rows (gate, then up).  Same
+// row rule as dispatch.inc; none -> hipErrorInvalidConfiguration.
+"""
+
+
+def render(gate_up: bool = False) -> str:
     sel = _select()
-    out = [HEAD]
-    for m_max, n_min, tag, kind, p in sel.LADDER:
-        band, fit = condition(sel, kind, p, m_max, n_min)
-        out.append("TEMPO_ROW(%s, %s,\n          (%s), \"%s\")" % (band, fit, instantiation(kind, p), tag))
+    out = [HEAD_GATE_UP if gate_up else HEAD]
+    for m_max, n_min, tag, kind, p in (sel.LADDER_GATE_UP if gate_up else sel.LADDER):
+        band, fit = condition(sel, kind, p, m_max, n_min, gate_up)
+        out.append("TEMPO_ROW(%s, %s,\n          (%s), \"%s\")"
+                   % (band, fit, instantiation(kind, p, 1 if gate_up else 0), tag))
     out.append("TEMPO_FALLBACK_ROW")
     return "\n".join(out) + "\n"
 
 
 def main():
-    sys.stdout.write(render())
+    sys.stdout.write(render(gate_up="--gate-up" in sys.argv[1:]))
     return 0
 
 

@@ -63,30 +63,35 @@ inline StreamArgs stream_args(const W8A16Params& p) {
   a.S = 1;
   a.chunk = p.K;
   a.group = p.fmt == 2 ? p.group : 0;
+  a.up = 0;
   return a;
 }
 
 // Activations staged in LDS (ALDS rows) only while M*(2K+16) bytes stay within this budget.
 constexpr size_t kStreamActLds = 96 * 1024;
 
-template <int MB, int R, int U, int ALDS>
+// EPI = 1: fused gate/up epilogue -- p.N is the output width; Wq, scale and zero hold 2N rows
+// (gate, then up) and C = silu(A.deq(W)[0..N)^T) * (A.deq(W)[N..2N)^T).
+template <int MB, int R, int U, int ALDS, int EPI = 0>
 inline hipError_t launch_stream(const W8A16Params& p, hipStream_t s) {
+  constexpr int RR = EPI ? 2 * R : R;
   StreamArgs a = stream_args(p);
+  a.up = EPI ? p.N : 0;
   stream_split(p.N, p.K, R, U, &a.S, &a.chunk);
   const dim3 grid(p.N / (16 * R)), blk(64 * a.S);
-  const size_t red = a.S > 1 ? (size_t)a.S * R * MB * 64 * 16 : 0;
+  const size_t red = a.S > 1 ? (size_t)a.S * RR * MB * 64 * 16 : 0;
   const size_t act = (size_t)p.M * (2 * (size_t)p.K + 16);
   const bool alds = ALDS && act <= kStreamActLds;
   if (p.fmt == 1) {
     if (alds)
-      hipLaunchKernelGGL((k_stream<MB, R, U, 1, 1>), grid, blk, act + red, s, a);
+      hipLaunchKernelGGL((k_stream<MB, R, U, 1, 1, EPI>), grid, blk, act + red, s, a);
     else
-      hipLaunchKernelGGL((k_stream<MB, R, U, 1, 0>), grid, blk, red, s, a);
+      hipLaunchKernelGGL((k_stream<MB, R, U, 1, 0, EPI>), grid, blk, red, s, a);
   } else {
     if (alds)
-      hipLaunchKernelGGL((k_stream<MB, R, U, 2, 1>), grid, blk, act + red, s, a);
+      hipLaunchKernelGGL((k_stream<MB, R, U, 2, 1, EPI>), grid, blk, act + red, s, a);
     else
-      hipLaunchKernelGGL((k_stream<MB, R, U, 2, 0>), grid, blk, red, s, a);
+      hipLaunchKernelGGL((k_stream<MB, R, U, 2, 0, EPI>), grid, blk, red, s, a);
   }
   return hipGetLastError();
 }
@@ -94,8 +99,10 @@ inline hipError_t launch_stream(const W8A16Params& p, hipStream_t s) {
 // k-chunks of the shared-activation kernel (same rule as the gemm_fp16 delivery's): about 2048
 // waves over the part, at most TPB/64 waves per workgroup (TPB = the kernel's launch bound), the stage count divisible by the chunk
 // count, activation rings of every chunk plus the reduction within the 160 KiB of LDS.
+// RR: row groups per wave (2R with the fused gate/up epilogue; 0 = R).
 inline void shared_split(int N, int K, int MB, int R, int U, int SN, int TPB, int* SK_out,
-                         int* chunk_out, size_t* lds_out) {
+                         int* chunk_out, size_t* lds_out, int RR = 0) {
+  if (RR == 0) RR = R;
   const int stages = K / (64 * U);
   const int wgs = N / (16 * R * SN);
   int SK = (2048 + wgs * SN - 1) / (wgs * SN);
@@ -103,7 +110,7 @@ inline void shared_split(int N, int K, int MB, int R, int U, int SN, int TPB, in
   if (SK < 1) SK = 1;
   const size_t stage = (size_t)16 * MB * 128 * U;
   auto lds = [&](int sk) {
-    return (size_t)sk * 2 * stage + (sk > 1 ? (size_t)SN * sk * R * MB * 1024 : 0);
+    return (size_t)sk * 2 * stage + (sk > 1 ? (size_t)SN * sk * RR * MB * 1024 : 0);
   };
   while (SK > 1 && (stages % SK != 0 || lds(SK) > 160 * 1024)) --SK;
   *SK_out = SK;
@@ -111,16 +118,19 @@ inline void shared_split(int N, int K, int MB, int R, int U, int SN, int TPB, in
   *lds_out = lds(SK);
 }
 
-template <int MB, int R, int U, int SN, int TPB>
+template <int MB, int R, int U, int SN, int TPB, int EPI = 0>
 inline hipError_t launch_shared(const W8A16Params& p, hipStream_t s) {
   StreamArgs a = stream_args(p);
+  a.up = EPI ? p.N : 0;
   size_t lds = 0;
-  shared_split(p.N, p.K, MB, R, U, SN, TPB, &a.S, &a.chunk, &lds);
-  const dim3 grid(p.N / (16 * R * SN)), blk(64 * SN * a.S);
+  // EPI: the slab waves pair up (gate, up), so the work is that of the plain kernel over 2N rows
+  const int rows = EPI ? 2 * p.N : p.N;
+  shared_split(rows, p.K, MB, R, U, SN, TPB, &a.S, &a.chunk, &lds);
+  const dim3 grid(rows / (16 * R * SN)), blk(64 * SN * a.S);
   if (p.fmt == 1)
-    hipLaunchKernelGGL((k_stream_sh<MB, R, U, 1, SN, TPB>), grid, blk, lds, s, a);
+    hipLaunchKernelGGL((k_stream_sh<MB, R, U, 1, SN, TPB, EPI>), grid, blk, lds, s, a);
   else
-    hipLaunchKernelGGL((k_stream_sh<MB, R, U, 2, SN, TPB>), grid, blk, lds, s, a);
+    hipLaunchKernelGGL((k_stream_sh<MB, R, U, 2, SN, TPB, EPI>), grid, blk, lds, s, a);
   return hipGetLastError();
 }
 
@@ -155,6 +165,12 @@ inline bool applicable(const W8A16Params& p) {
 
 hipError_t launch(const W8A16Params& p, hipStream_t s);
 const char* route(const W8A16Params& p);
+
+// Fused gate/up: C[M][N] = silu(A . deq(W)[0..N)^T) * (A . deq(W)[N..2N)^T), Wq / scale / zero
+// with 2N rows (gate, then up).  Its own ladder (dispatch_gate_up.inc); not covered ->
+// hipErrorInvalidConfiguration.
+hipError_t launch_gate_up(const W8A16Params& p, hipStream_t s);
+const char* route_gate_up(const W8A16Params& p);
 
 // Dequantise a [rows][cols] tile of the weights with the GEMM feeds' own device functions.
 inline hipError_t dequant_tile(const W8A16Params& p, int n0, int k0, int rows, int cols,

@@ -29,5 +29,25 @@ const char* route(const W8A16Params& p) {
 #undef TEMPO_FALLBACK_ROW
 }
 
+hipError_t launch_gate_up(const W8A16Params& p, hipStream_t s) {
+  if (!applicable(p)) return hipErrorInvalidConfiguration;
+#define TEMPO_ROW(band, fit, fn, tag) \
+  if ((band) && (fit)) return fn(p, s);
+#define TEMPO_FALLBACK_ROW return hipErrorInvalidConfiguration;
+#include "dispatch_gate_up.inc"
+#undef TEMPO_ROW
+#undef TEMPO_FALLBACK_ROW
+}
+
+const char* route_gate_up(const W8A16Params& p) {
+  if (!applicable(p)) return nullptr;
+#define TEMPO_ROW(band, fit, fn, tag) \
+  if ((band) && (fit)) return tag;
+#define TEMPO_FALLBACK_ROW return nullptr;
+#include "dispatch_gate_up.inc"
+#undef TEMPO_ROW
+#undef TEMPO_FALLBACK_ROW
+}
+
 }  // namespace gen8
 }  // namespace tempo

@@ -33,8 +33,32 @@ LADDER = [
      dict(BM=256, BN=256, BK=64, WM=2, WN=2, MS=32, SWZ=1, GROUP=8, XCD=1)),
 ]
 
+# Fused gate/up ladder (C = silu(A.deq(W)[0..N)^T) * (A.deq(W)[N..2N)^T), N = output width): the
+# decode kernels with EPI = 1 (shared: paired gate/up slab waves).  Rows measured on the
+# production gate_up shape (N, K) = (17408, 5120), both formats.  M > 32 is not covered (the
+# caller's own path).
+LADDER_GATE_UP = [
+    (1, 0, "g1a_r1u2", "stream", dict(MB=1, R=1, U=2, A=1, fmts=(1,))),
+    (1, 0, "g1a_r1u8", "stream", dict(MB=1, R=1, U=8, A=1, fmts=(2,))),
+    (1, 0, "g1a_r1u4", "stream", dict(MB=1, R=1, U=4, A=1)),
+    (16, 0, "gh16r1u2n2", "shared", dict(MB=1, R=1, U=2, SN=2, TPB=512, fmts=(1,))),
+    (16, 0, "gh16r1u4n2", "shared", dict(MB=1, R=1, U=4, SN=2, TPB=512)),
+    (16, 0, "g16r1u4", "stream", dict(MB=1, R=1, U=4, A=0)),
+    (32, 0, "gh32r1u2n4", "shared", dict(MB=2, R=1, U=2, SN=4, TPB=1024, fmts=(1,))),
+    (32, 0, "gh32r1u4n4", "shared", dict(MB=2, R=1, U=4, SN=4, TPB=512)),
+    (32, 0, "g32r1u4", "stream", dict(MB=2, R=1, U=4, A=0)),
+]
+
 STREAM_K_STEP = 64
 STREAM_N_ROWS = 16
+
+
+def _fits_gate_up(kind, p, M, N, K):
+    # N is the output width; the shared kernel's SN slab waves pair up (SN/2 output slabs)
+    if kind == "shared":
+        return (p["SN"] % 2 == 0 and N % (STREAM_N_ROWS * p["R"] * p["SN"] // 2) == 0
+                and K % (STREAM_K_STEP * p["U"]) == 0)
+    return _fits(kind, p, M, N, K)
 
 
 def _fits(kind, p, M, N, K):
@@ -55,10 +79,27 @@ def select(op, M, N, K, fmt=1, group=128, dtype_a="fp16", dtype_c="fp16", arch=A
         return None
     if fmt == 2 and (group != 128 or K % group):
         return None
-    for m_max, n_min, tag, kind, p in LADDER:
+    return _first(LADDER, M, N, K, fmt)
+
+
+def _first(ladder, M, N, K, fmt, fits=_fits):
+    for m_max, n_min, tag, kind, p in ladder:
         if fmt not in p.get("fmts", FORMATS):
             continue
-        if M <= m_max and N >= n_min and _fits(kind, p, M, N, K):
+        if M <= m_max and N >= n_min and fits(kind, p, M, N, K):
             q = {k: v for k, v in p.items() if k != "fmts"}
             return dict(tag=tag, kind=kind, fmt=fmt, **q)
     return None
+
+
+def select_gate_up(op, M, N, K, fmt=1, group=128, dtype_a="fp16", dtype_c="fp16", arch=ARCH):
+    """The fused gate/up row for output width N (the weights have 2N rows), or None."""
+    if op != "gemm_w8a16_gate_up" or arch != ARCH:
+        return None
+    if (dtype_a, dtype_c) != ("fp16", "fp16") or fmt not in FORMATS:
+        return None
+    if M <= 0 or N <= 0 or K <= 0 or N % 8 or K % 8:
+        return None
+    if fmt == 2 and (group != 128 or K % group):
+        return None
+    return _first(LADDER_GATE_UP, M, N, K, fmt, _fits_gate_up)

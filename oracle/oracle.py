@@ -223,3 +223,29 @@ def gptq_dense(qweight, qzeros, scales, G: int = 128):
     """W [K,N] fp16 = fp16_rn((q - z[k/G]) * s[k/G]) -- gemm_baseline.py:229."""
     wq, s, z = gptq_to_nk(qweight, qzeros, scales, G)
     return np.ascontiguousarray(dequant_asym(wq, s, z, G).T)
+
+
+def silu_mul(g, u) -> np.ndarray:
+    """The fused gate/up epilogue on fp16 GEMM results: fp16_rn(silu(g) * u), silu(x) =
+    x / (1 + e^-x), evaluated in fp64 (one rounding).  The reference names this fusion without
+    shipping it (docs/NOT_YET.md:141-146); its unfused form is F.silu(g) * u on the two fp16
+    outputs."""
+    g = np.asarray(g, np.float16).astype(np.float64)
+    u = np.asarray(u, np.float16).astype(np.float64)
+    with np.errstate(over="ignore"):
+        return (g / (1.0 + np.exp(-g)) * u).astype(np.float16)
+
+
+def gemm_gate_up_f16(A, B, threads: int = 0) -> np.ndarray:
+    """C [M,N] = silu_mul(A.B[:N]^T, A.B[N:]^T) for B [2N,K] (gate rows, then up rows)."""
+    N = B.shape[0] // 2
+    return silu_mul(gemm_f16(A, B[:N], threads), gemm_f16(A, B[N:], threads))
+
+
+def gemm_gate_up_w8a16(A, q, s, z=None, G: int = 0, fmt: int = 1, threads: int = 0) -> np.ndarray:
+    """The fused gate/up GEMM on 8-bit weights [2N,K] (scale / zero rows follow the weights)."""
+    N = q.shape[0] // 2
+    sg, su = (s[:N], s[N:])
+    zg, zu = (z[:N], z[N:]) if z is not None else (None, None)
+    return silu_mul(gemm_w8a16(A, q[:N], sg, zg, G, fmt, threads),
+                    gemm_w8a16(A, q[N:], su, zu, G, fmt, threads))

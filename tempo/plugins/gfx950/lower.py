@@ -42,12 +42,19 @@ _ENTRY = {
             ("common/cdna4.h", "gemm_mfma/kernel.hip")),
     "ring": ("k_stream_dma", ("MB", "R", "D", "BFMT"), "StreamArgs",
              ("common/cdna4.h", "gemv_stream/kernel.hip")),
-    "stream": ("k_stream", ("MB", "R", "U", "BFMT", "ALDS"), "StreamArgs",
+    "stream": ("k_stream", ("MB", "R", "U", "BFMT", "ALDS", "EPI"), "StreamArgs",
                ("common/cdna4.h", "gemv_stream/kernel.hip")),
-    "shared": ("k_stream_sh", ("MB", "R", "U", "BFMT", "SN", "TPB"), "StreamArgs",
+    "shared": ("k_stream_sh", ("MB", "R", "U", "BFMT", "SN", "TPB", "EPI"), "StreamArgs",
                ("common/cdna4.h", "gemv_stream/kernel.hip")),
 }
 NAMESPACE = "tempo::gen"
+# trailing template parameters with a default in the skeleton: named only when the hyperform
+# sets them (EPI = 1 is the fused gate/up epilogue of the decode kernels)
+_OPTIONAL = frozenset({"EPI"})
+
+
+def _order(kind: str, p: dict) -> tuple:
+    return tuple(k for k in _ENTRY[kind][1] if k in p or k not in _OPTIONAL)
 
 
 def _p(h: Hyperform) -> dict:
@@ -101,6 +108,8 @@ class Gfx950Skeletons:
         are the optimistic and pessimistic edges of one estimate."""
         p = _p(h)
         kind = p["kind"]
+        if kind == "stream" and p.get("EPI"):
+            p = dict(p, R=2 * p["R"])  # each wave carries the gate and the up row groups
         if kind in ("dma", "reg"):
             ms = p.get("MS", 32)
             nacc = 16 if ms == 32 else 4
@@ -221,7 +230,8 @@ class Gfx950Skeletons:
         kind = p["kind"]
         if kind not in _ENTRY:
             raise PluginCapabilityError("no entry declared for skeleton kind %r" % kind)
-        sym, order, args, files = _ENTRY[kind]
+        sym, _, args, files = _ENTRY[kind]
+        order = _order(kind, p)
         body = []
         for f in files:
             with open(os.path.join(SKEL, f), encoding="utf-8") as fh:
@@ -240,7 +250,8 @@ class Gfx950Skeletons:
     def entry_probe(self, h: Hyperform) -> str:
         """The kernel's name as the profiler prints it (demangled template id)."""
         p = _p(h)
-        sym, order, _, _ = _ENTRY[p["kind"]]
+        sym = _ENTRY[p["kind"]][0]
+        order = _order(p["kind"], p)
         vals = []
         for k in order:
             v = p[k]

@@ -26,7 +26,8 @@ from concurrent.futures import ProcessPoolExecutor
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.abspath(os.path.join(HERE, "..", "..", ".."))
 SHIPPED = os.path.join(ROOT, "kernels", "shipped")
-SIGNED = ("kernel.hip", "launch.h", "launch.hip", "dispatch.inc", "select.py")
+SIGNED = ("kernel.hip", "launch.h", "launch.hip", "dispatch.inc", "dispatch_gate_up.inc",
+          "select.py")
 
 OPS = {
     "gemm_fp16": dict(dtype="fp16 x fp16 -> fp16, fp32 accumulate",
@@ -54,7 +55,14 @@ def md5_of(op):
     return h.hexdigest()
 
 
-def hyper_params(kind, p, fmt):
+def ladder_rows(sel):
+    """Both ladders of a delivery: (M_max, N_min, tag, kind, params, epi); epi = 1 for the fused
+    gate/up ladder."""
+    return ([row + (0,) for row in sel.LADDER]
+            + [row + (1,) for row in getattr(sel, "LADDER_GATE_UP", [])])
+
+
+def hyper_params(kind, p, fmt, epi=0):
     """A ladder row of select.py (kind, template params) -> the plugin's hyperform params: the
     same kernel, named the way space.variants() names it."""
     pk = {"stream": "stream", "mfma": "reg", "dma": "dma", "shared": "shared"}[kind]
@@ -70,6 +78,8 @@ def hyper_params(kind, p, fmt):
         params.setdefault("XT", 0)
         params.setdefault("MINB", 1)
         params.setdefault("MS", 32)
+    if epi:
+        params["EPI"] = 1
     return params
 
 
@@ -166,10 +176,10 @@ def build_numbers(op):
         spec = OpSpec(kind="gemm", dtype_a="fp16", dtype_b=db, dtype_c="fp16", dtype_acc="fp32",
                       layout_a="k", layout_b="k", layout_c="n",
                       shapes={"M": 4096, "N": 15360, "K": 3840})
-        for m_max, n_min, tag, kind, p in sel.LADDER:
+        for m_max, n_min, tag, kind, p, epi in ladder_rows(sel):
             if fmt not in p.get("fmts", (fmt,)):
                 continue
-            params = hyper_params(kind, p, fmt)
+            params = hyper_params(kind, p, fmt, epi)
             h = Hyperform(plugin="gfx950", params=params, key="%s_f%d" % (tag, fmt))
             r = plug.skeletons.render(spec, h)
             with tempfile.TemporaryDirectory() as td:
@@ -212,6 +222,7 @@ def make(op, rows_files=()):
         "dispatch_rule": "rows in order; the first whose band holds (M, N) and whose kernel fits "
                          "the shape runs; none -> fallback",
         "dispatch": [],
+        "dispatch_gate_up": [],
         "build": build_numbers(op),
         "gate": gate_numbers(op),
         "source_md5": md5_of(op),
@@ -221,16 +232,18 @@ def make(op, rows_files=()):
     }
     if "rows_source_md5" in old:
         man["rows_source_md5"] = old["rows_source_md5"]
-    for m_max, n_min, tag, kind, p in sel.LADDER:
+    for m_max, n_min, tag, kind, p, epi in ladder_rows(sel):
         if kind == "stream":
             fit = "N %% %d == 0 and K %% %d == 0" % (sel.STREAM_N_ROWS * p["R"],
                                                     sel.STREAM_K_STEP * p["U"])
         elif kind == "shared":
-            fit = "N %% %d == 0 and K %% %d == 0" % (sel.STREAM_N_ROWS * p["R"] * p["SN"],
+            spw = p["SN"] // 2 if epi else p["SN"]
+            fit = "N %% %d == 0 and K %% %d == 0" % (sel.STREAM_N_ROWS * p["R"] * spw,
                                                     sel.STREAM_K_STEP * p["U"])
         else:
             fit = "N %% %d == 0 and K %% %d == 0" % (p["BN"], p["BK"])
-        man["dispatch"].append(dict(M_max=m_max, N_min=n_min, tag=tag, kind=kind,
+        man["dispatch" if not epi else "dispatch_gate_up"].append(dict(
+                                    M_max=m_max, N_min=n_min, tag=tag, kind=kind,
                                     params={k: v for k, v in p.items() if k != "fmts"},
                                     fmts=list(p.get("fmts", OPS[op]["fmts"])), fit=fit))
     if op == "gemm_w8a16":

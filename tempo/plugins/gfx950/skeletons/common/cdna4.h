@@ -115,3 +115,12 @@ __device__ __forceinline__ f16x8 dequant8_u8(uint32_t w0, uint32_t w1, uint8_t z
 
 __device__ __forceinline__ f16x8 as_f16x8(const u32x4& u) { return __builtin_bit_cast(f16x8, u); }
 __device__ __forceinline__ u32x4 as_u32x4(const f16x8& h) { return __builtin_bit_cast(u32x4, h); }
+
+// Fused gate/up epilogue: silu(g) * u on the fp16-rounded GEMM results, i.e. exactly what the
+// unfused chain (two fp16 GEMM outputs, then silu and a product) sees, in fp32, one rounding to
+// fp16 at the end.  silu(x) = x / (1 + e^-x); e^-x by the hardware exponential.
+__device__ __forceinline__ _Float16 silu_mul_f16(float g, float u) {
+  const float gh = (float)(_Float16)g;
+  const float uh = (float)(_Float16)u;
+  return (_Float16)(gh / (1.0f + __expf(-gh)) * uh);
+}

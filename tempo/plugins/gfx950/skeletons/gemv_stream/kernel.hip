@@ -20,6 +20,14 @@
 // and zero-point with group 128: the stage's scales and zero-points for its 64*U/128 groups
 // arrive with one small load each, in flight together with the weights).
 //
+// EPI (fused gate/up epilogue): 0 = plain C = A.B^T.  1 = C[m][n] = silu(G[m][n]) * U[m][n] with
+// G = A . B[0..N)^T and U = A . B[up..up+N)^T (B holds 2N rows: the gate rows, then the up rows;
+// scales and zero-points follow the B rows).  Each wave then carries 2R row groups, the gate
+// groups of its slab and the matching up groups, so the two results of one output meet in the
+// same lane and the epilogue combines them in registers (k_stream).  k_stream_sh pairs its slab
+// waves instead: half of them stream gate slabs, half the matching up slabs, and the up results
+// reach their gate partners through LDS before the epilogue.
+//
 // k order inside one 64-step: lane (row r = l%16, kgroup g = l/16) owns the 16 consecutive
 // k-values [16g, 16g+16) of its row; the first MFMA takes elements 0..7, the second 8..15.
 // The activation fragment uses the same map, so each product pairs equal k.
@@ -34,6 +42,7 @@ struct StreamArgs {
   int S;               // waves per workgroup = k chunks per slab
   int chunk;           // k per chunk (multiple of 64*U; K is a multiple of 64*U too)
   int group;           // k per scale group (fmt 2)
+  int up;              // EPI = 1: row offset of the "up" half of B (= N, the output width)
 };
 
 // Group-wise metadata of one stage for one lane's row (fmt 2, group 128): GPS = 64*U/128 groups.
@@ -83,17 +92,39 @@ struct WRaw<1> { u32x4 v; };     // 16 bytes int8
 template <>
 struct WRaw<2> { u32x4 v; };     // 16 bytes uint8
 
+// ---- result: lane holds C[m = b*16 + r16][n = nbase + r*16 + 4*kg + v], v = 0..3 ------------
+// (EPI: the gate result in acc[r], the up result of the same outputs in acc[r + R])
+template <int MB, int R, int EPI, int RR>
+__device__ __forceinline__ void stream_store(const StreamArgs& p, const f32x4 (&acc)[RR][MB],
+                                             int nbase, int r16, int kg) {
+#pragma unroll
+  for (int b = 0; b < MB; ++b) {
+    const int m = b * 16 + r16;
+    if (m >= p.M) continue;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int n = nbase + r * 16 + 4 * kg;
+      f16x4 o;
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        o[v] = EPI ? silu_mul_f16(acc[r][b][v], acc[r + R][b][v]) : (_Float16)acc[r][b][v];
+      *reinterpret_cast<f16x4*>(p.C + (long)m * p.ldc + n) = o;
+    }
+  }
+}
+
 // ALDS = 1: the workgroup first copies A[0..M)[0..K) into LDS (row stride 2K+16 bytes, so the 16
 // rows of one fragment read land in 16 distinct bank groups) and the k-loop reads activation
 // fragments from there -- one weight load per k-step instead of one weight + two activation
 // loads, and for M = 1 the 16 lanes of a k-group read one address (an LDS broadcast).  Chosen by
 // the launcher when M*(2K+16) bytes fit its LDS budget.
-template <int MB, int R, int U, int BFMT, int ALDS = 0>
+template <int MB, int R, int U, int BFMT, int ALDS = 0, int EPI = 0>
 __global__ __launch_bounds__(512) void k_stream(StreamArgs p) {
+  constexpr int RR = EPI ? 2 * R : R;  // row groups per wave
   extern __shared__ __attribute__((aligned(16))) uint8_t dsm_s[];
   const long arow_bytes = 2L * p.K + 16;
   const long act_bytes = ALDS ? (long)p.M * arow_bytes : 0;
-  f32x4* red = reinterpret_cast<f32x4*>(dsm_s + act_bytes);  // [S][R*MB][64] partials
+  f32x4* red = reinterpret_cast<f32x4*>(dsm_s + act_bytes);  // [S][RR*MB][64] partials
   const int lane = threadIdx.x & 63;
   const int split = threadIdx.x >> 6;
   const int slab = blockIdx.x;
@@ -105,11 +136,15 @@ __global__ __launch_bounds__(512) void k_stream(StreamArgs p) {
   const int nbase = slab * 16 * R;
 
   // weight row pointers
-  const uint8_t* wrow[R];
-  _Float16 rscale[R];
+  // row groups of this wave: gate groups 0..R-1, then (EPI) the matching up groups
+  auto row_of = [&](int r) -> long {
+    return (EPI && r >= R ? (long)p.up + nbase + (r - R) * 16 : (long)nbase + r * 16) + r16;
+  };
+  const uint8_t* wrow[RR];
+  _Float16 rscale[RR];
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const long n = nbase + r * 16 + r16;
+  for (int r = 0; r < RR; ++r) {
+    const long n = row_of(r);
     constexpr int EB = BFMT == 0 ? 2 : 1;
     wrow[r] = reinterpret_cast<const uint8_t*>(p.B) + (n * p.ldb + 16 * kg) * EB;
     if constexpr (BFMT == 1) rscale[r] = p.scale[n];
@@ -133,19 +168,19 @@ __global__ __launch_bounds__(512) void k_stream(StreamArgs p) {
     __syncthreads();
   }
 
-  f32x4 acc[R][MB], acc2[R][MB];
+  f32x4 acc[RR][MB], acc2[RR][MB];
 #pragma unroll
-  for (int r = 0; r < R; ++r)
+  for (int r = 0; r < RR; ++r)
 #pragma unroll
     for (int b = 0; b < MB; ++b) {
       acc[r][b] = f32x4{0.f, 0.f, 0.f, 0.f};
       acc2[r][b] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
-  WRaw<BFMT> w[2][U][R];
+  WRaw<BFMT> w[2][U][RR];
   u32x4 a[2][U][MB][ALDS ? 1 : 2];
   constexpr int GPS = (64 * U) / 128 > 0 ? (64 * U) / 128 : 1;  // groups per stage (fmt 2)
-  GMeta<GPS> gm[2][R];
+  GMeta<GPS> gm[2][RR];
   const long gstride = BFMT == 2 ? (long)(p.K / 128) : 0;  // groups per weight row
 
   // Every stage is whole: K and the chunk are multiples of 64*U (checked by the launcher), so
@@ -156,7 +191,7 @@ __global__ __launch_bounds__(512) void k_stream(StreamArgs p) {
     for (int u = 0; u < U; ++u) {
       const int k = k0 + 64 * u;
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
+      for (int r = 0; r < RR; ++r) {
         if constexpr (BFMT == 0) {
           const u32x4* q = reinterpret_cast<const u32x4*>(wrow[r] + (long)k * 2);
           w[buf][u][r].v[0] = q[0];
@@ -168,8 +203,8 @@ __global__ __launch_bounds__(512) void k_stream(StreamArgs p) {
       if constexpr (BFMT == 2) {
         if (u == 0) {
 #pragma unroll
-          for (int r = 0; r < R; ++r) {
-            const long gi = (long)(nbase + r * 16 + r16) * gstride + k0 / 128;
+          for (int r = 0; r < RR; ++r) {
+            const long gi = row_of(r) * gstride + k0 / 128;
             gmeta_load<GPS>(gm[buf][r], p.zero + gi, p.scale + gi);
           }
         }
@@ -192,7 +227,7 @@ __global__ __launch_bounds__(512) void k_stream(StreamArgs p) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
+      for (int r = 0; r < RR; ++r) {
         f16x8 w0, w1;
         if constexpr (BFMT == 0) {
           w0 = as_f16x8(w[buf][u][r].v[0]);
@@ -251,7 +286,7 @@ __global__ __launch_bounds__(512) void k_stream(StreamArgs p) {
     compute(IC<0>{}, k0);
   }
 #pragma unroll
-  for (int r = 0; r < R; ++r)
+  for (int r = 0; r < RR; ++r)
 #pragma unroll
     for (int b = 0; b < MB; ++b) acc[r][b] += acc2[r][b];
 
@@ -259,38 +294,24 @@ __global__ __launch_bounds__(512) void k_stream(StreamArgs p) {
   if (p.S > 1) {
     // partials of every wave through LDS; summed in wave order by wave 0
 #pragma unroll
-    for (int r = 0; r < R; ++r)
+    for (int r = 0; r < RR; ++r)
 #pragma unroll
-      for (int b = 0; b < MB; ++b) red[(split * R * MB + r * MB + b) * 64 + lane] = acc[r][b];
+      for (int b = 0; b < MB; ++b) red[(split * RR * MB + r * MB + b) * 64 + lane] = acc[r][b];
     __syncthreads();
     if (split != 0) return;
 #pragma unroll
-    for (int r = 0; r < R; ++r)
+    for (int r = 0; r < RR; ++r)
 #pragma unroll
       for (int b = 0; b < MB; ++b) {
         f32x4 t = red[(r * MB + b) * 64 + lane];
         for (int w = 1; w < p.S; ++w) {
-          const f32x4 v = red[(w * R * MB + r * MB + b) * 64 + lane];
+          const f32x4 v = red[(w * RR * MB + r * MB + b) * 64 + lane];
           t[0] += v[0]; t[1] += v[1]; t[2] += v[2]; t[3] += v[3];
         }
         acc[r][b] = t;
       }
   }
-#pragma unroll
-  for (int b = 0; b < MB; ++b) {
-    const int m = b * 16 + r16;
-    if (m >= p.M) continue;
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int n = nbase + r * 16 + 4 * kg;
-      f16x4 o;
-      o[0] = (_Float16)acc[r][b][0];
-      o[1] = (_Float16)acc[r][b][1];
-      o[2] = (_Float16)acc[r][b][2];
-      o[3] = (_Float16)acc[r][b][3];
-      *reinterpret_cast<f16x4*>(p.C + (long)m * p.ldc + n) = o;
-    }
-  }
+  stream_store<MB, R, EPI>(p, acc, nbase, r16, kg);
 }
 
 // Debug/verification entry: dequantise a [rows x cols] tile of B starting at (n0, k0) with the
@@ -598,8 +619,15 @@ struct StreamSh {
 };
 
 // TPB: the launch bound (512 or 1024 lanes; 1024 caps a lane at 128 registers)
-template <int MB, int R, int U, int BFMT, int SN, int TPB = 512>
+template <int MB, int R, int U, int BFMT, int SN, int TPB = 512, int EPI = 0>
 __global__ __launch_bounds__(TPB) void k_stream_sh(StreamArgs p) {
+  // EPI = 1 pairs the slab waves instead of widening them: of the SN slab waves of a workgroup
+  // the first SN/2 take gate slabs and the last SN/2 the matching up slabs, so a wave carries R
+  // row groups exactly as in the plain kernel; after the k reduction each up wave hands its
+  // result to its gate partner through LDS.
+  constexpr int RR = R;
+  static_assert(!EPI || SN % 2 == 0, "the fused gate/up pairing needs an even SN");
+  constexpr int SPW = EPI ? SN / 2 : SN;  // output slabs per workgroup
   using SS = StreamSh<MB, U>;
   constexpr int RB = SS::RB, STAGE = SS::STAGE, NBLK = SS::NBLK;
   static_assert(NBLK % SN == 0, "activation copy blocks split evenly over the slab waves");
@@ -615,17 +643,20 @@ __global__ __launch_bounds__(TPB) void k_stream_sh(StreamArgs p) {
 
   const int r16 = lane & 15;
   const int kg = lane >> 4;
-  const int slab = blockIdx.x * SN + ng;
-  const int nbase = slab * 16 * R;
+  const bool upw = EPI && ng >= SPW;  // an up wave (EPI)
+  const int slab = blockIdx.x * SPW + (upw ? ng - SPW : ng);
+  const int nbase = slab * 16 * R;  // output rows of this wave's slab
   const int kbeg = kgrp * p.chunk;
   constexpr int STEP = 64 * U;
   const int nst = p.chunk / STEP;  // identical for every k-chunk (launcher)
 
-  const uint8_t* wrow[R];
-  _Float16 rscale[R];
+  // row groups of this wave: gate groups 0..R-1, then (EPI) the matching up groups
+  auto row_of = [&](int r) -> long { return (upw ? (long)p.up : 0L) + nbase + r * 16 + r16; };
+  const uint8_t* wrow[RR];
+  _Float16 rscale[RR];
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const long n = nbase + r * 16 + r16;
+  for (int r = 0; r < RR; ++r) {
+    const long n = row_of(r);
     constexpr int EB = BFMT == 0 ? 2 : 1;
     wrow[r] = reinterpret_cast<const uint8_t*>(p.B) + (n * p.ldb + 16 * kg) * EB;
     if constexpr (BFMT == 1) rscale[r] = p.scale[n];
@@ -657,18 +688,18 @@ __global__ __launch_bounds__(TPB) void k_stream_sh(StreamArgs p) {
     aoff1[q] = r16 * RB + ((8 * q + 2 * kg + 1) ^ r16) * 16;
   }
 
-  f32x4 acc[R][MB], acc2[R][MB];
+  f32x4 acc[RR][MB], acc2[RR][MB];
 #pragma unroll
-  for (int r = 0; r < R; ++r)
+  for (int r = 0; r < RR; ++r)
 #pragma unroll
     for (int b = 0; b < MB; ++b) {
       acc[r][b] = f32x4{0.f, 0.f, 0.f, 0.f};
       acc2[r][b] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
-  WRaw<BFMT> w[2][U][R];
+  WRaw<BFMT> w[2][U][RR];
   constexpr int GPS = (64 * U) / 128 > 0 ? (64 * U) / 128 : 1;
-  GMeta<GPS> gm[2][R];
+  GMeta<GPS> gm[2][RR];
   const long gstride = BFMT == 2 ? (long)(p.K / 128) : 0;
 
   auto issue_w = [&](auto bufc, int k0) {
@@ -677,7 +708,7 @@ __global__ __launch_bounds__(TPB) void k_stream_sh(StreamArgs p) {
     for (int u = 0; u < U; ++u) {
       const int k = k0 + 64 * u;
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
+      for (int r = 0; r < RR; ++r) {
         if constexpr (BFMT == 0) {
           const u32x4* q = reinterpret_cast<const u32x4*>(wrow[r] + (long)k * 2);
           w[buf][u][r].v[0] = q[0];
@@ -689,8 +720,8 @@ __global__ __launch_bounds__(TPB) void k_stream_sh(StreamArgs p) {
     }
     if constexpr (BFMT == 2) {
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const long gi = (long)(nbase + r * 16 + r16) * gstride + k0 / 128;
+      for (int r = 0; r < RR; ++r) {
+        const long gi = row_of(r) * gstride + k0 / 128;
         gmeta_load<GPS>(gm[buf][r], p.zero + gi, p.scale + gi);
       }
     }
@@ -702,7 +733,7 @@ __global__ __launch_bounds__(TPB) void k_stream_sh(StreamArgs p) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
+      for (int r = 0; r < RR; ++r) {
         f16x8 w0, w1;
         if constexpr (BFMT == 0) {
           w0 = as_f16x8(w[buf][u][r].v[0]);
@@ -757,42 +788,53 @@ __global__ __launch_bounds__(TPB) void k_stream_sh(StreamArgs p) {
   if (s < nst) step(IC<0>{}, s);
 
 #pragma unroll
-  for (int r = 0; r < R; ++r)
+  for (int r = 0; r < RR; ++r)
 #pragma unroll
     for (int b = 0; b < MB; ++b) acc[r][b] += acc2[r][b];
 
   if (SK > 1) {
 #pragma unroll
-    for (int r = 0; r < R; ++r)
+    for (int r = 0; r < RR; ++r)
 #pragma unroll
-      for (int b = 0; b < MB; ++b) red[(wave * R * MB + r * MB + b) * 64 + lane] = acc[r][b];
+      for (int b = 0; b < MB; ++b) red[(wave * RR * MB + r * MB + b) * 64 + lane] = acc[r][b];
     __syncthreads();
-    if (kgrp != 0) return;
+    if (kgrp == 0) {
+#pragma unroll
+      for (int r = 0; r < RR; ++r)
+#pragma unroll
+        for (int b = 0; b < MB; ++b) {
+          f32x4 t = acc[r][b];
+          for (int g = 1; g < SK; ++g) {
+            const f32x4 v = red[((g * SN + ng) * RR * MB + r * MB + b) * 64 + lane];
+            t[0] += v[0]; t[1] += v[1]; t[2] += v[2]; t[3] += v[3];
+          }
+          acc[r][b] = t;
+        }
+    }
+  }
+  if constexpr (EPI) {
+    // every wave is past its last ring read (barrier), so ring memory carries the up results
+    f32x4* xb = reinterpret_cast<f32x4*>(dsh);
+    if (SK == 1) __syncthreads();
+    if (kgrp == 0 && upw) {
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int b = 0; b < MB; ++b) xb[(((ng - SPW) * R + r) * MB + b) * 64 + lane] = acc[r][b];
+    }
+    __syncthreads();
+    if (kgrp != 0 || upw) return;
+    f32x4 both[2 * R][MB];
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
       for (int b = 0; b < MB; ++b) {
-        f32x4 t = acc[r][b];
-        for (int g = 1; g < SK; ++g) {
-          const f32x4 v = red[((g * SN + ng) * R * MB + r * MB + b) * 64 + lane];
-          t[0] += v[0]; t[1] += v[1]; t[2] += v[2]; t[3] += v[3];
-        }
-        acc[r][b] = t;
+        both[r][b] = acc[r][b];
+        both[R + r][b] = xb[((ng * R + r) * MB + b) * 64 + lane];
       }
-  }
-#pragma unroll
-  for (int b = 0; b < MB; ++b) {
-    const int m = b * 16 + r16;
-    if (m >= p.M) continue;
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int n = nbase + r * 16 + 4 * kg;
-      f16x4 o;
-      o[0] = (_Float16)acc[r][b][0];
-      o[1] = (_Float16)acc[r][b][1];
-      o[2] = (_Float16)acc[r][b][2];
-      o[3] = (_Float16)acc[r][b][3];
-      *reinterpret_cast<f16x4*>(p.C + (long)m * p.ldc + n) = o;
-    }
+    stream_store<MB, R, 1>(p, both, nbase, r16, kg);
+  } else {
+    if (kgrp != 0) return;
+    stream_store<MB, R, 0>(p, acc, nbase, r16, kg);
   }
 }

@@ -123,3 +123,29 @@ def test_gptq_linear_module(gpu, tops, monkeypatch):
     r = O.rel_l2(host(y), ref)
     say("GPTQLinear relL2 %.2e" % r)
     assert r <= 3e-3
+
+
+@pytest.mark.parametrize("M", [1, 16, 64])
+def test_gate_up_entry_proof(gpu, tops, monkeypatch, M):
+    """Decode M: the fused kernel runs (counter = its ladder row, bit-for-bit the C-ABI call);
+    M = 64 is not covered: the fallback (F.linear, silu, product) runs and is counted."""
+    import torch
+    from cuda_tempiler_amd import capi
+
+    N, K = 4096, 2048
+    x = torch.randn((M, K), dtype=torch.float16, device=gpu) / K ** 0.5
+    w = torch.randn((2 * N, K), dtype=torch.float16, device=gpu)
+    monkeypatch.setenv("TEMPO_KERNELS", "1")
+    y = torch.ops.tempo.linear_gate_up_fp16(x, w)
+    torch.cuda.synchronize()
+    tag = capi.route(3, M, N, K)
+    say("gate_up entry M=%d" % M, tops.counters())
+    g, u = torch.nn.functional.linear(x, w).chunk(2, dim=-1)
+    own = torch.nn.functional.silu(g) * u
+    if tag:
+        assert tops.counters() == {tag: 1}
+        assert torch.equal(y.view(torch.int16), capi.gemm_fp16_gate_up(x, w).view(torch.int16))
+        assert O.rel_l2(host(y), host(own)) <= 3e-3
+    else:
+        assert tops.counters() == {"fallback": 1}
+        assert torch.equal(y, own)

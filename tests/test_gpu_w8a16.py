@@ -199,3 +199,25 @@ def test_gptq_checkpoint_to_gemm(gpu, M):
     r = O.rel_l2(got, ref)
     say("  relL2 %.3e" % r)
     assert r <= 3e-3
+
+
+@pytest.mark.parametrize("fmt", [1, 2])
+@pytest.mark.parametrize("shape", [(1, 64, 128), (7, 200, 384), (33, 1024, 1280)],
+                         ids=lambda s: "m%d_n%d_k%d" % s)
+def test_naive_w8a16_input_is_the_oracle(gpu, fmt, shape):
+    """The naive W8A16 input kernel (kernels/naive/gemm_w8a16.hip, the "vs input" bar of the
+    pipeline) is bit-exact against the oracle: same dequantisation, same sequential fp32 FMA."""
+    import torch
+    from cuda_tempiler_amd import capi
+
+    M, N, K = shape
+    say("naive w8a16", fmt, shape)
+    q, s, z = make_weights(N, K, fmt, seed=M + N + fmt)
+    g = np.random.Generator(np.random.PCG64(M))
+    A = O.f2h(g.standard_normal((M, K), dtype=np.float32))
+    C = capi.naive_gemm_w8a16(dev(A, gpu), dev(q, gpu), dev(s, gpu),
+                              dev(z, gpu) if z is not None else None, fmt=fmt, group=128,
+                              C=poisoned((M, N), gpu))
+    torch.cuda.synchronize()
+    ref = O.gemm_w8a16(A, q, s, z, 128, fmt)
+    assert np.array_equal(host(C).view(np.uint16), ref.view(np.uint16))

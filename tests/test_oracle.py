@@ -250,3 +250,47 @@ def test_gptq_dense_against_reference_formula():
             z = (int(qz[k // G, n // 4]) >> (8 * (n % 4))) & 0xFF
             ref[k, n] = np.float16(float(q - z) * float(sc[k // G, n]))
     assert np.array_equal(W.view(np.uint16), ref.view(np.uint16))
+
+
+def test_silu_mul_against_scipy_expit():
+    """silu(g) = g * expit(g) with scipy's logistic function, independent of the oracle's
+    formula; both rounded once to fp16: at most one unit in the last place apart (ties)."""
+    from scipy.special import expit
+
+    g = np.random.Generator(np.random.PCG64(4))
+    G = O.f2h((g.standard_normal(20000) * 4).astype(np.float32))
+    U = O.f2h(g.standard_normal(20000).astype(np.float32))
+    got = O.silu_mul(G, U)
+    ref = (G.astype(np.float64) * expit(G.astype(np.float64)) * U.astype(np.float64)).astype(np.float16)
+    d = np.abs(got.view(np.int16).astype(np.int32) - ref.view(np.int16).astype(np.int32))
+    assert d.max() <= 1 and (d == 0).mean() > 0.999
+
+
+def test_silu_mul_closed_forms():
+    one = np.ones(5, np.float16)
+    assert not np.any(O.silu_mul(np.zeros(5, np.float16), one).astype(np.float32))
+    big = np.array([12.0, 20.0, 100.0, 1000.0, 60000.0], np.float16)
+    assert np.array_equal(O.silu_mul(big, one), big)            # sigmoid -> 1
+    neg = -big
+    assert np.all(np.abs(O.silu_mul(neg, one).astype(np.float32)) < 1e-3)   # -> 0
+    x = O.f2h(np.linspace(-6, 6, 97).astype(np.float32))
+    odd = O.silu_mul(x, np.ones_like(x)).astype(np.float64) - O.silu_mul(-x, np.ones_like(x)).astype(np.float64)
+    assert np.max(np.abs(odd - x.astype(np.float64))) <= 8e-3   # silu(x) - silu(-x) = x
+    # u scales the result: u = 2 doubles it exactly (a power of two)
+    assert np.array_equal(O.silu_mul(x, np.full_like(x, 2)).astype(np.float32),
+                          2 * O.silu_mul(x, np.ones_like(x)).astype(np.float32))
+
+
+def test_gate_up_oracle_splits_rows_gate_then_up():
+    """Rows [0, N) are the gate, [N, 2N) the up: swapping the halves changes the result, and a
+    B whose up half is the identity's rows gives silu(gate) * A."""
+    g = np.random.Generator(np.random.PCG64(9))
+    M, N, K = 3, 8, 8
+    A = O.f2h(g.standard_normal((M, K)).astype(np.float32))
+    Bg = O.f2h(g.standard_normal((N, K)).astype(np.float32))
+    Bu = np.eye(N, K, dtype=np.float16)
+    C = O.gemm_gate_up_f16(A, np.concatenate([Bg, Bu]))
+    Gm = O.gemm_f16(A, Bg)
+    assert np.array_equal(C, O.silu_mul(Gm, A[:, :N]))
+    C2 = O.gemm_gate_up_f16(A, np.concatenate([Bu, Bg]))
+    assert not np.array_equal(C, C2)

@@ -121,13 +121,13 @@ def _gate_rows():
     out = []
     for opname in OPS:
         man = _manifest(opname)
-        ladder = {t: (k, p) for _, _, t, k, p in manifest._select(opname).LADDER}
+        ladder = {t: (k, p, e) for _, _, t, k, p, e in manifest.ladder_rows(manifest._select(opname))}
         for key, b in man["build"].items():
             tag, _, f = key.partition("/fmt")
             fmt = int(f) if f else 0
-            kind, p = ladder[tag]
+            kind, p, epi = ladder[tag]
             out.append((key, fmt, tuple(manifest.GATE_SHAPES[fmt][0]),
-                        manifest.hyper_params(kind, p, fmt), int(b["regs"]),
+                        manifest.hyper_params(kind, p, fmt, epi), int(b["regs"]),
                         bool(b["vgpr_spill"] or b["scratch_bytes_per_lane"])))
         for b in man["gate"]:
             out.append(("gate", b["fmt"], tuple(b["shape"]), b["params"], int(b["regs"]),

@@ -28,12 +28,14 @@ def _select(op):
 
 
 @pytest.mark.parametrize("op", OPS)
-def test_dispatch_inc_is_generated_from_select(op):
+@pytest.mark.parametrize("table", ["dispatch.inc", "dispatch_gate_up.inc"])
+def test_dispatch_inc_is_generated_from_select(op, table):
     d = os.path.join(SHIPPED, op, "gfx950")
-    text = subprocess.run([sys.executable, os.path.join(d, "gen_dispatch.py")], check=True,
-                          capture_output=True, text=True).stdout
-    with open(os.path.join(d, "dispatch.inc"), encoding="utf-8") as f:
-        assert f.read() == text, "dispatch.inc is stale: re-run the build"
+    args = ["--gate-up"] if table == "dispatch_gate_up.inc" else []
+    text = subprocess.run([sys.executable, os.path.join(d, "gen_dispatch.py")] + args,
+                          check=True, capture_output=True, text=True).stdout
+    with open(os.path.join(d, table), encoding="utf-8") as f:
+        assert f.read() == text, "%s is stale: re-run the build" % table
 
 
 def test_frozen_kernels_match_skeletons():
@@ -45,8 +47,8 @@ def test_frozen_kernels_match_skeletons():
 def test_delivery_layout():
     for op in OPS:
         d = os.path.join(SHIPPED, op, "gfx950")
-        for f in ("kernel.hip", "launch.h", "launch.hip", "dispatch.inc", "select.py",
-                  "gen_dispatch.py", "manifest.json"):
+        for f in ("kernel.hip", "launch.h", "launch.hip", "dispatch.inc", "dispatch_gate_up.inc",
+                  "select.py", "gen_dispatch.py", "manifest.json"):
             assert os.path.exists(os.path.join(d, f)), "%s/%s missing" % (op, f)
 
 
@@ -100,10 +102,25 @@ def test_compiled_route_agrees_with_select_w8a16(fmt):
             assert capi.route(fmt, M, N, K) == (r["tag"] if r else ""), (M, N, K, fmt)
 
 
+def test_compiled_route_agrees_with_select_gate_up():
+    from cuda_tempiler_amd import capi
+
+    s16, s8 = _select("gemm_fp16"), _select("gemm_w8a16")
+    for (N, K) in SWEEP_NK:
+        for M in SWEEP_M:
+            r = s16.select_gate_up("gemm_gate_up", M, N, K)
+            assert capi.route(3, M, N, K) == (r["tag"] if r else ""), (M, N, K)
+            for fmt in (1, 2):
+                r = s8.select_gate_up("gemm_w8a16_gate_up", M, N, K, fmt=fmt, group=128)
+                assert capi.route(3 + fmt, M, N, K) == (r["tag"] if r else ""), (M, N, K, fmt)
+    assert capi.route(3, 64, 17408, 5120) == ""  # prefill: the caller's own path
+
+
 def test_route_unknown_op_is_empty():
     from cuda_tempiler_amd import capi
 
     assert capi.route(7, 64, 64, 64) == ""
+    assert capi.route(6, 1, 64, 64) == ""
 
 
 def test_rows_fall_through_when_the_first_row_does_not_fit():

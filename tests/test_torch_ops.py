@@ -95,3 +95,22 @@ def test_linear_bias_is_added_after_the_product(tops):
     want = torch.nn.functional.linear(x, lin.weight) + lin.bias
     assert torch.equal(got, want)
     assert torch.allclose(got.float(), lin(x).float(), atol=2e-3, rtol=2e-3)
+
+
+def test_gate_up_fallback_is_silu_times_up(tops, monkeypatch):
+    x = torch.randn(2, 3, 64, dtype=torch.float16)
+    w = torch.randn(2 * 40, 64, dtype=torch.float16)
+    y = torch.ops.tempo.linear_gate_up_fp16(x, w)
+    g, u = torch.nn.functional.linear(x, w).chunk(2, dim=-1)
+    assert y.shape == (2, 3, 40)
+    assert torch.equal(y, torch.nn.functional.silu(g) * u)
+    assert tops.counters() == {"off": 1}
+    monkeypatch.setenv("TEMPO_KERNELS", "1")
+    assert torch.equal(torch.ops.tempo.linear_gate_up_fp16(x, w), y)  # host tensors: fallback
+    assert tops.counters() == {"off": 1, "fallback": 1}
+    torch.library.opcheck(torch.ops.tempo.linear_gate_up_fp16, (x, w))
+    q = torch.randint(-127, 128, (80, 64), dtype=torch.int8)
+    s = torch.rand(80, dtype=torch.float16) / 127
+    y8 = torch.ops.tempo.linear_gate_up_w8a16(x, q, s, None, 1, 128)
+    g8, u8 = torch.nn.functional.linear(x, tops.dequantize(q, s, None, 1)).chunk(2, dim=-1)
+    assert torch.equal(y8, torch.nn.functional.silu(g8) * u8)
