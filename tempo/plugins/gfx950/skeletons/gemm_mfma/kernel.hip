@@ -294,16 +294,11 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void k_gemm_dma(
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int TM = WTM / MS, TN = WTN / MS;
   constexpr int KS = BK / MF::KSTEP;
-  constexpr int A_BLKS = BM / RPB, B_BLKS = BN / RPB;  // 1 KiB DMA blocks per stage
-  constexpr int A_BLK = (A_BLKS + NW - 1) / NW;  // DMA instructions per wave per stage (at most)
-  constexpr int B_BLK = (B_BLKS + NW - 1) / NW;
-  constexpr bool EVEN = A_BLKS % NW == 0 && B_BLKS % NW == 0;
+  constexpr int A_BLK = BM / RPB / NW;  // DMA instructions per wave per stage
+  constexpr int B_BLK = BN / RPB / NW;
   constexpr int L = A_BLK + B_BLK;
   constexpr int STAGE_ELEMS = (BM + BN) * BK;
-  static_assert(BM % RPB == 0 && BN % RPB == 0, "whole DMA blocks");
-  // With an uneven split some waves issue one block less; the explicit waits then only stay
-  // exact where every wait is vmcnt(0): two stages, no cross-tile pipelining.
-  static_assert(EVEN || (STAGES == 2 && XT == 0), "uneven DMA split needs STAGES = 2, XT = 0");
+  static_assert(BM % (RPB * NW) == 0 && BN % (RPB * NW) == 0, "DMA blocks per wave");
   static_assert(STAGES >= 2 && (STAGES - 2 + XT) * L < 64, "stages / vmcnt range");
   static_assert(WTM % MS == 0 && WTN % MS == 0 && BK % MF::KSTEP == 0, "tile shape");
 
@@ -326,13 +321,13 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void k_gemm_dma(
     const int rin = lane / CPR, phys = lane % CPR;
 #pragma unroll
     for (int i = 0; i < A_BLK; ++i) {
-      const int row = min(i * NW + wave, A_BLKS - 1) * RPB + rin;  // clamp: unissued blocks
+      const int row = (i * NW + wave) * RPB + rin;
       const int c = lds_chunk<BK, SWZ>(row, phys);  // involution: logical chunk of slot `phys`
       srcA[i] = A + (long)min(m0 + row, M - 1) * lda + c * 8;
     }
 #pragma unroll
     for (int i = 0; i < B_BLK; ++i) {
-      const int row = min(i * NW + wave, B_BLKS - 1) * RPB + rin;
+      const int row = (i * NW + wave) * RPB + rin;
       const int c = lds_chunk<BK, SWZ>(row, phys);
       srcB[i] = B + (long)(n0 + row) * ldb + c * 8;
     }
@@ -344,14 +339,12 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void k_gemm_dma(
     const int k0 = kt * BK;
 #pragma unroll
     for (int i = 0; i < A_BLK; ++i)
-      if (EVEN || i * NW + wave < A_BLKS)  // wave-uniform
-        __builtin_amdgcn_global_load_lds((void*)(srcA[i] + k0),
-                                         (lds_void_t*)(sa + (i * NW + wave) * RPB * BK), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((void*)(srcA[i] + k0),
+                                       (lds_void_t*)(sa + (i * NW + wave) * RPB * BK), 16, 0, 0);
 #pragma unroll
     for (int i = 0; i < B_BLK; ++i)
-      if (EVEN || i * NW + wave < B_BLKS)
-        __builtin_amdgcn_global_load_lds((void*)(srcB[i] + k0),
-                                         (lds_void_t*)(sb + (i * NW + wave) * RPB * BK), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((void*)(srcB[i] + k0),
+                                       (lds_void_t*)(sb + (i * NW + wave) * RPB * BK), 16, 0, 0);
   };
 
   typename MF::acc_t acc[TM][TN];
