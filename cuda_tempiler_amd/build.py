@@ -38,6 +38,7 @@ INCLUDES = [
 ]
 UNITS = [
     os.path.join(SHIPPED, "gemm_fp16", "gfx950", "launch.hip"),
+    os.path.join(SHIPPED, "gemm_fp16", "gfx950", "launch_prefill.hip"),
     os.path.join(SHIPPED, "gemm_w8a16", "gfx950", "launch.hip"),
     os.path.join(HERE, "csrc", "fmha.hip"),
     os.path.join(HERE, "csrc", "gptq.hip"),
@@ -53,7 +54,10 @@ def regenerate() -> None:
     ship.write_all()
     for op in ("gemm_fp16", "gemm_w8a16"):
         d = os.path.join(SHIPPED, op, "gfx950")
-        for name, args in (("dispatch.inc", []), ("dispatch_gate_up.inc", ["--gate-up"])):
+        gens = [("dispatch.inc", []), ("dispatch_gate_up.inc", ["--gate-up"])]
+        if op == "gemm_fp16":
+            gens.append(("prefill.inc", ["--prefill"]))
+        for name, args in gens:
             text = subprocess.run([sys.executable, os.path.join(d, "gen_dispatch.py")] + args,
                                   check=True, capture_output=True, text=True).stdout
             path = os.path.join(d, name)
@@ -62,10 +66,23 @@ def regenerate() -> None:
                     f.write(text)
 
 
+def unit_flags(src: str) -> list:
+    """Flags a translation unit declares for itself ("// tempo:flags ..." in its first 40
+    lines): launch_prefill.hip asks for the register-pressure-minimising scheduler."""
+    out = []
+    with open(src, encoding="utf-8") as f:
+        for i, line in enumerate(f):
+            if i >= 40:
+                break
+            if line.startswith("// tempo:flags "):
+                out += line[len("// tempo:flags "):].split()
+    return out
+
+
 def _compile(src: str) -> str:
     name = os.path.relpath(src, ROOT).replace(os.sep, "_").replace(".hip", ".o")
     obj = os.path.join(BUILD, name)
-    cmd = [HIPCC] + FLAGS + INCLUDES + ["-c", src, "-o", obj]
+    cmd = [HIPCC] + FLAGS + unit_flags(src) + INCLUDES + ["-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError("hipcc failed on %s:\n%s\n%s" % (src, " ".join(cmd), r.stderr[-6000:]))

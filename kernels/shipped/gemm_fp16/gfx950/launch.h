@@ -144,6 +144,12 @@ inline hipError_t launch_dma(const GemmParams& p, hipStream_t s) {
   return hipGetLastError();
 }
 
+// The interleaved prefill kernel (k_gemm_ilv) lives in its own translation unit,
+// launch_prefill.hip, compiled with the register-pressure-minimising scheduler; its launchers
+// are instantiated there for the rows of the ladder (prefill.inc, generated from select.py).
+template <int BM, int BN, int BK, int WM, int WN, int STAGES, int GROUP, int XCD, int RSP>
+hipError_t launch_ilv(const GemmParams& p, hipStream_t s);
+
 // Applicability predicate.  false = the shape is not covered and the caller must take its own
 // path.  Dense row-major operands with 16-byte aligned rows; the band's divisibility is
 // checked again by the ladder in dispatch.inc.

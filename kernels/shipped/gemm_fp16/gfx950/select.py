@@ -12,7 +12,8 @@ through to the next one, so a narrower row can sit in front of a general one.)
               B).  A = 1 stages the activations in LDS once per workgroup (M = 1).  "shared"
               (k_stream_sh) lets SN slab waves share one LDS copy of each activation stage, which
               pays where N leaves enough slabs to fill the part (wide N).
-  * M >  32   mfma / dma: LDS-tiled MFMA kernels (dma = LDS-DMA copies), tile chosen by M.
+  * M >  32   mfma / ilv: LDS-tiled MFMA kernels, tile chosen by M.  ilv = the interleaved
+              4-wave kernel (128 x 128 wave tiles, LDS-DMA copies, hand-pipelined substeps).
 """
 
 ARCH = "gfx950"
@@ -26,8 +27,8 @@ LADDER = [
     (32, 0, "s32r1u4", "stream", dict(MB=2, R=1, U=4, A=0)),
     (256, 0, "m128x128k64", "mfma",
      dict(BM=128, BN=128, BK=64, WM=2, WN=2, MS=32, SWZ=1, GROUP=8, XCD=1)),
-    (1 << 30, 0, "d256x256k64w16m16", "dma",
-     dict(BM=256, BN=256, BK=64, WM=4, WN=4, STAGES=2, SWZ=2, GROUP=8, XCD=1, MS=16)),
+    (1 << 30, 0, "i256x256k64w4r8", "ilv",
+     dict(BM=256, BN=256, BK=64, WM=2, WN=2, STAGES=2, GROUP=8, XCD=1, RSP=8)),
 ]
 
 # Fused gate/up ladder (C = silu(A.B[0..N)^T) * (A.B[N..2N)^T), N = output width): the decode
@@ -57,6 +58,8 @@ def _fits_gate_up(kind, p, M, N, K):
 
 
 def _fits(kind, p, M, N, K):
+    if kind == "ilv":
+        return N % p["BN"] == 0 and K % max(64, p["BK"]) == 0
     if kind == "stream":
         return N % (STREAM_N_ROWS * p["R"]) == 0 and K % (STREAM_K_STEP * p["U"]) == 0
     if kind == "shared":

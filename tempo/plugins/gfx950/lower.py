@@ -32,6 +32,9 @@ CAPABILITIES = frozenset({
 
 # kernel symbol, template-parameter order, and argument list, per kind: the emitter's only data
 _ENTRY = {
+    "ilv": ("k_gemm_ilv", ("BM", "BN", "BK", "WM", "WN", "STAGES", "GROUP", "XCD", "RSP"),
+            "const _Float16*, const _Float16*, _Float16*, int, int, int, int, int, int",
+            ("common/cdna4.h", "gemm_mfma/kernel.hip", "gemm_mfma/ilv.hip")),
     "dma": ("k_gemm_dma", ("BM", "BN", "BK", "WM", "WN", "STAGES", "SWZ", "GROUP", "XCD", "XT",
                            "MINB", "MS"),
             "const _Float16*, const _Float16*, _Float16*, int, int, int, int, int, int",
@@ -48,6 +51,11 @@ _ENTRY = {
                ("common/cdna4.h", "gemv_stream/kernel.hip")),
 }
 NAMESPACE = "tempo::gen"
+# compiler flags a kind needs beyond the toolchain's own; render() writes them into the source as
+# a "// tempo:flags ..." line, which the toolchain (and the library build) read back.  The
+# interleaved kernel keeps its accumulator tuples in place only under the register-pressure-
+# minimising pre-RA scheduler (the skeleton's header says why).
+KIND_FLAGS = {"ilv": ("-mllvm", "-amdgpu-sched-strategy=iterative-minreg")}
 # trailing template parameters with a default in the skeleton: named only when the hyperform
 # sets them (EPI = 1 is the fused gate/up epilogue of the decode kernels)
 _OPTIONAL = frozenset({"EPI"})
@@ -110,6 +118,16 @@ class Gfx950Skeletons:
         kind = p["kind"]
         if kind == "stream" and p.get("EPI"):
             p = dict(p, R=2 * p["R"])  # each wave carries the gate and the up row groups
+        if kind == "ilv":
+            tm, tn = p["BM"] // p["WM"] // 16, p["BN"] // p["WN"] // 16
+            acc = tm * tn * 4
+            frags = 2 * (tm + tn) * 4
+            nw = p["WM"] * p["WN"]
+            L = (p["BM"] + p["BN"]) // (1024 // (p["BK"] * 2) * nw)
+            regs = acc + frags + 2 * L + 16  # + 64-bit copy sources, offsets
+            # pessimistic edge: the epilogue converts every accumulator (acc held twice when the
+            # budget allows it)
+            return regs, max(int(regs * 1.2), 2 * acc + 16), space.lds_bytes(kind, p)
         if kind in ("dma", "reg"):
             ms = p.get("MS", 32)
             nacc = 16 if ms == 32 else 4
@@ -157,7 +175,7 @@ class Gfx950Skeletons:
         M, N = int(op.shapes["M"]), int(op.shapes["N"])
         kind = p["kind"]
         minb, bound = 1, 0
-        if kind in ("dma", "reg"):
+        if kind in ("dma", "reg", "ilv"):
             grid = -(-M // p["BM"]) * (N // p["BN"])
             threads = p["WM"] * p["WN"] * 64
             minb = p.get("MINB", 1) if kind == "dma" else 1
@@ -189,8 +207,8 @@ class Gfx950Skeletons:
         per_cu = max(1, occ.ctas_per_sm)
         rounds = -(-lau.grid_ctas // (int(_M.rate("GEOM.SMS").value) * per_cu))
         atoms = []
-        if kind in ("dma", "reg"):
-            ms = p.get("MS", 32)
+        if kind in ("dma", "reg", "ilv"):
+            ms = p.get("MS", 32) if kind != "ilv" else 16
             tm, tn = p["BM"] // p["WM"] // ms, p["BN"] // p["WN"] // ms
             ks = p["BK"] // (16 if ms == 32 else 32)
             nw = p["WM"] * p["WN"]
@@ -215,7 +233,8 @@ class Gfx950Skeletons:
                               footprint={"LDS": float(lds_rd * reps)},
                               latency=_M.rate("LATENCY.LDS").value))
         atoms.append(Atom(uid=2, kind=AtomKind.XFER_ISSUE,
-                          op_id="global_load_lds_dwordx4" if kind in ("dma", "ring") else "global_load_dwordx4",
+                          op_id=("global_load_lds_dwordx4" if kind in ("dma", "ring", "ilv")
+                                 else "global_load_dwordx4"),
                           footprint={"VMEM": float(vmem * reps)},
                           latency=_M.rate("LATENCY.VMEM").value, token="copy"))
         atoms.append(Atom(uid=3, kind=AtomKind.XFER_WAIT, op_id="s_waitcnt vmcnt", footprint={},
@@ -237,8 +256,11 @@ class Gfx950Skeletons:
             with open(os.path.join(SKEL, f), encoding="utf-8") as fh:
                 body.append("// ===== %s =====\n%s\n" % (f, fh.read()))
         head = ("// GENERATED by tempo: plugin gfx950, hyperform %s, operation %s %sx%sx%s.\n"
-                "#include <hip/hip_runtime.h>\n#include <stdint.h>\n\nnamespace tempo {\nnamespace gen {\n\n"
                 % (h.key, op.kind, op.shapes.get("M"), op.shapes.get("N"), op.shapes.get("K")))
+        if kind in KIND_FLAGS:
+            head += "// tempo:flags %s\n" % " ".join(KIND_FLAGS[kind])
+        head += ("#include <hip/hip_runtime.h>\n#include <stdint.h>\n\nnamespace tempo {\n"
+                 "namespace gen {\n\n")
         inst = ("\n// explicit instantiation: the one kernel this file exists to contain\n"
                 "template __global__ void %s<%s>(%s);\n"
                 % (sym, ", ".join(str(int(p[k])) for k in order), args))

@@ -28,6 +28,8 @@ ROOT = os.path.abspath(os.path.join(HERE, "..", "..", ".."))
 SHIPPED = os.path.join(ROOT, "kernels", "shipped")
 SIGNED = ("kernel.hip", "launch.h", "launch.hip", "dispatch.inc", "dispatch_gate_up.inc",
           "select.py")
+# files only some deliveries have (gemm_fp16's prefill translation unit); signed when present
+SIGNED_OPTIONAL = ("launch_prefill.hip", "prefill.inc")
 
 OPS = {
     "gemm_fp16": dict(dtype="fp16 x fp16 -> fp16, fp32 accumulate",
@@ -49,10 +51,15 @@ def _select(op):
 def md5_of(op):
     d = os.path.join(SHIPPED, op, "gfx950")
     h = hashlib.md5()
-    for f in SIGNED:
+    for f in signed_files(op):
         with open(os.path.join(d, f), "rb") as fh:
             h.update(f.encode() + b"\0" + fh.read())
     return h.hexdigest()
+
+
+def signed_files(op):
+    d = os.path.join(SHIPPED, op, "gfx950")
+    return list(SIGNED) + [f for f in SIGNED_OPTIONAL if os.path.exists(os.path.join(d, f))]
 
 
 def ladder_rows(sel):
@@ -65,12 +72,12 @@ def ladder_rows(sel):
 def hyper_params(kind, p, fmt, epi=0):
     """A ladder row of select.py (kind, template params) -> the plugin's hyperform params: the
     same kernel, named the way space.variants() names it."""
-    pk = {"stream": "stream", "mfma": "reg", "dma": "dma", "shared": "shared"}[kind]
+    pk = {"stream": "stream", "mfma": "reg", "dma": "dma", "shared": "shared", "ilv": "ilv"}[kind]
     params = {k: v for k, v in p.items() if k != "fmts"}
     params["kind"] = pk
     if pk == "shared":
         params.setdefault("TPB", 1024)
-    if pk != "dma":
+    if pk not in ("dma", "ilv"):
         params["BFMT"] = fmt
     if pk == "stream":
         params["ALDS"] = params.pop("A", 0)
@@ -226,7 +233,7 @@ def make(op, rows_files=()):
         "build": build_numbers(op),
         "gate": gate_numbers(op),
         "source_md5": md5_of(op),
-        "source_md5_of": list(SIGNED),
+        "source_md5_of": signed_files(op),
         "rows": old.get("rows", []),
         "card": old.get("card", None),
     }
@@ -240,6 +247,8 @@ def make(op, rows_files=()):
             spw = p["SN"] // 2 if epi else p["SN"]
             fit = "N %% %d == 0 and K %% %d == 0" % (sel.STREAM_N_ROWS * p["R"] * spw,
                                                     sel.STREAM_K_STEP * p["U"])
+        elif kind == "ilv":
+            fit = "N %% %d == 0 and K %% %d == 0" % (p["BN"], max(64, p["BK"]))
         else:
             fit = "N %% %d == 0 and K %% %d == 0" % (p["BN"], p["BK"])
         man["dispatch" if not epi else "dispatch_gate_up"].append(dict(

@@ -1,0 +1,196 @@
+// gemm_mfma/ilv.hip -- the interleaved prefill GEMM (fp16 x fp16).  Uses the tile machinery of
+// gemm_mfma/kernel.hip (lds_chunk, tile_of, s_wait_vm, lds_void_t), which must come first.
+// ============================================================================================
+// k_gemm_ilv -- fp16 B only, prefill: one wave per SIMD, large wave tiles, and a main loop that
+// is software-pipelined by hand ("interleaved").
+//
+// Each wave owns a (BM/WM) x (BN/WN) tile of C (128 x 128 for the shipped 256 x 256 / 4-wave
+// row: 256 fp32 accumulators per lane, all in AGPRs), so every fragment byte read from LDS feeds
+// twice the MFMAs it does in a 64 x 64 wave tile: LDS traffic per flop is halved, which is what
+// the power-limited matrix cores of this part spend their budget on besides the MFMAs.
+//
+// Substep = 32 k (one v_mfma_f32_16x16x32_f16 per 16 x 16 block of the wave tile).  A substep
+// issues its TM*TN MFMAs on the fragments read during the previous substep, and between them
+// (in CH chunks fenced by sched_barrier) the LDS reads of the next substep's fragments -- in the
+// first RSP chunks, so they have landed long before they are needed -- and, in the substep that
+// holds the tile barrier, the LDS-DMA copies that refill the stage the barrier has just freed.
+// One barrier per k-tile; no MFMA ever waits on an LDS read issued in the same substep.
+//
+// Stage of tile t = t % STAGES.  The barrier of tile t (in its last substep) is passed once
+// every wave has finished reading tile t (lgkmcnt 0) and its own copies of tile t+1 have landed
+// (vmcnt); after it tile t+1 is readable by all and stage t % STAGES is refilled with tile
+// t + STAGES.  Past the last tile the refill re-copies tile NT-1 into a stage nobody reads again
+// and the last substep reads fragments it does not use: the loop body stays one straight-line
+// region, so the interleave holds from the first tile to the last.  Those copies are younger
+// than every copy a later wait counts, so the vmcnt arithmetic is unchanged, and the kernel
+// drains them (vmcnt 0) before the epilogue, so no copy lands after the workgroup has left.
+//
+// Requirements (applicable() + the ladder): N % BN == 0, K % 64 == 0 (an even number of
+// substeps), 16-byte aligned rows.  M is predicated: A rows past M-1 are re-read from row M-1
+// and never stored.
+//
+// Build: this kernel is compiled with -mllvm -amdgpu-sched-strategy=iterative-minreg (its own
+// translation unit).  The default pre-RA scheduler reorders the 256 accumulator chains of a
+// 128 x 128 wave tile such that the register allocator no longer keeps each accumulator in one
+// AGPR tuple, and the loop fills with v_accvgpr_read/write/mov copies.
+// ============================================================================================
+template <int BM, int BN, int BK, int WM, int WN, int STAGES, int GROUP, int XCD, int RSP>
+__global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv(
+    const _Float16* __restrict__ A, const _Float16* __restrict__ B, _Float16* __restrict__ C,
+    int M, int N, int K, int lda, int ldb, int ldc) {
+  using MF = Mfma<16>;
+  constexpr int SWZ = 2;
+  constexpr int NW = WM * WN;
+  constexpr int CPR = BK / 8;                 // 16-byte chunks per tile row
+  constexpr int RPB = 1024 / (BK * 2);        // tile rows per 1 KiB copy block
+  constexpr int R256 = BK * 2 >= 256 ? 1 : 256 / (BK * 2);  // rows per SWZ 2 key step
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int TM = WTM / 16, TN = WTN / 16;
+  constexpr int KS = BK / 32;                 // substeps per k-tile
+  constexpr int A_BLK = BM / RPB / NW, B_BLK = BN / RPB / NW;
+  constexpr int L = A_BLK + B_BLK;            // copies per wave per k-tile
+  constexpr int STAGE = (BM + BN) * BK;
+  constexpr int NMF = TM * TN, NR = TM + TN;  // MFMAs and fragment reads per substep
+  constexpr int CH = NR > L ? NR : L;
+  constexpr int RSPAN = RSP > 0 && RSP < CH ? RSP : CH;
+  static_assert(BM % (RPB * NW) == 0 && BN % (RPB * NW) == 0, "copy blocks per wave");
+  static_assert(STAGES >= 2 && (STAGES - 1) * L < 64, "stages / vmcnt range");
+  static_assert(WTM % 16 == 0 && WTN % 16 == 0 && (KS == 1 || KS == 2), "tile shape");
+  // rows 16 apart (fragment blocks) and NW*RPB apart (copy blocks) share the swizzle key, so
+  // one per-lane offset serves every block of an operand
+  static_assert((16 / R256) % CPR == 0 && (NW * RPB / R256) % CPR == 0, "swizzle periods");
+
+  __shared__ __attribute__((aligned(1024))) _Float16 smem[STAGES * STAGE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+
+  const int nm = (M + BM - 1) / BM, nn = N / BN;
+  int tmi, tni;
+  tile_of<GROUP, XCD>(blockIdx.x, nm, nn, tmi, tni);
+  const int m0 = tmi * BM, n0 = tni * BN;
+
+  // Copy d of this wave fills 1 KiB block (ib*NW + wave) of the A (d < A_BLK) or B tile; lane l
+  // fetches the 16-byte chunk that belongs at LDS slot l (the swizzle is an involution).
+  const int crow = wave * RPB + lane / CPR;                       // tile row of block ib = 0
+  const int cchunk = lds_chunk<BK, SWZ>(crow, lane % CPR) * 8;    // element offset in the row
+  const _Float16* srcB0 = B + (long)(n0 + crow) * ldb + cchunk;
+  auto dma = [&](int kt, int ksrc, int d) {
+    const bool isA = d < A_BLK;
+    const int ib = isA ? d : d - A_BLK;
+    _Float16* dst = smem + (kt % STAGES) * STAGE + (isA ? 0 : BM * BK) + (ib * NW + wave) * RPB * BK;
+    const _Float16* g =
+        isA ? A + (long)min(m0 + crow + ib * NW * RPB, M - 1) * lda + cchunk
+            : srcB0 + (long)ib * NW * RPB * ldb;
+    __builtin_amdgcn_global_load_lds((void*)(g + ksrc * BK), (lds_void_t*)dst, 16, 0, 0);
+  };
+
+  typename MF::acc_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[i][j][v] = 0.f;
+
+  const int fr = lane % 16, fk = lane / 16;
+  int aOff[KS], bOff[KS];  // fragment offsets (elements) inside a stage, per substep
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    const int ra = wm * WTM + fr, rb = wn * WTN + fr;
+    aOff[ks] = ra * BK + lds_chunk<BK, SWZ>(ra, ks * 4 + fk) * 8;
+    bOff[ks] = BM * BK + rb * BK + lds_chunk<BK, SWZ>(rb, ks * 4 + fk) * 8;
+  }
+
+  f16x8 fa[2][TM], fb[2][TN];
+  // One substep on fragment buffer bb: read the next substep (tile rkt, substep rks) into bb^1,
+  // refill (DMA) the stage of tile dkt with k-tile dsrc, and run the MFMAs on bb.
+  auto substep = [&](auto bufc, auto dmac, int rkt, int rks, int dkt, int dsrc) {
+    constexpr int bb = decltype(bufc)::value;
+    constexpr bool DMA = decltype(dmac)::value;
+    const _Float16* s = smem + (rkt % STAGES) * STAGE;
+#pragma unroll
+    for (int q = 0; q < CH; ++q) {
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        if (r * RSPAN / NR != q) continue;
+        if (r < TM)
+          fa[bb ^ 1][r] = *reinterpret_cast<const f16x8*>(s + aOff[rks] + r * 16 * BK);
+        else
+          fb[bb ^ 1][r - TM] = *reinterpret_cast<const f16x8*>(s + bOff[rks] + (r - TM) * 16 * BK);
+      }
+      if constexpr (DMA) {
+#pragma unroll
+        for (int d = 0; d < L; ++d)
+          if (d * CH / L == q) dma(dkt, dsrc, d);
+      }
+#pragma unroll
+      for (int t = q * NMF / CH; t < (q + 1) * NMF / CH; ++t)
+        acc[t / TN][t % TN] = MF::run(fb[bb][t % TN], fa[bb][t / TN], acc[t / TN][t % TN]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  const int NT = K / BK;
+  const int NU = NT * KS;  // substeps (even: K % 64 == 0)
+  auto step = [&](auto bufc, auto barc, int u) {
+    constexpr bool BAR = decltype(barc)::value;
+    const int kt = KS == 1 ? u : u >> 1;
+    asm volatile("" ::: "memory");
+    if constexpr (BAR) {
+      // this wave's reads of tile kt are done and its copies of tile kt+1 have landed ...
+      s_wait_vm<(STAGES - 2) * L>();
+      // ... and everyone's: tile kt+1 is readable, stage kt % STAGES is free
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      substep(bufc, IC<true>{}, kt + 1, 0, kt + STAGES, min(kt + STAGES, NT - 1));
+    } else {
+      // this substep's fragments were read in the first chunks of the previous one: the wait
+      // is free, and placing it here keeps the compiler from waiting after this substep's
+      // first reads instead
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+      asm volatile("" ::: "memory");
+      substep(bufc, IC<false>{}, kt, 1, 0, 0);
+    }
+  };
+
+  // prologue: every stage in flight, tile 0 landed and visible, its first fragments read
+#pragma unroll
+  for (int s = 0; s < STAGES; ++s)
+#pragma unroll
+    for (int d = 0; d < L; ++d) dma(s, min(s, NT - 1), d);
+  asm volatile("" ::: "memory");
+  s_wait_vm<(STAGES - 1) * L>();
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < TM; ++i) fa[0][i] = *reinterpret_cast<const f16x8*>(smem + aOff[0] + i * 16 * BK);
+#pragma unroll
+  for (int j = 0; j < TN; ++j) fb[0][j] = *reinterpret_cast<const f16x8*>(smem + bOff[0] + j * 16 * BK);
+  __builtin_amdgcn_sched_barrier(0);
+
+  for (int u = 0; u < NU; u += 2) {
+    step(IC<0>{}, IC<KS == 1>{}, u);
+    step(IC<1>{}, IC<true>{}, u + 1);
+  }
+  s_wait_vm<0>();  // the refills past the end land before the workgroup's LDS is released
+
+  // ---- epilogue: each lane owns 4 consecutive n of one m per MFMA block ---------------------
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int m = m0 + wm * WTM + i * 16 + fr;
+    if (m >= M) continue;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int n = n0 + wn * WTN + j * 16 + 4 * fk;
+      f16x4 o;
+      o[0] = (_Float16)acc[i][j][0];
+      o[1] = (_Float16)acc[i][j][1];
+      o[2] = (_Float16)acc[i][j][2];
+      o[3] = (_Float16)acc[i][j][3];
+      *reinterpret_cast<f16x4*>(C + (long)m * ldc + n) = o;
+    }
+  }
+}

@@ -1,6 +1,8 @@
 """gfx950: SEARCH SPACE -- axes and legal hyperforms (reference pattern tempo/plugins/sm70/space.py).
 
-Four skeleton kinds, each a kernel family of tempo/plugins/gfx950/skeletons:
+Five skeleton kinds, each a kernel family of tempo/plugins/gfx950/skeletons:
+  ilv     gemm_mfma/k_gemm_ilv      fp16 x fp16, one wave per SIMD, large wave tiles, LDS-DMA
+                                    copies and fragment reads interleaved with the MFMAs by hand
   dma     gemm_mfma/k_gemm_dma      fp16 x fp16, LDS-DMA multi-stage pipeline (prefill, M > 32)
   reg     gemm_mfma/k_gemm          any weight format, register-staged copy that can dequantise
                                     on the way into LDS (W8A16 prefill, fp16 fallback)
@@ -35,6 +37,8 @@ AXES = (
 )
 
 DOMAINS = {
+    "ilv": dict(BM=(128, 256), BN=(128, 192, 256), BK=(32, 64), STAGES=(2, 3, 4), GROUP=(4, 8, 16),
+                XCD=(0, 1), WAVES=((2, 2), (2, 4), (4, 2)), RSP=(0, 8, 12)),
     "dma": dict(BM=(128, 256), BN=(128, 192, 256), BK=(32, 64), STAGES=(2, 3, 4), SWZ=(0, 1, 2),
                 GROUP=(4, 8, 16), XCD=(0, 1), WAVES=((2, 2), (2, 4), (4, 2), (4, 4)), MS=(16, 32)),
     "reg": dict(BM=(64, 128, 256), BN=(128, 256), BK=(64,), MS=(16, 32), SWZ=(1, 2), GROUP=(8,),
@@ -56,7 +60,7 @@ def bfmt(op: OpSpec) -> int:
 
 
 def lds_bytes(kind: str, p: dict) -> int:
-    if kind == "dma":
+    if kind in ("dma", "ilv"):
         return p["STAGES"] * (p["BM"] + p["BN"]) * p["BK"] * 2
     if kind == "reg":
         return 2 * (p["BM"] + p["BN"]) * p["BK"] * 2
@@ -107,6 +111,9 @@ def shared_split(N: int, K: int, MB: int, R: int, U: int, SN: int, TPB: int = 10
 
 
 def tag(kind: str, p: dict) -> str:
+    if kind == "ilv":
+        return "ilv_m%dn%dk%d_w%dx%d_s%d_g%d_x%d_r%d" % (
+            p["BM"], p["BN"], p["BK"], p["WM"], p["WN"], p["STAGES"], p["GROUP"], p["XCD"], p["RSP"])
     if kind == "dma":
         return "dma_m%dn%dk%d_w%dx%d_s%d_z%d_g%d_x%d_f%d" % (
             p["BM"], p["BN"], p["BK"], p["WM"], p["WN"], p["STAGES"], p["SWZ"], p["GROUP"], p["XCD"],
@@ -123,6 +130,28 @@ def tag(kind: str, p: dict) -> str:
 
 def legal(kind: str, p: dict, M: int, N: int, K: int):
     """None when the hyperform compiles and launches for this shape, else the reason."""
+    if kind == "ilv":
+        BM, BN, BK, WM, WN = p["BM"], p["BN"], p["BK"], p["WM"], p["WN"]
+        if N % BN or K % max(64, BK):
+            return "tile %dx%d / even substep count does not divide N=%d / K=%d" % (BN, BK, N, K)
+        if BK not in (32, 64):
+            return "substeps per k-tile must be 1 or 2"
+        if (BM // WM) % 16 or (BN // WN) % 16:
+            return "wave tile not a multiple of 16"
+        rpb, nw = 1024 // (BK * 2), WM * WN
+        if BM % (rpb * nw) or BN % (rpb * nw):
+            return "copy blocks do not divide among waves"
+        r256 = 1 if BK * 2 >= 256 else 256 // (BK * 2)
+        if (16 // r256) % (BK // 8) or (nw * rpb // r256) % (BK // 8):
+            return "blocks do not share the swizzle key"
+        L = (BM + BN) // (rpb * nw)
+        if (p["STAGES"] - 1) * L >= 64:
+            return "vmcnt depth"
+        if nw * 64 > 1024:
+            return "more than 1024 lanes"
+        if lds_bytes(kind, p) > LDS_MAX:
+            return "LDS %d B > 160 KiB" % lds_bytes(kind, p)
+        return None
     if kind in ("dma", "reg"):
         BM, BN, BK = p["BM"], p["BN"], p["BK"]
         if N % BN or K % BK:
@@ -194,6 +223,18 @@ def variants(op: OpSpec) -> Iterator[Hyperform]:
                 for SN in DOMAINS["shared"]["SN"]:
                     out.append(("shared", dict(MB=MB, R=R, U=U, BFMT=b, SN=SN, TPB=1024)))
     if b == 0:
+        d = DOMAINS["ilv"]
+        for BM in d["BM"]:
+            for BN in d["BN"]:
+                for BK in d["BK"]:
+                    for ST in d["STAGES"]:
+                        for G in d["GROUP"]:
+                            for X in d["XCD"]:
+                                for (WM, WN) in d["WAVES"]:
+                                    for RS in d["RSP"]:
+                                        out.append(("ilv", dict(
+                                            BM=BM, BN=BN, BK=BK, WM=WM, WN=WN, STAGES=ST,
+                                            GROUP=G, XCD=X, RSP=RS)))
         d = DOMAINS["dma"]
         for BM in d["BM"]:
             for BN in d["BN"]:

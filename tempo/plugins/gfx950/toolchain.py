@@ -29,6 +29,19 @@ FLAGS = ["-O3", "-std=c++17", "--offload-arch=%s" % ARCH,
 _REMARK = re.compile(r"remark: ([^:]+):(\d+):\d+: (.+?) \[-Rpass-analysis")
 
 
+def source_flags(path) -> list:
+    """Extra compiler flags a source declares for itself: "// tempo:flags <flags>" lines in its
+    first 40 lines (the emitter writes one for kinds that need a particular scheduler)."""
+    out = []
+    with open(path, encoding="utf-8") as f:
+        for i, line in enumerate(f):
+            if i >= 40:
+                break
+            if line.startswith("// tempo:flags "):
+                out += line[len("// tempo:flags "):].split()
+    return out
+
+
 def parse_resource_remarks(text: str) -> dict:
     """{kernel symbol: {field: value}} from -Rpass-analysis=kernel-resource-usage output."""
     out, cur = {}, None
@@ -79,7 +92,8 @@ class Gfx950Toolchain:
         "exe" (link an executable)."""
         source, out = Path(source), Path(out)
         out.parent.mkdir(parents=True, exist_ok=True)
-        cmd = [HIPCC] + FLAGS + ["-Rpass-analysis=kernel-resource-usage"] + list(extra)
+        cmd = ([HIPCC] + FLAGS + source_flags(source) + ["-Rpass-analysis=kernel-resource-usage"]
+               + list(extra))
         if mode == "device":
             cmd += ["--cuda-device-only", "--no-gpu-bundle-output", "-c"]
         elif mode == "obj":

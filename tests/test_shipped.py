@@ -38,6 +38,25 @@ def test_dispatch_inc_is_generated_from_select(op, table):
         assert f.read() == text, "%s is stale: re-run the build" % table
 
 
+def test_prefill_inc_is_generated_from_select():
+    d = os.path.join(SHIPPED, "gemm_fp16", "gfx950")
+    text = subprocess.run([sys.executable, os.path.join(d, "gen_dispatch.py"), "--prefill"],
+                          check=True, capture_output=True, text=True).stdout
+    with open(os.path.join(d, "prefill.inc"), encoding="utf-8") as f:
+        assert f.read() == text, "prefill.inc is stale: re-run the build"
+    # every interleaved row of the ladder is instantiated there, and nothing else
+    rows = [r for r in _select("gemm_fp16").LADDER if r[3] == "ilv"]
+    assert rows and text.count("template hipError_t launch_ilv<") == len(rows)
+
+
+def test_prefill_unit_declares_its_scheduler():
+    from cuda_tempiler_amd import build
+
+    flags = build.unit_flags(os.path.join(SHIPPED, "gemm_fp16", "gfx950", "launch_prefill.hip"))
+    assert flags == ["-mllvm", "-amdgpu-sched-strategy=iterative-minreg"]
+    assert build.unit_flags(os.path.join(SHIPPED, "gemm_fp16", "gfx950", "launch.hip")) == []
+
+
 def test_frozen_kernels_match_skeletons():
     from tempo.plugins.gfx950 import ship
 
@@ -50,6 +69,8 @@ def test_delivery_layout():
         for f in ("kernel.hip", "launch.h", "launch.hip", "dispatch.inc", "dispatch_gate_up.inc",
                   "select.py", "gen_dispatch.py", "manifest.json"):
             assert os.path.exists(os.path.join(d, f)), "%s/%s missing" % (op, f)
+    for f in ("launch_prefill.hip", "prefill.inc"):
+        assert os.path.exists(os.path.join(SHIPPED, "gemm_fp16", "gfx950", f)), f
 
 
 def _declared():
@@ -133,7 +154,8 @@ def test_rows_fall_through_when_the_first_row_does_not_fit():
     assert capi.route(0, 1, 15360, 3840) == "s1a_r1u4"
     assert capi.route(1, 1, 5120, 5120) == "s1a_r1u8"
     assert capi.route(1, 1, 5120, 5376) == "s1a_r1u4"   # K % 512 != 0, K % 256 == 0
-    assert capi.route(0, 4096, 15360, 3840) == "d256x256k64w16m16"
+    assert capi.route(0, 4096, 15360, 3840) == "i256x256k64w4r8"
+    assert not capi.route(0, 4096, 15360, 3872)  # K % 64 != 0: no prefill row fits, fallback
 
 
 def test_gptq_repack_refuses_before_any_launch():
