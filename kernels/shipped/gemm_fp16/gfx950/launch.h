@@ -121,6 +121,60 @@ inline hipError_t launch_shared(const GemmParams& p, hipStream_t s) {
   return hipGetLastError();
 }
 
+// k split of the line kernel (k_stream_line): about `waves` waves over the part, at most 16 per
+// workgroup, every chunk whole steps of 128 k, the workgroup's rings (+ the fmt 2 metadata and the
+// reduction) within the 160 KiB of LDS.  false: no split fits (the caller's own path).
+template <class SL>
+inline bool line_split(int slabs, int K, int waves, int* S_out, int* chunk_out, int* G_out,
+                       size_t* lds_out) {
+  const int steps = K / 128;
+  int S = (waves + slabs - 1) / slabs;
+  if (S > 16) S = 16;
+  if (S > steps) S = steps;
+  if (S < 1) S = 1;
+  for (;; --S) {
+    const int per = (steps + S - 1) / S;  // steps per wave
+    const int s2 = (steps + per - 1) / per;
+    const size_t lds = SL::lds(s2, per);
+    if (lds <= 160 * 1024) {
+      *S_out = s2;
+      *chunk_out = per * 128;
+      *G_out = per;
+      *lds_out = lds;
+      return true;
+    }
+    if (S == 1) return false;
+  }
+}
+
+// The line kernel (whole-line nontemporal weight stream through per-wave LDS rings).  MB = 0:
+// M = 1; MB = 1 / 2: M <= 16 / 32.  EPI = 1: fused gate/up (p.N the output width, B 2N rows).
+template <int MB, int R, int D, int WAVES, int EPI = 0>
+inline hipError_t launch_line(const GemmParams& p, hipStream_t s) {
+  using SL = StreamLine<MB, R, D, 0, EPI>;
+  StreamArgs a;
+  a.A = p.A;
+  a.B = p.B;
+  a.scale = nullptr;
+  a.zero = nullptr;
+  a.C = p.C;
+  a.M = p.M;
+  a.N = p.N;
+  a.K = p.K;
+  a.lda = p.lda;
+  a.ldb = p.ldb;
+  a.ldc = p.ldc;
+  a.group = 0;
+  a.up = EPI ? p.N : 0;
+  int G = 0;
+  size_t lds = 0;
+  if (!line_split<SL>(p.N / (16 * R), p.K, WAVES, &a.S, &a.chunk, &G, &lds))
+    return hipErrorInvalidConfiguration;
+  hipLaunchKernelGGL((k_stream_line<MB, R, D, 0, EPI>), dim3(p.N / (16 * R)), dim3(64 * a.S), lds,
+                     s, a, G);
+  return hipGetLastError();
+}
+
 template <int BM, int BN, int BK, int WM, int WN, int MS, int SWZ, int GROUP, int XCD>
 inline hipError_t launch_mfma(const GemmParams& p, hipStream_t s) {
   const int nm = (p.M + BM - 1) / BM;

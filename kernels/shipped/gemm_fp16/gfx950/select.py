@@ -8,8 +8,9 @@ Rows are tried in order; the first row whose band holds (M, N) -- M <= M_max and
 AND whose kernel fits the shape (divisibility) is taken.  No such row: None, the caller's own
 path.  (The reference stops at the first band that holds M; here a row that does not fit falls
 through to the next one, so a narrower row can sit in front of a general one.)
-  * M <= 32   stream / shared: the weight-streaming decode kernels (HBM-bound; one pass over
-              B).  A = 1 stages the activations in LDS once per workgroup (M = 1).  "shared"
+  * M <= 32   line / stream / shared: the weight-streaming decode kernels (HBM-bound; one
+              pass over B).  line = whole 128-byte weight lines by nontemporal LDS-DMA into
+              per-wave rings (needs K % 128); stream / shared are its fallbacks.  A = 1 stages the activations in LDS once per workgroup (M = 1).  "shared"
               (k_stream_sh) lets SN slab waves share one LDS copy of each activation stage, which
               pays where N leaves enough slabs to fill the part (wide N).
   * M >  32   mfma / ilv: LDS-tiled MFMA kernels, tile chosen by M.  ilv = the interleaved
@@ -20,9 +21,12 @@ ARCH = "gfx950"
 
 # (M_max, N_min, tag, kind, template params).  First row that holds (M, N) and fits wins.
 LADDER = [
+    (1, 0, "l0r1d3", "line", dict(MB=0, R=1, D=3, W=2048)),
     (1, 0, "s1a_r1u4", "stream", dict(MB=1, R=1, U=4, A=1)),
+    (16, 0, "l1r1d3", "line", dict(MB=1, R=1, D=3, W=2048)),
     (16, 12288, "h16r1u4n4", "shared", dict(MB=1, R=1, U=4, SN=4)),
     (16, 0, "s16r1u4", "stream", dict(MB=1, R=1, U=4, A=0)),
+    (32, 0, "l2r2d2", "line", dict(MB=2, R=2, D=2, W=2048)),
     (32, 12288, "h32r1u4n4", "shared", dict(MB=2, R=1, U=4, SN=4)),
     (32, 0, "s32r1u4", "stream", dict(MB=2, R=1, U=4, A=0)),
     (256, 0, "m128x128k64", "mfma",
@@ -47,6 +51,8 @@ LADDER_GATE_UP = [
 # Divisibility each kind needs (checked at run time by dispatch.inc, mirrored here).
 STREAM_K_STEP = 64  # k per pipeline step of the stream kernel
 STREAM_N_ROWS = 16  # weight rows per MFMA row group (times R)
+LINE_K_STEP = 128   # k per step of the line kernel (one 128-byte line of an int8 row)
+LINE_K_MAX = 65536  # the line kernel's LDS holds one wave's metadata (fmt 2): bounded k
 
 
 def _fits_gate_up(kind, p, M, N, K):
@@ -58,6 +64,8 @@ def _fits_gate_up(kind, p, M, N, K):
 
 
 def _fits(kind, p, M, N, K):
+    if kind == "line":
+        return N % (STREAM_N_ROWS * p["R"]) == 0 and K % LINE_K_STEP == 0 and K <= LINE_K_MAX
     if kind == "ilv":
         return N % p["BN"] == 0 and K % max(64, p["BK"]) == 0
     if kind == "stream":

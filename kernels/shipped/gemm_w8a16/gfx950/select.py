@@ -15,6 +15,10 @@ FORMATS = (1, 2)
 # holds (M, N) -- M <= M_max and N >= N_min -- whose weight format is listed (params "fmts";
 # absent = both) and whose kernel fits the shape is taken.
 LADDER = [
+    (1, 0, "l0r1d4", "line", dict(MB=0, R=1, D=4, W=2048)),
+    (8, 0, "l1r1d4", "line", dict(MB=1, R=1, D=4, W=2048)),
+    (16, 0, "l1r2d4", "line", dict(MB=1, R=2, D=4, W=2048)),
+    (32, 0, "l2r2d3", "line", dict(MB=2, R=2, D=3, W=2048, fmts=(1,))),
     (1, 0, "s1a_r1u8", "stream", dict(MB=1, R=1, U=8, A=1)),
     (1, 0, "s1a_r1u4", "stream", dict(MB=1, R=1, U=4, A=1)),
     (8, 16384, "h8r1u2n2", "shared", dict(MB=1, R=1, U=2, SN=2, fmts=(1,))),
@@ -51,6 +55,8 @@ LADDER_GATE_UP = [
 
 STREAM_K_STEP = 64
 STREAM_N_ROWS = 16
+LINE_K_STEP = 128   # k per step of the line kernel (one 128-byte line of an int8 row)
+LINE_K_MAX = 65536  # the line kernel's LDS holds one wave's metadata (fmt 2): bounded k
 
 
 def _fits_gate_up(kind, p, M, N, K):
@@ -62,6 +68,8 @@ def _fits_gate_up(kind, p, M, N, K):
 
 
 def _fits(kind, p, M, N, K):
+    if kind == "line":
+        return N % (STREAM_N_ROWS * p["R"]) == 0 and K % LINE_K_STEP == 0 and K <= LINE_K_MAX
     if kind == "stream":
         return N % (STREAM_N_ROWS * p["R"]) == 0 and K % (STREAM_K_STEP * p["U"]) == 0
     if kind == "shared":

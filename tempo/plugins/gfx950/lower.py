@@ -43,6 +43,8 @@ _ENTRY = {
             "const _Float16*, const void*, const _Float16*, const uint8_t*, _Float16*, int, int, "
             "int, int, int, int, int",
             ("common/cdna4.h", "gemm_mfma/kernel.hip")),
+    "line": ("k_stream_line", ("MB", "R", "D", "BFMT", "EPI"), "StreamArgs, int",
+             ("common/cdna4.h", "gemv_stream/kernel.hip")),
     "ring": ("k_stream_dma", ("MB", "R", "D", "BFMT"), "StreamArgs",
              ("common/cdna4.h", "gemv_stream/kernel.hip")),
     "stream": ("k_stream", ("MB", "R", "U", "BFMT", "ALDS", "EPI"), "StreamArgs",
@@ -146,6 +148,17 @@ class Gfx950Skeletons:
             # fp16 conversion, so when the budget allows it the compiler holds acc twice
             return regs, max(int(regs * 1.2), 2 * acc + 16), space.lds_bytes(kind, p)
         wb = 2 if p["BFMT"] == 0 else 1
+        if kind == "line":
+            rr = 2 * p["R"] if p.get("EPI") else p["R"]
+            mbe = max(1, p["MB"])
+            # fragments of one step (2 halves x (2 per row group for fp16, 1 for 8-bit) + the
+            # activation fragments), two accumulator chains, the fp16 expansion of 8-bit
+            # weights, 64-bit copy sources, scales / zero-points
+            regs = (2 * rr * (2 if wb == 2 else 1) * 4 + 2 * mbe * 2 * 4 + 2 * rr * mbe * 4
+                    + (8 * rr if p["BFMT"] else 0) + 2 * (2 * rr + (4 * p["MB"] if p["MB"] else 1))
+                    + 2 * rr + 16)
+            sp = space.line_split(int(op.shapes["N"]), int(op.shapes["K"]), p)
+            return regs, int(regs * 1.25), (sp[2] if sp else space.LDS_MAX + 1)
         S, _ = self._split(op, p)
         if kind == "shared":
             # weights double-buffered (U steps x R slabs x 4*wb VGPRs), the activation fragments
@@ -184,6 +197,11 @@ class Gfx950Skeletons:
             grid = N // (16 * p["R"] * p["SN"])
             threads = 64 * p["SN"] * S
             bound = p["TPB"]  # __launch_bounds__(TPB)
+        elif kind == "line":
+            sp = space.line_split(N, int(op.shapes["K"]), p)
+            grid = N // (16 * p["R"])
+            threads = 64 * (sp[0] if sp else 1)
+            bound = 1024  # k_stream_line: __launch_bounds__(1024)
         else:
             S, _ = self._split(op, p)
             grid = N // (16 * p["R"])
@@ -218,6 +236,14 @@ class Gfx950Skeletons:
             vmem = (p["BM"] + p["BN"]) * p["BK"] * 2 // nw
             if p.get("BFMT", 0):
                 vmem = p["BM"] * p["BK"] * 2 // nw + p["BN"] * p["BK"] // nw
+        elif kind == "line":
+            wb = 2 if p["BFMT"] == 0 else 1
+            sp = space.line_split(N, K, p)
+            reps = (sp[1] if sp else K // 128) * rounds
+            flops = 4 * p["R"] * max(1, p["MB"]) * space.MFMA_FLOPS[16]
+            copies, slot = space.line_geometry(p)
+            vmem = slot
+            lds_rd = slot
         else:
             wb = 2 if p["BFMT"] == 0 else 1
             S, chunk = self._split(op, p)
@@ -233,7 +259,7 @@ class Gfx950Skeletons:
                               footprint={"LDS": float(lds_rd * reps)},
                               latency=_M.rate("LATENCY.LDS").value))
         atoms.append(Atom(uid=2, kind=AtomKind.XFER_ISSUE,
-                          op_id=("global_load_lds_dwordx4" if kind in ("dma", "ring", "ilv")
+                          op_id=("global_load_lds_dwordx4" if kind in ("dma", "ring", "ilv", "line")
                                  else "global_load_dwordx4"),
                           footprint={"VMEM": float(vmem * reps)},
                           latency=_M.rate("LATENCY.VMEM").value, token="copy"))

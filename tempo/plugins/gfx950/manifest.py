@@ -72,7 +72,8 @@ def ladder_rows(sel):
 def hyper_params(kind, p, fmt, epi=0):
     """A ladder row of select.py (kind, template params) -> the plugin's hyperform params: the
     same kernel, named the way space.variants() names it."""
-    pk = {"stream": "stream", "mfma": "reg", "dma": "dma", "shared": "shared", "ilv": "ilv"}[kind]
+    pk = {"stream": "stream", "mfma": "reg", "dma": "dma", "shared": "shared", "ilv": "ilv",
+          "line": "line"}[kind]
     params = {k: v for k, v in p.items() if k != "fmts"}
     params["kind"] = pk
     if pk == "shared":
@@ -249,6 +250,9 @@ def make(op, rows_files=()):
                                                     sel.STREAM_K_STEP * p["U"])
         elif kind == "ilv":
             fit = "N %% %d == 0 and K %% %d == 0" % (p["BN"], max(64, p["BK"]))
+        elif kind == "line":
+            fit = "N %% %d == 0 and K %% %d == 0 and K <= %d" % (
+                sel.STREAM_N_ROWS * p["R"], sel.LINE_K_STEP, sel.LINE_K_MAX)
         else:
             fit = "N %% %d == 0 and K %% %d == 0" % (p["BN"], p["BK"])
         man["dispatch" if not epi else "dispatch_gate_up"].append(dict(

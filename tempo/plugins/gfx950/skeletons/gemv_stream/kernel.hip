@@ -838,3 +838,252 @@ __global__ __launch_bounds__(TPB) void k_stream_sh(StreamArgs p) {
     stream_store<MB, R, 0>(p, acc, nbase, r16, kg);
   }
 }
+
+// ============================================================================================
+// k_stream_line -- the decode kernel whose weight stream travels in whole 128-byte lines.
+//
+// A 16-byte weight fragment in the MFMA operand layout (row l % 16, k-group l / 16) puts only
+// 64 bytes of each row into one load instruction: every 128-byte line of the weights is touched
+// by two instructions, and the streaming rate stays near 6 TB/s.  Here the weights go HBM -> LDS
+// by LDS-DMA (global_load_lds_dwordx4) with the nontemporal cache policy, and each copy
+// instruction fetches 8 rows x 128 bytes -- lane l takes 16 bytes of row l / 8 -- so every line
+// is fetched whole by one instruction, never cached, and the stream runs at about 7 TB/s.  The
+// fragments are read back from LDS in the MFMA layout; which 16-byte chunk a lane fetches is
+// chosen so the LDS image is swizzled (chunk c of row r stored at chunk c ^ ((r / 2) % 8)) and
+// those reads are free of bank conflicts.
+//
+// Each wave owns a PRIVATE ring of D steps (no barrier inside the loop).  A step is 128 k of
+// RR row groups (16 weight rows each): EB lines per row (EB = 1 byte per weight for int8/uint8,
+// 2 for fp16), plus the activations of those 128 k: for MB = 0 (M = 1) the 256-byte slice of
+// row 0 by one dword copy, read back by broadcast; for MB = 1 or 2 (M <= 16 or 32) the 16*MB
+// rows x 256 bytes (rows past M re-read row M-1), chunk c of row m stored at chunk c ^ (m % 16).
+// Every step issues the same copies, so one constant wait -- vmcnt((D-1) * copies per step) --
+// is exactly "step j has landed"; the copies past the chunk's end re-fetch its last step into a
+// slot nobody reads, and the kernel drains them before the LDS is reused.
+//
+// Work split: one workgroup = one slab of 16*R weight rows, its S waves take S contiguous k
+// chunks (whole steps) and add their partial sums through LDS in wave order, as k_stream does.
+// k order of a step: lane (row l % 16, kgroup g = l / 16) takes k [64h + 16g, 64h + 16g + 16) of
+// each half h = 0, 1 -- the activation fragments use the same map.
+// fmt 2: the zero-point and scale of (row, group) are staged in the wave's LDS before the loop
+// (one group = one step).  EPI = 1: each wave carries the gate row groups of its slab and the
+// matching up row groups (rows p.up + ...), combined in registers as in k_stream.
+// Requirements (launcher): K % 128 == 0, the chunk a multiple of 128, N % (16 R) == 0.
+// ============================================================================================
+template <int MB, int R, int D, int BFMT, int EPI = 0>
+struct StreamLine {
+  static constexpr int RR = EPI ? 2 * R : R;             // row groups per wave
+  static constexpr int EB = BFMT == 0 ? 2 : 1;           // bytes per weight
+  static constexpr int MBE = MB > 0 ? MB : 1;            // 16-column blocks of the result
+  static constexpr int WSLOT = RR * EB * 2048;           // weight bytes per step
+  static constexpr int ASLOT = MB > 0 ? MB * 16 * 256 : 256;  // activation bytes per step
+  static constexpr int SLOT = WSLOT + ASLOT;
+  static constexpr int LA = MB > 0 ? 4 * MB : 1;         // activation copies per step
+  static constexpr int L = 2 * RR * EB + LA;             // copies per step
+  static constexpr int WAIT = (D - 1) * L;
+  static_assert(D >= 2 && WAIT < 64, "ring depth / vmcnt range");
+  // LDS of one wave: D ring slots + (fmt 2) the staged zero-points and scales of G groups
+  static constexpr size_t wave_bytes(int G) {
+    return ((size_t)D * SLOT + (BFMT == 2 ? ((size_t)RR * 16 * G * 3 + 15) / 16 * 16 : 0) + 1023) /
+           1024 * 1024;
+  }
+  static constexpr size_t lds(int S, int G) {
+    return (size_t)S * wave_bytes(G) + (S > 1 ? (size_t)S * RR * MBE * 1024 : 0);
+  }
+};
+
+__device__ __forceinline__ int line_key(int row16) { return (row16 >> 1) & 7; }
+
+template <int MB, int R, int D, int BFMT, int EPI = 0>
+__global__ __launch_bounds__(1024) void k_stream_line(StreamArgs p, int G) {
+  using SL = StreamLine<MB, R, D, BFMT, EPI>;
+  constexpr int RR = SL::RR, EB = SL::EB, MBE = SL::MBE, SLOT = SL::SLOT, WSLOT = SL::WSLOT;
+  extern __shared__ __attribute__((aligned(1024))) uint8_t dsm[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const size_t wbytes = SL::wave_bytes(G);
+  uint8_t* ring = dsm + wave * wbytes;
+  uint8_t* meta_z = ring + D * SLOT;                                   // fmt 2: [RR*16][G]
+  _Float16* meta_s = reinterpret_cast<_Float16*>(meta_z + (RR * 16 * G + 1) / 2 * 2);
+  f32x4* red = reinterpret_cast<f32x4*>(dsm + p.S * wbytes);
+
+  const int kbeg = min(p.K, wave * p.chunk);
+  const int kend = min(p.K, kbeg + p.chunk);
+  const int n = (kend - kbeg) / 128;  // steps of this wave (>= 1: the launcher's split)
+  const int r16 = lane & 15, kg = lane >> 4;
+  const int nbase = blockIdx.x * 16 * R;
+  auto row_of = [&](int r) -> long {  // first row of row group r
+    return EPI && r >= R ? (long)p.up + nbase + (r - R) * 16 : (long)nbase + r * 16;
+  };
+
+  // weight copy (r, h, i) fills rows 8i .. 8i+7 of row group r with line h of the step; lane l
+  // takes slot l: row 8i + l/8, physical chunk l%8, i.e. logical chunk (l%8) ^ key(row)
+  const uint8_t* wsrc[RR][2];
+#pragma unroll
+  for (int r = 0; r < RR; ++r)
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int rr = 8 * i + lane / 8;
+      const int c = (lane % 8) ^ line_key(rr);
+      wsrc[r][i] = reinterpret_cast<const uint8_t*>(p.B) + ((row_of(r) + rr) * p.ldb + kbeg) * EB + c * 16;
+    }
+  // activation copies: MB = 0 -> lane l takes bytes [4l, 4l+4) of row 0's 256-byte slice;
+  // MB > 0 -> copy t fills rows 4t .. 4t+3, lane l the physical chunk l%16 of row 4t + l/16
+  const uint8_t* asrc[SL::LA];
+#pragma unroll
+  for (int t = 0; t < SL::LA; ++t) {
+    if constexpr (MB == 0) {
+      asrc[t] = reinterpret_cast<const uint8_t*>(p.A) + 2L * kbeg + 4 * lane;
+    } else {
+      const int m = 4 * t + lane / 16;
+      const int c = (lane % 16) ^ (m & 15);
+      asrc[t] = reinterpret_cast<const uint8_t*>(p.A + (long)min(m, p.M - 1) * p.lda) + 2L * kbeg + c * 16;
+    }
+  }
+  auto dma = [&](int j) {
+    const int jj = min(j, n - 1);
+    uint8_t* slot = ring + (j % D) * SLOT;
+#pragma unroll
+    for (int r = 0; r < RR; ++r)
+#pragma unroll
+      for (int h = 0; h < EB; ++h)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+          __builtin_amdgcn_global_load_lds((void*)(wsrc[r][i] + (long)jj * 128 * EB + 128 * h),
+                                           (lds_void_stream_t*)(slot + (r * EB + h) * 2048 + i * 1024),
+                                           16, 0, 2 /* nt */);
+#pragma unroll
+    for (int t = 0; t < SL::LA; ++t) {
+      if constexpr (MB == 0)
+        __builtin_amdgcn_global_load_lds((void*)(asrc[t] + jj * 256), (lds_void_stream_t*)(slot + WSLOT),
+                                         4, 0, 0);
+      else
+        __builtin_amdgcn_global_load_lds((void*)(asrc[t] + jj * 256),
+                                         (lds_void_stream_t*)(slot + WSLOT + t * 1024), 16, 0, 0);
+    }
+  };
+
+  _Float16 rscale[RR];
+  if constexpr (BFMT == 1) {
+#pragma unroll
+    for (int r = 0; r < RR; ++r) rscale[r] = p.scale[row_of(r) + r16];
+  }
+  for (int j = 0; j < D; ++j) dma(j);
+  if constexpr (BFMT == 2) {  // this wave's zero-points and scales, one group per step
+    const long gstride = p.K / 128;
+    const int g0 = kbeg / 128;
+    for (int i = lane; i < RR * 16 * n; i += 64) {
+      const int row = i / n, g = i - row * n;
+      const long gi = (row_of(row / 16) + row % 16) * gstride + g0 + g;
+      meta_z[row * G + g] = p.zero[gi];
+      meta_s[row * G + g] = p.scale[gi];
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // prologue copies landed, scales and metadata loaded
+
+  f32x4 acc[RR][MBE], acc2[RR][MBE];
+#pragma unroll
+  for (int r = 0; r < RR; ++r)
+#pragma unroll
+    for (int b = 0; b < MBE; ++b) {
+      acc[r][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+      acc2[r][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  const int key = line_key(r16);
+
+  for (int j = 0; j < n; ++j) {
+    asm volatile("" ::: "memory");
+    s_wait_vm_stream<SL::WAIT>();  // step j has landed
+    asm volatile("" ::: "memory");
+    const uint8_t* slot = ring + (j % D) * SLOT;
+    u32x4 w[RR][2][2], a[MBE][2][2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {  // the two 64-k halves of the step
+#pragma unroll
+      for (int b = 0; b < MBE; ++b)
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const int c = 8 * h + 2 * kg + q;  // 16-byte chunk of the 256-byte activation slice
+          if constexpr (MB == 0)
+            a[b][h][q] = *reinterpret_cast<const u32x4*>(slot + WSLOT + c * 16);
+          else
+            a[b][h][q] = *reinterpret_cast<const u32x4*>(slot + WSLOT + (16 * b + r16) * 256 +
+                                                         ((c ^ r16) * 16));
+        }
+#pragma unroll
+      for (int r = 0; r < RR; ++r) {
+        if constexpr (BFMT == 0) {
+#pragma unroll
+          for (int q = 0; q < 2; ++q)
+            w[r][h][q] = *reinterpret_cast<const u32x4*>(slot + (r * 2 + h) * 2048 + r16 * 128 +
+                                                         (((2 * kg + q) ^ key) * 16));
+        } else {
+          w[r][h][0] = *reinterpret_cast<const u32x4*>(slot + r * 2048 + r16 * 128 +
+                                                       (((4 * h + kg) ^ key) * 16));
+        }
+      }
+    }
+    uint8_t z[RR];
+    _Float16 sc[RR];
+    if constexpr (BFMT == 2) {
+#pragma unroll
+      for (int r = 0; r < RR; ++r) {
+        z[r] = meta_z[(16 * r + r16) * G + j];
+        sc[r] = meta_s[(16 * r + r16) * G + j];
+      }
+    }
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): slot j is read, it may be refilled
+    asm volatile("" ::: "memory");
+    dma(j + D);
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int r = 0; r < RR; ++r) {
+        f16x8 w0, w1;
+        if constexpr (BFMT == 0) {
+          w0 = as_f16x8(w[r][h][0]);
+          w1 = as_f16x8(w[r][h][1]);
+        } else if constexpr (BFMT == 1) {
+          const u32x4 v = w[r][h][0];
+          w0 = dequant8_i8(v[0], v[1], rscale[r]);
+          w1 = dequant8_i8(v[2], v[3], rscale[r]);
+        } else {
+          const u32x4 v = w[r][h][0];
+          w0 = dequant8_u8(v[0], v[1], z[r], sc[r]);
+          w1 = dequant8_u8(v[2], v[3], z[r], sc[r]);
+        }
+#pragma unroll
+        for (int b = 0; b < MBE; ++b) {
+          acc[r][b] = Mfma<16>::run(w0, as_f16x8(a[b][h][0]), acc[r][b]);
+          acc2[r][b] = Mfma<16>::run(w1, as_f16x8(a[b][h][1]), acc2[r][b]);
+        }
+      }
+  }
+  s_wait_vm_stream<0>();  // the copies past the end land before the LDS is reused
+#pragma unroll
+  for (int r = 0; r < RR; ++r)
+#pragma unroll
+    for (int b = 0; b < MBE; ++b) acc[r][b] += acc2[r][b];
+
+  if (p.S > 1) {  // partial sums of the S k chunks, added in wave order by wave 0
+#pragma unroll
+    for (int r = 0; r < RR; ++r)
+#pragma unroll
+      for (int b = 0; b < MBE; ++b) red[((wave * RR + r) * MBE + b) * 64 + lane] = acc[r][b];
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int r = 0; r < RR; ++r)
+#pragma unroll
+      for (int b = 0; b < MBE; ++b) {
+        f32x4 t = red[(r * MBE + b) * 64 + lane];
+        for (int w = 1; w < p.S; ++w) {
+          const f32x4 v = red[((w * RR + r) * MBE + b) * 64 + lane];
+          t[0] += v[0]; t[1] += v[1]; t[2] += v[2]; t[3] += v[3];
+        }
+        acc[r][b] = t;
+      }
+  }
+  stream_store<MBE, R, EPI>(p, acc, nbase, r16, kg);
+}

@@ -6,6 +6,8 @@ Five skeleton kinds, each a kernel family of tempo/plugins/gfx950/skeletons:
   dma     gemm_mfma/k_gemm_dma      fp16 x fp16, LDS-DMA multi-stage pipeline (prefill, M > 32)
   reg     gemm_mfma/k_gemm          any weight format, register-staged copy that can dequantise
                                     on the way into LDS (W8A16 prefill, fp16 fallback)
+  line    gemv_stream/k_stream_line decode (M <= 32): whole 128-byte weight lines by nontemporal
+                                    LDS-DMA into per-wave rings, fragments read back swizzled
   ring    gemv_stream/k_stream_dma  decode (M <= 32): per-wave LDS-DMA ring of k-steps
   stream  gemv_stream/k_stream      decode, register-staged prefetch (kept as a measured arm)
 
@@ -43,6 +45,7 @@ DOMAINS = {
                 GROUP=(4, 8, 16), XCD=(0, 1), WAVES=((2, 2), (2, 4), (4, 2), (4, 4)), MS=(16, 32)),
     "reg": dict(BM=(64, 128, 256), BN=(128, 256), BK=(64,), MS=(16, 32), SWZ=(1, 2), GROUP=(8,),
                 XCD=(1,)),
+    "line": dict(R=(1, 2, 4), D=(2, 3, 4, 5, 6), W=(1024, 2048, 4096)),
     "ring": dict(R=(1, 2, 4), D=(4, 5, 6, 8, 10, 12, 14, 16)),
     "stream": dict(R=(1, 2, 4), U=(2, 4, 8), ALDS=(0, 1)),
     "shared": dict(R=(1, 2), U=(2, 4), SN=(2, 4, 8)),
@@ -57,6 +60,38 @@ def bfmt(op: OpSpec) -> int:
         raise PluginCapabilityError("gfx950 skeletons take A fp16 with B fp16|int8|uint8; got %s x %s"
                                     % key)
     return BFMT_OF[key]
+
+
+def line_geometry(p: dict):
+    """(copies per step, ring slot bytes) of the line kernel, as skeletons/gemv_stream declares."""
+    rr = 2 * p["R"] if p.get("EPI") else p["R"]
+    eb = 2 if p["BFMT"] == 0 else 1
+    la = 4 * p["MB"] if p["MB"] else 1
+    slot = rr * eb * 2048 + (p["MB"] * 16 * 256 if p["MB"] else 256)
+    return 2 * rr * eb + la, slot
+
+
+def line_split(N: int, K: int, p: dict):
+    """(S, steps per wave, LDS bytes) as the shipped launchers compute them; None if none fits."""
+    rr = 2 * p["R"] if p.get("EPI") else p["R"]
+    slabs = N // (16 * p["R"])
+    steps = K // 128
+    _, slot = line_geometry(p)
+    S = max(1, min(16, steps, -(-p["W"] // max(1, slabs))))
+
+    def lds(s_, per):
+        meta = -(-(rr * 16 * per * 3) // 16) * 16 if p["BFMT"] == 2 else 0
+        wave = -(-(p["D"] * slot + meta) // 1024) * 1024
+        return s_ * wave + (s_ * rr * max(1, p["MB"]) * 1024 if s_ > 1 else 0)
+
+    while True:
+        per = -(-steps // S)
+        s2 = -(-steps // per)
+        if lds(s2, per) <= LDS_MAX:
+            return s2, per, lds(s2, per)
+        if S == 1:
+            return None
+        S -= 1
 
 
 def lds_bytes(kind: str, p: dict) -> int:
@@ -121,6 +156,9 @@ def tag(kind: str, p: dict) -> str:
     if kind == "reg":
         return "reg_m%dn%dk%d_w%dx%d_f%d_z%d_b%d" % (p["BM"], p["BN"], p["BK"], p["WM"], p["WN"],
                                                    p["MS"], p["SWZ"], p["BFMT"])
+    if kind == "line":
+        return "line_mb%d_r%d_d%d_w%d_b%d%s" % (p["MB"], p["R"], p["D"], p["W"], p["BFMT"],
+                                              "_e1" if p.get("EPI") else "")
     if kind == "ring":
         return "ring_mb%d_r%d_d%d_b%d" % (p["MB"], p["R"], p["D"], p["BFMT"])
     if kind == "shared":
@@ -176,6 +214,17 @@ def legal(kind: str, p: dict, M: int, N: int, K: int):
     R = p["R"]
     if N % (16 * R):
         return "N %% %d" % (16 * R)
+    if kind == "line":
+        if M > max(1, 16 * p["MB"]):
+            return "M > 16*MB (MB = 0: M = 1)"
+        if K % 128 or K > 65536:
+            return "K % 128 / K > 65536"
+        L, _ = line_geometry(p)
+        if (p["D"] - 1) * L >= 64 or p["D"] < 2:
+            return "vmcnt depth"
+        if line_split(N, K, p) is None:
+            return "LDS"
+        return None
     if M > 16 * p["MB"]:
         return "M > 16*MB"
     if kind == "shared":
@@ -211,6 +260,11 @@ def variants(op: OpSpec) -> Iterator[Hyperform]:
     out = []
     if M <= 32:
         MB = 1 if M <= 16 else 2
+        d = DOMAINS["line"]
+        for R in d["R"]:
+            for D in d["D"]:
+                for W in d["W"]:
+                    out.append(("line", dict(MB=0 if M == 1 else MB, R=R, D=D, W=W, BFMT=b)))
         for R in DOMAINS["ring"]["R"]:
             for D in DOMAINS["ring"]["D"]:
                 out.append(("ring", dict(MB=MB, R=R, D=D, BFMT=b)))

@@ -103,6 +103,23 @@ def test_w8a16_parity_small_m(gpu, fmt, M):
 
 
 @pytest.mark.parametrize("fmt", [1, 2])
+@pytest.mark.parametrize("M", [1, 16, 32])
+def test_w8a16_parity_past_the_line_rows(gpu, fmt, M):
+    """K > 65536 is past the line kernel's rows: the register-pipelined stream / shared rows
+    (its fallbacks) run, and must hold the same bar."""
+    N, K = 512, 65536 + 512
+    say("w8a16 fmt", fmt, "M", M, "N", N, "K", K, "route", _route(fmt, M, N, K))
+    assert not _route(fmt, M, N, K).startswith("l")
+    A = O.randn_f16((M, K), 11, K ** -0.5)
+    q, s, z = make_weights(N, K, fmt, 77)
+    C = _run(A, q, s, z, fmt, gpu)
+    assert O.count_poison(C) == 0
+    rel = O.rel_l2(C, O.gemm_w8a16(A, q, s, z, 128, fmt))
+    say("  relL2 %.3e" % rel)
+    assert rel <= 3e-3
+
+
+@pytest.mark.parametrize("fmt", [1, 2])
 def test_w8a16_parity_prefill(gpu, fmt):
     """M = 2048 on two of the dense shapes; oracle on sampled rows."""
     for N, K in [(5120, 6144), (7168, 5120)]:
