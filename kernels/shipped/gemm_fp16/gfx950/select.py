@@ -23,10 +23,12 @@ ARCH = "gfx950"
 LADDER = [
     (1, 0, "l0r1d3", "line", dict(MB=0, R=1, D=3, W=2048)),
     (1, 0, "s1a_r1u4", "stream", dict(MB=1, R=1, U=4, A=1)),
-    (16, 0, "l1r1d3", "line", dict(MB=1, R=1, D=3, W=2048)),
+    (16, 12288, "l1r1n4d3", "line", dict(MB=1, R=1, D=3, SN=4, W=2048)),
+    (16, 0, "l1r1d4", "line", dict(MB=1, R=1, D=4, W=2048)),
     (16, 12288, "h16r1u4n4", "shared", dict(MB=1, R=1, U=4, SN=4)),
     (16, 0, "s16r1u4", "stream", dict(MB=1, R=1, U=4, A=0)),
-    (32, 0, "l2r2d2", "line", dict(MB=2, R=2, D=2, W=2048)),
+    (32, 12288, "l2r1n4d3", "line", dict(MB=2, R=1, D=3, SN=4, W=2048)),
+    (32, 0, "l2r1d4", "line", dict(MB=2, R=1, D=4, W=2048)),
     (32, 12288, "h32r1u4n4", "shared", dict(MB=2, R=1, U=4, SN=4)),
     (32, 0, "s32r1u4", "stream", dict(MB=2, R=1, U=4, A=0)),
     (256, 0, "m128x128k64", "mfma",
@@ -41,6 +43,12 @@ LADDER = [
 # (7680, 3840) against the plain GEMM + a separate silu*mul kernel.  M > 32 is not covered: the
 # caller runs the plain GEMM and its own elementwise step.
 LADDER_GATE_UP = [
+    (1, 0, "gl0r1n2d3", "line", dict(MB=0, R=1, D=3, SN=2, W=2048)),
+    (1, 0, "gl0r1d3", "line", dict(MB=0, R=1, D=3, W=2048)),
+    (16, 12288, "gl1r1n4d3", "line", dict(MB=1, R=1, D=3, SN=4, W=2048)),
+    (16, 0, "gl1r1d3", "line", dict(MB=1, R=1, D=3, W=2048)),
+    (32, 12288, "gl2r1n4d3", "line", dict(MB=2, R=1, D=3, SN=4, W=2048)),
+    (32, 0, "gl2r1d3", "line", dict(MB=2, R=1, D=3, W=2048)),
     (1, 0, "gh1r1u2n2", "shared", dict(MB=1, R=1, U=2, SN=2, TPB=512)),
     (16, 0, "gh16r1u4n2", "shared", dict(MB=1, R=1, U=4, SN=2, TPB=512)),
     (16, 0, "g16r1u4", "stream", dict(MB=1, R=1, U=4, A=0)),
@@ -56,7 +64,11 @@ LINE_K_MAX = 65536  # the line kernel's LDS holds one wave's metadata (fmt 2): b
 
 
 def _fits_gate_up(kind, p, M, N, K):
-    # N is the output width; the shared kernel's SN slab waves pair up (SN/2 output slabs)
+    # N is the output width; the slab waves of the shared kernel and of the line kernel with
+    # SN >= 2 pair up (SN/2 output slabs per workgroup)
+    if kind == "line" and p.get("SN", 1) >= 2:
+        return (N % (STREAM_N_ROWS * p["R"] * p["SN"] // 2) == 0 and K % LINE_K_STEP == 0
+                and K <= LINE_K_MAX)
     if kind == "shared":
         return (p["SN"] % 2 == 0 and N % (STREAM_N_ROWS * p["R"] * p["SN"] // 2) == 0
                 and K % (STREAM_K_STEP * p["U"]) == 0)
@@ -65,7 +77,8 @@ def _fits_gate_up(kind, p, M, N, K):
 
 def _fits(kind, p, M, N, K):
     if kind == "line":
-        return N % (STREAM_N_ROWS * p["R"]) == 0 and K % LINE_K_STEP == 0 and K <= LINE_K_MAX
+        return (N % (STREAM_N_ROWS * p["R"] * p.get("SN", 1)) == 0 and K % LINE_K_STEP == 0
+                and K <= LINE_K_MAX)
     if kind == "ilv":
         return N % p["BN"] == 0 and K % max(64, p["BK"]) == 0
     if kind == "stream":

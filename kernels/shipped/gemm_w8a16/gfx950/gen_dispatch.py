@@ -37,7 +37,8 @@ HEAD = """// GENERATED from select.py -- do not edit.  Regenerate with:
 def instantiation(kind, p, epi=0):
     tail = ",%d" % epi if epi else ""
     if kind == "line":
-        return "launch_line<%d,%d,%d,%d%s>" % (p["MB"], p["R"], p["D"], p["W"], tail)
+        return "launch_line<%d,%d,%d,%d,%d%s>" % (p["MB"], p["R"], p["D"], p.get("SN", 1), p["W"],
+                                                  tail)
     if kind == "shared":
         return "launch_shared<%d,%d,%d,%d,%d%s>" % (p["MB"], p["R"], p["U"], p["SN"],
                                                     p.get("TPB", 1024), tail)
@@ -51,8 +52,9 @@ def instantiation(kind, p, epi=0):
 
 def condition(sel, kind, p, m_max, n_min=0, gate_up=False):
     if kind == "line":
+        sno = p.get("SN", 1) // 2 if gate_up and p.get("SN", 1) >= 2 else p.get("SN", 1)
         fit = "(p.N %% %d) == 0 && (p.K %% %d) == 0 && p.K <= %d" % (
-            sel.STREAM_N_ROWS * p["R"], sel.LINE_K_STEP, sel.LINE_K_MAX)
+            sel.STREAM_N_ROWS * p["R"] * sno, sel.LINE_K_STEP, sel.LINE_K_MAX)
     elif kind == "stream":
         fit = "(p.N %% %d) == 0 && (p.K %% %d) == 0" % (sel.STREAM_N_ROWS * p["R"],
                                                           sel.STREAM_K_STEP * p["U"])

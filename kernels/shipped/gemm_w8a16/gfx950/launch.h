@@ -134,22 +134,24 @@ inline hipError_t launch_shared(const W8A16Params& p, hipStream_t s) {
   return hipGetLastError();
 }
 
-// k split of the line kernel (k_stream_line): about `waves` waves over the part, at most 16 per
-// workgroup, every chunk whole steps of 128 k, the workgroup's rings (+ the fmt 2 metadata and the
-// reduction) within the 160 KiB of LDS.  false: no split fits (the caller's own path).
+// k split of the line kernel (k_stream_line): `wgs` workgroups of SN slab waves, each split
+// into S k chunks of whole 128-k steps -- about `waves` waves over the part, at most 1024
+// threads per workgroup, equal chunks when the slab waves share the activation ring (SN > 1:
+// they pass the same barriers), the workgroup's rings (+ the fmt 2 metadata and the reduction)
+// within the 160 KiB of LDS.  false: no split fits (the caller's own path).
 template <class SL>
-inline bool line_split(int slabs, int K, int waves, int* S_out, int* chunk_out, int* G_out,
+inline bool line_split(int wgs, int SN, int K, int waves, int* S_out, int* chunk_out, int* G_out,
                        size_t* lds_out) {
   const int steps = K / 128;
-  int S = (waves + slabs - 1) / slabs;
-  if (S > 16) S = 16;
+  int S = (waves + wgs * SN - 1) / (wgs * SN);
+  if (S > 16 / SN) S = 16 / SN;
   if (S > steps) S = steps;
   if (S < 1) S = 1;
   for (;; --S) {
     const int per = (steps + S - 1) / S;  // steps per wave
     const int s2 = (steps + per - 1) / per;
     const size_t lds = SL::lds(s2, per);
-    if (lds <= 160 * 1024) {
+    if (lds <= 160 * 1024 && (SN == 1 || steps % s2 == 0)) {
       *S_out = s2;
       *chunk_out = per * 128;
       *G_out = per;
@@ -161,26 +163,27 @@ inline bool line_split(int slabs, int K, int waves, int* S_out, int* chunk_out, 
 }
 
 // The line kernel (whole-line nontemporal weight stream through per-wave LDS rings).  MB = 0:
-// M = 1; MB = 1 / 2: M <= 16 / 32.  EPI = 1: fused gate/up (p.N the output width; Wq, scale and
-// zero hold 2N rows).
-template <int BFMT, int MB, int R, int D, int WAVES, int EPI>
+// M = 1; MB = 1 / 2: M <= 16 / 32.  SN slab waves of a workgroup share one activation ring.
+// EPI = 1: fused gate/up (p.N the output width; Wq, scale and zero hold 2N rows).
+template <int BFMT, int MB, int R, int D, int SN, int WAVES, int EPI>
 inline hipError_t launch_line_fmt(const W8A16Params& p, hipStream_t s) {
-  using SL = StreamLine<MB, R, D, BFMT, EPI>;
+  using SL = StreamLine<MB, R, D, BFMT, EPI, SN>;
   StreamArgs a = stream_args(p);
   a.up = EPI ? p.N : 0;
   int G = 0;
   size_t lds = 0;
-  if (!line_split<SL>(p.N / (16 * R), p.K, WAVES, &a.S, &a.chunk, &G, &lds))
+  const int wgs = p.N / (16 * R * SL::SNO);  // output slabs / per workgroup
+  if (!line_split<SL>(wgs, SN, p.K, WAVES, &a.S, &a.chunk, &G, &lds))
     return hipErrorInvalidConfiguration;
-  hipLaunchKernelGGL((k_stream_line<MB, R, D, BFMT, EPI>), dim3(p.N / (16 * R)), dim3(64 * a.S),
-                     lds, s, a, G);
+  hipLaunchKernelGGL((k_stream_line<MB, R, D, BFMT, EPI, SN>), dim3(wgs), dim3(64 * SN * a.S), lds,
+                     s, a, G);
   return hipGetLastError();
 }
 
-template <int MB, int R, int D, int WAVES, int EPI = 0>
+template <int MB, int R, int D, int SN, int WAVES, int EPI = 0>
 inline hipError_t launch_line(const W8A16Params& p, hipStream_t s) {
-  if (p.fmt == 1) return launch_line_fmt<1, MB, R, D, WAVES, EPI>(p, s);
-  return launch_line_fmt<2, MB, R, D, WAVES, EPI>(p, s);
+  if (p.fmt == 1) return launch_line_fmt<1, MB, R, D, SN, WAVES, EPI>(p, s);
+  return launch_line_fmt<2, MB, R, D, SN, WAVES, EPI>(p, s);
 }
 
 template <int BM, int BN, int BK, int WM, int WN, int MS, int SWZ, int GROUP, int XCD>

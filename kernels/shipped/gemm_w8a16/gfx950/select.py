@@ -16,9 +16,10 @@ FORMATS = (1, 2)
 # absent = both) and whose kernel fits the shape is taken.
 LADDER = [
     (1, 0, "l0r1d4", "line", dict(MB=0, R=1, D=4, W=2048)),
-    (8, 0, "l1r1d4", "line", dict(MB=1, R=1, D=4, W=2048)),
-    (16, 0, "l1r2d4", "line", dict(MB=1, R=2, D=4, W=2048)),
-    (32, 0, "l2r2d3", "line", dict(MB=2, R=2, D=3, W=2048, fmts=(1,))),
+    (16, 12288, "l1r1n4d3", "line", dict(MB=1, R=1, D=3, SN=4, W=2048)),
+    (16, 0, "l1r1n2d4", "line", dict(MB=1, R=1, D=4, SN=2, W=2048)),
+    (32, 12288, "l2r1n4d4", "line", dict(MB=2, R=1, D=4, SN=4, W=2048)),
+    (32, 0, "l2r1n2d4", "line", dict(MB=2, R=1, D=4, SN=2, W=2048)),
     (1, 0, "s1a_r1u8", "stream", dict(MB=1, R=1, U=8, A=1)),
     (1, 0, "s1a_r1u4", "stream", dict(MB=1, R=1, U=4, A=1)),
     (8, 16384, "h8r1u2n2", "shared", dict(MB=1, R=1, U=2, SN=2, fmts=(1,))),
@@ -42,6 +43,12 @@ LADDER = [
 # production gate_up shape (N, K) = (17408, 5120), both formats.  M > 32 is not covered (the
 # caller's own path).
 LADDER_GATE_UP = [
+    (1, 0, "gl0r1n2d4", "line", dict(MB=0, R=1, D=4, SN=2, W=2048)),
+    (1, 0, "gl0r1d4", "line", dict(MB=0, R=1, D=4, W=2048)),
+    (16, 12288, "gl1r1n4d3", "line", dict(MB=1, R=1, D=3, SN=4, W=2048)),
+    (16, 0, "gl1r1n2d4", "line", dict(MB=1, R=1, D=4, SN=2, W=2048)),
+    (32, 12288, "gl2r1n4d4", "line", dict(MB=2, R=1, D=4, SN=4, W=2048)),
+    (32, 0, "gl2r1n2d4", "line", dict(MB=2, R=1, D=4, SN=2, W=2048)),
     (1, 0, "g1a_r1u2", "stream", dict(MB=1, R=1, U=2, A=1, fmts=(1,))),
     (1, 0, "g1a_r1u8", "stream", dict(MB=1, R=1, U=8, A=1, fmts=(2,))),
     (1, 0, "g1a_r1u4", "stream", dict(MB=1, R=1, U=4, A=1)),
@@ -60,7 +67,11 @@ LINE_K_MAX = 65536  # the line kernel's LDS holds one wave's metadata (fmt 2): b
 
 
 def _fits_gate_up(kind, p, M, N, K):
-    # N is the output width; the shared kernel's SN slab waves pair up (SN/2 output slabs)
+    # N is the output width; the slab waves of the shared kernel and of the line kernel with
+    # SN >= 2 pair up (SN/2 output slabs per workgroup)
+    if kind == "line" and p.get("SN", 1) >= 2:
+        return (N % (STREAM_N_ROWS * p["R"] * p["SN"] // 2) == 0 and K % LINE_K_STEP == 0
+                and K <= LINE_K_MAX)
     if kind == "shared":
         return (p["SN"] % 2 == 0 and N % (STREAM_N_ROWS * p["R"] * p["SN"] // 2) == 0
                 and K % (STREAM_K_STEP * p["U"]) == 0)
@@ -69,7 +80,8 @@ def _fits_gate_up(kind, p, M, N, K):
 
 def _fits(kind, p, M, N, K):
     if kind == "line":
-        return N % (STREAM_N_ROWS * p["R"]) == 0 and K % LINE_K_STEP == 0 and K <= LINE_K_MAX
+        return (N % (STREAM_N_ROWS * p["R"] * p.get("SN", 1)) == 0 and K % LINE_K_STEP == 0
+                and K <= LINE_K_MAX)
     if kind == "stream":
         return N % (STREAM_N_ROWS * p["R"]) == 0 and K % (STREAM_K_STEP * p["U"]) == 0
     if kind == "shared":

@@ -43,7 +43,7 @@ _ENTRY = {
             "const _Float16*, const void*, const _Float16*, const uint8_t*, _Float16*, int, int, "
             "int, int, int, int, int",
             ("common/cdna4.h", "gemm_mfma/kernel.hip")),
-    "line": ("k_stream_line", ("MB", "R", "D", "BFMT", "EPI"), "StreamArgs, int",
+    "line": ("k_stream_line", ("MB", "R", "D", "BFMT", "EPI", "SN"), "StreamArgs, int",
              ("common/cdna4.h", "gemv_stream/kernel.hip")),
     "ring": ("k_stream_dma", ("MB", "R", "D", "BFMT"), "StreamArgs",
              ("common/cdna4.h", "gemv_stream/kernel.hip")),
@@ -60,11 +60,15 @@ NAMESPACE = "tempo::gen"
 KIND_FLAGS = {"ilv": ("-mllvm", "-amdgpu-sched-strategy=iterative-minreg")}
 # trailing template parameters with a default in the skeleton: named only when the hyperform
 # sets them (EPI = 1 is the fused gate/up epilogue of the decode kernels)
-_OPTIONAL = frozenset({"EPI"})
+_OPTIONAL = frozenset({"EPI", "SN"})
 
 
 def _order(kind: str, p: dict) -> tuple:
-    return tuple(k for k in _ENTRY[kind][1] if k in p or k not in _OPTIONAL)
+    """Template parameters to name: every required one, and the optional (defaulted, trailing)
+    ones up to the last the hyperform sets -- an earlier unset one is named with its default 0."""
+    names = _ENTRY[kind][1]
+    last = max((i for i, k in enumerate(names) if k in p or k not in _OPTIONAL), default=-1)
+    return tuple(names[:last + 1])
 
 
 def _p(h: Hyperform) -> dict:
@@ -149,7 +153,7 @@ class Gfx950Skeletons:
             return regs, max(int(regs * 1.2), 2 * acc + 16), space.lds_bytes(kind, p)
         wb = 2 if p["BFMT"] == 0 else 1
         if kind == "line":
-            rr = 2 * p["R"] if p.get("EPI") else p["R"]
+            rr = 2 * p["R"] if p.get("EPI") and not space.line_paired(p) else p["R"]
             mbe = max(1, p["MB"])
             # fragments of one step (2 halves x (2 per row group for fp16, 1 for 8-bit) + the
             # activation fragments), two accumulator chains, the fp16 expansion of 8-bit
@@ -199,8 +203,8 @@ class Gfx950Skeletons:
             bound = p["TPB"]  # __launch_bounds__(TPB)
         elif kind == "line":
             sp = space.line_split(N, int(op.shapes["K"]), p)
-            grid = N // (16 * p["R"])
-            threads = 64 * (sp[0] if sp else 1)
+            grid = N // (16 * p["R"] * (p["SN"] // 2 if space.line_paired(p) else p.get("SN", 1)))
+            threads = 64 * p.get("SN", 1) * (sp[0] if sp else 1)
             bound = 1024  # k_stream_line: __launch_bounds__(1024)
         else:
             S, _ = self._split(op, p)
@@ -241,9 +245,9 @@ class Gfx950Skeletons:
             sp = space.line_split(N, K, p)
             reps = (sp[1] if sp else K // 128) * rounds
             flops = 4 * p["R"] * max(1, p["MB"]) * space.MFMA_FLOPS[16]
-            copies, slot = space.line_geometry(p)
-            vmem = slot
-            lds_rd = slot
+            copies, wslot, aslot = space.line_geometry(p)
+            vmem = wslot + aslot // p.get("SN", 1)
+            lds_rd = wslot + aslot
         else:
             wb = 2 if p["BFMT"] == 0 else 1
             S, chunk = self._split(op, p)
@@ -289,7 +293,7 @@ class Gfx950Skeletons:
                  "namespace gen {\n\n")
         inst = ("\n// explicit instantiation: the one kernel this file exists to contain\n"
                 "template __global__ void %s<%s>(%s);\n"
-                % (sym, ", ".join(str(int(p[k])) for k in order), args))
+                % (sym, ", ".join(str(int(p.get(k, 0))) for k in order), args))
         src = head + "".join(body) + inst + "\n}  // namespace gen\n}  // namespace tempo\n"
         return Rendered(source=src, launch=self.launch_of(op, h), includes=(),
                         notes="namespace wrap + one explicit instantiation; logic lives in the skeleton",
@@ -302,6 +306,6 @@ class Gfx950Skeletons:
         order = _order(p["kind"], p)
         vals = []
         for k in order:
-            v = p[k]
+            v = p.get(k, 0)
             vals.append("true" if v is True else "false" if v is False else str(int(v)))
         return "%s::%s<%s>" % (NAMESPACE, sym, ", ".join(vals))

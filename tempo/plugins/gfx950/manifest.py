@@ -252,7 +252,7 @@ def make(op, rows_files=()):
             fit = "N %% %d == 0 and K %% %d == 0" % (p["BN"], max(64, p["BK"]))
         elif kind == "line":
             fit = "N %% %d == 0 and K %% %d == 0 and K <= %d" % (
-                sel.STREAM_N_ROWS * p["R"], sel.LINE_K_STEP, sel.LINE_K_MAX)
+                sel.STREAM_N_ROWS * p["R"] * p.get("SN", 1), sel.LINE_K_STEP, sel.LINE_K_MAX)
         else:
             fit = "N %% %d == 0 and K %% %d == 0" % (p["BN"], p["BK"])
         man["dispatch" if not epi else "dispatch_gate_up"].append(dict(

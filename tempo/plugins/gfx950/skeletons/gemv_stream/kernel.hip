@@ -861,58 +861,94 @@ __global__ __launch_bounds__(TPB) void k_stream_sh(StreamArgs p) {
 // is exactly "step j has landed"; the copies past the chunk's end re-fetch its last step into a
 // slot nobody reads, and the kernel drains them before the LDS is reused.
 //
-// Work split: one workgroup = one slab of 16*R weight rows, its S waves take S contiguous k
-// chunks (whole steps) and add their partial sums through LDS in wave order, as k_stream does.
+// Work split: one workgroup = SN slabs of 16*R weight rows x S k chunks (whole steps); wave w
+// takes slab w % SN and chunk w / SN.  The S partial sums of a slab are added through LDS in
+// chunk order and written by its chunk-0 wave, as k_stream does.
+// SN = 1: every wave also owns its activation ring (no barrier in the loop).  SN > 1: the SN
+// waves of one k chunk walk the same steps and SHARE one activation ring -- each issues LA/SN of
+// the copies of a step -- so the activation traffic drops by SN; one workgroup barrier per step
+// orders them: at iteration j every wave has its own copies of step j landed (vmcnt), then the
+// barrier makes all of step j readable and guarantees that every wave has finished reading step
+// j-1, whose activation slot is refilled in this iteration (with step j+D-1: the shared ring runs
+// one step shallower than the private weight rings).  All chunks then hold the same number of
+// steps (the launcher's split), so every wave passes the same barriers.
 // k order of a step: lane (row l % 16, kgroup g = l / 16) takes k [64h + 16g, 64h + 16g + 16) of
 // each half h = 0, 1 -- the activation fragments use the same map.
 // fmt 2: the zero-point and scale of (row, group) are staged in the wave's LDS before the loop
-// (one group = one step).  EPI = 1: each wave carries the gate row groups of its slab and the
-// matching up row groups (rows p.up + ...), combined in registers as in k_stream.
-// Requirements (launcher): K % 128 == 0, the chunk a multiple of 128, N % (16 R) == 0.
+// (one group = one step).  EPI = 1 (fused gate/up, output width p.N, up rows from p.up): with
+// SN = 1 each wave carries the gate row groups of its slab and the matching up row groups,
+// combined in registers as in k_stream; with SN >= 2 the slab waves pair up -- waves sg < SN/2
+// stream gate slabs, the others the matching up slabs (same activation ring) -- and each up
+// result reaches its gate partner through LDS before the epilogue.
+// Requirements (launcher): K % 128 == 0, the chunk a multiple of 128, N % (16 R SNO) == 0 with
+// SNO the output slabs per workgroup (SN, or SN/2 when paired).
 // ============================================================================================
-template <int MB, int R, int D, int BFMT, int EPI = 0>
+template <int MB, int R, int D, int BFMT, int EPI = 0, int SN = 1>
 struct StreamLine {
-  static constexpr int RR = EPI ? 2 * R : R;             // row groups per wave
+  // EPI with SN >= 2 pairs the slab waves (gate, up); with SN = 1 each wave carries both
+  static constexpr bool PAIRED = EPI && SN >= 2;
+  static_assert(!PAIRED || SN % 2 == 0, "paired gate/up slab waves");
+  static constexpr int SNO = PAIRED ? SN / 2 : SN;       // output slabs per workgroup
+  static constexpr int RR = EPI && !PAIRED ? 2 * R : R;  // row groups per wave
   static constexpr int EB = BFMT == 0 ? 2 : 1;           // bytes per weight
   static constexpr int MBE = MB > 0 ? MB : 1;            // 16-column blocks of the result
   static constexpr int WSLOT = RR * EB * 2048;           // weight bytes per step
   static constexpr int ASLOT = MB > 0 ? MB * 16 * 256 : 256;  // activation bytes per step
-  static constexpr int SLOT = WSLOT + ASLOT;
-  static constexpr int LA = MB > 0 ? 4 * MB : 1;         // activation copies per step
-  static constexpr int L = 2 * RR * EB + LA;             // copies per step
-  static constexpr int WAIT = (D - 1) * L;
-  static_assert(D >= 2 && WAIT < 64, "ring depth / vmcnt range");
-  // LDS of one wave: D ring slots + (fmt 2) the staged zero-points and scales of G groups
+  // activation copies per step: MB > 0: 4 per 16 rows (1 KiB each), split over the SN slab
+  // waves; MB = 0: every wave copies the whole 256-byte slice (one dword per lane) into the same
+  // slot -- identical bytes, so the copies of different waves may land in any order -- which
+  // keeps one copy per wave and step, whatever SN is
+  static constexpr int LA = MB > 0 ? 4 * MB : SN;
+  static constexpr int LAW = LA / SN;                    // ... issued by each wave
+  static constexpr int L = 2 * RR * EB + LAW;            // copies per step per wave
+  static constexpr int WAIT = (SN > 1 ? D - 2 : D - 1) * L;
+  static_assert(SN >= 1 && LA % SN == 0, "activation copies split evenly over the slab waves");
+  static_assert(D >= (SN > 1 ? 3 : 2) && (D - 1) * L < 64, "ring depth / vmcnt range");
+  // LDS of one wave: D weight slots (+ its own activation ring when SN = 1) + (fmt 2) the staged
+  // zero-points and scales of G groups; one shared activation ring per k chunk when SN > 1
   static constexpr size_t wave_bytes(int G) {
-    return ((size_t)D * SLOT + (BFMT == 2 ? ((size_t)RR * 16 * G * 3 + 15) / 16 * 16 : 0) + 1023) /
-           1024 * 1024;
+    return ((size_t)D * (WSLOT + (SN == 1 ? ASLOT : 0)) +
+            (BFMT == 2 ? ((size_t)RR * 16 * G * 3 + 15) / 16 * 16 : 0) + 1023) / 1024 * 1024;
   }
+  static constexpr size_t act_bytes() { return SN > 1 ? ((size_t)D * ASLOT + 1023) / 1024 * 1024 : 0; }
   static constexpr size_t lds(int S, int G) {
-    return (size_t)S * wave_bytes(G) + (S > 1 ? (size_t)S * RR * MBE * 1024 : 0);
+    return (size_t)S * (SN * wave_bytes(G) + act_bytes()) +
+           (S > 1 ? (size_t)S * SN * RR * MBE * 1024 : 0);
   }
 };
 
 __device__ __forceinline__ int line_key(int row16) { return (row16 >> 1) & 7; }
 
-template <int MB, int R, int D, int BFMT, int EPI = 0>
+template <int MB, int R, int D, int BFMT, int EPI = 0, int SN = 1>
 __global__ __launch_bounds__(1024) void k_stream_line(StreamArgs p, int G) {
-  using SL = StreamLine<MB, R, D, BFMT, EPI>;
-  constexpr int RR = SL::RR, EB = SL::EB, MBE = SL::MBE, SLOT = SL::SLOT, WSLOT = SL::WSLOT;
+  using SL = StreamLine<MB, R, D, BFMT, EPI, SN>;
+  constexpr int RR = SL::RR, EB = SL::EB, MBE = SL::MBE, WSLOT = SL::WSLOT, ASLOT = SL::ASLOT;
+  constexpr int WSTRIDE = SN == 1 ? WSLOT + ASLOT : WSLOT;  // bytes per ring slot of a wave
   extern __shared__ __attribute__((aligned(1024))) uint8_t dsm[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int sg = wave % SN, kc = wave / SN;  // slab of the workgroup, k chunk
   const size_t wbytes = SL::wave_bytes(G);
-  uint8_t* ring = dsm + wave * wbytes;
-  uint8_t* meta_z = ring + D * SLOT;                                   // fmt 2: [RR*16][G]
+  uint8_t* group = dsm + kc * (SN * wbytes + SL::act_bytes());  // k chunk's LDS
+  uint8_t* ring = group + SL::act_bytes() + sg * wbytes;         // this wave's weight ring
+  // activation slot of step j: inside the wave's own ring slot (SN = 1) or the shared ring
+  auto aslot = [&](int j) -> uint8_t* {
+    return SN == 1 ? ring + (j % D) * WSTRIDE + WSLOT : group + (j % D) * ASLOT;
+  };
+  uint8_t* meta_z = ring + D * WSTRIDE;                                  // fmt 2: [RR*16][G]
   _Float16* meta_s = reinterpret_cast<_Float16*>(meta_z + (RR * 16 * G + 1) / 2 * 2);
-  f32x4* red = reinterpret_cast<f32x4*>(dsm + p.S * wbytes);
+  const int S = p.S;  // k chunks
+  f32x4* red = reinterpret_cast<f32x4*>(dsm + S * (SN * wbytes + SL::act_bytes()));
 
-  const int kbeg = min(p.K, wave * p.chunk);
+  const int kbeg = min(p.K, kc * p.chunk);
   const int kend = min(p.K, kbeg + p.chunk);
-  const int n = (kend - kbeg) / 128;  // steps of this wave (>= 1: the launcher's split)
+  const int n = (kend - kbeg) / 128;  // steps of this wave (>= 1; equal in all chunks if SN > 1)
   const int r16 = lane & 15, kg = lane >> 4;
-  const int nbase = blockIdx.x * 16 * R;
+  constexpr bool PAIRED = SL::PAIRED;
+  const bool upw = PAIRED && sg >= SN / 2;                         // paired: an up wave
+  const int nbase = (blockIdx.x * SL::SNO + (PAIRED ? sg % (SN / 2) : sg)) * 16 * R;
   auto row_of = [&](int r) -> long {  // first row of row group r
+    if constexpr (PAIRED) return (upw ? (long)p.up : 0L) + nbase + r * 16;
     return EPI && r >= R ? (long)p.up + nbase + (r - R) * 16 : (long)nbase + r * 16;
   };
 
@@ -927,22 +963,24 @@ __global__ __launch_bounds__(1024) void k_stream_line(StreamArgs p, int G) {
       const int c = (lane % 8) ^ line_key(rr);
       wsrc[r][i] = reinterpret_cast<const uint8_t*>(p.B) + ((row_of(r) + rr) * p.ldb + kbeg) * EB + c * 16;
     }
-  // activation copies: MB = 0 -> lane l takes bytes [4l, 4l+4) of row 0's 256-byte slice;
-  // MB > 0 -> copy t fills rows 4t .. 4t+3, lane l the physical chunk l%16 of row 4t + l/16
-  const uint8_t* asrc[SL::LA];
+  // activation copies: MB = 0 -> lane l takes bytes [4l, 4l+4) of row 0's 256-byte slice (every
+  // wave the whole slice); MB > 0 -> copy t fills rows 4t .. 4t+3, lane l the physical chunk l%16
+  // of row 4t + l/16, and this wave issues copies t = sg + SN*u, u < LAW.
+  const uint8_t* asrc[SL::LAW];
 #pragma unroll
-  for (int t = 0; t < SL::LA; ++t) {
+  for (int u = 0; u < SL::LAW; ++u) {
+    const int t = sg + SN * u;
     if constexpr (MB == 0) {
-      asrc[t] = reinterpret_cast<const uint8_t*>(p.A) + 2L * kbeg + 4 * lane;
+      asrc[u] = reinterpret_cast<const uint8_t*>(p.A) + 2L * kbeg + 4 * lane;
     } else {
       const int m = 4 * t + lane / 16;
       const int c = (lane % 16) ^ (m & 15);
-      asrc[t] = reinterpret_cast<const uint8_t*>(p.A + (long)min(m, p.M - 1) * p.lda) + 2L * kbeg + c * 16;
+      asrc[u] = reinterpret_cast<const uint8_t*>(p.A + (long)min(m, p.M - 1) * p.lda) + 2L * kbeg + c * 16;
     }
   }
-  auto dma = [&](int j) {
+  auto dma_w = [&](int j) {
     const int jj = min(j, n - 1);
-    uint8_t* slot = ring + (j % D) * SLOT;
+    uint8_t* slot = ring + (j % D) * WSTRIDE;
 #pragma unroll
     for (int r = 0; r < RR; ++r)
 #pragma unroll
@@ -952,14 +990,18 @@ __global__ __launch_bounds__(1024) void k_stream_line(StreamArgs p, int G) {
           __builtin_amdgcn_global_load_lds((void*)(wsrc[r][i] + (long)jj * 128 * EB + 128 * h),
                                            (lds_void_stream_t*)(slot + (r * EB + h) * 2048 + i * 1024),
                                            16, 0, 2 /* nt */);
+  };
+  auto dma_a = [&](int j) {
+    const int jj = min(j, n - 1);
+    uint8_t* slot = aslot(j);
 #pragma unroll
-    for (int t = 0; t < SL::LA; ++t) {
+    for (int u = 0; u < SL::LAW; ++u) {
       if constexpr (MB == 0)
-        __builtin_amdgcn_global_load_lds((void*)(asrc[t] + jj * 256), (lds_void_stream_t*)(slot + WSLOT),
-                                         4, 0, 0);
+        __builtin_amdgcn_global_load_lds((void*)(asrc[u] + jj * 256),
+                                         (lds_void_stream_t*)slot, 4, 0, 0);
       else
-        __builtin_amdgcn_global_load_lds((void*)(asrc[t] + jj * 256),
-                                         (lds_void_stream_t*)(slot + WSLOT + t * 1024), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((void*)(asrc[u] + jj * 256),
+                                         (lds_void_stream_t*)(slot + (sg + SN * u) * 1024), 16, 0, 0);
     }
   };
 
@@ -968,7 +1010,13 @@ __global__ __launch_bounds__(1024) void k_stream_line(StreamArgs p, int G) {
 #pragma unroll
     for (int r = 0; r < RR; ++r) rscale[r] = p.scale[row_of(r) + r16];
   }
-  for (int j = 0; j < D; ++j) dma(j);
+  // prologue: copy units in the loop's order -- weights of step j with the activations of step j
+  // (SN = 1) or of step j-1 (SN > 1, the shared ring one step shallower)
+  for (int j = 0; j < D; ++j) {
+    dma_w(j);
+    if (SN == 1) dma_a(j);
+    else if (j >= 1) dma_a(j - 1);
+  }
   if constexpr (BFMT == 2) {  // this wave's zero-points and scales, one group per step
     const long gstride = p.K / 128;
     const int g0 = kbeg / 128;
@@ -980,6 +1028,7 @@ __global__ __launch_bounds__(1024) void k_stream_line(StreamArgs p, int G) {
     }
   }
   __builtin_amdgcn_s_waitcnt(0);  // prologue copies landed, scales and metadata loaded
+  if constexpr (SN > 1) __syncthreads();
 
   f32x4 acc[RR][MBE], acc2[RR][MBE];
 #pragma unroll
@@ -993,9 +1042,11 @@ __global__ __launch_bounds__(1024) void k_stream_line(StreamArgs p, int G) {
 
   for (int j = 0; j < n; ++j) {
     asm volatile("" ::: "memory");
-    s_wait_vm_stream<SL::WAIT>();  // step j has landed
+    s_wait_vm_stream<SL::WAIT>();  // this wave's copies of step j have landed
+    if constexpr (SN > 1) __builtin_amdgcn_s_barrier();  // ... and everyone's
     asm volatile("" ::: "memory");
-    const uint8_t* slot = ring + (j % D) * SLOT;
+    const uint8_t* slot = ring + (j % D) * WSTRIDE;
+    const uint8_t* as = aslot(j);
     u32x4 w[RR][2][2], a[MBE][2][2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {  // the two 64-k halves of the step
@@ -1005,10 +1056,9 @@ __global__ __launch_bounds__(1024) void k_stream_line(StreamArgs p, int G) {
         for (int q = 0; q < 2; ++q) {
           const int c = 8 * h + 2 * kg + q;  // 16-byte chunk of the 256-byte activation slice
           if constexpr (MB == 0)
-            a[b][h][q] = *reinterpret_cast<const u32x4*>(slot + WSLOT + c * 16);
+            a[b][h][q] = *reinterpret_cast<const u32x4*>(as + c * 16);
           else
-            a[b][h][q] = *reinterpret_cast<const u32x4*>(slot + WSLOT + (16 * b + r16) * 256 +
-                                                         ((c ^ r16) * 16));
+            a[b][h][q] = *reinterpret_cast<const u32x4*>(as + (16 * b + r16) * 256 + ((c ^ r16) * 16));
         }
 #pragma unroll
       for (int r = 0; r < RR; ++r) {
@@ -1035,7 +1085,8 @@ __global__ __launch_bounds__(1024) void k_stream_line(StreamArgs p, int G) {
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): slot j is read, it may be refilled
     asm volatile("" ::: "memory");
-    dma(j + D);
+    dma_w(j + D);
+    dma_a(SN == 1 ? j + D : j + D - 1);  // SN > 1: slot (j-1) % D, free since the barrier
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
@@ -1066,24 +1117,48 @@ __global__ __launch_bounds__(1024) void k_stream_line(StreamArgs p, int G) {
 #pragma unroll
     for (int b = 0; b < MBE; ++b) acc[r][b] += acc2[r][b];
 
-  if (p.S > 1) {  // partial sums of the S k chunks, added in wave order by wave 0
+  if (S > 1) {  // partial sums of the S k chunks of each slab, added in chunk order
 #pragma unroll
     for (int r = 0; r < RR; ++r)
 #pragma unroll
       for (int b = 0; b < MBE; ++b) red[((wave * RR + r) * MBE + b) * 64 + lane] = acc[r][b];
     __syncthreads();
-    if (wave != 0) return;
+    if (kc != 0) return;
 #pragma unroll
     for (int r = 0; r < RR; ++r)
 #pragma unroll
       for (int b = 0; b < MBE; ++b) {
-        f32x4 t = red[(r * MBE + b) * 64 + lane];
-        for (int w = 1; w < p.S; ++w) {
-          const f32x4 v = red[((w * RR + r) * MBE + b) * 64 + lane];
+        f32x4 t = red[((sg * RR + r) * MBE + b) * 64 + lane];
+        for (int c = 1; c < S; ++c) {
+          const f32x4 v = red[(((c * SN + sg) * RR + r) * MBE + b) * 64 + lane];
           t[0] += v[0]; t[1] += v[1]; t[2] += v[2]; t[3] += v[3];
         }
         acc[r][b] = t;
       }
   }
-  stream_store<MBE, R, EPI>(p, acc, nbase, r16, kg);
+  if constexpr (PAIRED) {
+    // every wave is past its last ring read (vmcnt 0 above; the barrier below or the reduction's)
+    // so ring memory of chunk 0 carries the up results to their gate partners
+    f32x4* xb = reinterpret_cast<f32x4*>(dsm);
+    if (S == 1) __syncthreads();
+    if (upw) {
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int b = 0; b < MBE; ++b) xb[(((sg - SN / 2) * R + r) * MBE + b) * 64 + lane] = acc[r][b];
+    }
+    __syncthreads();
+    if (upw) return;
+    f32x4 both[2 * R][MBE];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int b = 0; b < MBE; ++b) {
+        both[r][b] = acc[r][b];
+        both[R + r][b] = xb[((sg * R + r) * MBE + b) * 64 + lane];
+      }
+    stream_store<MBE, R, 1>(p, both, nbase, r16, kg);
+  } else {
+    stream_store<MBE, R, EPI>(p, acc, nbase, r16, kg);
+  }
 }

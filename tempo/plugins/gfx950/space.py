@@ -45,7 +45,7 @@ DOMAINS = {
                 GROUP=(4, 8, 16), XCD=(0, 1), WAVES=((2, 2), (2, 4), (4, 2), (4, 4)), MS=(16, 32)),
     "reg": dict(BM=(64, 128, 256), BN=(128, 256), BK=(64,), MS=(16, 32), SWZ=(1, 2), GROUP=(8,),
                 XCD=(1,)),
-    "line": dict(R=(1, 2, 4), D=(2, 3, 4, 5, 6), W=(1024, 2048, 4096)),
+    "line": dict(R=(1, 2, 4), D=(2, 3, 4, 5, 6), W=(1024, 2048, 4096), SN=(1, 2, 4)),
     "ring": dict(R=(1, 2, 4), D=(4, 5, 6, 8, 10, 12, 14, 16)),
     "stream": dict(R=(1, 2, 4), U=(2, 4, 8), ALDS=(0, 1)),
     "shared": dict(R=(1, 2), U=(2, 4), SN=(2, 4, 8)),
@@ -62,32 +62,40 @@ def bfmt(op: OpSpec) -> int:
     return BFMT_OF[key]
 
 
+def line_paired(p: dict) -> bool:
+    """The fused gate/up line kernel with SN >= 2 pairs its slab waves (gate, up)."""
+    return bool(p.get("EPI")) and p.get("SN", 1) >= 2
+
+
 def line_geometry(p: dict):
-    """(copies per step, ring slot bytes) of the line kernel, as skeletons/gemv_stream declares."""
-    rr = 2 * p["R"] if p.get("EPI") else p["R"]
+    """(copies per step per wave, weight slot bytes, activation slot bytes) of the line kernel,
+    as skeletons/gemv_stream declares them."""
+    rr = 2 * p["R"] if p.get("EPI") and not line_paired(p) else p["R"]
     eb = 2 if p["BFMT"] == 0 else 1
-    la = 4 * p["MB"] if p["MB"] else 1
-    slot = rr * eb * 2048 + (p["MB"] * 16 * 256 if p["MB"] else 256)
-    return 2 * rr * eb + la, slot
+    sn = p.get("SN", 1)
+    la = 4 * p["MB"] if p["MB"] else sn
+    return 2 * rr * eb + la // sn, rr * eb * 2048, (p["MB"] * 16 * 256 if p["MB"] else 256)
 
 
 def line_split(N: int, K: int, p: dict):
     """(S, steps per wave, LDS bytes) as the shipped launchers compute them; None if none fits."""
-    rr = 2 * p["R"] if p.get("EPI") else p["R"]
-    slabs = N // (16 * p["R"])
+    rr = 2 * p["R"] if p.get("EPI") and not line_paired(p) else p["R"]
+    sn = p.get("SN", 1)
+    wgs = N // (16 * p["R"] * (sn // 2 if line_paired(p) else sn))
     steps = K // 128
-    _, slot = line_geometry(p)
-    S = max(1, min(16, steps, -(-p["W"] // max(1, slabs))))
+    _, wslot, aslot = line_geometry(p)
+    S = max(1, min(16 // sn, steps, -(-p["W"] // max(1, wgs * sn))))
 
     def lds(s_, per):
         meta = -(-(rr * 16 * per * 3) // 16) * 16 if p["BFMT"] == 2 else 0
-        wave = -(-(p["D"] * slot + meta) // 1024) * 1024
-        return s_ * wave + (s_ * rr * max(1, p["MB"]) * 1024 if s_ > 1 else 0)
+        wave = -(-(p["D"] * (wslot + (aslot if sn == 1 else 0)) + meta) // 1024) * 1024
+        act = -(-(p["D"] * aslot) // 1024) * 1024 if sn > 1 else 0
+        return s_ * (sn * wave + act) + (s_ * sn * rr * max(1, p["MB"]) * 1024 if s_ > 1 else 0)
 
     while True:
         per = -(-steps // S)
         s2 = -(-steps // per)
-        if lds(s2, per) <= LDS_MAX:
+        if lds(s2, per) <= LDS_MAX and (sn == 1 or steps % s2 == 0):
             return s2, per, lds(s2, per)
         if S == 1:
             return None
@@ -157,8 +165,8 @@ def tag(kind: str, p: dict) -> str:
         return "reg_m%dn%dk%d_w%dx%d_f%d_z%d_b%d" % (p["BM"], p["BN"], p["BK"], p["WM"], p["WN"],
                                                    p["MS"], p["SWZ"], p["BFMT"])
     if kind == "line":
-        return "line_mb%d_r%d_d%d_w%d_b%d%s" % (p["MB"], p["R"], p["D"], p["W"], p["BFMT"],
-                                              "_e1" if p.get("EPI") else "")
+        return "line_mb%d_r%d_n%d_d%d_w%d_b%d%s" % (p["MB"], p["R"], p.get("SN", 1), p["D"], p["W"],
+                                                  p["BFMT"], "_e1" if p.get("EPI") else "")
     if kind == "ring":
         return "ring_mb%d_r%d_d%d_b%d" % (p["MB"], p["R"], p["D"], p["BFMT"])
     if kind == "shared":
@@ -215,12 +223,18 @@ def legal(kind: str, p: dict, M: int, N: int, K: int):
     if N % (16 * R):
         return "N %% %d" % (16 * R)
     if kind == "line":
+        sn = p.get("SN", 1)
         if M > max(1, 16 * p["MB"]):
             return "M > 16*MB (MB = 0: M = 1)"
+        sno = sn // 2 if line_paired(p) else sn
+        if N % (16 * R * sno):
+            return "N %% %d" % (16 * R * sno)
         if K % 128 or K > 65536:
             return "K % 128 / K > 65536"
-        L, _ = line_geometry(p)
-        if (p["D"] - 1) * L >= 64 or p["D"] < 2:
+        if (4 * p["MB"] if p["MB"] else sn) % sn or (not p["MB"] and sn not in (1, 2, 4)):
+            return "activation copies do not split over the slab waves"
+        L, _, _ = line_geometry(p)
+        if (p["D"] - 1) * L >= 64 or p["D"] < (3 if sn > 1 else 2):
             return "vmcnt depth"
         if line_split(N, K, p) is None:
             return "LDS"
@@ -264,7 +278,11 @@ def variants(op: OpSpec) -> Iterator[Hyperform]:
         for R in d["R"]:
             for D in d["D"]:
                 for W in d["W"]:
-                    out.append(("line", dict(MB=0 if M == 1 else MB, R=R, D=D, W=W, BFMT=b)))
+                    for SN in d["SN"]:
+                        q = dict(MB=0 if M == 1 else MB, R=R, D=D, W=W, BFMT=b)
+                        if SN > 1:
+                            q["SN"] = SN
+                        out.append(("line", q))
         for R in DOMAINS["ring"]["R"]:
             for D in DOMAINS["ring"]["D"]:
                 out.append(("ring", dict(MB=MB, R=R, D=D, BFMT=b)))

@@ -147,13 +147,14 @@ def test_route_unknown_op_is_empty():
 def test_rows_fall_through_when_the_first_row_does_not_fit():
     from cuda_tempiler_amd import capi
 
-    assert capi.route(0, 8, 15360, 3840) == "l1r1d3"
+    assert capi.route(0, 8, 15360, 3840) == "l1r1n4d3"
+    assert capi.route(0, 8, 12304, 3840) == "l1r1d4"      # N % 64 != 0: the unshared line row
     assert capi.route(0, 8, 15360, 65792) == "h16r1u4n4"  # K > 65536: past the line rows
     assert capi.route(0, 8, 12304, 65792) == "s16r1u4"    # ... and N % 64 != 0
-    assert capi.route(1, 16, 34816, 5120) == "l1r2d4"
-    assert capi.route(2, 16, 34816, 5120) == "l1r2d4"
-    assert capi.route(1, 32, 34816, 5120) == "l2r2d3"
-    assert capi.route(2, 32, 34816, 5120) == "h32r1u4n4"  # the M <= 32 line row is int8 only
+    assert capi.route(1, 16, 34816, 5120) == "l1r1n4d3"
+    assert capi.route(2, 16, 5120, 17408) == "l1r1n2d4"
+    assert capi.route(1, 32, 34816, 5120) == "l2r1n4d4"
+    assert capi.route(2, 32, 34816, 65536 + 256) == "h32r1u4n4"
     assert capi.route(0, 1, 15360, 3840) == "l0r1d3"
     assert capi.route(1, 1, 5120, 5120) == "l0r1d4"
     assert capi.route(1, 1, 5120, 65536 + 512) == "s1a_r1u8"
