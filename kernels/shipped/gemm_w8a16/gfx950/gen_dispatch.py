@@ -55,6 +55,8 @@ def condition(sel, kind, p, m_max, n_min=0, gate_up=False):
         sno = p.get("SN", 1) // 2 if gate_up and p.get("SN", 1) >= 2 else p.get("SN", 1)
         fit = "(p.N %% %d) == 0 && (p.K %% %d) == 0 && p.K <= %d" % (
             sel.STREAM_N_ROWS * p["R"] * sno, sel.LINE_K_STEP, sel.LINE_K_MAX)
+        if "NMAX" in p:
+            fit += " && p.N < %d" % p["NMAX"]
     elif kind == "stream":
         fit = "(p.N %% %d) == 0 && (p.K %% %d) == 0" % (sel.STREAM_N_ROWS * p["R"],
                                                           sel.STREAM_K_STEP * p["U"])

@@ -135,16 +135,16 @@ inline hipError_t launch_shared(const W8A16Params& p, hipStream_t s) {
 }
 
 // k split of the line kernel (k_stream_line): `wgs` workgroups of SN slab waves, each split
-// into S k chunks of whole 128-k steps -- about `waves` waves over the part, at most 1024
-// threads per workgroup, equal chunks when the slab waves share the activation ring (SN > 1:
+// into S k chunks of whole 128-k steps -- about `waves` waves over the part, at most `tpb`
+// threads per workgroup (the kernel's launch bound), equal chunks when the slab waves share the activation ring (SN > 1:
 // they pass the same barriers), the workgroup's rings (+ the fmt 2 metadata and the reduction)
 // within the 160 KiB of LDS.  false: no split fits (the caller's own path).
 template <class SL>
 inline bool line_split(int wgs, int SN, int K, int waves, int* S_out, int* chunk_out, int* G_out,
-                       size_t* lds_out) {
+                       size_t* lds_out, int tpb = 1024) {
   const int steps = K / 128;
   int S = (waves + wgs * SN - 1) / (wgs * SN);
-  if (S > 16 / SN) S = 16 / SN;
+  if (S > tpb / 64 / SN) S = tpb / 64 / SN;
   if (S > steps) S = steps;
   if (S < 1) S = 1;
   for (;; --S) {
@@ -173,10 +173,11 @@ inline hipError_t launch_line_fmt(const W8A16Params& p, hipStream_t s) {
   int G = 0;
   size_t lds = 0;
   const int wgs = p.N / (16 * R * SL::SNO);  // output slabs / per workgroup
-  if (!line_split<SL>(wgs, SN, p.K, WAVES, &a.S, &a.chunk, &G, &lds))
+  constexpr int TPB = MB >= 4 ? 512 : 1024;  // many activation blocks: 256 VGPRs per lane
+  if (!line_split<SL>(wgs, SN, p.K, WAVES, &a.S, &a.chunk, &G, &lds, TPB))
     return hipErrorInvalidConfiguration;
-  hipLaunchKernelGGL((k_stream_line<MB, R, D, BFMT, EPI, SN>), dim3(wgs), dim3(64 * SN * a.S), lds,
-                     s, a, G);
+  hipLaunchKernelGGL((k_stream_line<MB, R, D, BFMT, EPI, SN, TPB>), dim3(wgs),
+                     dim3(64 * SN * a.S), lds, s, a, G);
   return hipGetLastError();
 }
 

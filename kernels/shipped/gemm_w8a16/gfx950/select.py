@@ -32,6 +32,9 @@ LADDER = [
     (32, 16384, "h32r1u4n4", "shared", dict(MB=2, R=1, U=4, SN=4)),
     (32, 0, "h32r1u4n2", "shared", dict(MB=2, R=1, U=4, SN=2, TPB=512)),
     (32, 0, "s32r2u4", "stream", dict(MB=2, R=2, U=4, A=0)),
+    (64, 12288, "l4r1n4d3", "line", dict(MB=4, R=1, D=3, SN=4, W=2048)),
+    (64, 0, "l4r1n2d3", "line", dict(MB=4, R=1, D=3, SN=2, W=2048)),
+    (128, 0, "l8r1n2d3", "line", dict(MB=8, R=1, D=3, SN=2, W=2048, NMAX=12288)),
     (256, 0, "m128x128k64", "mfma",
      dict(BM=128, BN=128, BK=64, WM=2, WN=2, MS=32, SWZ=1, GROUP=8, XCD=1)),
     (1 << 30, 0, "m256x256k64", "mfma",
@@ -79,9 +82,9 @@ def _fits_gate_up(kind, p, M, N, K):
 
 
 def _fits(kind, p, M, N, K):
-    if kind == "line":
+    if kind == "line":  # NMAX (optional): the row holds narrower N only
         return (N % (STREAM_N_ROWS * p["R"] * p.get("SN", 1)) == 0 and K % LINE_K_STEP == 0
-                and K <= LINE_K_MAX)
+                and K <= LINE_K_MAX and N < p.get("NMAX", 1 << 30))
     if kind == "stream":
         return N % (STREAM_N_ROWS * p["R"]) == 0 and K % (STREAM_K_STEP * p["U"]) == 0
     if kind == "shared":

@@ -43,7 +43,7 @@ _ENTRY = {
             "const _Float16*, const void*, const _Float16*, const uint8_t*, _Float16*, int, int, "
             "int, int, int, int, int",
             ("common/cdna4.h", "gemm_mfma/kernel.hip")),
-    "line": ("k_stream_line", ("MB", "R", "D", "BFMT", "EPI", "SN"), "StreamArgs, int",
+    "line": ("k_stream_line", ("MB", "R", "D", "BFMT", "EPI", "SN", "TPB"), "StreamArgs, int",
              ("common/cdna4.h", "gemv_stream/kernel.hip")),
     "ring": ("k_stream_dma", ("MB", "R", "D", "BFMT"), "StreamArgs",
              ("common/cdna4.h", "gemv_stream/kernel.hip")),
@@ -60,12 +60,14 @@ NAMESPACE = "tempo::gen"
 KIND_FLAGS = {"ilv": ("-mllvm", "-amdgpu-sched-strategy=iterative-minreg")}
 # trailing template parameters with a default in the skeleton: named only when the hyperform
 # sets them (EPI = 1 is the fused gate/up epilogue of the decode kernels)
-_OPTIONAL = frozenset({"EPI", "SN"})
+_OPTIONAL = frozenset({"EPI", "SN", "TPB"})
+# default of an optional parameter left out in front of one that is named
+_DEFAULT = {"EPI": 0, "SN": 1, "TPB": 1024}
 
 
 def _order(kind: str, p: dict) -> tuple:
     """Template parameters to name: every required one, and the optional (defaulted, trailing)
-    ones up to the last the hyperform sets -- an earlier unset one is named with its default 0."""
+    ones up to the last the hyperform sets -- an earlier unset one is named with its default."""
     names = _ENTRY[kind][1]
     last = max((i for i, k in enumerate(names) if k in p or k not in _OPTIONAL), default=-1)
     return tuple(names[:last + 1])
@@ -205,7 +207,7 @@ class Gfx950Skeletons:
             sp = space.line_split(N, int(op.shapes["K"]), p)
             grid = N // (16 * p["R"] * (p["SN"] // 2 if space.line_paired(p) else p.get("SN", 1)))
             threads = 64 * p.get("SN", 1) * (sp[0] if sp else 1)
-            bound = 1024  # k_stream_line: __launch_bounds__(1024)
+            bound = p.get("TPB", 1024)  # k_stream_line: __launch_bounds__(TPB)
         else:
             S, _ = self._split(op, p)
             grid = N // (16 * p["R"])
@@ -293,7 +295,7 @@ class Gfx950Skeletons:
                  "namespace gen {\n\n")
         inst = ("\n// explicit instantiation: the one kernel this file exists to contain\n"
                 "template __global__ void %s<%s>(%s);\n"
-                % (sym, ", ".join(str(int(p.get(k, 0))) for k in order), args))
+                % (sym, ", ".join(str(int(p.get(k, _DEFAULT.get(k, 0)))) for k in order), args))
         src = head + "".join(body) + inst + "\n}  // namespace gen\n}  // namespace tempo\n"
         return Rendered(source=src, launch=self.launch_of(op, h), includes=(),
                         notes="namespace wrap + one explicit instantiation; logic lives in the skeleton",
@@ -306,6 +308,6 @@ class Gfx950Skeletons:
         order = _order(p["kind"], p)
         vals = []
         for k in order:
-            v = p.get(k, 0)
+            v = p.get(k, _DEFAULT.get(k, 0))
             vals.append("true" if v is True else "false" if v is False else str(int(v)))
         return "%s::%s<%s>" % (NAMESPACE, sym, ", ".join(vals))

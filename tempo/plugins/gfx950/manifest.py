@@ -74,10 +74,13 @@ def hyper_params(kind, p, fmt, epi=0):
     same kernel, named the way space.variants() names it."""
     pk = {"stream": "stream", "mfma": "reg", "dma": "dma", "shared": "shared", "ilv": "ilv",
           "line": "line"}[kind]
-    params = {k: v for k, v in p.items() if k != "fmts"}
+    params = {k: v for k, v in p.items() if k not in ("fmts", "NMAX")}
     params["kind"] = pk
     if pk == "shared":
         params.setdefault("TPB", 1024)
+    if pk == "line" and params["MB"] >= 4:  # the shipped launchers bound these at 512 threads
+        params.setdefault("SN", 1)
+        params["TPB"] = 512
     if pk not in ("dma", "ilv"):
         params["BFMT"] = fmt
     if pk == "stream":
@@ -253,6 +256,8 @@ def make(op, rows_files=()):
         elif kind == "line":
             fit = "N %% %d == 0 and K %% %d == 0 and K <= %d" % (
                 sel.STREAM_N_ROWS * p["R"] * p.get("SN", 1), sel.LINE_K_STEP, sel.LINE_K_MAX)
+            if "NMAX" in p:
+                fit += " and N < %d" % p["NMAX"]
         else:
             fit = "N %% %d == 0 and K %% %d == 0" % (p["BN"], p["BK"])
         man["dispatch" if not epi else "dispatch_gate_up"].append(dict(

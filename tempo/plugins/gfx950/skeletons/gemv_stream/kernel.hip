@@ -919,8 +919,8 @@ struct StreamLine {
 
 __device__ __forceinline__ int line_key(int row16) { return (row16 >> 1) & 7; }
 
-template <int MB, int R, int D, int BFMT, int EPI = 0, int SN = 1>
-__global__ __launch_bounds__(1024) void k_stream_line(StreamArgs p, int G) {
+template <int MB, int R, int D, int BFMT, int EPI = 0, int SN = 1, int TPB = 1024>
+__global__ __launch_bounds__(TPB) void k_stream_line(StreamArgs p, int G) {
   using SL = StreamLine<MB, R, D, BFMT, EPI, SN>;
   constexpr int RR = SL::RR, EB = SL::EB, MBE = SL::MBE, WSLOT = SL::WSLOT, ASLOT = SL::ASLOT;
   constexpr int WSTRIDE = SN == 1 ? WSLOT + ASLOT : WSLOT;  // bytes per ring slot of a wave
@@ -1040,6 +1040,40 @@ __global__ __launch_bounds__(1024) void k_stream_line(StreamArgs p, int G) {
     }
   const int key = line_key(r16);
 
+  // fragments of half h of step j (weights of every row group, activations of every block)
+  auto read_w = [&](const uint8_t* slot, int r, int h, u32x4 (&w)[2]) {
+    if constexpr (BFMT == 0) {
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+        w[q] = *reinterpret_cast<const u32x4*>(slot + (r * 2 + h) * 2048 + r16 * 128 +
+                                               (((2 * kg + q) ^ key) * 16));
+    } else {
+      w[0] = *reinterpret_cast<const u32x4*>(slot + r * 2048 + r16 * 128 + (((4 * h + kg) ^ key) * 16));
+    }
+  };
+  auto read_a = [&](const uint8_t* as, int b, int h, u32x4 (&a)[2]) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int c = 8 * h + 2 * kg + q;  // 16-byte chunk of the 256-byte activation slice
+      if constexpr (MB == 0)
+        a[q] = *reinterpret_cast<const u32x4*>(as + c * 16);
+      else
+        a[q] = *reinterpret_cast<const u32x4*>(as + (16 * b + r16) * 256 + ((c ^ r16) * 16));
+    }
+  };
+  auto dequant = [&](const u32x4 (&w)[2], int r, uint8_t z, _Float16 sc, f16x8& w0, f16x8& w1) {
+    if constexpr (BFMT == 0) {
+      w0 = as_f16x8(w[0]);
+      w1 = as_f16x8(w[1]);
+    } else if constexpr (BFMT == 1) {
+      w0 = dequant8_i8(w[0][0], w[0][1], rscale[r]);
+      w1 = dequant8_i8(w[0][2], w[0][3], rscale[r]);
+    } else {
+      w0 = dequant8_u8(w[0][0], w[0][1], z, sc);
+      w1 = dequant8_u8(w[0][2], w[0][3], z, sc);
+    }
+  };
+
   for (int j = 0; j < n; ++j) {
     asm volatile("" ::: "memory");
     s_wait_vm_stream<SL::WAIT>();  // this wave's copies of step j have landed
@@ -1047,32 +1081,6 @@ __global__ __launch_bounds__(1024) void k_stream_line(StreamArgs p, int G) {
     asm volatile("" ::: "memory");
     const uint8_t* slot = ring + (j % D) * WSTRIDE;
     const uint8_t* as = aslot(j);
-    u32x4 w[RR][2][2], a[MBE][2][2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {  // the two 64-k halves of the step
-#pragma unroll
-      for (int b = 0; b < MBE; ++b)
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-          const int c = 8 * h + 2 * kg + q;  // 16-byte chunk of the 256-byte activation slice
-          if constexpr (MB == 0)
-            a[b][h][q] = *reinterpret_cast<const u32x4*>(as + c * 16);
-          else
-            a[b][h][q] = *reinterpret_cast<const u32x4*>(as + (16 * b + r16) * 256 + ((c ^ r16) * 16));
-        }
-#pragma unroll
-      for (int r = 0; r < RR; ++r) {
-        if constexpr (BFMT == 0) {
-#pragma unroll
-          for (int q = 0; q < 2; ++q)
-            w[r][h][q] = *reinterpret_cast<const u32x4*>(slot + (r * 2 + h) * 2048 + r16 * 128 +
-                                                         (((2 * kg + q) ^ key) * 16));
-        } else {
-          w[r][h][0] = *reinterpret_cast<const u32x4*>(slot + r * 2048 + r16 * 128 +
-                                                       (((4 * h + kg) ^ key) * 16));
-        }
-      }
-    }
     uint8_t z[RR];
     _Float16 sc[RR];
     if constexpr (BFMT == 2) {
@@ -1082,34 +1090,62 @@ __global__ __launch_bounds__(1024) void k_stream_line(StreamArgs p, int G) {
         sc[r] = meta_s[(16 * r + r16) * G + j];
       }
     }
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): slot j is read, it may be refilled
-    asm volatile("" ::: "memory");
-    dma_w(j + D);
-    dma_a(SN == 1 ? j + D : j + D - 1);  // SN > 1: slot (j-1) % D, free since the barrier
+    if constexpr (MB <= 2) {
+      // early reads: every fragment of the step into registers, then the slot is refilled while
+      // the MFMAs run
+      u32x4 w[RR][2][2], a[MBE][2][2];
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+      for (int h = 0; h < 2; ++h) {
 #pragma unroll
-      for (int r = 0; r < RR; ++r) {
-        f16x8 w0, w1;
-        if constexpr (BFMT == 0) {
-          w0 = as_f16x8(w[r][h][0]);
-          w1 = as_f16x8(w[r][h][1]);
-        } else if constexpr (BFMT == 1) {
-          const u32x4 v = w[r][h][0];
-          w0 = dequant8_i8(v[0], v[1], rscale[r]);
-          w1 = dequant8_i8(v[2], v[3], rscale[r]);
-        } else {
-          const u32x4 v = w[r][h][0];
-          w0 = dequant8_u8(v[0], v[1], z[r], sc[r]);
-          w1 = dequant8_u8(v[2], v[3], z[r], sc[r]);
+        for (int b = 0; b < MBE; ++b) read_a(as, b, h, a[b][h]);
+#pragma unroll
+        for (int r = 0; r < RR; ++r) read_w(slot, r, h, w[r][h]);
+      }
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): slot j is read, it may be refilled
+      asm volatile("" ::: "memory");
+      dma_w(j + D);
+      dma_a(SN == 1 ? j + D : j + D - 1);  // SN > 1: slot (j-1) % D, free since the barrier
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int r = 0; r < RR; ++r) {
+          f16x8 w0, w1;
+          dequant(w[r][h], r, z[r], sc[r], w0, w1);
+#pragma unroll
+          for (int b = 0; b < MBE; ++b) {
+            acc[r][b] = Mfma<16>::run(w0, as_f16x8(a[b][h][0]), acc[r][b]);
+            acc2[r][b] = Mfma<16>::run(w1, as_f16x8(a[b][h][1]), acc2[r][b]);
+          }
         }
+    } else {
+      // late reads (many activation blocks): half by half, fragments read just before their
+      // MFMAs; the slot is refilled once both halves are done
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        u32x4 w[RR][2];
+#pragma unroll
+        for (int r = 0; r < RR; ++r) read_w(slot, r, h, w[r]);
+        f16x8 w0[RR], w1[RR];
+#pragma unroll
+        for (int r = 0; r < RR; ++r) dequant(w[r], r, z[r], sc[r], w0[r], w1[r]);
 #pragma unroll
         for (int b = 0; b < MBE; ++b) {
-          acc[r][b] = Mfma<16>::run(w0, as_f16x8(a[b][h][0]), acc[r][b]);
-          acc2[r][b] = Mfma<16>::run(w1, as_f16x8(a[b][h][1]), acc2[r][b]);
+          u32x4 a[2];
+          read_a(as, b, h, a);
+#pragma unroll
+          for (int r = 0; r < RR; ++r) {
+            acc[r][b] = Mfma<16>::run(w0[r], as_f16x8(a[0]), acc[r][b]);
+            acc2[r][b] = Mfma<16>::run(w1[r], as_f16x8(a[1]), acc2[r][b]);
+          }
         }
       }
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): slot j is read, it may be refilled
+      asm volatile("" ::: "memory");
+      dma_w(j + D);
+      dma_a(SN == 1 ? j + D : j + D - 1);
+    }
   }
   s_wait_vm_stream<0>();  // the copies past the end land before the LDS is reused
 #pragma unroll

@@ -84,7 +84,8 @@ def line_split(N: int, K: int, p: dict):
     wgs = N // (16 * p["R"] * (sn // 2 if line_paired(p) else sn))
     steps = K // 128
     _, wslot, aslot = line_geometry(p)
-    S = max(1, min(16 // sn, steps, -(-p["W"] // max(1, wgs * sn))))
+    tpb = p.get("TPB", 1024)  # the kernel's launch bound
+    S = max(1, min(tpb // 64 // sn, steps, -(-p["W"] // max(1, wgs * sn))))
 
     def lds(s_, per):
         meta = -(-(rr * 16 * per * 3) // 16) * 16 if p["BFMT"] == 2 else 0
@@ -272,8 +273,8 @@ def variants(op: OpSpec) -> Iterator[Hyperform]:
     M, N, K = int(op.shapes["M"]), int(op.shapes["N"]), int(op.shapes["K"])
     b = bfmt(op)
     out = []
-    if M <= 32:
-        MB = 1 if M <= 16 else 2
+    if M <= 128:
+        MB = 1 if M <= 16 else 2 if M <= 32 else 4 if M <= 64 else 8
         d = DOMAINS["line"]
         for R in d["R"]:
             for D in d["D"]:
@@ -282,7 +283,12 @@ def variants(op: OpSpec) -> Iterator[Hyperform]:
                         q = dict(MB=0 if M == 1 else MB, R=R, D=D, W=W, BFMT=b)
                         if SN > 1:
                             q["SN"] = SN
+                        if MB >= 4 and M > 32:  # the shipped launchers' bound: 256 VGPRs
+                            q["SN"] = SN
+                            q["TPB"] = 512
                         out.append(("line", q))
+    if M <= 32:
+        MB = 1 if M <= 16 else 2
         for R in DOMAINS["ring"]["R"]:
             for D in DOMAINS["ring"]["D"]:
                 out.append(("ring", dict(MB=MB, R=R, D=D, BFMT=b)))
