@@ -19,7 +19,7 @@ route around libtempo_gfx950.so.
     y = torch.ops.tempo.linear_fp16(x, w)              # x [..., K] fp16, w [N, K] fp16
     y = torch.ops.tempo.linear_w8a16(x, wq, s, z, 2, 128)
     h = torch.ops.tempo.linear_gate_up_fp16(x, w_gate_up)   # silu(x.Wg^T) * (x.Wu^T), fused
-    tops.counters()                                     # {"d256x256k64w16m16": 3, "off": 1, ...}
+    tops.counters()                                     # {"i256x256k64w4r8": 3, "off": 1, ...}
 """
 from __future__ import annotations
 
