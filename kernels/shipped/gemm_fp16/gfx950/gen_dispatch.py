@@ -72,8 +72,9 @@ def condition(sel, kind, p, m_max, n_min=0, gate_up=False):
         spw = p["SN"] // 2 if gate_up else p["SN"]  # gate/up: the slab waves pair up
         fit = "(p.N %% %d) == 0 && (p.K %% %d) == 0" % (sel.STREAM_N_ROWS * p["R"] * spw,
                                                           sel.STREAM_K_STEP * p["U"])
-    elif kind == "ilv":  # an even number of 32-k substeps
-        fit = "(p.N %% %d) == 0 && (p.K %% %d) == 0" % (p["BN"], max(64, p["BK"]))
+    elif kind == "ilv":  # an even number of 32-k substeps; 31-bit panel byte offsets
+        fit = "(p.N %% %d) == 0 && (p.K %% %d) == 0 && p.lda <= %d && p.ldb <= %d" % (
+            p["BN"], max(64, p["BK"]), sel.ilv_ld_max(p), sel.ilv_ld_max(p))
     else:
         fit = "(p.N %% %d) == 0 && (p.K %% %d) == 0" % (p["BN"], p["BK"])
     band = "p.M <= %d" % m_max

@@ -79,12 +79,18 @@ def _fits_gate_up(kind, p, M, N, K):
     return _fits(kind, p, M, N, K)
 
 
+def ilv_ld_max(p):
+    """Largest leading dimension the interleaved kernel takes: its copies address a BM- or
+    BN-row panel with 31-bit byte offsets."""
+    return (2 ** 31 - 1) // (2 * max(p["BM"], p["BN"]))
+
+
 def _fits(kind, p, M, N, K):
     if kind == "line":  # NMAX (optional): the row holds narrower N only
         return (N % (STREAM_N_ROWS * p["R"] * p.get("SN", 1)) == 0 and K % LINE_K_STEP == 0
                 and K <= LINE_K_MAX and N < p.get("NMAX", 1 << 30))
     if kind == "ilv":
-        return N % p["BN"] == 0 and K % max(64, p["BK"]) == 0
+        return N % p["BN"] == 0 and K % max(64, p["BK"]) == 0 and K <= ilv_ld_max(p)
     if kind == "stream":
         return N % (STREAM_N_ROWS * p["R"]) == 0 and K % (STREAM_K_STEP * p["U"]) == 0
     if kind == "shared":

@@ -265,7 +265,8 @@ class Gfx950Skeletons:
                               footprint={"LDS": float(lds_rd * reps)},
                               latency=_M.rate("LATENCY.LDS").value))
         atoms.append(Atom(uid=2, kind=AtomKind.XFER_ISSUE,
-                          op_id=("global_load_lds_dwordx4" if kind in ("dma", "ring", "ilv", "line")
+                          op_id=("buffer_load_dwordx4 lds" if kind == "ilv" else
+                                 "global_load_lds_dwordx4" if kind in ("dma", "ring", "line")
                                  else "global_load_dwordx4"),
                           footprint={"VMEM": float(vmem * reps)},
                           latency=_M.rate("LATENCY.VMEM").value, token="copy"))

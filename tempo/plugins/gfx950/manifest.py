@@ -252,7 +252,8 @@ def make(op, rows_files=()):
             fit = "N %% %d == 0 and K %% %d == 0" % (sel.STREAM_N_ROWS * p["R"] * spw,
                                                     sel.STREAM_K_STEP * p["U"])
         elif kind == "ilv":
-            fit = "N %% %d == 0 and K %% %d == 0" % (p["BN"], max(64, p["BK"]))
+            fit = "N %% %d == 0 and K %% %d == 0 and K <= %d" % (p["BN"], max(64, p["BK"]),
+                                                                 sel.ilv_ld_max(p))
         elif kind == "line":
             fit = "N %% %d == 0 and K %% %d == 0 and K <= %d" % (
                 sel.STREAM_N_ROWS * p["R"] * p.get("SN", 1), sel.LINE_K_STEP, sel.LINE_K_MAX)

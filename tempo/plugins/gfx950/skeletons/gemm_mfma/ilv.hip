@@ -25,15 +25,39 @@
 // than every copy a later wait counts, so the vmcnt arithmetic is unchanged, and the kernel
 // drains them (vmcnt 0) before the epilogue, so no copy lands after the workgroup has left.
 //
+// Copies are buffer loads with an LDS destination (buffer_load_dwordx4 ... lds): the resource
+// descriptor (SGPRs) points at this tile's A or B panel, each copy's per-lane byte offset is a
+// loop constant and the k offset goes in the scalar offset, so a copy costs no vector address
+// arithmetic (the 64-bit per-copy address adds of the global form took VALU issue slots next to
+// the MFMAs).
+//
+// Epilogue: where the C tile fits the stages (and a C row is a power of two of at least 256
+// bytes), it goes through LDS (free by then) -- fp16 values written in the MFMA layout into a
+// row-major image whose 16-byte chunks are XOR-swizzled by row, read back as whole rows and
+// written out with 16-byte nontemporal stores, eight lanes per 128-byte line.  Stored straight
+// from the MFMA layout, each row gets 32-byte pieces per instruction, and those partial-line
+// writes took twice as long (8 us against 4 us per 256 x 256 tile).
+//
 // Requirements (applicable() + the ladder): N % BN == 0, K % 64 == 0 (an even number of
-// substeps), 16-byte aligned rows.  M is predicated: A rows past M-1 are re-read from row M-1
-// and never stored.
+// substeps), 16-byte aligned rows of A and B, C and ldc 8-byte aligned, panel byte offsets below
+// 2^31 (BM*lda*2, BN*ldb*2).  M is predicated: A rows past M-1 are re-read from row M-1 and
+// never stored.
 //
 // Build: this kernel is compiled with -mllvm -amdgpu-sched-strategy=iterative-minreg (its own
 // translation unit).  The default pre-RA scheduler reorders the 256 accumulator chains of a
 // 128 x 128 wave tile such that the register allocator no longer keeps each accumulator in one
 // AGPR tuple, and the loop fills with v_accvgpr_read/write/mov copies.
 // ============================================================================================
+// 16-byte-per-lane buffer load into LDS: lane l's 16 bytes at byte offset voff + soff of the
+// raw buffer [base, base + nrec) land at lds + 16 l.  (A helper function rather than inline in
+// the kernel's lambdas: inside a lambda of a kernel template the host pass drops the kernel's
+// launch stub.)
+__device__ __forceinline__ void buf_lds16(const void* base, int nrec, void* lds, int voff, int soff) {
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, nrec, 0x00020000);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)lds, 16, voff, soff, 0, 0);
+}
+
 template <int BM, int BN, int BK, int WM, int WN, int STAGES, int GROUP, int XCD, int RSP>
 __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv(
     const _Float16* __restrict__ A, const _Float16* __restrict__ B, _Float16* __restrict__ C,
@@ -73,18 +97,25 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv(
   const int m0 = tmi * BM, n0 = tni * BN;
 
   // Copy d of this wave fills 1 KiB block (ib*NW + wave) of the A (d < A_BLK) or B tile; lane l
-  // fetches the 16-byte chunk that belongs at LDS slot l (the swizzle is an involution).
+  // fetches the 16-byte chunk that belongs at LDS slot l (the swizzle is an involution).  The
+  // buffers start at the tile's panels; A rows past M-1 are clamped to row M-1.
   const int crow = wave * RPB + lane / CPR;                       // tile row of block ib = 0
   const int cchunk = lds_chunk<BK, SWZ>(crow, lane % CPR) * 8;    // element offset in the row
-  const _Float16* srcB0 = B + (long)(n0 + crow) * ldb + cchunk;
+  const _Float16* panelA = A + (long)m0 * lda;
+  const _Float16* panelB = B + (long)n0 * ldb;
+  const int nrecA = min(M - m0, BM) * lda * 2, nrecB = BN * ldb * 2;
+  int voff[L];
+#pragma unroll
+  for (int d = 0; d < L; ++d) {
+    const bool isA = d < A_BLK;
+    const int r = crow + (isA ? d : d - A_BLK) * NW * RPB;
+    voff[d] = isA ? (min(r, M - 1 - m0) * lda + cchunk) * 2 : (r * ldb + cchunk) * 2;
+  }
   auto dma = [&](int kt, int ksrc, int d) {
     const bool isA = d < A_BLK;
     const int ib = isA ? d : d - A_BLK;
     _Float16* dst = smem + (kt % STAGES) * STAGE + (isA ? 0 : BM * BK) + (ib * NW + wave) * RPB * BK;
-    const _Float16* g =
-        isA ? A + (long)min(m0 + crow + ib * NW * RPB, M - 1) * lda + cchunk
-            : srcB0 + (long)ib * NW * RPB * ldb;
-    __builtin_amdgcn_global_load_lds((void*)(g + ksrc * BK), (lds_void_t*)dst, 16, 0, 0);
+    buf_lds16(isA ? panelA : panelB, isA ? nrecA : nrecB, dst, voff[d], ksrc * BK * 2);
   };
 
   typename MF::acc_t acc[TM][TN];
@@ -177,20 +208,65 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv(
   }
   s_wait_vm<0>();  // the refills past the end land before the workgroup's LDS is released
 
-  // ---- epilogue: each lane owns 4 consecutive n of one m per MFMA block ---------------------
+  // ---- epilogue ------------------------------------------------------------------------------
+  // Rows are written out in 16-byte pieces when C and ldc allow it, else in 8-byte halves.
+  const bool c16 = ((reinterpret_cast<uintptr_t>(C) | (uintptr_t)ldc * 2) & 15) == 0;
+  auto store16 = [&](_Float16* dst, const u32x4& v) {
+    if (c16) {
+      __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(dst));
+    } else {
+      __builtin_nontemporal_store(u32x2{v[0], v[1]}, reinterpret_cast<u32x2*>(dst));
+      __builtin_nontemporal_store(u32x2{v[2], v[3]}, reinterpret_cast<u32x2*>(dst + 4));
+    }
+  };
+  constexpr int RB = BN * 2;                  // bytes per C row
+  constexpr int CPRW = RB / 16;               // 16-byte chunks per C row
+  constexpr bool LDS_EPI = BM * BN <= STAGES * STAGE && CPRW >= 16 && (CPRW & (CPRW - 1)) == 0 &&
+                           (NW * 64) % CPRW == 0;
+  if constexpr (LDS_EPI) {
+    // The C tile through LDS (the stages are free by then): a row-major fp16 image whose 16-byte
+    // chunk c of row r sits at chunk c ^ (r % 16), so the 16 rows of an MFMA block write to 16
+    // distinct bank groups and a row's chunks read back conflict-free; then whole rows out.
+    constexpr int RPP = NW * 64 / CPRW;       // C rows per pass of the whole workgroup
+    __syncthreads();                          // every wave is done with the stages
+    uint8_t* cs = reinterpret_cast<uint8_t*>(smem);
 #pragma unroll
-  for (int i = 0; i < TM; ++i) {
-    const int m = m0 + wm * WTM + i * 16 + fr;
-    if (m >= M) continue;
+    for (int i = 0; i < TM; ++i) {
+      const int r = wm * WTM + i * 16 + fr;
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int n = n0 + wn * WTN + j * 16 + 4 * fk;
-      f16x4 o;
-      o[0] = (_Float16)acc[i][j][0];
-      o[1] = (_Float16)acc[i][j][1];
-      o[2] = (_Float16)acc[i][j][2];
-      o[3] = (_Float16)acc[i][j][3];
-      *reinterpret_cast<f16x4*>(C + (long)m * ldc + n) = o;
+      for (int j = 0; j < TN; ++j) {
+        const int cb = (wn * WTN + j * 16 + 4 * fk) * 2;  // byte offset of the lane's 4 values
+        f16x4 o;
+        o[0] = (_Float16)acc[i][j][0];
+        o[1] = (_Float16)acc[i][j][1];
+        o[2] = (_Float16)acc[i][j][2];
+        o[3] = (_Float16)acc[i][j][3];
+        *reinterpret_cast<f16x4*>(cs + r * RB + (((cb >> 4) ^ (r & 15)) << 4) + (cb & 15)) = o;
+      }
+    }
+    __syncthreads();
+#pragma unroll 4
+    for (int p = 0; p < BM / RPP; ++p) {
+      const int r = p * RPP + tid / CPRW, c = tid % CPRW;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(cs + r * RB + ((c ^ (r & 15)) << 4));
+      if (m0 + r < M) store16(C + (long)(m0 + r) * ldc + n0 + c * 8, v);
+    }
+  } else {
+    // straight from the MFMA layout: each lane owns 4 consecutive n of one m per block
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int m = m0 + wm * WTM + i * 16 + fr;
+      if (m >= M) continue;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int n = n0 + wn * WTN + j * 16 + 4 * fk;
+        f16x4 o;
+        o[0] = (_Float16)acc[i][j][0];
+        o[1] = (_Float16)acc[i][j][1];
+        o[2] = (_Float16)acc[i][j][2];
+        o[3] = (_Float16)acc[i][j][3];
+        *reinterpret_cast<f16x4*>(C + (long)m * ldc + n) = o;
+      }
     }
   }
 }
