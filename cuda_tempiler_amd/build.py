@@ -40,6 +40,7 @@ UNITS = [
     os.path.join(SHIPPED, "gemm_fp16", "gfx950", "launch.hip"),
     os.path.join(SHIPPED, "gemm_fp16", "gfx950", "launch_prefill.hip"),
     os.path.join(SHIPPED, "gemm_w8a16", "gfx950", "launch.hip"),
+    os.path.join(SHIPPED, "gemm_w8a16", "gfx950", "launch_prefill.hip"),
     os.path.join(HERE, "csrc", "fmha.hip"),
     os.path.join(HERE, "csrc", "gptq.hip"),
     os.path.join(HERE, "csrc", "capi.hip"),
@@ -55,8 +56,7 @@ def regenerate() -> None:
     for op in ("gemm_fp16", "gemm_w8a16"):
         d = os.path.join(SHIPPED, op, "gfx950")
         gens = [("dispatch.inc", []), ("dispatch_gate_up.inc", ["--gate-up"])]
-        if op == "gemm_fp16":
-            gens.append(("prefill.inc", ["--prefill"]))
+        gens.append(("prefill.inc", ["--prefill"]))
         for name, args in gens:
             text = subprocess.run([sys.executable, os.path.join(d, "gen_dispatch.py")] + args,
                                   check=True, capture_output=True, text=True).stdout

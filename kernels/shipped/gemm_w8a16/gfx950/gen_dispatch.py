@@ -46,6 +46,10 @@ def instantiation(kind, p, epi=0):
         return "launch_stream<%d,%d,%d,%d%s>" % (p["MB"], p["R"], p["U"], p.get("A", 0), tail)
     if epi:
         raise ValueError("the fused gate/up epilogue exists for the stream kernels only")
+    if kind == "ilv8":
+        return "launch_ilv8<%d,%d,%d,%d,%d,%d,%d,%d,%d>" % (
+            p["BM"], p["BN"], p["BK"], p["WM"], p["WN"], p["STAGES"], p["GROUP"], p["XCD"],
+            p["RSP"])
     return "launch_mfma<%d,%d,%d,%d,%d,%d,%d,%d,%d>" % (
         p["BM"], p["BN"], p["BK"], p["WM"], p["WN"], p["MS"], p["SWZ"], p["GROUP"], p["XCD"])
 
@@ -64,6 +68,9 @@ def condition(sel, kind, p, m_max, n_min=0, gate_up=False):
         spw = p["SN"] // 2 if gate_up else p["SN"]  # gate/up: the slab waves pair up
         fit = "(p.N %% %d) == 0 && (p.K %% %d) == 0" % (sel.STREAM_N_ROWS * p["R"] * spw,
                                                           sel.STREAM_K_STEP * p["U"])
+    elif kind == "ilv8":  # a scale group is two k-tiles; 31-bit panel byte offsets
+        fit = "(p.N %% %d) == 0 && (p.K %% 128) == 0 && p.lda <= %d && p.ldw <= %d" % (
+            p["BN"], sel.ilv_ld_max(p), sel.ilv_ld_max(p))
     else:
         fit = "(p.N %% %d) == 0 && (p.K %% %d) == 0" % (p["BN"], p["BK"])
     band = "p.M <= %d" % m_max
@@ -93,8 +100,34 @@ def render(gate_up: bool = False) -> str:
     return "\n".join(out) + "\n"
 
 
+HEAD_PREFILL = """// GENERATED from select.py -- do not edit.  Regenerate with:
+//   python3 kernels/shipped/gemm_w8a16/gfx950/gen_dispatch.py --prefill > prefill.inc
+//
+// Explicit instantiations of the interleaved int8 prefill launchers the ladder names; included
+// by launch_prefill.hip, the translation unit that builds k_gemm_ilv8.
+"""
+
+
+def render_prefill() -> str:
+    sel = _select()
+    out = [HEAD_PREFILL]
+    seen = set()
+    for _m, _n, _tag, kind, p in sel.LADDER:
+        if kind != "ilv8":
+            continue
+        inst = instantiation(kind, p)
+        if inst in seen:
+            continue
+        seen.add(inst)
+        out.append("template hipError_t %s(const W8A16Params&, hipStream_t);" % inst)
+    return "\n".join(out) + "\n"
+
+
 def main():
-    sys.stdout.write(render(gate_up="--gate-up" in sys.argv[1:]))
+    if "--prefill" in sys.argv[1:]:
+        sys.stdout.write(render_prefill())
+    else:
+        sys.stdout.write(render(gate_up="--gate-up" in sys.argv[1:]))
     return 0
 
 

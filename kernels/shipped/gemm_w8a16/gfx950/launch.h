@@ -187,6 +187,12 @@ inline hipError_t launch_line(const W8A16Params& p, hipStream_t s) {
   return launch_line_fmt<2, MB, R, D, SN, WAVES, EPI>(p, s);
 }
 
+// The interleaved int8 prefill kernel (k_gemm_ilv8) lives in its own translation unit,
+// launch_prefill.hip, compiled with the register-pressure-minimising scheduler; its launchers
+// are instantiated there for the rows of the ladder (prefill.inc, generated from select.py).
+template <int BM, int BN, int BK, int WM, int WN, int STAGES, int GROUP, int XCD, int RSP>
+hipError_t launch_ilv8(const W8A16Params& p, hipStream_t s);
+
 template <int BM, int BN, int BK, int WM, int WN, int MS, int SWZ, int GROUP, int XCD>
 inline hipError_t launch_mfma(const W8A16Params& p, hipStream_t s) {
   const int nm = (p.M + BM - 1) / BM;

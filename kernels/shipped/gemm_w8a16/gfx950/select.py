@@ -5,7 +5,8 @@ kernels/shipped/gemm_fp16/sm_70/select.py:23-58).  The weight formats:
   fmt 1  int8 symmetric, fp16 scale per output channel
   fmt 2  uint8 asymmetric, fp16 scale + uint8 zero-point per (row, group of `group` k)
 Every row of the ladder is instantiated for both formats; dispatch.inc is generated from this
-file by gen_dispatch.py.
+file by gen_dispatch.py, and so is prefill.inc (the instantiations of the interleaved int8
+prefill kernel, built in their own translation unit, launch_prefill.hip).
 """
 
 ARCH = "gfx950"
@@ -37,6 +38,8 @@ LADDER = [
     (128, 0, "l8r1n2d3", "line", dict(MB=8, R=1, D=3, SN=2, W=2048, NMAX=12288)),
     (256, 0, "m128x128k64", "mfma",
      dict(BM=128, BN=128, BK=64, WM=2, WN=2, MS=32, SWZ=1, GROUP=8, XCD=1)),
+    (1 << 30, 0, "i8x256k64s3", "ilv8",
+     dict(BM=256, BN=256, BK=64, WM=2, WN=2, STAGES=3, GROUP=8, XCD=1, RSP=8)),
     (1 << 30, 0, "m256x256k64", "mfma",
      dict(BM=256, BN=256, BK=64, WM=2, WN=2, MS=32, SWZ=1, GROUP=8, XCD=1)),
 ]
@@ -81,7 +84,15 @@ def _fits_gate_up(kind, p, M, N, K):
     return _fits(kind, p, M, N, K)
 
 
+def ilv_ld_max(p):
+    """Largest leading dimension the interleaved int8 kernel takes: its copies address a 256-row
+    panel with 31-bit byte offsets (A rows are fp16)."""
+    return (2 ** 31 - 1) // (2 * max(p["BM"], p["BN"]))
+
+
 def _fits(kind, p, M, N, K):
+    if kind == "ilv8":  # a scale group of 128 k is two k-tiles
+        return N % p["BN"] == 0 and K % 128 == 0 and K <= ilv_ld_max(p)
     if kind == "line":  # NMAX (optional): the row holds narrower N only
         return (N % (STREAM_N_ROWS * p["R"] * p.get("SN", 1)) == 0 and K % LINE_K_STEP == 0
                 and K <= LINE_K_MAX and N < p.get("NMAX", 1 << 30))

@@ -35,6 +35,10 @@ _ENTRY = {
     "ilv": ("k_gemm_ilv", ("BM", "BN", "BK", "WM", "WN", "STAGES", "GROUP", "XCD", "RSP"),
             "const _Float16*, const _Float16*, _Float16*, int, int, int, int, int, int",
             ("common/cdna4.h", "gemm_mfma/kernel.hip", "gemm_mfma/ilv.hip")),
+    "ilv8": ("k_gemm_ilv8", ("BM", "BN", "BK", "WM", "WN", "STAGES", "GROUP", "XCD", "RSP", "BFMT"),
+             "const _Float16*, const uint8_t*, const _Float16*, const uint8_t*, _Float16*, int, int, "
+             "int, int, int, int",
+             ("common/cdna4.h", "gemm_mfma/kernel.hip", "gemm_mfma/ilv8.hip")),
     "dma": ("k_gemm_dma", ("BM", "BN", "BK", "WM", "WN", "STAGES", "SWZ", "GROUP", "XCD", "XT",
                            "MINB", "MS"),
             "const _Float16*, const _Float16*, _Float16*, int, int, int, int, int, int",
@@ -57,7 +61,8 @@ NAMESPACE = "tempo::gen"
 # a "// tempo:flags ..." line, which the toolchain (and the library build) read back.  The
 # interleaved kernel keeps its accumulator tuples in place only under the register-pressure-
 # minimising pre-RA scheduler (the skeleton's header says why).
-KIND_FLAGS = {"ilv": ("-mllvm", "-amdgpu-sched-strategy=iterative-minreg")}
+KIND_FLAGS = {"ilv": ("-mllvm", "-amdgpu-sched-strategy=iterative-minreg"),
+              "ilv8": ("-mllvm", "-amdgpu-sched-strategy=iterative-minreg")}
 # trailing template parameters with a default in the skeleton: named only when the hyperform
 # sets them (EPI = 1 is the fused gate/up epilogue of the decode kernels)
 _OPTIONAL = frozenset({"EPI", "SN", "TPB"})
@@ -126,13 +131,17 @@ class Gfx950Skeletons:
         kind = p["kind"]
         if kind == "stream" and p.get("EPI"):
             p = dict(p, R=2 * p["R"])  # each wave carries the gate and the up row groups
-        if kind == "ilv":
+        if kind in ("ilv", "ilv8"):
             tm, tn = p["BM"] // p["WM"] // 16, p["BN"] // p["WN"] // 16
             acc = tm * tn * 4
-            frags = 2 * (tm + tn) * 4
             nw = p["WM"] * p["WN"]
-            L = (p["BM"] + p["BN"]) // (1024 // (p["BK"] * 2) * nw)
-            regs = acc + frags + 2 * L + 16  # + 64-bit copy sources, offsets
+            if kind == "ilv":
+                frags = 2 * (tm + tn) * 4
+                L = (p["BM"] + p["BN"]) // (1024 // (p["BK"] * 2) * nw)
+            else:  # A fragments double-buffered, weight bytes double-buffered, two dequantised
+                frags = 2 * tm * 4 + 2 * tn * 2 + 2 * 4 + 4 * tn
+                L = p["BM"] // (1024 // (p["BK"] * 2) * nw) + p["BN"] // (16 * nw)
+            regs = acc + frags + 2 * L + 16  # + copy offsets, fragment offsets
             # pessimistic edge: the epilogue converts every accumulator (acc held twice when the
             # budget allows it)
             return regs, max(int(regs * 1.2), 2 * acc + 16), space.lds_bytes(kind, p)
@@ -194,7 +203,7 @@ class Gfx950Skeletons:
         M, N = int(op.shapes["M"]), int(op.shapes["N"])
         kind = p["kind"]
         minb, bound = 1, 0
-        if kind in ("dma", "reg", "ilv"):
+        if kind in ("dma", "reg", "ilv", "ilv8"):
             grid = -(-M // p["BM"]) * (N // p["BN"])
             threads = p["WM"] * p["WN"] * 64
             minb = p.get("MINB", 1) if kind == "dma" else 1
@@ -231,14 +240,14 @@ class Gfx950Skeletons:
         per_cu = max(1, occ.ctas_per_sm)
         rounds = -(-lau.grid_ctas // (int(_M.rate("GEOM.SMS").value) * per_cu))
         atoms = []
-        if kind in ("dma", "reg", "ilv"):
-            ms = p.get("MS", 32) if kind != "ilv" else 16
+        if kind in ("dma", "reg", "ilv", "ilv8"):
+            ms = p.get("MS", 32) if kind not in ("ilv", "ilv8") else 16
             tm, tn = p["BM"] // p["WM"] // ms, p["BN"] // p["WN"] // ms
             ks = p["BK"] // (16 if ms == 32 else 32)
             nw = p["WM"] * p["WN"]
             reps = (K // p["BK"]) * rounds
             flops = tm * tn * ks * space.MFMA_FLOPS[ms]
-            lds_rd = (tm + tn) * ks * 1024
+            lds_rd = (tm + tn) * ks * 1024 if kind != "ilv8" else (tm * 1024 + tn * 512) * ks
             vmem = (p["BM"] + p["BN"]) * p["BK"] * 2 // nw
             if p.get("BFMT", 0):
                 vmem = p["BM"] * p["BK"] * 2 // nw + p["BN"] * p["BK"] // nw
@@ -265,7 +274,7 @@ class Gfx950Skeletons:
                               footprint={"LDS": float(lds_rd * reps)},
                               latency=_M.rate("LATENCY.LDS").value))
         atoms.append(Atom(uid=2, kind=AtomKind.XFER_ISSUE,
-                          op_id=("buffer_load_dwordx4 lds" if kind == "ilv" else
+                          op_id=("buffer_load_dwordx4 lds" if kind in ("ilv", "ilv8") else
                                  "global_load_lds_dwordx4" if kind in ("dma", "ring", "line")
                                  else "global_load_dwordx4"),
                           footprint={"VMEM": float(vmem * reps)},

@@ -73,7 +73,7 @@ def hyper_params(kind, p, fmt, epi=0):
     """A ladder row of select.py (kind, template params) -> the plugin's hyperform params: the
     same kernel, named the way space.variants() names it."""
     pk = {"stream": "stream", "mfma": "reg", "dma": "dma", "shared": "shared", "ilv": "ilv",
-          "line": "line"}[kind]
+          "ilv8": "ilv8", "line": "line"}[kind]
     params = {k: v for k, v in p.items() if k not in ("fmts", "NMAX")}
     params["kind"] = pk
     if pk == "shared":
@@ -254,6 +254,8 @@ def make(op, rows_files=()):
         elif kind == "ilv":
             fit = "N %% %d == 0 and K %% %d == 0 and K <= %d" % (p["BN"], max(64, p["BK"]),
                                                                  sel.ilv_ld_max(p))
+        elif kind == "ilv8":
+            fit = "N %% %d == 0 and K %% 128 == 0 and K <= %d" % (p["BN"], sel.ilv_ld_max(p))
         elif kind == "line":
             fit = "N %% %d == 0 and K %% %d == 0 and K <= %d" % (
                 sel.STREAM_N_ROWS * p["R"] * p.get("SN", 1), sel.LINE_K_STEP, sel.LINE_K_MAX)

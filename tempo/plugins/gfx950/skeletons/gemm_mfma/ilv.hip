@@ -1,5 +1,5 @@
 // gemm_mfma/ilv.hip -- the interleaved prefill GEMM (fp16 x fp16).  Uses the tile machinery of
-// gemm_mfma/kernel.hip (lds_chunk, tile_of, s_wait_vm, lds_void_t), which must come first.
+// gemm_mfma/kernel.hip (lds_chunk, tile_of, s_wait_vm, buf_lds16), which must come first.
 // ============================================================================================
 // k_gemm_ilv -- fp16 B only, prefill: one wave per SIMD, large wave tiles, and a main loop that
 // is software-pipelined by hand ("interleaved").
@@ -48,16 +48,6 @@
 // 128 x 128 wave tile such that the register allocator no longer keeps each accumulator in one
 // AGPR tuple, and the loop fills with v_accvgpr_read/write/mov copies.
 // ============================================================================================
-// 16-byte-per-lane buffer load into LDS: lane l's 16 bytes at byte offset voff + soff of the
-// raw buffer [base, base + nrec) land at lds + 16 l.  (A helper function rather than inline in
-// the kernel's lambdas: inside a lambda of a kernel template the host pass drops the kernel's
-// launch stub.)
-__device__ __forceinline__ void buf_lds16(const void* base, int nrec, void* lds, int voff, int soff) {
-  const __amdgpu_buffer_rsrc_t r =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, nrec, 0x00020000);
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)lds, 16, voff, soff, 0, 0);
-}
-
 template <int BM, int BN, int BK, int WM, int WN, int STAGES, int GROUP, int XCD, int RSP>
 __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv(
     const _Float16* __restrict__ A, const _Float16* __restrict__ B, _Float16* __restrict__ C,

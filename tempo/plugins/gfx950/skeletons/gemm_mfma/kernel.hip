@@ -275,6 +275,27 @@ __device__ __forceinline__ void s_wait_vm() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0x0 << 8));
 }
 
+// 16-byte-per-lane buffer load into LDS: lane l's 16 bytes at byte offset voff + soff of the
+// raw buffer [base, base + nrec) land at lds + 16 l.  (A helper function rather than inline in
+// the kernel's lambdas: inside a lambda of a kernel template the host pass drops the kernel's
+// launch stub.)
+__device__ __forceinline__ void buf_lds16(const void* base, int nrec, void* lds, int voff, int soff) {
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, nrec, 0x00020000);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)lds, 16, voff, soff, 0, 0);
+}
+// The same with 1- or 2-byte lanes (zero-points, scales); such lanes land 4 bytes apart in LDS.
+template <int SIZE>
+__device__ __forceinline__ void buf_lds_n(const void* base, int nrec, void* lds, int voff, int soff) {
+  static_assert(SIZE == 1 || SIZE == 2, "byte or half lanes");
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, nrec, 0x00020000);
+  if constexpr (SIZE == 1)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)lds, 1, voff, soff, 0, 0);
+  else
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)lds, 2, voff, soff, 0, 0);
+}
+
 // XT = 1 pipelines across k-tile boundaries: the wait + barrier for tile kt+1, the DMA issue of
 // tile kt+STAGES and the first fragment reads of tile kt+1 all happen BEFORE the last MFMA group
 // of tile kt, so the matrix cores have work while the workgroup synchronises.  The prologue then

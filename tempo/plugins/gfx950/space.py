@@ -1,8 +1,10 @@
 """gfx950: SEARCH SPACE -- axes and legal hyperforms (reference pattern tempo/plugins/sm70/space.py).
 
-Five skeleton kinds, each a kernel family of tempo/plugins/gfx950/skeletons:
+The skeleton kinds, each a kernel family of tempo/plugins/gfx950/skeletons:
   ilv     gemm_mfma/k_gemm_ilv      fp16 x fp16, one wave per SIMD, large wave tiles, LDS-DMA
                                     copies and fragment reads interleaved with the MFMAs by hand
+  ilv8    gemm_mfma/k_gemm_ilv8     int8 / uint8 weights (W8A16 prefill): k_gemm_ilv with the
+                                    weight tile as bytes, dequantised after its fragment reads
   dma     gemm_mfma/k_gemm_dma      fp16 x fp16, LDS-DMA multi-stage pipeline (prefill, M > 32)
   reg     gemm_mfma/k_gemm          any weight format, register-staged copy that can dequantise
                                     on the way into LDS (W8A16 prefill, fp16 fallback)
@@ -41,6 +43,7 @@ AXES = (
 DOMAINS = {
     "ilv": dict(BM=(128, 256), BN=(128, 192, 256), BK=(32, 64), STAGES=(2, 3, 4), GROUP=(4, 8, 16),
                 XCD=(0, 1), WAVES=((2, 2), (2, 4), (4, 2)), RSP=(0, 8, 12)),
+    "ilv8": dict(STAGES=(3,), GROUP=(4, 8, 16), XCD=(0, 1), RSP=(4, 8, 12)),
     "dma": dict(BM=(128, 256), BN=(128, 192, 256), BK=(32, 64), STAGES=(2, 3, 4), SWZ=(0, 1, 2),
                 GROUP=(4, 8, 16), XCD=(0, 1), WAVES=((2, 2), (2, 4), (4, 2), (4, 4)), MS=(16, 32)),
     "reg": dict(BM=(64, 128, 256), BN=(128, 256), BK=(64,), MS=(16, 32), SWZ=(1, 2), GROUP=(8,),
@@ -106,6 +109,10 @@ def line_split(N: int, K: int, p: dict):
 def lds_bytes(kind: str, p: dict) -> int:
     if kind in ("dma", "ilv"):
         return p["STAGES"] * (p["BM"] + p["BN"]) * p["BK"] * 2
+    if kind == "ilv8":  # fp16 A tile, byte weight tile, fmt 2 metadata per stage; fmt 1 scales
+        meta = p["BN"] * 8 if p["BFMT"] == 2 else 0
+        return (p["STAGES"] * (p["BM"] * p["BK"] * 2 + p["BN"] * p["BK"] + meta)
+                + (p["BN"] * 4 if p["BFMT"] == 1 else 0))
     if kind == "reg":
         return 2 * (p["BM"] + p["BN"]) * p["BK"] * 2
     if kind == "ring":
@@ -158,6 +165,10 @@ def tag(kind: str, p: dict) -> str:
     if kind == "ilv":
         return "ilv_m%dn%dk%d_w%dx%d_s%d_g%d_x%d_r%d" % (
             p["BM"], p["BN"], p["BK"], p["WM"], p["WN"], p["STAGES"], p["GROUP"], p["XCD"], p["RSP"])
+    if kind == "ilv8":
+        return "ilv8_m%dn%dk%d_w%dx%d_s%d_g%d_x%d_r%d_b%d" % (
+            p["BM"], p["BN"], p["BK"], p["WM"], p["WN"], p["STAGES"], p["GROUP"], p["XCD"], p["RSP"],
+            p["BFMT"])
     if kind == "dma":
         return "dma_m%dn%dk%d_w%dx%d_s%d_z%d_g%d_x%d_f%d" % (
             p["BM"], p["BN"], p["BK"], p["WM"], p["WN"], p["STAGES"], p["SWZ"], p["GROUP"], p["XCD"],
@@ -196,6 +207,22 @@ def legal(kind: str, p: dict, M: int, N: int, K: int):
             return "vmcnt depth"
         if nw * 64 > 1024:
             return "more than 1024 lanes"
+        if lds_bytes(kind, p) > LDS_MAX:
+            return "LDS %d B > 160 KiB" % lds_bytes(kind, p)
+        return None
+    if kind == "ilv8":
+        BM, BN, BK, WM, WN = p["BM"], p["BN"], p["BK"], p["WM"], p["WN"]
+        if (BM, BN, BK, WM, WN) != (256, 256, 64, 2, 2):
+            return "the int8 interleaved kernel is written for 256 x 256 x 64 tiles on 2 x 2 waves"
+        if p["BFMT"] not in (1, 2):
+            return "weights must be int8 (fmt 1) or uint8 group-128 (fmt 2)"
+        if N % BN or K % 128:
+            return "N %% %d / K %% 128 (one scale group = two k-tiles)" % BN
+        L = BM // 8 // 4 + BN // 16 // 4 + (2 if p["BFMT"] == 2 else 0)
+        if (p["STAGES"] - 1) * L >= 64:
+            return "vmcnt depth"
+        if BM * BN * 2 > p["STAGES"] * (BM * BK * 2 + BN * BK):
+            return "the C tile does not fit the stages"
         if lds_bytes(kind, p) > LDS_MAX:
             return "LDS %d B > 160 KiB" % lds_bytes(kind, p)
         return None
@@ -326,6 +353,14 @@ def variants(op: OpSpec) -> Iterator[Hyperform]:
                                             out.append(("dma", dict(
                                                 BM=BM, BN=BN, BK=BK, WM=WM, WN=WN, STAGES=ST,
                                                 SWZ=SW, GROUP=G, XCD=X, XT=0, MINB=1, MS=MS)))
+    if b in (1, 2) and M > 128:
+        d = DOMAINS["ilv8"]
+        for ST in d["STAGES"]:
+            for G in d["GROUP"]:
+                for X in d["XCD"]:
+                    for RS in d["RSP"]:
+                        out.append(("ilv8", dict(BM=256, BN=256, BK=64, WM=2, WN=2, STAGES=ST,
+                                                 GROUP=G, XCD=X, RSP=RS, BFMT=b)))
     d = DOMAINS["reg"]
     for BM in d["BM"]:
         for BN in d["BN"]:

@@ -137,6 +137,30 @@ def test_w8a16_parity_prefill(gpu, fmt):
 
 
 @pytest.mark.parametrize("fmt", [1, 2])
+@pytest.mark.parametrize("M, N, K", [(2049, 1024, 5120), (512, 5120, 17408), (2048, 1024, 5184)])
+def test_w8a16_parity_interleaved_prefill_rows(gpu, fmt, M, N, K):
+    """The interleaved int8 prefill kernel: a ragged last tile row (M = 2049), a long k loop
+    (K = 17408), and K % 128 != 0, which it does not take (fmt 1: the register-staged row runs;
+    fmt 2 needs whole 128-k groups, so the shape is not covered at all)."""
+    route = _route(fmt, M, N, K)
+    say("w8a16 fmt", fmt, "M", M, "N", N, "K", K, "route", route)
+    if K % 128:
+        assert route == ("m256x256k64" if fmt == 1 else "")
+        if fmt == 2:
+            return
+    else:
+        assert route == "i8x256k64s3"
+    A = O.randn_f16((M, K), 13, K ** -0.5)
+    q, s, z = make_weights(N, K, fmt, 79)
+    C = _run(A, q, s, z, fmt, gpu)
+    assert O.count_poison(C) == 0
+    rows = np.r_[0:32, M // 2:M // 2 + 32, M - 32:M]
+    rel = O.rel_l2(np.ascontiguousarray(C[rows]), O.gemm_w8a16(A[rows], q, s, z, 128, fmt))
+    say("  relL2 %.3e" % rel)
+    assert rel <= 3e-3
+
+
+@pytest.mark.parametrize("fmt", [1, 2])
 @pytest.mark.parametrize("M", [1, 8, 16, 32, 300])
 @pytest.mark.parametrize("N", [1024, 17408])
 def test_w8a16_exact_regime_bit_exact(gpu, fmt, M, N):

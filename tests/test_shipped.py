@@ -38,23 +38,25 @@ def test_dispatch_inc_is_generated_from_select(op, table):
         assert f.read() == text, "%s is stale: re-run the build" % table
 
 
-def test_prefill_inc_is_generated_from_select():
-    d = os.path.join(SHIPPED, "gemm_fp16", "gfx950")
+@pytest.mark.parametrize("op,kind", [("gemm_fp16", "ilv"), ("gemm_w8a16", "ilv8")])
+def test_prefill_inc_is_generated_from_select(op, kind):
+    d = os.path.join(SHIPPED, op, "gfx950")
     text = subprocess.run([sys.executable, os.path.join(d, "gen_dispatch.py"), "--prefill"],
                           check=True, capture_output=True, text=True).stdout
     with open(os.path.join(d, "prefill.inc"), encoding="utf-8") as f:
         assert f.read() == text, "prefill.inc is stale: re-run the build"
     # every interleaved row of the ladder is instantiated there, and nothing else
-    rows = [r for r in _select("gemm_fp16").LADDER if r[3] == "ilv"]
-    assert rows and text.count("template hipError_t launch_ilv<") == len(rows)
+    rows = [r for r in _select(op).LADDER if r[3] == kind]
+    assert rows and text.count("template hipError_t launch_%s<" % kind) == len(rows)
 
 
-def test_prefill_unit_declares_its_scheduler():
+@pytest.mark.parametrize("op", ["gemm_fp16", "gemm_w8a16"])
+def test_prefill_unit_declares_its_scheduler(op):
     from cuda_tempiler_amd import build
 
-    flags = build.unit_flags(os.path.join(SHIPPED, "gemm_fp16", "gfx950", "launch_prefill.hip"))
+    flags = build.unit_flags(os.path.join(SHIPPED, op, "gfx950", "launch_prefill.hip"))
     assert flags == ["-mllvm", "-amdgpu-sched-strategy=iterative-minreg"]
-    assert build.unit_flags(os.path.join(SHIPPED, "gemm_fp16", "gfx950", "launch.hip")) == []
+    assert build.unit_flags(os.path.join(SHIPPED, op, "gfx950", "launch.hip")) == []
 
 
 def test_frozen_kernels_match_skeletons():
@@ -69,8 +71,9 @@ def test_delivery_layout():
         for f in ("kernel.hip", "launch.h", "launch.hip", "dispatch.inc", "dispatch_gate_up.inc",
                   "select.py", "gen_dispatch.py", "manifest.json"):
             assert os.path.exists(os.path.join(d, f)), "%s/%s missing" % (op, f)
-    for f in ("launch_prefill.hip", "prefill.inc"):
-        assert os.path.exists(os.path.join(SHIPPED, "gemm_fp16", "gfx950", f)), f
+    for op in OPS:
+        for f in ("launch_prefill.hip", "prefill.inc"):
+            assert os.path.exists(os.path.join(SHIPPED, op, "gfx950", f)), (op, f)
 
 
 def _declared():
