@@ -38,6 +38,10 @@ LADDER = [
     (128, 0, "l8r1n2d3", "line", dict(MB=8, R=1, D=3, SN=2, W=2048, NMAX=12288)),
     (256, 0, "m128x128k64", "mfma",
      dict(BM=128, BN=128, BK=64, WM=2, WN=2, MS=32, SWZ=1, GROUP=8, XCD=1)),
+    # narrow N (fewer than 8 tiles of 256 columns): 256x256 tiles leave most CUs idle, so
+    # 128x128 tiles of the register-staged kernel (4x the workgroups) are faster there
+    (1 << 30, 0, "m128x128k64s16", "mfma",
+     dict(BM=128, BN=128, BK=64, WM=2, WN=2, MS=16, SWZ=1, GROUP=8, XCD=1, NMAX=2048)),
     (1 << 30, 0, "i8x256k64s3", "ilv8",
      dict(BM=256, BN=256, BK=64, WM=2, WN=2, STAGES=3, GROUP=8, XCD=1, RSP=8)),
     (1 << 30, 0, "m256x256k64", "mfma",
@@ -101,7 +105,8 @@ def _fits(kind, p, M, N, K):
     if kind == "shared":
         return (N % (STREAM_N_ROWS * p["R"] * p["SN"]) == 0
                 and K % (STREAM_K_STEP * p["U"]) == 0)
-    return N % p["BN"] == 0 and K % p["BK"] == 0
+    # mfma: NMAX (optional) as for the line rows
+    return N % p["BN"] == 0 and K % p["BK"] == 0 and N < p.get("NMAX", 1 << 30)
 
 
 def select(op, M, N, K, fmt=1, group=128, dtype_a="fp16", dtype_c="fp16", arch=ARCH):

@@ -263,6 +263,8 @@ def make(op, rows_files=()):
                 fit += " and N < %d" % p["NMAX"]
         else:
             fit = "N %% %d == 0 and K %% %d == 0" % (p["BN"], p["BK"])
+            if "NMAX" in p:
+                fit += " and N < %d" % p["NMAX"]
         man["dispatch" if not epi else "dispatch_gate_up"].append(dict(
                                     M_max=m_max, N_min=n_min, tag=tag, kind=kind,
                                     params={k: v for k, v in p.items() if k != "fmts"},

@@ -137,17 +137,21 @@ def test_w8a16_parity_prefill(gpu, fmt):
 
 
 @pytest.mark.parametrize("fmt", [1, 2])
-@pytest.mark.parametrize("M, N, K", [(2049, 1024, 5120), (512, 5120, 17408), (2048, 1024, 5184)])
+@pytest.mark.parametrize("M, N, K", [(2049, 2048, 5120), (512, 5120, 17408), (2048, 2048, 5184),
+                                     (2049, 1024, 5120), (300, 1792, 5120)])
 def test_w8a16_parity_interleaved_prefill_rows(gpu, fmt, M, N, K):
     """The interleaved int8 prefill kernel: a ragged last tile row (M = 2049), a long k loop
     (K = 17408), and K % 128 != 0, which it does not take (fmt 1: the register-staged row runs;
-    fmt 2 needs whole 128-k groups, so the shape is not covered at all)."""
+    fmt 2 needs whole 128-k groups, so the shape is not covered at all).  Narrow N (< 2048)
+    takes the 128x128 register-staged row instead, ragged M included."""
     route = _route(fmt, M, N, K)
     say("w8a16 fmt", fmt, "M", M, "N", N, "K", K, "route", route)
     if K % 128:
         assert route == ("m256x256k64" if fmt == 1 else "")
         if fmt == 2:
             return
+    elif N < 2048:
+        assert route == "m128x128k64s16"
     else:
         assert route == "i8x256k64s3"
     A = O.randn_f16((M, K), 13, K ** -0.5)
