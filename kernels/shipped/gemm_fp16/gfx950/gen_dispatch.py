@@ -77,6 +77,8 @@ def condition(sel, kind, p, m_max, n_min=0, gate_up=False):
             p["BN"], max(64, p["BK"]), sel.ilv_ld_max(p), sel.ilv_ld_max(p))
     else:
         fit = "(p.N %% %d) == 0 && (p.K %% %d) == 0" % (p["BN"], p["BK"])
+        if "NMAX" in p:
+            fit += " && p.N < %d" % p["NMAX"]
     band = "p.M <= %d" % m_max
     if n_min:
         band += " && p.N >= %d" % n_min

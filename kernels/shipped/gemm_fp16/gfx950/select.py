@@ -35,6 +35,10 @@ LADDER = [
     (64, 0, "l4r1d3", "line", dict(MB=4, R=1, D=3, W=2048)),
     (128, 12288, "l8r1n4d3", "line", dict(MB=8, R=1, D=3, SN=4, W=2048)),
     (128, 0, "l8r1n2d3", "line", dict(MB=8, R=1, D=3, SN=2, W=2048)),
+    # narrow N with a long k loop (N=3840, K=15360): 64x64 tiles give 4x the workgroups of
+    # 128x128 (240 instead of 60) and are faster despite the larger operand traffic per flop
+    (256, 0, "m64x64k64s16", "mfma",
+     dict(BM=64, BN=64, BK=64, WM=2, WN=2, MS=16, SWZ=1, GROUP=8, XCD=1, NMAX=8192)),
     (256, 0, "m128x128k64", "mfma",
      dict(BM=128, BN=128, BK=64, WM=2, WN=2, MS=32, SWZ=1, GROUP=8, XCD=1)),
     (1 << 30, 0, "i256x256k64w4r8", "ilv",
@@ -96,7 +100,8 @@ def _fits(kind, p, M, N, K):
     if kind == "shared":
         return (N % (STREAM_N_ROWS * p["R"] * p["SN"]) == 0
                 and K % (STREAM_K_STEP * p["U"]) == 0)
-    return N % p["BN"] == 0 and K % p["BK"] == 0
+    # mfma: NMAX (optional) as for the line rows
+    return N % p["BN"] == 0 and K % p["BK"] == 0 and N < p.get("NMAX", 1 << 30)
 
 
 def select(op, M, N, K, dtype_a="fp16", dtype_b="fp16", dtype_c="fp16", arch=ARCH):
