@@ -13,8 +13,11 @@ through to the next one, so a narrower row can sit in front of a general one.)
               per-wave rings (needs K % 128); stream / shared are its fallbacks.  A = 1 stages the activations in LDS once per workgroup (M = 1).  "shared"
               (k_stream_sh) lets SN slab waves share one LDS copy of each activation stage, which
               pays where N leaves enough slabs to fill the part (wide N).
-  * M >  32   mfma / ilv: LDS-tiled MFMA kernels, tile chosen by M.  ilv = the interleaved
-              4-wave kernel (128 x 128 wave tiles, LDS-DMA copies, hand-pipelined substeps).
+  * 32 < M <= 64  line rows with more activation blocks.
+  * 64 < M <= 256  dma: k_gemm_dma tiles (64x64 to 128x128, 4-stage LDS-DMA ring), tile chosen
+              by M and N; the line and register-staged (mfma) rows stay behind them as fallbacks.
+  * M > 256   ilv: the interleaved 4-wave kernel (128 x 128 wave tiles, LDS-DMA copies,
+              hand-pipelined substeps).
 """
 
 ARCH = "gfx950"
@@ -33,12 +36,21 @@ LADDER = [
     (32, 0, "s32r1u4", "stream", dict(MB=2, R=1, U=4, A=0)),
     (64, 12288, "l4r1n4d3", "line", dict(MB=4, R=1, D=3, SN=4, W=2048)),
     (64, 0, "l4r1d3", "line", dict(MB=4, R=1, D=3, W=2048)),
+    # 64 < M <= 256: LDS-DMA tiles with a 4-stage ring.  Per CU they keep more operand bytes in
+    # flight than the line kernel (which re-reads the activations per slab wave) or the
+    # register-staged tiles, and the tile is sized so the grid still covers the 256 CUs
+    (128, 12288, "d128x64k64s4", "dma",
+     dict(BM=128, BN=64, BK=64, WM=2, WN=2, STAGES=4, SWZ=1, GROUP=8, XCD=1, MS=16)),
+    (128, 0, "d64x64k64s4", "dma",
+     dict(BM=64, BN=64, BK=64, WM=2, WN=2, STAGES=4, SWZ=1, GROUP=8, XCD=1, MS=16)),
     (128, 12288, "l8r1n4d3", "line", dict(MB=8, R=1, D=3, SN=4, W=2048)),
     (128, 0, "l8r1n2d3", "line", dict(MB=8, R=1, D=3, SN=2, W=2048)),
-    # narrow N with a long k loop (N=3840, K=15360): 64x64 tiles give 4x the workgroups of
-    # 128x128 (240 instead of 60) and are faster despite the larger operand traffic per flop
-    (256, 0, "m64x64k64s16", "mfma",
-     dict(BM=64, BN=64, BK=64, WM=2, WN=2, MS=16, SWZ=1, GROUP=8, XCD=1, NMAX=8192)),
+    (256, 12288, "d128x128k64s4", "dma",
+     dict(BM=128, BN=128, BK=64, WM=2, WN=2, STAGES=4, SWZ=1, GROUP=8, XCD=1, MS=16)),
+    (256, 6144, "d128x64k64s4", "dma",
+     dict(BM=128, BN=64, BK=64, WM=2, WN=2, STAGES=4, SWZ=1, GROUP=8, XCD=1, MS=16)),
+    (256, 0, "d64x64k64s4", "dma",
+     dict(BM=64, BN=64, BK=64, WM=2, WN=2, STAGES=4, SWZ=1, GROUP=8, XCD=1, MS=16)),
     (256, 0, "m128x128k64", "mfma",
      dict(BM=128, BN=128, BK=64, WM=2, WN=2, MS=32, SWZ=1, GROUP=8, XCD=1)),
     (1 << 30, 0, "i256x256k64w4r8", "ilv",

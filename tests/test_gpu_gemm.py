@@ -74,7 +74,8 @@ def test_shipped_known_answers_bit_exact(gpu):
 # first matching row does not fit (N = 12304: N % 64 != 0, falls through to the next row)
 SHAPES = [(1, 15360, 3840), (1, 3840, 15360), (8, 15360, 3840), (8, 12304, 3840),
           (16, 3840, 15360), (17, 4096, 3840), (24, 15360, 3840), (32, 3840, 15360),
-          (64, 15360, 3840), (128, 3840, 15360), (200, 4096, 3840), (256, 15360, 3840),
+          (64, 15360, 3840), (96, 15360, 3840), (128, 3840, 15360), (200, 4096, 3840),
+          (256, 15360, 3840),
           (256, 3840, 15360), (256, 8192, 3840),
           (512, 4096, 3840), (300, 15360, 3840), (1000, 4096, 3840), (2049, 3840, 15360),
           # K > 65536: past the line rows, the stream rows run
