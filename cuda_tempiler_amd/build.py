@@ -89,16 +89,66 @@ def _compile(src: str) -> str:
     return obj
 
 
-def build(verbose: bool = False) -> str:
+# Delivery-only builds: each shipped delivery compiled from its own directory alone (-I there and
+# nowhere else), linked with its ship_probe.hip into an executable.  This is what a host tree
+# that vendors kernels/shipped/<op>/gfx950/ gets; tests run the probes on the GPU.
+PROBE_OPS = ("gemm_fp16", "gemm_w8a16")
+PROBE_FLAGS = ["-O3", "-std=c++17", "--offload-arch=%s" % ARCH,
+               "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-Wno-unused-result"]
+
+
+def probe_path(op: str) -> str:
+    return os.path.join(BUILD, "ship_probe_%s" % op)
+
+
+def _compile_delivery_unit(job):
+    op, name = job
+    d = os.path.join(SHIPPED, op, "gfx950")
+    src = os.path.join(d, name)
+    obj = os.path.join(BUILD, "delivery_%s_%s" % (op, name.replace(".hip", ".o")))
+    cmd = [HIPCC] + PROBE_FLAGS + unit_flags(src) + ["-I", d, "-c", src, "-o", obj]
+    r = subprocess.run(cmd, capture_output=True, text=True, cwd=d)
+    if r.returncode != 0:
+        raise RuntimeError("delivery-only compile of %s failed:\n%s\n%s"
+                           % (src, " ".join(cmd), r.stderr[-6000:]))
+    return obj
+
+
+def delivery_units(op: str):
+    d = os.path.join(SHIPPED, op, "gfx950")
+    return [n for n in ("launch.hip", "launch_prefill.hip", "ship_probe.hip")
+            if os.path.exists(os.path.join(d, n))]
+
+
+def build_probes(ex) -> list:
+    jobs = [(op, n) for op in PROBE_OPS for n in delivery_units(op)]
+    objs = dict(zip(jobs, ex.map(_compile_delivery_unit, jobs)))
+    out = []
+    for op in PROBE_OPS:
+        exe = probe_path(op)
+        cmd = [HIPCC, "--offload-arch=%s" % ARCH, "-o", exe + ".tmp"] + \
+            [objs[(op, n)] for n in delivery_units(op)]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError("ship probe link failed for %s:\n%s" % (op, r.stderr[-4000:]))
+        os.replace(exe + ".tmp", exe)
+        out.append(exe)
+    return out
+
+
+def build(verbose: bool = False, probes: bool = True) -> str:
     os.makedirs(BUILD, exist_ok=True)
     regenerate()
-    with cf.ThreadPoolExecutor(max_workers=len(UNITS)) as ex:
+    with cf.ThreadPoolExecutor(max_workers=8) as ex:
+        fut_probes = ex.submit(build_probes, ex) if probes else None
         objs = list(ex.map(_compile, UNITS))
-    cmd = [HIPCC, "--offload-arch=%s" % ARCH, "-shared", "-fPIC", "-o", OUT + ".tmp"] + objs
-    r = subprocess.run(cmd, capture_output=True, text=True)
-    if r.returncode != 0:
-        raise RuntimeError("link failed:\n%s" % r.stderr[-4000:])
-    os.replace(OUT + ".tmp", OUT)
+        cmd = [HIPCC, "--offload-arch=%s" % ARCH, "-shared", "-fPIC", "-o", OUT + ".tmp"] + objs
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError("link failed:\n%s" % r.stderr[-4000:])
+        os.replace(OUT + ".tmp", OUT)
+        if fut_probes is not None:
+            fut_probes.result()
     if verbose:
         print(OUT)
     return OUT

@@ -157,6 +157,7 @@ def gemm_w8a16_gate_up(A, Wq, scale, zero=None, fmt: int = W8_SYM_I8, group: int
 
     M = A.shape[0]
     N = Wq.shape[0] // 2
+    _require_w8(A, Wq, scale, zero, fmt, group)
     if C is None:
         C = torch.empty((M, N), dtype=torch.float16, device=A.device)
     p = w8a16_params(A, Wq, scale, zero, C, fmt, group)
@@ -164,6 +165,55 @@ def gemm_w8a16_gate_up(A, Wq, scale, zero=None, fmt: int = W8_SYM_I8, group: int
     _check(lib().tempo_gemm_w8a16_gate_up_launch(p, _stream(stream)),
            "tempo_gemm_w8a16_gate_up_launch")
     return C
+
+
+def w8a16_operand_error(A, Wq, scale, zero, fmt: int, group: int = 128, rows=None):
+    """Why these tensors are not a well-formed W8A16 operand set (None if they are).
+
+    The kernels read the weight bytes, scales and zero-points as raw memory of the declared
+    layout, so a wrong dtype or shape would be read as something else (or past its end):
+      A     fp16 [M, K], unit inner stride
+      Wq    [rows, K], unit inner stride: int8 for fmt 1, uint8 for fmt 2
+      scale fp16, contiguous: [rows] for fmt 1, [rows, K/group] for fmt 2
+      zero  None for fmt 1; uint8 [rows, K/group], contiguous, for fmt 2
+    `rows` defaults to Wq.shape[0] (the gate/up weight has 2N rows and so does its metadata).
+    """
+    import torch
+
+    if fmt not in (W8_SYM_I8, W8_ASYM_U8):
+        return "fmt %r is neither 1 (int8 symmetric) nor 2 (uint8 asymmetric)" % (fmt,)
+    if A.dtype != torch.float16 or A.dim() != 2 or A.stride(1) != 1:
+        return "A must be fp16 [M, K] with unit inner stride"
+    if Wq.dim() != 2 or Wq.stride(1) != 1 or Wq.shape[1] != A.shape[1]:
+        return "Wq must be [N, K] with unit inner stride and the K of A"
+    want = torch.int8 if fmt == W8_SYM_I8 else torch.uint8
+    if Wq.dtype != want:
+        return "fmt %d takes %s weights, got %s" % (fmt, want, Wq.dtype)
+    rows = Wq.shape[0] if rows is None else rows
+    K = A.shape[1]
+    if scale is None or scale.dtype != torch.float16 or not scale.is_contiguous():
+        return "scale must be a contiguous fp16 tensor"
+    if fmt == W8_SYM_I8:
+        if tuple(scale.shape) != (rows,):
+            return "fmt 1 scale must be [%d], got %s" % (rows, tuple(scale.shape))
+        if zero is not None:
+            return "fmt 1 takes no zero-points"
+        return None
+    if group <= 0 or K % group:
+        return "K = %d is not a whole number of groups of %d" % (K, group)
+    meta = (rows, K // group)
+    if tuple(scale.shape) != meta:
+        return "fmt 2 scale must be %s, got %s" % (meta, tuple(scale.shape))
+    if zero is None or zero.dtype != torch.uint8 or not zero.is_contiguous() \
+            or tuple(zero.shape) != meta:
+        return "fmt 2 zero must be a contiguous uint8 tensor of shape %s" % (meta,)
+    return None
+
+
+def _require_w8(A, Wq, scale, zero, fmt, group, rows=None):
+    why = w8a16_operand_error(A, Wq, scale, zero, fmt, group, rows)
+    if why:
+        raise ValueError("W8A16 operands: " + why)
 
 
 def w8a16_params(A, Wq, scale, zero, C, fmt: int, group: int = 128) -> TempoW8A16Params:
@@ -180,6 +230,7 @@ def gemm_w8a16(A, Wq, scale, zero=None, fmt: int = W8_SYM_I8, group: int = 128, 
 
     M = A.shape[0]
     N = Wq.shape[0]
+    _require_w8(A, Wq, scale, zero, fmt, group)
     if C is None:
         C = torch.empty((M, N), dtype=torch.float16, device=A.device)
     p = w8a16_params(A, Wq, scale, zero, C, fmt, group)
@@ -251,11 +302,34 @@ def naive_gemm_w8a16(A, Wq, scale, zero=None, fmt: int = W8_SYM_I8, group: int =
     return C
 
 
+def gptq_operand_error(qweight, qzeros, scales, group: int = 128):
+    """Why these are not GPTQ int8 checkpoint tensors of one layer (None if they are):
+    qweight int32 [K/4, N], qzeros int32 [K/group, N/4], scales fp16 [K/group, N], all
+    contiguous (the layout of bench/gemm_baseline.py:214-232 in the reference)."""
+    import torch
+
+    if qweight.dtype != torch.int32 or qweight.dim() != 2 or not qweight.is_contiguous():
+        return "qweight must be a contiguous int32 [K/4, N] tensor"
+    K, N = qweight.shape[0] * 4, qweight.shape[1]
+    if group <= 0 or K % group or N % 4:
+        return "K = %d must be a multiple of group %d and N = %d of 4" % (K, group, N)
+    if qzeros.dtype != torch.int32 or not qzeros.is_contiguous() or \
+            tuple(qzeros.shape) != (K // group, N // 4):
+        return "qzeros must be a contiguous int32 tensor of shape %s" % ((K // group, N // 4),)
+    if scales.dtype != torch.float16 or not scales.is_contiguous() or \
+            tuple(scales.shape) != (K // group, N):
+        return "scales must be a contiguous fp16 tensor of shape %s" % ((K // group, N),)
+    return None
+
+
 def gptq_repack(qweight, qzeros, scales, group: int = 128, stream=None):
     """GPTQ int8 checkpoint tensors (qweight int32 [K/4,N], qzeros int32 [K/G,N/4], scales fp16
     [K/G,N]) -> (wq uint8 [N,K], scale fp16 [N,K/G], zero uint8 [N,K/G]) for gemm_w8a16 fmt 2."""
     import torch
 
+    why = gptq_operand_error(qweight, qzeros, scales, group)
+    if why:
+        raise ValueError("GPTQ tensors: " + why)
     K = qweight.shape[0] * 4
     N = qweight.shape[1]
     dev = qweight.device

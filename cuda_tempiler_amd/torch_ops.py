@@ -124,6 +124,17 @@ def dequantize(wq: torch.Tensor, scale: torch.Tensor, zero: Optional[torch.Tenso
     return ((wq.float() - z) * s).half()
 
 
+def _w8_covered(x, wq, scale, zero, fmt, group) -> bool:
+    """The kernels take these operands as they are: right dtypes and shapes (the library reads
+    them as raw memory of the declared layout), one device, x fp16 [..., K].  Anything else is
+    the caller's own path, which gives the answer its own semantics give (or raises)."""
+    if x.dtype != torch.float16 or x.dim() < 1 or not _covered_device(x, wq, scale, zero):
+        return False
+    x2 = x.reshape(-1, x.shape[-1])
+    return capi.w8a16_operand_error(x2 if x2.stride(-1) == 1 else x2.contiguous(), wq, scale,
+                                    zero, fmt, group) is None
+
+
 def _linear_w8a16_impl(x, wq, scale, zero, fmt, group):
     def own_path():
         return F.linear(x, dequantize(wq, scale, zero, fmt, group).to(x.device))
@@ -131,9 +142,7 @@ def _linear_w8a16_impl(x, wq, scale, zero, fmt, group):
     if not enabled():
         _count("off")
         return own_path()
-    if (x.dtype != torch.float16 or wq.dim() != 2 or wq.stride(1) != 1
-            or not _covered_device(x, wq, scale, zero) or x.shape[-1] != wq.shape[1]
-            or fmt not in (capi.W8_SYM_I8, capi.W8_ASYM_U8)):
+    if not _w8_covered(x, wq, scale, zero, fmt, group):
         _count("fallback")
         return own_path()
     x2 = _rows(x)
@@ -142,8 +151,7 @@ def _linear_w8a16_impl(x, wq, scale, zero, fmt, group):
     tag = capi.route(fmt, M, N, K)
     y = torch.empty((M, N), dtype=torch.float16, device=x.device)
     try:
-        capi.gemm_w8a16(x2, wq, scale.contiguous(),
-                        zero.contiguous() if zero is not None else None, fmt=fmt, group=group, C=y)
+        capi.gemm_w8a16(x2, wq, scale, zero, fmt=fmt, group=group, C=y)
     except capi.NotCovered:
         _count("fallback")
         return own_path()
@@ -220,16 +228,12 @@ def linear_gate_up_w8a16(x: torch.Tensor, wq: torch.Tensor, scale: torch.Tensor,
     def own_path():
         return _silu_mul_own(F.linear(x, dequantize(wq, scale, zero, fmt, group).to(x.device)))
 
-    if (x.dtype != torch.float16 or wq.dim() != 2 or wq.shape[0] % 2 or wq.stride(1) != 1
-            or not _covered_device(x, wq, scale, zero) or x.shape[-1] != K
-            or fmt not in (capi.W8_SYM_I8, capi.W8_ASYM_U8)):
+    if wq.dim() != 2 or wq.shape[0] % 2 or not _w8_covered(x, wq, scale, zero, fmt, group):
         if enabled():
             _count("fallback")
             return own_path()
     return _gate_up_impl(
-        x, lambda x2, y: capi.gemm_w8a16_gate_up(x2, wq, scale.contiguous(),
-                                                 zero.contiguous() if zero is not None else None,
-                                                 fmt=fmt, group=group, C=y),
+        x, lambda x2, y: capi.gemm_w8a16_gate_up(x2, wq, scale, zero, fmt=fmt, group=group, C=y),
         own_path, 3 + fmt, N, K)
 
 

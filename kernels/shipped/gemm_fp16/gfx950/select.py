@@ -8,14 +8,13 @@ Rows are tried in order; the first row whose band holds (M, N) -- M <= M_max and
 AND whose kernel fits the shape (divisibility) is taken.  No such row: None, the caller's own
 path.  (The reference stops at the first band that holds M; here a row that does not fit falls
 through to the next one, so a narrower row can sit in front of a general one.)
-  * M <= 32   line / stream / shared: the weight-streaming decode kernels (HBM-bound; one
-              pass over B).  line = whole 128-byte weight lines by nontemporal LDS-DMA into
-              per-wave rings (needs K % 128); stream / shared are its fallbacks.  A = 1 stages the activations in LDS once per workgroup (M = 1).  "shared"
-              (k_stream_sh) lets SN slab waves share one LDS copy of each activation stage, which
-              pays where N leaves enough slabs to fill the part (wide N).
+  * M <= 32   line / stream: the weight-streaming decode kernels (HBM-bound; one pass over B).
+              line = whole 128-byte weight lines by nontemporal LDS-DMA into per-wave rings
+              (needs K % 128 and K <= 65536); stream (register-pipelined) takes the rest.  A = 1
+              stages the activations in LDS once per workgroup (M = 1).
   * 32 < M <= 64  line rows with more activation blocks.
   * 64 < M <= 256  dma: k_gemm_dma tiles (64x64 to 128x128, 4-stage LDS-DMA ring), tile chosen
-              by M and N; the line and register-staged (mfma) rows stay behind them as fallbacks.
+              by M and N; a line row takes the shapes whose N is not a multiple of 64.
   * M > 256   ilv: the interleaved 4-wave kernel (128 x 128 wave tiles, LDS-DMA copies,
               hand-pipelined substeps).
 """
@@ -28,22 +27,19 @@ LADDER = [
     (1, 0, "s1a_r1u4", "stream", dict(MB=1, R=1, U=4, A=1)),
     (16, 12288, "l1r1n4d3", "line", dict(MB=1, R=1, D=3, SN=4, W=2048)),
     (16, 0, "l1r1d4", "line", dict(MB=1, R=1, D=4, W=2048)),
-    (16, 12288, "h16r1u4n4", "shared", dict(MB=1, R=1, U=4, SN=4)),
     (16, 0, "s16r1u4", "stream", dict(MB=1, R=1, U=4, A=0)),
     (32, 12288, "l2r1n4d3", "line", dict(MB=2, R=1, D=3, SN=4, W=2048)),
     (32, 0, "l2r1d4", "line", dict(MB=2, R=1, D=4, W=2048)),
-    (32, 12288, "h32r1u4n4", "shared", dict(MB=2, R=1, U=4, SN=4)),
     (32, 0, "s32r1u4", "stream", dict(MB=2, R=1, U=4, A=0)),
     (64, 12288, "l4r1n4d3", "line", dict(MB=4, R=1, D=3, SN=4, W=2048)),
     (64, 0, "l4r1d3", "line", dict(MB=4, R=1, D=3, W=2048)),
     # 64 < M <= 256: LDS-DMA tiles with a 4-stage ring.  Per CU they keep more operand bytes in
     # flight than the line kernel (which re-reads the activations per slab wave) or the
-    # register-staged tiles, and the tile is sized so the grid still covers the 256 CUs
+    # register-staged tiles.  Narrow N gives few workgroups (N = 3840: 60 column tiles)
     (128, 12288, "d128x64k64s4", "dma",
      dict(BM=128, BN=64, BK=64, WM=2, WN=2, STAGES=4, SWZ=1, GROUP=8, XCD=1, MS=16)),
     (128, 0, "d64x64k64s4", "dma",
      dict(BM=64, BN=64, BK=64, WM=2, WN=2, STAGES=4, SWZ=1, GROUP=8, XCD=1, MS=16)),
-    (128, 12288, "l8r1n4d3", "line", dict(MB=8, R=1, D=3, SN=4, W=2048)),
     (128, 0, "l8r1n2d3", "line", dict(MB=8, R=1, D=3, SN=2, W=2048)),
     (256, 12288, "d128x128k64s4", "dma",
      dict(BM=128, BN=128, BK=64, WM=2, WN=2, STAGES=4, SWZ=1, GROUP=8, XCD=1, MS=16)),
@@ -51,8 +47,6 @@ LADDER = [
      dict(BM=128, BN=64, BK=64, WM=2, WN=2, STAGES=4, SWZ=1, GROUP=8, XCD=1, MS=16)),
     (256, 0, "d64x64k64s4", "dma",
      dict(BM=64, BN=64, BK=64, WM=2, WN=2, STAGES=4, SWZ=1, GROUP=8, XCD=1, MS=16)),
-    (256, 0, "m128x128k64", "mfma",
-     dict(BM=128, BN=128, BK=64, WM=2, WN=2, MS=32, SWZ=1, GROUP=8, XCD=1)),
     (1 << 30, 0, "i256x256k64w4r8", "ilv",
      dict(BM=256, BN=256, BK=64, WM=2, WN=2, STAGES=2, GROUP=8, XCD=1, RSP=8)),
 ]
@@ -64,14 +58,12 @@ LADDER = [
 # caller runs the plain GEMM and its own elementwise step.
 LADDER_GATE_UP = [
     (1, 0, "gl0r1n2d3", "line", dict(MB=0, R=1, D=3, SN=2, W=2048)),
-    (1, 0, "gl0r1d3", "line", dict(MB=0, R=1, D=3, W=2048)),
     (16, 12288, "gl1r1n4d3", "line", dict(MB=1, R=1, D=3, SN=4, W=2048)),
     (16, 0, "gl1r1d3", "line", dict(MB=1, R=1, D=3, W=2048)),
     (32, 12288, "gl2r1n4d3", "line", dict(MB=2, R=1, D=3, SN=4, W=2048)),
     (32, 0, "gl2r1d3", "line", dict(MB=2, R=1, D=3, W=2048)),
     (1, 0, "gh1r1u2n2", "shared", dict(MB=1, R=1, U=2, SN=2, TPB=512)),
     (16, 0, "gh16r1u4n2", "shared", dict(MB=1, R=1, U=4, SN=2, TPB=512)),
-    (16, 0, "g16r1u4", "stream", dict(MB=1, R=1, U=4, A=0)),
     (32, 0, "gh32r1u4n4", "shared", dict(MB=2, R=1, U=4, SN=4, TPB=1024)),
     (32, 0, "g32r1u4", "stream", dict(MB=2, R=1, U=4, A=0)),
 ]

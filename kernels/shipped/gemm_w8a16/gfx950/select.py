@@ -23,16 +23,10 @@ LADDER = [
     (32, 0, "l2r1n2d4", "line", dict(MB=2, R=1, D=4, SN=2, W=2048)),
     (1, 0, "s1a_r1u8", "stream", dict(MB=1, R=1, U=8, A=1)),
     (1, 0, "s1a_r1u4", "stream", dict(MB=1, R=1, U=4, A=1)),
-    (8, 16384, "h8r1u2n2", "shared", dict(MB=1, R=1, U=2, SN=2, fmts=(1,))),
-    (8, 16384, "h8r1u4n2", "shared", dict(MB=1, R=1, U=4, SN=2)),
     (8, 0, "s8r2u4", "stream", dict(MB=1, R=2, U=4, A=0)),
-    (16, 16384, "h16r1u2n2", "shared", dict(MB=1, R=1, U=2, SN=2, fmts=(1,))),
     (16, 0, "h16r1u4n2", "shared", dict(MB=1, R=1, U=4, SN=2)),
     (16, 0, "s16r1u4", "stream", dict(MB=1, R=1, U=4, A=0)),
-    (32, 16384, "h32r1u2n4", "shared", dict(MB=2, R=1, U=2, SN=4, fmts=(1,))),
-    (32, 16384, "h32r1u4n4", "shared", dict(MB=2, R=1, U=4, SN=4)),
     (32, 0, "h32r1u4n2", "shared", dict(MB=2, R=1, U=4, SN=2, TPB=512)),
-    (32, 0, "s32r2u4", "stream", dict(MB=2, R=2, U=4, A=0)),
     (64, 12288, "l4r1n4d3", "line", dict(MB=4, R=1, D=3, SN=4, W=2048)),
     (64, 0, "l4r1n2d3", "line", dict(MB=4, R=1, D=3, SN=2, W=2048)),
     (128, 0, "l8r1n2d3", "line", dict(MB=8, R=1, D=3, SN=2, W=2048, NMAX=12288)),
@@ -45,7 +39,7 @@ LADDER = [
     (1 << 30, 0, "i8x256k64s3", "ilv8",
      dict(BM=256, BN=256, BK=64, WM=2, WN=2, STAGES=3, GROUP=8, XCD=1, RSP=8)),
     (1 << 30, 0, "m256x256k64", "mfma",
-     dict(BM=256, BN=256, BK=64, WM=2, WN=2, MS=32, SWZ=1, GROUP=8, XCD=1)),
+     dict(BM=256, BN=256, BK=64, WM=2, WN=2, MS=32, SWZ=1, GROUP=8, XCD=1, fmts=(1,))),
 ]
 
 # Fused gate/up ladder (C = silu(A.deq(W)[0..N)^T) * (A.deq(W)[N..2N)^T), N = output width): the
@@ -54,19 +48,17 @@ LADDER = [
 # caller's own path).
 LADDER_GATE_UP = [
     (1, 0, "gl0r1n2d4", "line", dict(MB=0, R=1, D=4, SN=2, W=2048)),
-    (1, 0, "gl0r1d4", "line", dict(MB=0, R=1, D=4, W=2048)),
     (16, 12288, "gl1r1n4d3", "line", dict(MB=1, R=1, D=3, SN=4, W=2048)),
     (16, 0, "gl1r1n2d4", "line", dict(MB=1, R=1, D=4, SN=2, W=2048)),
     (32, 12288, "gl2r1n4d4", "line", dict(MB=2, R=1, D=4, SN=4, W=2048)),
     (32, 0, "gl2r1n2d4", "line", dict(MB=2, R=1, D=4, SN=2, W=2048)),
     (1, 0, "g1a_r1u2", "stream", dict(MB=1, R=1, U=2, A=1, fmts=(1,))),
     (1, 0, "g1a_r1u8", "stream", dict(MB=1, R=1, U=8, A=1, fmts=(2,))),
-    (1, 0, "g1a_r1u4", "stream", dict(MB=1, R=1, U=4, A=1)),
+    (1, 0, "g1a_r1u4", "stream", dict(MB=1, R=1, U=4, A=1, fmts=(2,))),
     (16, 0, "gh16r1u2n2", "shared", dict(MB=1, R=1, U=2, SN=2, TPB=512, fmts=(1,))),
-    (16, 0, "gh16r1u4n2", "shared", dict(MB=1, R=1, U=4, SN=2, TPB=512)),
-    (16, 0, "g16r1u4", "stream", dict(MB=1, R=1, U=4, A=0)),
+    (16, 0, "gh16r1u4n2", "shared", dict(MB=1, R=1, U=4, SN=2, TPB=512, fmts=(2,))),
     (32, 0, "gh32r1u2n4", "shared", dict(MB=2, R=1, U=2, SN=4, TPB=1024, fmts=(1,))),
-    (32, 0, "gh32r1u4n4", "shared", dict(MB=2, R=1, U=4, SN=4, TPB=512)),
+    (32, 0, "gh32r1u4n4", "shared", dict(MB=2, R=1, U=4, SN=4, TPB=512, fmts=(2,))),
     (32, 0, "g32r1u4", "stream", dict(MB=2, R=1, U=4, A=0)),
 ]
 

@@ -50,7 +50,9 @@ class Gfx950Plugin:
             "clock locking (Meters.clock_lock) is not offered: clocks are recorded, not set",
             "classifier.control_fields: the AMD ISA has no scheduling control words",
             "FMHA is a fixed skeleton (skeletons/fmha_fwd), outside the searched space",
-            "no epilogue fusion (silu(gate)*up), as in the reference",
+            "the fused silu(gate)*up epilogue covers decode (M <= 32) only; prefill-sized M "
+            "returns TEMPO_FALLBACK and the caller runs the plain GEMM plus its own elementwise "
+            "step",
         )
 
     def selftest(self) -> Report:

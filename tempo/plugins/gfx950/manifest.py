@@ -210,7 +210,26 @@ def build_numbers(op):
     return out
 
 
-def make(op, rows_files=()):
+def fold_counters(rows, counter_files, op):
+    """Attach the counter step's per-launch figures (measure_shipped --counters) to the measured
+    rows of the same shape and format; returns how many rows got them."""
+    n = 0
+    for cf_ in counter_files:
+        with open(cf_) as f:
+            got = json.load(f)
+        if got.get("op") != op:
+            continue
+        by = {(r["M"], r["N"], r["K"], r["fmt"]): r for r in got["rows"]}
+        for row in rows:
+            c = by.get((row["M"], row["N"], row["K"], row["fmt"]))
+            if c is not None:
+                row["counters"] = dict(c["counters"], groups=got.get("groups"),
+                                       route=c.get("route"))
+                n += 1
+    return n
+
+
+def make(op, rows_files=(), counter_files=()):
     sel = _select(op)
     d = os.path.join(SHIPPED, op, "gfx950")
     path = os.path.join(d, "manifest.json")
@@ -280,6 +299,7 @@ def make(op, rows_files=()):
         man["rows"] = got["rows"]
         man["card"] = {"before": got.get("card_before"), "after": got.get("card_after")}
         man["rows_source_md5"] = md5_of(op)
+    fold_counters(man["rows"], counter_files, op)
     with open(path, "w") as f:
         json.dump(man, f, indent=1)
         f.write("\n")
@@ -289,10 +309,11 @@ def make(op, rows_files=()):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--rows", nargs="*", default=[])
+    ap.add_argument("--counters", nargs="*", default=[])
     ap.add_argument("--op", nargs="*", default=list(OPS))
     a = ap.parse_args()
     for op in a.op:
-        print(make(op, a.rows))
+        print(make(op, a.rows, a.counters))
 
 
 if __name__ == "__main__":

@@ -14,6 +14,18 @@ For every configuration shape of the op (C1/C2 for gemm_fp16; C3/C4 for gemm_w8a
      rotated through > 512 MiB, and reports the median of the per-round ratios (reference
      tempo/core/measure/ratio.py:63-73).
 Rows go to DIR/rows_<op>.json; tempo.plugins.gfx950.manifest folds them into manifest.json.
+
+Counter step (the reference's Meters stage, tempo/plugins/sm70/counters.py:84-86):
+
+    python3 -m tempo.plugins.gfx950.measure_shipped OP --counters [--groups hbm_read hbm_write mfma]
+
+runs one rocprofv3 --pmc pass per counter group over a child program (`--counter-pass`) that
+launches the shipped kernel REPS times per configuration shape, after a calibration device copy
+of known size; the dispatches are attributed to the shapes in launch order and reduced to
+per-launch figures (HBM bytes from FETCH_SIZE / WRITE_SIZE scaled by the copy, MFMA utilisation,
+engine clock).  The parent process never touches the GPU (it only starts the profiler); the
+figures go to DIR/counters_<op>.json, which the manifest folds into the matching rows.  OP may
+also be "fmha" (configuration C5) for the counter step.
 """
 from __future__ import annotations
 
@@ -72,6 +84,140 @@ def _rel_l2(got, ref):
     return float(torch.sqrt(torch.sum((g - r) ** 2) / den).item()) if den > 0 else 0.0
 
 
+def cases_of(op: str, quick: bool = False):
+    if op == "gemm_fp16":
+        cases = [(M, N, K, 0) for (M, N, K) in SHAPES_FP16]
+    elif op == "gemm_w8a16":
+        cases = [(M, N, K, f) for f in (1, 2) for (M, N, K) in SHAPES_W8]
+    else:  # fmha: configuration C5 (B, H, Hkv, S, D) carried as (S, H, D, Hkv)
+        cases = [(4096, 16, 256, 8)]
+    return cases[::4] if quick else cases
+
+
+def label_of(M, N, K, fmt):
+    return "%d,%d,%d,%d" % (M, N, K, fmt)
+
+
+def algorithmic_bytes(op, M, N, K, fmt):
+    if op == "fmha":
+        S, H, D, Hkv = M, N, K, fmt
+        return 2 * (2 * H * S * D + 2 * Hkv * S * D)
+    wbytes = 2 * N * K if fmt == 0 else N * K + (2 * N if fmt == 1 else 3 * N * K // 128)
+    return wbytes + 2 * M * K + 2 * M * N
+
+
+def algorithmic_flops(op, M, N, K, fmt):
+    if op == "fmha":
+        S, H, D, Hkv = M, N, K, fmt
+        return 4.0 * D * H * S * (S + 1) / 2
+    return 2.0 * M * N * K
+
+
+CALIB_BYTES = 1 << 30
+REPS = 3
+
+
+def counter_pass(op: str, segfile: str, quick: bool = False) -> int:
+    """The program a counter pass profiles: a calibration copy (3 x 1 GiB device copies), then
+    REPS launches of the shipped kernel per configuration shape (inputs generated on the device
+    beforehand).  Writes the launch order to `segfile` for assign_segments()."""
+    import torch
+
+    from cuda_tempiler_amd import capi
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    segs = []
+    src = torch.ones(CALIB_BYTES, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    segs.append(dict(label="calibration", count=3, copy_bytes=CALIB_BYTES))
+    del src, dst
+    for (M, N, K, fmt) in cases_of(op, quick):
+        _say("counter pass %s %s" % (op, label_of(M, N, K, fmt)))
+        gen.manual_seed(1000 * M + N + K + fmt)
+        if op == "fmha":
+            S, H, D, Hkv = M, N, K, fmt
+            Q = torch.randn((1, S, H, D), generator=gen, device=dev).half()
+            Kt = torch.randn((1, S, Hkv, D), generator=gen, device=dev).half()
+            V = torch.randn((1, S, Hkv, D), generator=gen, device=dev).half()
+            run = lambda: capi.fmha_fwd(Q, Kt, V, D ** -0.5, True)  # noqa: E731
+        else:
+            A = (torch.randn((M, K), generator=gen, device=dev) / K ** 0.5).half()
+            C = torch.empty((M, N), dtype=torch.float16, device=dev)
+            if fmt == 0:
+                W = (torch.randn((N, K), generator=gen, device=dev) / K ** 0.5).half()
+                run = lambda: capi.gemm_fp16(A, W, C)  # noqa: E731
+            elif fmt == 1:
+                W = torch.randint(-127, 128, (N, K), generator=gen, device=dev, dtype=torch.int8)
+                S1 = (torch.rand(N, generator=gen, device=dev) + 0.5).div(127).half()
+                run = lambda: capi.gemm_w8a16(A, W, S1, None, fmt=1, C=C)  # noqa: E731
+            else:
+                W = torch.randint(0, 256, (N, K), generator=gen, device=dev, dtype=torch.uint8)
+                S2 = (torch.rand((N, K // 128), generator=gen, device=dev) + 0.5).div(255).half()
+                Z = torch.randint(100, 157, (N, K // 128), generator=gen, device=dev,
+                                  dtype=torch.uint8)
+                run = lambda: capi.gemm_w8a16(A, W, S2, Z, fmt=2, C=C)  # noqa: E731
+        torch.cuda.synchronize()
+        try:
+            run()
+        except capi.NotCovered:
+            continue
+        for _ in range(REPS - 1):
+            run()
+        torch.cuda.synchronize()
+        segs.append(dict(label=label_of(M, N, K, fmt), count=REPS,
+                         route=capi.route(fmt, M, N, K) if op != "fmha" else "k_fmha_fwd3"))
+    with open(segfile, "w") as f:
+        json.dump(segs, f, indent=1)
+    return 0
+
+
+def counters(op: str, out: str, groups, quick: bool = False) -> str:
+    """Parent of the counter passes (never touches the GPU): one rocprofv3 --pmc run per group,
+    then per-launch figures per configuration shape into out/counters_<op>.json."""
+    from tempo.plugins.gfx950.counters import (Gfx950Meters, GROUPS, assign_segments,
+                                               copy_scales, derive, medians)
+
+    meters = Gfx950Meters()
+    per_shape, scales, routes = {}, {}, {}
+    for g in groups:
+        d = os.path.abspath(os.path.join(out, "pmc_%s_%s" % (op, g)))
+        seg = os.path.join(d, "segments.json")
+        os.makedirs(d, exist_ok=True)
+        argv = [sys.executable, "-m", "tempo.plugins.gfx950.measure_shipped", op,
+                "--counter-pass", seg] + (["--quick"] if quick else [])
+        _say("counter group %s: %s" % (g, " ".join(GROUPS[g])))
+        disp = meters.run_pass(argv, GROUPS[g], d)
+        with open(seg) as f:
+            segs = json.load(f)
+        got = assign_segments(disp, segs, "tempo")
+        calib = got.pop("calibration")
+        scales.update(copy_scales(calib, CALIB_BYTES))
+        for s in segs:
+            if s["label"] in got:
+                routes[s["label"]] = s.get("route")
+                per_shape.setdefault(s["label"], {}).update(medians(got[s["label"]]))
+    rows = []
+    for lab, med in per_shape.items():
+        M, N, K, fmt = (int(x) for x in lab.split(","))
+        fig = derive(med, scales, algorithmic_bytes(op, M, N, K, fmt))
+        if med.get("_duration_ns"):
+            fig["pmc_duration_us"] = med["_duration_ns"] / 1e3
+        rows.append(dict(M=M, N=N, K=K, fmt=fmt, route=routes.get(lab),
+                         algorithmic_bytes=algorithmic_bytes(op, M, N, K, fmt),
+                         algorithmic_flops=algorithmic_flops(op, M, N, K, fmt),
+                         counters=fig))
+    path = os.path.join(out, "counters_%s.json" % op)
+    with open(path, "w") as f:
+        json.dump({"op": op, "groups": list(groups), "scales": scales, "reps": REPS,
+                   "rows": rows}, f, indent=1)
+    _say("wrote %s: %d shapes" % (path, len(rows)))
+    return path
+
+
 def measure(op: str, quick: bool = False):
     import torch
 
@@ -81,13 +227,7 @@ def measure(op: str, quick: bool = False):
     stream = torch.cuda.current_stream()
     gen = torch.Generator(device=dev)
     rows = []
-    if op == "gemm_fp16":
-        cases = [(M, N, K, 0) for (M, N, K) in SHAPES_FP16]
-    else:
-        cases = [(M, N, K, f) for f in (1, 2) for (M, N, K) in SHAPES_W8]
-    if quick:
-        cases = cases[::4]
-    for (M, N, K, fmt) in cases:
+    for (M, N, K, fmt) in cases_of(op, quick):
         _say("measure %s fmt=%d M=%d N=%d K=%d" % (op, fmt, M, N, K))
         gen.manual_seed(1000 * M + N + K + fmt)
         A = (torch.randn((M, K), generator=gen, device=dev) / K ** 0.5).half()
@@ -207,11 +347,24 @@ def card_state():
 
 def main():
     ap = argparse.ArgumentParser()
-    ap.add_argument("op", nargs="?", default="gemm_fp16", choices=("gemm_fp16", "gemm_w8a16"))
+    ap.add_argument("op", nargs="?", default="gemm_fp16",
+                    choices=("gemm_fp16", "gemm_w8a16", "fmha"))
     ap.add_argument("--out", default="gpurun_out")
     ap.add_argument("--quick", action="store_true")
+    ap.add_argument("--counters", action="store_true",
+                    help="run the counter step (rocprofv3 --pmc passes) instead of timing")
+    ap.add_argument("--groups", nargs="*", default=["hbm_read", "hbm_write", "mfma"])
+    ap.add_argument("--counter-pass", metavar="SEGFILE",
+                    help="(internal) the program a counter pass profiles")
     a = ap.parse_args()
     os.makedirs(a.out, exist_ok=True)
+    if a.counter_pass:
+        return counter_pass(a.op, a.counter_pass, a.quick)
+    if a.counters:
+        counters(a.op, a.out, a.groups, a.quick)
+        return 0
+    if a.op == "fmha":
+        ap.error("fmha has a counter step only (--counters)")
     before = card_state()
     rows = measure(a.op, a.quick)
     after = card_state()

@@ -8,275 +8,38 @@
 // fp32 running max/sum, fp16 P and O, fp32 accumulation of P.V.
 //
 // Mapping onto CDNA4 (one workgroup = 4 waves = BQ = 128 query rows of one (b, h); each wave owns
-// 32 rows; key/value blocks of BKV = 64):
+// 32 rows; key/value blocks of BKV2 keys):
 //   * S^T = K . Q^T on v_mfma_f32_32x32x16_f16: K rows are the "A" operand, Q rows the "B"
 //     operand, so every lane's result registers belong to ONE query row (column = lane % 32) --
 //     row max and row sum are in-lane plus one exchange with lane ^ 32.  Q stays in registers
-//     for the whole key loop (16 fragments of 8 halves).
+//     for the whole key loop (D/16 fragments of 8 halves).
 //   * O^T = V^T . P^T: P^T is the "B" operand and is taken straight from the S^T accumulators
 //     (lane l, k-group l/32 holds exactly the 8 key indices that operand slot needs), so P never
 //     touches LDS.  O^T's column is again the query row, so the online-softmax rescale is one
-//     per-lane factor for all 128 accumulator registers.
-//   * V is staged into LDS as [j/4][d][4] (four consecutive keys of one d contiguous), so the
-//     V^T operand (8 keys of one d) is two 8-byte LDS reads; K is staged [j][d] with the 16-byte
-//     chunk index XOR-swizzled by row.  Both are double-buffered, register-staged from global.
-//   * Causal work is triangular: workgroups are issued heaviest query block first.
-
-namespace fmha {
-
-constexpr int BQ = 128;
-constexpr int BKV = 64;
-constexpr int WAVES = 4;
-
-template <int DCH>
-__device__ __forceinline__ int kswz(int row, int chunk) { return chunk ^ (row & (DCH - 1)); }
-
-template <int D>
-struct Smem {
-  static constexpr int K_ELEMS = BKV * D;  // [64][D]
-  static constexpr int V_ELEMS = BKV * D;  // [16][D][4]
-  static constexpr int BYTES = 2 * (K_ELEMS + V_ELEMS) * 2;
-};
-
-template <int D, bool CAUSAL>
-__global__ __launch_bounds__(256, 1) void k_fmha_fwd(
-    const _Float16* __restrict__ Q, const _Float16* __restrict__ Kg,
-    const _Float16* __restrict__ Vg, _Float16* __restrict__ O, float* __restrict__ LSE, int H,
-    int Hkv, int Sq, int Sk, float scale_log2, long q_sb, long q_ss, long q_sh, long k_sb,
-    long k_ss, long k_sh, long v_sb, long v_ss, long v_sh, long o_sb, long o_ss, long o_sh) {
-  static_assert(D == 128 || D == 256, "head dim 128 or 256");
-  constexpr int DCH = D / 8;     // 16-byte chunks per K row
-  constexpr int DS = D / 16;     // MFMA k-steps over d
-  constexpr int DB = D / 32;     // 32-wide d blocks of O^T
-  constexpr int K_IT = BKV * DCH / 256;             // K chunks per thread per block
-  constexpr int V_IT = (BKV / 4) * (D / 8) / 256;   // V 4x8 sub-blocks per thread per block
-
-  __shared__ __attribute__((aligned(16))) _Float16 smem[2 * (Smem<D>::K_ELEMS + Smem<D>::V_ELEMS)];
-  _Float16* const sK = smem;                                  // [2][64][D] swizzled
-  _Float16* const sV = smem + 2 * Smem<D>::K_ELEMS;           // [2][16][D][4]
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int hl = lane >> 5;      // k-group / half of the wave
-  const int l32 = lane & 31;
-
-  // heaviest query block first (causal work grows with the block index)
-  const int nqb = (Sq + BQ - 1) / BQ;
-  const int qb = CAUSAL ? (nqb - 1 - (int)blockIdx.x) : (int)blockIdx.x;
-  const int h = blockIdx.y, b = blockIdx.z;
-  const int hk = h / (H / Hkv);
-  const long off = (long)Sk - Sq;
-  const int q0 = qb * BQ;
-  const int qi = q0 + wave * 32 + l32;                    // this lane's query row
-  const int qrow = min(qi, Sq - 1);
-
-  const _Float16* Qp = Q + b * q_sb + (long)h * q_sh;
-  const _Float16* Kp = Kg + b * k_sb + (long)hk * k_sh;
-  const _Float16* Vp = Vg + b * v_sb + (long)hk * v_sh;
-
-  // ---- Q fragments: lane supplies row qrow, d in [16s + 8*hl, +8) for s = 0..DS-1 -----------
-  f16x8 qf[DS];
-#pragma unroll
-  for (int s = 0; s < DS; ++s)
-    qf[s] = *reinterpret_cast<const f16x8*>(Qp + (long)qrow * q_ss + 16 * s + 8 * hl);
-
-  // ---- key range ---------------------------------------------------------------------------
-  long kend = Sk;
-  if (CAUSAL) {
-    const long last = (long)min(q0 + BQ, Sq) - 1 + off;  // last key any row of the block sees
-    kend = last + 1 < Sk ? last + 1 : Sk;
-    if (kend < 0) kend = 0;
-  }
-  const int nkb = (int)((kend + BKV - 1) / BKV);
-
-  // ---- staging registers -------------------------------------------------------------------
-  u32x4 rk[K_IT];
-  u32x4 rv[V_IT][4];
-  auto load_kv = [&](int kb) {
-    const int j0 = kb * BKV;
-#pragma unroll
-    for (int i = 0; i < K_IT; ++i) {
-      const int q = tid + i * 256, r = q / DCH, c = q % DCH;
-      const int j = min(j0 + r, Sk - 1);
-      rk[i] = *reinterpret_cast<const u32x4*>(Kp + (long)j * k_ss + c * 8);
-    }
-#pragma unroll
-    for (int i = 0; i < V_IT; ++i) {
-      const int q = tid + i * 256, jq = q / (D / 8), dg = q % (D / 8);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int j = min(j0 + 4 * jq + e, Sk - 1);
-        rv[i][e] = *reinterpret_cast<const u32x4*>(Vp + (long)j * v_ss + dg * 8);
-      }
-    }
-  };
-  auto store_kv = [&](int buf) {
-    _Float16* k = sK + buf * Smem<D>::K_ELEMS;
-    _Float16* v = sV + buf * Smem<D>::V_ELEMS;
-#pragma unroll
-    for (int i = 0; i < K_IT; ++i) {
-      const int q = tid + i * 256, r = q / DCH, c = q % DCH;
-      *reinterpret_cast<u32x4*>(k + r * D + kswz<DCH>(r, c) * 8) = rk[i];
-    }
-#pragma unroll
-    for (int i = 0; i < V_IT; ++i) {
-      const int q = tid + i * 256, jq = q / (D / 8), dg = q % (D / 8);
-      // transpose 4 keys x 8 d (4 rows of 4 dwords) into 8 d x 4 keys (8 runs of 8 bytes)
-      u32x4 o[4];
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {  // dword w holds d = 2w, 2w+1 of each key row
-        const uint32_t a0 = rv[i][0][w], a1 = rv[i][1][w], a2 = rv[i][2][w], a3 = rv[i][3][w];
-        // d = 2w   : keys 0..3 low halves ; d = 2w+1 : keys 0..3 high halves
-        const uint32_t lo01 = __builtin_amdgcn_perm(a1, a0, 0x05040100u);
-        const uint32_t lo23 = __builtin_amdgcn_perm(a3, a2, 0x05040100u);
-        const uint32_t hi01 = __builtin_amdgcn_perm(a1, a0, 0x07060302u);
-        const uint32_t hi23 = __builtin_amdgcn_perm(a3, a2, 0x07060302u);
-        o[w] = u32x4{lo01, lo23, hi01, hi23};
-      }
-      u32x4* dst = reinterpret_cast<u32x4*>(v + ((long)jq * D + dg * 8) * 4);
-#pragma unroll
-      for (int w = 0; w < 4; ++w) dst[w] = o[w];
-    }
-  };
-
-  f32x16 acc_o[DB];
-#pragma unroll
-  for (int i = 0; i < DB; ++i)
-#pragma unroll
-    for (int v = 0; v < 16; ++v) acc_o[i][v] = 0.f;
-  float m_run = -__builtin_inff();
-  float l_run = 0.f;
-
-  if (nkb > 0) {
-    load_kv(0);
-    store_kv(0);
-  }
-  __syncthreads();
-
-  for (int kb = 0; kb < nkb; ++kb) {
-    const int cur = kb & 1;
-    if (kb + 1 < nkb) load_kv(kb + 1);
-    const _Float16* k = sK + cur * Smem<D>::K_ELEMS;
-    const _Float16* v = sV + cur * Smem<D>::V_ELEMS;
-    const int j0 = kb * BKV;
-
-    // S^T for two 32-key blocks: lane holds keys j0 + 32*jb + 8g + 4*hl + e (reg 4g+e) of row qi
-    f32x16 s[2];
-#pragma unroll
-    for (int jb = 0; jb < 2; ++jb) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s[jb][r] = 0.f;
-      const int kr = jb * 32 + l32;
-#pragma unroll
-      for (int st = 0; st < DS; ++st) {
-        const f16x8 kf =
-            *reinterpret_cast<const f16x8*>(k + kr * D + kswz<DCH>(kr, 2 * st + hl) * 8);
-        s[jb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[st], s[jb], 0, 0, 0);
-      }
-    }
-
-    // scale, mask, block row max
-    const bool need_mask = (j0 + BKV > Sk) || (CAUSAL && (long)(j0 + BKV - 1) > (long)q0 + off);
-    float mx = -__builtin_inff();
-#pragma unroll
-    for (int jb = 0; jb < 2; ++jb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float x = s[jb][r] * scale_log2;
-        if (need_mask) {
-          const int j = j0 + jb * 32 + 8 * (r >> 2) + 4 * hl + (r & 3);
-          const bool hide = (j >= Sk) || (CAUSAL && (long)j > (long)qi + off);
-          x = hide ? -__builtin_inff() : x;
-        }
-        s[jb][r] = x;
-        mx = fmaxf(mx, x);
-      }
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m_run, mx);
-    const float m_use = (m_new == -__builtin_inff()) ? 0.f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-    float psum = 0.f;
-    f16x8 pf[4];  // P^T operand fragments for the four 16-key MFMA steps
-#pragma unroll
-    for (int jb = 0; jb < 2; ++jb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = __builtin_amdgcn_exp2f(s[jb][r] - m_use);
-        psum += p;
-        pf[jb * 2 + (r >> 3)][r & 7] = (_Float16)p;
-      }
-    psum += __shfl_xor(psum, 32);
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-#pragma unroll
-    for (int i = 0; i < DB; ++i)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc_o[i][r] *= alpha;
-
-    // O^T += V^T . P^T over the 64 keys of this block (4 MFMA k-steps of 16 keys)
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      // keys of step t for k-group hl: 32*(t/2) + 16*(t%2) + 8*(e/4) + 4*hl + e%4
-      const int jq0 = 8 * (t >> 1) + 4 * (t & 1) + hl;  // j/4 of elements 0..3
-      const int jq1 = jq0 + 2;                          // j/4 of elements 4..7
-#pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        const int d = db * 32 + l32;
-        const u32x2 v0 = *reinterpret_cast<const u32x2*>(v + ((long)jq0 * D + d) * 4);
-        const u32x2 v1 = *reinterpret_cast<const u32x2*>(v + ((long)jq1 * D + d) * 4);
-        const u32x4 vv = {v0[0], v0[1], v1[0], v1[1]};
-        acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(vv), pf[t], acc_o[db], 0, 0, 0);
-      }
-    }
-
-    if (kb + 1 < nkb) store_kv(cur ^ 1);
-    __syncthreads();
-  }
-
-  // ---- epilogue: O[qi][d] = acc / l; lane holds d = db*32 + 8g + 4*hl + e ----------------------
-  if (qi < Sq) {
-    const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
-    _Float16* Op = O + b * o_sb + (long)qi * o_ss + (long)h * o_sh;
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        f16x4 o;
-        o[0] = (_Float16)(acc_o[db][4 * g + 0] * inv);
-        o[1] = (_Float16)(acc_o[db][4 * g + 1] * inv);
-        o[2] = (_Float16)(acc_o[db][4 * g + 2] * inv);
-        o[3] = (_Float16)(acc_o[db][4 * g + 3] * inv);
-        *reinterpret_cast<f16x4*>(Op + db * 32 + 8 * g + 4 * hl) = o;
-      }
-    if (LSE && hl == 0)
-      LSE[((long)b * H + h) * Sq + qi] =
-          l_run > 0.f ? m_run * 0.6931471805599453f + __logf(l_run) : -__builtin_inff();
-  }
-}
-
-// ============================================================================================
-// k_fmha_fwd2 -- the DMA form.  Same semantics and the same MFMA formulation (S^T = K.Q^T, each
-// lane owns one query row; O^T += V^T.P^T with P^T taken from the S^T accumulators), changed in
-// how the key/value blocks reach the matrix cores and in the softmax bookkeeping:
-//   * K and V blocks of BKV keys are copied global -> LDS with LDS-DMA (global_load_lds_dwordx4),
-//     no register staging.  Both are stored in their natural [key][d] order with the 16-byte
-//     chunk index XOR-ed by fmha_swz(key % 16), a bit swap of the 4-bit row index chosen so that
-//     both read patterns are free of bank conflicts on the 64-bank LDS: the K read (16 rows, one
-//     chunk) and the transposed V read (4 rows x 4 consecutive chunks) each land on 16 distinct
-//     16-byte slots of a 256-byte bank window.  The swizzle is applied on the global side (lane l
-//     of a DMA instruction writes bytes [16l, 16l+16) of a 1 KiB block and fetches the chunk
-//     that belongs there).
+//     per-lane factor for all accumulator registers.
+//   * K and V blocks are copied global -> LDS with LDS-DMA (global_load_lds_dwordx4), no register
+//     staging.  Both are stored in their natural [key][d] order with the 16-byte chunk index
+//     XOR-ed by fmha_swz(key % 16), a bit swap of the 4-bit row index chosen so that both read
+//     patterns are free of bank conflicts on the 64-bank LDS: the K read (16 rows, one chunk) and
+//     the transposed V read (4 rows x 4 consecutive chunks) each land on 16 distinct 16-byte
+//     slots of a 256-byte bank window.  The swizzle is applied on the global side (lane l of a
+//     DMA instruction writes bytes [16l, 16l+16) of a 1 KiB block and fetches the chunk that
+//     belongs there).
 //   * The V^T operand (8 keys of one d per lane) is read with ds_read_b64_tr_b16: within each
 //     group of 16 lanes, lane j supplies the address of 4 consecutive d of key row (base + j/4),
 //     and lane i receives, for e = 0..3, element i%4 of the row supplied by lane 4e + i/4 --
 //     i.e. key base+e at d = d0 + i.  Two such reads give the 8 keys of one MFMA k-group.
-//   * All LDS read addresses are a per-lane offset (computed once) plus a compile-time constant,
-//     and all DMA sources a per-lane 32-bit offset from a wave-uniform block base.
 //   * Rescale threshold: the running max used for the exponentials only moves when some lane's
-//     block max exceeds it by more than TAU (base-2 units).  Any reference value gives the same
-//     softmax (the numerator and l use the same one), exp2 arguments stay <= TAU, and the O
-//     rescale -- 128 AGPR read/multiply/write triples per lane -- is almost never paid.
-//   * Blocks are numbered heaviest query block first over ALL heads and batches.
-// ============================================================================================
+//     block max exceeds it by more than FMHA_TAU (base-2 units).  Any reference value gives the
+//     same softmax (the numerator and l use the same one), exp2 arguments stay <= TAU, and the O
+//     rescale is almost never paid.
+//   * Causal work is triangular: workgroups are numbered heaviest query block first over ALL
+//     heads and batches.
+
+namespace fmha {
+
+constexpr int BQ = 128;  // query rows per workgroup (4 waves x 32)
+
 typedef __attribute__((address_space(3))) void fmha_lds_void_t;
 typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 fmha_h4;
 typedef __attribute__((address_space(3))) fmha_h4 fmha_lds_h4;
@@ -298,246 +61,15 @@ constexpr float FMHA_TAU = 8.f;  // log2 of the largest unnormalised probability
 // swizzle key of a key row (only its low 4 bits matter): swap the two 2-bit halves
 __device__ __forceinline__ int fmha_swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
 
-// WAVES = 4 or 8 waves per workgroup, 32 query rows each (the query block is 32*WAVES rows).
-template <int D, bool CAUSAL, int BKV2, int MINB, int WAVES = 4>
-__global__ __launch_bounds__(64 * WAVES, MINB) void k_fmha_fwd2(
-    const _Float16* __restrict__ Q, const _Float16* __restrict__ Kg,
-    const _Float16* __restrict__ Vg, _Float16* __restrict__ O, float* __restrict__ LSE, int B,
-    int H, int Hkv, int Sq, int Sk, float scale_log2, long q_sb, long q_ss, long q_sh, long k_sb,
-    long k_ss, long k_sh, long v_sb, long v_ss, long v_sh, long o_sb, long o_ss, long o_sh) {
-  static_assert(D == 128 || D == 256, "head dim 128 or 256");
-  static_assert(BKV2 == 32 || BKV2 == 64, "key block 32 or 64");
-  constexpr int NJ = BKV2 / 32;              // 32-key MFMA blocks of S per key block
-  constexpr int DCH = D / 8;                 // 16-byte chunks per key row
-  constexpr int DS = D / 16;                 // MFMA k-steps over d for S
-  constexpr int DB = D / 32;                 // 32-wide d blocks of O^T
-  constexpr int RB = D * 2;                  // bytes per key row in LDS
-  constexpr int ROWS_PER_KB = 1024 / RB;     // key rows per 1 KiB DMA block
-  constexpr int BLK = BKV2 / ROWS_PER_KB;    // DMA blocks per operand per KV block
-  constexpr int BLK_W = BLK / WAVES;         // ... per wave
-  constexpr int BQW = 32 * WAVES;            // query rows per workgroup
-  constexpr int TILE_B = BKV2 * RB;          // bytes of one K (or V) block
-  static_assert(BLK % WAVES == 0, "DMA blocks split over the waves");
-
-  __shared__ __attribute__((aligned(1024))) char smem[2 * 2 * TILE_B];  // [stage][K,V][BKV][D]
-
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int hl = lane >> 5;
-  const int l32 = lane & 31;
-
-  // heaviest query block first over all (b, h)
-  const int nqb = (Sq + BQW - 1) / BQW;
-  const int bid = blockIdx.x;
-  const int per_qb = H * B;
-  const int qb = CAUSAL ? (nqb - 1 - bid / per_qb) : bid / per_qb;
-  const int hb = bid % per_qb;
-  const int h = hb % H, b = hb / H;
-  const int hk = h / (H / Hkv);
-  const int off = Sk - Sq;
-  const int q0 = qb * BQW;
-  const int qi = q0 + wave * 32 + l32;
-  const int qrow = min(qi, Sq - 1);
-
-  const _Float16* Qp = Q + b * q_sb + (long)h * q_sh;
-  const char* Kp = reinterpret_cast<const char*>(Kg + b * k_sb + (long)hk * k_sh);
-  const char* Vp = reinterpret_cast<const char*>(Vg + b * v_sb + (long)hk * v_sh);
-
-  f16x8 qf[DS];
-#pragma unroll
-  for (int st = 0; st < DS; ++st)
-    qf[st] = *reinterpret_cast<const f16x8*>(Qp + (long)qrow * q_ss + 16 * st + 8 * hl);
-
-  int kend = Sk;
-  if (CAUSAL) {
-    const int last = min(q0 + BQW, Sq) - 1 + off;
-    kend = last + 1 < Sk ? last + 1 : Sk;
-    if (kend < 0) kend = 0;
-  }
-  const int nkb = (kend + BKV2 - 1) / BKV2;
-
-  // ---- DMA: block i of this wave = operand block (i*WAVES + wave); lane -> (row, phys chunk) ---
-  const int rin = lane / DCH, phys = lane % DCH;
-  unsigned ksrc[BLK_W], vsrc[BLK_W];  // byte offsets from the key block's first row
-  int drow[BLK_W];
-#pragma unroll
-  for (int i = 0; i < BLK_W; ++i) {
-    const int r = (i * WAVES + wave) * ROWS_PER_KB + rin;
-    const int c = phys ^ fmha_swz(r);  // logical chunk stored at slot `phys`
-    drow[i] = r;
-    ksrc[i] = (unsigned)(r * k_ss * 2 + c * 16);
-    vsrc[i] = (unsigned)(r * v_ss * 2 + c * 16);
-  }
-  auto issue = [&](int kb) {
-    char* sk = smem + (kb & 1) * 2 * TILE_B;
-    char* sv = sk + TILE_B;
-    const int j0 = kb * BKV2;
-    const char* kblk = Kp + (long)j0 * k_ss * 2;
-    const char* vblk = Vp + (long)j0 * v_ss * 2;
-    if (j0 + BKV2 <= Sk) {
-#pragma unroll
-      for (int i = 0; i < BLK_W; ++i) {
-        __builtin_amdgcn_global_load_lds((void*)(kblk + ksrc[i]),
-                                         (fmha_lds_void_t*)(sk + (i * WAVES + wave) * 1024), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds((void*)(vblk + vsrc[i]),
-                                         (fmha_lds_void_t*)(sv + (i * WAVES + wave) * 1024), 16, 0, 0);
-      }
-    } else {  // ragged key tail: rows past Sk re-read row Sk-1 (masked out of the softmax)
-#pragma unroll
-      for (int i = 0; i < BLK_W; ++i) {
-        const long back = (long)max(0, j0 + drow[i] - (Sk - 1));
-        __builtin_amdgcn_global_load_lds((void*)(kblk + ksrc[i] - back * k_ss * 2),
-                                         (fmha_lds_void_t*)(sk + (i * WAVES + wave) * 1024), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds((void*)(vblk + vsrc[i] - back * v_ss * 2),
-                                         (fmha_lds_void_t*)(sv + (i * WAVES + wave) * 1024), 16, 0, 0);
-      }
-    }
-  };
-
-  // ---- LDS read offsets (bytes within a stage's K or V tile) ------------------------------------
-  // K (S^T operand): row kr = 32*jb + l32, logical chunk 2*st + hl, swizzle key fmha_swz(l32)
-  // (same for every jb).  (2st + hl) ^ key only touches bits 0..3, i.e. st & 7: eight offsets.
-  const int kkey = fmha_swz(l32);
-  int koff[8];
-#pragma unroll
-  for (int s7 = 0; s7 < 8; ++s7) koff[s7] = l32 * RB + (((2 * s7) | hl) ^ kkey) * 16;
-  // V^T (transposed reads): lane (group tg, index tj) addresses key row R(t) + tk (+8 for the
-  // second read; R(t) is a multiple of 16, so the row's swizzle key is fmha_swz(tk) or
-  // fmha_swz(tk + 8)) at d = 32*db + 16*(tg&1) + 4*(tj&3): logical chunk 4*db + cd, byte 8*(tj&1).
-  const int tg = lane >> 4, tj = lane & 15;
-  const int tk = 4 * (tg >> 1) + (tj >> 2);          // 0..7: the swizzle key of the first read
-  const int cd = 2 * (tg & 1) + ((tj & 3) >> 1);     // 0..3
-  const int half = 8 * (tj & 1);
-  // (4db + cd) ^ key touches bits 0..3 only: four lane offsets per read, by db & 3
-  int voff0[4], voff1[4];
-#pragma unroll
-  for (int p4 = 0; p4 < 4; ++p4) {
-    voff0[p4] = tk * RB + (((p4 << 2) | cd) ^ fmha_swz(tk)) * 16 + half;
-    voff1[p4] = (tk + 8) * RB + (((p4 << 2) | cd) ^ fmha_swz(tk + 8)) * 16 + half;
-  }
-
-  f32x16 acc_o[DB];
-#pragma unroll
-  for (int i = 0; i < DB; ++i)
-#pragma unroll
-    for (int v = 0; v < 16; ++v) acc_o[i][v] = 0.f;
-  float m_run = -__builtin_inff();  // reference value of the exponentials (base 2, scaled)
-  float l_run = 0.f;
-
-  if (nkb > 0) issue(0);
-
-  for (int kb = 0; kb < nkb; ++kb) {
-    asm volatile("" ::: "memory");
-    fmha_wait_vm<0>();
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    if (kb + 1 < nkb) issue(kb + 1);
-    const char* k = smem + (kb & 1) * 2 * TILE_B;
-    const char* v = k + TILE_B;
-    const int j0 = kb * BKV2;
-
-    // S^T in 32-key blocks: lane holds keys j0 + 32*jb + 8*(r>>2) + 4*hl + (r&3) of row qi
-    f32x16 s[NJ];
-#pragma unroll
-    for (int jb = 0; jb < NJ; ++jb) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s[jb][r] = 0.f;
-#pragma unroll
-      for (int st = 0; st < DS; ++st) {
-        const f16x8 kf = *reinterpret_cast<const f16x8*>(k + koff[st & 7] + (st >> 3) * 256 +
-                                                         jb * 32 * RB);
-        s[jb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[st], s[jb], 0, 0, 0);
-      }
-    }
-
-    // masked raw-score max (scale > 0, so the max commutes with the scaling)
-    const bool need_mask = (j0 + BKV2 > Sk) || (CAUSAL && j0 + BKV2 - 1 > q0 + off);
-    float mx = -__builtin_inff();
-#pragma unroll
-    for (int jb = 0; jb < NJ; ++jb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float x = s[jb][r];
-        if (need_mask) {
-          const int j = j0 + 32 * jb + 8 * (r >> 2) + 4 * hl + (r & 3);
-          const bool hide = (j >= Sk) || (CAUSAL && j > qi + off);
-          x = hide ? -__builtin_inff() : x;
-        }
-        s[jb][r] = x;
-        mx = fmaxf(mx, x);
-      }
-    mx = fmaxf(mx, __shfl_xor(mx, 32)) * scale_log2;
-    // move the reference only when some lane's max overtook it by more than TAU (or it was unset)
-    const bool move = !(mx - m_run <= FMHA_TAU);  // true for m_run = -inf and a finite mx
-    if (__builtin_amdgcn_ballot_w64(move) != 0) {
-      const float m_new = fmaxf(m_run, mx);
-      const float alpha = (m_new == -__builtin_inff()) ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
-      l_run *= alpha;
-      m_run = m_new;
-#pragma unroll
-      for (int i = 0; i < DB; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc_o[i][r] *= alpha;
-    }
-    const float m_use = (m_run == -__builtin_inff()) ? 0.f : m_run;
-    float psum = 0.f;
-    f16x8 pf[2 * NJ];
-#pragma unroll
-    for (int jb = 0; jb < NJ; ++jb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[jb][r], scale_log2, -m_use));
-        psum += p;
-        pf[2 * jb + (r >> 3)][r & 7] = (_Float16)p;
-      }
-    psum += __shfl_xor(psum, 32);
-    l_run += psum;
-
-    // O^T += V^T . P^T in MFMA k-steps of 16 keys; step t, element e <-> key
-    // 32(t/2) + 16(t%2) + 8(e/4) + 4*hl + e%4, matching pf[t][e] above
-#pragma unroll
-    for (int t = 0; t < 2 * NJ; ++t) {
-      const int rt = 32 * (t >> 1) + 16 * (t & 1);
-#pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        const u32x2 v0 = fmha_tr_read(v + voff0[db & 3] + rt * RB + (db >> 2) * 256);
-        const u32x2 v1 = fmha_tr_read(v + voff1[db & 3] + rt * RB + (db >> 2) * 256);
-        const u32x4 vv = {v0[0], v0[1], v1[0], v1[1]};
-        acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(vv), pf[t], acc_o[db], 0, 0, 0);
-      }
-    }
-  }
-
-  if (qi < Sq) {
-    const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
-    _Float16* Op = O + b * o_sb + (long)qi * o_ss + (long)h * o_sh;
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        f16x4 o;
-        o[0] = (_Float16)(acc_o[db][4 * g + 0] * inv);
-        o[1] = (_Float16)(acc_o[db][4 * g + 1] * inv);
-        o[2] = (_Float16)(acc_o[db][4 * g + 2] * inv);
-        o[3] = (_Float16)(acc_o[db][4 * g + 3] * inv);
-        *reinterpret_cast<f16x4*>(Op + db * 32 + 8 * g + 4 * hl) = o;
-      }
-    if (LSE && hl == 0)
-      LSE[((long)b * H + h) * Sq + qi] =
-          l_run > 0.f ? m_run * 0.6931471805599453f + __logf(l_run) : -__builtin_inff();
-  }
-}
-
 // ============================================================================================
-// k_fmha_fwd3 -- k_fmha_fwd2 with the score MFMAs of the NEXT key block overlapping the softmax
+// k_fmha_fwd3 -- software-pipelined: the score MFMAs of the NEXT key block overlap the softmax
 // of the current one.  Iteration kb computes S(kb+1) = K(kb+1).Q^T on the matrix cores while the
 // VALU turns S(kb) into P(kb) (max, exponentials, sums), then O^T += V(kb)^T . P(kb)^T.  K runs
 // one block ahead of V: K(kb+2) and V(kb+1) are copied during iteration kb into the slots that
-// K(kb) and V(kb-1) left, so the LDS footprint is the same two K and two V blocks as before.
-// sched_group_barrier hints interleave one MFMA with a few VALU/LDS instructions so the wave
-// keeps issuing softmax work while each MFMA occupies the matrix core.
+// K(kb) and V(kb-1) left, so the LDS footprint is two K and two V blocks.
 // ============================================================================================
-// SG = 1 adds sched_group_barrier hints that interleave MFMAs with LDS reads and VALU work.
+// SG = 1 adds sched_group_barrier hints that interleave MFMAs with LDS reads and VALU work
+// (measured slower at C5; the shipped instantiation has SG = 0).
 template <int D, bool CAUSAL, int BKV2, int SG = 0>
 __global__ __launch_bounds__(256, 1) void k_fmha_fwd3(
     const _Float16* __restrict__ Q, const _Float16* __restrict__ Kg,

@@ -1,0 +1,134 @@
+"""GPU parity cases that reach every row of the shipped ladders, named by the row they must take.
+
+One list per ladder (plain and fused gate/up, per weight format).  Each case is
+(row tag, M, N, K); for the gate/up ladders N is the output width (the weight has 2N rows).
+tests/test_ladder_coverage.py checks on the CPU, with the deliveries' own select.py, that every
+case routes to the row it names and that every row of every ladder (per format) is named by some
+case; tests/test_gpu_ladder_rows.py runs every case on the GPU against the oracle and checks the
+compiled dispatcher's route as well.  Shapes are the BASELINE configs where a config reaches the
+row, else the smallest realistic shape that does (K > 65536 is past the line kernel's rows).
+
+The pattern is the reference's dispatch consistency gate
+(kernels/shipped/gemm_fp16/sm_70/test_gate.py:102-146) and its ship probe
+(kernels/shipped/gemm_fp16/sm_70/ship_probe.cu:41-79), extended to run every row.
+"""
+
+FP16 = [
+    ("l0r1d3", 1, 15360, 3840),
+    ("l0r1d3", 1, 3840, 15360),
+    ("s1a_r1u4", 1, 512, 65792),
+    ("l1r1n4d3", 8, 15360, 3840),
+    ("l1r1d4", 16, 3840, 15360),
+    ("s16r1u4", 16, 512, 65792),
+    ("l2r1n4d3", 24, 15360, 3840),
+    ("l2r1d4", 32, 3840, 15360),
+    ("s32r1u4", 32, 512, 65792),
+    ("l4r1n4d3", 64, 15360, 3840),
+    ("l4r1d3", 64, 3840, 15360),           # the C2 decode-sweep point M = 64, N = 3840
+    ("d128x64k64s4", 128, 15360, 3840),
+    ("d128x64k64s4", 200, 8192, 3840),
+    ("d64x64k64s4", 128, 3840, 15360),
+    ("d64x64k64s4", 256, 3840, 15360),
+    ("l8r1n2d3", 100, 3872, 3840),         # 64 < M <= 128 with N % 64 == 32
+    ("d128x128k64s4", 256, 15360, 3840),
+    ("i256x256k64w4r8", 512, 4096, 3840),
+    ("i256x256k64w4r8", 2049, 3840, 15360),
+]
+
+# Strided operands and an 8-byte-aligned C (its rows take the 8-byte store path): (row, M, N, K,
+# extra elements per row of A, B, C)
+FP16_STRIDED = [
+    ("l1r1d4", 16, 3840, 3840, 8, 16, 4),
+    ("l4r1d3", 64, 3840, 3840, 8, 8, 4),
+    ("d64x64k64s4", 128, 3840, 3840, 8, 8, 4),
+    ("d128x128k64s4", 256, 15360, 3840, 16, 8, 4),
+    ("i256x256k64w4r8", 300, 4096, 3840, 8, 16, 4),
+    ("i256x256k64w4r8", 512, 4096, 3840, 64, 64, 64),
+]
+
+FP16_GATE_UP = [
+    ("gl0r1n2d3", 1, 17408, 5120),
+    ("gl1r1n4d3", 16, 17408, 5120),
+    ("gl1r1d3", 16, 7680, 3840),
+    ("gl2r1n4d3", 32, 17408, 5120),
+    ("gl2r1d3", 32, 7680, 3840),
+    ("gh1r1u2n2", 1, 512, 65664),
+    ("gh16r1u4n2", 16, 512, 65792),
+    ("gh32r1u4n4", 32, 512, 65792),
+    ("g32r1u4", 32, 496, 65792),
+]
+
+W8 = {
+    1: [
+        ("l0r1d4", 1, 7168, 5120),
+        ("l1r1n4d3", 16, 34816, 5120),
+        ("l1r1n2d4", 16, 5120, 17408),
+        ("l2r1n4d4", 32, 34816, 5120),
+        ("l2r1n2d4", 32, 5120, 6144),
+        ("s1a_r1u8", 1, 512, 66048),
+        ("s1a_r1u4", 1, 512, 65792),
+        ("s8r2u4", 8, 512, 65792),
+        ("h16r1u4n2", 16, 512, 65792),
+        ("s16r1u4", 16, 1040, 5120),
+        ("h32r1u4n2", 32, 512, 65792),
+        ("l4r1n4d3", 64, 34816, 5120),
+        ("l4r1n2d3", 64, 5120, 17408),
+        ("l8r1n2d3", 128, 5120, 17408),
+        ("m128x128k64", 128, 34816, 5120),
+        ("m128x128k64", 256, 5120, 5120),
+        ("m128x128k64s16", 2048, 1024, 5120),
+        ("i8x256k64s3", 2048, 7168, 5120),
+        ("m256x256k64", 512, 2048, 5184),
+    ],
+    2: [
+        ("l0r1d4", 1, 7168, 5120),
+        ("l1r1n4d3", 16, 34816, 5120),
+        ("l1r1n2d4", 16, 5120, 17408),
+        ("l2r1n4d4", 32, 34816, 5120),
+        ("l2r1n2d4", 32, 5120, 6144),
+        ("s1a_r1u8", 1, 512, 66048),
+        ("s1a_r1u4", 1, 512, 65792),
+        ("s8r2u4", 8, 512, 65792),
+        ("h16r1u4n2", 16, 512, 65792),
+        ("s16r1u4", 16, 1040, 5120),
+        ("h32r1u4n2", 32, 512, 65792),
+        ("l4r1n4d3", 64, 34816, 5120),
+        ("l4r1n2d3", 64, 5120, 17408),
+        ("l8r1n2d3", 128, 5120, 17408),
+        ("m128x128k64", 128, 34816, 5120),
+        ("m128x128k64", 256, 5120, 5120),
+        ("m128x128k64s16", 2048, 1024, 5120),
+        ("i8x256k64s3", 2048, 7168, 5120),
+    ],
+}
+
+W8_GATE_UP = {
+    1: [
+        ("gl0r1n2d4", 1, 17408, 5120),
+        ("gl1r1n4d3", 16, 17408, 5120),
+        ("gl1r1n2d4", 8, 7680, 3840),
+        ("gl2r1n4d4", 32, 17408, 5120),
+        ("gl2r1n2d4", 32, 7680, 3840),
+        ("g1a_r1u2", 1, 512, 65664),
+        ("gh16r1u2n2", 16, 512, 65664),
+        ("gh32r1u2n4", 32, 512, 65664),
+        ("g32r1u4", 32, 496, 65792),
+    ],
+    2: [
+        ("gl0r1n2d4", 1, 17408, 5120),
+        ("gl1r1n4d3", 16, 17408, 5120),
+        ("gl1r1n2d4", 8, 7680, 3840),
+        ("gl2r1n4d4", 32, 17408, 5120),
+        ("gl2r1n2d4", 32, 7680, 3840),
+        ("g1a_r1u8", 1, 512, 66048),
+        ("g1a_r1u4", 1, 512, 65792),
+        ("gh16r1u4n2", 16, 512, 65792),
+        ("gh32r1u4n4", 32, 512, 65792),
+        ("g32r1u4", 32, 496, 65792),
+    ],
+}
+
+
+def case_id(case) -> str:
+    tag, M, N, K = case[:4]
+    return "%s-m%d-n%d-k%d" % (tag, M, N, K)

@@ -117,17 +117,19 @@ def test_fmha_strided_bhsd(gpu):
 
 
 def test_fmha_c5_sampled_rows(gpu):
-    """Config C5 at full size (B=1, H=16, Hkv=8, S=4096, D=256, causal); the oracle computes a
-    sample of query rows: the first and last of the sequence, the edges of query blocks and a
-    seeded random set."""
+    """Config C5 at full size (B=1, H=16, Hkv=8, S=4096, D=256, causal); the oracle computes 512
+    query rows of all 16 heads: the first and last of the sequence, the edges of query blocks and
+    a seeded random set."""
     B, S, H, Hkv, D = 1, 4096, 16, 8, 256
     Q, K, V = _inputs(B, S, S, H, Hkv, D, seed=5)
     scale = 1.0 / 16
     got, lse = _run(Q, K, V, scale, True, gpu)
     assert O.count_poison(got) == 0
     g = np.random.Generator(np.random.PCG64(99))
-    rows = np.unique(np.concatenate([[0, 1, 63, 64, 127, 128, 2047, 2048, S - 129, S - 1],
-                                     g.integers(0, S, 22)])).astype(np.int32)
+    edges = [0, 1, 31, 32, 63, 64, 127, 128, 255, 256, 2047, 2048, S - 129, S - 128, S - 2, S - 1]
+    rest = g.permutation(np.setdiff1d(np.arange(S), edges))[:512 - len(edges)]
+    rows = np.unique(np.concatenate([edges, rest])).astype(np.int32)
+    assert rows.size == 512
     ref, lref = O.fmha_fwd(Q, K, V, scale, True, rows=rows)
     r = O.rel_l2(got[:, rows], ref[:, rows])
     say("C5 sampled relL2 %.3e over %d rows x %d heads" % (r, rows.size, H))

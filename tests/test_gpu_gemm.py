@@ -97,20 +97,22 @@ def test_gemm_fp16_parity(gpu, M, N, K):
 
 
 def test_gemm_fp16_parity_config1(gpu):
-    """BASELINE config 1 at full size: 4096 x 15360 x 3840.  Coverage over every cell; values
-    against the oracle on 256 sampled rows (both tile edges) and fp64 on 2048 cells."""
+    """BASELINE config 1 at full size: 4096 x 15360 x 3840.  Coverage over every cell; the WHOLE
+    output against the oracle (relL2), fp64 on 2048 cells, and the worst row's relL2 so a
+    localised error (one bad tile) cannot hide in the global norm."""
     M, N, K = 4096, 15360, 3840
     say("config1", M, N, K)
     A = O.randn_f16((M, K), 11, K ** -0.5)
     B = O.randn_f16((N, K), 77, K ** -0.5)
     C = _run(A, B, gpu)
     assert O.count_poison(C) == 0
-    rows = np.r_[0:128, M - 128:M]
-    ref = O.gemm_f16(A[rows], B)
-    rel = O.rel_l2(np.ascontiguousarray(C[rows]), ref)
+    ref = O.gemm_f16(A, B)
+    rel = O.rel_l2(C, ref)
+    d = C.astype(np.float64) - ref.astype(np.float64)
+    row_rel = np.sqrt((d * d).sum(1) / np.maximum((ref.astype(np.float64) ** 2).sum(1), 1e-30))
     worst, bad = O.spot_fp64(A, B, C, cells=2048)
-    say("  relL2 %.3e spot %.3e" % (rel, worst))
-    assert rel <= 3e-3 and bad == 0
+    say("  relL2 %.3e worst row %.3e spot %.3e" % (rel, row_rel.max(), worst))
+    assert rel <= 3e-3 and row_rel.max() <= 3e-3 and bad == 0
 
 
 def test_not_covered_returns_fallback(gpu):

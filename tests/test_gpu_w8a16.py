@@ -120,20 +120,19 @@ def test_w8a16_parity_past_the_line_rows(gpu, fmt, M):
 
 
 @pytest.mark.parametrize("fmt", [1, 2])
-def test_w8a16_parity_prefill(gpu, fmt):
-    """M = 2048 on two of the dense shapes; oracle on sampled rows."""
-    for N, K in [(5120, 6144), (7168, 5120)]:
-        M = 2048
-        say("w8a16 prefill fmt", fmt, M, N, K)
-        A = O.randn_f16((M, K), 11, K ** -0.5)
-        q, s, z = make_weights(N, K, fmt, 77)
-        C = _run(A, q, s, z, fmt, gpu)
-        assert O.count_poison(C) == 0
-        rows = np.r_[0:64, 1000:1064, M - 64:M]
-        ref = O.gemm_w8a16(A[rows], q, s, z, 128, fmt)
-        rel = O.rel_l2(np.ascontiguousarray(C[rows]), ref)
-        say("  relL2 %.3e" % rel)
-        assert rel <= 3e-3
+@pytest.mark.parametrize("NK", SHAPES_NK, ids=lambda nk: "n%d_k%d" % nk)
+def test_w8a16_parity_prefill(gpu, fmt, NK):
+    """M = 2048 (configs 3 and 4) on all six dense shapes; the whole output against the oracle."""
+    N, K = NK
+    M = 2048
+    say("w8a16 prefill fmt", fmt, M, N, K, "route", _route(fmt, M, N, K))
+    A = O.randn_f16((M, K), 11, K ** -0.5)
+    q, s, z = make_weights(N, K, fmt, 77)
+    C = _run(A, q, s, z, fmt, gpu)
+    assert O.count_poison(C) == 0
+    rel = O.rel_l2(C, O.gemm_w8a16(A, q, s, z, 128, fmt))
+    say("  relL2 %.3e" % rel)
+    assert rel <= 3e-3
 
 
 @pytest.mark.parametrize("fmt", [1, 2])

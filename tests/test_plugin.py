@@ -203,6 +203,33 @@ def test_recognize_refuses_mismatched_signature(tmp_path):
         recognize.from_file(str(p), C1)
 
 
+def test_recognize_refusals():
+    """The refusals of the reference's recogniser (tempo/core/op/recognize.py:41-141)."""
+    from tempo.core.op import recognize as R
+
+    good = open(NAIVE, encoding="utf-8").read()
+    with pytest.raises(R.NotRecognised):            # no block at all
+        R.from_text("__global__ void k(int* x) {}", C1)
+    with pytest.raises(R.NotRecognised):            # block names no entry
+        R.from_text(good.replace("entry: naive_gemm_fp16", "entry_x: y"), C1)
+    with pytest.raises(R.NotRecognised):            # '*' shape not supplied
+        R.from_text(good, {"M": 4, "N": 8})
+    # the block's own mention of the entry never counts as its declaration
+    body = good.split("TEMPO-OP-END", 1)[0] + "TEMPO-OP-END\n"
+    with pytest.raises(R.NotRecognised):
+        R.from_text(body, C1)
+    # parameter counting is bracket-aware: a template argument's comma is not a parameter
+    tmpl = good.replace("int M, int N, int K)", "int M, int N, Pair<int, int> K)", 1)
+    assert R.from_text(tmpl, C1).shapes == {"M": 4096, "N": 15360, "K": 3840}
+    extra = good.replace("int M, int N, int K)", "int M, int N, int K, int L)", 1)
+    with pytest.raises(R.NotRecognised):
+        R.from_text(extra, C1)
+    # given shapes override declared ones; declared numbers are used when none is given
+    fixed = good.replace("shape: M=* N=* K=*", "shape: M=7 N=8 K=16")
+    assert R.from_text(fixed).shapes == {"M": 7, "N": 8, "K": 16}
+    assert R.from_text(fixed, {"M": 9}).shapes == {"M": 9, "N": 8, "K": 16}
+
+
 # ---- core oracle gate / coverage / ratio ------------------------------------------------------
 def test_oracle_gate_needs_named_independent_path():
     from tempo.core.op.oracle import OracleResult
@@ -255,3 +282,58 @@ def test_tensor_result_maps_are_bijections(plug):
     for ms in (32, 16):
         rows, cols = result_map(ms)
         assert len({(a, b) for a, b in zip(rows.ravel(), cols.ravel())}) == ms * ms
+
+
+# ---- meters: the counter step's parsing and attribution (no GPU) ------------------------------
+def _csv(path, dispatches):
+    import csv
+
+    cols = ["Correlation_Id", "Dispatch_Id", "Agent_Id", "Queue_Id", "Process_Id", "Thread_Id",
+            "Grid_Size", "Kernel_Id", "Kernel_Name", "Workgroup_Size", "LDS_Block_Size",
+            "Scratch_Size", "VGPR_Count", "Accum_VGPR_Count", "SGPR_Count", "Counter_Name",
+            "Counter_Value", "Start_Timestamp", "End_Timestamp"]
+    with open(path, "w", newline="") as f:
+        w = csv.DictWriter(f, cols)
+        w.writeheader()
+        for did, (name, cnt, t0, t1) in enumerate(dispatches, 1):
+            for c, v in cnt.items():
+                w.writerow({"Dispatch_Id": did, "Kernel_Name": name, "Grid_Size": 256,
+                            "Counter_Name": c, "Counter_Value": v, "Start_Timestamp": t0,
+                            "End_Timestamp": t1})
+
+
+def test_counter_step_attribution_and_figures(tmp_path):
+    from tempo.plugins.gfx950 import counters as C
+
+    copy = "__amd_rocclr_copyBuffer"
+    ours = "void tempo::gen::k_gemm_ilv<256, 256>(...)"
+    gib = 1 << 30
+    rows = [("at::native::fill", {"FETCH_SIZE": 5.0}, 0, 10)]
+    rows += [(copy, {"FETCH_SIZE": gib / 2048.0, "WRITE_SIZE": gib / 1024.0}, 0, 10)] * 3
+    rows += [("at::native::normal", {"FETCH_SIZE": 1.0}, 0, 10)]
+    for k in range(3):  # shape 1: three launches, the middle one the median
+        rows.append((ours, {"FETCH_SIZE": 1000.0 + k, "WRITE_SIZE": 500.0,
+                            "GRBM_GUI_ACTIVE": 8 * 2000.0,
+                            "SQ_VALU_MFMA_BUSY_CYCLES": 0.5 * 2000 * 1024}, 0, 1000))
+    rows.append(("at::native::normal", {"FETCH_SIZE": 1.0}, 0, 10))
+    rows += [(ours, {"FETCH_SIZE": 10.0, "WRITE_SIZE": 1.0}, 0, 10)] * 3
+    path = tmp_path / "c.csv"
+    _csv(path, rows)
+    disp = C.parse_dispatches(str(path))
+    assert len(disp) == len(rows) and [d["id"] for d in disp] == sorted(d["id"] for d in disp)
+    segs = [dict(label="calibration", count=3, copy_bytes=gib), dict(label="a", count=3),
+            dict(label="b", count=3)]
+    got = C.assign_segments(disp, segs, "tempo")
+    assert [len(got[k]) for k in ("calibration", "a", "b")] == [3, 3, 3]
+    sc = C.copy_scales(got["calibration"], gib)
+    assert abs(sc["FETCH_SIZE"] - 2.0) < 1e-12 and abs(sc["WRITE_SIZE"] - 1.0) < 1e-12
+    fig = C.derive(C.medians(got["a"]), sc, algorithmic_bytes=1001 * 2048 + 500 * 1024)
+    assert fig["fetch_bytes"] == 1001 * 1024 * 2.0 and fig["write_bytes"] == 500 * 1024
+    assert abs(fig["traffic_over_algorithmic"] - 1.0) < 1e-12
+    assert abs(fig["mfma_util"] - 0.5) < 1e-12
+    assert abs(fig["sclk_ghz"] - 2.0) < 1e-12   # 2000 cycles per XCD in 1000 ns
+    # a pass that ran fewer launches than it declared is an error, not a silent shift
+    import pytest as _pt
+
+    with _pt.raises(RuntimeError):
+        C.assign_segments(disp, segs + [dict(label="c", count=1)], "tempo")

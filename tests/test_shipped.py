@@ -152,12 +152,11 @@ def test_rows_fall_through_when_the_first_row_does_not_fit():
 
     assert capi.route(0, 8, 15360, 3840) == "l1r1n4d3"
     assert capi.route(0, 8, 12304, 3840) == "l1r1d4"      # N % 64 != 0: the unshared line row
-    assert capi.route(0, 8, 15360, 65792) == "h16r1u4n4"  # K > 65536: past the line rows
-    assert capi.route(0, 8, 12304, 65792) == "s16r1u4"    # ... and N % 64 != 0
+    assert capi.route(0, 8, 15360, 65792) == "s16r1u4"    # K > 65536: past the line rows
     assert capi.route(1, 16, 34816, 5120) == "l1r1n4d3"
     assert capi.route(2, 16, 5120, 17408) == "l1r1n2d4"
     assert capi.route(1, 32, 34816, 5120) == "l2r1n4d4"
-    assert capi.route(2, 32, 34816, 65536 + 256) == "h32r1u4n4"
+    assert capi.route(2, 32, 34816, 65536 + 256) == "h32r1u4n2"
     assert capi.route(0, 1, 15360, 3840) == "l0r1d3"
     assert capi.route(1, 1, 5120, 5120) == "l0r1d4"
     assert capi.route(1, 1, 5120, 65536 + 512) == "s1a_r1u8"
@@ -178,3 +177,34 @@ def test_gptq_repack_refuses_before_any_launch():
     assert L.tempo_gptq_repack_u8(p, p, p, 5120, 6144 + 4, 128, p, p, p, s) == capi.TEMPO_FALLBACK
     assert L.tempo_gptq_repack_u8(p, p, p, 0, 6144, 128, p, p, p, s) == capi.TEMPO_FALLBACK
     assert L.tempo_gptq_repack_u8(None, p, p, 5120, 6144, 128, p, p, p, s) != 0
+
+
+# ---- delivery-only build (reference kernels/shipped/gemm_fp16/sm_70/test_gate.py:230-285) ------
+@pytest.mark.parametrize("op", ["gemm_fp16", "gemm_w8a16"])
+def test_delivery_builds_from_its_own_directory(op, tmp_path):
+    """A host tree that vendors kernels/shipped/<op>/gfx950/ compiles it with -I pointing there and
+    nowhere else, and links a launcher: the ship probe links against the delivery's objects."""
+    import concurrent.futures as cf
+    import subprocess
+
+    from cuda_tempiler_amd import build as B
+
+    d = os.path.join(ROOT, "kernels", "shipped", op, "gfx950")
+    units = B.delivery_units(op)
+    assert units[-1] == "ship_probe.hip" and "launch.hip" in units
+
+    def cc(name):
+        src = os.path.join(d, name)
+        obj = str(tmp_path / name.replace(".hip", ".o"))
+        cmd = [B.HIPCC] + B.PROBE_FLAGS + B.unit_flags(src) + ["-I", d, "-c", src, "-o", obj]
+        r = subprocess.run(cmd, capture_output=True, text=True, cwd=str(tmp_path))
+        assert r.returncode == 0, r.stderr[-3000:]
+        return obj
+
+    with cf.ThreadPoolExecutor(len(units)) as ex:
+        objs = list(ex.map(cc, units))
+    exe = str(tmp_path / "probe")
+    r = subprocess.run([B.HIPCC, "--offload-arch=gfx950", "-o", exe] + objs,
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-3000:]
+    assert os.path.getsize(exe) > 0

@@ -114,3 +114,99 @@ def test_gate_up_fallback_is_silu_times_up(tops, monkeypatch):
     y8 = torch.ops.tempo.linear_gate_up_w8a16(x, q, s, None, 1, 128)
     g8, u8 = torch.nn.functional.linear(x, tops.dequantize(q, s, None, 1)).chunk(2, dim=-1)
     assert torch.equal(y8, torch.nn.functional.silu(g8) * u8)
+
+
+# ---- operand validation: malformed 8-bit operands never reach the kernels ---------------------
+def _w8(fmt, N=64, K=256, G=128):
+    A = torch.zeros(3, K, dtype=torch.float16)
+    if fmt == 1:
+        return A, torch.zeros(N, K, dtype=torch.int8), torch.ones(N, dtype=torch.float16), None
+    return (A, torch.zeros(N, K, dtype=torch.uint8), torch.ones(N, K // G, dtype=torch.float16),
+            torch.zeros(N, K // G, dtype=torch.uint8))
+
+
+@pytest.mark.parametrize("fmt", [1, 2])
+def test_w8_operands_well_formed(fmt):
+    from cuda_tempiler_amd import capi
+
+    assert capi.w8a16_operand_error(*_w8(fmt), fmt, 128) is None
+
+
+@pytest.mark.parametrize("case", [
+    "u8_with_fmt1", "i8_with_fmt2", "fp32_scale", "gptq_layout_scale", "short_scale",
+    "short_zero", "zero_wrong_dtype", "zero_with_fmt1", "no_zero_fmt2", "strided_scale",
+    "bad_fmt", "ragged_group", "k_mismatch"])
+def test_w8_operands_malformed_are_refused(case):
+    from cuda_tempiler_amd import capi
+
+    fmt = 2 if case in ("i8_with_fmt2", "gptq_layout_scale", "short_zero", "zero_wrong_dtype",
+                        "no_zero_fmt2", "ragged_group") else 1
+    A, wq, s, z = _w8(fmt)
+    N, K = wq.shape
+    group = 128
+    if case == "u8_with_fmt1":
+        wq = wq.to(torch.uint8)
+    elif case == "i8_with_fmt2":
+        wq = wq.to(torch.int8)
+    elif case == "fp32_scale":
+        s = s.float()
+    elif case == "gptq_layout_scale":          # [K/G, N] has the element count of [N, K/G]
+        s = torch.ones(K // 128, N, dtype=torch.float16)
+    elif case == "short_scale":
+        s = s[: N // 2]
+    elif case == "short_zero":
+        z = z[: N // 2]
+    elif case == "zero_wrong_dtype":
+        z = z.to(torch.int8)
+    elif case == "zero_with_fmt1":
+        z = torch.zeros(N, 2, dtype=torch.uint8)
+    elif case == "no_zero_fmt2":
+        z = None
+    elif case == "strided_scale":
+        s = torch.ones(N, 2, dtype=torch.float16)[:, 0]
+    elif case == "bad_fmt":
+        fmt = 3
+    elif case == "ragged_group":
+        group = 96
+    elif case == "k_mismatch":
+        A = torch.zeros(3, K + 8, dtype=torch.float16)
+    assert capi.w8a16_operand_error(A, wq, s, z, fmt, group) is not None
+    with pytest.raises(ValueError):
+        capi._require_w8(A, wq, s, z, fmt, group)
+
+
+def test_w8_gate_on_malformed_takes_own_path(tops, monkeypatch):
+    """With the gate on, a malformed operand set is the caller's path (counted 'fallback'), and
+    that path computes the same thing it computes with the gate off."""
+    monkeypatch.setenv("TEMPO_KERNELS", "1")
+    x = torch.randn(2, 256, dtype=torch.float16)
+    wq = torch.randint(-127, 128, (64, 256), dtype=torch.int8)
+    s = (torch.rand(64) / 127).float()   # fp32 scale: not the kernels' layout
+    y_on = torch.ops.tempo.linear_w8a16(x, wq, s, None, 1, 128)
+    monkeypatch.setenv("TEMPO_KERNELS", "0")
+    y_off = torch.ops.tempo.linear_w8a16(x, wq, s, None, 1, 128)
+    assert torch.equal(y_on, y_off)
+    assert tops.counters() == {"fallback": 1, "off": 1}
+
+
+@pytest.mark.parametrize("case", ["ok", "qweight_dtype", "qzeros_shape", "scales_layout",
+                                  "scales_dtype", "ragged_k"])
+def test_gptq_operand_checks(case):
+    from cuda_tempiler_amd import capi
+
+    K, N, G = 256, 64, 128
+    qw = torch.zeros(K // 4, N, dtype=torch.int32)
+    qz = torch.zeros(K // G, N // 4, dtype=torch.int32)
+    sc = torch.ones(K // G, N, dtype=torch.float16)
+    if case == "qweight_dtype":
+        qw = qw.to(torch.int64)
+    elif case == "qzeros_shape":
+        qz = torch.zeros(K // G, N, dtype=torch.int32)
+    elif case == "scales_layout":               # kernel layout [N, K/G] instead of [K/G, N]
+        sc = torch.ones(N, K // G, dtype=torch.float16)
+    elif case == "scales_dtype":
+        sc = sc.float()
+    elif case == "ragged_k":
+        qw = torch.zeros(K // 4 - 8, N, dtype=torch.int32)
+    why = capi.gptq_operand_error(qw, qz, sc, G)
+    assert (why is None) == (case == "ok"), why
