@@ -73,6 +73,8 @@ EXPORTS = {
     "tempo_gemm_w8a16_gate_up_launch": ([ct.POINTER(TempoW8A16Params), _p], _i),
     "tempo_naive_gemm_w8a16_launch": ([ct.POINTER(TempoW8A16Params), _p], _i),
     "tempo_gptq_repack_u8": ([_p, _p, _p, _i, _i, _i, _p, _p, _p, _p], _i),
+    "tempo_gemm_fp16_workspace_bytes": ([ct.POINTER(TempoGemmParams)], ct.c_size_t),
+    "tempo_gemm_w8a16_workspace_bytes": ([ct.POINTER(TempoW8A16Params)], ct.c_size_t),
 }
 
 
@@ -108,6 +110,18 @@ def _stream(stream):
     if isinstance(stream, int):
         return _p(stream)
     return _p(stream.cuda_stream)
+
+
+def workspace_bytes(op: int, M: int, N: int, K: int) -> int:
+    """Host-only: workspace bytes the shipped row for this shape needs (0 = none / not covered).
+    op 0 = gemm_fp16, 1 / 2 = gemm_w8a16 fmt 1 / 2 (dense strides)."""
+    fake = _p(0x1000)
+    if op == 0:
+        return int(lib().tempo_gemm_fp16_workspace_bytes(
+            TempoGemmParams(fake, fake, fake, M, N, K, K, K, N)))
+    return int(lib().tempo_gemm_w8a16_workspace_bytes(
+        TempoW8A16Params(fake, fake, fake, fake if op == 2 else None, fake, M, N, K, K, K, N,
+                         128 if op == 2 else 0, op)))
 
 
 def route(op: int, M: int, N: int, K: int) -> str:

@@ -97,6 +97,16 @@ int tempo_gemm_fp16_launch(const TempoGemmParams* p, tempo_stream_t stream) {
   return (int)tempo::gen::launch(to_pod(p), static_cast<hipStream_t>(stream));
 }
 
+size_t tempo_gemm_fp16_workspace_bytes(const TempoGemmParams* p) {
+  if (!p) return 0;
+  return tempo::gen::workspace_bytes(to_pod(p));
+}
+
+size_t tempo_gemm_w8a16_workspace_bytes(const TempoW8A16Params* p) {
+  if (!p) return 0;
+  return tempo::gen8::workspace_bytes(to_pod(p));
+}
+
 int tempo_gemm_w8a16_applicable(const TempoW8A16Params* p) {
   if (!p) return 0;
   return tempo::gen8::route(to_pod(p)) != nullptr;

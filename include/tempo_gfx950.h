@@ -7,7 +7,14 @@
  * Conventions (all entry points):
  *   - plain pointers and sizes; no framework types.  Device pointers are HIP device memory.
  *   - `stream` is a hipStream_t passed as void* (NULL = the null stream).  Every launch is
- *     asynchronous on that stream and never synchronises; the caller owns every buffer.
+ *     asynchronous on that stream; the caller owns every input and output buffer.
+ *   - split-K rows (narrow N, long K: fp32 partial sums of k ranges, reduced by a second kernel
+ *     on the same stream) need a workspace of tempo_gemm_*_workspace_bytes() bytes.  The launch
+ *     entry points take it from the library's pool: one device buffer per (device, stream),
+ *     allocated with hipMalloc the first time a shape needs it and grown (after a synchronise of
+ *     that stream) when a larger one does.  So the first split-K call on a stream allocates;
+ *     later calls of the same or smaller shapes do not.  Calls on different streams never
+ *     share a workspace.  Every other row uses no workspace and allocates nothing.
  *   - the int returned is a hipError_t value: 0 = success; TEMPO_FALLBACK (9, the value of
  *     hipErrorInvalidConfiguration) = "shape not covered, take your own path" -- a legal
  *     answer, not a failure (reference kernels/shipped/gemm_fp16/sm_70/dispatch.inc:12-13,26).
@@ -48,6 +55,10 @@ typedef struct TempoGemmParams {
 int tempo_gemm_fp16_applicable(const TempoGemmParams* p);
 /* Reference: launch.cu:20-22 tempo::gen::launch(const GemmParams&, cudaStream_t). */
 int tempo_gemm_fp16_launch(const TempoGemmParams* p, tempo_stream_t stream);
+/* Bytes of workspace the row tempo_gemm_fp16_launch runs for this shape needs (0: none, or not
+ * covered).  Host-only.  No reference counterpart: the reference's ladder has no split-K row
+ * (kernels/shipped/gemm_fp16/sm_70/dispatch.inc:15-26). */
+size_t tempo_gemm_fp16_workspace_bytes(const TempoGemmParams* p);
 
 /* ------------------------------------------------------------------------------------------
  * gemm_w8a16:  C = fp16_rn( A . deq(Wq)^T ), fp32 accumulation, weights dequantised in
@@ -77,6 +88,10 @@ typedef struct TempoW8A16Params {
 
 int tempo_gemm_w8a16_applicable(const TempoW8A16Params* p);
 int tempo_gemm_w8a16_launch(const TempoW8A16Params* p, tempo_stream_t stream);
+/* Bytes of workspace the row tempo_gemm_w8a16_launch runs for this shape needs (0: none, or not
+ * covered).  Host-only; no reference counterpart (as for tempo_gemm_fp16_workspace_bytes). */
+size_t tempo_gemm_w8a16_workspace_bytes(const TempoW8A16Params* p);
+
 
 /* ------------------------------------------------------------------------------------------
  * Fused gate/up epilogue (the MLP's first projection):

@@ -47,9 +47,9 @@ def instantiation(kind, p, epi=0):
     if epi:
         raise ValueError("the fused gate/up epilogue exists for the stream kernels only")
     if kind == "ilv":
-        return "launch_ilv<%d,%d,%d,%d,%d,%d,%d,%d,%d>" % (
+        return "launch_ilv<%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d>" % (
             p["BM"], p["BN"], p["BK"], p["WM"], p["WN"], p["STAGES"], p["GROUP"], p["XCD"],
-            p["RSP"])
+            p["RSP"], p.get("SW", 0), p.get("MINKT", 0))
     if kind == "dma":
         return "launch_dma<%d,%d,%d,%d,%d,%d,%d,%d,%d,%d>" % (
             p["BM"], p["BN"], p["BK"], p["WM"], p["WN"], p["STAGES"], p["SWZ"], p["GROUP"],
@@ -75,6 +75,8 @@ def condition(sel, kind, p, m_max, n_min=0, gate_up=False):
     elif kind == "ilv":  # an even number of 32-k substeps; 31-bit panel byte offsets
         fit = "(p.N %% %d) == 0 && (p.K %% %d) == 0 && p.lda <= %d && p.ldb <= %d" % (
             p["BN"], max(64, p["BK"]), sel.ilv_ld_max(p), sel.ilv_ld_max(p))
+        if "NMAX" in p:
+            fit += " && p.N < %d" % p["NMAX"]
     else:
         fit = "(p.N %% %d) == 0 && (p.K %% %d) == 0" % (p["BN"], p["BK"])
         if "NMAX" in p:
@@ -123,7 +125,8 @@ def render_prefill() -> str:
         if inst in seen:
             continue
         seen.add(inst)
-        out.append("template hipError_t %s(const GemmParams&, hipStream_t);" % inst)
+        out.append("template hipError_t %s(const GemmParams&, hipStream_t, const Workspace&);"
+                   % inst)
     return "\n".join(out) + "\n"
 
 

@@ -5,8 +5,13 @@
 // given stream, never synchronises, and the caller owns every buffer.  A shape the ladder
 // does not cover returns hipErrorInvalidConfiguration: "take your own path" (dispatch.inc).
 //
-// The launcher keeps no state and allocates nothing: concurrent calls on different streams are
-// independent.
+// Split-K rows (narrow N, long K) add fp32 partial sums of the k ranges in a workspace and reduce
+// them with a second kernel on the same stream.  launch() takes that workspace from the
+// delivery's pool -- one buffer per (device, stream), allocated on first use and grown when a
+// larger shape needs it (hipMalloc; the old buffer is freed after a stream synchronise) -- so
+// calls on different streams stay independent, and calls on one stream are ordered by it.
+// launch_with() takes the caller's workspace instead and never allocates; no other row touches a
+// workspace.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -206,8 +211,24 @@ inline hipError_t launch_dma(const GemmParams& p, hipStream_t s) {
 // The interleaved prefill kernel (k_gemm_ilv) lives in its own translation unit,
 // launch_prefill.hip, compiled with the register-pressure-minimising scheduler; its launchers
 // are instantiated there for the rows of the ladder (prefill.inc, generated from select.py).
-template <int BM, int BN, int BK, int WM, int WN, int STAGES, int GROUP, int XCD, int RSP>
-hipError_t launch_ilv(const GemmParams& p, hipStream_t s);
+// SW > 0: split-K towards SW workgroups, at least MINKT k-tiles per split (split_count).
+template <int BM, int BN, int BK, int WM, int WN, int STAGES, int GROUP, int XCD, int RSP,
+          int SW, int MINKT>
+hipError_t launch_ilv(const GemmParams& p, hipStream_t s, const Workspace& w);
+
+// One dispatch row: launchers without a workspace ignore it (and, asked for their need, report 0).
+inline hipError_t call_row(hipError_t (*f)(const GemmParams&, hipStream_t), const GemmParams& p,
+                           hipStream_t s, const Workspace& w) {
+  if (w.need) {
+    *w.need = 0;
+    return hipSuccess;
+  }
+  return f(p, s);
+}
+inline hipError_t call_row(hipError_t (*f)(const GemmParams&, hipStream_t, const Workspace&),
+                           const GemmParams& p, hipStream_t s, const Workspace& w) {
+  return f(p, s, w);
+}
 
 // Applicability predicate.  false = the shape is not covered and the caller must take its own
 // path.  Dense row-major operands with 16-byte aligned rows; the band's divisibility is
@@ -224,8 +245,13 @@ inline bool applicable(const GemmParams& p) {
 }
 
 // Shape dispatcher; body is the generated ladder (dispatch.inc), defined in launch.hip, the
-// one translation unit of the delivery.
+// one translation unit of the delivery.  launch(): split-K rows use the delivery's pool.
 hipError_t launch(const GemmParams& p, hipStream_t s);
+// The same ladder with the caller's workspace: never allocates; a split-K row whose workspace
+// does not fit returns hipErrorOutOfMemory (launching nothing).
+hipError_t launch_with(const GemmParams& p, hipStream_t s, const Workspace& w);
+// Bytes of workspace the row launch() would run needs for this shape (0: none, or not covered).
+size_t workspace_bytes(const GemmParams& p);
 
 // Host-only: tag of the ladder row launch() would run, nullptr when not covered.
 const char* route(const GemmParams& p);

@@ -1,0 +1,40 @@
+// launch_prefill.h -- the launchers of the interleaved prefill kernel (k_gemm_ilv): template
+// definitions, instantiated by launch_prefill.hip for the ladder's rows (prefill.inc) -- or by
+// any other translation unit built with the same scheduler flag (the plugin's tuning
+// harness instantiates its candidates from this header).
+#pragma once
+#include "launch.h"
+
+namespace tempo {
+namespace gen {
+
+template <int BM, int BN, int BK, int WM, int WN, int STAGES, int GROUP, int XCD, int RSP,
+          int SW, int MINKT>
+hipError_t launch_ilv(const GemmParams& p, hipStream_t s, const Workspace& w) {
+  const int nm = (p.M + BM - 1) / BM;
+  const int nn = p.N / BN;
+  const int splits = split_count(nm * nn, p.K / BK, SW, MINKT);
+  const size_t bytes = splits > 1 ? (size_t)splits * p.M * p.N * sizeof(float) : 0;
+  if (w.need) {
+    *w.need = bytes;
+    return hipSuccess;
+  }
+  const dim3 blk(WM * WN * 64);
+  if (splits == 1) {
+    hipLaunchKernelGGL((k_gemm_ilv<BM, BN, BK, WM, WN, STAGES, GROUP, XCD, RSP, 0>),
+                       dim3(nm * nn), blk, 0, s, p.A, p.B, p.C, p.M, p.N, p.K, p.lda, p.ldb,
+                       p.ldc, static_cast<float*>(nullptr), 1);
+    return hipGetLastError();
+  }
+  float* ws = workspace_for(w, bytes, s);
+  if (!ws) return hipErrorOutOfMemory;
+  hipLaunchKernelGGL((k_gemm_ilv<BM, BN, BK, WM, WN, STAGES, GROUP, XCD, RSP, 1>),
+                     dim3(nm * nn * splits), blk, 0, s, p.A, p.B, p.C, p.M, p.N, p.K, p.lda, p.ldb,
+                     p.ldc, ws, splits);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  return launch_reduce(ws, splits, p.M, p.N, p.C, p.ldc, s);
+}
+
+}  // namespace gen
+}  // namespace tempo

@@ -11,20 +11,10 @@
 //                    -mllvm -amdgpu-sched-strategy=iterative-minreg -c launch_prefill.hip
 // The flags line below is read by the library build (cuda_tempiler_amd/build.py):
 // tempo:flags -mllvm -amdgpu-sched-strategy=iterative-minreg
-#include "launch.h"
+#include "launch_prefill.h"
 
 namespace tempo {
 namespace gen {
-
-template <int BM, int BN, int BK, int WM, int WN, int STAGES, int GROUP, int XCD, int RSP>
-hipError_t launch_ilv(const GemmParams& p, hipStream_t s) {
-  const int nm = (p.M + BM - 1) / BM;
-  const int nn = p.N / BN;
-  const dim3 grid(nm * nn), blk(WM * WN * 64);
-  hipLaunchKernelGGL((k_gemm_ilv<BM, BN, BK, WM, WN, STAGES, GROUP, XCD, RSP>), grid, blk, 0, s,
-                     p.A, p.B, p.C, p.M, p.N, p.K, p.lda, p.ldb, p.ldc);
-  return hipGetLastError();
-}
 
 #include "prefill.inc"
 

@@ -12,9 +12,11 @@ through to the next one, so a narrower row can sit in front of a general one.)
               line = whole 128-byte weight lines by nontemporal LDS-DMA into per-wave rings
               (needs K % 128 and K <= 65536); stream (register-pipelined) takes the rest.  A = 1
               stages the activations in LDS once per workgroup (M = 1).
-  * 32 < M <= 64  line rows with more activation blocks.
-  * 64 < M <= 256  dma: k_gemm_dma tiles (64x64 to 128x128, 4-stage LDS-DMA ring), tile chosen
-              by M and N; a line row takes the shapes whose N is not a multiple of 64.
+  * 32 < M <= 64  line rows with more activation blocks; narrow N (< 6144) takes the interleaved
+              kernel with split-K (64 x 192 tiles).
+  * 64 < M <= 256  narrow N (< 6144 for M <= 128): the interleaved kernel with split-K (128 x 128
+              or 128 x 256 tiles); otherwise dma: k_gemm_dma tiles (64x64 to 128x128, 4-stage
+              LDS-DMA ring), tile chosen by M and N; a line row takes N % 64 != 0.
   * M > 256   ilv: the interleaved 4-wave kernel (128 x 128 wave tiles, LDS-DMA copies,
               hand-pipelined substeps).
 """
@@ -32,12 +34,21 @@ LADDER = [
     (32, 0, "l2r1d4", "line", dict(MB=2, R=1, D=4, W=2048)),
     (32, 0, "s32r1u4", "stream", dict(MB=2, R=1, U=4, A=0)),
     (64, 12288, "l4r1n4d3", "line", dict(MB=4, R=1, D=3, SN=4, W=2048)),
+    # narrow N, long K: split-K over the interleaved kernel's tiles (fp32 partials in the
+    # workspace, reduced in order) gives the 20 column tiles of N = 3840 enough workgroups;
+    # measured by the variant driver (tempo/plugins/gfx950/tune.py) at (64|128|256, 3840, 15360)
+    (64, 0, "i64x192k64s3w256", "ilv",
+     dict(BM=64, BN=192, BK=64, WM=1, WN=4, STAGES=3, GROUP=8, XCD=1, RSP=8, SW=256, MINKT=8,
+          NMAX=6144)),
     (64, 0, "l4r1d3", "line", dict(MB=4, R=1, D=3, W=2048)),
     # 64 < M <= 256: LDS-DMA tiles with a 4-stage ring.  Per CU they keep more operand bytes in
     # flight than the line kernel (which re-reads the activations per slab wave) or the
     # register-staged tiles.  Narrow N gives few workgroups (N = 3840: 60 column tiles)
     (128, 12288, "d128x64k64s4", "dma",
      dict(BM=128, BN=64, BK=64, WM=2, WN=2, STAGES=4, SWZ=1, GROUP=8, XCD=1, MS=16)),
+    (128, 0, "i128x128k64s3w256", "ilv",
+     dict(BM=128, BN=128, BK=64, WM=2, WN=2, STAGES=3, GROUP=8, XCD=1, RSP=8, SW=256, MINKT=8,
+          NMAX=6144)),
     (128, 0, "d64x64k64s4", "dma",
      dict(BM=64, BN=64, BK=64, WM=2, WN=2, STAGES=4, SWZ=1, GROUP=8, XCD=1, MS=16)),
     (128, 0, "l8r1n2d3", "line", dict(MB=8, R=1, D=3, SN=2, W=2048)),
@@ -45,6 +56,8 @@ LADDER = [
      dict(BM=128, BN=128, BK=64, WM=2, WN=2, STAGES=4, SWZ=1, GROUP=8, XCD=1, MS=16)),
     (256, 6144, "d128x64k64s4", "dma",
      dict(BM=128, BN=64, BK=64, WM=2, WN=2, STAGES=4, SWZ=1, GROUP=8, XCD=1, MS=16)),
+    (256, 0, "i128x256k64s3w256", "ilv",
+     dict(BM=128, BN=256, BK=64, WM=1, WN=4, STAGES=3, GROUP=8, XCD=1, RSP=8, SW=256, MINKT=8)),
     (256, 0, "d64x64k64s4", "dma",
      dict(BM=64, BN=64, BK=64, WM=2, WN=2, STAGES=4, SWZ=1, GROUP=8, XCD=1, MS=16)),
     (1 << 30, 0, "i256x256k64w4r8", "ilv",
@@ -97,8 +110,9 @@ def _fits(kind, p, M, N, K):
     if kind == "line":  # NMAX (optional): the row holds narrower N only
         return (N % (STREAM_N_ROWS * p["R"] * p.get("SN", 1)) == 0 and K % LINE_K_STEP == 0
                 and K <= LINE_K_MAX and N < p.get("NMAX", 1 << 30))
-    if kind == "ilv":
-        return N % p["BN"] == 0 and K % max(64, p["BK"]) == 0 and K <= ilv_ld_max(p)
+    if kind == "ilv":  # NMAX (optional): the row holds narrower N only
+        return (N % p["BN"] == 0 and K % max(64, p["BK"]) == 0 and K <= ilv_ld_max(p)
+                and N < p.get("NMAX", 1 << 30))
     if kind == "stream":
         return N % (STREAM_N_ROWS * p["R"]) == 0 and K % (STREAM_K_STEP * p["U"]) == 0
     if kind == "shared":

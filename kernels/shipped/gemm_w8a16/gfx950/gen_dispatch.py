@@ -47,9 +47,9 @@ def instantiation(kind, p, epi=0):
     if epi:
         raise ValueError("the fused gate/up epilogue exists for the stream kernels only")
     if kind == "ilv8":
-        return "launch_ilv8<%d,%d,%d,%d,%d,%d,%d,%d,%d>" % (
+        return "launch_ilv8<%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d>" % (
             p["BM"], p["BN"], p["BK"], p["WM"], p["WN"], p["STAGES"], p["GROUP"], p["XCD"],
-            p["RSP"])
+            p["RSP"], p.get("SW", 0), p.get("MINKT", 0))
     return "launch_mfma<%d,%d,%d,%d,%d,%d,%d,%d,%d>" % (
         p["BM"], p["BN"], p["BK"], p["WM"], p["WN"], p["MS"], p["SWZ"], p["GROUP"], p["XCD"])
 
@@ -71,6 +71,10 @@ def condition(sel, kind, p, m_max, n_min=0, gate_up=False):
     elif kind == "ilv8":  # a scale group is two k-tiles; 31-bit panel byte offsets
         fit = "(p.N %% %d) == 0 && (p.K %% 128) == 0 && p.lda <= %d && p.ldw <= %d" % (
             p["BN"], sel.ilv_ld_max(p), sel.ilv_ld_max(p))
+        if "NMAX" in p:
+            fit += " && p.N < %d" % p["NMAX"]
+        if "KMIN" in p:
+            fit += " && p.K >= %d" % p["KMIN"]
     else:
         fit = "(p.N %% %d) == 0 && (p.K %% %d) == 0" % (p["BN"], p["BK"])
         if "NMAX" in p:
@@ -121,7 +125,8 @@ def render_prefill() -> str:
         if inst in seen:
             continue
         seen.add(inst)
-        out.append("template hipError_t %s(const W8A16Params&, hipStream_t);" % inst)
+        out.append("template hipError_t %s(const W8A16Params&, hipStream_t, const Workspace&);"
+                   % inst)
     return "\n".join(out) + "\n"
 
 

@@ -7,8 +7,9 @@
 //   fmt 2: Wq uint8 [N][ldw], scale fp16 [N][K/group], zero uint8 [N][K/group]
 //          W = fp16_rn((q - z) * s)
 // Asynchronous on the given stream, never synchronises, caller owns every buffer.  Not covered
-// -> hipErrorInvalidConfiguration (take your own path).  The launcher keeps no state and
-// allocates nothing.
+// -> hipErrorInvalidConfiguration (take your own path).  Split-K rows (narrow N, long K) add fp32
+// partial sums in a workspace: launch() takes it from the delivery's per-(device, stream) pool
+// (allocated on first use, grown on demand), launch_with() from the caller and never allocates.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -190,8 +191,24 @@ inline hipError_t launch_line(const W8A16Params& p, hipStream_t s) {
 // The interleaved int8 prefill kernel (k_gemm_ilv8) lives in its own translation unit,
 // launch_prefill.hip, compiled with the register-pressure-minimising scheduler; its launchers
 // are instantiated there for the rows of the ladder (prefill.inc, generated from select.py).
-template <int BM, int BN, int BK, int WM, int WN, int STAGES, int GROUP, int XCD, int RSP>
-hipError_t launch_ilv8(const W8A16Params& p, hipStream_t s);
+// SW > 0: split-K towards SW workgroups, at least MINKT k-tiles per split (split_count).
+template <int BM, int BN, int BK, int WM, int WN, int STAGES, int GROUP, int XCD, int RSP,
+          int SW, int MINKT>
+hipError_t launch_ilv8(const W8A16Params& p, hipStream_t s, const Workspace& w);
+
+// One dispatch row: launchers without a workspace ignore it (and, asked for their need, report 0).
+inline hipError_t call_row(hipError_t (*f)(const W8A16Params&, hipStream_t), const W8A16Params& p,
+                           hipStream_t s, const Workspace& w) {
+  if (w.need) {
+    *w.need = 0;
+    return hipSuccess;
+  }
+  return f(p, s);
+}
+inline hipError_t call_row(hipError_t (*f)(const W8A16Params&, hipStream_t, const Workspace&),
+                           const W8A16Params& p, hipStream_t s, const Workspace& w) {
+  return f(p, s, w);
+}
 
 template <int BM, int BN, int BK, int WM, int WN, int MS, int SWZ, int GROUP, int XCD>
 inline hipError_t launch_mfma(const W8A16Params& p, hipStream_t s) {
@@ -224,6 +241,11 @@ inline bool applicable(const W8A16Params& p) {
 
 hipError_t launch(const W8A16Params& p, hipStream_t s);
 const char* route(const W8A16Params& p);
+// The same ladder with the caller's workspace: never allocates; a split-K row whose workspace
+// does not fit returns hipErrorOutOfMemory (launching nothing).
+hipError_t launch_with(const W8A16Params& p, hipStream_t s, const Workspace& w);
+// Bytes of workspace the row launch() would run needs for this shape (0: none, or not covered).
+size_t workspace_bytes(const W8A16Params& p);
 
 // Fused gate/up: C[M][N] = silu(A . deq(W)[0..N)^T) * (A . deq(W)[N..2N)^T), Wq / scale / zero
 // with 2N rows (gate, then up).  Its own ladder (dispatch_gate_up.inc); not covered ->

@@ -9,14 +9,27 @@
 namespace tempo {
 namespace gen8 {
 
-hipError_t launch(const W8A16Params& p, hipStream_t s) {
+hipError_t launch_with(const W8A16Params& p, hipStream_t s, const Workspace& w) {
   if (!applicable(p)) return hipErrorInvalidConfiguration;
 #define TEMPO_ROW(band, fit, fn, tag) \
-  if ((band) && (fit)) return fn(p, s);
+  if ((band) && (fit)) return call_row(fn, p, s, w);
 #define TEMPO_FALLBACK_ROW return hipErrorInvalidConfiguration;
 #include "dispatch.inc"
 #undef TEMPO_ROW
 #undef TEMPO_FALLBACK_ROW
+}
+
+hipError_t launch(const W8A16Params& p, hipStream_t s) {
+  Workspace w;
+  w.pool = true;
+  return launch_with(p, s, w);
+}
+
+size_t workspace_bytes(const W8A16Params& p) {
+  size_t need = 0;
+  Workspace w;
+  w.need = &need;
+  return launch_with(p, nullptr, w) == hipSuccess ? need : 0;
 }
 
 const char* route(const W8A16Params& p) {
@@ -31,8 +44,9 @@ const char* route(const W8A16Params& p) {
 
 hipError_t launch_gate_up(const W8A16Params& p, hipStream_t s) {
   if (!applicable(p)) return hipErrorInvalidConfiguration;
+  const Workspace w{};
 #define TEMPO_ROW(band, fit, fn, tag) \
-  if ((band) && (fit)) return fn(p, s);
+  if ((band) && (fit)) return call_row(fn, p, s, w);
 #define TEMPO_FALLBACK_ROW return hipErrorInvalidConfiguration;
 #include "dispatch_gate_up.inc"
 #undef TEMPO_ROW

@@ -28,12 +28,25 @@ LADDER = [
     (16, 0, "s16r1u4", "stream", dict(MB=1, R=1, U=4, A=0)),
     (32, 0, "h32r1u4n2", "shared", dict(MB=2, R=1, U=4, SN=2, TPB=512)),
     (64, 12288, "l4r1n4d3", "line", dict(MB=4, R=1, D=3, SN=4, W=2048)),
+    # 32 < M <= 64, narrow N and long K: the int8 interleaved kernel on 128 x 256 tiles with
+    # split-K (measured 1.3x the line row at (64, 5120, 17408), 0.9x at K = 5120)
+    (64, 0, "i8x128x256s3w256", "ilv8",
+     dict(BM=128, BN=256, BK=64, WM=1, WN=4, STAGES=3, GROUP=8, XCD=1, RSP=8, SW=256, MINKT=8,
+          NMAX=12288, KMIN=12288)),
     (64, 0, "l4r1n2d3", "line", dict(MB=4, R=1, D=3, SN=2, W=2048)),
+    # 64 < M <= 128: 128 x 256 tiles (one tile row), split-K where the column tiles are too few
+    # to fill the part (the variant driver's rows: 1.5-2.9x the line and register-staged rows)
+    (128, 0, "i8x128x256s3w256", "ilv8",
+     dict(BM=128, BN=256, BK=64, WM=1, WN=4, STAGES=3, GROUP=8, XCD=1, RSP=8, SW=256, MINKT=8)),
     (128, 0, "l8r1n2d3", "line", dict(MB=8, R=1, D=3, SN=2, W=2048, NMAX=12288)),
     (256, 0, "m128x128k64", "mfma",
      dict(BM=128, BN=128, BK=64, WM=2, WN=2, MS=32, SWZ=1, GROUP=8, XCD=1)),
-    # narrow N (fewer than 8 tiles of 256 columns): 256x256 tiles leave most CUs idle, so
-    # 128x128 tiles of the register-staged kernel (4x the workgroups) are faster there
+    # narrow N (fewer than 8 tiles of 256 columns): 256x256 tiles leave most CUs idle; 128 x 256
+    # tiles with split-K fill the part (1.97x the 128 x 128 register-staged row at
+    # (2048, 1024, 5120)), which stays behind them for N % 256 != 0
+    (1 << 30, 0, "i8x128x256s3w256", "ilv8",
+     dict(BM=128, BN=256, BK=64, WM=1, WN=4, STAGES=3, GROUP=8, XCD=1, RSP=8, SW=256, MINKT=8,
+          NMAX=2048)),
     (1 << 30, 0, "m128x128k64s16", "mfma",
      dict(BM=128, BN=128, BK=64, WM=2, WN=2, MS=16, SWZ=1, GROUP=8, XCD=1, NMAX=2048)),
     (1 << 30, 0, "i8x256k64s3", "ilv8",
@@ -87,8 +100,9 @@ def ilv_ld_max(p):
 
 
 def _fits(kind, p, M, N, K):
-    if kind == "ilv8":  # a scale group of 128 k is two k-tiles
-        return N % p["BN"] == 0 and K % 128 == 0 and K <= ilv_ld_max(p)
+    if kind == "ilv8":  # a scale group of 128 k is two k-tiles; NMAX / KMIN (optional) bounds
+        return (N % p["BN"] == 0 and K % 128 == 0 and K <= ilv_ld_max(p)
+                and N < p.get("NMAX", 1 << 30) and K >= p.get("KMIN", 0))
     if kind == "line":  # NMAX (optional): the row holds narrower N only
         return (N % (STREAM_N_ROWS * p["R"] * p.get("SN", 1)) == 0 and K % LINE_K_STEP == 0
                 and K <= LINE_K_MAX and N < p.get("NMAX", 1 << 30))

@@ -32,12 +32,13 @@ CAPABILITIES = frozenset({
 
 # kernel symbol, template-parameter order, and argument list, per kind: the emitter's only data
 _ENTRY = {
-    "ilv": ("k_gemm_ilv", ("BM", "BN", "BK", "WM", "WN", "STAGES", "GROUP", "XCD", "RSP"),
-            "const _Float16*, const _Float16*, _Float16*, int, int, int, int, int, int",
+    "ilv": ("k_gemm_ilv", ("BM", "BN", "BK", "WM", "WN", "STAGES", "GROUP", "XCD", "RSP", "SPLIT"),
+            "const _Float16*, const _Float16*, _Float16*, int, int, int, int, int, int, float*, int",
             ("common/cdna4.h", "gemm_mfma/kernel.hip", "gemm_mfma/ilv.hip")),
-    "ilv8": ("k_gemm_ilv8", ("BM", "BN", "BK", "WM", "WN", "STAGES", "GROUP", "XCD", "RSP", "BFMT"),
+    "ilv8": ("k_gemm_ilv8", ("BM", "BN", "BK", "WM", "WN", "STAGES", "GROUP", "XCD", "RSP", "BFMT",
+                             "SPLIT"),
              "const _Float16*, const uint8_t*, const _Float16*, const uint8_t*, _Float16*, int, int, "
-             "int, int, int, int",
+             "int, int, int, int, float*, int",
              ("common/cdna4.h", "gemm_mfma/kernel.hip", "gemm_mfma/ilv8.hip")),
     "dma": ("k_gemm_dma", ("BM", "BN", "BK", "WM", "WN", "STAGES", "SWZ", "GROUP", "XCD", "XT",
                            "MINB", "MS"),
@@ -65,9 +66,9 @@ KIND_FLAGS = {"ilv": ("-mllvm", "-amdgpu-sched-strategy=iterative-minreg"),
               "ilv8": ("-mllvm", "-amdgpu-sched-strategy=iterative-minreg")}
 # trailing template parameters with a default in the skeleton: named only when the hyperform
 # sets them (EPI = 1 is the fused gate/up epilogue of the decode kernels)
-_OPTIONAL = frozenset({"EPI", "SN", "TPB"})
+_OPTIONAL = frozenset({"EPI", "SN", "TPB", "SPLIT"})
 # default of an optional parameter left out in front of one that is named
-_DEFAULT = {"EPI": 0, "SN": 1, "TPB": 1024}
+_DEFAULT = {"EPI": 0, "SN": 1, "TPB": 1024, "SPLIT": 0}
 
 
 def _order(kind: str, p: dict) -> tuple:
@@ -143,8 +144,10 @@ class Gfx950Skeletons:
                 L = p["BM"] // (1024 // (p["BK"] * 2) * nw) + p["BN"] // (16 * nw)
             regs = acc + frags + 2 * L + 16  # + copy offsets, fragment offsets
             # pessimistic edge: the epilogue converts every accumulator (acc held twice when the
-            # budget allows it)
-            return regs, max(int(regs * 1.2), 2 * acc + 16), space.lds_bytes(kind, p)
+            # budget allows it); the split-K epilogue stores fp32 partials straight from the
+            # accumulators, at worst with an address pair live per accumulator block
+            pess = max(int(regs * 1.2), 2 * acc + 16) + (2 * tm * tn if p.get("SPLIT") else 0)
+            return regs, pess, space.lds_bytes(kind, p)
         if kind in ("dma", "reg"):
             ms = p.get("MS", 32)
             nacc = 16 if ms == 32 else 4
@@ -204,7 +207,8 @@ class Gfx950Skeletons:
         kind = p["kind"]
         minb, bound = 1, 0
         if kind in ("dma", "reg", "ilv", "ilv8"):
-            grid = -(-M // p["BM"]) * (N // p["BN"])
+            grid = (-(-M // p["BM"]) * (N // p["BN"])
+                    * space.splits_of(kind, p, M, N, int(op.shapes["K"])))
             threads = p["WM"] * p["WN"] * 64
             minb = p.get("MINB", 1) if kind == "dma" else 1
         elif kind == "shared":
@@ -245,7 +249,8 @@ class Gfx950Skeletons:
             tm, tn = p["BM"] // p["WM"] // ms, p["BN"] // p["WN"] // ms
             ks = p["BK"] // (16 if ms == 32 else 32)
             nw = p["WM"] * p["WN"]
-            reps = (K // p["BK"]) * rounds
+            sp = space.splits_of(kind, p, M, N, K)
+            reps = -(-(K // p["BK"]) // sp) * rounds  # k-tiles of one split
             flops = tm * tn * ks * space.MFMA_FLOPS[ms]
             lds_rd = (tm + tn) * ks * 1024 if kind != "ilv8" else (tm * 1024 + tn * 512) * ks
             vmem = (p["BM"] + p["BN"]) * p["BK"] * 2 // nw

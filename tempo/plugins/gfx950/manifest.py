@@ -29,7 +29,7 @@ SHIPPED = os.path.join(ROOT, "kernels", "shipped")
 SIGNED = ("kernel.hip", "launch.h", "launch.hip", "dispatch.inc", "dispatch_gate_up.inc",
           "select.py")
 # files only some deliveries have (gemm_fp16's prefill translation unit); signed when present
-SIGNED_OPTIONAL = ("launch_prefill.hip", "prefill.inc")
+SIGNED_OPTIONAL = ("launch_prefill.hip", "launch_prefill.h", "prefill.inc", "ship_probe.hip")
 
 OPS = {
     "gemm_fp16": dict(dtype="fp16 x fp16 -> fp16, fp32 accumulate",
@@ -74,7 +74,7 @@ def hyper_params(kind, p, fmt, epi=0):
     same kernel, named the way space.variants() names it."""
     pk = {"stream": "stream", "mfma": "reg", "dma": "dma", "shared": "shared", "ilv": "ilv",
           "ilv8": "ilv8", "line": "line"}[kind]
-    params = {k: v for k, v in p.items() if k not in ("fmts", "NMAX")}
+    params = {k: v for k, v in p.items() if k not in ("fmts", "NMAX", "KMIN")}
     params["kind"] = pk
     if pk == "shared":
         params.setdefault("TPB", 1024)
@@ -89,6 +89,8 @@ def hyper_params(kind, p, fmt, epi=0):
         params.setdefault("XT", 0)
         params.setdefault("MINB", 1)
         params.setdefault("MS", 32)
+    if pk in ("ilv", "ilv8") and params.get("SW", 0):
+        params["SPLIT"] = 1  # the split-K instantiation of the kernel
     if epi:
         params["EPI"] = 1
     return params
@@ -284,6 +286,14 @@ def make(op, rows_files=(), counter_files=()):
             fit = "N %% %d == 0 and K %% %d == 0" % (p["BN"], p["BK"])
             if "NMAX" in p:
                 fit += " and N < %d" % p["NMAX"]
+        if kind in ("ilv", "ilv8"):
+            if "NMAX" in p:
+                fit += " and N < %d" % p["NMAX"]
+            if "KMIN" in p:
+                fit += " and K >= %d" % p["KMIN"]
+            if p.get("SW"):
+                fit += "; split-K: at most %d workgroups, >= %d k-tiles per split" % (
+                    p["SW"], p.get("MINKT", 0))
         man["dispatch" if not epi else "dispatch_gate_up"].append(dict(
                                     M_max=m_max, N_min=n_min, tag=tag, kind=kind,
                                     params={k: v for k, v in p.items() if k != "fmts"},

@@ -43,15 +43,22 @@
 // 2^31 (BM*lda*2, BN*ldb*2).  M is predicated: A rows past M-1 are re-read from row M-1 and
 // never stored.
 //
+// SPLIT = 1 (split-K): the grid is tiles x ksplit workgroups (split_tile_of); workgroup split sk
+// takes the k-tiles [sk*kper, min((sk+1)*kper, K/BK)), kper = ceil((K/BK) / ksplit) -- the host
+// picks ksplit so that no split is empty -- and writes its fp32 partial tile straight from the
+// accumulators to ws[sk][M][N] (16 bytes per lane and block); k_splitk_reduce then adds the
+// splits in order and rounds once.  Narrow-N, long-K shapes get enough workgroups this way.
+//
 // Build: this kernel is compiled with -mllvm -amdgpu-sched-strategy=iterative-minreg (its own
 // translation unit).  The default pre-RA scheduler reorders the 256 accumulator chains of a
 // 128 x 128 wave tile such that the register allocator no longer keeps each accumulator in one
 // AGPR tuple, and the loop fills with v_accvgpr_read/write/mov copies.
 // ============================================================================================
-template <int BM, int BN, int BK, int WM, int WN, int STAGES, int GROUP, int XCD, int RSP>
+template <int BM, int BN, int BK, int WM, int WN, int STAGES, int GROUP, int XCD, int RSP,
+          int SPLIT = 0>
 __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv(
     const _Float16* __restrict__ A, const _Float16* __restrict__ B, _Float16* __restrict__ C,
-    int M, int N, int K, int lda, int ldb, int ldc) {
+    int M, int N, int K, int lda, int ldb, int ldc, float* __restrict__ ws, int ksplit) {
   using MF = Mfma<16>;
   constexpr int SWZ = 2;
   constexpr int NW = WM * WN;
@@ -82,9 +89,17 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv(
   const int wm = wave / WN, wn = wave % WN;
 
   const int nm = (M + BM - 1) / BM, nn = N / BN;
-  int tmi, tni;
-  tile_of<GROUP, XCD>(blockIdx.x, nm, nn, tmi, tni);
+  int tmi, tni, sk = 0;
+  if constexpr (SPLIT)
+    split_tile_of<GROUP, XCD>(blockIdx.x, nm, nn, ksplit, tmi, tni, sk);
+  else
+    tile_of<GROUP, XCD>(blockIdx.x, nm, nn, tmi, tni);
   const int m0 = tmi * BM, n0 = tni * BN;
+  // k-tiles of this workgroup: [kbase, kbase + NT)
+  const int NTALL = K / BK;
+  const int kper = SPLIT ? (NTALL + ksplit - 1) / ksplit : NTALL;
+  const int kbase = sk * kper;
+  const int NT = min(kper, NTALL - kbase);
 
   // Copy d of this wave fills 1 KiB block (ib*NW + wave) of the A (d < A_BLK) or B tile; lane l
   // fetches the 16-byte chunk that belongs at LDS slot l (the swizzle is an involution).  The
@@ -105,7 +120,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv(
     const bool isA = d < A_BLK;
     const int ib = isA ? d : d - A_BLK;
     _Float16* dst = smem + (kt % STAGES) * STAGE + (isA ? 0 : BM * BK) + (ib * NW + wave) * RPB * BK;
-    buf_lds16(isA ? panelA : panelB, isA ? nrecA : nrecB, dst, voff[d], ksrc * BK * 2);
+    buf_lds16(isA ? panelA : panelB, isA ? nrecA : nrecB, dst, voff[d], (kbase + ksrc) * BK * 2);
   };
 
   typename MF::acc_t acc[TM][TN];
@@ -154,7 +169,6 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv(
     }
   };
 
-  const int NT = K / BK;
   const int NU = NT * KS;  // substeps (even: K % 64 == 0)
   auto step = [&](auto bufc, auto barc, int u) {
     constexpr bool BAR = decltype(barc)::value;
@@ -197,6 +211,20 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv(
     step(IC<1>{}, IC<true>{}, u + 1);
   }
   s_wait_vm<0>();  // the refills past the end land before the workgroup's LDS is released
+
+  if constexpr (SPLIT) {
+    // fp32 partial tile of split sk: each lane's 4 consecutive n of one m per block, 16 bytes
+    float* part = ws + (long)sk * M * N;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int m = m0 + wm * WTM + i * 16 + fr;
+      if (m >= M) continue;
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        *reinterpret_cast<f32x4*>(part + (long)m * N + n0 + wn * WTN + j * 16 + 4 * fk) = acc[i][j];
+    }
+    return;
+  }
 
   // ---- epilogue ------------------------------------------------------------------------------
   // Rows are written out in 16-byte pieces when C and ldc allow it, else in 8-byte halves.

@@ -22,15 +22,19 @@
 //     becomes current once that substep's own MFMAs (still tile kt's) are issued.  The loop runs
 //     one k-tile per iteration (unrolled further, the register allocator split the accumulator
 //     chains).
-// Requirements (the ladder's fit): N % 256 == 0, K % 128 == 0, 16-byte aligned rows, panel byte
+// Requirements (the ladder's fit): N % BN == 0, K % 128 == 0, 16-byte aligned rows, panel byte
 // offsets below 2^31.  M is predicated (A rows past M-1 clamped, never stored).
+// SPLIT = 1 (split-K), as in k_gemm_ilv: workgroup split sk of split_tile_of takes k-tiles
+// [sk*kper, ...), writes its fp32 partial tile to ws[sk][M][N]; k_splitk_reduce rounds the sum.
+// A split may start at an odd k-tile: the scale group of k-tile t is t/2 in every stage.
 // Build: -mllvm -amdgpu-sched-strategy=iterative-minreg, like k_gemm_ilv (own translation unit).
 // ============================================================================================
-template <int BM, int BN, int BK, int WM, int WN, int STAGES, int GROUP, int XCD, int RSP, int BFMT>
+template <int BM, int BN, int BK, int WM, int WN, int STAGES, int GROUP, int XCD, int RSP, int BFMT,
+          int SPLIT = 0>
 __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv8(
     const _Float16* __restrict__ A, const uint8_t* __restrict__ W, const _Float16* __restrict__ scale,
     const uint8_t* __restrict__ zero, _Float16* __restrict__ C, int M, int N, int K, int lda,
-    int ldw, int ldc) {
+    int ldw, int ldc, float* __restrict__ ws, int ksplit) {
   using MF = Mfma<16>;
   constexpr int SWZ = 2;
   constexpr int NW = WM * WN;
@@ -63,11 +67,18 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv8(
   const int wm = wave / WN, wn = wave % WN;
 
   const int nm = (M + BM - 1) / BM, nn = N / BN;
-  const int NT = K / BK;
   const int ng = K / 128;                     // scale groups per weight row
-  int tmi, tni;
-  tile_of<GROUP, XCD>(blockIdx.x, nm, nn, tmi, tni);
+  int tmi, tni, sk = 0;
+  if constexpr (SPLIT)
+    split_tile_of<GROUP, XCD>(blockIdx.x, nm, nn, ksplit, tmi, tni, sk);
+  else
+    tile_of<GROUP, XCD>(blockIdx.x, nm, nn, tmi, tni);
   const int m0 = tmi * BM, n0 = tni * BN;
+  // k-tiles of this workgroup: [kbase, kbase + NT)
+  const int NTALL = K / BK;
+  const int kper = SPLIT ? (NTALL + ksplit - 1) / ksplit : NTALL;
+  const int kbase = sk * kper;
+  const int NT = min(kper, NTALL - kbase);
 
   // ---- copies -------------------------------------------------------------------------------
   // A: as k_gemm_ilv (SWZ2 chunk swizzle of 128-byte rows).  W: 64-byte rows, 16-byte chunk c of
@@ -93,7 +104,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv8(
   const _Float16* panelS = scale + (BFMT == 2 ? (long)n0 * ng : (long)n0);
   const int mrow = wave * 64 + lane;
   auto dma = [&](int kt, int d) {
-    const int ks = min(kt, NT - 1);
+    const int ks = kbase + min(kt, NT - 1);
     uint8_t* st = smem + (kt % STAGES) * SBYTES;
     if (d < A_BLK) {
       buf_lds16(panelA, nrecA, st + (d * NW + wave) * 1024, voff[d], ks * BK * 2);
@@ -153,7 +164,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv8(
   constexpr int NRD = TM + TN + (BFMT == 2 ? 2 * TN : 0);  // reads of a substep with metadata
   constexpr int CH = NMF / 4;                              // chunks of 4 MFMAs
   constexpr int CPJ = CH / TN;                             // chunks per block column
-  static_assert(CH % TN == 0 && CPJ >= 2 && RSPAN <= CH && L <= CH, "substep chunking");
+  static_assert(CH % TN == 0 && CPJ >= 2 && RSPAN <= CH && L <= 2 * CH, "substep chunking");
   auto substep = [&](auto bufc, auto dmac, auto metac, int rkt, int rks, int dkt) {
     constexpr int bb = decltype(bufc)::value;
     constexpr bool DMA = decltype(dmac)::value;
@@ -239,6 +250,20 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv8(
 
   for (int kt = 0; kt < NT; ++kt) ktile(IC<BFMT == 2>{}, kt);
   s_wait_vm<0>();
+
+  if constexpr (SPLIT) {
+    // fp32 partial tile of split sk: each lane's 4 consecutive n of one m per block, 16 bytes
+    float* part = ws + (long)sk * M * N;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int m = m0 + wm * WTM + i * 16 + fr;
+      if (m >= M) continue;
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        *reinterpret_cast<f32x4*>(part + (long)m * N + n0 + wn * WTN + j * 16 + 4 * fk) = acc[i][j];
+    }
+    return;
+  }
 
   // ---- epilogue: C tile through LDS, as k_gemm_ilv ---------------------------------------------
   constexpr int RB = BN * 2, CPRW = RB / 16, RPP = NW * 64 / CPRW;

@@ -69,6 +69,51 @@ __device__ __forceinline__ void tile_of(int bid, int nm, int nn, int& tm, int& t
   }
 }
 
+// Split-K tile order: block id -> (tile_m, tile_n, split).  The XCD remap runs over all
+// tiles x ksplit workgroups, then the order is split-major: the workgroups an XCD holds at once
+// share k ranges, i.e. the same activation panel slices, in that XCD's L2.
+template <int GROUP, int XCD>
+__device__ __forceinline__ void split_tile_of(int bid, int nm, int nn, int ksplit, int& tm, int& tn,
+                                              int& sk) {
+  const int tiles = nm * nn;
+  if constexpr (XCD) {
+    const int total = tiles * ksplit;
+    if ((total & 7) == 0) bid = (bid & 7) * (total >> 3) + (bid >> 3);
+  }
+  sk = bid / tiles;
+  tile_of<GROUP, 0>(bid - sk * tiles, nm, nn, tm, tn);
+}
+
+// Split-K reduction: C[m][n] = fp16_rn(ws[0][m][n] + ws[1][m][n] + ... + ws[S-1][m][n]), the
+// partial sums added in the fixed order s = 0 .. S-1 in fp32 (deterministic), one rounding to
+// fp16.  ws is [S][M][N] fp32 (rows of N), N % 4 == 0; each thread takes 4 consecutive n.  The
+// partial loads of UNROLL splits are issued together before their adds, so a thread keeps UNROLL
+// loads in flight instead of waiting for each one (the reduction is a pure streaming read).
+// (A template so that every translation unit that includes this file may instantiate it.)
+template <int UNROLL = 8>
+__global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__ ws, int S, int M,
+                                                       int N, _Float16* __restrict__ C, int ldc) {
+  const long per = (long)M * N;
+  const long i4 = ((long)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i4 >= per) return;
+  const int m = (int)(i4 / N), n = (int)(i4 - (long)m * N);
+  const float* src = ws + i4;
+  f32x4 acc = *reinterpret_cast<const f32x4*>(src);
+  int s = 1;
+  for (; s + UNROLL <= S; s += UNROLL) {
+    f32x4 v[UNROLL];
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) v[u] = *reinterpret_cast<const f32x4*>(src + (s + u) * per);
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) acc += v[u];
+  }
+  for (; s < S; ++s) acc += *reinterpret_cast<const f32x4*>(src + s * per);
+  f16x4 o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o[e] = (_Float16)acc[e];
+  *reinterpret_cast<f16x4*>(C + (long)m * ldc + n) = o;
+}
+
 template <int BM, int BN, int BK, int WM, int WN, int MS, int SWZ, int GROUP, int XCD, int BFMT>
 struct GemmCfg {
   static constexpr int THREADS = WM * WN * 64;

@@ -41,9 +41,11 @@ AXES = (
 )
 
 DOMAINS = {
-    "ilv": dict(BM=(128, 256), BN=(128, 192, 256), BK=(32, 64), STAGES=(2, 3, 4), GROUP=(4, 8, 16),
-                XCD=(0, 1), WAVES=((2, 2), (2, 4), (4, 2)), RSP=(0, 8, 12)),
-    "ilv8": dict(STAGES=(3,), GROUP=(4, 8, 16), XCD=(0, 1), RSP=(4, 8, 12)),
+    "ilv": dict(BM=(64, 128, 256), BN=(128, 192, 256), BK=(32, 64), STAGES=(2, 3, 4),
+                GROUP=(4, 8, 16), XCD=(0, 1), WAVES=((2, 2), (2, 4), (4, 2), (1, 4)),
+                RSP=(0, 8, 12), SW=(0, 256, 512)),
+    "ilv8": dict(TILES=((256, 256, 2, 2), (128, 256, 1, 4)), STAGES=(3, 4), GROUP=(4, 8, 16),
+                 XCD=(0, 1), RSP=(4, 8, 12), SW=(0, 256, 512)),
     "dma": dict(BM=(64, 128, 256), BN=(64, 128, 192, 256), BK=(32, 64), STAGES=(2, 3, 4), SWZ=(0, 1, 2),
                 GROUP=(4, 8, 16), XCD=(0, 1), WAVES=((2, 2), (2, 4), (4, 2), (4, 4)), MS=(16, 32)),
     "reg": dict(BM=(64, 128, 256), BN=(64, 128, 256), BK=(64,), MS=(16, 32), SWZ=(1, 2), GROUP=(8,),
@@ -55,6 +57,28 @@ DOMAINS = {
 }
 
 BFMT_OF = {("fp16", "fp16"): 0, ("fp16", "int8"): 1, ("fp16", "uint8"): 2}
+SPLIT_MINKT = 8  # split-K rows keep at least this many k-tiles per split
+
+
+def split_count(tiles: int, ktiles: int, slots: int, minkt: int) -> int:
+    """Splits of a split-K row, as the shipped launchers compute them (split_count in
+    skeletons/common/splitk_host.h): the most splits with tiles x splits <= `slots` workgroups,
+    at least `minkt` k-tiles per split, no split empty; 1 = no split."""
+    if slots <= 0 or minkt <= 0 or 2 * tiles > slots:
+        return 1
+    sp = min(slots // tiles, ktiles // minkt)
+    if sp <= 1:
+        return 1
+    per = -(-ktiles // sp)
+    return -(-ktiles // per)
+
+
+def splits_of(kind: str, p: dict, M: int, N: int, K: int) -> int:
+    """Split count of an ilv / ilv8 hyperform at this shape (1 for every other kind)."""
+    if kind not in ("ilv", "ilv8") or not p.get("SW", 0):
+        return 1
+    tiles = -(-M // p["BM"]) * (N // p["BN"])
+    return split_count(tiles, K // p["BK"], p["SW"], p.get("MINKT", SPLIT_MINKT))
 
 
 def bfmt(op: OpSpec) -> int:
@@ -162,13 +186,15 @@ def shared_split(N: int, K: int, MB: int, R: int, U: int, SN: int, TPB: int = 10
 
 
 def tag(kind: str, p: dict) -> str:
+    sw = "_sw%d" % p["SW"] if p.get("SW", 0) else ""
     if kind == "ilv":
-        return "ilv_m%dn%dk%d_w%dx%d_s%d_g%d_x%d_r%d" % (
-            p["BM"], p["BN"], p["BK"], p["WM"], p["WN"], p["STAGES"], p["GROUP"], p["XCD"], p["RSP"])
-    if kind == "ilv8":
-        return "ilv8_m%dn%dk%d_w%dx%d_s%d_g%d_x%d_r%d_b%d" % (
+        return "ilv_m%dn%dk%d_w%dx%d_s%d_g%d_x%d_r%d%s" % (
             p["BM"], p["BN"], p["BK"], p["WM"], p["WN"], p["STAGES"], p["GROUP"], p["XCD"], p["RSP"],
-            p["BFMT"])
+            sw)
+    if kind == "ilv8":
+        return "ilv8_m%dn%dk%d_w%dx%d_s%d_g%d_x%d_r%d_b%d%s" % (
+            p["BM"], p["BN"], p["BK"], p["WM"], p["WN"], p["STAGES"], p["GROUP"], p["XCD"], p["RSP"],
+            p["BFMT"], sw)
     if kind == "dma":
         return "dma_m%dn%dk%d_w%dx%d_s%d_z%d_g%d_x%d_f%d" % (
             p["BM"], p["BN"], p["BK"], p["WM"], p["WN"], p["STAGES"], p["SWZ"], p["GROUP"], p["XCD"],
@@ -212,8 +238,9 @@ def legal(kind: str, p: dict, M: int, N: int, K: int):
         return None
     if kind == "ilv8":
         BM, BN, BK, WM, WN = p["BM"], p["BN"], p["BK"], p["WM"], p["WN"]
-        if (BM, BN, BK, WM, WN) != (256, 256, 64, 2, 2):
-            return "the int8 interleaved kernel is written for 256 x 256 x 64 tiles on 2 x 2 waves"
+        if (BM, BN, BK, WM, WN) not in ((256, 256, 64, 2, 2), (128, 256, 64, 1, 4)):
+            return ("the int8 interleaved kernel takes 256 x 256 (2 x 2 waves) or 128 x 256 "
+                    "(1 x 4 waves) tiles of 64 k: 64 weight rows per wave, >= 128-row wave tiles")
         if p["BFMT"] not in (1, 2):
             return "weights must be int8 (fmt 1) or uint8 group-128 (fmt 2)"
         if N % BN or K % 128:
@@ -293,6 +320,14 @@ def legal(kind: str, p: dict, M: int, N: int, K: int):
     return None
 
 
+def _with_split(p: dict, sw: int) -> dict:
+    """An ilv / ilv8 hyperform with split-K towards `sw` workgroups: the kernel's SPLIT template
+    parameter plus the launch-time rule (SW, MINKT); sw = 0 leaves the hyperform unsplit."""
+    if sw:
+        p.update(SW=sw, MINKT=SPLIT_MINKT, SPLIT=1)
+    return p
+
+
 def variants(op: OpSpec) -> Iterator[Hyperform]:
     if op.kind != "gemm":
         raise PluginCapabilityError("gfx950 skeletons take 'gemm' in the pipeline; FMHA is a "
@@ -337,9 +372,10 @@ def variants(op: OpSpec) -> Iterator[Hyperform]:
                             for X in d["XCD"]:
                                 for (WM, WN) in d["WAVES"]:
                                     for RS in d["RSP"]:
-                                        out.append(("ilv", dict(
-                                            BM=BM, BN=BN, BK=BK, WM=WM, WN=WN, STAGES=ST,
-                                            GROUP=G, XCD=X, RSP=RS)))
+                                        for SW in d["SW"]:
+                                            out.append(("ilv", _with_split(dict(
+                                                BM=BM, BN=BN, BK=BK, WM=WM, WN=WN, STAGES=ST,
+                                                GROUP=G, XCD=X, RSP=RS), SW)))
         d = DOMAINS["dma"]
         for BM in d["BM"]:
             for BN in d["BN"]:
@@ -353,14 +389,17 @@ def variants(op: OpSpec) -> Iterator[Hyperform]:
                                             out.append(("dma", dict(
                                                 BM=BM, BN=BN, BK=BK, WM=WM, WN=WN, STAGES=ST,
                                                 SWZ=SW, GROUP=G, XCD=X, XT=0, MINB=1, MS=MS)))
-    if b in (1, 2) and M > 128:
+    if b in (1, 2) and M > 32:
         d = DOMAINS["ilv8"]
-        for ST in d["STAGES"]:
-            for G in d["GROUP"]:
-                for X in d["XCD"]:
-                    for RS in d["RSP"]:
-                        out.append(("ilv8", dict(BM=256, BN=256, BK=64, WM=2, WN=2, STAGES=ST,
-                                                 GROUP=G, XCD=X, RSP=RS, BFMT=b)))
+        for (BM, BN, WM, WN) in d["TILES"]:
+            for ST in d["STAGES"]:
+                for G in d["GROUP"]:
+                    for X in d["XCD"]:
+                        for RS in d["RSP"]:
+                            for SW in d["SW"]:
+                                out.append(("ilv8", _with_split(dict(
+                                    BM=BM, BN=BN, BK=64, WM=WM, WN=WN, STAGES=ST, GROUP=G, XCD=X,
+                                    RSP=RS, BFMT=b), SW)))
     d = DOMAINS["reg"]
     for BM in d["BM"]:
         for BN in d["BN"]:

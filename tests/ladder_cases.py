@@ -24,12 +24,18 @@ FP16 = [
     ("l2r1d4", 32, 3840, 15360),
     ("s32r1u4", 32, 512, 65792),
     ("l4r1n4d3", 64, 15360, 3840),
-    ("l4r1d3", 64, 3840, 15360),           # the C2 decode-sweep point M = 64, N = 3840
+    ("i64x192k64s3w256", 64, 3840, 15360),  # the C2 decode-sweep point M = 64, N = 3840
+    ("i64x192k64s3w256", 40, 1920, 4096),   # ragged M, few k-tiles per split
+    ("l4r1d3", 64, 4096, 3840),             # N % 192 != 0
     ("d128x64k64s4", 128, 15360, 3840),
     ("d128x64k64s4", 200, 8192, 3840),
-    ("d64x64k64s4", 128, 3840, 15360),
-    ("d64x64k64s4", 256, 3840, 15360),
-    ("l8r1n2d3", 100, 3872, 3840),         # 64 < M <= 128 with N % 64 == 32
+    ("i128x128k64s3w256", 128, 3840, 15360),
+    ("i128x128k64s3w256", 100, 3840, 3840),
+    ("d64x64k64s4", 128, 8192, 3840),       # N >= 6144: past the split-K row's band
+    ("d64x64k64s4", 256, 3904, 3840),       # N % 256 != 0
+    ("i128x256k64s3w256", 256, 3840, 15360),
+    ("i128x256k64s3w256", 130, 2048, 7680),
+    ("l8r1n2d3", 100, 3872, 3840),          # 64 < M <= 128 with N % 64 == 32
     ("d128x128k64s4", 256, 15360, 3840),
     ("i256x256k64w4r8", 512, 4096, 3840),
     ("i256x256k64w4r8", 2049, 3840, 15360),
@@ -39,8 +45,9 @@ FP16 = [
 # extra elements per row of A, B, C)
 FP16_STRIDED = [
     ("l1r1d4", 16, 3840, 3840, 8, 16, 4),
-    ("l4r1d3", 64, 3840, 3840, 8, 8, 4),
-    ("d64x64k64s4", 128, 3840, 3840, 8, 8, 4),
+    ("i64x192k64s3w256", 64, 3840, 3840, 8, 8, 4),
+    ("i128x128k64s3w256", 128, 3840, 3840, 8, 8, 4),
+    ("d64x64k64s4", 128, 8192, 3840, 8, 8, 4),
     ("d128x128k64s4", 256, 15360, 3840, 16, 8, 4),
     ("i256x256k64w4r8", 300, 4096, 3840, 8, 16, 4),
     ("i256x256k64w4r8", 512, 4096, 3840, 64, 64, 64),
@@ -72,11 +79,15 @@ W8 = {
         ("s16r1u4", 16, 1040, 5120),
         ("h32r1u4n2", 32, 512, 65792),
         ("l4r1n4d3", 64, 34816, 5120),
-        ("l4r1n2d3", 64, 5120, 17408),
-        ("l8r1n2d3", 128, 5120, 17408),
-        ("m128x128k64", 128, 34816, 5120),
+        ("i8x128x256s3w256", 64, 5120, 17408),
+        ("l4r1n2d3", 64, 5120, 6144),
+        ("i8x128x256s3w256", 128, 5120, 17408),
+        ("i8x128x256s3w256", 128, 34816, 5120),
+        ("i8x128x256s3w256", 100, 7168, 5120),
+        ("l8r1n2d3", 128, 5152, 5120),
         ("m128x128k64", 256, 5120, 5120),
-        ("m128x128k64s16", 2048, 1024, 5120),
+        ("i8x128x256s3w256", 2048, 1024, 5120),
+        ("m128x128k64s16", 2048, 1152, 5120),
         ("i8x256k64s3", 2048, 7168, 5120),
         ("m256x256k64", 512, 2048, 5184),
     ],
@@ -93,11 +104,15 @@ W8 = {
         ("s16r1u4", 16, 1040, 5120),
         ("h32r1u4n2", 32, 512, 65792),
         ("l4r1n4d3", 64, 34816, 5120),
-        ("l4r1n2d3", 64, 5120, 17408),
-        ("l8r1n2d3", 128, 5120, 17408),
-        ("m128x128k64", 128, 34816, 5120),
+        ("i8x128x256s3w256", 64, 5120, 17408),
+        ("l4r1n2d3", 64, 5120, 6144),
+        ("i8x128x256s3w256", 128, 5120, 17408),
+        ("i8x128x256s3w256", 128, 34816, 5120),
+        ("i8x128x256s3w256", 100, 7168, 5120),
+        ("l8r1n2d3", 128, 5152, 5120),
         ("m128x128k64", 256, 5120, 5120),
-        ("m128x128k64s16", 2048, 1024, 5120),
+        ("i8x128x256s3w256", 2048, 1024, 5120),
+        ("m128x128k64s16", 2048, 1152, 5120),
         ("i8x256k64s3", 2048, 7168, 5120),
     ],
 }

@@ -45,9 +45,16 @@ def test_prefill_inc_is_generated_from_select(op, kind):
                           check=True, capture_output=True, text=True).stdout
     with open(os.path.join(d, "prefill.inc"), encoding="utf-8") as f:
         assert f.read() == text, "prefill.inc is stale: re-run the build"
-    # every interleaved row of the ladder is instantiated there, and nothing else
-    rows = [r for r in _select(op).LADDER if r[3] == kind]
-    assert rows and text.count("template hipError_t launch_%s<" % kind) == len(rows)
+    # every interleaved row of the ladder is instantiated there, once per distinct launcher, and
+    # nothing else
+    import importlib.util as iu
+
+    spec = iu.spec_from_file_location("gd_" + op, os.path.join(d, "gen_dispatch.py"))
+    gd = iu.module_from_spec(spec)
+    spec.loader.exec_module(gd)
+    insts = {gd.instantiation(r[3], r[4]) for r in _select(op).LADDER if r[3] == kind}
+    assert insts and text.count("template hipError_t launch_%s<" % kind) == len(insts)
+    assert all(i in text for i in insts)
 
 
 @pytest.mark.parametrize("op", ["gemm_fp16", "gemm_w8a16"])
@@ -79,7 +86,7 @@ def test_delivery_layout():
 def _declared():
     with open(HEADER, encoding="utf-8") as f:
         text = f.read()
-    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(tempo_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(tempo_\w+)\s*\(", text, re.M)))
 
 
 def test_library_exports_every_declared_symbol():
