@@ -75,7 +75,9 @@ EXPORTS = {
     "tempo_gptq_repack_u8": ([_p, _p, _p, _i, _i, _i, _p, _p, _p, _p], _i),
     "tempo_gemm_fp16_workspace_bytes": ([ct.POINTER(TempoGemmParams)], ct.c_size_t),
     "tempo_gemm_w8a16_workspace_bytes": ([ct.POINTER(TempoW8A16Params)], ct.c_size_t),
+    "tempo_gemm_w8a16_launch_noalloc": ([ct.POINTER(TempoW8A16Params), _p], _i),
 }
+NOALLOC_SCRATCH_BYTES = 32 << 20
 
 
 def lib():
@@ -249,6 +251,19 @@ def gemm_w8a16(A, Wq, scale, zero=None, fmt: int = W8_SYM_I8, group: int = 128, 
         C = torch.empty((M, N), dtype=torch.float16, device=A.device)
     p = w8a16_params(A, Wq, scale, zero, C, fmt, group)
     _check(lib().tempo_gemm_w8a16_launch(p, _stream(stream)), "tempo_gemm_w8a16_launch")
+    return C
+
+
+def gemm_w8a16_noalloc(A, Wq, scale, zero=None, fmt: int = W8_SYM_I8, group: int = 128, C=None,
+                       stream=None):
+    """gemm_w8a16 through the allocation-free entry point (the library's static per-GPU scratch
+    serves split-K rows); C must be given (this helper allocates nothing either)."""
+    if C is None:
+        raise ValueError("gemm_w8a16_noalloc writes into a caller-provided C")
+    _require_w8(A, Wq, scale, zero, fmt, group)
+    p = w8a16_params(A, Wq, scale, zero, C, fmt, group)
+    _check(lib().tempo_gemm_w8a16_launch_noalloc(p, _stream(stream)),
+           "tempo_gemm_w8a16_launch_noalloc")
     return C
 
 

@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstring>
+#include <mutex>
 
 #include "tempo_gfx950.h"
 #include "gemm_fp16/gfx950/launch.h"
@@ -72,6 +73,36 @@ tempo::gen8::W8A16Params to_pod(const TempoW8A16Params* p) {
   return g;
 }
 
+// ---- the allocation-free entry point's scratch ------------------------------------------------
+// A file-scope device array: every GPU the library runs on holds its own copy, at its own address,
+// from module load until the process ends.  Host code never passes `scratch` itself to a kernel
+// (in host code the name is a stand-in, not a device address): the address is looked up once per
+// device with hipGetSymbolAddress, with that device current, and kept in scratch_ptr[].
+static __device__ __align__(256) unsigned char scratch[TEMPO_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+void* scratch_ptr[kMaxDevices] = {};
+std::mutex scratch_mu;
+
+// The current device's scratch address (nullptr with *err set when it cannot be had).
+void* device_scratch(hipError_t* err) {
+  int dev = 0;
+  *err = hipGetDevice(&dev);
+  if (*err != hipSuccess) return nullptr;
+  if (dev < 0 || dev >= kMaxDevices) {
+    *err = hipErrorInvalidDevice;
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (!scratch_ptr[dev]) {
+    void* p = nullptr;
+    *err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (*err != hipSuccess) return nullptr;
+    scratch_ptr[dev] = p;
+  }
+  return scratch_ptr[dev];
+}
+
 int copy_tag(const char* t, char* tag, int tag_len) {
   if (tag && tag_len > 0) {
     const char* s = t ? t : "";
@@ -115,6 +146,17 @@ int tempo_gemm_w8a16_applicable(const TempoW8A16Params* p) {
 int tempo_gemm_w8a16_launch(const TempoW8A16Params* p, tempo_stream_t stream) {
   if (!p) return (int)hipErrorInvalidValue;
   return (int)tempo::gen8::launch(to_pod(p), static_cast<hipStream_t>(stream));
+}
+
+int tempo_gemm_w8a16_launch_noalloc(const TempoW8A16Params* p, tempo_stream_t stream) {
+  if (!p) return (int)hipErrorInvalidValue;
+  hipError_t err = hipSuccess;
+  tempo::gen8::Workspace w;
+  w.ptr = device_scratch(&err);
+  if (!w.ptr) return (int)err;
+  w.bytes = TEMPO_NOALLOC_SCRATCH_BYTES;
+  w.pool = false;  // a row whose workspace exceeds the scratch returns hipErrorOutOfMemory
+  return (int)tempo::gen8::launch_with(to_pod(p), static_cast<hipStream_t>(stream), w);
 }
 
 int tempo_gemm_fp16_gate_up_launch(const TempoGemmParams* p, tempo_stream_t stream) {

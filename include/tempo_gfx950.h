@@ -92,6 +92,19 @@ int tempo_gemm_w8a16_launch(const TempoW8A16Params* p, tempo_stream_t stream);
  * covered).  Host-only; no reference counterpart (as for tempo_gemm_fp16_workspace_bytes). */
 size_t tempo_gemm_w8a16_workspace_bytes(const TempoW8A16Params* p);
 
+/* tempo_gemm_w8a16_launch that allocates nothing, for callers that cannot allocate (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  No counterpart in
+ * the reference.  Same rows, kernels and results as tempo_gemm_w8a16_launch (bit for bit); a
+ * split-K row takes its workspace from a static device array of TEMPO_NOALLOC_SCRATCH_BYTES per
+ * GPU instead of the allocating pool, and a row that would need more returns
+ * hipErrorOutOfMemory (2) without launching.  The current ladder never needs more: a split-K row
+ * keeps tiles x splits <= 256, so its workspace is at most 256 x 128 x 256 x 4 bytes = 32 MiB.
+ * Every call on one GPU shares that GPU's array (the first call on a device looks its address
+ * up): calls that overlap on one GPU -- on different streams, or from different threads without
+ * ordering -- race on it.  Nothing in it needs clearing: a split-K launch writes every partial
+ * sum it later reads. */
+#define TEMPO_NOALLOC_SCRATCH_BYTES (32u << 20)
+int tempo_gemm_w8a16_launch_noalloc(const TempoW8A16Params* p, tempo_stream_t stream);
 
 /* ------------------------------------------------------------------------------------------
  * Fused gate/up epilogue (the MLP's first projection):
