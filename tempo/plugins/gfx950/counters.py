@@ -15,6 +15,12 @@ How the raw numbers become the figures the measure stage reports (per dispatch):
   * MFMA utilisation = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / XCDs x SIMDs) -- rocprofv3's
     own MfmaUtil expression; GRBM_GUI_ACTIVE is reported summed over the 8 XCDs.
   * engine clock = GRBM_GUI_ACTIVE / XCDs / dispatch duration (the counter run's timestamps).
+    Under counter collection GRBM_GUI_ACTIVE also covers a fixed stretch around each dispatch
+    (about 15k cycles on this part), so the clock and the GUI-based MFMA utilisation are only
+    reported for dispatches of at least MIN_CLOCK_NS; shorter ones get the utilisation against
+    the spec clock only.
+  * MFMA utilisation at the spec clock = SQ_VALU_MFMA_BUSY_CYCLES / (duration x SPEC_GHZ x SIMDs):
+    the share of the spec-peak matrix throughput the dispatch used, whatever clock it ran at.
 """
 from __future__ import annotations
 
@@ -48,6 +54,8 @@ GROUPS = {
 COPY_KERNEL = "__amd_rocclr_copyBuffer"
 XCDS = 8
 SIMDS = 1024  # 256 CUs x 4 SIMDs
+SPEC_GHZ = 2.4  # the engine clock the published peaks assume
+MIN_CLOCK_NS = 100_000
 
 
 class Gfx950Meters:
@@ -132,7 +140,8 @@ def assign_segments(dispatches: list, segments: list, match: str) -> dict:
     """Attribute dispatches to the segments a counter-pass program declared, in order.
 
     segments: [{"label": str, "count": n, "copy_bytes": b (calibration segments only)}] in the
-    order the program launched them.  A calibration segment takes the next `count` device-copy
+    order the program launched them; `count` is the number of DISPATCHES (launches x
+    dispatches per launch).  A calibration segment takes the next `count` device-copy
     dispatches; any other segment takes the next `count` dispatches whose kernel name contains
     `match` (the library's namespace).  Other kernels (input generation) are skipped.
     Returns {label: [dispatch, ...]}; raises if the pass ran fewer dispatches than declared."""
@@ -181,16 +190,19 @@ def derive(per_counter: dict, scales: dict, algorithmic_bytes: float = 0.0) -> d
         out["hbm_bytes"] = out["fetch_bytes"] + out["write_bytes"]
         if algorithmic_bytes:
             out["traffic_over_algorithmic"] = out["hbm_bytes"] / algorithmic_bytes
+    dur = c.get("_duration_ns", 0.0)
+    if dur and "SQ_VALU_MFMA_BUSY_CYCLES" in c:
+        out["mfma_util_spec_clock"] = c["SQ_VALU_MFMA_BUSY_CYCLES"] / (dur * SPEC_GHZ * SIMDS)
     gui = c.get("GRBM_GUI_ACTIVE")
     if gui:
         cycles = gui / XCDS
         out["gui_cycles"] = cycles
-        if "SQ_VALU_MFMA_BUSY_CYCLES" in c:
-            out["mfma_util"] = c["SQ_VALU_MFMA_BUSY_CYCLES"] / (cycles * SIMDS)
         if "SQ_LDS_BANK_CONFLICT" in c:
             out["lds_bank_conflict_per_cu_cycle"] = c["SQ_LDS_BANK_CONFLICT"] / (cycles * 256)
-        if c.get("_duration_ns"):
-            out["sclk_ghz"] = cycles / c["_duration_ns"]
+        if dur >= MIN_CLOCK_NS:
+            out["sclk_ghz"] = cycles / dur
+            if "SQ_VALU_MFMA_BUSY_CYCLES" in c:
+                out["mfma_util"] = c["SQ_VALU_MFMA_BUSY_CYCLES"] / (cycles * SIMDS)
     for k in ("SQ_INSTS_VALU_MFMA_MOPS_F16", "SQ_INSTS_LDS", "SQ_LDS_IDX_ACTIVE",
               "SQ_INSTS_VMEM_RD", "SQ_INSTS_VMEM_WR", "TA_BUSY_avr", "SQ_LDS_BANK_CONFLICT"):
         if k in c:
@@ -200,14 +212,28 @@ def derive(per_counter: dict, scales: dict, algorithmic_bytes: float = 0.0) -> d
     return out
 
 
-def medians(dispatches: list) -> dict:
-    """Per-counter median over a kernel's dispatches, plus its median duration (ns)."""
+def medians(dispatches: list, per_launch: int = 1) -> dict:
+    """Per-counter median over launches, plus the median launch duration (ns).  A launch is
+    `per_launch` consecutive dispatches (a split-K row dispatches its main kernel and then the
+    reduction); its counters and durations are the sums over them."""
+    launches = []
+    for i in range(0, len(dispatches) - per_launch + 1, per_launch):
+        grp = dispatches[i:i + per_launch]
+        if [d["kernel"] for d in grp] != [d["kernel"] for d in dispatches[:per_launch]]:
+            raise RuntimeError("launch %d dispatched %s, not the kernels of the first launch (%s)"
+                               % (i // per_launch, [d["kernel"] for d in grp],
+                                  [d["kernel"] for d in dispatches[:per_launch]]))
+        cnt = {}
+        for d in grp:
+            for k, v in d["counters"].items():
+                cnt[k] = cnt.get(k, 0.0) + v
+        dur = sum(d["end"] - d["start"] for d in grp if d["end"] > d["start"])
+        launches.append((cnt, dur))
     keys = set()
-    for d in dispatches:
-        keys |= set(d["counters"])
-    out = {k: _median([d["counters"][k] for d in dispatches if k in d["counters"]])
-           for k in keys}
-    durs = [d["end"] - d["start"] for d in dispatches if d["end"] > d["start"]]
+    for cnt, _ in launches:
+        keys |= set(cnt)
+    out = {k: _median([cnt[k] for cnt, _ in launches if k in cnt]) for k in keys}
+    durs = [dur for _, dur in launches if dur > 0]
     if durs:
         out["_duration_ns"] = _median(durs)
     return out

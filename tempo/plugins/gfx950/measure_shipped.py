@@ -168,8 +168,10 @@ def counter_pass(op: str, segfile: str, quick: bool = False) -> int:
         for _ in range(REPS - 1):
             run()
         torch.cuda.synchronize()
-        segs.append(dict(label=label_of(M, N, K, fmt), count=REPS,
-                         route=capi.route(fmt, M, N, K) if op != "fmha" else "k_fmha_fwd3"))
+        # a split-K row dispatches two kernels per launch: its main kernel, then the reduction
+        per = 1 if op == "fmha" or capi.workspace_bytes(fmt, M, N, K) == 0 else 2
+        segs.append(dict(label=label_of(M, N, K, fmt), count=REPS * per, per_launch=per,
+                         route=capi.route(fmt, M, N, K) if op != "fmha" else "k_fmha_fwd4"))
     with open(segfile, "w") as f:
         json.dump(segs, f, indent=1)
     return 0
@@ -182,7 +184,7 @@ def counters(op: str, out: str, groups, quick: bool = False) -> str:
                                                copy_scales, derive, medians)
 
     meters = Gfx950Meters()
-    per_shape, scales, routes = {}, {}, {}
+    per_shape, scales, routes, per_launch = {}, {}, {}, {}
     for g in groups:
         d = os.path.abspath(os.path.join(out, "pmc_%s_%s" % (op, g)))
         seg = os.path.join(d, "segments.json")
@@ -199,7 +201,9 @@ def counters(op: str, out: str, groups, quick: bool = False) -> str:
         for s in segs:
             if s["label"] in got:
                 routes[s["label"]] = s.get("route")
-                per_shape.setdefault(s["label"], {}).update(medians(got[s["label"]]))
+                per_launch[s["label"]] = s.get("per_launch", 1)
+                per_shape.setdefault(s["label"], {}).update(
+                    medians(got[s["label"]], s.get("per_launch", 1)))
     rows = []
     for lab, med in per_shape.items():
         M, N, K, fmt = (int(x) for x in lab.split(","))
@@ -207,6 +211,7 @@ def counters(op: str, out: str, groups, quick: bool = False) -> str:
         if med.get("_duration_ns"):
             fig["pmc_duration_us"] = med["_duration_ns"] / 1e3
         rows.append(dict(M=M, N=N, K=K, fmt=fmt, route=routes.get(lab),
+                         dispatches_per_launch=per_launch.get(lab, 1),
                          algorithmic_bytes=algorithmic_bytes(op, M, N, K, fmt),
                          algorithmic_flops=algorithmic_flops(op, M, N, K, fmt),
                          counters=fig))

@@ -17,8 +17,8 @@
 //     (lane l, k-group l/32 holds exactly the 8 key indices that operand slot needs), so P never
 //     touches LDS.  O^T's column is again the query row, so the online-softmax rescale is one
 //     per-lane factor for all accumulator registers.
-//   * K and V blocks are copied global -> LDS with LDS-DMA (global_load_lds_dwordx4), no register
-//     staging.  Both are stored in their natural [key][d] order with the 16-byte chunk index
+//   * K and V blocks are copied global -> LDS with LDS-DMA (buffer_load_dwordx4 ... lds), no
+//     register staging.  Both are stored in their natural [key][d] order with the 16-byte chunk index
 //     XOR-ed by fmha_swz(key % 16), a bit swap of the 4-bit row index chosen so that both read
 //     patterns are free of bank conflicts on the 64-bank LDS: the K read (16 rows, one chunk) and
 //     the transposed V read (4 rows x 4 consecutive chunks) each land on 16 distinct 16-byte
@@ -61,39 +61,66 @@ constexpr float FMHA_TAU = 8.f;  // log2 of the largest unnormalised probability
 // swizzle key of a key row (only its low 4 bits matter): swap the two 2-bit halves
 __device__ __forceinline__ int fmha_swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
 
+// 16-byte-per-lane buffer load into LDS (MUBUF buffer_load ... lds): lane l's 16 bytes at byte
+// offset voff of the raw buffer [base, base + nrec) land at lds + 16 l; reads past nrec return
+// zeros.  The MUBUF form, not global_load_lds: the compiler counts a FLAT-encoded LDS copy on
+// both counters and then waits for every LDS read with lgkmcnt(0).
+__device__ __forceinline__ void fmha_buf_lds16(const void* base, unsigned nrec, void* lds,
+                                               unsigned voff) {
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)nrec, 0x00020000);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (fmha_lds_void_t*)lds, 16, (int)voff, 0, 0, 0);
+}
+
 // ============================================================================================
-// k_fmha_fwd3 -- software-pipelined: the score MFMAs of the NEXT key block overlap the softmax
-// of the current one.  Iteration kb computes S(kb+1) = K(kb+1).Q^T on the matrix cores while the
-// VALU turns S(kb) into P(kb) (max, exponentials, sums), then O^T += V(kb)^T . P(kb)^T.  K runs
-// one block ahead of V: K(kb+2) and V(kb+1) are copied during iteration kb into the slots that
-// K(kb) and V(kb-1) left, so the LDS footprint is two K and two V blocks.
+// k_fmha_fwd4 -- software-pipelined over 32-key blocks: iteration kb computes S(kb+1) = K(kb+1).Q^T
+// on the matrix cores while the VALU turns S(kb) into P(kb) (max, exponentials, sums), then
+// O^T += V(kb)^T . P(kb)^T.  K runs one block ahead of V: K(kb+2) and V(kb+1) are copied during
+// iteration kb into the slots K(kb) and V(kb-1) left (two K and two V slots).  Laid out for one
+// wave per SIMD (the 128 O accumulators, Q and the fragments take ~376 registers), where
+// nothing but the wave's own instruction order hides a latency:
+//   * one LDS array per slot (K0, K1, V0, V1) and the key loop unrolled by two, so every slot is
+//     a compile-time choice: the compiler's LDS alias scopes then keep the reads of one slot
+//     from waiting for the copies in flight into the other (one shared array made every V read
+//     wait for all outstanding copies, s_waitcnt vmcnt(0), every key block);
+//   * the score chain of block kb+1 is cut into DS chunks, one MFMA each, fenced with
+//     sched_barrier; each chunk also issues the next K fragment read (KP ahead), one pair of
+//     transposed V reads for the PV step of block kb, and one slice of block kb's softmax --
+//     row max, the cross-half exchange, and the exponentials against the running reference,
+//     computed speculatively and pinned into their chunk (the causal mask of the last blocks is
+//     applied before the chain, behind one uniform branch);
+//   * then the rare move of the reference (ballot): O and l rescaled in place in the
+//     accumulator registers and the exponentials redone; then the 2 DB PV MFMAs back to back.
+// Every sum is taken in a fixed order (the row max and sums, then P.V by k-step), so results do
+// not depend on the schedule.
 // ============================================================================================
-// SG = 1 adds sched_group_barrier hints that interleave MFMAs with LDS reads and VALU work
-// (measured slower at C5; the shipped instantiation has SG = 0).
-template <int D, bool CAUSAL, int BKV2, int SG = 0>
-__global__ __launch_bounds__(256, 1) void k_fmha_fwd3(
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(256, 1) void k_fmha_fwd4(
     const _Float16* __restrict__ Q, const _Float16* __restrict__ Kg,
     const _Float16* __restrict__ Vg, _Float16* __restrict__ O, float* __restrict__ LSE, int B,
     int H, int Hkv, int Sq, int Sk, float scale_log2, long q_sb, long q_ss, long q_sh, long k_sb,
     long k_ss, long k_sh, long v_sb, long v_ss, long v_sh, long o_sb, long o_ss, long o_sh) {
   static_assert(D == 128 || D == 256, "head dim 128 or 256");
-  static_assert(BKV2 == 32 || BKV2 == 64, "key block 32 or 64");
+  constexpr int BKV2 = 32;
   constexpr int WAVES = 4;
-  constexpr int NJ = BKV2 / 32;
   constexpr int DCH = D / 8;
-  constexpr int DS = D / 16;
-  constexpr int DB = D / 32;
+  constexpr int DS = D / 16;   // score MFMAs (k = 16 each) per key block = chunks
+  constexpr int DB = D / 32;   // 32-wide d blocks of O
   constexpr int RB = D * 2;
   constexpr int ROWS_PER_KB = 1024 / RB;
   constexpr int BLK = BKV2 / ROWS_PER_KB;
   constexpr int BLK_W = BLK / WAVES;
   constexpr int BQW = 32 * WAVES;
   constexpr int TILE_B = BKV2 * RB;
+  constexpr int KP = 4;        // K fragment reads ahead of the chain
+  constexpr int NX = DS - 4;   // chunks carrying exponentials (chunks 2-3: max, exchange)
+  static_assert(DS >= 8 && 2 * DB == DS, "one V pair per chunk");
   static_assert(BLK % WAVES == 0, "DMA blocks split over the waves");
 
-  __shared__ __attribute__((aligned(1024))) char smem[4 * TILE_B];  // K[2] then V[2]
-  char* const kbuf = smem;
-  char* const vbuf = smem + 2 * TILE_B;
+  __shared__ __attribute__((aligned(1024))) char k0s[TILE_B];
+  __shared__ __attribute__((aligned(1024))) char k1s[TILE_B];
+  __shared__ __attribute__((aligned(1024))) char v0s[TILE_B];
+  __shared__ __attribute__((aligned(1024))) char v1s[TILE_B];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -140,26 +167,34 @@ __global__ __launch_bounds__(256, 1) void k_fmha_fwd3(
     ksrc[i] = (unsigned)(r * k_ss * 2 + c * 16);
     vsrc[i] = (unsigned)(r * v_ss * 2 + c * 16);
   }
-  // one operand block j (K or V) -> its slot j & 1; rows past Sk re-read row Sk-1
-  auto copy_block = [&](const char* base, long ss, const unsigned* src, char* slots, int j) {
-    char* dst = slots + (j & 1) * TILE_B;
+  // block j of one operand into the slot array dst; rows past Sk re-read row Sk-1.  The buffer
+  // starts at the block's first row and ends with row Sk-1 (every offset below is inside it).
+  auto copy_block = [&](const char* base, long ss, const unsigned* src, char* dst, int j) {
     const int j0 = j * BKV2;
     const char* blk = base + (long)j0 * ss * 2;
+    // (capped at 2^32 - 1: every offset used is below 32 rows x ss x 2 < 2^31)
+    const long span = (long)(Sk - 1 - j0) * ss * 2 + D * 2;
+    const unsigned nrec = span < 0xFFFFFFFFL ? (unsigned)span : 0xFFFFFFFFu;
     if (j0 + BKV2 <= Sk) {
 #pragma unroll
       for (int i = 0; i < BLK_W; ++i)
-        __builtin_amdgcn_global_load_lds((void*)(blk + src[i]),
-                                         (fmha_lds_void_t*)(dst + (i * WAVES + wave) * 1024), 16,
-                                         0, 0);
+        fmha_buf_lds16(blk, nrec, dst + (i * WAVES + wave) * 1024, src[i]);
     } else {
 #pragma unroll
       for (int i = 0; i < BLK_W; ++i) {
-        const long back = (long)max(0, j0 + drow[i] - (Sk - 1));
-        __builtin_amdgcn_global_load_lds((void*)(blk + src[i] - back * ss * 2),
-                                         (fmha_lds_void_t*)(dst + (i * WAVES + wave) * 1024), 16,
-                                         0, 0);
+        const unsigned back = (unsigned)max(0, j0 + drow[i] - (Sk - 1));
+        fmha_buf_lds16(blk, nrec, dst + (i * WAVES + wave) * 1024,
+                       src[i] - back * (unsigned)(ss * 2));
       }
     }
+  };
+  auto kslot = [&](auto par) -> char* {
+    if constexpr (decltype(par)::value) return k1s;
+    else return k0s;
+  };
+  auto vslot = [&](auto par) -> char* {
+    if constexpr (decltype(par)::value) return v1s;
+    else return v0s;
   };
 
   const int kkey = fmha_swz(l32);
@@ -185,136 +220,128 @@ __global__ __launch_bounds__(256, 1) void k_fmha_fwd3(
   float m_run = -__builtin_inff();
   float l_run = 0.f;
 
-  // S^T of block j from K slot j & 1 into s (NJ 32-key blocks)
-  auto scores = [&](f32x16* s, int j) {
-    const char* k = kbuf + (j & 1) * TILE_B;
-#pragma unroll
-    for (int jb = 0; jb < NJ; ++jb) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s[jb][r] = 0.f;
-#pragma unroll
-      for (int st = 0; st < DS; ++st) {
-        const f16x8 kf = *reinterpret_cast<const f16x8*>(k + koff[st & 7] + (st >> 3) * 256 +
-                                                         jb * 32 * RB);
-        s[jb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[st], s[jb], 0, 0, 0);
-      }
-    }
-  };
-  // softmax, part 1: masked row max of block j (scale > 0 commutes with the max)
-  auto softmax_max = [&](f32x16* s, int j) {
-    const int j0 = j * BKV2;
-    const bool need_mask = (j0 + BKV2 > Sk) || (CAUSAL && j0 + BKV2 - 1 > q0 + off);
-    float mx = -__builtin_inff();
-#pragma unroll
-    for (int jb = 0; jb < NJ; ++jb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float x = s[jb][r];
-        if (need_mask) {
-          const int jj = j0 + 32 * jb + 8 * (r >> 2) + 4 * hl + (r & 3);
-          const bool hide = (jj >= Sk) || (CAUSAL && jj > qi + off);
-          x = hide ? -__builtin_inff() : x;
-        }
-        s[jb][r] = x;
-        mx = fmaxf(mx, x);
-      }
-    return fmaxf(mx, __shfl_xor(mx, 32)) * scale_log2;
-  };
-  // the (rare) move of the reference value, with the O rescale it implies
-  auto move_ref = [&](float mx) {
-    const bool move = !(mx - m_run <= FMHA_TAU);
-    if (__builtin_amdgcn_ballot_w64(move) != 0) {
-      const float m_new = fmaxf(m_run, mx);
-      const float alpha =
-          (m_new == -__builtin_inff()) ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
-      l_run *= alpha;
-      m_run = m_new;
-#pragma unroll
-      for (int i = 0; i < DB; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc_o[i][r] *= alpha;
-    }
-  };
-  // softmax, part 2 fused with O^T += V^T . P^T: the 8 probabilities of MFMA k-step t are made
-  // right before the step's MFMAs, so the exponentials of step t+1 overlap the MFMAs of step t.
-  // Step t, element e <-> key 32(t/2) + 16(t%2) + 8(e/4) + 4*hl + e%4 = S register 8(t%2) + e of
-  // 32-key block t/2.
-  auto exp_pv = [&](const f32x16* s, int j) {
-    const char* v = vbuf + (j & 1) * TILE_B;
-    const float m_use = (m_run == -__builtin_inff()) ? 0.f : m_run;
-    float psum = 0.f;
-#pragma unroll
-    for (int t = 0; t < 2 * NJ; ++t) {
-      f16x8 pt;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float pv = __builtin_amdgcn_exp2f(
-            __builtin_fmaf(s[t >> 1][8 * (t & 1) + e], scale_log2, -m_use));
-        psum += pv;
-        pt[e] = (_Float16)pv;
-      }
-      const int rt = 32 * (t >> 1) + 16 * (t & 1);
-#pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        const u32x2 v0 = fmha_tr_read(v + voff0[db & 3] + rt * RB + (db >> 2) * 256);
-        const u32x2 v1 = fmha_tr_read(v + voff1[db & 3] + rt * RB + (db >> 2) * 256);
-        const u32x4 vv = {v0[0], v0[1], v1[0], v1[1]};
-        acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(vv), pt, acc_o[db], 0, 0, 0);
-      }
-    }
-    psum += __shfl_xor(psum, 32);
-    l_run += psum;
-  };
   auto sync_top = [&]() {
     asm volatile("" ::: "memory");
     fmha_wait_vm<0>();
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
   };
-
-  f32x16 sa[NJ], sb[NJ];
-  if (nkb > 0) {
-    copy_block(Kp, k_ss, ksrc, kbuf, 0);
-    copy_block(Vp, v_ss, vsrc, vbuf, 0);
-    if (nkb > 1) copy_block(Kp, k_ss, ksrc, kbuf, 1);
-    sync_top();
-    scores(sa, 0);
-  }
-  // iteration kb: K(kb+1), V(kb) resident; copy K(kb+2), V(kb+1); S(kb+1) || max(kb); exp + PV(kb).
-  // The scores of a block past the end read a stale K slot and are never used (unconditional so
-  // the MFMAs and the max share one scheduling region).
-  auto iter = [&](f32x16* cur, f32x16* nxt, int kb) {
-    sync_top();
-    if (kb + 2 < nkb) copy_block(Kp, k_ss, ksrc, kbuf, kb + 2);
-    if (kb + 1 < nkb) copy_block(Vp, v_ss, vsrc, vbuf, kb + 1);
-    scores(nxt, kb + 1);
-    const float mx = softmax_max(cur, kb);
-    if constexpr (SG) {
+  // exponentials e0..e1-1 of block row s into pt, summed into psum in order; the sum starts at
+  // element 0 (0 + p == p exactly for p >= 0, and a sum that starts from a zero constant was
+  // miscompiled here: the constant's register was reused inside the loop)
+  auto exps = [&](const f32x16& s, float m_use, f16x8 (&pt)[2], float& psum, int e0, int e1) {
 #pragma unroll
-      for (int i = 0; i < NJ * DS; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);  // MFMA
-        __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0);  // LDS read
-        __builtin_amdgcn_sched_group_barrier(0x0002, 2, 0);  // VALU
-      }
+    for (int e = e0; e < e1; ++e) {
+      const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s[e], scale_log2, -m_use));
+      psum = e == 0 ? pv : psum + pv;
+      pt[e >> 3][e & 7] = (_Float16)pv;
     }
-    move_ref(mx);
-    exp_pv(cur, kb);
-    if constexpr (SG) {
+  };
+
+  f32x16 sa, sb;
+  if (nkb > 0) {
+    copy_block(Kp, k_ss, ksrc, k0s, 0);
+    copy_block(Vp, v_ss, vsrc, v0s, 0);
+    if (nkb > 1) copy_block(Kp, k_ss, ksrc, k1s, 1);
+    sync_top();
 #pragma unroll
-      for (int i = 0; i < 2 * NJ * DB; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);  // MFMA
-        __builtin_amdgcn_sched_group_barrier(0x0100, 2, 0);  // LDS read
-        __builtin_amdgcn_sched_group_barrier(0x0002, 3, 0);  // VALU
-        __builtin_amdgcn_sched_group_barrier(0x0400, 1, 0);  // transcendental
+    for (int r = 0; r < 16; ++r) sa[r] = 0.f;
+#pragma unroll
+    for (int st = 0; st < DS; ++st) {
+      const f16x8 kf = *reinterpret_cast<const f16x8*>(k0s + koff[st & 7] + (st >> 3) * 256);
+      sa = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[st], sa, 0, 0, 0);
+    }
+  }
+  // iteration kb (parity P = kb % 2): K(kb+1) in slot 1-P and V(kb) in slot P are resident;
+  // copy K(kb+2) -> slot P, V(kb+1) -> slot 1-P; S(kb+1) = K(kb+1).Q^T || softmax of S(kb);
+  // O += V(kb)^T . P(kb)^T.  The scores of a block past the end read a stale slot and are
+  // never used.
+  auto iter4 = [&](auto par, f32x16& cur, f32x16& nxt, int kb) {
+    constexpr int P = decltype(par)::value;
+    sync_top();
+    if (kb + 2 < nkb) copy_block(Kp, k_ss, ksrc, kslot(IC<P>{}), kb + 2);
+    if (kb + 1 < nkb) copy_block(Vp, v_ss, vsrc, vslot(IC<1 - P>{}), kb + 1);
+    const char* const kr = kslot(IC<1 - P>{});
+    const char* const vr = vslot(IC<P>{});
+    // mask of the current block (the last blocks only; one uniform branch): key c of this
+    // lane's half is hidden iff c > lim
+    const int j0 = kb * BKV2;
+    if ((j0 + BKV2 > Sk) || (CAUSAL && j0 + BKV2 - 1 > q0 + off)) {
+      const int lim = (CAUSAL ? min(Sk - 1, qi + off) : Sk - 1) - j0 - 4 * hl;
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        cur[r] = (8 * (r >> 2) + (r & 3)) > lim ? -__builtin_inff() : cur[r];
+    }
+    const float m_use0 = (m_run == -__builtin_inff()) ? 0.f : m_run;
+    f16x8 kf[DS];
+    u32x2 vp[DS][2];  // V pair i: PV step i / DB, d block i % DB
+    f16x8 pt[2];
+    float mx = -__builtin_inff(), mxs = 0.f, psum;
+#pragma unroll
+    for (int st = 0; st < KP; ++st)
+      kf[st] = *reinterpret_cast<const f16x8*>(kr + koff[st & 7] + (st >> 3) * 256);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) nxt[r] = 0.f;
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int c = 0; c < DS; ++c) {
+      nxt = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[c], qf[c], nxt, 0, 0, 0);
+      if (c + KP < DS)
+        kf[c + KP] =
+            *reinterpret_cast<const f16x8*>(kr + koff[(c + KP) & 7] + ((c + KP) >> 3) * 256);
+      {
+        const int tt = c / DB, db = c % DB;
+        vp[c][0] = fmha_tr_read(vr + voff0[db & 3] + 16 * tt * RB + (db >> 2) * 256);
+        vp[c][1] = fmha_tr_read(vr + voff1[db & 3] + 16 * tt * RB + (db >> 2) * 256);
       }
+      if (c == 2) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, cur[r]);
+      } else if (c == 3) {
+        mxs = fmaxf(mx, __shfl_xor(mx, 32)) * scale_log2;
+      } else {
+        exps(cur, m_use0, pt, psum, 16 * (c - 4) / NX, 16 * (c - 3) / NX);
+        // keep the slice in this chunk: otherwise the speculative exponentials are sunk past
+        // the branch below, out of the matrix pipe's shadow
+        asm volatile("" : "+v"(psum), "+v"(pt[0]), "+v"(pt[1]));
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (__builtin_amdgcn_ballot_w64(!(mxs - m_run <= FMHA_TAU)) != 0) {
+      const float m_new = fmaxf(m_run, mxs);
+      const float alpha =
+          (m_new == -__builtin_inff()) ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
+      l_run *= alpha;
+      m_run = m_new;
+      // in place in the accumulator registers (a plain multiply makes the register allocator
+      // keep a VGPR copy of all of O across the loop for this rare branch)
+#pragma unroll
+      for (int i = 0; i < DB; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float x = acc_o[i][r], tmp;
+          asm volatile(
+              "v_accvgpr_read_b32 %1, %0\n\tv_mul_f32 %1, %1, %2\n\tv_accvgpr_write_b32 %0, %1"
+              : "+a"(x), "=&v"(tmp)
+              : "v"(alpha));
+          acc_o[i][r] = x;
+        }
+      exps(cur, (m_run == -__builtin_inff()) ? 0.f : m_run, pt, psum, 0, 16);
+    }
+    l_run += psum + __shfl_xor(psum, 32);
+#pragma unroll
+    for (int i = 0; i < DS; ++i) {
+      const u32x4 vv = {vp[i][0][0], vp[i][0][1], vp[i][1][0], vp[i][1][1]};
+      acc_o[i % DB] =
+          __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(vv), pt[i / DB], acc_o[i % DB], 0, 0, 0);
     }
   };
   int kb = 0;
   for (; kb + 1 < nkb; kb += 2) {
-    iter(sa, sb, kb);
-    iter(sb, sa, kb + 1);
+    iter4(IC<0>{}, sa, sb, kb);
+    iter4(IC<1>{}, sb, sa, kb + 1);
   }
-  if (kb < nkb) iter(sa, sb, kb);
+  if (kb < nkb) iter4(IC<0>{}, sa, sb, kb);
 
   if (qi < Sq) {
     const float inv = l_run > 0.f ? 1.f / l_run : 0.f;

@@ -313,8 +313,8 @@ def test_counter_step_attribution_and_figures(tmp_path):
     rows += [("at::native::normal", {"FETCH_SIZE": 1.0}, 0, 10)]
     for k in range(3):  # shape 1: three launches, the middle one the median
         rows.append((ours, {"FETCH_SIZE": 1000.0 + k, "WRITE_SIZE": 500.0,
-                            "GRBM_GUI_ACTIVE": 8 * 2000.0,
-                            "SQ_VALU_MFMA_BUSY_CYCLES": 0.5 * 2000 * 1024}, 0, 1000))
+                            "GRBM_GUI_ACTIVE": 8 * 400000.0,
+                            "SQ_VALU_MFMA_BUSY_CYCLES": 0.5 * 400000 * 1024}, 0, 200000))
     rows.append(("at::native::normal", {"FETCH_SIZE": 1.0}, 0, 10))
     rows += [(ours, {"FETCH_SIZE": 10.0, "WRITE_SIZE": 1.0}, 0, 10)] * 3
     path = tmp_path / "c.csv"
@@ -331,7 +331,23 @@ def test_counter_step_attribution_and_figures(tmp_path):
     assert fig["fetch_bytes"] == 1001 * 1024 * 2.0 and fig["write_bytes"] == 500 * 1024
     assert abs(fig["traffic_over_algorithmic"] - 1.0) < 1e-12
     assert abs(fig["mfma_util"] - 0.5) < 1e-12
-    assert abs(fig["sclk_ghz"] - 2.0) < 1e-12   # 2000 cycles per XCD in 1000 ns
+    assert abs(fig["sclk_ghz"] - 2.0) < 1e-12   # 400k cycles per XCD in 200 us
+    # busy half the cycles at 2.0 GHz = 2.0 / 2.4 x 0.5 of the spec-clock matrix throughput
+    assert abs(fig["mfma_util_spec_clock"] - 0.5 * 2.0 / 2.4) < 1e-12
+    # a short dispatch: the profiler's fixed stretch in GRBM_GUI_ACTIVE would dominate its clock
+    short = C.derive({"GRBM_GUI_ACTIVE": 8 * 30000.0, "SQ_VALU_MFMA_BUSY_CYCLES": 1024 * 1000.0,
+                      "_duration_ns": 5000.0}, sc)
+    assert "sclk_ghz" not in short and "mfma_util" not in short
+    assert abs(short["mfma_util_spec_clock"] - 1000.0 / (5000 * 2.4)) < 1e-12
+    # a split-K launch is two dispatches (main kernel, reduction): summed per launch
+    two = [dict(id=i, kernel=ours, grid=1, start=0, end=100 * (i + 1),
+                counters={"FETCH_SIZE": float(10 * (i % 2) + 1)}) for i in range(6)]
+    m2 = C.medians(two, per_launch=2)
+    assert m2["FETCH_SIZE"] == 12.0 and m2["_duration_ns"] == 700
+    # a launch whose kernels differ from the first launch's means the grouping slipped
+    two[3] = dict(two[3], kernel="tempo::gen::k_splitk_reduce<8>")
+    with pytest.raises(RuntimeError):
+        C.medians(two, per_launch=2)
     # a pass that ran fewer launches than it declared is an error, not a silent shift
     import pytest as _pt
 
