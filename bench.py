@@ -14,7 +14,8 @@ the reference's kernels/shipped/gemm_fp16/sm_70/ship_probe.cu:70-79).
 Extra fields of the one JSON line:
   roofline      the C1 kernel against the fp16 dense MFMA peak; `achieved` from HIP events on
                 the launch stream; `traffic` (HBM bytes per launch) from the committed rocprofv3
-                --pmc summary profiles/gemm_fp16_c1_traffic.txt when present, else null.
+                --pmc summary profiles/counters_gemm_fp16_configs.md (its C1 "bytes" line) when
+                present, else null.
   settle        clock settling before warm-up: back-to-back C1 launches in timed batches of 20
                 until two batches agree within 2 % (the engine clock ramps over the first few
                 hundred ms of load); `warmup` and `steps` keep their meaning after it.
@@ -42,7 +43,7 @@ sys.path.insert(0, HERE)
 METRIC = ("GEMM TFLOP/s & % fp16 MFMA peak (prefill); HBM GB/s & % peak (decode M≤32)")
 PEAK_FP16_TFLOPS = 2516.6   # 256 CUs x 2.4 GHz x 4096 flop/clk (AMD dense fp16 figure)
 PEAK_HBM_GBPS = 8000.0      # MI355X HBM3E
-TRAFFIC_FILE = os.path.join(HERE, "profiles", "gemm_fp16_c1_traffic.txt")
+TRAFFIC_FILE = os.path.join(HERE, "profiles", "counters_gemm_fp16_configs.md")
 
 C1 = dict(M=4096, N=15360, K=3840)
 SEED_A, SEED_B = 11, 77
@@ -96,9 +97,10 @@ def read_traffic():
     if not os.path.exists(TRAFFIC_FILE):
         return None
     with open(TRAFFIC_FILE, encoding="utf-8") as f:
-        for line in f:
-            if line.startswith("traffic_bytes_per_launch:"):
-                return int(float(line.split(":", 1)[1]))
+        for line in f:  # "bytes M,N,K,fmt: fetch F write W traffic T algorithmic A"
+            w = line.split()
+            if w[:2] == ["bytes", "%d,%d,%d,0:" % (C1["M"], C1["N"], C1["K"])]:
+                return int(w[w.index("traffic") + 1])
     return None
 
 

@@ -30,7 +30,8 @@ LADDER = [
     (16, 12288, "l1r1n4d3", "line", dict(MB=1, R=1, D=3, SN=4, W=2048)),
     (16, 0, "l1r1d4", "line", dict(MB=1, R=1, D=4, W=2048)),
     (16, 0, "s16r1u4", "stream", dict(MB=1, R=1, U=4, A=0)),
-    (32, 12288, "l2r1n4d3", "line", dict(MB=2, R=1, D=3, SN=4, W=2048)),
+    # four ring stages (1.08-1.12x three at M = 24-32, N = 12288-15360)
+    (32, 12288, "l2r1n4d4", "line", dict(MB=2, R=1, D=4, SN=4, W=2048)),
     (32, 0, "l2r1d4", "line", dict(MB=2, R=1, D=4, W=2048)),
     (32, 0, "s32r1u4", "stream", dict(MB=2, R=1, U=4, A=0)),
     (64, 12288, "l4r1n4d3", "line", dict(MB=4, R=1, D=3, SN=4, W=2048)),

@@ -75,6 +75,8 @@ def condition(sel, kind, p, m_max, n_min=0, gate_up=False):
             fit += " && p.N < %d" % p["NMAX"]
         if "KMIN" in p:
             fit += " && p.K >= %d" % p["KMIN"]
+        if "KMAX" in p:
+            fit += " && p.K < %d" % p["KMAX"]
     else:
         fit = "(p.N %% %d) == 0 && (p.K %% %d) == 0" % (p["BN"], p["BK"])
         if "NMAX" in p:

@@ -16,6 +16,9 @@ FORMATS = (1, 2)
 # holds (M, N) -- M <= M_max and N >= N_min -- whose weight format is listed (params "fmts";
 # absent = both) and whose kernel fits the shape is taken.
 LADDER = [
+    # M = 1 on N = 4096..6144, int8: five ring stages and two slab waves per activation ring
+    # (1.06-1.14x l0r1d4 at N = 5120; 0.78-0.89x at N = 1024 and 7168; uint8 within 2 %)
+    (1, 4096, "l0r1n2d5", "line", dict(MB=0, R=1, D=5, SN=2, W=1024, NMAX=6145, fmts=(1,))),
     (1, 0, "l0r1d4", "line", dict(MB=0, R=1, D=4, W=2048)),
     (16, 12288, "l1r1n4d3", "line", dict(MB=1, R=1, D=3, SN=4, W=2048)),
     (16, 0, "l1r1n2d4", "line", dict(MB=1, R=1, D=4, SN=2, W=2048)),
@@ -34,6 +37,11 @@ LADDER = [
      dict(BM=128, BN=256, BK=64, WM=1, WN=4, STAGES=3, GROUP=8, XCD=1, RSP=8, SW=256, MINKT=8,
           NMAX=12288, KMIN=12288)),
     (64, 0, "l4r1n2d3", "line", dict(MB=4, R=1, D=3, SN=2, W=2048)),
+    # 64 < M <= 128, N <= 6144 and K < 8192: 128 x 128 tiles (2 x 2 waves of 64 x 64), four
+    # stages (1.11-1.32x the 128 x 256 row below at N = 1024-6144, both formats)
+    (128, 0, "i8x128x128s4w256", "ilv8",
+     dict(BM=128, BN=128, BK=64, WM=2, WN=2, STAGES=4, GROUP=16, XCD=0, RSP=8, SW=256, MINKT=8,
+          NMAX=6145, KMAX=8192)),
     # 64 < M <= 128: 128 x 256 tiles (one tile row), split-K where the column tiles are too few
     # to fill the part (the variant driver's rows: 1.5-2.9x the line and register-staged rows)
     (128, 0, "i8x128x256s3w256", "ilv8",
@@ -100,9 +108,10 @@ def ilv_ld_max(p):
 
 
 def _fits(kind, p, M, N, K):
-    if kind == "ilv8":  # a scale group of 128 k is two k-tiles; NMAX / KMIN (optional) bounds
+    if kind == "ilv8":  # a scale group of 128 k is two k-tiles; NMAX / KMIN / KMAX (optional)
         return (N % p["BN"] == 0 and K % 128 == 0 and K <= ilv_ld_max(p)
-                and N < p.get("NMAX", 1 << 30) and K >= p.get("KMIN", 0))
+                and N < p.get("NMAX", 1 << 30) and K >= p.get("KMIN", 0)
+                and K < p.get("KMAX", 1 << 30))
     if kind == "line":  # NMAX (optional): the row holds narrower N only
         return (N % (STREAM_N_ROWS * p["R"] * p.get("SN", 1)) == 0 and K % LINE_K_STEP == 0
                 and K <= LINE_K_MAX and N < p.get("NMAX", 1 << 30))

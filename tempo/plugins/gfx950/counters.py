@@ -21,6 +21,9 @@ How the raw numbers become the figures the measure stage reports (per dispatch):
     the spec clock only.
   * MFMA utilisation at the spec clock = SQ_VALU_MFMA_BUSY_CYCLES / (duration x SPEC_GHZ x SIMDs):
     the share of the spec-peak matrix throughput the dispatch used, whatever clock it ran at.
+  * LDS utilisation = SQ_LDS_IDX_ACTIVE / (GRBM_GUI_ACTIVE / XCDs x CUs) and bank conflicts per
+    access = SQ_LDS_BANK_CONFLICT / (SQ_LDS_IDX_ACTIVE - SQ_LDS_BANK_CONFLICT): rocprofv3's own
+    expressions (rocprofv3 -L prints them).
 """
 from __future__ import annotations
 
@@ -53,6 +56,7 @@ GROUPS = {
 
 COPY_KERNEL = "__amd_rocclr_copyBuffer"
 XCDS = 8
+CUS = 256
 SIMDS = 1024  # 256 CUs x 4 SIMDs
 SPEC_GHZ = 2.4  # the engine clock the published peaks assume
 MIN_CLOCK_NS = 100_000
@@ -197,12 +201,16 @@ def derive(per_counter: dict, scales: dict, algorithmic_bytes: float = 0.0) -> d
     if gui:
         cycles = gui / XCDS
         out["gui_cycles"] = cycles
-        if "SQ_LDS_BANK_CONFLICT" in c:
-            out["lds_bank_conflict_per_cu_cycle"] = c["SQ_LDS_BANK_CONFLICT"] / (cycles * 256)
         if dur >= MIN_CLOCK_NS:
             out["sclk_ghz"] = cycles / dur
             if "SQ_VALU_MFMA_BUSY_CYCLES" in c:
                 out["mfma_util"] = c["SQ_VALU_MFMA_BUSY_CYCLES"] / (cycles * SIMDS)
+            if "SQ_LDS_IDX_ACTIVE" in c:  # rocprofv3's LDS utilisation expression
+                out["lds_util"] = c["SQ_LDS_IDX_ACTIVE"] / (cycles * CUS)
+    if "SQ_LDS_BANK_CONFLICT" in c and c.get("SQ_LDS_IDX_ACTIVE", 0) > c["SQ_LDS_BANK_CONFLICT"]:
+        # conflict cycles per conflict-free LDS cycle (rocprofv3's bank-conflict expression)
+        out["lds_conflicts_per_access"] = c["SQ_LDS_BANK_CONFLICT"] / (
+            c["SQ_LDS_IDX_ACTIVE"] - c["SQ_LDS_BANK_CONFLICT"])
     for k in ("SQ_INSTS_VALU_MFMA_MOPS_F16", "SQ_INSTS_LDS", "SQ_LDS_IDX_ACTIVE",
               "SQ_INSTS_VMEM_RD", "SQ_INSTS_VMEM_WR", "TA_BUSY_avr", "SQ_LDS_BANK_CONFLICT"):
         if k in c:

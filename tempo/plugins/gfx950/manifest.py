@@ -74,7 +74,7 @@ def hyper_params(kind, p, fmt, epi=0):
     same kernel, named the way space.variants() names it."""
     pk = {"stream": "stream", "mfma": "reg", "dma": "dma", "shared": "shared", "ilv": "ilv",
           "ilv8": "ilv8", "line": "line"}[kind]
-    params = {k: v for k, v in p.items() if k not in ("fmts", "NMAX", "KMIN")}
+    params = {k: v for k, v in p.items() if k not in ("fmts", "NMAX", "KMIN", "KMAX")}
     params["kind"] = pk
     if pk == "shared":
         params.setdefault("TPB", 1024)
@@ -291,6 +291,8 @@ def make(op, rows_files=(), counter_files=()):
                 fit += " and N < %d" % p["NMAX"]
             if "KMIN" in p:
                 fit += " and K >= %d" % p["KMIN"]
+            if "KMAX" in p:
+                fit += " and K < %d" % p["KMAX"]
             if p.get("SW"):
                 fit += "; split-K: at most %d workgroups, >= %d k-tiles per split" % (
                     p["SW"], p.get("MINKT", 0))

@@ -223,6 +223,50 @@ def counters(op: str, out: str, groups, quick: bool = False) -> str:
     return path
 
 
+def render_counters(path: str) -> str:
+    """A counter step's JSON (counters()) as a markdown table, one row per configuration shape:
+    per-launch duration under counters, HBM bytes against the algorithmic bytes, MFMA
+    utilisation at the spec clock (and, for launches of 100 us or more, against the measured
+    engine clock, with that clock and the LDS utilisation), LDS bank conflicts per access."""
+    from tempo.plugins.gfx950.counters import CUS, MIN_CLOCK_NS
+
+    with open(path) as f:
+        got = json.load(f)
+    lines = ["| M | N | K | fmt | route | disp./launch | us (pmc) | HBM MB | traffic / alg. "
+             "| MFMA util (spec clk) | MFMA util (meas. clk) | sclk GHz | LDS util "
+             "| LDS confl./access |", "|" + "---|" * 14]
+
+    def f(x, fmt):
+        return "-" if x is None else fmt % x
+
+    for r in got["rows"]:
+        c = r["counters"]
+        long_ = c.get("pmc_duration_us", 0) * 1e3 >= MIN_CLOCK_NS
+        lds = c.get("lds_util")
+        if lds is None and long_ and c.get("gui_cycles") and "SQ_LDS_IDX_ACTIVE" in c:
+            lds = c["SQ_LDS_IDX_ACTIVE"] / (c["gui_cycles"] * CUS)
+        confl = c.get("lds_conflicts_per_access")
+        if confl is None and c.get("SQ_LDS_IDX_ACTIVE", 0) > c.get("SQ_LDS_BANK_CONFLICT", 0) > 0:
+            confl = c["SQ_LDS_BANK_CONFLICT"] / (c["SQ_LDS_IDX_ACTIVE"] - c["SQ_LDS_BANK_CONFLICT"])
+        elif confl is None and "SQ_LDS_BANK_CONFLICT" in c:
+            confl = 0.0
+        lines.append("| %d | %d | %d | %d | %s | %d | %s | %s | %s | %s | %s | %s | %s | %s |" % (
+            r["M"], r["N"], r["K"], r["fmt"], r.get("route") or "-",
+            r.get("dispatches_per_launch", 1), f(c.get("pmc_duration_us"), "%.1f"),
+            f(c.get("hbm_bytes", 0) / 1e6 if "hbm_bytes" in c else None, "%.1f"),
+            f(c.get("traffic_over_algorithmic"), "%.2f"), f(c.get("mfma_util_spec_clock"), "%.3f"),
+            f(c.get("mfma_util") if long_ else None, "%.3f"),
+            f(c.get("sclk_ghz") if long_ else None, "%.2f"), f(lds, "%.3f"), f(confl, "%.3f")))
+    lines += ["", "Exact HBM bytes per launch (M,N,K,fmt: fetch, write, total, algorithmic):", ""]
+    for r in got["rows"]:
+        c = r["counters"]
+        if "hbm_bytes" in c:
+            lines.append("    bytes %d,%d,%d,%d: fetch %d write %d traffic %d algorithmic %d" % (
+                r["M"], r["N"], r["K"], r["fmt"], round(c["fetch_bytes"]), round(c["write_bytes"]),
+                round(c["hbm_bytes"]), r["algorithmic_bytes"]))
+    return "\n".join(lines) + "\n"
+
+
 def measure(op: str, quick: bool = False):
     import torch
 
@@ -361,7 +405,12 @@ def main():
     ap.add_argument("--groups", nargs="*", default=["hbm_read", "hbm_write", "mfma"])
     ap.add_argument("--counter-pass", metavar="SEGFILE",
                     help="(internal) the program a counter pass profiles")
+    ap.add_argument("--render", metavar="COUNTERS_JSON",
+                    help="print a counter step's JSON as a markdown table (no GPU)")
     a = ap.parse_args()
+    if a.render:
+        sys.stdout.write(render_counters(a.render))
+        return 0
     os.makedirs(a.out, exist_ok=True)
     if a.counter_pass:
         return counter_pass(a.op, a.counter_pass, a.quick)

@@ -2,9 +2,9 @@
 // C = A . deq(W)^T.  Uses the tile machinery of gemm_mfma/kernel.hip (lds_chunk, tile_of,
 // s_wait_vm, buf_lds16, buf_lds_n) and the dequantisation of common/cdna4.h.
 // ============================================================================================
-// k_gemm_ilv8 has the structure of k_gemm_ilv -- 4 waves, 128 x 128 wave tiles on
-// v_mfma_f32_16x16x32_f16, chunked substeps fenced by sched_barrier, buffer LDS-DMA copies, the C
-// tile written out through LDS -- with the weight tile travelling as bytes:
+// k_gemm_ilv8 has the structure of k_gemm_ilv -- 4 waves (wave tiles of 128 x 128, 128 x 64 or
+// 64 x 64) on v_mfma_f32_16x16x32_f16, chunked substeps fenced by sched_barrier, buffer LDS-DMA
+// copies, the C tile written out through LDS -- with the weight tile travelling as bytes:
 //   * A stage holds the fp16 A tile (BM x 64, SWZ2 chunk swizzle of its 128-byte rows), the weight
 //     tile (BN x 64 bytes; 16-byte chunk c of row r stored at chunk c ^ ((r / 4) % 4), which makes
 //     the 8-byte fragment reads below conflict-free) and, fmt 2, the tile's zero-points and
@@ -14,7 +14,7 @@
 //   * Fragments: A as in k_gemm_ilv (ds_read_b128); a weight fragment (16 rows x 32 k) is one
 //     8-byte read per lane.  The MFMAs of a substep run block column by block column, and each
 //     column's 8 weight bytes are dequantised in registers (cdna4.h dequant8: bit-exact
-//     fp16_rn((q - z) s)) one chunk before its 8 MFMAs -- so at most two dequantised fragments
+//     fp16_rn((q - z) s)) one chunk before its TM MFMAs -- so at most two dequantised fragments
 //     are live, and the register budget (256 AGPR accumulators + 256 VGPRs) is not exceeded.
 //   * fmt 1 (int8, per-channel scale): the wave's 8 row scales are copied into LDS once and held
 //     in registers.  fmt 2 (uint8, group-128 zero-point and scale): every stage carries its tile's
@@ -48,18 +48,23 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv8(
   constexpr int B_BLK = BN / 16 / NW;         // W copies (16 rows x 64 bytes each) per wave
   constexpr int M_BLK = BFMT == 2 ? 2 : 0;    // fmt 2: one zero-point and one scale copy
   constexpr int L = A_BLK + B_BLK + M_BLK;    // copies per wave per k-tile
-  constexpr int ABYTES = BM * BK * 2, BBYTES = BN * BK, MBYTES = BFMT == 2 ? BN * 8 : 0;
+  // metadata slots: every wave copies 64 rows (one byte / half per lane, 4 bytes apart); with
+  // BN < 64 NW the waves past BN / 64 copy rows (wave % (BN / 64)) * 64 + lane again into slots
+  // nobody reads, so the copy count (and the vmcnt arithmetic) is the same in every wave
+  constexpr int MROWS = BN > 64 * NW ? BN : 64 * NW;
+  constexpr int ABYTES = BM * BK * 2, BBYTES = BN * BK, MBYTES = BFMT == 2 ? MROWS * 8 : 0;
   constexpr int SBYTES = ABYTES + BBYTES + MBYTES;  // one stage
   constexpr int NMF = TM * TN;
   constexpr int RSPAN = RSP > 0 && RSP < NMF / 4 ? RSP : NMF / 4;
   static_assert(BK == 64 && KS == 2, "64-k tiles (a 128-k scale group is two of them)");
-  static_assert(BM % (RPB * NW) == 0 && BN % (16 * NW) == 0 && (BFMT != 2 || BN == 64 * NW), "copy blocks");
+  static_assert(BM % (RPB * NW) == 0 && BN % (16 * NW) == 0 && BN % 64 == 0 && (64 * NW) % BN == 0,
+                "copy blocks");
   static_assert(STAGES >= 2 && (STAGES - 1) * L < 64, "stages / vmcnt range");
   static_assert((16 / R256) % CPR == 0 && (NW * RPB / R256) % CPR == 0, "swizzle periods");
   static_assert(BFMT == 1 || BFMT == 2, "int8 per-channel or uint8 group-128");
 
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * SBYTES + (BFMT == 1 ? BN * 4 : 0)];
-  static_assert(STAGES * SBYTES + (BFMT == 1 ? BN * 4 : 0) <= 160 * 1024, "LDS");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * SBYTES + (BFMT == 1 ? MROWS * 4 : 0)];
+  static_assert(STAGES * SBYTES + (BFMT == 1 ? MROWS * 4 : 0) <= 160 * 1024, "LDS");
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -102,7 +107,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv8(
   // one half per lane at a 4-byte lane stride
   const uint8_t* panelZ = zero + (BFMT == 2 ? (long)n0 * ng : 0);
   const _Float16* panelS = scale + (BFMT == 2 ? (long)n0 * ng : (long)n0);
-  const int mrow = wave * 64 + lane;
+  const int mrow = (wave % (BN / 64)) * 64 + lane;
   auto dma = [&](int kt, int d) {
     const int ks = kbase + min(kt, NT - 1);
     uint8_t* st = smem + (kt % STAGES) * SBYTES;
@@ -115,7 +120,8 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv8(
       if (d == A_BLK + B_BLK)
         buf_lds_n<1>(panelZ, BN * ng, st + ABYTES + BBYTES + wave * 256, mrow * ng, g);
       else
-        buf_lds_n<2>(panelS, BN * ng * 2, st + ABYTES + BBYTES + BN * 4 + wave * 256, mrow * ng * 2, g * 2);
+        buf_lds_n<2>(panelS, BN * ng * 2, st + ABYTES + BBYTES + MROWS * 4 + wave * 256, mrow * ng * 2,
+                     g * 2);
     }
   };
 
@@ -148,7 +154,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv8(
   }
   auto read_meta = [&](const uint8_t* st, _Float16 (&bi)[TN], _Float16 (&s)[TN], int j) {
     bi[j] = (_Float16)(1024.0f + (float)st[ABYTES + BBYTES + rowm + j * 64]);
-    s[j] = *reinterpret_cast<const _Float16*>(st + ABYTES + BBYTES + BN * 4 + rowm + j * 64);
+    s[j] = *reinterpret_cast<const _Float16*>(st + ABYTES + BBYTES + MROWS * 4 + rowm + j * 64);
   };
   auto deq = [&](const u32x2& w, int j) -> f16x8 {
     const uint32_t x0 = BFMT == 1 ? w[0] ^ 0x80808080u : w[0];
@@ -164,7 +170,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv8(
   constexpr int NRD = TM + TN + (BFMT == 2 ? 2 * TN : 0);  // reads of a substep with metadata
   constexpr int CH = NMF / 4;                              // chunks of 4 MFMAs
   constexpr int CPJ = CH / TN;                             // chunks per block column
-  static_assert(CH % TN == 0 && CPJ >= 2 && RSPAN <= CH && L <= 2 * CH, "substep chunking");
+  static_assert(CH % TN == 0 && CPJ >= 1 && RSPAN <= CH && L <= 2 * CH, "substep chunking");
   auto substep = [&](auto bufc, auto dmac, auto metac, int rkt, int rks, int dkt) {
     constexpr int bb = decltype(bufc)::value;
     constexpr bool DMA = decltype(dmac)::value;

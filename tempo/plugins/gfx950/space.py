@@ -43,9 +43,9 @@ AXES = (
 DOMAINS = {
     "ilv": dict(BM=(64, 128, 256), BN=(128, 192, 256), BK=(32, 64), STAGES=(2, 3, 4),
                 GROUP=(4, 8, 16), XCD=(0, 1), WAVES=((2, 2), (2, 4), (4, 2), (1, 4)),
-                RSP=(0, 8, 12), SW=(0, 256, 512)),
-    "ilv8": dict(TILES=((256, 256, 2, 2), (128, 256, 1, 4)), STAGES=(3, 4), GROUP=(4, 8, 16),
-                 XCD=(0, 1), RSP=(4, 8, 12), SW=(0, 256, 512)),
+                RSP=(0, 8, 12), SW=(0, 128, 256, 512)),
+    "ilv8": dict(TILES=((256, 256, 2, 2), (128, 256, 1, 4), (128, 128, 2, 2)), STAGES=(3, 4),
+                 GROUP=(4, 8, 16), XCD=(0, 1), RSP=(4, 8, 12), SW=(0, 128, 256, 512)),
     "dma": dict(BM=(64, 128, 256), BN=(64, 128, 192, 256), BK=(32, 64), STAGES=(2, 3, 4), SWZ=(0, 1, 2),
                 GROUP=(4, 8, 16), XCD=(0, 1), WAVES=((2, 2), (2, 4), (4, 2), (4, 4)), MS=(16, 32)),
     "reg": dict(BM=(64, 128, 256), BN=(64, 128, 256), BK=(64,), MS=(16, 32), SWZ=(1, 2), GROUP=(8,),
@@ -134,9 +134,10 @@ def lds_bytes(kind: str, p: dict) -> int:
     if kind in ("dma", "ilv"):
         return p["STAGES"] * (p["BM"] + p["BN"]) * p["BK"] * 2
     if kind == "ilv8":  # fp16 A tile, byte weight tile, fmt 2 metadata per stage; fmt 1 scales
-        meta = p["BN"] * 8 if p["BFMT"] == 2 else 0
+        mrows = max(p["BN"], 64 * p["WM"] * p["WN"])  # metadata slots: 64 rows per wave
+        meta = mrows * 8 if p["BFMT"] == 2 else 0
         return (p["STAGES"] * (p["BM"] * p["BK"] * 2 + p["BN"] * p["BK"] + meta)
-                + (p["BN"] * 4 if p["BFMT"] == 1 else 0))
+                + (mrows * 4 if p["BFMT"] == 1 else 0))
     if kind == "reg":
         return 2 * (p["BM"] + p["BN"]) * p["BK"] * 2
     if kind == "ring":
@@ -238,9 +239,10 @@ def legal(kind: str, p: dict, M: int, N: int, K: int):
         return None
     if kind == "ilv8":
         BM, BN, BK, WM, WN = p["BM"], p["BN"], p["BK"], p["WM"], p["WN"]
-        if (BM, BN, BK, WM, WN) not in ((256, 256, 64, 2, 2), (128, 256, 64, 1, 4)):
-            return ("the int8 interleaved kernel takes 256 x 256 (2 x 2 waves) or 128 x 256 "
-                    "(1 x 4 waves) tiles of 64 k: 64 weight rows per wave, >= 128-row wave tiles")
+        if (BM, BN, BK, WM, WN) not in ((256, 256, 64, 2, 2), (128, 256, 64, 1, 4),
+                                        (128, 128, 64, 2, 2)):
+            return ("the int8 interleaved kernel takes 256 x 256 (2 x 2 waves), 128 x 256 "
+                    "(1 x 4 waves) or 128 x 128 (2 x 2 waves) tiles of 64 k")
         if p["BFMT"] not in (1, 2):
             return "weights must be int8 (fmt 1) or uint8 group-128 (fmt 2)"
         if N % BN or K % 128:

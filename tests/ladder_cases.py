@@ -20,7 +20,7 @@ FP16 = [
     ("l1r1n4d3", 8, 15360, 3840),
     ("l1r1d4", 16, 3840, 15360),
     ("s16r1u4", 16, 512, 65792),
-    ("l2r1n4d3", 24, 15360, 3840),
+    ("l2r1n4d4", 24, 15360, 3840),
     ("l2r1d4", 32, 3840, 15360),
     ("s32r1u4", 32, 512, 65792),
     ("l4r1n4d3", 64, 15360, 3840),
@@ -67,6 +67,7 @@ FP16_GATE_UP = [
 
 W8 = {
     1: [
+        ("l0r1n2d5", 1, 5120, 17408),
         ("l0r1d4", 1, 7168, 5120),
         ("l1r1n4d3", 16, 34816, 5120),
         ("l1r1n2d4", 16, 5120, 17408),
@@ -84,6 +85,8 @@ W8 = {
         ("i8x128x256s3w256", 128, 5120, 17408),
         ("i8x128x256s3w256", 128, 34816, 5120),
         ("i8x128x256s3w256", 100, 7168, 5120),
+        ("i8x128x128s4w256", 128, 5120, 5120),
+        ("i8x128x128s4w256", 100, 1024, 5120),
         ("l8r1n2d3", 128, 5152, 5120),
         ("m128x128k64", 256, 5120, 5120),
         ("i8x128x256s3w256", 2048, 1024, 5120),
@@ -109,6 +112,8 @@ W8 = {
         ("i8x128x256s3w256", 128, 5120, 17408),
         ("i8x128x256s3w256", 128, 34816, 5120),
         ("i8x128x256s3w256", 100, 7168, 5120),
+        ("i8x128x128s4w256", 128, 5120, 5120),
+        ("i8x128x128s4w256", 100, 1024, 5120),
         ("l8r1n2d3", 128, 5152, 5120),
         ("m128x128k64", 256, 5120, 5120),
         ("i8x128x256s3w256", 2048, 1024, 5120),

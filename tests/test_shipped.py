@@ -165,7 +165,9 @@ def test_rows_fall_through_when_the_first_row_does_not_fit():
     assert capi.route(1, 32, 34816, 5120) == "l2r1n4d4"
     assert capi.route(2, 32, 34816, 65536 + 256) == "h32r1u4n2"
     assert capi.route(0, 1, 15360, 3840) == "l0r1d3"
-    assert capi.route(1, 1, 5120, 5120) == "l0r1d4"
+    assert capi.route(1, 1, 5120, 5120) == "l0r1n2d5"
+    assert capi.route(2, 1, 5120, 5120) == "l0r1d4"     # the D = 5 row is int8 only
+    assert capi.route(1, 1, 7168, 5120) == "l0r1d4"     # past its N band
     assert capi.route(1, 1, 5120, 65536 + 512) == "s1a_r1u8"
     assert capi.route(1, 1, 5120, 65536 + 256) == "s1a_r1u4"   # K % 512 != 0, K % 256 == 0
     assert capi.route(0, 4096, 15360, 3840) == "i256x256k64w4r8"
