@@ -52,6 +52,11 @@ GROUPS = {
     "l2": ["TCC_HIT_sum", "TCC_MISS_sum"],
     # waves and stalls
     "waves": ["SQ_WAVES", "SQ_WAVE_CYCLES", "SQ_BUSY_CYCLES", "SQ_WAIT_INST_ANY"],
+    # where the wave-cycles go (SQ cycle counters count in units of 4 cycles; ratios to
+    # SQ_WAVE_CYCLES of the waves group are unit-free)
+    "stall": ["SQ_WAIT_ANY", "SQ_WAIT_INST_LDS", "SQ_ACTIVE_INST_ANY", "SQ_ACTIVE_INST_LDS",
+              "SQ_ACTIVE_INST_VALU", "SQ_ACTIVE_INST_VMEM", "SQ_ACTIVE_INST_SCA", "SQ_INSTS_VALU",
+              "GRBM_GUI_ACTIVE"],
 }
 
 COPY_KERNEL = "__amd_rocclr_copyBuffer"
@@ -211,10 +216,9 @@ def derive(per_counter: dict, scales: dict, algorithmic_bytes: float = 0.0) -> d
         # conflict cycles per conflict-free LDS cycle (rocprofv3's bank-conflict expression)
         out["lds_conflicts_per_access"] = c["SQ_LDS_BANK_CONFLICT"] / (
             c["SQ_LDS_IDX_ACTIVE"] - c["SQ_LDS_BANK_CONFLICT"])
-    for k in ("SQ_INSTS_VALU_MFMA_MOPS_F16", "SQ_INSTS_LDS", "SQ_LDS_IDX_ACTIVE",
-              "SQ_INSTS_VMEM_RD", "SQ_INSTS_VMEM_WR", "TA_BUSY_avr", "SQ_LDS_BANK_CONFLICT"):
-        if k in c:
-            out[k] = c[k]
+    for k, v in c.items():  # the raw per-launch medians as well
+        if not k.startswith("_"):
+            out[k] = v
     if "SQ_INSTS_VALU_MFMA_MOPS_F16" in c:
         out["mfma_flops"] = c["SQ_INSTS_VALU_MFMA_MOPS_F16"] * 512.0
     return out

@@ -45,7 +45,7 @@ ROUNDS = 5
 SHAPES_FP16 = [(4096, 15360, 3840)] + [(M, N, K) for (N, K) in ((15360, 3840), (3840, 15360))
                                         for M in (1, 8, 16, 32, 64, 128, 256)]
 NK_W8 = [(7168, 5120), (5120, 6144), (34816, 5120), (5120, 17408), (1024, 5120), (5120, 5120)]
-SHAPES_W8 = [(M, N, K) for (N, K) in NK_W8 for M in (1, 16, 128, 2048)]
+SHAPES_W8 = [(M, N, K) for (N, K) in NK_W8 for M in (1, 16, 32, 128, 2048)]
 
 
 def _say(*a):
