@@ -37,6 +37,8 @@ HEAD = """// GENERATED from select.py -- do not edit.  Regenerate with:
 def instantiation(kind, p, epi=0):
     tail = ",%d" % epi if epi else ""
     if kind == "line":
+        if p.get("TL"):
+            tail = ",%d,1" % epi
         return "launch_line<%d,%d,%d,%d,%d%s>" % (p["MB"], p["R"], p["D"], p.get("SN", 1), p["W"],
                                                   tail)
     if kind == "shared":
@@ -55,7 +57,10 @@ def instantiation(kind, p, epi=0):
 
 
 def condition(sel, kind, p, m_max, n_min=0, gate_up=False):
-    if kind == "line":
+    if kind == "line" and p.get("TL"):
+        fit = "(p.N %% %d) == 0 && (p.K %% %d) == 0 && (line_tail_fits<%d,%d,%d,%d>(p))" % (
+            sel.STREAM_N_ROWS * p["R"], sel.LINE_K_STEP, p["MB"], p["R"], p["D"], p["SN"])
+    elif kind == "line":
         sno = p.get("SN", 1) // 2 if gate_up and p.get("SN", 1) >= 2 else p.get("SN", 1)
         fit = "(p.N %% %d) == 0 && (p.K %% %d) == 0 && p.K <= %d" % (
             sel.STREAM_N_ROWS * p["R"] * sno, sel.LINE_K_STEP, sel.LINE_K_MAX)

@@ -15,6 +15,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
+
 #include "kernel.hip"
 
 namespace tempo {
@@ -163,29 +165,65 @@ inline bool line_split(int wgs, int SN, int K, int waves, int* S_out, int* chunk
   }
 }
 
+// Tail grid of the line kernel (TL = 1): q whole rounds of SN-slab workgroups, kLineCus per
+// round, then one single-wave workgroup per remaining slab.  It applies when q >= 1, at most one
+// slab per CU remains, and a CU holds its q workgroups and one tail at once (LDS: the launch's
+// size is the larger of the two bodies'; waves: 16).  The ladder's fit predicate calls
+// line_tail_fits, so a row that fits always launches.
+constexpr int kLineCus = 256;  // CUs of the part (MI355X, MI350X)
+template <int MB, int R, int D, int SN>
+inline bool line_tail_grid(const W8A16Params& p, int* nbig, int* grid, size_t* lds) {
+  if (p.N % (16 * R) || p.K % 128 || p.K > 65536) return false;
+  const int slabs = p.N / (16 * R);
+  const int q = slabs / (kLineCus * SN);
+  const int tail = slabs - q * kLineCus * SN;
+  if (q < 1 || tail > kLineCus) return false;
+  const int G = p.K / 128;
+  const size_t L =
+      p.fmt == 1 ? std::max(StreamLine<MB, R, D, 1, 0, SN>::lds(1, G), StreamLine<MB, R, D, 1, 0, 1>::lds(1, G))
+                 : std::max(StreamLine<MB, R, D, 2, 0, SN>::lds(1, G), StreamLine<MB, R, D, 2, 0, 1>::lds(1, G));
+  if ((size_t)(q + 1) * L > 160 * 1024 || (q + 1) * SN > 16) return false;
+  *nbig = q * kLineCus;
+  *grid = q * kLineCus + tail;
+  *lds = L;
+  return true;
+}
+template <int MB, int R, int D, int SN>
+inline bool line_tail_fits(const W8A16Params& p) {
+  int nbig = 0, grid = 0;
+  size_t lds = 0;
+  return line_tail_grid<MB, R, D, SN>(p, &nbig, &grid, &lds);
+}
+
 // The line kernel (whole-line nontemporal weight stream through per-wave LDS rings).  MB = 0:
 // M = 1; MB = 1 / 2: M <= 16 / 32.  SN slab waves of a workgroup share one activation ring.
 // EPI = 1: fused gate/up (p.N the output width; Wq, scale and zero hold 2N rows).
-template <int BFMT, int MB, int R, int D, int SN, int WAVES, int EPI>
+// TL = 1: the tail grid above, one k chunk per slab.
+template <int BFMT, int MB, int R, int D, int SN, int WAVES, int EPI, int TL>
 inline hipError_t launch_line_fmt(const W8A16Params& p, hipStream_t s) {
   using SL = StreamLine<MB, R, D, BFMT, EPI, SN>;
   StreamArgs a = stream_args(p);
   a.up = EPI ? p.N : 0;
   int G = 0;
   size_t lds = 0;
-  const int wgs = p.N / (16 * R * SL::SNO);  // output slabs / per workgroup
+  int wgs = p.N / (16 * R * SL::SNO);  // output slabs / per workgroup
   constexpr int TPB = MB >= 4 ? 512 : 1024;  // many activation blocks: 256 VGPRs per lane
-  if (!line_split<SL>(wgs, SN, p.K, WAVES, &a.S, &a.chunk, &G, &lds, TPB))
+  if constexpr (TL) {
+    static_assert(SN > 1 && EPI == 0, "tail grid: shared activation ring, plain epilogue");
+    if (!line_tail_grid<MB, R, D, SN>(p, &a.nbig, &wgs, &lds)) return hipErrorInvalidConfiguration;
+    G = p.K / 128;
+  } else if (!line_split<SL>(wgs, SN, p.K, WAVES, &a.S, &a.chunk, &G, &lds, TPB)) {
     return hipErrorInvalidConfiguration;
-  hipLaunchKernelGGL((k_stream_line<MB, R, D, BFMT, EPI, SN, TPB>), dim3(wgs),
+  }
+  hipLaunchKernelGGL((k_stream_line<MB, R, D, BFMT, EPI, SN, TPB, TL>), dim3(wgs),
                      dim3(64 * SN * a.S), lds, s, a, G);
   return hipGetLastError();
 }
 
-template <int MB, int R, int D, int SN, int WAVES, int EPI = 0>
+template <int MB, int R, int D, int SN, int WAVES, int EPI = 0, int TL = 0>
 inline hipError_t launch_line(const W8A16Params& p, hipStream_t s) {
-  if (p.fmt == 1) return launch_line_fmt<1, MB, R, D, SN, WAVES, EPI>(p, s);
-  return launch_line_fmt<2, MB, R, D, SN, WAVES, EPI>(p, s);
+  if (p.fmt == 1) return launch_line_fmt<1, MB, R, D, SN, WAVES, EPI, TL>(p, s);
+  return launch_line_fmt<2, MB, R, D, SN, WAVES, EPI, TL>(p, s);
 }
 
 // The interleaved int8 prefill kernel (k_gemm_ilv8) lives in its own translation unit,

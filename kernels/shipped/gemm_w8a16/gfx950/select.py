@@ -20,8 +20,13 @@ LADDER = [
     # (1.06-1.14x l0r1d4 at N = 5120; 0.78-0.89x at N = 1024 and 7168; uint8 within 2 %)
     (1, 4096, "l0r1n2d5", "line", dict(MB=0, R=1, D=5, SN=2, W=1024, NMAX=6145, fmts=(1,))),
     (1, 0, "l0r1d4", "line", dict(MB=0, R=1, D=4, W=2048)),
+    # M <= 16 / 32, wide N: the tail grid -- whole rounds of 4- / 8-slab workgroups (one ring of
+    # activations each) and one single-wave workgroup per remaining slab, so the slabs per CU
+    # differ by at most one (1.10-1.19x / 1.29-1.31x the rows after them at (34816, 5120))
+    (16, 12288, "l1r1n4d2t", "line", dict(MB=1, R=1, D=2, SN=4, W=2048, TL=1)),
     (16, 12288, "l1r1n4d3", "line", dict(MB=1, R=1, D=3, SN=4, W=2048)),
     (16, 0, "l1r1n2d4", "line", dict(MB=1, R=1, D=4, SN=2, W=2048)),
+    (32, 12288, "l2r1n8d2t", "line", dict(MB=2, R=1, D=2, SN=8, W=2048, TL=1)),
     (32, 12288, "l2r1n4d4", "line", dict(MB=2, R=1, D=4, SN=4, W=2048)),
     (32, 0, "l2r1n2d4", "line", dict(MB=2, R=1, D=4, SN=2, W=2048)),
     (1, 0, "s1a_r1u8", "stream", dict(MB=1, R=1, U=8, A=1)),
@@ -87,9 +92,34 @@ STREAM_K_STEP = 64
 STREAM_N_ROWS = 16
 LINE_K_STEP = 128   # k per step of the line kernel (one 128-byte line of an int8 row)
 LINE_K_MAX = 65536  # the line kernel's LDS holds one wave's metadata (fmt 2): bounded k
+LINE_CUS = 256      # CUs of the part: one round of workgroups of the line kernel's tail grid
+LINE_LDS = 160 * 1024
 
 
-def _fits_gate_up(kind, p, M, N, K):
+def _line_lds(p, fmt, K, sn):
+    """LDS of one workgroup of the line kernel with one k chunk, as StreamLine::lds(1, K/128)
+    declares it: sn weight rings (their own activation slots too when sn = 1), the fmt 2
+    metadata of K/128 groups per wave, and (sn > 1) the shared activation ring of D + 1 slots."""
+    wslot, aslot = p["R"] * 2048, (p["MB"] * 16 * 256 if p["MB"] else 256)
+    meta = -(-(p["R"] * 16 * (K // LINE_K_STEP) * 3) // 16) * 16 if fmt == 2 else 0
+    wave = -(-(p["D"] * (wslot + (aslot if sn == 1 else 0)) + meta) // 1024) * 1024
+    act = -(-((p["D"] + 1) * aslot) // 1024) * 1024 if sn > 1 else 0
+    return sn * wave + act
+
+
+def line_tail_fits(p, N, K, fmt):
+    """The tail grid (TL = 1) of the line kernel (launch.h line_tail_grid): q >= 1 whole rounds of
+    SN-slab workgroups, at most one remaining slab per CU, and a CU's q workgroups plus one tail
+    resident together (LDS and 16 waves)."""
+    slabs, rnd = N // (STREAM_N_ROWS * p["R"]), LINE_CUS * p["SN"]
+    q = slabs // rnd
+    if q < 1 or slabs - q * rnd > LINE_CUS or K > LINE_K_MAX:
+        return False
+    lds = max(_line_lds(p, fmt, K, p["SN"]), _line_lds(p, fmt, K, 1))
+    return (q + 1) * lds <= LINE_LDS and (q + 1) * p["SN"] <= 16
+
+
+def _fits_gate_up(kind, p, M, N, K, fmt=1):
     # N is the output width; the slab waves of the shared kernel and of the line kernel with
     # SN >= 2 pair up (SN/2 output slabs per workgroup)
     if kind == "line" and p.get("SN", 1) >= 2:
@@ -98,7 +128,7 @@ def _fits_gate_up(kind, p, M, N, K):
     if kind == "shared":
         return (p["SN"] % 2 == 0 and N % (STREAM_N_ROWS * p["R"] * p["SN"] // 2) == 0
                 and K % (STREAM_K_STEP * p["U"]) == 0)
-    return _fits(kind, p, M, N, K)
+    return _fits(kind, p, M, N, K, fmt)
 
 
 def ilv_ld_max(p):
@@ -107,11 +137,14 @@ def ilv_ld_max(p):
     return (2 ** 31 - 1) // (2 * max(p["BM"], p["BN"]))
 
 
-def _fits(kind, p, M, N, K):
+def _fits(kind, p, M, N, K, fmt=1):
     if kind == "ilv8":  # a scale group of 128 k is two k-tiles; NMAX / KMIN / KMAX (optional)
         return (N % p["BN"] == 0 and K % 128 == 0 and K <= ilv_ld_max(p)
                 and N < p.get("NMAX", 1 << 30) and K >= p.get("KMIN", 0)
                 and K < p.get("KMAX", 1 << 30))
+    if kind == "line" and p.get("TL"):  # tail grid: whole slabs, one k chunk
+        return (N % (STREAM_N_ROWS * p["R"]) == 0 and K % LINE_K_STEP == 0
+                and line_tail_fits(p, N, K, fmt))
     if kind == "line":  # NMAX (optional): the row holds narrower N only
         return (N % (STREAM_N_ROWS * p["R"] * p.get("SN", 1)) == 0 and K % LINE_K_STEP == 0
                 and K <= LINE_K_MAX and N < p.get("NMAX", 1 << 30))
@@ -140,7 +173,7 @@ def _first(ladder, M, N, K, fmt, fits=_fits):
     for m_max, n_min, tag, kind, p in ladder:
         if fmt not in p.get("fmts", FORMATS):
             continue
-        if M <= m_max and N >= n_min and fits(kind, p, M, N, K):
+        if M <= m_max and N >= n_min and fits(kind, p, M, N, K, fmt):
             q = {k: v for k, v in p.items() if k != "fmts"}
             return dict(tag=tag, kind=kind, fmt=fmt, **q)
     return None

@@ -277,6 +277,11 @@ def make(op, rows_files=(), counter_files=()):
                                                                  sel.ilv_ld_max(p))
         elif kind == "ilv8":
             fit = "N %% %d == 0 and K %% 128 == 0 and K <= %d" % (p["BN"], sel.ilv_ld_max(p))
+        elif kind == "line" and p.get("TL"):
+            fit = ("N %% %d == 0 and K %% %d == 0 and K <= %d; tail grid: q = (N / %d) // %d >= 1 "
+                   "whole rounds, at most %d slabs left, q + 1 workgroups resident per CU" % (
+                       sel.STREAM_N_ROWS * p["R"], sel.LINE_K_STEP, sel.LINE_K_MAX,
+                       sel.STREAM_N_ROWS * p["R"], sel.LINE_CUS * p["SN"], sel.LINE_CUS))
         elif kind == "line":
             fit = "N %% %d == 0 and K %% %d == 0 and K <= %d" % (
                 sel.STREAM_N_ROWS * p["R"] * p.get("SN", 1), sel.LINE_K_STEP, sel.LINE_K_MAX)

@@ -43,6 +43,7 @@ struct StreamArgs {
   int chunk;           // k per chunk (multiple of 64*U; K is a multiple of 64*U too)
   int group;           // k per scale group (fmt 2)
   int up;              // EPI = 1: row offset of the "up" half of B (= N, the output width)
+  int nbig = 0;        // k_stream_line with TL = 1: workgroups of SN slabs (the rest: tails)
 };
 
 // Group-wise metadata of one stage for one lane's row (fmt 2, group 128): GPS = 64*U/128 groups.
@@ -869,9 +870,11 @@ __global__ __launch_bounds__(TPB) void k_stream_sh(StreamArgs p) {
 // the copies of a step -- so the activation traffic drops by SN; one workgroup barrier per step
 // orders them: at iteration j every wave has its own copies of step j landed (vmcnt), then the
 // barrier makes all of step j readable and guarantees that every wave has finished reading step
-// j-1, whose activation slot is refilled in this iteration (with step j+D-1: the shared ring runs
-// one step shallower than the private weight rings).  All chunks then hold the same number of
-// steps (the launcher's split), so every wave passes the same barriers.
+// j-1.  The shared ring has D+1 slots, one more than the weight rings, so the slot of step j-1 is
+// the one step j+D goes into: each iteration issues the weights and the activations of the same
+// step, and the constant wait leaves D-1 whole steps of weights in flight, as with SN = 1.  All
+// chunks then hold the same number of steps (the launcher's split), so every wave passes the same
+// barriers.
 // k order of a step: lane (row l % 16, kgroup g = l / 16) takes k [64h + 16g, 64h + 16g + 16) of
 // each half h = 0, 1 -- the activation fragments use the same map.
 // fmt 2: the zero-point and scale of (row, group) are staged in the wave's LDS before the loop
@@ -901,16 +904,17 @@ struct StreamLine {
   static constexpr int LA = MB > 0 ? 4 * MB : SN;
   static constexpr int LAW = LA / SN;                    // ... issued by each wave
   static constexpr int L = 2 * RR * EB + LAW;            // copies per step per wave
-  static constexpr int WAIT = (SN > 1 ? D - 2 : D - 1) * L;
+  static constexpr int WAIT = (D - 1) * L;
+  static constexpr int DA = SN > 1 ? D + 1 : D;          // slots of the shared activation ring
   static_assert(SN >= 1 && LA % SN == 0, "activation copies split evenly over the slab waves");
-  static_assert(D >= (SN > 1 ? 3 : 2) && (D - 1) * L < 64, "ring depth / vmcnt range");
+  static_assert(D >= 2 && (D - 1) * L < 64, "ring depth / vmcnt range");
   // LDS of one wave: D weight slots (+ its own activation ring when SN = 1) + (fmt 2) the staged
   // zero-points and scales of G groups; one shared activation ring per k chunk when SN > 1
   static constexpr size_t wave_bytes(int G) {
     return ((size_t)D * (WSLOT + (SN == 1 ? ASLOT : 0)) +
             (BFMT == 2 ? ((size_t)RR * 16 * G * 3 + 15) / 16 * 16 : 0) + 1023) / 1024 * 1024;
   }
-  static constexpr size_t act_bytes() { return SN > 1 ? ((size_t)D * ASLOT + 1023) / 1024 * 1024 : 0; }
+  static constexpr size_t act_bytes() { return SN > 1 ? ((size_t)DA * ASLOT + 1023) / 1024 * 1024 : 0; }
   static constexpr size_t lds(int S, int G) {
     return (size_t)S * (SN * wave_bytes(G) + act_bytes()) +
            (S > 1 ? (size_t)S * SN * RR * MBE * 1024 : 0);
@@ -919,12 +923,12 @@ struct StreamLine {
 
 __device__ __forceinline__ int line_key(int row16) { return (row16 >> 1) & 7; }
 
-template <int MB, int R, int D, int BFMT, int EPI = 0, int SN = 1, int TPB = 1024>
-__global__ __launch_bounds__(TPB) void k_stream_line(StreamArgs p, int G) {
+// The body of k_stream_line for the workgroup that covers slab group `wgi` (SNO output slabs).
+template <int MB, int R, int D, int BFMT, int EPI, int SN>
+__device__ __forceinline__ void line_body(const StreamArgs& p, int G, int wgi, uint8_t* dsm) {
   using SL = StreamLine<MB, R, D, BFMT, EPI, SN>;
   constexpr int RR = SL::RR, EB = SL::EB, MBE = SL::MBE, WSLOT = SL::WSLOT, ASLOT = SL::ASLOT;
   constexpr int WSTRIDE = SN == 1 ? WSLOT + ASLOT : WSLOT;  // bytes per ring slot of a wave
-  extern __shared__ __attribute__((aligned(1024))) uint8_t dsm[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int sg = wave % SN, kc = wave / SN;  // slab of the workgroup, k chunk
@@ -933,7 +937,7 @@ __global__ __launch_bounds__(TPB) void k_stream_line(StreamArgs p, int G) {
   uint8_t* ring = group + SL::act_bytes() + sg * wbytes;         // this wave's weight ring
   // activation slot of step j: inside the wave's own ring slot (SN = 1) or the shared ring
   auto aslot = [&](int j) -> uint8_t* {
-    return SN == 1 ? ring + (j % D) * WSTRIDE + WSLOT : group + (j % D) * ASLOT;
+    return SN == 1 ? ring + (j % D) * WSTRIDE + WSLOT : group + (j % SL::DA) * ASLOT;
   };
   uint8_t* meta_z = ring + D * WSTRIDE;                                  // fmt 2: [RR*16][G]
   _Float16* meta_s = reinterpret_cast<_Float16*>(meta_z + (RR * 16 * G + 1) / 2 * 2);
@@ -946,7 +950,7 @@ __global__ __launch_bounds__(TPB) void k_stream_line(StreamArgs p, int G) {
   const int r16 = lane & 15, kg = lane >> 4;
   constexpr bool PAIRED = SL::PAIRED;
   const bool upw = PAIRED && sg >= SN / 2;                         // paired: an up wave
-  const int nbase = (blockIdx.x * SL::SNO + (PAIRED ? sg % (SN / 2) : sg)) * 16 * R;
+  const int nbase = (wgi * SL::SNO + (PAIRED ? sg % (SN / 2) : sg)) * 16 * R;
   auto row_of = [&](int r) -> long {  // first row of row group r
     if constexpr (PAIRED) return (upw ? (long)p.up : 0L) + nbase + r * 16;
     return EPI && r >= R ? (long)p.up + nbase + (r - R) * 16 : (long)nbase + r * 16;
@@ -1010,12 +1014,10 @@ __global__ __launch_bounds__(TPB) void k_stream_line(StreamArgs p, int G) {
 #pragma unroll
     for (int r = 0; r < RR; ++r) rscale[r] = p.scale[row_of(r) + r16];
   }
-  // prologue: copy units in the loop's order -- weights of step j with the activations of step j
-  // (SN = 1) or of step j-1 (SN > 1, the shared ring one step shallower)
+  // prologue: copy units in the loop's order -- weights of step j, then its activations
   for (int j = 0; j < D; ++j) {
     dma_w(j);
-    if (SN == 1) dma_a(j);
-    else if (j >= 1) dma_a(j - 1);
+    dma_a(j);
   }
   if constexpr (BFMT == 2) {  // this wave's zero-points and scales, one group per step
     const long gstride = p.K / 128;
@@ -1101,11 +1103,16 @@ __global__ __launch_bounds__(TPB) void k_stream_line(StreamArgs p, int G) {
 #pragma unroll
         for (int r = 0; r < RR; ++r) read_w(slot, r, h, w[r][h]);
       }
+      // the fences keep the matrix work below the copies: left to itself the scheduler moves
+      // MFMAs and dequantisation between the reads, each read then waits on its own and the
+      // next step's copies go out only after all of them
+      __builtin_amdgcn_sched_barrier(0);
       asm volatile("" ::: "memory");
       __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): slot j is read, it may be refilled
       asm volatile("" ::: "memory");
       dma_w(j + D);
-      dma_a(SN == 1 ? j + D : j + D - 1);  // SN > 1: slot (j-1) % D, free since the barrier
+      dma_a(j + D);  // SN > 1: slot (j-1) % (D+1), free since the barrier
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
@@ -1144,7 +1151,7 @@ __global__ __launch_bounds__(TPB) void k_stream_line(StreamArgs p, int G) {
       __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): slot j is read, it may be refilled
       asm volatile("" ::: "memory");
       dma_w(j + D);
-      dma_a(SN == 1 ? j + D : j + D - 1);
+      dma_a(j + D);
     }
   }
   s_wait_vm_stream<0>();  // the copies past the end land before the LDS is reused
@@ -1197,4 +1204,25 @@ __global__ __launch_bounds__(TPB) void k_stream_line(StreamArgs p, int G) {
   } else {
     stream_store<MBE, R, EPI>(p, acc, nbase, r16, kg);
   }
+}
+
+// TL = 1 (SN > 1, EPI = 0, one k chunk): the grid is p.nbig workgroups of SN slabs -- a whole
+// number of them per CU -- followed by one workgroup per remaining slab, in which wave 0 streams
+// that slab over the whole K with its own activation ring (the body with SN = 1) and the other
+// waves leave at once.  A grid of whole rounds plus at most one such tail per CU keeps the slabs
+// per CU within one of each other; with workgroups of SN slabs alone, a partial last round puts
+// 2 SN slabs on some CUs and SN on others (N = 34816, SN = 4: 8 or 12).
+template <int MB, int R, int D, int BFMT, int EPI = 0, int SN = 1, int TPB = 1024, int TL = 0>
+__global__ __launch_bounds__(TPB) void k_stream_line(StreamArgs p, int G) {
+  extern __shared__ __attribute__((aligned(1024))) uint8_t dsm[];
+  if constexpr (TL) {
+    static_assert(SN > 1 && EPI == 0, "tail workgroups: shared activation ring, plain epilogue");
+    const int wgi = blockIdx.x;
+    if (wgi >= p.nbig) {
+      if (threadIdx.x >= 64) return;
+      line_body<MB, R, D, BFMT, 0, 1>(p, G, p.nbig * SN + (wgi - p.nbig), dsm);
+      return;
+    }
+  }
+  line_body<MB, R, D, BFMT, EPI, SN>(p, G, blockIdx.x, dsm);
 }

@@ -50,7 +50,7 @@ DOMAINS = {
                 GROUP=(4, 8, 16), XCD=(0, 1), WAVES=((2, 2), (2, 4), (4, 2), (4, 4)), MS=(16, 32)),
     "reg": dict(BM=(64, 128, 256), BN=(64, 128, 256), BK=(64,), MS=(16, 32), SWZ=(1, 2), GROUP=(8,),
                 XCD=(1,)),
-    "line": dict(R=(1, 2, 4), D=(2, 3, 4, 5, 6), W=(1024, 2048, 4096), SN=(1, 2, 4)),
+    "line": dict(R=(1, 2, 4), D=(2, 3, 4, 5, 6), W=(1024, 2048, 4096), SN=(1, 2, 4, 8), TL=(0, 1)),
     "ring": dict(R=(1, 2, 4), D=(4, 5, 6, 8, 10, 12, 14, 16)),
     "stream": dict(R=(1, 2, 4), U=(2, 4, 8), ALDS=(0, 1)),
     "shared": dict(R=(1, 2), U=(2, 4), SN=(2, 4, 8)),
@@ -104,10 +104,38 @@ def line_geometry(p: dict):
     return 2 * rr * eb + la // sn, rr * eb * 2048, (p["MB"] * 16 * 256 if p["MB"] else 256)
 
 
+LINE_CUS = 256  # one round of the tail grid: the part's CUs
+
+
+def line_tail_grid(N: int, K: int, p: dict):
+    """(workgroups of SN slabs, grid) of the line kernel's tail grid (TL = 1), or None: q >= 1
+    whole rounds of LINE_CUS workgroups, then one single-wave workgroup per remaining slab (at
+    most one per CU), a CU's q workgroups and one tail resident together.  As
+    kernels/shipped/gemm_w8a16/gfx950/launch.h line_tail_grid."""
+    slabs, sn = N // (16 * p["R"]), p.get("SN", 1)
+    q = slabs // (LINE_CUS * sn)
+    tail = slabs - q * LINE_CUS * sn
+    split = line_split(N, K, p)
+    if q < 1 or tail > LINE_CUS or split is None:
+        return None
+    if (q + 1) * split[2] > LDS_MAX or (q + 1) * sn > 16:
+        return None
+    return q * LINE_CUS, q * LINE_CUS + tail
+
+
 def line_split(N: int, K: int, p: dict):
     """(S, steps per wave, LDS bytes) as the shipped launchers compute them; None if none fits."""
     rr = 2 * p["R"] if p.get("EPI") and not line_paired(p) else p["R"]
     sn = p.get("SN", 1)
+    if p.get("TL"):  # one k chunk; LDS of the shared-ring body or the tail body, the larger
+        steps = K // 128
+        _, wslot, aslot = line_geometry(p)
+        meta = -(-(rr * 16 * steps * 3) // 16) * 16 if p["BFMT"] == 2 else 0
+        wave_big = -(-(p["D"] * wslot + meta) // 1024) * 1024
+        act = -(-((p["D"] + 1) * aslot) // 1024) * 1024
+        wave_one = -(-(p["D"] * (wslot + aslot) + meta) // 1024) * 1024
+        lds = max(sn * wave_big + act, wave_one)
+        return (1, steps, lds) if lds <= LDS_MAX else None
     wgs = N // (16 * p["R"] * (sn // 2 if line_paired(p) else sn))
     steps = K // 128
     _, wslot, aslot = line_geometry(p)
@@ -117,7 +145,7 @@ def line_split(N: int, K: int, p: dict):
     def lds(s_, per):
         meta = -(-(rr * 16 * per * 3) // 16) * 16 if p["BFMT"] == 2 else 0
         wave = -(-(p["D"] * (wslot + (aslot if sn == 1 else 0)) + meta) // 1024) * 1024
-        act = -(-(p["D"] * aslot) // 1024) * 1024 if sn > 1 else 0
+        act = -(-((p["D"] + 1) * aslot) // 1024) * 1024 if sn > 1 else 0  # D+1 shared slots
         return s_ * (sn * wave + act) + (s_ * sn * rr * max(1, p["MB"]) * 1024 if s_ > 1 else 0)
 
     while True:
@@ -204,8 +232,9 @@ def tag(kind: str, p: dict) -> str:
         return "reg_m%dn%dk%d_w%dx%d_f%d_z%d_b%d" % (p["BM"], p["BN"], p["BK"], p["WM"], p["WN"],
                                                    p["MS"], p["SWZ"], p["BFMT"])
     if kind == "line":
-        return "line_mb%d_r%d_n%d_d%d_w%d_b%d%s" % (p["MB"], p["R"], p.get("SN", 1), p["D"], p["W"],
-                                                  p["BFMT"], "_e1" if p.get("EPI") else "")
+        return "line_mb%d_r%d_n%d_d%d_w%d_b%d%s%s" % (
+            p["MB"], p["R"], p.get("SN", 1), p["D"], p["W"], p["BFMT"],
+            "_e1" if p.get("EPI") else "", "_tl" if p.get("TL") else "")
     if kind == "ring":
         return "ring_mb%d_r%d_d%d_b%d" % (p["MB"], p["R"], p["D"], p["BFMT"])
     if kind == "shared":
@@ -291,8 +320,14 @@ def legal(kind: str, p: dict, M: int, N: int, K: int):
         if (4 * p["MB"] if p["MB"] else sn) % sn or (not p["MB"] and sn not in (1, 2, 4)):
             return "activation copies do not split over the slab waves"
         L, _, _ = line_geometry(p)
-        if (p["D"] - 1) * L >= 64 or p["D"] < (3 if sn > 1 else 2):
+        if (p["D"] - 1) * L >= 64 or p["D"] < 2:
             return "vmcnt depth"
+        if p.get("TL"):
+            if sn == 1 or p.get("EPI"):
+                return "tail grid: SN > 1, plain epilogue"
+            if line_tail_grid(N, K, p) is None:
+                return "tail grid: no whole round, > 1 tail slab per CU, or not co-resident"
+            return None
         if line_split(N, K, p) is None:
             return "LDS"
         return None
@@ -343,10 +378,14 @@ def variants(op: OpSpec) -> Iterator[Hyperform]:
         for R in d["R"]:
             for D in d["D"]:
                 for W in d["W"]:
-                    for SN in d["SN"]:
+                    for SN, TL in ((sn, tl) for sn in d["SN"] for tl in d["TL"]):
+                        if TL and (SN == 1 or W != 2048 or MB >= 4 or M > 32):
+                            continue  # the tail grid ignores W; decode rows only
                         q = dict(MB=0 if M == 1 else MB, R=R, D=D, W=W, BFMT=b)
                         if SN > 1:
                             q["SN"] = SN
+                        if TL:
+                            q["TL"] = 1
                         if MB >= 4 and M > 32:  # the shipped launchers' bound: 256 VGPRs
                             q["SN"] = SN
                             q["TPB"] = 512

@@ -90,18 +90,20 @@ def row_of(params: dict):
             return None
         if p.get("SN", 1) == 1:
             p.pop("SN", None)
+        if not p.get("TL"):
+            p.pop("TL", None)
     if kind == "shared" and p.get("TPB", 1024) == 1024:
         p.pop("TPB", None)
     return ({"reg": "mfma"}.get(kind, kind), p)
 
 
 def _match(params: dict, where) -> bool:
-    """--where filters: KEY=VALUE pairs a hyperform's params must all equal (values as ints when
-    they parse)."""
+    """--where filters: KEY=VALUE pairs, each a hyperform's params must match; VALUE may list
+    alternatives separated by commas (KEY=2,3,4).  Values compare as ints when they parse."""
     for cond in where or ():
         key, _, val = cond.partition("=")
-        want = int(val) if val.lstrip("-").isdigit() else val
-        if params.get(key, 0 if key in ("SW", "SPLIT") else None) != want:
+        wants = [int(v) if v.lstrip("-").isdigit() else v for v in val.split(",")]
+        if params.get(key, {"SW": 0, "SPLIT": 0, "SN": 1}.get(key)) not in wants:
             return False
     return True
 
@@ -420,7 +422,7 @@ def main():
     a.add_argument("--kinds", nargs="*")
     a.add_argument("--per-kind", type=int, default=6)
     a.add_argument("--where", nargs="*", default=[], metavar="KEY=VALUE",
-                   help="keep only hyperforms whose params match (e.g. BM=128 SW=256)")
+                   help="keep only hyperforms whose params match (e.g. BM=128 SW=0,256)")
     a.add_argument("--out", default="gpurun_out/tune")
     for name in ("run", "report", "peak"):
         b = sub.add_parser(name)

@@ -69,9 +69,15 @@ W8 = {
     1: [
         ("l0r1n2d5", 1, 5120, 17408),
         ("l0r1d4", 1, 7168, 5120),
-        ("l1r1n4d3", 16, 34816, 5120),
+        ("l1r1n4d2t", 16, 34816, 5120),
+        ("l1r1n4d2t", 16, 16400, 256),    # one remaining slab
+        ("l1r1n4d2t", 9, 16384, 384),     # whole rounds, no tail
+        ("l1r1n4d3", 16, 15360, 5120),    # too few slabs for a round of the tail grid
         ("l1r1n2d4", 16, 5120, 17408),
-        ("l2r1n4d4", 32, 34816, 5120),
+        ("l2r1n8d2t", 32, 34816, 5120),
+        ("l2r1n8d2t", 17, 32784, 256),    # one remaining slab
+        ("l2r1n8d2t", 32, 36864, 128),    # one slab per CU remaining, a single k step
+        ("l2r1n4d4", 32, 15360, 5120),
         ("l2r1n2d4", 32, 5120, 6144),
         ("s1a_r1u8", 1, 512, 66048),
         ("s1a_r1u4", 1, 512, 65792),
@@ -96,9 +102,15 @@ W8 = {
     ],
     2: [
         ("l0r1d4", 1, 7168, 5120),
-        ("l1r1n4d3", 16, 34816, 5120),
+        ("l1r1n4d2t", 16, 34816, 5120),
+        ("l1r1n4d2t", 16, 16400, 256),    # one remaining slab
+        ("l1r1n4d2t", 9, 16384, 384),     # whole rounds, no tail
+        ("l1r1n4d3", 16, 15360, 5120),    # too few slabs for a round of the tail grid
         ("l1r1n2d4", 16, 5120, 17408),
-        ("l2r1n4d4", 32, 34816, 5120),
+        ("l2r1n8d2t", 32, 34816, 5120),
+        ("l2r1n8d2t", 17, 32784, 256),    # one remaining slab
+        ("l2r1n8d2t", 32, 36864, 128),    # one slab per CU remaining, a single k step
+        ("l2r1n4d4", 32, 15360, 5120),
         ("l2r1n2d4", 32, 5120, 6144),
         ("s1a_r1u8", 1, 512, 66048),
         ("s1a_r1u4", 1, 512, 65792),

@@ -109,7 +109,11 @@ def test_abi_version():
 SWEEP_M = (1, 2, 8, 16, 17, 31, 32, 33, 64, 128, 255, 256, 257, 1000, 2048, 4096)
 SWEEP_NK = ((15360, 3840), (3840, 15360), (7168, 5120), (5120, 6144), (34816, 5120),
             (5120, 17408), (1024, 5120), (5120, 5120), (512, 384), (520, 384), (384, 100),
-            (4096, 192), (4096, 320))
+            (4096, 192), (4096, 320),
+            # the line kernel's tail grid: one slab left, none left, one per CU left, too many
+            # waves per CU, fmt 2 metadata past the LDS, more rounds
+            (16400, 256), (16384, 384), (36864, 128), (69632, 5120), (34816, 16384),
+            (32784, 256), (49152, 5120))
 
 
 def test_compiled_route_agrees_with_select_fp16():
@@ -160,9 +164,12 @@ def test_rows_fall_through_when_the_first_row_does_not_fit():
     assert capi.route(0, 8, 15360, 3840) == "l1r1n4d3"
     assert capi.route(0, 8, 12304, 3840) == "l1r1d4"      # N % 64 != 0: the unshared line row
     assert capi.route(0, 8, 15360, 65792) == "s16r1u4"    # K > 65536: past the line rows
-    assert capi.route(1, 16, 34816, 5120) == "l1r1n4d3"
+    assert capi.route(1, 16, 34816, 5120) == "l1r1n4d2t"
+    assert capi.route(1, 16, 15360, 5120) == "l1r1n4d3"  # too few slabs for the tail grid
+    assert capi.route(1, 16, 69632, 5120) == "l1r1n4d3"  # 5 workgroups of 4 waves per CU
     assert capi.route(2, 16, 5120, 17408) == "l1r1n2d4"
-    assert capi.route(1, 32, 34816, 5120) == "l2r1n4d4"
+    assert capi.route(1, 32, 34816, 5120) == "l2r1n8d2t"
+    assert capi.route(2, 32, 34816, 16384) == "l2r1n4d4"  # fmt 2 metadata: not co-resident
     assert capi.route(2, 32, 34816, 65536 + 256) == "h32r1u4n2"
     assert capi.route(0, 1, 15360, 3840) == "l0r1d3"
     assert capi.route(1, 1, 5120, 5120) == "l0r1n2d5"
