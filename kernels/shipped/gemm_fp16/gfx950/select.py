@@ -25,13 +25,21 @@ ARCH = "gfx950"
 
 # (M_max, N_min, tag, kind, template params).  First row that holds (M, N) and fits wins.
 LADDER = [
+    # M = 1, long K: a two-step ring (1.05x three steps at (1, 3840, 15360))
+    (1, 0, "l0r1d2", "line", dict(MB=0, R=1, D=2, W=1024, KMIN=12288)),
     (1, 0, "l0r1d3", "line", dict(MB=0, R=1, D=3, W=2048)),
     (1, 0, "s1a_r1u4", "stream", dict(MB=1, R=1, U=4, A=1)),
     (16, 12288, "l1r1n4d3", "line", dict(MB=1, R=1, D=3, SN=4, W=2048)),
+    # narrow N, long K: k slices across workgroups (KS, fp32 partials reduced in slice order)
+    # spread the 60 four-slab workgroups of N = 3840 over the part (1.10x the row below at
+    # (16, 3840, 15360); 0.99x at M = 8)
+    (16, 0, "l1r1n4d4k8", "line", dict(MB=1, R=1, D=4, SN=4, W=2048, KS=8, KMIN=12288)),
     (16, 0, "l1r1d4", "line", dict(MB=1, R=1, D=4, W=2048)),
     (16, 0, "s16r1u4", "stream", dict(MB=1, R=1, U=4, A=0)),
     # four ring stages (1.08-1.12x three at M = 24-32, N = 12288-15360)
     (32, 12288, "l2r1n4d4", "line", dict(MB=2, R=1, D=4, SN=4, W=2048)),
+    # k slices as above (1.28x the row below at (32, 3840, 15360))
+    (32, 0, "l2r1n4d3k8", "line", dict(MB=2, R=1, D=3, SN=4, W=2048, KS=8, KMIN=12288)),
     (32, 0, "l2r1d4", "line", dict(MB=2, R=1, D=4, W=2048)),
     (32, 0, "s32r1u4", "stream", dict(MB=2, R=1, U=4, A=0)),
     (64, 12288, "l4r1n4d3", "line", dict(MB=4, R=1, D=3, SN=4, W=2048)),
@@ -108,9 +116,9 @@ def ilv_ld_max(p):
 
 
 def _fits(kind, p, M, N, K):
-    if kind == "line":  # NMAX (optional): the row holds narrower N only
+    if kind == "line":  # NMAX / KMIN (optional): the row holds narrower N / longer K only
         return (N % (STREAM_N_ROWS * p["R"] * p.get("SN", 1)) == 0 and K % LINE_K_STEP == 0
-                and K <= LINE_K_MAX and N < p.get("NMAX", 1 << 30))
+                and K <= LINE_K_MAX and N < p.get("NMAX", 1 << 30) and K >= p.get("KMIN", 0))
     if kind == "ilv":  # NMAX (optional): the row holds narrower N only
         return (N % p["BN"] == 0 and K % max(64, p["BK"]) == 0 and K <= ilv_ld_max(p)
                 and N < p.get("NMAX", 1 << 30))

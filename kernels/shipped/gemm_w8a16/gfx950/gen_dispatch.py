@@ -36,6 +36,11 @@ HEAD = """// GENERATED from select.py -- do not edit.  Regenerate with:
 
 def instantiation(kind, p, epi=0):
     tail = ",%d" % epi if epi else ""
+    if kind == "line" and p.get("KS", 1) > 1:  # k slices across workgroups: a workspace row
+        if epi or p.get("TL"):
+            raise ValueError("k slices take the plain epilogue and no tail grid")
+        return "launch_line_ks<%d,%d,%d,%d,%d,%d>" % (p["MB"], p["R"], p["D"], p.get("SN", 1),
+                                                      p["W"], p["KS"])
     if kind == "line":
         if p.get("TL"):
             tail = ",%d,1" % epi
@@ -66,6 +71,8 @@ def condition(sel, kind, p, m_max, n_min=0, gate_up=False):
             sel.STREAM_N_ROWS * p["R"] * sno, sel.LINE_K_STEP, sel.LINE_K_MAX)
         if "NMAX" in p:
             fit += " && p.N < %d" % p["NMAX"]
+        if "KMIN" in p:
+            fit += " && p.K >= %d" % p["KMIN"]
     elif kind == "stream":
         fit = "(p.N %% %d) == 0 && (p.K %% %d) == 0" % (sel.STREAM_N_ROWS * p["R"],
                                                           sel.STREAM_K_STEP * p["U"])

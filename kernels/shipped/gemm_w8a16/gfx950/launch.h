@@ -195,13 +195,34 @@ inline bool line_tail_fits(const W8A16Params& p) {
   return line_tail_grid<MB, R, D, SN>(p, &nbig, &grid, &lds);
 }
 
+// k slices of the line kernel across workgroups (KS = the most a row allows): the count that
+// spreads wgs x ks workgroups most evenly over the part's CUs, each slice a whole number of
+// 128-k steps and at least kLineMinSteps of them.  A split pays a partial-sum pass and a second
+// launch, so it is taken only when it lifts the evenness (workgroups / whole rounds of
+// kLineCus) by at least 0.08 over no split; ties keep fewer slices.
+constexpr int kLineMinSteps = 8;
+inline int line_kslices(int wgs, int K, int KS) {
+  const int steps = K / 128;
+  auto even = [&](int ks) {
+    const long w = (long)wgs * ks;
+    return (double)w / (double)(((w + kLineCus - 1) / kLineCus) * kLineCus);
+  };
+  int best = 1;
+  for (int ks = 2; ks <= KS; ++ks)
+    if (steps % ks == 0 && steps / ks >= kLineMinSteps && even(ks) > even(best) + 1e-9) best = ks;
+  return even(best) >= even(1) + 0.08 ? best : 1;
+}
+
 // The line kernel (whole-line nontemporal weight stream through per-wave LDS rings).  MB = 0:
 // M = 1; MB = 1 / 2: M <= 16 / 32.  SN slab waves of a workgroup share one activation ring.
 // EPI = 1: fused gate/up (p.N the output width; Wq, scale and zero hold 2N rows).
 // TL = 1: the tail grid above, one k chunk per slab.
-template <int BFMT, int MB, int R, int D, int SN, int WAVES, int EPI, int TL>
-inline hipError_t launch_line_fmt(const W8A16Params& p, hipStream_t s) {
+// KS > 1 (plain epilogue): up to KS k slices across workgroups (line_kslices), their fp32
+// partial sums in the workspace `w`, added by k_splitk_reduce on the same stream.
+template <int BFMT, int MB, int R, int D, int SN, int WAVES, int EPI, int TL, int KS = 0>
+inline hipError_t launch_line_fmt(const W8A16Params& p, hipStream_t s, const Workspace* w = nullptr) {
   using SL = StreamLine<MB, R, D, BFMT, EPI, SN>;
+  static_assert(KS <= 1 || (EPI == 0 && TL == 0), "k slices: plain epilogue, no tail grid");
   StreamArgs a = stream_args(p);
   a.up = EPI ? p.N : 0;
   int G = 0;
@@ -212,18 +233,42 @@ inline hipError_t launch_line_fmt(const W8A16Params& p, hipStream_t s) {
     static_assert(SN > 1 && EPI == 0, "tail grid: shared activation ring, plain epilogue");
     if (!line_tail_grid<MB, R, D, SN>(p, &a.nbig, &wgs, &lds)) return hipErrorInvalidConfiguration;
     G = p.K / 128;
-  } else if (!line_split<SL>(wgs, SN, p.K, WAVES, &a.S, &a.chunk, &G, &lds, TPB)) {
-    return hipErrorInvalidConfiguration;
+  } else {
+    if constexpr (KS > 1) {
+      a.ks = line_kslices(wgs, p.K, KS);
+      a.kspan = p.K / a.ks;
+    }
+    if (!line_split<SL>(wgs * a.ks, SN, a.ks > 1 ? a.kspan : p.K, WAVES, &a.S, &a.chunk, &G, &lds,
+                        TPB))
+      return hipErrorInvalidConfiguration;
   }
-  hipLaunchKernelGGL((k_stream_line<MB, R, D, BFMT, EPI, SN, TPB, TL>), dim3(wgs),
+  const size_t bytes = a.ks > 1 ? (size_t)a.ks * p.M * p.N * sizeof(float) : 0;
+  if (w && w->need) {
+    *w->need = bytes;
+    return hipSuccess;
+  }
+  if (a.ks > 1) {
+    a.part = workspace_for(*w, bytes, s);
+    if (!a.part) return hipErrorOutOfMemory;
+  }
+  hipLaunchKernelGGL((k_stream_line<MB, R, D, BFMT, EPI, SN, TPB, TL>), dim3(wgs * a.ks),
                      dim3(64 * SN * a.S), lds, s, a, G);
-  return hipGetLastError();
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess || a.ks == 1) return e;
+  return launch_reduce(a.part, a.ks, p.M, p.N, p.C, p.ldc, s);
 }
 
 template <int MB, int R, int D, int SN, int WAVES, int EPI = 0, int TL = 0>
 inline hipError_t launch_line(const W8A16Params& p, hipStream_t s) {
   if (p.fmt == 1) return launch_line_fmt<1, MB, R, D, SN, WAVES, EPI, TL>(p, s);
   return launch_line_fmt<2, MB, R, D, SN, WAVES, EPI, TL>(p, s);
+}
+
+// The line kernel with up to KS k slices across workgroups (a workspace row).
+template <int MB, int R, int D, int SN, int WAVES, int KS>
+inline hipError_t launch_line_ks(const W8A16Params& p, hipStream_t s, const Workspace& w) {
+  if (p.fmt == 1) return launch_line_fmt<1, MB, R, D, SN, WAVES, 0, 0, KS>(p, s, &w);
+  return launch_line_fmt<2, MB, R, D, SN, WAVES, 0, 0, KS>(p, s, &w);
 }
 
 // The interleaved int8 prefill kernel (k_gemm_ilv8) lives in its own translation unit,

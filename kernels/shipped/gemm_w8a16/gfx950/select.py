@@ -16,18 +16,40 @@ FORMATS = (1, 2)
 # holds (M, N) -- M <= M_max and N >= N_min -- whose weight format is listed (params "fmts";
 # absent = both) and whose kernel fits the shape is taken.
 LADDER = [
-    # M = 1 on N = 4096..6144, int8: five ring stages and two slab waves per activation ring
-    # (1.06-1.14x l0r1d4 at N = 5120; 0.78-0.89x at N = 1024 and 7168; uint8 within 2 %)
-    (1, 4096, "l0r1n2d5", "line", dict(MB=0, R=1, D=5, SN=2, W=1024, NMAX=6145, fmts=(1,))),
+    # M = 1, long K: k slices across workgroups (KS, fp32 partials reduced in slice order) spread
+    # the 320 slabs of N = 5120 evenly over the part; two ring steps (1.04x / 1.12x the rows
+    # below at (1, 5120, 17408), int8 / uint8)
+    (1, 0, "l0r1d2k8", "line", dict(MB=0, R=1, D=2, W=2048, KS=8, KMIN=12288)),
+    # M = 1 on N = 4096..6144: two slab waves per activation ring, two ring steps (1.10-1.14x
+    # the five-step row it replaced at N = 5120, K = 5120-6144)
+    (1, 4096, "l0r1n2d2", "line", dict(MB=0, R=1, D=2, SN=2, W=2048, NMAX=6145)),
+    # M = 1, narrow N: two ring steps (1.24x four at (1, 1024, 5120))
+    (1, 0, "l0r1d2", "line", dict(MB=0, R=1, D=2, W=2048, NMAX=4096)),
     (1, 0, "l0r1d4", "line", dict(MB=0, R=1, D=4, W=2048)),
     # M <= 16 / 32, wide N: the tail grid -- whole rounds of 4- / 8-slab workgroups (one ring of
     # activations each) and one single-wave workgroup per remaining slab, so the slabs per CU
     # differ by at most one (1.10-1.19x / 1.29-1.31x the rows after them at (34816, 5120))
     (16, 12288, "l1r1n4d2t", "line", dict(MB=1, R=1, D=2, SN=4, W=2048, TL=1)),
     (16, 12288, "l1r1n4d3", "line", dict(MB=1, R=1, D=3, SN=4, W=2048)),
-    (16, 0, "l1r1n2d4", "line", dict(MB=1, R=1, D=4, SN=2, W=2048)),
+    # long K: k slices (1.17x / 1.25x the row below at (16, 5120, 17408))
+    (16, 0, "l1r1n4d2k8", "line", dict(MB=1, R=1, D=2, SN=4, W=2048, KS=8, KMIN=12288)),
+    # narrow N: one slab wave per ring, k slices over the part (1.43-1.47x the two-slab
+    # four-step row at (16, 1024, 5120))
+    (16, 0, "l1r1d2k8", "line", dict(MB=1, R=1, D=2, W=2048, KS=8, NMAX=2048)),
+    # two ring steps (1.10-1.11x four at (16, 5120 | 7168, 5120))
+    (16, 0, "l1r1n2d2", "line", dict(MB=1, R=1, D=2, SN=2, W=2048)),
     (32, 12288, "l2r1n8d2t", "line", dict(MB=2, R=1, D=2, SN=8, W=2048, TL=1)),
     (32, 12288, "l2r1n4d4", "line", dict(MB=2, R=1, D=4, SN=4, W=2048)),
+    # long K: k slices, eight slab waves per activation ring (1.37x / 1.46x the row below at
+    # (32, 5120, 17408), int8 / uint8)
+    (32, 0, "l2r1n8d3k8", "line", dict(MB=2, R=1, D=3, SN=8, W=1024, KS=8, KMIN=12288, fmts=(1,))),
+    (32, 0, "l2r1n8d2k8", "line", dict(MB=2, R=1, D=2, SN=8, W=2048, KS=8, KMIN=12288, fmts=(2,))),
+    # narrow N: one slab wave per ring, k slices (1.53-1.62x at (32, 1024, 5120))
+    (32, 0, "l2r1d2k8", "line", dict(MB=2, R=1, D=2, W=2048, KS=8, NMAX=2048)),
+    # four slab waves per ring, two steps, k slices where they even out the grid (1.20x / 1.30x
+    # the two-slab four-step row at (32, 5120, 6144); at K = 5120 the slices leave the grid
+    # uneven and the row below stays ahead)
+    (32, 0, "l2r1n4d2k8", "line", dict(MB=2, R=1, D=2, SN=4, W=2048, KS=8, KMIN=6144)),
     (32, 0, "l2r1n2d4", "line", dict(MB=2, R=1, D=4, SN=2, W=2048)),
     (1, 0, "s1a_r1u8", "stream", dict(MB=1, R=1, U=8, A=1)),
     (1, 0, "s1a_r1u4", "stream", dict(MB=1, R=1, U=4, A=1)),
@@ -145,9 +167,9 @@ def _fits(kind, p, M, N, K, fmt=1):
     if kind == "line" and p.get("TL"):  # tail grid: whole slabs, one k chunk
         return (N % (STREAM_N_ROWS * p["R"]) == 0 and K % LINE_K_STEP == 0
                 and line_tail_fits(p, N, K, fmt))
-    if kind == "line":  # NMAX (optional): the row holds narrower N only
+    if kind == "line":  # NMAX / KMIN (optional): the row holds narrower N / longer K only
         return (N % (STREAM_N_ROWS * p["R"] * p.get("SN", 1)) == 0 and K % LINE_K_STEP == 0
-                and K <= LINE_K_MAX and N < p.get("NMAX", 1 << 30))
+                and K <= LINE_K_MAX and N < p.get("NMAX", 1 << 30) and K >= p.get("KMIN", 0))
     if kind == "stream":
         return N % (STREAM_N_ROWS * p["R"]) == 0 and K % (STREAM_K_STEP * p["U"]) == 0
     if kind == "shared":

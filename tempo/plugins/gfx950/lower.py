@@ -218,7 +218,8 @@ class Gfx950Skeletons:
             bound = p["TPB"]  # __launch_bounds__(TPB)
         elif kind == "line":
             sp = space.line_split(N, int(op.shapes["K"]), p)
-            grid = N // (16 * p["R"] * (p["SN"] // 2 if space.line_paired(p) else p.get("SN", 1)))
+            grid = (N // (16 * p["R"] * (p["SN"] // 2 if space.line_paired(p) else p.get("SN", 1)))
+                    * (sp[3] if sp else 1))
             threads = 64 * p.get("SN", 1) * (sp[0] if sp else 1)
             bound = p.get("TPB", 1024)  # k_stream_line: __launch_bounds__(TPB)
         else:
@@ -287,6 +288,21 @@ class Gfx950Skeletons:
         atoms.append(Atom(uid=3, kind=AtomKind.XFER_WAIT, op_id="s_waitcnt vmcnt", footprint={},
                           token="copy"))
         atoms.append(Atom(uid=4, kind=AtomKind.BARRIER, op_id="s_barrier", footprint={}))
+        # device-wide HBM floor: the operation's HBM bytes (weights and their metadata once,
+        # activations, output, and the fp32 partial sums a split writes and reads back), each CU
+        # carrying 1/CUS of them, per resident wave
+        bf = p.get("BFMT", 0)
+        hbm = (N * K * (2 if bf == 0 else 1) + (2 * N if bf == 1 else 3 * N * K // 128 if bf == 2 else 0)
+               + 2 * M * K + 2 * M * N)
+        if kind in ("ilv", "ilv8"):
+            hbm += 2 * 4 * M * N * space.splits_of(kind, p, M, N, K) if p.get("SW") else 0
+        elif kind == "line":
+            sp = space.line_split(N, K, p)
+            hbm += 2 * 4 * M * N * sp[3] if sp and sp[3] > 1 else 0
+        cus = int(_M.rate("GEOM.SMS").value)
+        atoms.append(Atom(uid=5, kind=AtomKind.MEM_READ, op_id="HBM (device share)",
+                          footprint={"HBM": float(hbm) / (cus * max(1, occ.warps_per_sm))},
+                          latency=_M.rate("LATENCY.VMEM").value))
         return atoms
 
     # -- emission ------------------------------------------------------------------------------

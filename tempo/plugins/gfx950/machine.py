@@ -50,11 +50,14 @@ class Gfx950Machine:
     def channels(self) -> Mapping[str, Channel]:
         """Channels of the bound model, all per compute unit (scope "sm"): footprints are per
         wave, the bound multiplies by resident waves and divides by the CU's per-clock
-        capacity."""
+        capacity.  HBM is the device-wide floor: every CU carries 1/CUS of the operation's HBM
+        bytes against its share of the HBM peak, so a grid spread over more CUs cannot bound
+        itself below bytes / peak."""
         return {
             "MFMA": Channel("MFMA", "sm", self.rate("CAP.MFMA_F16")),
             "LDS": Channel("LDS", "sm", self.rate("CAP.LDS")),
             "VMEM": Channel("VMEM", "sm", self.rate("CAP.VMEM_L2")),
+            "HBM": Channel("HBM", "sm", self.rate("CAP.HBM_SHARE")),
         }
 
     def latency(self, atom_class: str) -> Rate:

@@ -44,6 +44,9 @@ struct StreamArgs {
   int group;           // k per scale group (fmt 2)
   int up;              // EPI = 1: row offset of the "up" half of B (= N, the output width)
   int nbig = 0;        // k_stream_line with TL = 1: workgroups of SN slabs (the rest: tails)
+  int ks = 1;          // k_stream_line: k slices across workgroups (grid = workgroups x ks)
+  int kspan = 0;       // ks > 1: k per slice (whole 128-k steps)
+  float* part = nullptr;  // ks > 1: fp32 partial sums [ks][M][N], summed by k_splitk_reduce
 };
 
 // Group-wise metadata of one stage for one lane's row (fmt 2, group 128): GPS = 64*U/128 groups.
@@ -111,6 +114,22 @@ __device__ __forceinline__ void stream_store(const StreamArgs& p, const f32x4 (&
         o[v] = EPI ? silu_mul_f16(acc[r][b][v], acc[r + R][b][v]) : (_Float16)acc[r][b][v];
       *reinterpret_cast<f16x4*>(p.C + (long)m * p.ldc + n) = o;
     }
+  }
+}
+
+// ks > 1: the fp32 partial sums of k slice `ksi` go to part[ksi][m][n] (same lane map), to be
+// added in slice order by k_splitk_reduce.
+template <int MB, int R, int RR>
+__device__ __forceinline__ void stream_store_part(const StreamArgs& p, const f32x4 (&acc)[RR][MB],
+                                                  int nbase, int r16, int kg, int ksi) {
+  float* dst = p.part + (long)ksi * p.M * p.N;
+#pragma unroll
+  for (int b = 0; b < MB; ++b) {
+    const int m = b * 16 + r16;
+    if (m >= p.M) continue;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      *reinterpret_cast<f32x4*>(dst + (long)m * p.N + nbase + r * 16 + 4 * kg) = acc[r][b];
   }
 }
 
@@ -864,7 +883,11 @@ __global__ __launch_bounds__(TPB) void k_stream_sh(StreamArgs p) {
 //
 // Work split: one workgroup = SN slabs of 16*R weight rows x S k chunks (whole steps); wave w
 // takes slab w % SN and chunk w / SN.  The S partial sums of a slab are added through LDS in
-// chunk order and written by its chunk-0 wave, as k_stream does.
+// chunk order and written by its chunk-0 wave, as k_stream does.  With ks > 1 (plain epilogue)
+// the grid holds ks workgroups per slab group, workgroup b taking k slice b % ks of kspan k; the
+// S chunks split that slice, and the slice's sum goes to the fp32 partials (k_splitk_reduce adds
+// the slices in order) -- so a slab count that is not a multiple of the CU count still spreads
+// evenly over the part.
 // SN = 1: every wave also owns its activation ring (no barrier in the loop).  SN > 1: the SN
 // waves of one k chunk walk the same steps and SHARE one activation ring -- each issues LA/SN of
 // the copies of a step -- so the activation traffic drops by SN; one workgroup barrier per step
@@ -925,7 +948,8 @@ __device__ __forceinline__ int line_key(int row16) { return (row16 >> 1) & 7; }
 
 // The body of k_stream_line for the workgroup that covers slab group `wgi` (SNO output slabs).
 template <int MB, int R, int D, int BFMT, int EPI, int SN>
-__device__ __forceinline__ void line_body(const StreamArgs& p, int G, int wgi, uint8_t* dsm) {
+__device__ __forceinline__ void line_body(const StreamArgs& p, int G, int wgi, int ksi,
+                                          uint8_t* dsm) {
   using SL = StreamLine<MB, R, D, BFMT, EPI, SN>;
   constexpr int RR = SL::RR, EB = SL::EB, MBE = SL::MBE, WSLOT = SL::WSLOT, ASLOT = SL::ASLOT;
   constexpr int WSTRIDE = SN == 1 ? WSLOT + ASLOT : WSLOT;  // bytes per ring slot of a wave
@@ -944,8 +968,9 @@ __device__ __forceinline__ void line_body(const StreamArgs& p, int G, int wgi, u
   const int S = p.S;  // k chunks
   f32x4* red = reinterpret_cast<f32x4*>(dsm + S * (SN * wbytes + SL::act_bytes()));
 
-  const int kbeg = min(p.K, kc * p.chunk);
-  const int kend = min(p.K, kbeg + p.chunk);
+  const int k0 = ksi * p.kspan, k1 = ksi * p.kspan + (p.ks > 1 ? p.kspan : p.K);  // k slice
+  const int kbeg = min(k1, k0 + kc * p.chunk);
+  const int kend = min(k1, kbeg + p.chunk);
   const int n = (kend - kbeg) / 128;  // steps of this wave (>= 1; equal in all chunks if SN > 1)
   const int r16 = lane & 15, kg = lane >> 4;
   constexpr bool PAIRED = SL::PAIRED;
@@ -1201,6 +1226,8 @@ __device__ __forceinline__ void line_body(const StreamArgs& p, int G, int wgi, u
         both[R + r][b] = xb[((sg * R + r) * MBE + b) * 64 + lane];
       }
     stream_store<MBE, R, 1>(p, both, nbase, r16, kg);
+  } else if (EPI == 0 && p.ks > 1) {
+    stream_store_part<MBE, R>(p, acc, nbase, r16, kg, ksi);
   } else {
     stream_store<MBE, R, EPI>(p, acc, nbase, r16, kg);
   }
@@ -1220,9 +1247,10 @@ __global__ __launch_bounds__(TPB) void k_stream_line(StreamArgs p, int G) {
     const int wgi = blockIdx.x;
     if (wgi >= p.nbig) {
       if (threadIdx.x >= 64) return;
-      line_body<MB, R, D, BFMT, 0, 1>(p, G, p.nbig * SN + (wgi - p.nbig), dsm);
+      line_body<MB, R, D, BFMT, 0, 1>(p, G, p.nbig * SN + (wgi - p.nbig), 0, dsm);
       return;
     }
   }
-  line_body<MB, R, D, BFMT, EPI, SN>(p, G, blockIdx.x, dsm);
+  const int wgi = p.ks > 1 ? (int)blockIdx.x / p.ks : (int)blockIdx.x;
+  line_body<MB, R, D, BFMT, EPI, SN>(p, G, wgi, (int)blockIdx.x - wgi * p.ks, dsm);
 }

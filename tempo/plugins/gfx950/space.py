@@ -50,7 +50,8 @@ DOMAINS = {
                 GROUP=(4, 8, 16), XCD=(0, 1), WAVES=((2, 2), (2, 4), (4, 2), (4, 4)), MS=(16, 32)),
     "reg": dict(BM=(64, 128, 256), BN=(64, 128, 256), BK=(64,), MS=(16, 32), SWZ=(1, 2), GROUP=(8,),
                 XCD=(1,)),
-    "line": dict(R=(1, 2, 4), D=(2, 3, 4, 5, 6), W=(1024, 2048, 4096), SN=(1, 2, 4, 8), TL=(0, 1)),
+    "line": dict(R=(1, 2, 4), D=(2, 3, 4, 5, 6), W=(1024, 2048, 4096), SN=(1, 2, 4, 8), TL=(0, 1),
+                 KS=(1, 4, 8, 16)),
     "ring": dict(R=(1, 2, 4), D=(4, 5, 6, 8, 10, 12, 14, 16)),
     "stream": dict(R=(1, 2, 4), U=(2, 4, 8), ALDS=(0, 1)),
     "shared": dict(R=(1, 2), U=(2, 4), SN=(2, 4, 8)),
@@ -105,6 +106,25 @@ def line_geometry(p: dict):
 
 
 LINE_CUS = 256  # one round of the tail grid: the part's CUs
+LINE_MIN_STEPS = 8  # k slices keep at least this many 128-k steps
+
+
+def line_kslices(wgs: int, K: int, KS: int) -> int:
+    """k slices across workgroups of a line hyperform that allows up to KS, as the shipped
+    launchers choose them (line_kslices in kernels/shipped/*/gfx950/launch.h): the count whose
+    wgs x ks workgroups fill whole rounds of LINE_CUS most evenly, each slice whole steps and at
+    least LINE_MIN_STEPS of them; taken only when it lifts the evenness by 0.08 over no split."""
+    steps = K // 128
+
+    def even(ks):
+        w = wgs * ks
+        return w / (-(-w // LINE_CUS) * LINE_CUS)
+
+    best = 1
+    for ks in range(2, KS + 1):
+        if steps % ks == 0 and steps // ks >= LINE_MIN_STEPS and even(ks) > even(best) + 1e-9:
+            best = ks
+    return best if even(best) >= even(1) + 0.08 else 1
 
 
 def line_tail_grid(N: int, K: int, p: dict):
@@ -124,7 +144,8 @@ def line_tail_grid(N: int, K: int, p: dict):
 
 
 def line_split(N: int, K: int, p: dict):
-    """(S, steps per wave, LDS bytes) as the shipped launchers compute them; None if none fits."""
+    """(S, steps per wave, LDS bytes, k slices across workgroups) as the shipped launchers
+    compute them; None if none fits."""
     rr = 2 * p["R"] if p.get("EPI") and not line_paired(p) else p["R"]
     sn = p.get("SN", 1)
     if p.get("TL"):  # one k chunk; LDS of the shared-ring body or the tail body, the larger
@@ -135,12 +156,13 @@ def line_split(N: int, K: int, p: dict):
         act = -(-((p["D"] + 1) * aslot) // 1024) * 1024
         wave_one = -(-(p["D"] * (wslot + aslot) + meta) // 1024) * 1024
         lds = max(sn * wave_big + act, wave_one)
-        return (1, steps, lds) if lds <= LDS_MAX else None
+        return (1, steps, lds, 1) if lds <= LDS_MAX else None
     wgs = N // (16 * p["R"] * (sn // 2 if line_paired(p) else sn))
-    steps = K // 128
+    ks = line_kslices(wgs, K, p["KS"]) if p.get("KS", 1) > 1 else 1
+    steps = K // 128 // ks
     _, wslot, aslot = line_geometry(p)
     tpb = p.get("TPB", 1024)  # the kernel's launch bound
-    S = max(1, min(tpb // 64 // sn, steps, -(-p["W"] // max(1, wgs * sn))))
+    S = max(1, min(tpb // 64 // sn, steps, -(-p["W"] // max(1, wgs * ks * sn))))
 
     def lds(s_, per):
         meta = -(-(rr * 16 * per * 3) // 16) * 16 if p["BFMT"] == 2 else 0
@@ -152,7 +174,7 @@ def line_split(N: int, K: int, p: dict):
         per = -(-steps // S)
         s2 = -(-steps // per)
         if lds(s2, per) <= LDS_MAX and (sn == 1 or steps % s2 == 0):
-            return s2, per, lds(s2, per)
+            return s2, per, lds(s2, per), ks
         if S == 1:
             return None
         S -= 1
@@ -232,9 +254,10 @@ def tag(kind: str, p: dict) -> str:
         return "reg_m%dn%dk%d_w%dx%d_f%d_z%d_b%d" % (p["BM"], p["BN"], p["BK"], p["WM"], p["WN"],
                                                    p["MS"], p["SWZ"], p["BFMT"])
     if kind == "line":
-        return "line_mb%d_r%d_n%d_d%d_w%d_b%d%s%s" % (
+        return "line_mb%d_r%d_n%d_d%d_w%d_b%d%s%s%s" % (
             p["MB"], p["R"], p.get("SN", 1), p["D"], p["W"], p["BFMT"],
-            "_e1" if p.get("EPI") else "", "_tl" if p.get("TL") else "")
+            "_e1" if p.get("EPI") else "", "_tl" if p.get("TL") else "",
+            "_ks%d" % p["KS"] if p.get("KS", 1) > 1 else "")
     if kind == "ring":
         return "ring_mb%d_r%d_d%d_b%d" % (p["MB"], p["R"], p["D"], p["BFMT"])
     if kind == "shared":
@@ -322,6 +345,8 @@ def legal(kind: str, p: dict, M: int, N: int, K: int):
         L, _, _ = line_geometry(p)
         if (p["D"] - 1) * L >= 64 or p["D"] < 2:
             return "vmcnt depth"
+        if p.get("KS", 1) > 1 and (p.get("TL") or p.get("EPI")):
+            return "k slices: plain epilogue, no tail grid"
         if p.get("TL"):
             if sn == 1 or p.get("EPI"):
                 return "tail grid: SN > 1, plain epilogue"
@@ -378,14 +403,19 @@ def variants(op: OpSpec) -> Iterator[Hyperform]:
         for R in d["R"]:
             for D in d["D"]:
                 for W in d["W"]:
-                    for SN, TL in ((sn, tl) for sn in d["SN"] for tl in d["TL"]):
+                    for SN, TL, KS in ((sn, tl, ks) for sn in d["SN"] for tl in d["TL"]
+                                       for ks in d["KS"]):
                         if TL and (SN == 1 or W != 2048 or MB >= 4 or M > 32):
                             continue  # the tail grid ignores W; decode rows only
+                        if TL and KS > 1:
+                            continue  # the tail grid takes whole k
                         q = dict(MB=0 if M == 1 else MB, R=R, D=D, W=W, BFMT=b)
                         if SN > 1:
                             q["SN"] = SN
                         if TL:
                             q["TL"] = 1
+                        if KS > 1:
+                            q["KS"] = KS
                         if MB >= 4 and M > 32:  # the shipped launchers' bound: 256 VGPRs
                             q["SN"] = SN
                             q["TPB"] = 512

@@ -14,14 +14,19 @@ The pattern is the reference's dispatch consistency gate
 """
 
 FP16 = [
+    ("l0r1d2", 1, 3840, 15360),
     ("l0r1d3", 1, 15360, 3840),
-    ("l0r1d3", 1, 3840, 15360),
     ("s1a_r1u4", 1, 512, 65792),
     ("l1r1n4d3", 8, 15360, 3840),
-    ("l1r1d4", 16, 3840, 15360),
+    ("l1r1n4d4k8", 16, 3840, 15360),        # 60 workgroups x 8 k slices
+    ("l1r1n4d4k8", 5, 3840, 12288),         # ragged M, 12 steps per slice
+    ("l1r1n4d4k8", 16, 3840, 12416),        # 97 steps (prime): no slices (no workspace)
+    ("l1r1d4", 16, 3840, 3840),
     ("s16r1u4", 16, 512, 65792),
     ("l2r1n4d4", 24, 15360, 3840),
-    ("l2r1d4", 32, 3840, 15360),
+    ("l2r1n4d3k8", 32, 3840, 15360),
+    ("l2r1n4d3k8", 20, 3840, 12288),
+    ("l2r1d4", 32, 3840, 3840),
     ("s32r1u4", 32, 512, 65792),
     ("l4r1n4d3", 64, 15360, 3840),
     ("i64x192k64s3w256", 64, 3840, 15360),  # the C2 decode-sweep point M = 64, N = 3840
@@ -67,23 +72,36 @@ FP16_GATE_UP = [
 
 W8 = {
     1: [
-        ("l0r1n2d5", 1, 5120, 17408),
+        ("l0r1d2k8", 1, 5120, 17408),     # 320 slabs x 4 k slices
+        ("l0r1d2k8", 1, 4096, 16384),     # 256 slabs: no slices (no workspace)
+        ("l0r1n2d2", 1, 5120, 6144),
+        ("l0r1d2", 1, 1024, 5120),
         ("l0r1d4", 1, 7168, 5120),
         ("l1r1n4d2t", 16, 34816, 5120),
         ("l1r1n4d2t", 16, 16400, 256),    # one remaining slab
         ("l1r1n4d2t", 9, 16384, 384),     # whole rounds, no tail
         ("l1r1n4d3", 16, 15360, 5120),    # too few slabs for a round of the tail grid
-        ("l1r1n2d4", 16, 5120, 17408),
+        ("l1r1n4d2k8", 16, 5120, 17408),
+        ("l1r1n4d2k8", 3, 5120, 12288),   # ragged M
+        ("l1r1d2k8", 16, 1024, 5120),
+        ("l1r1d2k8", 7, 1024, 1024),      # 8 steps: no slices (no workspace)
+        ("l1r1n2d2", 16, 5120, 6144),
+        ("l1r1n2d2", 16, 7168, 5120),
         ("l2r1n8d2t", 32, 34816, 5120),
         ("l2r1n8d2t", 17, 32784, 256),    # one remaining slab
         ("l2r1n8d2t", 32, 36864, 128),    # one slab per CU remaining, a single k step
         ("l2r1n4d4", 32, 15360, 5120),
-        ("l2r1n2d4", 32, 5120, 6144),
+        ("l2r1n8d3k8", 32, 5120, 17408),
+        ("l2r1n8d3k8", 25, 5120, 12288),
+        ("l2r1d2k8", 32, 1024, 5120),
+        ("l2r1n4d2k8", 32, 5120, 6144),
+        ("l2r1n4d2k8", 30, 7168, 6144),
+        ("l2r1n2d4", 32, 5152, 5120),     # N % 64 == 32
         ("s1a_r1u8", 1, 512, 66048),
         ("s1a_r1u4", 1, 512, 65792),
         ("s8r2u4", 8, 512, 65792),
         ("h16r1u4n2", 16, 512, 65792),
-        ("s16r1u4", 16, 1040, 5120),
+        ("s16r1u4", 16, 2064, 5120),      # N % 32 == 16, past the narrow-N row
         ("h32r1u4n2", 32, 512, 65792),
         ("l4r1n4d3", 64, 34816, 5120),
         ("i8x128x256s3w256", 64, 5120, 17408),
@@ -101,22 +119,36 @@ W8 = {
         ("m256x256k64", 512, 2048, 5184),
     ],
     2: [
+        ("l0r1d2k8", 1, 5120, 17408),
+        ("l0r1d2k8", 1, 4096, 16384),
+        ("l0r1n2d2", 1, 5120, 5120),
+        ("l0r1d2", 1, 1024, 5120),
         ("l0r1d4", 1, 7168, 5120),
         ("l1r1n4d2t", 16, 34816, 5120),
         ("l1r1n4d2t", 16, 16400, 256),    # one remaining slab
         ("l1r1n4d2t", 9, 16384, 384),     # whole rounds, no tail
         ("l1r1n4d3", 16, 15360, 5120),    # too few slabs for a round of the tail grid
-        ("l1r1n2d4", 16, 5120, 17408),
+        ("l1r1n4d2k8", 16, 5120, 17408),
+        ("l1r1n4d2k8", 3, 5120, 12288),   # ragged M
+        ("l1r1d2k8", 16, 1024, 5120),
+        ("l1r1d2k8", 7, 1024, 1024),      # 8 steps: no slices (no workspace)
+        ("l1r1n2d2", 16, 5120, 6144),
+        ("l1r1n2d2", 16, 7168, 5120),
         ("l2r1n8d2t", 32, 34816, 5120),
         ("l2r1n8d2t", 17, 32784, 256),    # one remaining slab
         ("l2r1n8d2t", 32, 36864, 128),    # one slab per CU remaining, a single k step
         ("l2r1n4d4", 32, 15360, 5120),
-        ("l2r1n2d4", 32, 5120, 6144),
+        ("l2r1n8d2k8", 32, 5120, 17408),
+        ("l2r1n8d2k8", 25, 5120, 12288),
+        ("l2r1d2k8", 32, 1024, 5120),
+        ("l2r1n4d2k8", 32, 5120, 6144),
+        ("l2r1n4d2k8", 30, 7168, 6144),
+        ("l2r1n2d4", 32, 5152, 5120),     # N % 64 == 32
         ("s1a_r1u8", 1, 512, 66048),
         ("s1a_r1u4", 1, 512, 65792),
         ("s8r2u4", 8, 512, 65792),
         ("h16r1u4n2", 16, 512, 65792),
-        ("s16r1u4", 16, 1040, 5120),
+        ("s16r1u4", 16, 2064, 5120),      # N % 32 == 16, past the narrow-N row
         ("h32r1u4n2", 32, 512, 65792),
         ("l4r1n4d3", 64, 34816, 5120),
         ("i8x128x256s3w256", 64, 5120, 17408),

@@ -167,14 +167,20 @@ def test_rows_fall_through_when_the_first_row_does_not_fit():
     assert capi.route(1, 16, 34816, 5120) == "l1r1n4d2t"
     assert capi.route(1, 16, 15360, 5120) == "l1r1n4d3"  # too few slabs for the tail grid
     assert capi.route(1, 16, 69632, 5120) == "l1r1n4d3"  # 5 workgroups of 4 waves per CU
-    assert capi.route(2, 16, 5120, 17408) == "l1r1n2d4"
+    assert capi.route(2, 16, 5120, 17408) == "l1r1n4d2k8"   # long K: the k-slice row
+    assert capi.route(2, 16, 5120, 6144) == "l1r1n2d2"
+    assert capi.route(2, 16, 1024, 5120) == "l1r1d2k8"     # narrow N
+    assert capi.route(1, 32, 5120, 5120) == "l2r1n2d4"     # K < 6144: past the k-slice row
     assert capi.route(1, 32, 34816, 5120) == "l2r1n8d2t"
     assert capi.route(2, 32, 34816, 16384) == "l2r1n4d4"  # fmt 2 metadata: not co-resident
     assert capi.route(2, 32, 34816, 65536 + 256) == "h32r1u4n2"
     assert capi.route(0, 1, 15360, 3840) == "l0r1d3"
-    assert capi.route(1, 1, 5120, 5120) == "l0r1n2d5"
-    assert capi.route(2, 1, 5120, 5120) == "l0r1d4"     # the D = 5 row is int8 only
+    assert capi.route(0, 1, 3840, 15360) == "l0r1d2"    # long K
+    assert capi.route(1, 1, 5120, 5120) == "l0r1n2d2"
+    assert capi.route(2, 1, 5120, 5120) == "l0r1n2d2"
+    assert capi.route(1, 1, 5120, 17408) == "l0r1d2k8"  # long K: k slices
     assert capi.route(1, 1, 7168, 5120) == "l0r1d4"     # past its N band
+    assert capi.route(1, 1, 1024, 5120) == "l0r1d2"     # narrow N
     assert capi.route(1, 1, 5120, 65536 + 512) == "s1a_r1u8"
     assert capi.route(1, 1, 5120, 65536 + 256) == "s1a_r1u4"   # K % 512 != 0, K % 256 == 0
     assert capi.route(0, 4096, 15360, 3840) == "i256x256k64w4r8"
