@@ -35,7 +35,7 @@ static hipError_t run(const TempoFmhaParams& p, hipStream_t s) {
   const int nqb = (p.Sq + fmha::BQ - 1) / fmha::BQ;
   const dim3 grid((unsigned)nqb * p.H * p.B), blk(256);
   const float scale_log2 = p.scale * 1.4426950408889634f;
-  hipLaunchKernelGGL((fmha::k_fmha_fwd4<D, CAUSAL>), grid, blk, 0, s,
+  hipLaunchKernelGGL((fmha::k_fmha_fwd<D, CAUSAL>), grid, blk, 0, s,
                      static_cast<const _Float16*>(p.Q), static_cast<const _Float16*>(p.K),
                      static_cast<const _Float16*>(p.V), static_cast<_Float16*>(p.O), p.LSE, p.B,
                      p.H, p.Hkv, p.Sq, p.Sk, scale_log2, p.q_sb, p.q_ss, p.q_sh, p.k_sb, p.k_ss,

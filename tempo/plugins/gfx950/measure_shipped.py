@@ -171,7 +171,7 @@ def counter_pass(op: str, segfile: str, quick: bool = False) -> int:
         # a split-K row dispatches two kernels per launch: its main kernel, then the reduction
         per = 1 if op == "fmha" or capi.workspace_bytes(fmt, M, N, K) == 0 else 2
         segs.append(dict(label=label_of(M, N, K, fmt), count=REPS * per, per_launch=per,
-                         route=capi.route(fmt, M, N, K) if op != "fmha" else "k_fmha_fwd4"))
+                         route=capi.route(fmt, M, N, K) if op != "fmha" else "k_fmha_fwd"))
     with open(segfile, "w") as f:
         json.dump(segs, f, indent=1)
     return 0

@@ -73,29 +73,46 @@ __device__ __forceinline__ void fmha_buf_lds16(const void* base, unsigned nrec, 
 }
 
 // ============================================================================================
-// k_fmha_fwd4 -- software-pipelined over 32-key blocks: iteration kb computes S(kb+1) = K(kb+1).Q^T
-// on the matrix cores while the VALU turns S(kb) into P(kb) (max, exponentials, sums), then
-// O^T += V(kb)^T . P(kb)^T.  K runs one block ahead of V: K(kb+2) and V(kb+1) are copied during
-// iteration kb into the slots K(kb) and V(kb-1) left (two K and two V slots).  Laid out for one
-// wave per SIMD (the 128 O accumulators, Q and the fragments take ~376 registers), where
-// nothing but the wave's own instruction order hides a latency:
-//   * one LDS array per slot (K0, K1, V0, V1) and the key loop unrolled by two, so every slot is
-//     a compile-time choice: the compiler's LDS alias scopes then keep the reads of one slot
-//     from waiting for the copies in flight into the other (one shared array made every V read
-//     wait for all outstanding copies, s_waitcnt vmcnt(0), every key block);
-//   * the score chain of block kb+1 is cut into DS chunks, one MFMA each, fenced with
-//     sched_barrier; each chunk also issues the next K fragment read (KP ahead), one pair of
-//     transposed V reads for the PV step of block kb, and one slice of block kb's softmax --
-//     row max, the cross-half exchange, and the exponentials against the running reference,
-//     computed speculatively and pinned into their chunk (the causal mask of the last blocks is
-//     applied before the chain, behind one uniform branch);
-//   * then the rare move of the reference (ballot): O and l rescaled in place in the
-//     accumulator registers and the exponentials redone; then the 2 DB PV MFMAs back to back.
-// Every sum is taken in a fixed order (the row max and sums, then P.V by k-step), so results do
-// not depend on the schedule.
+// k_fmha_fwd -- software-pipelined over 32-key blocks, laid out for one wave per SIMD (the 128 O
+// accumulators, Q and the fragments take ~440 registers), where nothing but the wave's own
+// instruction order hides a latency.
+//
+// Iteration kb computes, on the matrix cores, S(kb+1) = K(kb+1).Q^T and O^T += V(kb-1)^T .
+// P(kb-1)^T, while the VALU turns S(kb) into P(kb) (row max, exponentials, sums):
+//   * the chain of iteration kb is cut into DS chunks fenced with sched_barrier; each chunk
+//     holds one score MFMA, one P.V MFMA, the K fragment read KP chunks ahead, the transposed V
+//     pair read VP chunks ahead, and one slice of the softmax of block kb (chunk 2: row max,
+//     chunk 3: the exchange with lane ^ 32, the others: the exponentials against the running
+//     reference, computed speculatively and pinned into their chunk), so the exponentials run
+//     in the matrix pipe's shadow;
+//   * P(kb) lives in registers until the next iteration consumes it (two P sets, alternating;
+//     the scores likewise), so the P.V product of a block runs one iteration after its
+//     softmax, interleaved with the next block's scores;
+//   * after the chain, the rare move of the reference (ballot): O and l rescaled in place in
+//     the accumulator registers -- O then holds P(0..kb-1).V, all relative to the old reference
+//     -- and the exponentials of block kb redone against the new one; after the last block
+//     one more P.V step (the last block's) runs on its own.
+//
+// K and V travel by LDS-DMA two blocks at a time, two blocks ahead.  Each operand has four
+// block slots (two pairs); K blocks are paired as (2c+1, 2c+2), V blocks as (2c-1, 2c), so both
+// pairs held by one slot pair are read by the same two iterations (2c, 2c+1) and are free after
+// the second.  Every EVEN iteration kb starts with one wait (this wave's copies, issued two
+// iterations earlier, have landed) and one workgroup barrier (everyone's have, and every wave
+// is done with the slots about to be refilled), then copies K(kb+3), K(kb+4) and V(kb+1),
+// V(kb+2) into the slots the previous two iterations read; odd iterations neither wait nor
+// synchronise.  Block j of K lives in slot (j - 1) % 4, block j of V in slot (j + 1) % 4, so
+// iteration kb reads slot kb % 4 of both.  One LDS array per slot and a four-iteration loop
+// body make every slot a compile-time choice: the compiler's LDS alias scopes then keep the
+// reads of one slot from waiting for the copies in flight into another (with one shared array
+// every read waited for all outstanding copies).  The four-body loop is written as a counted
+// for-loop with a phased tail: a while-loop with a break after every body made the register
+// allocator spill Q and the accumulators.
+//
+// Every sum is taken in a fixed order (the row max and sums, then P.V by key block and, within
+// a block, k-step 0 then 1), so results do not depend on the schedule.
 // ============================================================================================
 template <int D, bool CAUSAL>
-__global__ __launch_bounds__(256, 1) void k_fmha_fwd4(
+__global__ __launch_bounds__(256, 1) void k_fmha_fwd(
     const _Float16* __restrict__ Q, const _Float16* __restrict__ Kg,
     const _Float16* __restrict__ Vg, _Float16* __restrict__ O, float* __restrict__ LSE, int B,
     int H, int Hkv, int Sq, int Sk, float scale_log2, long q_sb, long q_ss, long q_sh, long k_sb,
@@ -113,14 +130,19 @@ __global__ __launch_bounds__(256, 1) void k_fmha_fwd4(
   constexpr int BQW = 32 * WAVES;
   constexpr int TILE_B = BKV2 * RB;
   constexpr int KP = 4;        // K fragment reads ahead of the chain
+  constexpr int VP = 2;        // V pair reads ahead of their P.V MFMA
   constexpr int NX = DS - 4;   // chunks carrying exponentials (chunks 2-3: max, exchange)
   static_assert(DS >= 8 && 2 * DB == DS, "one V pair per chunk");
   static_assert(BLK % WAVES == 0, "DMA blocks split over the waves");
 
   __shared__ __attribute__((aligned(1024))) char k0s[TILE_B];
   __shared__ __attribute__((aligned(1024))) char k1s[TILE_B];
+  __shared__ __attribute__((aligned(1024))) char k2s[TILE_B];
+  __shared__ __attribute__((aligned(1024))) char k3s[TILE_B];
   __shared__ __attribute__((aligned(1024))) char v0s[TILE_B];
   __shared__ __attribute__((aligned(1024))) char v1s[TILE_B];
+  __shared__ __attribute__((aligned(1024))) char v2s[TILE_B];
+  __shared__ __attribute__((aligned(1024))) char v3s[TILE_B];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -168,11 +190,11 @@ __global__ __launch_bounds__(256, 1) void k_fmha_fwd4(
     vsrc[i] = (unsigned)(r * v_ss * 2 + c * 16);
   }
   // block j of one operand into the slot array dst; rows past Sk re-read row Sk-1.  The buffer
-  // starts at the block's first row and ends with row Sk-1 (every offset below is inside it).
+  // starts at the block's first row and ends with row Sk-1 (every offset below is inside it;
+  // capped at 2^32 - 1: every offset used is below 32 rows x ss x 2 < 2^31).
   auto copy_block = [&](const char* base, long ss, const unsigned* src, char* dst, int j) {
     const int j0 = j * BKV2;
     const char* blk = base + (long)j0 * ss * 2;
-    // (capped at 2^32 - 1: every offset used is below 32 rows x ss x 2 < 2^31)
     const long span = (long)(Sk - 1 - j0) * ss * 2 + D * 2;
     const unsigned nrec = span < 0xFFFFFFFFL ? (unsigned)span : 0xFFFFFFFFu;
     if (j0 + BKV2 <= Sk) {
@@ -188,13 +210,19 @@ __global__ __launch_bounds__(256, 1) void k_fmha_fwd4(
       }
     }
   };
-  auto kslot = [&](auto par) -> char* {
-    if constexpr (decltype(par)::value) return k1s;
-    else return k0s;
+  auto kslot = [&](auto sl) -> char* {
+    constexpr int S4 = decltype(sl)::value % 4;
+    if constexpr (S4 == 0) return k0s;
+    else if constexpr (S4 == 1) return k1s;
+    else if constexpr (S4 == 2) return k2s;
+    else return k3s;
   };
-  auto vslot = [&](auto par) -> char* {
-    if constexpr (decltype(par)::value) return v1s;
-    else return v0s;
+  auto vslot = [&](auto sl) -> char* {
+    constexpr int S4 = decltype(sl)::value % 4;
+    if constexpr (S4 == 0) return v0s;
+    else if constexpr (S4 == 1) return v1s;
+    else if constexpr (S4 == 2) return v2s;
+    else return v3s;
   };
 
   const int kkey = fmha_swz(l32);
@@ -211,6 +239,14 @@ __global__ __launch_bounds__(256, 1) void k_fmha_fwd4(
     voff0[p4] = tk * RB + (((p4 << 2) | cd) ^ fmha_swz(tk)) * 16 + half;
     voff1[p4] = (tk + 8) * RB + (((p4 << 2) | cd) ^ fmha_swz(tk + 8)) * 16 + half;
   }
+  // V pair i of a slot: P.V k-step i / DB, d block i % DB
+  auto vread = [&](const char* vr, int i) -> f16x8 {
+    const int tt = i / DB, db = i % DB;
+    const u32x2 a = fmha_tr_read(vr + voff0[db & 3] + 16 * tt * RB + (db >> 2) * 256);
+    const u32x2 c = fmha_tr_read(vr + voff1[db & 3] + 16 * tt * RB + (db >> 2) * 256);
+    const u32x4 vv = {a[0], a[1], c[0], c[1]};
+    return as_f16x8(vv);
+  };
 
   f32x16 acc_o[DB];
 #pragma unroll
@@ -226,9 +262,6 @@ __global__ __launch_bounds__(256, 1) void k_fmha_fwd4(
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
   };
-  // exponentials e0..e1-1 of block row s into pt, summed into psum in order; the sum starts at
-  // element 0 (0 + p == p exactly for p >= 0, and a sum that starts from a zero constant was
-  // miscompiled here: the constant's register was reused inside the loop)
   auto exps = [&](const f32x16& s, float m_use, f16x8 (&pt)[2], float& psum, int e0, int e1) {
 #pragma unroll
     for (int e = e0; e < e1; ++e) {
@@ -239,32 +272,40 @@ __global__ __launch_bounds__(256, 1) void k_fmha_fwd4(
   };
 
   f32x16 sa, sb;
+  f16x8 pa[2], pb[2];
   if (nkb > 0) {
-    copy_block(Kp, k_ss, ksrc, k0s, 0);
-    copy_block(Vp, v_ss, vsrc, v0s, 0);
-    if (nkb > 1) copy_block(Kp, k_ss, ksrc, k1s, 1);
+    // K(0) -> slot 3, K(1), K(2) -> slots 0, 1; V(0) -> slot 1
+    copy_block(Kp, k_ss, ksrc, k3s, 0);
+    if (nkb > 1) copy_block(Kp, k_ss, ksrc, k0s, 1);
+    if (nkb > 2) copy_block(Kp, k_ss, ksrc, k1s, 2);
+    copy_block(Vp, v_ss, vsrc, v1s, 0);
     sync_top();
 #pragma unroll
     for (int r = 0; r < 16; ++r) sa[r] = 0.f;
 #pragma unroll
     for (int st = 0; st < DS; ++st) {
-      const f16x8 kf = *reinterpret_cast<const f16x8*>(k0s + koff[st & 7] + (st >> 3) * 256);
+      const f16x8 kf = *reinterpret_cast<const f16x8*>(k3s + koff[st & 7] + (st >> 3) * 256);
       sa = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[st], sa, 0, 0, 0);
     }
   }
-  // iteration kb (parity P = kb % 2): K(kb+1) in slot 1-P and V(kb) in slot P are resident;
-  // copy K(kb+2) -> slot P, V(kb+1) -> slot 1-P; S(kb+1) = K(kb+1).Q^T || softmax of S(kb);
-  // O += V(kb)^T . P(kb)^T.  The scores of a block past the end read a stale slot and are
-  // never used.
-  auto iter4 = [&](auto par, f32x16& cur, f32x16& nxt, int kb) {
-    constexpr int P = decltype(par)::value;
-    sync_top();
-    if (kb + 2 < nkb) copy_block(Kp, k_ss, ksrc, kslot(IC<P>{}), kb + 2);
-    if (kb + 1 < nkb) copy_block(Vp, v_ss, vsrc, vslot(IC<1 - P>{}), kb + 1);
-    const char* const kr = kslot(IC<1 - P>{});
-    const char* const vr = vslot(IC<P>{});
-    // mask of the current block (the last blocks only; one uniform branch): key c of this
-    // lane's half is hidden iff c > lim
+  // iteration kb (phase T = kb % 4; FIRST: kb = 0): K(kb+1) and V(kb-1) are resident in slot
+  // T; an even iteration first waits for its copies of two iterations ago and synchronises,
+  // then copies K(kb+3), K(kb+4) -> slots T+2, T+3 and V(kb+1), V(kb+2) -> slots T+2, T+3;
+  // S(kb+1) = K(kb+1).Q^T || O += V(kb-1)^T . P(kb-1)^T (ppv) || softmax of S(kb) -> P(kb)
+  // (pcur).  The scores of a block past the end read a stale slot and are never used.
+  auto iter = [&](auto phase, auto first, f32x16& cur, f32x16& nxt, const f16x8 (&ppv)[2],
+                   f16x8 (&pcur)[2], int kb) {
+    constexpr int T = decltype(phase)::value;
+    constexpr bool FIRST = decltype(first)::value;
+    if constexpr (T % 2 == 0) {
+      sync_top();
+      if (kb + 3 < nkb) copy_block(Kp, k_ss, ksrc, kslot(IC<T + 2>{}), kb + 3);
+      if (kb + 4 < nkb) copy_block(Kp, k_ss, ksrc, kslot(IC<T + 3>{}), kb + 4);
+      if (kb + 1 < nkb) copy_block(Vp, v_ss, vsrc, vslot(IC<T + 2>{}), kb + 1);
+      if (kb + 2 < nkb) copy_block(Vp, v_ss, vsrc, vslot(IC<T + 3>{}), kb + 2);
+    }
+    const char* const kr = kslot(IC<T>{});
+    const char* const vr = vslot(IC<T>{});
     const int j0 = kb * BKV2;
     if ((j0 + BKV2 > Sk) || (CAUSAL && j0 + BKV2 - 1 > q0 + off)) {
       const int lim = (CAUSAL ? min(Sk - 1, qi + off) : Sk - 1) - j0 - 4 * hl;
@@ -274,25 +315,29 @@ __global__ __launch_bounds__(256, 1) void k_fmha_fwd4(
     }
     const float m_use0 = (m_run == -__builtin_inff()) ? 0.f : m_run;
     f16x8 kf[DS];
-    u32x2 vp[DS][2];  // V pair i: PV step i / DB, d block i % DB
-    f16x8 pt[2];
+    f16x8 vf[DS];
     float mx = -__builtin_inff(), mxs = 0.f, psum;
 #pragma unroll
     for (int st = 0; st < KP; ++st)
       kf[st] = *reinterpret_cast<const f16x8*>(kr + koff[st & 7] + (st >> 3) * 256);
+    if constexpr (!FIRST) {
+#pragma unroll
+      for (int i = 0; i < VP; ++i) vf[i] = vread(vr, i);
+    }
 #pragma unroll
     for (int r = 0; r < 16; ++r) nxt[r] = 0.f;
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int c = 0; c < DS; ++c) {
       nxt = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[c], qf[c], nxt, 0, 0, 0);
+      if constexpr (!FIRST)
+        acc_o[c % DB] =
+            __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[c], ppv[c / DB], acc_o[c % DB], 0, 0, 0);
       if (c + KP < DS)
         kf[c + KP] =
             *reinterpret_cast<const f16x8*>(kr + koff[(c + KP) & 7] + ((c + KP) >> 3) * 256);
-      {
-        const int tt = c / DB, db = c % DB;
-        vp[c][0] = fmha_tr_read(vr + voff0[db & 3] + 16 * tt * RB + (db >> 2) * 256);
-        vp[c][1] = fmha_tr_read(vr + voff1[db & 3] + 16 * tt * RB + (db >> 2) * 256);
+      if constexpr (!FIRST) {
+        if (c + VP < DS) vf[c + VP] = vread(vr, c + VP);
       }
       if (c == 2) {
 #pragma unroll
@@ -300,10 +345,8 @@ __global__ __launch_bounds__(256, 1) void k_fmha_fwd4(
       } else if (c == 3) {
         mxs = fmaxf(mx, __shfl_xor(mx, 32)) * scale_log2;
       } else {
-        exps(cur, m_use0, pt, psum, 16 * (c - 4) / NX, 16 * (c - 3) / NX);
-        // keep the slice in this chunk: otherwise the speculative exponentials are sunk past
-        // the branch below, out of the matrix pipe's shadow
-        asm volatile("" : "+v"(psum), "+v"(pt[0]), "+v"(pt[1]));
+        exps(cur, m_use0, pcur, psum, 16 * (c - 4) / NX, 16 * (c - 3) / NX);
+        asm volatile("" : "+v"(psum), "+v"(pcur[0]), "+v"(pcur[1]));
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -313,8 +356,8 @@ __global__ __launch_bounds__(256, 1) void k_fmha_fwd4(
           (m_new == -__builtin_inff()) ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
       l_run *= alpha;
       m_run = m_new;
-      // in place in the accumulator registers (a plain multiply makes the register allocator
-      // keep a VGPR copy of all of O across the loop for this rare branch)
+      // the chain's last P.V MFMAs write O: wait states before the accumulators are read
+      asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
 #pragma unroll
       for (int i = 0; i < DB; ++i)
 #pragma unroll
@@ -326,22 +369,40 @@ __global__ __launch_bounds__(256, 1) void k_fmha_fwd4(
               : "v"(alpha));
           acc_o[i][r] = x;
         }
-      exps(cur, (m_run == -__builtin_inff()) ? 0.f : m_run, pt, psum, 0, 16);
+      exps(cur, (m_run == -__builtin_inff()) ? 0.f : m_run, pcur, psum, 0, 16);
     }
     l_run += psum + __shfl_xor(psum, 32);
-#pragma unroll
-    for (int i = 0; i < DS; ++i) {
-      const u32x4 vv = {vp[i][0][0], vp[i][0][1], vp[i][1][0], vp[i][1][1]};
-      acc_o[i % DB] =
-          __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(vv), pt[i / DB], acc_o[i % DB], 0, 0, 0);
-    }
   };
-  int kb = 0;
-  for (; kb + 1 < nkb; kb += 2) {
-    iter4(IC<0>{}, sa, sb, kb);
-    iter4(IC<1>{}, sb, sa, kb + 1);
+  // the P.V step of the last block (V(nkb-1) in slot nkb % 4)
+  auto pv_last = [&](const f16x8 (&pl)[2]) {
+    sync_top();
+    const int t4 = nkb & 3;
+    const char* const vr = t4 == 0 ? v0s : t4 == 1 ? v1s : t4 == 2 ? v2s : v3s;
+#pragma unroll
+    for (int i = 0; i < DS; ++i)
+      acc_o[i % DB] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vread(vr, i), pl[i / DB],
+                                                             acc_o[i % DB], 0, 0, 0);
+  };
+  if (nkb > 0) {
+    iter(IC<0>{}, IC<1>{}, sa, sb, pb, pa, 0);
+    int kb = 1;
+    for (; kb + 3 < nkb; kb += 4) {
+      iter(IC<1>{}, IC<0>{}, sb, sa, pa, pb, kb);
+      iter(IC<2>{}, IC<0>{}, sa, sb, pb, pa, kb + 1);
+      iter(IC<3>{}, IC<0>{}, sb, sa, pa, pb, kb + 2);
+      iter(IC<0>{}, IC<0>{}, sa, sb, pb, pa, kb + 3);
+    }
+    // the last 0-3 blocks continue the phase sequence 1, 2, 3
+    if (kb < nkb) {
+      iter(IC<1>{}, IC<0>{}, sb, sa, pa, pb, kb);
+      if (kb + 1 < nkb) {
+        iter(IC<2>{}, IC<0>{}, sa, sb, pb, pa, kb + 1);
+        if (kb + 2 < nkb) iter(IC<3>{}, IC<0>{}, sb, sa, pa, pb, kb + 2);
+      }
+    }
+    if (nkb & 1) pv_last(pa);
+    else pv_last(pb);
   }
-  if (kb < nkb) iter4(IC<0>{}, sa, sb, kb);
 
   if (qi < Sq) {
     const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
@@ -362,5 +423,7 @@ __global__ __launch_bounds__(256, 1) void k_fmha_fwd4(
           l_run > 0.f ? m_run * 0.6931471805599453f + __logf(l_run) : -__builtin_inff();
   }
 }
+
+
 
 }  // namespace fmha
