@@ -46,7 +46,8 @@ class Gfx950Plugin:
     def declared_stubs(self):
         return (
             "HBM.STREAM_READ is NOT_MEASURED in the rate table until a clean-card run records it "
-            "with its CardState; the bound therefore has no HBM channel and is loose for decode",
+            "with its CardState; the bound's HBM channel uses each CU's share of the spec peak "
+            "(CAP.HBM_SHARE), so it is loose for decode",
             "clock locking (Meters.clock_lock) is not offered: clocks are recorded, not set",
             "classifier.control_fields: the AMD ISA has no scheduling control words",
             "FMHA is a fixed skeleton (skeletons/fmha_fwd), outside the searched space",
