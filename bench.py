@@ -258,7 +258,8 @@ def decode_lines(steps):
 def gate_up_lines(steps):
     """The fused gate/up epilogue on the production gate_up shape (2N = 34816, K = 5120; both
     W8A16 formats and fp16 weights) against the unfused chain on the same stream: the plain
-    shipped GEMM into [M, 2N], then torch's silu and product."""
+    shipped GEMM into [M, 2N], then torch's silu and product.  Decode M (the streaming kernels)
+    and prefill M (the interleaved kernels' fused epilogue)."""
     import torch
     import torch.nn.functional as F
     from cuda_tempiler_amd import capi
@@ -284,7 +285,7 @@ def gate_up_lines(steps):
                 W.append(torch.randint(0, 256, (2 * N, K), dtype=torch.uint8, device="cuda:0"))
                 S.append(torch.empty((2 * N, K // G), dtype=torch.float16, device="cuda:0").uniform_(0.5, 1.5) / 255)
                 Z.append(torch.randint(100, 157, (2 * N, K // G), dtype=torch.uint8, device="cuda:0"))
-        for M in (1, 16, 32):
+        for M in (1, 16, 32, 128, 2048):
             A = torch.randn((M, K), dtype=torch.float16, device="cuda:0") / K ** 0.5
             C = torch.empty((M, N), dtype=torch.float16, device="cuda:0")
             T = torch.empty((M, 2 * N), dtype=torch.float16, device="cuda:0")
@@ -307,10 +308,12 @@ def gate_up_lines(steps):
             ms_u = time_launches(unfused, steps, max(10, steps // 5), stream)
             byts = nb + 2 * M * K + 2 * M * N
             gbps = byts / (ms_f * 1e-3) / 1e9
+            tf = 2.0 * M * (2 * N) * K / (ms_f * 1e-3) / 1e12
             out.append({"op": "gate_up", "fmt": ["fp16", "sym_i8", "asym_u8_g128"][fmt],
                         "M": M, "N": N, "K": K, "us": round(ms_f * 1e3, 2),
                         "unfused_us": round(ms_u * 1e3, 2), "speedup": round(ms_u / ms_f, 3),
                         "GBps": round(gbps, 1), "hbm_frac": round(gbps / PEAK_HBM_GBPS, 4),
+                        "TFLOPs": round(tf, 1), "mfma_frac": round(tf / PEAK_FP16_TFLOPS, 4),
                         "route": capi.route(3 + fmt, M, N, K)})
         del W, S, Z
     return out

@@ -49,8 +49,12 @@ def instantiation(kind, p, epi=0):
                                                     p.get("TPB", 1024), tail)
     if kind == "stream":
         return "launch_stream<%d,%d,%d,%d%s>" % (p["MB"], p["R"], p["U"], p.get("A", 0), tail)
+    if epi and kind == "ilv":
+        return "launch_ilv_gu<%d,%d,%d,%d,%d,%d,%d,%d,%d>" % (
+            p["BM"], p["BN"], p["BK"], p["WM"], p["WN"], p["STAGES"], p["GROUP"], p["XCD"],
+            p["RSP"])
     if epi:
-        raise ValueError("the fused gate/up epilogue exists for the stream kernels only")
+        raise ValueError("the fused gate/up epilogue exists for the stream and interleaved kernels")
     if kind == "ilv":
         return "launch_ilv<%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d>" % (
             p["BM"], p["BN"], p["BK"], p["WM"], p["WN"], p["STAGES"], p["GROUP"], p["XCD"],
@@ -81,7 +85,8 @@ def condition(sel, kind, p, m_max, n_min=0, gate_up=False):
                                                           sel.STREAM_K_STEP * p["U"])
     elif kind == "ilv":  # an even number of 32-k substeps; 31-bit panel byte offsets
         fit = "(p.N %% %d) == 0 && (p.K %% %d) == 0 && p.lda <= %d && p.ldb <= %d" % (
-            p["BN"], max(64, p["BK"]), sel.ilv_ld_max(p), sel.ilv_ld_max(p))
+            p["BN"] // 2 if gate_up else p["BN"], max(64, p["BK"]), sel.ilv_ld_max(p),
+            sel.ilv_ld_max(p))
         if "NMAX" in p:
             fit += " && p.N < %d" % p["NMAX"]
     else:
@@ -125,10 +130,11 @@ def render_prefill() -> str:
     sel = _select()
     out = [HEAD_PREFILL]
     seen = set()
-    for _m, _n, _tag, kind, p in sel.LADDER:
+    for _m, _n, _tag, kind, p, epi in ([r + (0,) for r in sel.LADDER]
+                                       + [r + (1,) for r in sel.LADDER_GATE_UP]):
         if kind != "ilv":
             continue
-        inst = instantiation(kind, p)
+        inst = instantiation(kind, p, epi)
         if inst in seen:
             continue
         seen.add(inst)

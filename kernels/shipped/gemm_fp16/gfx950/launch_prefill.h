@@ -36,5 +36,21 @@ hipError_t launch_ilv(const GemmParams& p, hipStream_t s, const Workspace& w) {
   return launch_reduce(ws, splits, p.M, p.N, p.C, p.ldc, s);
 }
 
+// Fused gate/up (EPI = 1): p.N is the output width and B holds 2N rows (gate, then up); each
+// tile covers BN/2 output columns.  No split-K, no workspace.
+template <int BM, int BN, int BK, int WM, int WN, int STAGES, int GROUP, int XCD, int RSP>
+hipError_t launch_ilv_gu(const GemmParams& p, hipStream_t s, const Workspace& w) {
+  if (w.need) {
+    *w.need = 0;
+    return hipSuccess;
+  }
+  const int nm = (p.M + BM - 1) / BM;
+  const int nn = p.N / (BN / 2);
+  hipLaunchKernelGGL((k_gemm_ilv<BM, BN, BK, WM, WN, STAGES, GROUP, XCD, RSP, 0, 1>),
+                     dim3(nm * nn), dim3(WM * WN * 64), 0, s, p.A, p.B, p.C, p.M, p.N, p.K, p.lda,
+                     p.ldb, p.ldc, static_cast<float*>(nullptr), 1);
+  return hipGetLastError();
+}
+
 }  // namespace gen
 }  // namespace tempo

@@ -75,9 +75,10 @@ LADDER = [
 
 # Fused gate/up ladder (C = silu(A.B[0..N)^T) * (A.B[N..2N)^T), N = output width): the decode
 # kernels with EPI = 1 (shared: the slab waves pair up, gate and up; stream: each wave carries
-# the gate and the up row groups of its slab).  Rows measured on (N, K) = (17408, 5120) and
-# (7680, 3840) against the plain GEMM + a separate silu*mul kernel.  M > 32 is not covered: the
-# caller runs the plain GEMM and its own elementwise step.
+# the gate and the up row groups of its slab), rows measured on (N, K) = (17408, 5120) and
+# (7680, 3840) against the plain GEMM + a separate silu*mul kernel; then the interleaved prefill
+# kernel with EPI = 1 (each tile holds BN/2 gate and the BN/2 matching up rows of B, and pairs
+# them in the epilogue) for every M.
 LADDER_GATE_UP = [
     (1, 0, "gl0r1n2d3", "line", dict(MB=0, R=1, D=3, SN=2, W=2048)),
     (16, 12288, "gl1r1n4d3", "line", dict(MB=1, R=1, D=3, SN=4, W=2048)),
@@ -88,6 +89,10 @@ LADDER_GATE_UP = [
     (16, 0, "gh16r1u4n2", "shared", dict(MB=1, R=1, U=4, SN=2, TPB=512)),
     (32, 0, "gh32r1u4n4", "shared", dict(MB=2, R=1, U=4, SN=4, TPB=1024)),
     (32, 0, "g32r1u4", "stream", dict(MB=2, R=1, U=4, A=0)),
+    (128, 0, "gi128x256k64s3", "ilv",
+     dict(BM=128, BN=256, BK=64, WM=1, WN=4, STAGES=3, GROUP=8, XCD=1, RSP=8)),
+    (1 << 30, 0, "gi256x256k64w4r8", "ilv",
+     dict(BM=256, BN=256, BK=64, WM=2, WN=2, STAGES=2, GROUP=8, XCD=1, RSP=8)),
 ]
 
 # Divisibility each kind needs (checked at run time by dispatch.inc, mirrored here).
@@ -106,6 +111,8 @@ def _fits_gate_up(kind, p, M, N, K):
     if kind == "shared":
         return (p["SN"] % 2 == 0 and N % (STREAM_N_ROWS * p["R"] * p["SN"] // 2) == 0
                 and K % (STREAM_K_STEP * p["U"]) == 0)
+    if kind == "ilv":  # a tile covers BN/2 output columns
+        return N % (p["BN"] // 2) == 0 and K % max(64, p["BK"]) == 0 and K <= ilv_ld_max(p)
     return _fits(kind, p, M, N, K)
 
 

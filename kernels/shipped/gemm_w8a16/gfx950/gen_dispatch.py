@@ -51,8 +51,12 @@ def instantiation(kind, p, epi=0):
                                                     p.get("TPB", 1024), tail)
     if kind == "stream":
         return "launch_stream<%d,%d,%d,%d%s>" % (p["MB"], p["R"], p["U"], p.get("A", 0), tail)
+    if epi and kind == "ilv8":
+        return "launch_ilv8_gu<%d,%d,%d,%d,%d,%d,%d,%d,%d>" % (
+            p["BM"], p["BN"], p["BK"], p["WM"], p["WN"], p["STAGES"], p["GROUP"], p["XCD"],
+            p["RSP"])
     if epi:
-        raise ValueError("the fused gate/up epilogue exists for the stream kernels only")
+        raise ValueError("the fused gate/up epilogue exists for the stream and interleaved kernels")
     if kind == "ilv8":
         return "launch_ilv8<%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d>" % (
             p["BM"], p["BN"], p["BK"], p["WM"], p["WN"], p["STAGES"], p["GROUP"], p["XCD"],
@@ -82,7 +86,7 @@ def condition(sel, kind, p, m_max, n_min=0, gate_up=False):
                                                           sel.STREAM_K_STEP * p["U"])
     elif kind == "ilv8":  # a scale group is two k-tiles; 31-bit panel byte offsets
         fit = "(p.N %% %d) == 0 && (p.K %% 128) == 0 && p.lda <= %d && p.ldw <= %d" % (
-            p["BN"], sel.ilv_ld_max(p), sel.ilv_ld_max(p))
+            p["BN"] // 2 if gate_up else p["BN"], sel.ilv_ld_max(p), sel.ilv_ld_max(p))
         if "NMAX" in p:
             fit += " && p.N < %d" % p["NMAX"]
         if "KMIN" in p:
@@ -132,10 +136,11 @@ def render_prefill() -> str:
     sel = _select()
     out = [HEAD_PREFILL]
     seen = set()
-    for _m, _n, _tag, kind, p in sel.LADDER:
+    for _m, _n, _tag, kind, p, epi in ([r + (0,) for r in sel.LADDER]
+                                       + [r + (1,) for r in sel.LADDER_GATE_UP]):
         if kind != "ilv8":
             continue
-        inst = instantiation(kind, p)
+        inst = instantiation(kind, p, epi)
         if inst in seen:
             continue
         seen.add(inst)

@@ -278,6 +278,9 @@ inline hipError_t launch_line_ks(const W8A16Params& p, hipStream_t s, const Work
 template <int BM, int BN, int BK, int WM, int WN, int STAGES, int GROUP, int XCD, int RSP,
           int SW, int MINKT>
 hipError_t launch_ilv8(const W8A16Params& p, hipStream_t s, const Workspace& w);
+// The same kernel with the fused gate/up epilogue (p.N the output width, 2N weight rows).
+template <int BM, int BN, int BK, int WM, int WN, int STAGES, int GROUP, int XCD, int RSP>
+hipError_t launch_ilv8_gu(const W8A16Params& p, hipStream_t s, const Workspace& w);
 
 // One dispatch row: launchers without a workspace ignore it (and, asked for their need, report 0).
 inline hipError_t call_row(hipError_t (*f)(const W8A16Params&, hipStream_t), const W8A16Params& p,

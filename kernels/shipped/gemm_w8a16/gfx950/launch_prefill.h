@@ -46,5 +46,25 @@ hipError_t launch_ilv8(const W8A16Params& p, hipStream_t s, const Workspace& w) 
   return launch_reduce(ws, splits, p.M, p.N, p.C, p.ldc, s);
 }
 
+// Fused gate/up (EPI = 1): p.N is the output width; Wq, scale and zero hold 2N rows (gate, then
+// up); each tile covers BN/2 output columns.  No split-K, no workspace.
+template <int BM, int BN, int BK, int WM, int WN, int STAGES, int GROUP, int XCD, int RSP>
+hipError_t launch_ilv8_gu(const W8A16Params& p, hipStream_t s, const Workspace& w) {
+  if (w.need) {
+    *w.need = 0;
+    return hipSuccess;
+  }
+  const dim3 grid(((p.M + BM - 1) / BM) * (p.N / (BN / 2))), blk(WM * WN * 64);
+  if (p.fmt == 1)
+    hipLaunchKernelGGL((k_gemm_ilv8<BM, BN, BK, WM, WN, STAGES, GROUP, XCD, RSP, 1, 0, 1>), grid,
+                       blk, 0, s, p.A, static_cast<const uint8_t*>(p.Wq), p.scale, p.zero, p.C,
+                       p.M, p.N, p.K, p.lda, p.ldw, p.ldc, static_cast<float*>(nullptr), 1);
+  else
+    hipLaunchKernelGGL((k_gemm_ilv8<BM, BN, BK, WM, WN, STAGES, GROUP, XCD, RSP, 2, 0, 1>), grid,
+                       blk, 0, s, p.A, static_cast<const uint8_t*>(p.Wq), p.scale, p.zero, p.C,
+                       p.M, p.N, p.K, p.lda, p.ldw, p.ldc, static_cast<float*>(nullptr), 1);
+  return hipGetLastError();
+}
+
 }  // namespace gen8
 }  // namespace tempo

@@ -91,9 +91,9 @@ LADDER = [
 ]
 
 # Fused gate/up ladder (C = silu(A.deq(W)[0..N)^T) * (A.deq(W)[N..2N)^T), N = output width): the
-# decode kernels with EPI = 1 (shared: paired gate/up slab waves).  Rows measured on the
-# production gate_up shape (N, K) = (17408, 5120), both formats.  M > 32 is not covered (the
-# caller's own path).
+# decode kernels with EPI = 1 (shared: paired gate/up slab waves), rows measured on the
+# production gate_up shape (N, K) = (17408, 5120), both formats; then the interleaved int8
+# kernel with EPI = 1 for every M.
 LADDER_GATE_UP = [
     (1, 0, "gl0r1n2d4", "line", dict(MB=0, R=1, D=4, SN=2, W=2048)),
     (16, 12288, "gl1r1n4d3", "line", dict(MB=1, R=1, D=3, SN=4, W=2048)),
@@ -108,6 +108,12 @@ LADDER_GATE_UP = [
     (32, 0, "gh32r1u2n4", "shared", dict(MB=2, R=1, U=2, SN=4, TPB=1024, fmts=(1,))),
     (32, 0, "gh32r1u4n4", "shared", dict(MB=2, R=1, U=4, SN=4, TPB=512, fmts=(2,))),
     (32, 0, "g32r1u4", "stream", dict(MB=2, R=1, U=4, A=0)),
+    # M > 32 (and what the decode rows leave): the interleaved int8 kernel with EPI = 1 -- each
+    # tile holds BN/2 gate and the BN/2 matching up weight rows and pairs them in the epilogue
+    (128, 0, "gi8x128x256s3", "ilv8",
+     dict(BM=128, BN=256, BK=64, WM=1, WN=4, STAGES=3, GROUP=8, XCD=1, RSP=8)),
+    (1 << 30, 0, "gi8x256k64s3", "ilv8",
+     dict(BM=256, BN=256, BK=64, WM=2, WN=2, STAGES=3, GROUP=8, XCD=1, RSP=8)),
 ]
 
 STREAM_K_STEP = 64
@@ -150,6 +156,8 @@ def _fits_gate_up(kind, p, M, N, K, fmt=1):
     if kind == "shared":
         return (p["SN"] % 2 == 0 and N % (STREAM_N_ROWS * p["R"] * p["SN"] // 2) == 0
                 and K % (STREAM_K_STEP * p["U"]) == 0)
+    if kind == "ilv8":  # a tile covers BN/2 output columns; a scale group is two k-tiles
+        return N % (p["BN"] // 2) == 0 and K % 128 == 0 and K <= ilv_ld_max(p)
     return _fits(kind, p, M, N, K, fmt)
 
 

@@ -49,13 +49,20 @@
 // accumulators to ws[sk][M][N] (16 bytes per lane and block); k_splitk_reduce then adds the
 // splits in order and rounds once.  Narrow-N, long-K shapes get enough workgroups this way.
 //
+// EPI = 1 (fused gate/up, prefill): C[M][N] = silu(A.B[0..N)^T) * (A.B[N..2N)^T), B holding the
+// gate rows then the up rows (2N rows, N the output width).  A workgroup covers BN/2 output
+// columns: its B tile is BN/2 gate rows followed by the BN/2 matching up rows (two panels, the
+// copy blocks of each half a compile-time set), so the gate and up results of one output sit
+// in the same C tile image in LDS, BN/2 columns apart; the epilogue reads both halves back and
+// writes fp16_rn(silu(g) * u) of the fp16-rounded g and u (silu_mul_f16).  No split-K.
+//
 // Build: this kernel is compiled with -mllvm -amdgpu-sched-strategy=iterative-minreg (its own
 // translation unit).  The default pre-RA scheduler reorders the 256 accumulator chains of a
 // 128 x 128 wave tile such that the register allocator no longer keeps each accumulator in one
 // AGPR tuple, and the loop fills with v_accvgpr_read/write/mov copies.
 // ============================================================================================
 template <int BM, int BN, int BK, int WM, int WN, int STAGES, int GROUP, int XCD, int RSP,
-          int SPLIT = 0>
+          int SPLIT = 0, int EPI = 0>
 __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv(
     const _Float16* __restrict__ A, const _Float16* __restrict__ B, _Float16* __restrict__ C,
     int M, int N, int K, int lda, int ldb, int ldc, float* __restrict__ ws, int ksplit) {
@@ -76,6 +83,9 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv(
   constexpr int RSPAN = RSP > 0 && RSP < CH ? RSP : CH;
   static_assert(BM % (RPB * NW) == 0 && BN % (RPB * NW) == 0, "copy blocks per wave");
   static_assert(STAGES >= 2 && (STAGES - 1) * L < 64, "stages / vmcnt range");
+  // EPI: the gate half of the B tile is its first HB copy blocks of every wave
+  constexpr int HB = (BN / 2) / (NW * RPB);
+  static_assert(!EPI || (SPLIT == 0 && (BN / 2) % (NW * RPB) == 0), "gate/up: whole copy blocks");
   static_assert(WTM % 16 == 0 && WTN % 16 == 0 && (KS == 1 || KS == 2), "tile shape");
   // rows 16 apart (fragment blocks) and NW*RPB apart (copy blocks) share the swizzle key, so
   // one per-lane offset serves every block of an operand
@@ -88,13 +98,14 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv(
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WN, wn = wave % WN;
 
-  const int nm = (M + BM - 1) / BM, nn = N / BN;
+  constexpr int BNO = EPI ? BN / 2 : BN;  // output columns per tile
+  const int nm = (M + BM - 1) / BM, nn = N / BNO;
   int tmi, tni, sk = 0;
   if constexpr (SPLIT)
     split_tile_of<GROUP, XCD>(blockIdx.x, nm, nn, ksplit, tmi, tni, sk);
   else
     tile_of<GROUP, XCD>(blockIdx.x, nm, nn, tmi, tni);
-  const int m0 = tmi * BM, n0 = tni * BN;
+  const int m0 = tmi * BM, n0 = tni * BNO;
   // k-tiles of this workgroup: [kbase, kbase + NT)
   const int NTALL = K / BK;
   const int kper = SPLIT ? (NTALL + ksplit - 1) / ksplit : NTALL;
@@ -108,19 +119,24 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv(
   const int cchunk = lds_chunk<BK, SWZ>(crow, lane % CPR) * 8;    // element offset in the row
   const _Float16* panelA = A + (long)m0 * lda;
   const _Float16* panelB = B + (long)n0 * ldb;
-  const int nrecA = min(M - m0, BM) * lda * 2, nrecB = BN * ldb * 2;
+  // EPI: the up half of the B tile starts at row N + n0
+  const _Float16* panelU = B + (long)(N + n0) * ldb;
+  const int nrecA = min(M - m0, BM) * lda * 2, nrecB = (EPI ? BN / 2 : BN) * ldb * 2;
   int voff[L];
 #pragma unroll
   for (int d = 0; d < L; ++d) {
     const bool isA = d < A_BLK;
-    const int r = crow + (isA ? d : d - A_BLK) * NW * RPB;
-    voff[d] = isA ? (min(r, M - 1 - m0) * lda + cchunk) * 2 : (r * ldb + cchunk) * 2;
+    const int ib = isA ? d : d - A_BLK;
+    const int r = crow + ib * NW * RPB;
+    const int rb = EPI && !isA && ib >= HB ? r - BN / 2 : r;  // row inside its B panel
+    voff[d] = isA ? (min(r, M - 1 - m0) * lda + cchunk) * 2 : (rb * ldb + cchunk) * 2;
   }
   auto dma = [&](int kt, int ksrc, int d) {
     const bool isA = d < A_BLK;
     const int ib = isA ? d : d - A_BLK;
     _Float16* dst = smem + (kt % STAGES) * STAGE + (isA ? 0 : BM * BK) + (ib * NW + wave) * RPB * BK;
-    buf_lds16(isA ? panelA : panelB, isA ? nrecA : nrecB, dst, voff[d], (kbase + ksrc) * BK * 2);
+    const _Float16* pan = isA ? panelA : (EPI && ib >= HB ? panelU : panelB);
+    buf_lds16(pan, isA ? nrecA : nrecB, dst, voff[d], (kbase + ksrc) * BK * 2);
   };
 
   typename MF::acc_t acc[TM][TN];
@@ -241,6 +257,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv(
   constexpr int CPRW = RB / 16;               // 16-byte chunks per C row
   constexpr bool LDS_EPI = BM * BN <= STAGES * STAGE && CPRW >= 16 && (CPRW & (CPRW - 1)) == 0 &&
                            (NW * 64) % CPRW == 0;
+  static_assert(!EPI || LDS_EPI, "gate/up: the epilogue pairs the halves through LDS");
   if constexpr (LDS_EPI) {
     // The C tile through LDS (the stages are free by then): a row-major fp16 image whose 16-byte
     // chunk c of row r sits at chunk c ^ (r % 16), so the 16 rows of an MFMA block write to 16
@@ -263,6 +280,22 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv(
       }
     }
     __syncthreads();
+    if constexpr (EPI) {
+      // output row r, chunk c (8 columns): gate chunk c, up chunk c + CPRW/2 of image row r
+      constexpr int CPO = CPRW / 2, RPO = NW * 64 / CPO;
+#pragma unroll 4
+      for (int p = 0; p < BM / RPO; ++p) {
+        const int r = p * RPO + tid / CPO, c = tid % CPO;
+        const f16x8 g = as_f16x8(*reinterpret_cast<const u32x4*>(cs + r * RB + ((c ^ (r & 15)) << 4)));
+        const f16x8 u =
+            as_f16x8(*reinterpret_cast<const u32x4*>(cs + r * RB + (((c + CPO) ^ (r & 15)) << 4)));
+        f16x8 o;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = silu_mul_f16((float)g[e], (float)u[e]);
+        if (m0 + r < M) store16(C + (long)(m0 + r) * ldc + n0 + c * 8, __builtin_bit_cast(u32x4, o));
+      }
+      return;
+    }
 #pragma unroll 4
     for (int p = 0; p < BM / RPP; ++p) {
       const int r = p * RPP + tid / CPRW, c = tid % CPRW;

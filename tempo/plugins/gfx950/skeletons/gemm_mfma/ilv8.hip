@@ -27,10 +27,13 @@
 // SPLIT = 1 (split-K), as in k_gemm_ilv: workgroup split sk of split_tile_of takes k-tiles
 // [sk*kper, ...), writes its fp32 partial tile to ws[sk][M][N]; k_splitk_reduce rounds the sum.
 // A split may start at an odd k-tile: the scale group of k-tile t is t/2 in every stage.
+// EPI = 1 (fused gate/up), as in k_gemm_ilv: W (and its scales and zero-points) hold the gate
+// rows then the up rows, a tile covers BN/2 output columns with BN/2 gate and the BN/2 matching
+// up rows, and the epilogue writes fp16_rn(silu(g) * u) from the two halves of the C image.
 // Build: -mllvm -amdgpu-sched-strategy=iterative-minreg, like k_gemm_ilv (own translation unit).
 // ============================================================================================
 template <int BM, int BN, int BK, int WM, int WN, int STAGES, int GROUP, int XCD, int RSP, int BFMT,
-          int SPLIT = 0>
+          int SPLIT = 0, int EPI = 0>
 __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv8(
     const _Float16* __restrict__ A, const uint8_t* __restrict__ W, const _Float16* __restrict__ scale,
     const uint8_t* __restrict__ zero, _Float16* __restrict__ C, int M, int N, int K, int lda,
@@ -62,6 +65,10 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv8(
   static_assert(STAGES >= 2 && (STAGES - 1) * L < 64, "stages / vmcnt range");
   static_assert((16 / R256) % CPR == 0 && (NW * RPB / R256) % CPR == 0, "swizzle periods");
   static_assert(BFMT == 1 || BFMT == 2, "int8 per-channel or uint8 group-128");
+  // EPI: weight copy block d of every wave is in the gate half iff d < HB
+  constexpr int HB = (BN / 2) / (16 * NW);
+  static_assert(!EPI || (SPLIT == 0 && (BN / 2) % (16 * NW) == 0 && (BN / 2) % 64 == 0),
+                "gate/up: whole copy and metadata blocks per half");
 
   __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * SBYTES + (BFMT == 1 ? MROWS * 4 : 0)];
   static_assert(STAGES * SBYTES + (BFMT == 1 ? MROWS * 4 : 0) <= 160 * 1024, "LDS");
@@ -71,14 +78,15 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv8(
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WN, wn = wave % WN;
 
-  const int nm = (M + BM - 1) / BM, nn = N / BN;
+  constexpr int BNO = EPI ? BN / 2 : BN;  // output columns per tile
+  const int nm = (M + BM - 1) / BM, nn = N / BNO;
   const int ng = K / 128;                     // scale groups per weight row
   int tmi, tni, sk = 0;
   if constexpr (SPLIT)
     split_tile_of<GROUP, XCD>(blockIdx.x, nm, nn, ksplit, tmi, tni, sk);
   else
     tile_of<GROUP, XCD>(blockIdx.x, nm, nn, tmi, tni);
-  const int m0 = tmi * BM, n0 = tni * BN;
+  const int m0 = tmi * BM, n0 = tni * BNO;
   // k-tiles of this workgroup: [kbase, kbase + NT)
   const int NTALL = K / BK;
   const int kper = SPLIT ? (NTALL + ksplit - 1) / ksplit : NTALL;
@@ -93,7 +101,8 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv8(
   const int cchunk = lds_chunk<BK, SWZ>(crow, lane % CPR) * 8;
   const _Float16* panelA = A + (long)m0 * lda;
   const uint8_t* panelW = W + (long)n0 * ldw;
-  const int nrecA = min(M - m0, BM) * lda * 2, nrecW = BN * ldw;
+  const uint8_t* panelWu = W + (long)(N + n0) * ldw;  // EPI: the up half of the tile
+  const int nrecA = min(M - m0, BM) * lda * 2, nrecW = BNO * ldw;
   int voff[A_BLK + B_BLK];
 #pragma unroll
   for (int d = 0; d < A_BLK; ++d)
@@ -101,27 +110,32 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv8(
 #pragma unroll
   for (int d = 0; d < B_BLK; ++d) {
     const int r = (d * NW + wave) * 16 + lane / 4;
-    voff[A_BLK + d] = r * ldw + (((lane % 4) ^ (lane / 16)) * 16);
+    const int rb = EPI && d >= HB ? r - BN / 2 : r;  // row inside its panel
+    voff[A_BLK + d] = rb * ldw + (((lane % 4) ^ (lane / 16)) * 16);
   }
   // fmt 2: zero-point and scale of row q*64 + l (q = this wave) for the stage's group, one byte /
-  // one half per lane at a 4-byte lane stride
-  const uint8_t* panelZ = zero + (BFMT == 2 ? (long)n0 * ng : 0);
-  const _Float16* panelS = scale + (BFMT == 2 ? (long)n0 * ng : (long)n0);
+  // one half per lane at a 4-byte lane stride.  EPI: rows of the up half come from the up rows.
   const int mrow = (wave % (BN / 64)) * 64 + lane;
+  const bool mup = EPI && (wave % (BN / 64)) * 64 >= BN / 2;
+  const long mbase = mup ? (long)N + n0 : (long)n0;
+  const int mrel = mup ? mrow - BN / 2 : mrow;  // row inside its metadata panel
+  const uint8_t* panelZ = zero + (BFMT == 2 ? mbase * ng : 0);
+  const _Float16* panelS = scale + (BFMT == 2 ? mbase * ng : mbase);
   auto dma = [&](int kt, int d) {
     const int ks = kbase + min(kt, NT - 1);
     uint8_t* st = smem + (kt % STAGES) * SBYTES;
     if (d < A_BLK) {
       buf_lds16(panelA, nrecA, st + (d * NW + wave) * 1024, voff[d], ks * BK * 2);
     } else if (d < A_BLK + B_BLK) {
-      buf_lds16(panelW, nrecW, st + ABYTES + ((d - A_BLK) * NW + wave) * 1024, voff[d], ks * BK);
+      buf_lds16(EPI && d - A_BLK >= HB ? panelWu : panelW, nrecW,
+                st + ABYTES + ((d - A_BLK) * NW + wave) * 1024, voff[d], ks * BK);
     } else if constexpr (BFMT == 2) {
       const int g = ks * BK / 128;
       if (d == A_BLK + B_BLK)
-        buf_lds_n<1>(panelZ, BN * ng, st + ABYTES + BBYTES + wave * 256, mrow * ng, g);
+        buf_lds_n<1>(panelZ, BNO * ng, st + ABYTES + BBYTES + wave * 256, mrel * ng, g);
       else
-        buf_lds_n<2>(panelS, BN * ng * 2, st + ABYTES + BBYTES + MROWS * 4 + wave * 256, mrow * ng * 2,
-                     g * 2);
+        buf_lds_n<2>(panelS, BNO * ng * 2, st + ABYTES + BBYTES + MROWS * 4 + wave * 256,
+                     mrel * ng * 2, g * 2);
     }
   };
 
@@ -234,7 +248,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv8(
   // metadata and first fragments read
   uint8_t* const sc1 = smem + STAGES * SBYTES;
   if constexpr (BFMT == 1)
-    buf_lds_n<2>(panelS, BN * 2, sc1 + wave * 256, mrow * 2, 0);
+    buf_lds_n<2>(panelS, BNO * 2, sc1 + wave * 256, mrel * 2, 0);
 #pragma unroll
   for (int s = 0; s < STAGES; ++s)
 #pragma unroll
@@ -291,6 +305,31 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv8(
     }
   }
   __syncthreads();
+  if constexpr (EPI) {
+    // output row r, chunk c (8 columns): gate chunk c, up chunk c + CPRW/2 of image row r
+    constexpr int CPO = CPRW / 2, RPO = NW * 64 / CPO;
+#pragma unroll 4
+    for (int p = 0; p < BM / RPO; ++p) {
+      const int r = p * RPO + tid / CPO, c = tid % CPO;
+      const f16x8 g = as_f16x8(*reinterpret_cast<const u32x4*>(smem + r * RB + ((c ^ (r & 15)) << 4)));
+      const f16x8 u =
+          as_f16x8(*reinterpret_cast<const u32x4*>(smem + r * RB + (((c + CPO) ^ (r & 15)) << 4)));
+      f16x8 o;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = silu_mul_f16((float)g[e], (float)u[e]);
+      const u32x4 v = __builtin_bit_cast(u32x4, o);
+      if (m0 + r < M) {
+        _Float16* dst = C + (long)(m0 + r) * ldc + n0 + c * 8;
+        if (c16) {
+          __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(dst));
+        } else {
+          __builtin_nontemporal_store(u32x2{v[0], v[1]}, reinterpret_cast<u32x2*>(dst));
+          __builtin_nontemporal_store(u32x2{v[2], v[3]}, reinterpret_cast<u32x2*>(dst + 4));
+        }
+      }
+    }
+    return;
+  }
 #pragma unroll 4
   for (int p = 0; p < BM / RPP; ++p) {
     const int r = p * RPP + tid / CPRW, c = tid % CPRW;

@@ -68,6 +68,10 @@ FP16_GATE_UP = [
     ("gh16r1u4n2", 16, 512, 65792),
     ("gh32r1u4n4", 32, 512, 65792),
     ("g32r1u4", 32, 496, 65792),
+    ("gi128x256k64s3", 64, 17408, 5120),
+    ("gi128x256k64s3", 100, 7680, 3840),    # ragged M
+    ("gi256x256k64w4r8", 300, 7680, 3840),
+    ("gi256x256k64w4r8", 512, 4096, 5120),
 ]
 
 W8 = {
@@ -177,6 +181,9 @@ W8_GATE_UP = {
         ("gh16r1u2n2", 16, 512, 65664),
         ("gh32r1u2n4", 32, 512, 65664),
         ("g32r1u4", 32, 496, 65792),
+        ("gi8x128x256s3", 64, 17408, 5120),
+        ("gi8x128x256s3", 100, 7680, 3840),
+        ("gi8x256k64s3", 300, 7680, 3840),
     ],
     2: [
         ("gl0r1n2d4", 1, 17408, 5120),
@@ -189,6 +196,9 @@ W8_GATE_UP = {
         ("gh16r1u4n2", 16, 512, 65792),
         ("gh32r1u4n4", 32, 512, 65792),
         ("g32r1u4", 32, 496, 65792),
+        ("gi8x128x256s3", 64, 17408, 5120),
+        ("gi8x128x256s3", 100, 7680, 3840),
+        ("gi8x256k64s3", 300, 7680, 3840),
     ],
 }
 

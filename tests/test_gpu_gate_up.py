@@ -22,7 +22,7 @@ def _route(op, M, N, K):
     return capi.route(op, M, N, K)
 
 
-@pytest.mark.parametrize("M", [1, 5, 16, 27, 32])
+@pytest.mark.parametrize("M", [1, 5, 16, 27, 32, 33, 128, 300])
 @pytest.mark.parametrize("NK", [(17408, 5120), (1024, 3840)], ids=lambda nk: "n%d_k%d" % nk)
 def test_fp16_gate_up_parity(gpu, M, NK):
     import torch
@@ -43,7 +43,7 @@ def test_fp16_gate_up_parity(gpu, M, NK):
     assert r <= TOL
 
 
-@pytest.mark.parametrize("M", [1, 16, 32])
+@pytest.mark.parametrize("M", [1, 16, 32, 64, 257])
 def test_fp16_gate_up_exact_regime(gpu, M):
     """Small-integer inputs: every gate and up sum is exact, so only the exponential differs."""
     import torch
@@ -63,7 +63,7 @@ def test_fp16_gate_up_exact_regime(gpu, M):
 
 
 @pytest.mark.parametrize("fmt", [1, 2])
-@pytest.mark.parametrize("M", [1, 8, 16, 32])
+@pytest.mark.parametrize("M", [1, 8, 16, 32, 64, 300])
 def test_w8a16_gate_up_parity(gpu, fmt, M):
     """The production shape S1 (bench/shapes/qwen36_27b_int8.json): gate_up with 2N = 34816."""
     import torch
@@ -93,10 +93,11 @@ def test_w8a16_gate_up_parity(gpu, fmt, M):
     assert r <= TOL
 
 
-def test_gate_up_prefill_is_not_covered(gpu):
+def test_gate_up_uncovered_shape_is_refused(gpu):
+    """N % 128 != 0 past the decode band: no row fits, the caller's own path (TEMPO_FALLBACK)."""
     from cuda_tempiler_amd import capi
 
     A = dev(np.zeros((64, 512), np.float16), gpu)
-    B = dev(np.zeros((2 * 1024, 512), np.float16), gpu)
+    B = dev(np.zeros((2 * 1000, 512), np.float16), gpu)
     with pytest.raises(capi.NotCovered):
         capi.gemm_fp16_gate_up(A, B)
