@@ -114,8 +114,9 @@ int tempo_gemm_w8a16_launch_noalloc(const TempoW8A16Params* p, tempo_stream_t st
  * bench/shapes/qwen36_27b_int8.json is this GEMM at 2N = 34816).  G and U are rounded to fp16
  * before the epilogue, so the result is the unfused chain's up to the last bit of silu.  The
  * reference names this fusion and its price and does not ship it (docs/NOT_YET.md:141-146,
- * kernels/shipped/gemm_fp16/sm_70/INTEGRATION.md:21).  Decode shapes (M <= 32) are covered;
- * others return TEMPO_FALLBACK (run the plain GEMM and the elementwise step).
+ * kernels/shipped/gemm_fp16/sm_70/INTEGRATION.md:21).  Every M is covered (decode rows on the
+ * streaming kernels, prefill rows on the interleaved kernels) where N % 128 == 0 and K fits a
+ * row; other shapes return TEMPO_FALLBACK (run the plain GEMM and the elementwise step).
  * ------------------------------------------------------------------------------------------ */
 int tempo_gemm_fp16_gate_up_launch(const TempoGemmParams* p, tempo_stream_t stream);
 int tempo_gemm_w8a16_gate_up_launch(const TempoW8A16Params* p, tempo_stream_t stream);

@@ -51,9 +51,8 @@ class Gfx950Plugin:
             "clock locking (Meters.clock_lock) is not offered: clocks are recorded, not set",
             "classifier.control_fields: the AMD ISA has no scheduling control words",
             "FMHA is a fixed skeleton (skeletons/fmha_fwd), outside the searched space",
-            "the fused silu(gate)*up epilogue covers decode (M <= 32) only; prefill-sized M "
-            "returns TEMPO_FALLBACK and the caller runs the plain GEMM plus its own elementwise "
-            "step",
+            "the fused silu(gate)*up epilogue of the interleaved prefill kernels has no split-K "
+            "form: mid-M gate/up shapes with few column tiles leave CUs idle",
         )
 
     def selftest(self) -> Report:
