@@ -64,6 +64,9 @@ LADDER = [
      dict(BM=128, BN=256, BK=64, WM=1, WN=4, STAGES=3, GROUP=8, XCD=1, RSP=8, SW=256, MINKT=8,
           NMAX=12288, KMIN=12288)),
     (64, 0, "l4r1n2d3", "line", dict(MB=4, R=1, D=3, SN=2, W=2048)),
+    # 64 < M <= 128, narrow N (< 2048): the line kernel with eight activation blocks, two slab
+    # waves per ring and k slices (1.09x the 128 x 128 tile row below at (128, 1024, 5120))
+    (128, 0, "l8r1n2d2k8", "line", dict(MB=8, R=1, D=2, SN=2, W=2048, KS=8, NMAX=2048)),
     # 64 < M <= 128, N <= 6144 and K < 8192: 128 x 128 tiles (2 x 2 waves of 64 x 64), four
     # stages (1.11-1.32x the 128 x 256 row below at N = 1024-6144, both formats)
     (128, 0, "i8x128x128s4w256", "ilv8",
@@ -95,10 +98,11 @@ LADDER = [
 # production gate_up shape (N, K) = (17408, 5120), both formats; then the interleaved int8
 # kernel with EPI = 1 for every M.
 LADDER_GATE_UP = [
-    (1, 0, "gl0r1n2d4", "line", dict(MB=0, R=1, D=4, SN=2, W=2048)),
+    # two ring steps at M = 1 and M = 32 (1.05-1.08x / 1.02-1.06x four, both formats)
+    (1, 0, "gl0r1n2d2", "line", dict(MB=0, R=1, D=2, SN=2, W=2048)),
     (16, 12288, "gl1r1n4d3", "line", dict(MB=1, R=1, D=3, SN=4, W=2048)),
     (16, 0, "gl1r1n2d4", "line", dict(MB=1, R=1, D=4, SN=2, W=2048)),
-    (32, 12288, "gl2r1n4d4", "line", dict(MB=2, R=1, D=4, SN=4, W=2048)),
+    (32, 12288, "gl2r1n4d2", "line", dict(MB=2, R=1, D=2, SN=4, W=2048)),
     (32, 0, "gl2r1n2d4", "line", dict(MB=2, R=1, D=4, SN=2, W=2048)),
     (1, 0, "g1a_r1u2", "stream", dict(MB=1, R=1, U=2, A=1, fmts=(1,))),
     (1, 0, "g1a_r1u8", "stream", dict(MB=1, R=1, U=8, A=1, fmts=(2,))),

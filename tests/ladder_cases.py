@@ -114,7 +114,9 @@ W8 = {
         ("i8x128x256s3w256", 128, 34816, 5120),
         ("i8x128x256s3w256", 100, 7168, 5120),
         ("i8x128x128s4w256", 128, 5120, 5120),
-        ("i8x128x128s4w256", 100, 1024, 5120),
+        ("i8x128x128s4w256", 100, 2048, 5120),
+        ("l8r1n2d2k8", 128, 1024, 5120),
+        ("l8r1n2d2k8", 100, 1024, 5120),
         ("l8r1n2d3", 128, 5152, 5120),
         ("m128x128k64", 256, 5120, 5120),
         ("i8x128x256s3w256", 2048, 1024, 5120),
@@ -161,7 +163,9 @@ W8 = {
         ("i8x128x256s3w256", 128, 34816, 5120),
         ("i8x128x256s3w256", 100, 7168, 5120),
         ("i8x128x128s4w256", 128, 5120, 5120),
-        ("i8x128x128s4w256", 100, 1024, 5120),
+        ("i8x128x128s4w256", 100, 2048, 5120),
+        ("l8r1n2d2k8", 128, 1024, 5120),
+        ("l8r1n2d2k8", 100, 1024, 5120),
         ("l8r1n2d3", 128, 5152, 5120),
         ("m128x128k64", 256, 5120, 5120),
         ("i8x128x256s3w256", 2048, 1024, 5120),
@@ -172,10 +176,10 @@ W8 = {
 
 W8_GATE_UP = {
     1: [
-        ("gl0r1n2d4", 1, 17408, 5120),
+        ("gl0r1n2d2", 1, 17408, 5120),
         ("gl1r1n4d3", 16, 17408, 5120),
         ("gl1r1n2d4", 8, 7680, 3840),
-        ("gl2r1n4d4", 32, 17408, 5120),
+        ("gl2r1n4d2", 32, 17408, 5120),
         ("gl2r1n2d4", 32, 7680, 3840),
         ("g1a_r1u2", 1, 512, 65664),
         ("gh16r1u2n2", 16, 512, 65664),
@@ -186,10 +190,10 @@ W8_GATE_UP = {
         ("gi8x256k64s3", 300, 7680, 3840),
     ],
     2: [
-        ("gl0r1n2d4", 1, 17408, 5120),
+        ("gl0r1n2d2", 1, 17408, 5120),
         ("gl1r1n4d3", 16, 17408, 5120),
         ("gl1r1n2d4", 8, 7680, 3840),
-        ("gl2r1n4d4", 32, 17408, 5120),
+        ("gl2r1n4d2", 32, 17408, 5120),
         ("gl2r1n2d4", 32, 7680, 3840),
         ("g1a_r1u8", 1, 512, 66048),
         ("g1a_r1u4", 1, 512, 65792),
