@@ -58,20 +58,32 @@ LADDER = [
     (16, 0, "s16r1u4", "stream", dict(MB=1, R=1, U=4, A=0)),
     (32, 0, "h32r1u4n2", "shared", dict(MB=2, R=1, U=4, SN=2, TPB=512)),
     (64, 12288, "l4r1n4d3", "line", dict(MB=4, R=1, D=3, SN=4, W=2048)),
-    # 32 < M <= 64, narrow N and long K: the int8 interleaved kernel on 128 x 256 tiles with
-    # split-K (measured 1.3x the line row at (64, 5120, 17408), 0.9x at K = 5120)
-    (64, 0, "i8x128x256s3w256", "ilv8",
-     dict(BM=128, BN=256, BK=64, WM=1, WN=4, STAGES=3, GROUP=8, XCD=1, RSP=8, SW=256, MINKT=8,
+    # 32 < M <= 64, narrow N and long K: the int8 interleaved kernel on 128 x 256 tiles of 128 k
+    # (whole weight lines) with split-K (1.09x the 64-k tile row at (64, 5120, 17408), which was
+    # 1.3x the line row)
+    (64, 0, "i8x128x256k128s2w256", "ilv8",
+     dict(BM=128, BN=256, BK=128, WM=1, WN=4, STAGES=2, GROUP=8, XCD=1, RSP=8, SW=256, MINKT=8,
           NMAX=12288, KMIN=12288)),
+    # 32 < M <= 64, narrow N: 128 x 128 tiles of 128 k, split-K (1.23x the line row below at
+    # (64, 7168, 5120))
+    (64, 0, "i8x128x128k128s2w256", "ilv8",
+     dict(BM=128, BN=128, BK=128, WM=2, WN=2, STAGES=2, GROUP=8, XCD=1, RSP=8, SW=256, MINKT=8,
+          NMAX=12288)),
     (64, 0, "l4r1n2d3", "line", dict(MB=4, R=1, D=3, SN=2, W=2048)),
     # 64 < M <= 128, narrow N (< 2048): the line kernel with eight activation blocks, two slab
     # waves per ring and k slices (1.09x the 128 x 128 tile row below at (128, 1024, 5120))
     (128, 0, "l8r1n2d2k8", "line", dict(MB=8, R=1, D=2, SN=2, W=2048, KS=8, NMAX=2048)),
-    # 64 < M <= 128, N <= 6144 and K < 8192: 128 x 128 tiles (2 x 2 waves of 64 x 64), four
-    # stages (1.11-1.32x the 128 x 256 row below at N = 1024-6144, both formats)
-    (128, 0, "i8x128x128s4w256", "ilv8",
-     dict(BM=128, BN=128, BK=64, WM=2, WN=2, STAGES=4, GROUP=16, XCD=0, RSP=8, SW=256, MINKT=8,
-          NMAX=6145, KMAX=8192)),
+    # 64 < M <= 128, N < 12288, uint8 and long K: 128 x 256 tiles of 128 k, split-K (1.11x the
+    # 64-k row at (128, 5120, 17408))
+    (128, 0, "i8x128x256k128s2w256", "ilv8",
+     dict(BM=128, BN=256, BK=128, WM=1, WN=4, STAGES=2, GROUP=8, XCD=1, RSP=8, SW=256, MINKT=8,
+          NMAX=12288, KMIN=12288, fmts=(2,))),
+    # 64 < M <= 128, N < 12288: 128 x 128 tiles (2 x 2 waves of 64 x 64) of 128 k -- every
+    # k-tile takes whole 128-byte lines of the weight rows -- two stages, split-K (1.04-1.21x
+    # the 64-k tile rows at N = 5120-7168, both formats)
+    (128, 0, "i8x128x128k128s2w256", "ilv8",
+     dict(BM=128, BN=128, BK=128, WM=2, WN=2, STAGES=2, GROUP=8, XCD=1, RSP=8, SW=256, MINKT=8,
+          NMAX=12288)),
     # 64 < M <= 128: 128 x 256 tiles (one tile row), split-K where the column tiles are too few
     # to fill the part (the variant driver's rows: 1.5-2.9x the line and register-staged rows)
     (128, 0, "i8x128x256s3w256", "ilv8",
@@ -79,14 +91,16 @@ LADDER = [
     (128, 0, "l8r1n2d3", "line", dict(MB=8, R=1, D=3, SN=2, W=2048, NMAX=12288)),
     (256, 0, "m128x128k64", "mfma",
      dict(BM=128, BN=128, BK=64, WM=2, WN=2, MS=32, SWZ=1, GROUP=8, XCD=1)),
-    # narrow N (fewer than 8 tiles of 256 columns): 256x256 tiles leave most CUs idle; 128 x 256
-    # tiles with split-K fill the part (1.97x the 128 x 128 register-staged row at
-    # (2048, 1024, 5120)), which stays behind them for N % 256 != 0
-    (1 << 30, 0, "i8x128x256s3w256", "ilv8",
-     dict(BM=128, BN=256, BK=64, WM=1, WN=4, STAGES=3, GROUP=8, XCD=1, RSP=8, SW=256, MINKT=8,
+    # narrow N (fewer than 8 tiles of 256 columns): 256x256 tiles leave most CUs idle; 128 x 128
+    # tiles of 128 k with split-K fill the part (1.08x the 128 x 256 64-k row at (2048, 1024,
+    # 5120), which was 1.97x the 128 x 128 register-staged row behind them)
+    (1 << 30, 0, "i8x128x128k128s2w256", "ilv8",
+     dict(BM=128, BN=128, BK=128, WM=2, WN=2, STAGES=2, GROUP=8, XCD=1, RSP=8, SW=256, MINKT=8,
           NMAX=2048)),
+    # what the 128-k tiles leave at narrow N: K % 128 == 64 (int8 only; uint8 groups are whole
+    # 128-k)
     (1 << 30, 0, "m128x128k64s16", "mfma",
-     dict(BM=128, BN=128, BK=64, WM=2, WN=2, MS=16, SWZ=1, GROUP=8, XCD=1, NMAX=2048)),
+     dict(BM=128, BN=128, BK=64, WM=2, WN=2, MS=16, SWZ=1, GROUP=8, XCD=1, NMAX=2048, fmts=(1,))),
     (1 << 30, 0, "i8x256k64s3", "ilv8",
      dict(BM=256, BN=256, BK=64, WM=2, WN=2, STAGES=3, GROUP=8, XCD=1, RSP=8)),
     (1 << 30, 0, "m256x256k64", "mfma",

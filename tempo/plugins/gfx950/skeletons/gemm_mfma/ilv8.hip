@@ -5,12 +5,15 @@
 // k_gemm_ilv8 has the structure of k_gemm_ilv -- 4 waves (wave tiles of 128 x 128, 128 x 64 or
 // 64 x 64) on v_mfma_f32_16x16x32_f16, chunked substeps fenced by sched_barrier, buffer LDS-DMA
 // copies, the C tile written out through LDS -- with the weight tile travelling as bytes:
-//   * A stage holds the fp16 A tile (BM x 64, SWZ2 chunk swizzle of its 128-byte rows), the weight
-//     tile (BN x 64 bytes; 16-byte chunk c of row r stored at chunk c ^ ((r / 4) % 4), which makes
-//     the 8-byte fragment reads below conflict-free) and, fmt 2, the tile's zero-points and
-//     scales (one byte / one half per row, 4 bytes apart).  Three stages (150 KiB): the weight
-//     tile is half the size of an fp16 one, so a third stage fits, and the C tile (128 KiB) fits
-//     the stages for the epilogue.
+//   * A stage holds the fp16 A tile (BM x BK, SWZ2 chunk swizzle of its rows), the weight tile
+//     (BN x BK bytes; 16-byte chunk c of row r stored at chunk c ^ wswz(r), wswz = (r / 4) % 4 for
+//     64-byte rows and (r / 2) % 8 for 128-byte rows, which makes the 8-byte fragment reads below
+//     conflict-free) and, fmt 2, the tile's zero-points and scales (one byte / one half per row,
+//     4 bytes apart).  BK = 64: three stages (150 KiB) -- the weight tile is half the size of an
+//     fp16 one, so a third stage fits.  BK = 128: every k-tile takes a whole 128-byte line of
+//     each weight row, the granularity at which HBM streams near its peak (64-byte pieces of
+//     scattered rows stream at about two thirds of the rate); two stages of 64 KiB at BM = 128,
+//     BN = 256.  The C tile fits the stages for the epilogue.
 //   * Fragments: A as in k_gemm_ilv (ds_read_b128); a weight fragment (16 rows x 32 k) is one
 //     8-byte read per lane.  The MFMAs of a substep run block column by block column, and each
 //     column's 8 weight bytes are dequantised in registers (cdna4.h dequant8: bit-exact
@@ -26,7 +29,8 @@
 // offsets below 2^31.  M is predicated (A rows past M-1 clamped, never stored).
 // SPLIT = 1 (split-K), as in k_gemm_ilv: workgroup split sk of split_tile_of takes k-tiles
 // [sk*kper, ...), writes its fp32 partial tile to ws[sk][M][N]; k_splitk_reduce rounds the sum.
-// A split may start at an odd k-tile: the scale group of k-tile t is t/2 in every stage.
+// A split may start at an odd k-tile: the scale group of k-tile t is t * BK / 128 in every
+// stage.
 // EPI = 1 (fused gate/up), as in k_gemm_ilv: W (and its scales and zero-points) hold the gate
 // rows then the up rows, a tile covers BN/2 output columns with BN/2 gate and the BN/2 matching
 // up rows, and the epilogue writes fp16_rn(silu(g) * u) from the two halves of the C image.
@@ -48,7 +52,9 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv8(
   constexpr int TM = WTM / 16, TN = WTN / 16;
   constexpr int KS = BK / 32;
   constexpr int A_BLK = BM / RPB / NW;        // A copies per wave per k-tile
-  constexpr int B_BLK = BN / 16 / NW;         // W copies (16 rows x 64 bytes each) per wave
+  constexpr int WCH = BK / 16;                // 16-byte chunks per weight row
+  constexpr int RPW = 1024 / BK;              // weight rows per 1 KiB copy block
+  constexpr int B_BLK = BN / RPW / NW;        // W copies (RPW rows x BK bytes each) per wave
   constexpr int M_BLK = BFMT == 2 ? 2 : 0;    // fmt 2: one zero-point and one scale copy
   constexpr int L = A_BLK + B_BLK + M_BLK;    // copies per wave per k-tile
   // metadata slots: every wave copies 64 rows (one byte / half per lane, 4 bytes apart); with
@@ -59,17 +65,21 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv8(
   constexpr int SBYTES = ABYTES + BBYTES + MBYTES;  // one stage
   constexpr int NMF = TM * TN;
   constexpr int RSPAN = RSP > 0 && RSP < NMF / 4 ? RSP : NMF / 4;
-  static_assert(BK == 64 && KS == 2, "64-k tiles (a 128-k scale group is two of them)");
-  static_assert(BM % (RPB * NW) == 0 && BN % (16 * NW) == 0 && BN % 64 == 0 && (64 * NW) % BN == 0,
+  static_assert((BK == 64 || BK == 128) && KS == BK / 32,
+                "64-k tiles (a scale group is two of them) or 128-k tiles (one each)");
+  static_assert(BM % (RPB * NW) == 0 && BN % (RPW * NW) == 0 && BN % 64 == 0 && (64 * NW) % BN == 0,
                 "copy blocks");
   static_assert(STAGES >= 2 && (STAGES - 1) * L < 64, "stages / vmcnt range");
   static_assert((16 / R256) % CPR == 0 && (NW * RPB / R256) % CPR == 0, "swizzle periods");
   static_assert(BFMT == 1 || BFMT == 2, "int8 per-channel or uint8 group-128");
   // EPI: weight copy block d of every wave is in the gate half iff d < HB
-  constexpr int HB = (BN / 2) / (16 * NW);
-  static_assert(!EPI || (SPLIT == 0 && (BN / 2) % (16 * NW) == 0 && (BN / 2) % 64 == 0),
+  constexpr int HB = (BN / 2) / (RPW * NW);
+  static_assert(!EPI || (SPLIT == 0 && (BN / 2) % (RPW * NW) == 0 && (BN / 2) % 64 == 0),
                 "gate/up: whole copy and metadata blocks per half");
 
+  // weight chunk swizzle (see the header): keeps 16 consecutive rows' fragment reads on distinct
+  // banks for 64-byte and 128-byte rows alike
+  auto wswz = [](int r) { return BK == 64 ? (r >> 2) & 3 : (r >> 1) & 7; };
   __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * SBYTES + (BFMT == 1 ? MROWS * 4 : 0)];
   static_assert(STAGES * SBYTES + (BFMT == 1 ? MROWS * 4 : 0) <= 160 * 1024, "LDS");
 
@@ -94,9 +104,9 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv8(
   const int NT = min(kper, NTALL - kbase);
 
   // ---- copies -------------------------------------------------------------------------------
-  // A: as k_gemm_ilv (SWZ2 chunk swizzle of 128-byte rows).  W: 64-byte rows, 16-byte chunk c of
-  // row r stored at chunk c ^ ((r / 4) % 4); copy b fills rows 16 b .. 16 b + 15, lane l the
-  // physical chunk l % 4 of row 16 b + l / 4, whose logical chunk is (l % 4) ^ (l / 16).
+  // A: as k_gemm_ilv (SWZ2 chunk swizzle).  W: BK-byte rows, 16-byte chunk c of row r stored at
+  // chunk c ^ wswz(r); copy b fills rows RPW b .. RPW b + RPW - 1, lane l the physical chunk
+  // l % WCH of row RPW b + l / WCH, whose logical chunk is (l % WCH) ^ wswz(that row).
   const int crow = wave * RPB + lane / CPR;
   const int cchunk = lds_chunk<BK, SWZ>(crow, lane % CPR) * 8;
   const _Float16* panelA = A + (long)m0 * lda;
@@ -109,9 +119,9 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv8(
     voff[d] = (min(crow + d * NW * RPB, M - 1 - m0) * lda + cchunk) * 2;
 #pragma unroll
   for (int d = 0; d < B_BLK; ++d) {
-    const int r = (d * NW + wave) * 16 + lane / 4;
+    const int r = (d * NW + wave) * RPW + lane / WCH;
     const int rb = EPI && d >= HB ? r - BN / 2 : r;  // row inside its panel
-    voff[A_BLK + d] = rb * ldw + (((lane % 4) ^ (lane / 16)) * 16);
+    voff[A_BLK + d] = rb * ldw + (((lane % WCH) ^ wswz(r)) * 16);
   }
   // fmt 2: zero-point and scale of row q*64 + l (q = this wave) for the stage's group, one byte /
   // one half per lane at a 4-byte lane stride.  EPI: rows of the up half come from the up rows.
@@ -153,7 +163,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv8(
   for (int ks = 0; ks < KS; ++ks) {
     const int ra = wm * WTM + fr, rb = wn * WTN + fr;
     aOff[ks] = (ra * BK + lds_chunk<BK, SWZ>(ra, ks * 4 + fk) * 8) * 2;
-    bOff[ks] = ABYTES + rb * BK + (((ks * 2 + fk / 2) ^ ((fr / 4) & 3)) * 16) + (fk & 1) * 8;
+    bOff[ks] = ABYTES + rb * BK + (((ks * 2 + fk / 2) ^ wswz(fr)) * 16) + (fk & 1) * 8;
   }
   const int rowm = (wn * WTN + fr) * 4;       // this lane's metadata slot of block j = 0
 
@@ -184,7 +194,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv8(
   constexpr int NRD = TM + TN + (BFMT == 2 ? 2 * TN : 0);  // reads of a substep with metadata
   constexpr int CH = NMF / 4;                              // chunks of 4 MFMAs
   constexpr int CPJ = CH / TN;                             // chunks per block column
-  static_assert(CH % TN == 0 && CPJ >= 1 && RSPAN <= CH && L <= 2 * CH, "substep chunking");
+  static_assert(CH % TN == 0 && CPJ >= 1 && RSPAN <= CH && L <= 4 * CH, "substep chunking");
   auto substep = [&](auto bufc, auto dmac, auto metac, int rkt, int rks, int dkt) {
     constexpr int bb = decltype(bufc)::value;
     constexpr bool DMA = decltype(dmac)::value;
@@ -220,22 +230,29 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv8(
     }
   };
 
-  const int NU = NT * KS;
-  // k-tile kt (substeps 0, 1).  Barrier substep: copies of tile kt+1 landed everywhere, stage
-  // kt % STAGES free; fmt 2: it also reads tile kt+1's metadata (every stage carries its scale
-  // group's), which becomes current right after it -- the barrier substep's own fragments are
-  // still tile kt's.
-  auto ktile = [&](auto metac, int kt) {
-    constexpr bool META = decltype(metac)::value;
+  // k-tile kt (substeps 0 .. KS-1).  The last is the barrier substep: copies of tile kt+1
+  // landed everywhere, stage kt % STAGES free; fmt 2: it also reads tile kt+1's metadata (every
+  // stage carries its scale group's), which becomes current right after it -- the barrier
+  // substep's own fragments are still tile kt's.
+  auto plain = [&](auto sc, int kt) {       // substep s < KS-1: MFMAs of s, fragments of s + 1
+    constexpr int s = decltype(sc)::value;
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_waitcnt(0xC07F);       // lgkmcnt(0): this substep's fragments are in
     asm volatile("" ::: "memory");
-    substep(IC<0>{}, IC<false>{}, IC<false>{}, kt, 1, 0);
+    substep(IC<s & 1>{}, IC<false>{}, IC<false>{}, kt, s + 1, 0);
+  };
+  auto ktile = [&](auto metac, int kt) {
+    constexpr bool META = decltype(metac)::value;
+    plain(IC<0>{}, kt);
+    if constexpr (KS == 4) {
+      plain(IC<1>{}, kt);
+      plain(IC<2>{}, kt);
+    }
     asm volatile("" ::: "memory");
     s_wait_vm<(STAGES - 2) * L>();            // (also lgkmcnt 0)
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    substep(IC<1>{}, IC<true>{}, metac, kt + 1, 0, kt + STAGES);
+    substep(IC<(KS - 1) & 1>{}, IC<true>{}, metac, kt + 1, 0, kt + STAGES);
     if constexpr (BFMT == 2 && META) {
       asm volatile("" ::: "memory");
       __builtin_amdgcn_s_waitcnt(0xC07F);

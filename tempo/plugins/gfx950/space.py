@@ -44,7 +44,8 @@ DOMAINS = {
     "ilv": dict(BM=(64, 128, 256), BN=(128, 192, 256), BK=(32, 64), STAGES=(2, 3, 4),
                 GROUP=(4, 8, 16), XCD=(0, 1), WAVES=((2, 2), (2, 4), (4, 2), (1, 4)),
                 RSP=(0, 8, 12), SW=(0, 128, 256, 512)),
-    "ilv8": dict(TILES=((256, 256, 2, 2), (128, 256, 1, 4), (128, 128, 2, 2)), STAGES=(3, 4),
+    "ilv8": dict(TILES=((256, 256, 2, 2), (128, 256, 1, 4), (128, 128, 2, 2)), BK=(64, 128),
+                 STAGES=(2, 3, 4),
                  GROUP=(4, 8, 16), XCD=(0, 1), RSP=(4, 8, 12), SW=(0, 128, 256, 512)),
     "dma": dict(BM=(64, 128, 256), BN=(64, 128, 192, 256), BK=(32, 64), STAGES=(2, 3, 4), SWZ=(0, 1, 2),
                 GROUP=(4, 8, 16), XCD=(0, 1), WAVES=((2, 2), (2, 4), (4, 2), (4, 4)), MS=(16, 32)),
@@ -292,14 +293,16 @@ def legal(kind: str, p: dict, M: int, N: int, K: int):
     if kind == "ilv8":
         BM, BN, BK, WM, WN = p["BM"], p["BN"], p["BK"], p["WM"], p["WN"]
         if (BM, BN, BK, WM, WN) not in ((256, 256, 64, 2, 2), (128, 256, 64, 1, 4),
-                                        (128, 128, 64, 2, 2)):
+                                        (128, 128, 64, 2, 2), (128, 256, 128, 1, 4),
+                                        (128, 128, 128, 2, 2)):
             return ("the int8 interleaved kernel takes 256 x 256 (2 x 2 waves), 128 x 256 "
-                    "(1 x 4 waves) or 128 x 128 (2 x 2 waves) tiles of 64 k")
+                    "(1 x 4 waves) or 128 x 128 (2 x 2 waves) tiles of 64 k, and the last two "
+                    "also of 128 k")
         if p["BFMT"] not in (1, 2):
             return "weights must be int8 (fmt 1) or uint8 group-128 (fmt 2)"
         if N % BN or K % 128:
             return "N %% %d / K %% 128 (one scale group = two k-tiles)" % BN
-        L = BM // 8 // 4 + BN // 16 // 4 + (2 if p["BFMT"] == 2 else 0)
+        L = BM // (512 // BK) // 4 + BN // (1024 // BK) // 4 + (2 if p["BFMT"] == 2 else 0)
         if (p["STAGES"] - 1) * L >= 64:
             return "vmcnt depth"
         if BM * BN * 2 > p["STAGES"] * (BM * BK * 2 + BN * BK):
@@ -463,14 +466,15 @@ def variants(op: OpSpec) -> Iterator[Hyperform]:
     if b in (1, 2) and M > 32:
         d = DOMAINS["ilv8"]
         for (BM, BN, WM, WN) in d["TILES"]:
-            for ST in d["STAGES"]:
-                for G in d["GROUP"]:
-                    for X in d["XCD"]:
-                        for RS in d["RSP"]:
-                            for SW in d["SW"]:
-                                out.append(("ilv8", _with_split(dict(
-                                    BM=BM, BN=BN, BK=64, WM=WM, WN=WN, STAGES=ST, GROUP=G, XCD=X,
-                                    RSP=RS, BFMT=b), SW)))
+            for BK in d["BK"]:
+                for ST in d["STAGES"]:
+                    for G in d["GROUP"]:
+                        for X in d["XCD"]:
+                            for RS in d["RSP"]:
+                                for SW in d["SW"]:
+                                    out.append(("ilv8", _with_split(dict(
+                                        BM=BM, BN=BN, BK=BK, WM=WM, WN=WN, STAGES=ST, GROUP=G,
+                                        XCD=X, RSP=RS, BFMT=b), SW)))
     d = DOMAINS["reg"]
     for BM in d["BM"]:
         for BN in d["BN"]:

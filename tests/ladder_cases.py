@@ -108,19 +108,22 @@ W8 = {
         ("s16r1u4", 16, 2064, 5120),      # N % 32 == 16, past the narrow-N row
         ("h32r1u4n2", 32, 512, 65792),
         ("l4r1n4d3", 64, 34816, 5120),
-        ("i8x128x256s3w256", 64, 5120, 17408),
-        ("l4r1n2d3", 64, 5120, 6144),
-        ("i8x128x256s3w256", 128, 5120, 17408),
+        ("i8x128x256k128s2w256", 64, 5120, 17408),
+        ("i8x128x128k128s2w256", 64, 5120, 6144),
+        ("i8x128x128k128s2w256", 40, 7168, 5120),
+        ("l4r1n2d3", 64, 5152, 5120),     # N % 128 == 32: no 128-column tiles
+        ("i8x128x128k128s2w256", 128, 5120, 17408),
         ("i8x128x256s3w256", 128, 34816, 5120),
-        ("i8x128x256s3w256", 100, 7168, 5120),
-        ("i8x128x128s4w256", 128, 5120, 5120),
-        ("i8x128x128s4w256", 100, 2048, 5120),
+        ("i8x128x128k128s2w256", 100, 7168, 5120),
+        ("i8x128x128k128s2w256", 128, 5120, 5120),
+        ("i8x128x128k128s2w256", 100, 2048, 5120),
         ("l8r1n2d2k8", 128, 1024, 5120),
         ("l8r1n2d2k8", 100, 1024, 5120),
         ("l8r1n2d3", 128, 5152, 5120),
         ("m128x128k64", 256, 5120, 5120),
-        ("i8x128x256s3w256", 2048, 1024, 5120),
-        ("m128x128k64s16", 2048, 1152, 5120),
+        ("i8x128x128k128s2w256", 2048, 1024, 5120),
+        ("i8x128x128k128s2w256", 2049, 1024, 5120),
+        ("m128x128k64s16", 2048, 1152, 5184),
         ("i8x256k64s3", 2048, 7168, 5120),
         ("m256x256k64", 512, 2048, 5184),
     ],
@@ -157,19 +160,23 @@ W8 = {
         ("s16r1u4", 16, 2064, 5120),      # N % 32 == 16, past the narrow-N row
         ("h32r1u4n2", 32, 512, 65792),
         ("l4r1n4d3", 64, 34816, 5120),
-        ("i8x128x256s3w256", 64, 5120, 17408),
-        ("l4r1n2d3", 64, 5120, 6144),
-        ("i8x128x256s3w256", 128, 5120, 17408),
+        ("i8x128x256k128s2w256", 64, 5120, 17408),
+        ("i8x128x128k128s2w256", 64, 5120, 6144),
+        ("i8x128x128k128s2w256", 40, 7168, 5120),
+        ("l4r1n2d3", 64, 5152, 5120),     # N % 128 == 32: no 128-column tiles
+        ("i8x128x256k128s2w256", 128, 5120, 17408),
+        ("i8x128x256k128s2w256", 77, 5120, 12288),
         ("i8x128x256s3w256", 128, 34816, 5120),
-        ("i8x128x256s3w256", 100, 7168, 5120),
-        ("i8x128x128s4w256", 128, 5120, 5120),
-        ("i8x128x128s4w256", 100, 2048, 5120),
+        ("i8x128x128k128s2w256", 100, 7168, 5120),
+        ("i8x128x128k128s2w256", 128, 5120, 5120),
+        ("i8x128x128k128s2w256", 100, 2048, 5120),
         ("l8r1n2d2k8", 128, 1024, 5120),
         ("l8r1n2d2k8", 100, 1024, 5120),
         ("l8r1n2d3", 128, 5152, 5120),
         ("m128x128k64", 256, 5120, 5120),
-        ("i8x128x256s3w256", 2048, 1024, 5120),
-        ("m128x128k64s16", 2048, 1152, 5120),
+        ("i8x128x128k128s2w256", 2048, 1024, 5120),
+        ("i8x128x128k128s2w256", 2049, 1024, 5120),
+        ("i8x128x128k128s2w256", 2048, 1152, 5120),
         ("i8x256k64s3", 2048, 7168, 5120),
     ],
 }

@@ -142,7 +142,8 @@ def test_w8a16_parity_interleaved_prefill_rows(gpu, fmt, M, N, K):
     """The interleaved int8 prefill kernel: a ragged last tile row (M = 2049), a long k loop
     (K = 17408), and K % 128 != 0, which it does not take (fmt 1: the register-staged row runs;
     fmt 2 needs whole 128-k groups, so the shape is not covered at all).  Narrow N (< 2048)
-    takes the 128 x 256 split-K row of the same kernel instead, ragged M included."""
+    takes the 128 x 128 split-K row of the same kernel on 128-k tiles instead, ragged M
+    included."""
     route = _route(fmt, M, N, K)
     say("w8a16 fmt", fmt, "M", M, "N", N, "K", K, "route", route)
     if K % 128:
@@ -150,7 +151,7 @@ def test_w8a16_parity_interleaved_prefill_rows(gpu, fmt, M, N, K):
         if fmt == 2:
             return
     elif N < 2048:
-        assert route == "i8x128x256s3w256"
+        assert route == "i8x128x128k128s2w256"
     else:
         assert route == "i8x256k64s3"
     A = O.randn_f16((M, K), 13, K ** -0.5)
