@@ -45,9 +45,10 @@ LADDER = [
     (64, 12288, "l4r1n4d3", "line", dict(MB=4, R=1, D=3, SN=4, W=2048)),
     # narrow N, long K: split-K over the interleaved kernel's tiles (fp32 partials in the
     # workspace, reduced in order) gives the 20 column tiles of N = 3840 enough workgroups;
-    # measured by the variant driver (tempo/plugins/gfx950/tune.py) at (64|128|256, 3840, 15360)
-    (64, 0, "i64x192k64s3w256", "ilv",
-     dict(BM=64, BN=192, BK=64, WM=1, WN=4, STAGES=3, GROUP=8, XCD=1, RSP=8, SW=256, MINKT=8,
+    # measured by the variant driver (tempo/plugins/gfx950/tune.py) at (64|128|256, 3840, 15360);
+    # at M <= 64 the 64 x 128 tiles on four stages (1.06x the 64 x 192 three-stage row)
+    (64, 0, "i64x128k64s4w256", "ilv",
+     dict(BM=64, BN=128, BK=64, WM=2, WN=2, STAGES=4, GROUP=8, XCD=1, RSP=8, SW=256, MINKT=8,
           NMAX=6144)),
     (64, 0, "l4r1d3", "line", dict(MB=4, R=1, D=3, W=2048)),
     # 64 < M <= 256: LDS-DMA tiles with a 4-stage ring.  Per CU they keep more operand bytes in

@@ -29,9 +29,9 @@ FP16 = [
     ("l2r1d4", 32, 3840, 3840),
     ("s32r1u4", 32, 512, 65792),
     ("l4r1n4d3", 64, 15360, 3840),
-    ("i64x192k64s3w256", 64, 3840, 15360),  # the C2 decode-sweep point M = 64, N = 3840
-    ("i64x192k64s3w256", 40, 1920, 4096),   # ragged M, few k-tiles per split
-    ("l4r1d3", 64, 4096, 3840),             # N % 192 != 0
+    ("i64x128k64s4w256", 64, 3840, 15360),  # the C2 decode-sweep point M = 64, N = 3840
+    ("i64x128k64s4w256", 40, 1920, 4096),   # ragged M, few k-tiles per split
+    ("l4r1d3", 64, 6144, 3840),             # N at the interleaved row's NMAX
     ("d128x64k64s4", 128, 15360, 3840),
     ("d128x64k64s4", 200, 8192, 3840),
     ("i128x128k64s3w256", 128, 3840, 15360),
@@ -50,7 +50,7 @@ FP16 = [
 # extra elements per row of A, B, C)
 FP16_STRIDED = [
     ("l1r1d4", 16, 3840, 3840, 8, 16, 4),
-    ("i64x192k64s3w256", 64, 3840, 3840, 8, 8, 4),
+    ("i64x128k64s4w256", 64, 3840, 3840, 8, 8, 4),
     ("i128x128k64s3w256", 128, 3840, 3840, 8, 8, 4),
     ("d64x64k64s4", 128, 8192, 3840, 8, 8, 4),
     ("d128x128k64s4", 256, 15360, 3840, 16, 8, 4),
