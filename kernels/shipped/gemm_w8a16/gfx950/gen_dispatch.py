@@ -57,6 +57,10 @@ def instantiation(kind, p, epi=0):
             p["RSP"])
     if epi:
         raise ValueError("the fused gate/up epilogue exists for the stream and interleaved kernels")
+    if kind == "ilv8" and p.get("TAIL"):  # N in two parts: whole rounds, then the tail tiles
+        return "launch_ilv8_tail<%d,%d,%d,%d,%d,%d,%d,%d,%d,%s>" % (
+            p["BM"], p["BN"], p["BK"], p["WM"], p["WN"], p["STAGES"], p["GROUP"], p["XCD"],
+            p["RSP"], ",".join(str(v) for v in _select().ILV8_TAIL_TILE))
     if kind == "ilv8":
         return "launch_ilv8<%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d>" % (
             p["BM"], p["BN"], p["BK"], p["WM"], p["WN"], p["STAGES"], p["GROUP"], p["XCD"],

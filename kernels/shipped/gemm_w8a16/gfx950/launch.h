@@ -278,6 +278,10 @@ inline hipError_t launch_line_ks(const W8A16Params& p, hipStream_t s, const Work
 template <int BM, int BN, int BK, int WM, int WN, int STAGES, int GROUP, int XCD, int RSP,
           int SW, int MINKT>
 hipError_t launch_ilv8(const W8A16Params& p, hipStream_t s, const Workspace& w);
+// The same kernel, N in two parts: whole rounds of BM x BN tiles, the rest on TBM x TBN tiles.
+template <int BM, int BN, int BK, int WM, int WN, int STAGES, int GROUP, int XCD, int RSP,
+          int TBM, int TBN, int TBK, int TWM, int TWN, int TSTAGES>
+hipError_t launch_ilv8_tail(const W8A16Params& p, hipStream_t s, const Workspace& w);
 // The same kernel with the fused gate/up epilogue (p.N the output width, 2N weight rows).
 template <int BM, int BN, int BK, int WM, int WN, int STAGES, int GROUP, int XCD, int RSP>
 hipError_t launch_ilv8_gu(const W8A16Params& p, hipStream_t s, const Workspace& w);

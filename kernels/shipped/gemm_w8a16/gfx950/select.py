@@ -101,8 +101,11 @@ LADDER = [
     # 128-k)
     (1 << 30, 0, "m128x128k64s16", "mfma",
      dict(BM=128, BN=128, BK=64, WM=2, WN=2, MS=16, SWZ=1, GROUP=8, XCD=1, NMAX=2048, fmts=(1,))),
-    (1 << 30, 0, "i8x256k64s3", "ilv8",
-     dict(BM=256, BN=256, BK=64, WM=2, WN=2, STAGES=3, GROUP=8, XCD=1, RSP=8)),
+    # TAIL: where the last round of 256 x 256 tiles is at most a quarter full (four rounds and
+    # 64 tiles at (2048, 34816)), the columns of the whole rounds run on these tiles and the rest
+    # of N on ILV8_TAIL_TILE tiles, one round of their own; any other grid runs this row plain
+    (1 << 30, 0, "i8x256k64s3t", "ilv8",
+     dict(BM=256, BN=256, BK=64, WM=2, WN=2, STAGES=3, GROUP=8, XCD=1, RSP=8, TAIL=1)),
     (1 << 30, 0, "m256x256k64", "mfma",
      dict(BM=256, BN=256, BK=64, WM=2, WN=2, MS=32, SWZ=1, GROUP=8, XCD=1, fmts=(1,))),
 ]
@@ -133,6 +136,21 @@ LADDER_GATE_UP = [
     (1 << 30, 0, "gi8x256k64s3", "ilv8",
      dict(BM=256, BN=256, BK=64, WM=2, WN=2, STAGES=3, GROUP=8, XCD=1, RSP=8)),
 ]
+
+# the tail tiles of the TAIL rows: BM, BN, BK, WM, WN, STAGES of k_gemm_ilv8 (no split)
+ILV8_TAIL_TILE = (128, 128, 128, 2, 2, 2)
+
+
+def tail_split(M, N, BM=256, BN=256, cus=256):
+    """Columns the whole rounds of a TAIL row take (0: the row runs plain, one dispatch; else it
+    dispatches twice, the rest of N on ILV8_TAIL_TILE tiles) -- the rule of launch_ilv8_tail in
+    launch_prefill.h."""
+    nm, nn = -(-M // BM), N // BN
+    tiles = nm * nn
+    whole = tiles // cus * cus
+    if whole == 0 or whole % nm or whole // nm == nn or 4 * (tiles - whole) > cus:
+        return 0
+    return whole // nm * BN
 
 STREAM_K_STEP = 64
 STREAM_N_ROWS = 16

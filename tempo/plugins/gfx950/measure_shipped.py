@@ -168,10 +168,15 @@ def counter_pass(op: str, segfile: str, quick: bool = False) -> int:
         for _ in range(REPS - 1):
             run()
         torch.cuda.synchronize()
-        # a split-K row dispatches two kernels per launch: its main kernel, then the reduction
+        # a split-K row dispatches two kernels per launch: its main kernel, then the reduction;
+        # a TAIL row whose N it splits in two, its two parts
+        route = capi.route(fmt, M, N, K) if op != "fmha" else "k_fmha_fwd"
         per = 1 if op == "fmha" or capi.workspace_bytes(fmt, M, N, K) == 0 else 2
+        if op == "gemm_w8a16" and route.endswith("t") and route.startswith("i8"):
+            from tempo.plugins.gfx950 import manifest
+            per = 2 if manifest._select(op).tail_split(M, N) else 1
         segs.append(dict(label=label_of(M, N, K, fmt), count=REPS * per, per_launch=per,
-                         route=capi.route(fmt, M, N, K) if op != "fmha" else "k_fmha_fwd"))
+                         route=route))
     with open(segfile, "w") as f:
         json.dump(segs, f, indent=1)
     return 0

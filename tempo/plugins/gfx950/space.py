@@ -244,9 +244,9 @@ def tag(kind: str, p: dict) -> str:
             p["BM"], p["BN"], p["BK"], p["WM"], p["WN"], p["STAGES"], p["GROUP"], p["XCD"], p["RSP"],
             sw)
     if kind == "ilv8":
-        return "ilv8_m%dn%dk%d_w%dx%d_s%d_g%d_x%d_r%d_b%d%s" % (
+        return "ilv8_m%dn%dk%d_w%dx%d_s%d_g%d_x%d_r%d_b%d%s%s" % (
             p["BM"], p["BN"], p["BK"], p["WM"], p["WN"], p["STAGES"], p["GROUP"], p["XCD"], p["RSP"],
-            p["BFMT"], sw)
+            p["BFMT"], sw, "_t" if p.get("TAIL") else "")
     if kind == "dma":
         return "dma_m%dn%dk%d_w%dx%d_s%d_z%d_g%d_x%d_f%d" % (
             p["BM"], p["BN"], p["BK"], p["WM"], p["WN"], p["STAGES"], p["SWZ"], p["GROUP"], p["XCD"],
@@ -475,6 +475,10 @@ def variants(op: OpSpec) -> Iterator[Hyperform]:
                                     out.append(("ilv8", _with_split(dict(
                                         BM=BM, BN=BN, BK=BK, WM=WM, WN=WN, STAGES=ST, GROUP=G,
                                         XCD=X, RSP=RS, BFMT=b), SW)))
+                                    if BM == 256 and not SW:  # N in two parts (select.py TAIL)
+                                        out.append(("ilv8", dict(
+                                            BM=BM, BN=BN, BK=BK, WM=WM, WN=WN, STAGES=ST,
+                                            GROUP=G, XCD=X, RSP=RS, BFMT=b, TAIL=1)))
     d = DOMAINS["reg"]
     for BM in d["BM"]:
         for BN in d["BN"]:

@@ -103,7 +103,7 @@ def _match(params: dict, where) -> bool:
     for cond in where or ():
         key, _, val = cond.partition("=")
         wants = [int(v) if v.lstrip("-").isdigit() else v for v in val.split(",")]
-        if params.get(key, {"SW": 0, "SPLIT": 0, "SN": 1, "KS": 1, "TL": 0}.get(key)) not in wants:
+        if params.get(key, {"SW": 0, "SPLIT": 0, "SN": 1, "KS": 1, "TL": 0, "TAIL": 0}.get(key)) not in wants:
             return False
     return True
 

@@ -124,7 +124,9 @@ W8 = {
         ("i8x128x128k128s2w256", 2048, 1024, 5120),
         ("i8x128x128k128s2w256", 2049, 1024, 5120),
         ("m128x128k64s16", 2048, 1152, 5184),
-        ("i8x256k64s3", 2048, 7168, 5120),
+        ("i8x256k64s3t", 2048, 7168, 5120),
+        ("i8x256k64s3t", 512, 34816, 1024),   # N in two parts: 256 tiles, then 16 in 128 x 128
+        ("i8x256k64s3t", 500, 34816, 1024),
         ("m256x256k64", 512, 2048, 5184),
     ],
     2: [
@@ -177,7 +179,9 @@ W8 = {
         ("i8x128x128k128s2w256", 2048, 1024, 5120),
         ("i8x128x128k128s2w256", 2049, 1024, 5120),
         ("i8x128x128k128s2w256", 2048, 1152, 5120),
-        ("i8x256k64s3", 2048, 7168, 5120),
+        ("i8x256k64s3t", 2048, 7168, 5120),
+        ("i8x256k64s3t", 512, 34816, 1024),   # N in two parts
+        ("i8x256k64s3t", 300, 34816, 1024),
     ],
 }
 

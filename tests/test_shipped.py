@@ -53,7 +53,9 @@ def test_prefill_inc_is_generated_from_select(op, kind):
     gd = iu.module_from_spec(spec)
     spec.loader.exec_module(gd)
     insts = {gd.instantiation(r[3], r[4]) for r in _select(op).LADDER if r[3] == kind}
-    assert insts and text.count("template hipError_t launch_%s<" % kind) == len(insts)
+    plain = [ln for ln in text.splitlines()
+             if ln.startswith("template hipError_t launch_%s" % kind) and "_gu<" not in ln]
+    assert insts and len(plain) == len(insts)
     assert all(i in text for i in insts)
 
 
@@ -232,3 +234,17 @@ def test_delivery_builds_from_its_own_directory(op, tmp_path):
                        capture_output=True, text=True)
     assert r.returncode == 0, r.stderr[-3000:]
     assert os.path.getsize(exe) > 0
+
+
+def test_tail_rule_of_the_two_part_row():
+    """The W8A16 TAIL row splits N only where the last round of 256 x 256 tiles is at most a
+    quarter full and the whole rounds are whole column blocks (select.tail_split mirrors
+    launch_ilv8_tail; the GPU ladder cases at (512 | 500 | 300, 34816, 1024) run both parts)."""
+    sel = _select("gemm_w8a16")
+    assert sel.tail_split(2048, 34816) == 32768   # 1088 tiles: four rounds, then 64
+    assert sel.tail_split(512, 34816) == 32768    # 272 tiles: one round, then 16
+    assert sel.tail_split(300, 34816) == 32768
+    assert sel.tail_split(2048, 5120) == 0        # 160 tiles: no whole round
+    assert sel.tail_split(2048, 7168) == 0        # 224 tiles
+    assert sel.tail_split(4096, 34816) == 0       # 2176 tiles: the last round half full
+    assert sel.tail_split(2048, 32768) == 0       # 1024 tiles: whole rounds only
