@@ -57,10 +57,10 @@ def instantiation(kind, p, epi=0):
             p["RSP"])
     if epi:
         raise ValueError("the fused gate/up epilogue exists for the stream and interleaved kernels")
-    if kind == "ilv8" and p.get("TAIL"):  # N in two parts: whole rounds, then the tail tiles
+    if kind == "ilv8" and p.get("TAIL"):  # N in two parts: whole rounds, then the tail part
         return "launch_ilv8_tail<%d,%d,%d,%d,%d,%d,%d,%d,%d,%s>" % (
             p["BM"], p["BN"], p["BK"], p["WM"], p["WN"], p["STAGES"], p["GROUP"], p["XCD"],
-            p["RSP"], ",".join(str(v) for v in _select().ILV8_TAIL_TILE))
+            p["RSP"], ",".join(str(v) for v in _select().ILV8_TAIL[p["TAIL"]]))
     if kind == "ilv8":
         return "launch_ilv8<%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d>" % (
             p["BM"], p["BN"], p["BK"], p["WM"], p["WN"], p["STAGES"], p["GROUP"], p["XCD"],
@@ -97,6 +97,8 @@ def condition(sel, kind, p, m_max, n_min=0, gate_up=False):
             fit += " && p.K >= %d" % p["KMIN"]
         if "KMAX" in p:
             fit += " && p.K < %d" % p["KMAX"]
+        if p.get("TAIL") == 2:  # fits only where N splits in two
+            fit += " && (ilv8_tail_cols<%d,%d>(p) > 0)" % (p["BM"], p["BN"])
     else:
         fit = "(p.N %% %d) == 0 && (p.K %% %d) == 0" % (p["BN"], p["BK"])
         if "NMAX" in p:

@@ -280,8 +280,17 @@ template <int BM, int BN, int BK, int WM, int WN, int STAGES, int GROUP, int XCD
 hipError_t launch_ilv8(const W8A16Params& p, hipStream_t s, const Workspace& w);
 // The same kernel, N in two parts: whole rounds of BM x BN tiles, the rest on TBM x TBN tiles.
 template <int BM, int BN, int BK, int WM, int WN, int STAGES, int GROUP, int XCD, int RSP,
-          int TBM, int TBN, int TBK, int TWM, int TWN, int TSTAGES>
+          int TBM, int TBN, int TBK, int TWM, int TWN, int TSTAGES, int TSW, int TMINKT>
 hipError_t launch_ilv8_tail(const W8A16Params& p, hipStream_t s, const Workspace& w);
+// Columns the whole rounds of such a row take (0: it runs plain).
+template <int BM, int BN>
+inline int ilv8_tail_cols(const W8A16Params& p) {
+  constexpr int CUS = 256;
+  const int nm = (p.M + BM - 1) / BM, nn = p.N / BN;
+  const int tiles = nm * nn, whole = tiles / CUS * CUS;
+  if (whole == 0 || whole % nm || whole / nm == nn || 4 * (tiles - whole) > CUS) return 0;
+  return whole / nm * BN;
+}
 // The same kernel with the fused gate/up epilogue (p.N the output width, 2N weight rows).
 template <int BM, int BN, int BK, int WM, int WN, int STAGES, int GROUP, int XCD, int RSP>
 hipError_t launch_ilv8_gu(const W8A16Params& p, hipStream_t s, const Workspace& w);

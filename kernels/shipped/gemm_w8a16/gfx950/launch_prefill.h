@@ -47,25 +47,17 @@ hipError_t launch_ilv8(const W8A16Params& p, hipStream_t s, const Workspace& w) 
 }
 
 // N in two parts, for grids whose last round of BM x BN tiles is at most a quarter full (1088
-// tiles of 256 x 256 at (2048, 34816): four rounds and 64 tiles): the whole rounds run as they
-// are on the leading columns, and the remaining columns -- at most a quarter round of the big
-// tiles -- run on TBM x TBN tiles, four or more times as many, as one more round of their own
-// (no split, no workspace).  Every other grid runs the plain row.
+// tiles of 256 x 256 at (2048, 34816): four rounds and 64 tiles; 272 tiles of 128 x 128 at
+// (128, 34816): one round and 16): the whole rounds run as they are on the leading columns, and
+// the remaining columns run as a launch of their own on TBM x TBN tiles -- four or more times as
+// many of them (no split), or split-K towards TSW workgroups.  ilv8_tail_cols (launch.h) gives
+// the split.
 template <int BM, int BN, int BK, int WM, int WN, int STAGES, int GROUP, int XCD, int RSP,
-          int TBM, int TBN, int TBK, int TWM, int TWN, int TSTAGES>
+          int TBM, int TBN, int TBK, int TWM, int TWN, int TSTAGES, int TSW, int TMINKT>
 hipError_t launch_ilv8_tail(const W8A16Params& p, hipStream_t s, const Workspace& w) {
-  constexpr int CUS = 256;
-  static_assert(BN % TBN == 0 && (BM * BN) / (TBM * TBN) >= 4, "tail tiles of a quarter or less");
-  if (w.need) {
-    *w.need = 0;
-    return hipSuccess;
-  }
-  const int nm = (p.M + BM - 1) / BM, nn = p.N / BN;
-  const int tiles = nm * nn, whole = tiles / CUS * CUS;
-  const int nmain = whole / nm;  // column blocks of the whole rounds
-  if (whole == 0 || whole % nm || nmain == nn || 4 * (tiles - whole) > CUS)
-    return launch_ilv8<BM, BN, BK, WM, WN, STAGES, GROUP, XCD, RSP, 0, 0>(p, s, w);
-  const int n0 = nmain * BN;
+  static_assert(BN % TBN == 0 && (TSW > 0 || (BM * BN) / (TBM * TBN) >= 4),
+                "tail tiles: a quarter of the size or less, or split-K");
+  const int n0 = ilv8_tail_cols<BM, BN>(p);
   W8A16Params a = p, b = p;
   a.N = n0;
   b.N = p.N - n0;
@@ -73,9 +65,15 @@ hipError_t launch_ilv8_tail(const W8A16Params& p, hipStream_t s, const Workspace
   b.scale = p.scale + (p.fmt == 1 ? (long)n0 : (long)n0 * (p.K / p.group));
   b.zero = p.zero ? p.zero + (long)n0 * (p.K / p.group) : nullptr;
   b.C = p.C + n0;
+  if (w.need) {  // the tail's split-K workspace, if any
+    if (n0 == 0) *w.need = 0;
+    else return launch_ilv8<TBM, TBN, TBK, TWM, TWN, TSTAGES, GROUP, XCD, RSP, TSW, TMINKT>(b, s, w);
+    return hipSuccess;
+  }
+  if (n0 == 0) return launch_ilv8<BM, BN, BK, WM, WN, STAGES, GROUP, XCD, RSP, 0, 0>(p, s, w);
   const hipError_t e = launch_ilv8<BM, BN, BK, WM, WN, STAGES, GROUP, XCD, RSP, 0, 0>(a, s, w);
   if (e != hipSuccess) return e;
-  return launch_ilv8<TBM, TBN, TBK, TWM, TWN, TSTAGES, GROUP, XCD, RSP, 0, 0>(b, s, w);
+  return launch_ilv8<TBM, TBN, TBK, TWM, TWN, TSTAGES, GROUP, XCD, RSP, TSW, TMINKT>(b, s, w);
 }
 
 // Fused gate/up (EPI = 1): p.N is the output width; Wq, scale and zero hold 2N rows (gate, then

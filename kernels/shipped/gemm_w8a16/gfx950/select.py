@@ -84,6 +84,13 @@ LADDER = [
     (128, 0, "i8x128x128k128s2w256", "ilv8",
      dict(BM=128, BN=128, BK=128, WM=2, WN=2, STAGES=2, GROUP=8, XCD=1, RSP=8, SW=256, MINKT=8,
           NMAX=12288)),
+    # 64 < M <= 128, wide N, uint8, where 128 x 128 tiles make whole rounds and at most a quarter
+    # round more ((128, 34816): 256 tiles, then 16): the whole rounds unsplit on three stages,
+    # the remaining columns split-K (TAIL = 2); 1.10x the 128 x 256 row below, whose 136 tiles
+    # leave 120 CUs idle (int8: 0.94x, the row below stays)
+    (128, 12288, "i8x128x128k128s3t2", "ilv8",
+     dict(BM=128, BN=128, BK=128, WM=2, WN=2, STAGES=3, GROUP=8, XCD=1, RSP=8, TAIL=2,
+          fmts=(2,))),
     # 64 < M <= 128: 128 x 256 tiles (one tile row), split-K where the column tiles are too few
     # to fill the part (the variant driver's rows: 1.5-2.9x the line and register-staged rows)
     (128, 0, "i8x128x256s3w256", "ilv8",
@@ -137,14 +144,15 @@ LADDER_GATE_UP = [
      dict(BM=256, BN=256, BK=64, WM=2, WN=2, STAGES=3, GROUP=8, XCD=1, RSP=8)),
 ]
 
-# the tail tiles of the TAIL rows: BM, BN, BK, WM, WN, STAGES of k_gemm_ilv8 (no split)
-ILV8_TAIL_TILE = (128, 128, 128, 2, 2, 2)
+# the tail part of the TAIL rows: BM, BN, BK, WM, WN, STAGES of k_gemm_ilv8, then SW and MINKT of
+# its split-K (0, 0: no split).  TAIL = 1: a quarter-size tile, and a row whose grid does not
+# split runs plain; TAIL = 2: the same tiles with split-K, and the row fits only where N splits.
+ILV8_TAIL = {1: (128, 128, 128, 2, 2, 2, 0, 0), 2: (128, 128, 128, 2, 2, 2, 256, 2)}
 
 
 def tail_split(M, N, BM=256, BN=256, cus=256):
-    """Columns the whole rounds of a TAIL row take (0: the row runs plain, one dispatch; else it
-    dispatches twice, the rest of N on ILV8_TAIL_TILE tiles) -- the rule of launch_ilv8_tail in
-    launch_prefill.h."""
+    """Columns the whole rounds of a TAIL row take (0: the row runs plain, one dispatch; else the
+    rest of N runs as a second launch on the ILV8_TAIL tiles) -- ilv8_tail_cols of launch.h."""
     nm, nn = -(-M // BM), N // BN
     tiles = nm * nn
     whole = tiles // cus * cus
@@ -207,7 +215,8 @@ def _fits(kind, p, M, N, K, fmt=1):
     if kind == "ilv8":  # a scale group of 128 k is two k-tiles; NMAX / KMIN / KMAX (optional)
         return (N % p["BN"] == 0 and K % 128 == 0 and K <= ilv_ld_max(p)
                 and N < p.get("NMAX", 1 << 30) and K >= p.get("KMIN", 0)
-                and K < p.get("KMAX", 1 << 30))
+                and K < p.get("KMAX", 1 << 30)
+                and (p.get("TAIL") != 2 or tail_split(M, N, p["BM"], p["BN"]) > 0))
     if kind == "line" and p.get("TL"):  # tail grid: whole slabs, one k chunk
         return (N % (STREAM_N_ROWS * p["R"]) == 0 and K % LINE_K_STEP == 0
                 and line_tail_fits(p, N, K, fmt))

@@ -175,6 +175,8 @@ def counter_pass(op: str, segfile: str, quick: bool = False) -> int:
         if op == "gemm_w8a16" and route.endswith("t") and route.startswith("i8"):
             from tempo.plugins.gfx950 import manifest
             per = 2 if manifest._select(op).tail_split(M, N) else 1
+        elif op == "gemm_w8a16" and route.endswith("t2") and route.startswith("i8"):
+            per = 3 if capi.workspace_bytes(fmt, M, N, K) else 2  # whole rounds, tail (+ reduce)
         segs.append(dict(label=label_of(M, N, K, fmt), count=REPS * per, per_launch=per,
                          route=route))
     with open(segfile, "w") as f:

@@ -246,7 +246,7 @@ def tag(kind: str, p: dict) -> str:
     if kind == "ilv8":
         return "ilv8_m%dn%dk%d_w%dx%d_s%d_g%d_x%d_r%d_b%d%s%s" % (
             p["BM"], p["BN"], p["BK"], p["WM"], p["WN"], p["STAGES"], p["GROUP"], p["XCD"], p["RSP"],
-            p["BFMT"], sw, "_t" if p.get("TAIL") else "")
+            p["BFMT"], sw, {0: "", 1: "_t", 2: "_t2"}[p.get("TAIL", 0)])
     if kind == "dma":
         return "dma_m%dn%dk%d_w%dx%d_s%d_z%d_g%d_x%d_f%d" % (
             p["BM"], p["BN"], p["BK"], p["WM"], p["WN"], p["STAGES"], p["SWZ"], p["GROUP"], p["XCD"],
@@ -475,10 +475,14 @@ def variants(op: OpSpec) -> Iterator[Hyperform]:
                                     out.append(("ilv8", _with_split(dict(
                                         BM=BM, BN=BN, BK=BK, WM=WM, WN=WN, STAGES=ST, GROUP=G,
                                         XCD=X, RSP=RS, BFMT=b), SW)))
-                                    if BM == 256 and not SW:  # N in two parts (select.py TAIL)
+                                    # N in two parts (select.py TAIL): quarter-size tail
+                                    # tiles behind 256 x 256, split-K tail behind 128 x 128 x 128
+                                    tl = (1 if BM == 256 else
+                                          2 if (BM, BN, BK) == (128, 128, 128) else 0)
+                                    if tl and not SW:
                                         out.append(("ilv8", dict(
                                             BM=BM, BN=BN, BK=BK, WM=WM, WN=WN, STAGES=ST,
-                                            GROUP=G, XCD=X, RSP=RS, BFMT=b, TAIL=1)))
+                                            GROUP=G, XCD=X, RSP=RS, BFMT=b, TAIL=tl)))
     d = DOMAINS["reg"]
     for BM in d["BM"]:
         for BN in d["BN"]:

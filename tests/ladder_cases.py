@@ -114,6 +114,7 @@ W8 = {
         ("l4r1n2d3", 64, 5152, 5120),     # N % 128 == 32: no 128-column tiles
         ("i8x128x128k128s2w256", 128, 5120, 17408),
         ("i8x128x256s3w256", 128, 34816, 5120),
+        ("i8x128x256s3w256", 128, 15360, 5120),
         ("i8x128x128k128s2w256", 100, 7168, 5120),
         ("i8x128x128k128s2w256", 128, 5120, 5120),
         ("i8x128x128k128s2w256", 100, 2048, 5120),
@@ -168,7 +169,9 @@ W8 = {
         ("l4r1n2d3", 64, 5152, 5120),     # N % 128 == 32: no 128-column tiles
         ("i8x128x256k128s2w256", 128, 5120, 17408),
         ("i8x128x256k128s2w256", 77, 5120, 12288),
-        ("i8x128x256s3w256", 128, 34816, 5120),
+        ("i8x128x128k128s3t2", 128, 34816, 5120),   # one round of 128 x 128, then 16 split
+        ("i8x128x128k128s3t2", 100, 34816, 1024),
+        ("i8x128x256s3w256", 128, 15360, 5120),     # 120 tiles of 128 x 128: no whole round
         ("i8x128x128k128s2w256", 100, 7168, 5120),
         ("i8x128x128k128s2w256", 128, 5120, 5120),
         ("i8x128x128k128s2w256", 100, 2048, 5120),
