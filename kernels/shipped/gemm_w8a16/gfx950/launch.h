@@ -291,9 +291,13 @@ inline int ilv8_tail_cols(const W8A16Params& p) {
   if (whole == 0 || whole % nm || whole / nm == nn || 4 * (tiles - whole) > CUS) return 0;
   return whole / nm * BN;
 }
-// The same kernel with the fused gate/up epilogue (p.N the output width, 2N weight rows).
+// The same kernel with the fused gate/up epilogue (p.N the output width, 2N weight rows), and
+// that row with the output columns in two parts.
 template <int BM, int BN, int BK, int WM, int WN, int STAGES, int GROUP, int XCD, int RSP>
 hipError_t launch_ilv8_gu(const W8A16Params& p, hipStream_t s, const Workspace& w);
+template <int BM, int BN, int BK, int WM, int WN, int STAGES, int GROUP, int XCD, int RSP,
+          int TBM, int TBN, int TBK, int TWM, int TWN, int TSTAGES, int TSW, int TMINKT>
+hipError_t launch_ilv8_gu_tail(const W8A16Params& p, hipStream_t s, const Workspace& w);
 
 // One dispatch row: launchers without a workspace ignore it (and, asked for their need, report 0).
 inline hipError_t call_row(hipError_t (*f)(const W8A16Params&, hipStream_t), const W8A16Params& p,

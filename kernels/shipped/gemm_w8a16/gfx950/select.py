@@ -140,8 +140,10 @@ LADDER_GATE_UP = [
     # tile holds BN/2 gate and the BN/2 matching up weight rows and pairs them in the epilogue
     (128, 0, "gi8x128x256s3", "ilv8",
      dict(BM=128, BN=256, BK=64, WM=1, WN=4, STAGES=3, GROUP=8, XCD=1, RSP=8)),
-    (1 << 30, 0, "gi8x256k64s3", "ilv8",
-     dict(BM=256, BN=256, BK=64, WM=2, WN=2, STAGES=3, GROUP=8, XCD=1, RSP=8)),
+    # TAIL = 1 as in the plain ladder: where the last round of tiles (128 output columns each) is
+    # at most a quarter full ((2048, 17408): 1088 tiles), the rest on 128 x 128 tiles of 128 k
+    (1 << 30, 0, "gi8x256k64s3t", "ilv8",
+     dict(BM=256, BN=256, BK=64, WM=2, WN=2, STAGES=3, GROUP=8, XCD=1, RSP=8, TAIL=1)),
 ]
 
 # the tail part of the TAIL rows: BM, BN, BK, WM, WN, STAGES of k_gemm_ilv8, then SW and MINKT of

@@ -38,7 +38,7 @@ _ENTRY = {
     "ilv8": ("k_gemm_ilv8", ("BM", "BN", "BK", "WM", "WN", "STAGES", "GROUP", "XCD", "RSP", "BFMT",
                              "SPLIT"),
              "const _Float16*, const uint8_t*, const _Float16*, const uint8_t*, _Float16*, int, int, "
-             "int, int, int, int, float*, int",
+             "int, int, int, int, float*, int, int",
              ("common/cdna4.h", "gemm_mfma/kernel.hip", "gemm_mfma/ilv8.hip")),
     "dma": ("k_gemm_dma", ("BM", "BN", "BK", "WM", "WN", "STAGES", "SWZ", "GROUP", "XCD", "XT",
                            "MINB", "MS"),

@@ -32,8 +32,10 @@
 // A split may start at an odd k-tile: the scale group of k-tile t is t * BK / 128 in every
 // stage.
 // EPI = 1 (fused gate/up), as in k_gemm_ilv: W (and its scales and zero-points) hold the gate
-// rows then the up rows, a tile covers BN/2 output columns with BN/2 gate and the BN/2 matching
-// up rows, and the epilogue writes fp16_rn(silu(g) * u) from the two halves of the C image.
+// rows then, from row `up` on (the full output width), the up rows; a tile covers BN/2 output
+// columns with BN/2 gate and the BN/2 matching up rows, and the epilogue writes
+// fp16_rn(silu(g) * u) from the two halves of the C image.  (`up` may exceed N: a launch over
+// some of the output columns, W and the metadata offset to its first gate row.)
 // Build: -mllvm -amdgpu-sched-strategy=iterative-minreg, like k_gemm_ilv (own translation unit).
 // ============================================================================================
 template <int BM, int BN, int BK, int WM, int WN, int STAGES, int GROUP, int XCD, int RSP, int BFMT,
@@ -41,7 +43,7 @@ template <int BM, int BN, int BK, int WM, int WN, int STAGES, int GROUP, int XCD
 __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv8(
     const _Float16* __restrict__ A, const uint8_t* __restrict__ W, const _Float16* __restrict__ scale,
     const uint8_t* __restrict__ zero, _Float16* __restrict__ C, int M, int N, int K, int lda,
-    int ldw, int ldc, float* __restrict__ ws, int ksplit) {
+    int ldw, int ldc, float* __restrict__ ws, int ksplit, int up) {
   using MF = Mfma<16>;
   constexpr int SWZ = 2;
   constexpr int NW = WM * WN;
@@ -111,7 +113,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv8(
   const int cchunk = lds_chunk<BK, SWZ>(crow, lane % CPR) * 8;
   const _Float16* panelA = A + (long)m0 * lda;
   const uint8_t* panelW = W + (long)n0 * ldw;
-  const uint8_t* panelWu = W + (long)(N + n0) * ldw;  // EPI: the up half of the tile
+  const uint8_t* panelWu = W + (long)(up + n0) * ldw;  // EPI: the up half of the tile
   const int nrecA = min(M - m0, BM) * lda * 2, nrecW = BNO * ldw;
   int voff[A_BLK + B_BLK];
 #pragma unroll
@@ -127,7 +129,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv8(
   // one half per lane at a 4-byte lane stride.  EPI: rows of the up half come from the up rows.
   const int mrow = (wave % (BN / 64)) * 64 + lane;
   const bool mup = EPI && (wave % (BN / 64)) * 64 >= BN / 2;
-  const long mbase = mup ? (long)N + n0 : (long)n0;
+  const long mbase = mup ? (long)up + n0 : (long)n0;
   const int mrel = mup ? mrow - BN / 2 : mrow;  // row inside its metadata panel
   const uint8_t* panelZ = zero + (BFMT == 2 ? mbase * ng : 0);
   const _Float16* panelS = scale + (BFMT == 2 ? mbase * ng : mbase);

@@ -201,7 +201,8 @@ W8_GATE_UP = {
         ("g32r1u4", 32, 496, 65792),
         ("gi8x128x256s3", 64, 17408, 5120),
         ("gi8x128x256s3", 100, 7680, 3840),
-        ("gi8x256k64s3", 300, 7680, 3840),
+        ("gi8x256k64s3t", 300, 7680, 3840),
+        ("gi8x256k64s3t", 512, 17408, 1024),   # output columns in two parts
     ],
     2: [
         ("gl0r1n2d2", 1, 17408, 5120),
@@ -216,7 +217,8 @@ W8_GATE_UP = {
         ("g32r1u4", 32, 496, 65792),
         ("gi8x128x256s3", 64, 17408, 5120),
         ("gi8x128x256s3", 100, 7680, 3840),
-        ("gi8x256k64s3", 300, 7680, 3840),
+        ("gi8x256k64s3t", 300, 7680, 3840),
+        ("gi8x256k64s3t", 512, 17408, 1024),   # output columns in two parts
     ],
 }
 

@@ -54,7 +54,7 @@ def test_prefill_inc_is_generated_from_select(op, kind):
     spec.loader.exec_module(gd)
     insts = {gd.instantiation(r[3], r[4]) for r in _select(op).LADDER if r[3] == kind}
     plain = [ln for ln in text.splitlines()
-             if ln.startswith("template hipError_t launch_%s" % kind) and "_gu<" not in ln]
+             if ln.startswith("template hipError_t launch_%s" % kind) and "_gu" not in ln]
     assert insts and len(plain) == len(insts)
     assert all(i in text for i in insts)
 
@@ -151,7 +151,7 @@ def test_compiled_route_agrees_with_select_gate_up():
                 r = s8.select_gate_up("gemm_w8a16_gate_up", M, N, K, fmt=fmt, group=128)
                 assert capi.route(3 + fmt, M, N, K) == (r["tag"] if r else ""), (M, N, K, fmt)
     assert capi.route(3, 64, 17408, 5120) == "gi128x256k64s3"  # prefill: the interleaved kernel
-    assert capi.route(4, 300, 17408, 5120) == "gi8x256k64s3"
+    assert capi.route(4, 300, 17408, 5120) == "gi8x256k64s3t"
     assert capi.route(3, 64, 1000, 512) == ""  # N % 128 != 0 past the decode band: fallback
 
 
