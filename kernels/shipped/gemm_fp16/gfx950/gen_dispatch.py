@@ -49,6 +49,10 @@ def instantiation(kind, p, epi=0):
                                                     p.get("TPB", 1024), tail)
     if kind == "stream":
         return "launch_stream<%d,%d,%d,%d%s>" % (p["MB"], p["R"], p["U"], p.get("A", 0), tail)
+    if epi and kind == "ilv" and p.get("TAIL"):  # output columns in two parts
+        return "launch_ilv_gu_tail<%d,%d,%d,%d,%d,%d,%d,%d,%d,%s>" % (
+            p["BM"], p["BN"], p["BK"], p["WM"], p["WN"], p["STAGES"], p["GROUP"], p["XCD"],
+            p["RSP"], ",".join(str(v) for v in _select().ILV_TAIL[p["TAIL"]]))
     if epi and kind == "ilv":
         return "launch_ilv_gu<%d,%d,%d,%d,%d,%d,%d,%d,%d>" % (
             p["BM"], p["BN"], p["BK"], p["WM"], p["WN"], p["STAGES"], p["GROUP"], p["XCD"],

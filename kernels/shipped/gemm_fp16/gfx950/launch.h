@@ -267,6 +267,10 @@ hipError_t launch_ilv(const GemmParams& p, hipStream_t s, const Workspace& w);
 // The same kernel with the fused gate/up epilogue (p.N the output width, B 2N rows).
 template <int BM, int BN, int BK, int WM, int WN, int STAGES, int GROUP, int XCD, int RSP>
 hipError_t launch_ilv_gu(const GemmParams& p, hipStream_t s, const Workspace& w);
+// That row with the output columns in two parts (whole rounds, then TBM x TBN/2-column tiles).
+template <int BM, int BN, int BK, int WM, int WN, int STAGES, int GROUP, int XCD, int RSP,
+          int TBM, int TBN, int TBK, int TWM, int TWN, int TSTAGES>
+hipError_t launch_ilv_gu_tail(const GemmParams& p, hipStream_t s, const Workspace& w);
 
 // One dispatch row: launchers without a workspace ignore it (and, asked for their need, report 0).
 inline hipError_t call_row(hipError_t (*f)(const GemmParams&, hipStream_t), const GemmParams& p,

@@ -92,9 +92,14 @@ LADDER_GATE_UP = [
     (32, 0, "g32r1u4", "stream", dict(MB=2, R=1, U=4, A=0)),
     (128, 0, "gi128x256k64s3", "ilv",
      dict(BM=128, BN=256, BK=64, WM=1, WN=4, STAGES=3, GROUP=8, XCD=1, RSP=8)),
-    (1 << 30, 0, "gi256x256k64w4r8", "ilv",
-     dict(BM=256, BN=256, BK=64, WM=2, WN=2, STAGES=2, GROUP=8, XCD=1, RSP=8)),
+    # TAIL: where the last round of tiles (128 output columns each) is at most a quarter full
+    # ((2048, 17408): 1088 tiles), the whole rounds, then the rest on ILV_TAIL tiles
+    (1 << 30, 0, "gi256x256k64w4r8t", "ilv",
+     dict(BM=256, BN=256, BK=64, WM=2, WN=2, STAGES=2, GROUP=8, XCD=1, RSP=8, TAIL=1)),
 ]
+
+# the tail tiles of the gate/up TAIL row: BM, BN, BK, WM, WN, STAGES of k_gemm_ilv (no split)
+ILV_TAIL = {1: (128, 128, 64, 2, 2, 3)}
 
 # Divisibility each kind needs (checked at run time by dispatch.inc, mirrored here).
 STREAM_K_STEP = 64  # k per pipeline step of the stream kernel

@@ -33,7 +33,8 @@ CAPABILITIES = frozenset({
 # kernel symbol, template-parameter order, and argument list, per kind: the emitter's only data
 _ENTRY = {
     "ilv": ("k_gemm_ilv", ("BM", "BN", "BK", "WM", "WN", "STAGES", "GROUP", "XCD", "RSP", "SPLIT"),
-            "const _Float16*, const _Float16*, _Float16*, int, int, int, int, int, int, float*, int",
+            "const _Float16*, const _Float16*, _Float16*, int, int, int, int, int, int, float*, int, "
+            "int",
             ("common/cdna4.h", "gemm_mfma/kernel.hip", "gemm_mfma/ilv.hip")),
     "ilv8": ("k_gemm_ilv8", ("BM", "BN", "BK", "WM", "WN", "STAGES", "GROUP", "XCD", "RSP", "BFMT",
                              "SPLIT"),

@@ -65,7 +65,7 @@ template <int BM, int BN, int BK, int WM, int WN, int STAGES, int GROUP, int XCD
           int SPLIT = 0, int EPI = 0>
 __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv(
     const _Float16* __restrict__ A, const _Float16* __restrict__ B, _Float16* __restrict__ C,
-    int M, int N, int K, int lda, int ldb, int ldc, float* __restrict__ ws, int ksplit) {
+    int M, int N, int K, int lda, int ldb, int ldc, float* __restrict__ ws, int ksplit, int up) {
   using MF = Mfma<16>;
   constexpr int SWZ = 2;
   constexpr int NW = WM * WN;
@@ -119,8 +119,9 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv(
   const int cchunk = lds_chunk<BK, SWZ>(crow, lane % CPR) * 8;    // element offset in the row
   const _Float16* panelA = A + (long)m0 * lda;
   const _Float16* panelB = B + (long)n0 * ldb;
-  // EPI: the up half of the B tile starts at row N + n0
-  const _Float16* panelU = B + (long)(N + n0) * ldb;
+  // EPI: the up half of the B tile starts at row up + n0 (up = the full output width; a launch
+  // over some of the output columns has B offset to its first gate row)
+  const _Float16* panelU = B + (long)(up + n0) * ldb;
   const int nrecA = min(M - m0, BM) * lda * 2, nrecB = (EPI ? BN / 2 : BN) * ldb * 2;
   int voff[L];
 #pragma unroll

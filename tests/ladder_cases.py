@@ -70,8 +70,9 @@ FP16_GATE_UP = [
     ("g32r1u4", 32, 496, 65792),
     ("gi128x256k64s3", 64, 17408, 5120),
     ("gi128x256k64s3", 100, 7680, 3840),    # ragged M
-    ("gi256x256k64w4r8", 300, 7680, 3840),
-    ("gi256x256k64w4r8", 512, 4096, 5120),
+    ("gi256x256k64w4r8t", 300, 7680, 3840),
+    ("gi256x256k64w4r8t", 512, 4096, 5120),
+    ("gi256x256k64w4r8t", 512, 17408, 1024),   # output columns in two parts
 ]
 
 W8 = {
