@@ -111,8 +111,10 @@ LADDER = [
     # TAIL: where the last round of 256 x 256 tiles is at most a quarter full (four rounds and
     # 64 tiles at (2048, 34816)), the columns of the whole rounds run on these tiles and the rest
     # of N on ILV8_TAIL_TILE tiles, one round of their own; any other grid runs this row plain
-    (1 << 30, 0, "i8x256k64s3t", "ilv8",
-     dict(BM=256, BN=256, BK=64, WM=2, WN=2, STAGES=3, GROUP=8, XCD=1, RSP=8, TAIL=1)),
+    # 1 x 4 waves (wave tiles of 256 x 64): each wave dequantises only its own 64 weight rows,
+    # where 2 x 2 waves dequantise every weight fragment twice (1.04-1.05x at M = 2048)
+    (1 << 30, 0, "i8x256w1x4k64s3t", "ilv8",
+     dict(BM=256, BN=256, BK=64, WM=1, WN=4, STAGES=3, GROUP=8, XCD=1, RSP=8, TAIL=1)),
     (1 << 30, 0, "m256x256k64", "mfma",
      dict(BM=256, BN=256, BK=64, WM=2, WN=2, MS=32, SWZ=1, GROUP=8, XCD=1, fmts=(1,))),
 ]
@@ -142,8 +144,8 @@ LADDER_GATE_UP = [
      dict(BM=128, BN=256, BK=64, WM=1, WN=4, STAGES=3, GROUP=8, XCD=1, RSP=8)),
     # TAIL = 1 as in the plain ladder: where the last round of tiles (128 output columns each) is
     # at most a quarter full ((2048, 17408): 1088 tiles), the rest on 128 x 128 tiles of 128 k
-    (1 << 30, 0, "gi8x256k64s3t", "ilv8",
-     dict(BM=256, BN=256, BK=64, WM=2, WN=2, STAGES=3, GROUP=8, XCD=1, RSP=8, TAIL=1)),
+    (1 << 30, 0, "gi8x256w1x4k64s3t", "ilv8",
+     dict(BM=256, BN=256, BK=64, WM=1, WN=4, STAGES=3, GROUP=8, XCD=1, RSP=8, TAIL=1)),
 ]
 
 # the tail part of the TAIL rows: BM, BN, BK, WM, WN, STAGES of k_gemm_ilv8, then SW and MINKT of

@@ -126,9 +126,9 @@ W8 = {
         ("i8x128x128k128s2w256", 2048, 1024, 5120),
         ("i8x128x128k128s2w256", 2049, 1024, 5120),
         ("m128x128k64s16", 2048, 1152, 5184),
-        ("i8x256k64s3t", 2048, 7168, 5120),
-        ("i8x256k64s3t", 512, 34816, 1024),   # N in two parts: 256 tiles, then 16 in 128 x 128
-        ("i8x256k64s3t", 500, 34816, 1024),
+        ("i8x256w1x4k64s3t", 2048, 7168, 5120),
+        ("i8x256w1x4k64s3t", 512, 34816, 1024),   # N in two parts: 256 tiles, then 16 in 128 x 128
+        ("i8x256w1x4k64s3t", 500, 34816, 1024),
         ("m256x256k64", 512, 2048, 5184),
     ],
     2: [
@@ -183,9 +183,9 @@ W8 = {
         ("i8x128x128k128s2w256", 2048, 1024, 5120),
         ("i8x128x128k128s2w256", 2049, 1024, 5120),
         ("i8x128x128k128s2w256", 2048, 1152, 5120),
-        ("i8x256k64s3t", 2048, 7168, 5120),
-        ("i8x256k64s3t", 512, 34816, 1024),   # N in two parts
-        ("i8x256k64s3t", 300, 34816, 1024),
+        ("i8x256w1x4k64s3t", 2048, 7168, 5120),
+        ("i8x256w1x4k64s3t", 512, 34816, 1024),   # N in two parts
+        ("i8x256w1x4k64s3t", 300, 34816, 1024),
     ],
 }
 
@@ -202,8 +202,8 @@ W8_GATE_UP = {
         ("g32r1u4", 32, 496, 65792),
         ("gi8x128x256s3", 64, 17408, 5120),
         ("gi8x128x256s3", 100, 7680, 3840),
-        ("gi8x256k64s3t", 300, 7680, 3840),
-        ("gi8x256k64s3t", 512, 17408, 1024),   # output columns in two parts
+        ("gi8x256w1x4k64s3t", 300, 7680, 3840),
+        ("gi8x256w1x4k64s3t", 512, 17408, 1024),   # output columns in two parts
     ],
     2: [
         ("gl0r1n2d2", 1, 17408, 5120),
@@ -218,8 +218,8 @@ W8_GATE_UP = {
         ("g32r1u4", 32, 496, 65792),
         ("gi8x128x256s3", 64, 17408, 5120),
         ("gi8x128x256s3", 100, 7680, 3840),
-        ("gi8x256k64s3t", 300, 7680, 3840),
-        ("gi8x256k64s3t", 512, 17408, 1024),   # output columns in two parts
+        ("gi8x256w1x4k64s3t", 300, 7680, 3840),
+        ("gi8x256w1x4k64s3t", 512, 17408, 1024),   # output columns in two parts
     ],
 }
 

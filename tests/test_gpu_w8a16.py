@@ -153,7 +153,7 @@ def test_w8a16_parity_interleaved_prefill_rows(gpu, fmt, M, N, K):
     elif N < 2048:
         assert route == "i8x128x128k128s2w256"
     else:
-        assert route == "i8x256k64s3t"
+        assert route == "i8x256w1x4k64s3t"
     A = O.randn_f16((M, K), 13, K ** -0.5)
     q, s, z = make_weights(N, K, fmt, 79)
     C = _run(A, q, s, z, fmt, gpu)

@@ -151,7 +151,7 @@ def test_compiled_route_agrees_with_select_gate_up():
                 r = s8.select_gate_up("gemm_w8a16_gate_up", M, N, K, fmt=fmt, group=128)
                 assert capi.route(3 + fmt, M, N, K) == (r["tag"] if r else ""), (M, N, K, fmt)
     assert capi.route(3, 64, 17408, 5120) == "gi128x256k64s3"  # prefill: the interleaved kernel
-    assert capi.route(4, 300, 17408, 5120) == "gi8x256k64s3t"
+    assert capi.route(4, 300, 17408, 5120) == "gi8x256w1x4k64s3t"
     assert capi.route(3, 64, 1000, 512) == ""  # N % 128 != 0 past the decode band: fallback
 
 
