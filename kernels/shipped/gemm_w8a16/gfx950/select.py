@@ -66,8 +66,8 @@ LADDER = [
           NMAX=12288, KMIN=12288)),
     # 32 < M <= 64, narrow N: 128 x 128 tiles of 128 k, split-K (1.23x the line row below at
     # (64, 7168, 5120))
-    (64, 0, "i8x128x128k128s2w256", "ilv8",
-     dict(BM=128, BN=128, BK=128, WM=2, WN=2, STAGES=2, GROUP=8, XCD=1, RSP=8, SW=256, MINKT=8,
+    (64, 0, "i8x128x128w1x4k128s2w256", "ilv8",
+     dict(BM=128, BN=128, BK=128, WM=1, WN=4, STAGES=2, GROUP=8, XCD=1, RSP=8, SW=256, MINKT=8,
           NMAX=12288)),
     (64, 0, "l4r1n2d3", "line", dict(MB=4, R=1, D=3, SN=2, W=2048)),
     # 64 < M <= 128, narrow N (< 2048): the line kernel with eight activation blocks, two slab
@@ -78,18 +78,19 @@ LADDER = [
     (128, 0, "i8x128x256k128s2w256", "ilv8",
      dict(BM=128, BN=256, BK=128, WM=1, WN=4, STAGES=2, GROUP=8, XCD=1, RSP=8, SW=256, MINKT=8,
           NMAX=12288, KMIN=12288, fmts=(2,))),
-    # 64 < M <= 128, N < 12288: 128 x 128 tiles (2 x 2 waves of 64 x 64) of 128 k -- every
-    # k-tile takes whole 128-byte lines of the weight rows -- two stages, split-K (1.04-1.21x
-    # the 64-k tile rows at N = 5120-7168, both formats)
-    (128, 0, "i8x128x128k128s2w256", "ilv8",
-     dict(BM=128, BN=128, BK=128, WM=2, WN=2, STAGES=2, GROUP=8, XCD=1, RSP=8, SW=256, MINKT=8,
+    # 64 < M <= 128, N < 12288: 128 x 128 tiles of 128 k -- every k-tile takes whole 128-byte
+    # lines of the weight rows -- two stages, split-K (1.04-1.21x the 64-k tile rows at N =
+    # 5120-7168, both formats); 1 x 4 waves of 128 x 32, each dequantising only its own weight
+    # rows (1.03-1.08x 2 x 2 waves of 64 x 64)
+    (128, 0, "i8x128x128w1x4k128s2w256", "ilv8",
+     dict(BM=128, BN=128, BK=128, WM=1, WN=4, STAGES=2, GROUP=8, XCD=1, RSP=8, SW=256, MINKT=8,
           NMAX=12288)),
     # 64 < M <= 128, wide N, uint8, where 128 x 128 tiles make whole rounds and at most a quarter
     # round more ((128, 34816): 256 tiles, then 16): the whole rounds unsplit on three stages,
     # the remaining columns split-K (TAIL = 2); 1.10x the 128 x 256 row below, whose 136 tiles
     # leave 120 CUs idle (int8: 0.94x, the row below stays)
-    (128, 12288, "i8x128x128k128s3t2", "ilv8",
-     dict(BM=128, BN=128, BK=128, WM=2, WN=2, STAGES=3, GROUP=8, XCD=1, RSP=8, TAIL=2,
+    (128, 12288, "i8x128x128w1x4k128s3t2", "ilv8",
+     dict(BM=128, BN=128, BK=128, WM=1, WN=4, STAGES=3, GROUP=8, XCD=1, RSP=8, TAIL=2,
           fmts=(2,))),
     # 64 < M <= 128: 128 x 256 tiles (one tile row), split-K where the column tiles are too few
     # to fill the part (the variant driver's rows: 1.5-2.9x the line and register-staged rows)
@@ -101,8 +102,8 @@ LADDER = [
     # narrow N (fewer than 8 tiles of 256 columns): 256x256 tiles leave most CUs idle; 128 x 128
     # tiles of 128 k with split-K fill the part (1.08x the 128 x 256 64-k row at (2048, 1024,
     # 5120), which was 1.97x the 128 x 128 register-staged row behind them)
-    (1 << 30, 0, "i8x128x128k128s2w256", "ilv8",
-     dict(BM=128, BN=128, BK=128, WM=2, WN=2, STAGES=2, GROUP=8, XCD=1, RSP=8, SW=256, MINKT=8,
+    (1 << 30, 0, "i8x128x128w1x4k128s2w256", "ilv8",
+     dict(BM=128, BN=128, BK=128, WM=1, WN=4, STAGES=2, GROUP=8, XCD=1, RSP=8, SW=256, MINKT=8,
           NMAX=2048)),
     # what the 128-k tiles leave at narrow N: K % 128 == 64 (int8 only; uint8 groups are whole
     # 128-k)
@@ -151,7 +152,7 @@ LADDER_GATE_UP = [
 # the tail part of the TAIL rows: BM, BN, BK, WM, WN, STAGES of k_gemm_ilv8, then SW and MINKT of
 # its split-K (0, 0: no split).  TAIL = 1: a quarter-size tile, and a row whose grid does not
 # split runs plain; TAIL = 2: the same tiles with split-K, and the row fits only where N splits.
-ILV8_TAIL = {1: (128, 128, 128, 2, 2, 2, 0, 0), 2: (128, 128, 128, 2, 2, 2, 256, 2)}
+ILV8_TAIL = {1: (128, 128, 128, 1, 4, 2, 0, 0), 2: (128, 128, 128, 1, 4, 2, 256, 2)}
 
 
 def tail_split(M, N, BM=256, BN=256, cus=256):

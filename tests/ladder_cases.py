@@ -110,21 +110,21 @@ W8 = {
         ("h32r1u4n2", 32, 512, 65792),
         ("l4r1n4d3", 64, 34816, 5120),
         ("i8x128x256k128s2w256", 64, 5120, 17408),
-        ("i8x128x128k128s2w256", 64, 5120, 6144),
-        ("i8x128x128k128s2w256", 40, 7168, 5120),
+        ("i8x128x128w1x4k128s2w256", 64, 5120, 6144),
+        ("i8x128x128w1x4k128s2w256", 40, 7168, 5120),
         ("l4r1n2d3", 64, 5152, 5120),     # N % 128 == 32: no 128-column tiles
-        ("i8x128x128k128s2w256", 128, 5120, 17408),
+        ("i8x128x128w1x4k128s2w256", 128, 5120, 17408),
         ("i8x128x256s3w256", 128, 34816, 5120),
         ("i8x128x256s3w256", 128, 15360, 5120),
-        ("i8x128x128k128s2w256", 100, 7168, 5120),
-        ("i8x128x128k128s2w256", 128, 5120, 5120),
-        ("i8x128x128k128s2w256", 100, 2048, 5120),
+        ("i8x128x128w1x4k128s2w256", 100, 7168, 5120),
+        ("i8x128x128w1x4k128s2w256", 128, 5120, 5120),
+        ("i8x128x128w1x4k128s2w256", 100, 2048, 5120),
         ("l8r1n2d2k8", 128, 1024, 5120),
         ("l8r1n2d2k8", 100, 1024, 5120),
         ("l8r1n2d3", 128, 5152, 5120),
         ("m128x128k64", 256, 5120, 5120),
-        ("i8x128x128k128s2w256", 2048, 1024, 5120),
-        ("i8x128x128k128s2w256", 2049, 1024, 5120),
+        ("i8x128x128w1x4k128s2w256", 2048, 1024, 5120),
+        ("i8x128x128w1x4k128s2w256", 2049, 1024, 5120),
         ("m128x128k64s16", 2048, 1152, 5184),
         ("i8x256w1x4k64s3t", 2048, 7168, 5120),
         ("i8x256w1x4k64s3t", 512, 34816, 1024),   # N in two parts: 256 tiles, then 16 in 128 x 128
@@ -165,24 +165,24 @@ W8 = {
         ("h32r1u4n2", 32, 512, 65792),
         ("l4r1n4d3", 64, 34816, 5120),
         ("i8x128x256k128s2w256", 64, 5120, 17408),
-        ("i8x128x128k128s2w256", 64, 5120, 6144),
-        ("i8x128x128k128s2w256", 40, 7168, 5120),
+        ("i8x128x128w1x4k128s2w256", 64, 5120, 6144),
+        ("i8x128x128w1x4k128s2w256", 40, 7168, 5120),
         ("l4r1n2d3", 64, 5152, 5120),     # N % 128 == 32: no 128-column tiles
         ("i8x128x256k128s2w256", 128, 5120, 17408),
         ("i8x128x256k128s2w256", 77, 5120, 12288),
-        ("i8x128x128k128s3t2", 128, 34816, 5120),   # one round of 128 x 128, then 16 split
-        ("i8x128x128k128s3t2", 100, 34816, 1024),
+        ("i8x128x128w1x4k128s3t2", 128, 34816, 5120),   # one round of 128 x 128, then 16 split
+        ("i8x128x128w1x4k128s3t2", 100, 34816, 1024),
         ("i8x128x256s3w256", 128, 15360, 5120),     # 120 tiles of 128 x 128: no whole round
-        ("i8x128x128k128s2w256", 100, 7168, 5120),
-        ("i8x128x128k128s2w256", 128, 5120, 5120),
-        ("i8x128x128k128s2w256", 100, 2048, 5120),
+        ("i8x128x128w1x4k128s2w256", 100, 7168, 5120),
+        ("i8x128x128w1x4k128s2w256", 128, 5120, 5120),
+        ("i8x128x128w1x4k128s2w256", 100, 2048, 5120),
         ("l8r1n2d2k8", 128, 1024, 5120),
         ("l8r1n2d2k8", 100, 1024, 5120),
         ("l8r1n2d3", 128, 5152, 5120),
         ("m128x128k64", 256, 5120, 5120),
-        ("i8x128x128k128s2w256", 2048, 1024, 5120),
-        ("i8x128x128k128s2w256", 2049, 1024, 5120),
-        ("i8x128x128k128s2w256", 2048, 1152, 5120),
+        ("i8x128x128w1x4k128s2w256", 2048, 1024, 5120),
+        ("i8x128x128w1x4k128s2w256", 2049, 1024, 5120),
+        ("i8x128x128w1x4k128s2w256", 2048, 1152, 5120),
         ("i8x256w1x4k64s3t", 2048, 7168, 5120),
         ("i8x256w1x4k64s3t", 512, 34816, 1024),   # N in two parts
         ("i8x256w1x4k64s3t", 300, 34816, 1024),

@@ -151,7 +151,7 @@ def test_w8a16_parity_interleaved_prefill_rows(gpu, fmt, M, N, K):
         if fmt == 2:
             return
     elif N < 2048:
-        assert route == "i8x128x128k128s2w256"
+        assert route == "i8x128x128w1x4k128s2w256"
     else:
         assert route == "i8x256w1x4k64s3t"
     A = O.randn_f16((M, K), 13, K ** -0.5)
