@@ -141,8 +141,8 @@ LADDER_GATE_UP = [
     (32, 0, "g32r1u4", "stream", dict(MB=2, R=1, U=4, A=0)),
     # M > 32 (and what the decode rows leave): the interleaved int8 kernel with EPI = 1 -- each
     # tile holds BN/2 gate and the BN/2 matching up weight rows and pairs them in the epilogue
-    (128, 0, "gi8x128x256s3", "ilv8",
-     dict(BM=128, BN=256, BK=64, WM=1, WN=4, STAGES=3, GROUP=8, XCD=1, RSP=8)),
+    (128, 0, "gi8x128x256k128s2", "ilv8",
+     dict(BM=128, BN=256, BK=128, WM=1, WN=4, STAGES=2, GROUP=8, XCD=1, RSP=8)),
     # TAIL = 1 as in the plain ladder: where the last round of tiles (128 output columns each) is
     # at most a quarter full ((2048, 17408): 1088 tiles), the rest on 128 x 128 tiles of 128 k
     (1 << 30, 0, "gi8x256w1x4k64s3t", "ilv8",

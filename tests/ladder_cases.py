@@ -200,8 +200,8 @@ W8_GATE_UP = {
         ("gh16r1u2n2", 16, 512, 65664),
         ("gh32r1u2n4", 32, 512, 65664),
         ("g32r1u4", 32, 496, 65792),
-        ("gi8x128x256s3", 64, 17408, 5120),
-        ("gi8x128x256s3", 100, 7680, 3840),
+        ("gi8x128x256k128s2", 64, 17408, 5120),
+        ("gi8x128x256k128s2", 100, 7680, 3840),
         ("gi8x256w1x4k64s3t", 300, 7680, 3840),
         ("gi8x256w1x4k64s3t", 512, 17408, 1024),   # output columns in two parts
     ],
@@ -216,8 +216,8 @@ W8_GATE_UP = {
         ("gh16r1u4n2", 16, 512, 65792),
         ("gh32r1u4n4", 32, 512, 65792),
         ("g32r1u4", 32, 496, 65792),
-        ("gi8x128x256s3", 64, 17408, 5120),
-        ("gi8x128x256s3", 100, 7680, 3840),
+        ("gi8x128x256k128s2", 64, 17408, 5120),
+        ("gi8x128x256k128s2", 100, 7680, 3840),
         ("gi8x256w1x4k64s3t", 300, 7680, 3840),
         ("gi8x256w1x4k64s3t", 512, 17408, 1024),   # output columns in two parts
     ],
