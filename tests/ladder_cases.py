@@ -18,7 +18,9 @@ FP16 = [
     ("l0r1d3", 1, 15360, 3840),
     ("s1a_r1u4", 1, 512, 65792),
     ("l1r1n4d3", 8, 15360, 3840),
+    ("l1r1n4d3", 16, 15360, 3840),          # the C2 point M = 16: the row's whole 16-row M tile
     ("l1r1n4d4k8", 16, 3840, 15360),        # 60 workgroups x 8 k slices
+    ("l1r1n4d4k8", 8, 3840, 15360),         # the C2 point M = 8, N = 3840
     ("l1r1n4d4k8", 5, 3840, 12288),         # ragged M, 12 steps per slice
     ("l1r1n4d4k8", 16, 3840, 12416),        # 97 steps (prime): no slices (no workspace)
     ("l1r1d4", 16, 3840, 3840),

@@ -96,6 +96,33 @@ def test_gemm_fp16_parity(gpu, M, N, K):
     assert rel <= 3e-3 and bad == 0
 
 
+# BASELINE config 2, every point of the decode sweep: (N, K) in {(15360, 3840), (3840, 15360)} x
+# M in {1, 8, 16, 32, 64, 128, 256}
+C2_SWEEP = [(M, N, K) for (N, K) in ((15360, 3840), (3840, 15360))
+            for M in (1, 8, 16, 32, 64, 128, 256)]
+
+
+@pytest.mark.parametrize("M,N,K", C2_SWEEP)
+def test_gemm_fp16_parity_config2_sweep(gpu, M, N, K):
+    """Each C2 point in full: coverage of every cell, the whole output and its worst row against
+    the oracle, and the fp64 spot rule on 512 cells; the test id carries the shape and the log the
+    ladder row the compiled dispatcher took."""
+    from cuda_tempiler_amd import capi
+
+    say("config2", M, N, K, capi.route(0, M, N, K))
+    A = O.randn_f16((M, K), 11, K ** -0.5)
+    B = O.randn_f16((N, K), 77, K ** -0.5)
+    C = _run(A, B, gpu)
+    assert O.count_poison(C) == 0
+    ref = O.gemm_f16(A, B)
+    rel = O.rel_l2(C, ref)
+    d = C.astype(np.float64) - ref.astype(np.float64)
+    row_rel = np.sqrt((d * d).sum(1) / np.maximum((ref.astype(np.float64) ** 2).sum(1), 1e-30))
+    worst, bad = O.spot_fp64(A, B, C, cells=512)
+    say("  relL2 %.3e worst row %.3e spot %.3e" % (rel, row_rel.max(), worst))
+    assert rel <= 3e-3 and row_rel.max() <= 3e-3 and bad == 0
+
+
 def test_gemm_fp16_parity_config1(gpu):
     """BASELINE config 1 at full size: 4096 x 15360 x 3840.  Coverage over every cell; the WHOLE
     output against the oracle (relL2), fp64 on 2048 cells, and the worst row's relL2 so a

@@ -106,6 +106,38 @@ def test_dequant_asym_exhaustive_over_q_and_z():
         assert np.array_equal(got.view(np.uint16), ref.view(np.uint16))
 
 
+def test_dequant_asym_distinct_scales_per_row_and_group():
+    """Every (row, group) gets its own scale and zero-point, so a swapped or shifted metadata
+    index changes the result.  Reference: the GPTQ formula of bench/gemm_baseline.py:229,
+    W[k, n] = half((q[k, n] - z[k // G, n]) * s[k // G, n]), evaluated here in numpy on the
+    reference's k-major storage and transposed to the oracle's [N, K] layout."""
+    G, N, K = 128, 48, 1024
+    ng = K // G
+    g = np.random.Generator(np.random.PCG64(21))
+    q_kn = g.integers(0, 256, (K, N), dtype=np.uint8)
+    z_gn = g.integers(100, 157, (ng, N), dtype=np.uint8)
+    # N * ng distinct fp16 scales in [0.5, 1.5] / 255 (a random draw of distinct bit patterns)
+    lo = np.float16(0.5 / 255).view(np.uint16)
+    hi = np.float16(1.5 / 255).view(np.uint16)
+    bits = g.choice(np.arange(lo, hi + 1, dtype=np.uint16), N * ng, replace=False)
+    s_gn = bits.reshape(ng, N).view(np.float16)
+    gidx = np.arange(K) // G
+    W_kn = ((q_kn.astype(np.float32) - z_gn.astype(np.float32)[gidx])
+            * s_gn.astype(np.float32)[gidx]).astype(np.float16)
+    got = O.dequant_asym(q_kn.T.copy(), s_gn.T.copy(), z_gn.T.copy(), G=G)
+    assert np.array_equal(got.view(np.uint16), W_kn.T.view(np.uint16))
+    # sensitivity: the same formula with the metadata of the next group (a shifted index) or of
+    # the row's mirror (a transposed index) disagrees almost everywhere
+    for perm in (np.roll(np.arange(ng), 1), None):
+        if perm is None:
+            s_bad, z_bad = s_gn[:, ::-1], z_gn[:, ::-1]
+        else:
+            s_bad, z_bad = s_gn[perm], z_gn[perm]
+        W_bad = ((q_kn.astype(np.float32) - z_bad.astype(np.float32)[gidx])
+                 * s_bad.astype(np.float32)[gidx]).astype(np.float16)
+        assert np.mean(got.view(np.uint16) != W_bad.T.view(np.uint16)) > 0.9
+
+
 def test_dequant_invariants():
     g = np.random.Generator(np.random.PCG64(4))
     q = g.integers(0, 256, (8, 256), dtype=np.uint8)
