@@ -50,8 +50,9 @@ class Gfx950Classifier:
         raise NotSupported("gfx950 ISA carries no scheduling control words")
 
 
-def parse_disasm(text: str, kernel_regex: str = ".*") -> dict:
-    """{symbol: [mnemonic, ...]} from llvm-objdump -d output."""
+def parse_disasm(text: str, kernel_regex: str = ".*", operands: bool = False) -> dict:
+    """{symbol: [mnemonic, ...]} from llvm-objdump -d output; with operands=True the entries are
+    (mnemonic, operand text) pairs, the operand text cut at the encoding comment."""
     rx = re.compile(kernel_regex)
     cur, out = None, {}
     for line in text.splitlines():
@@ -63,7 +64,10 @@ def parse_disasm(text: str, kernel_regex: str = ".*") -> dict:
             continue
         if cur is None:
             continue
-        m = re.match(r"^\s+([a-z_][a-z0-9_]*)\b", line)
+        m = re.match(r"^\s+([a-z_][a-z0-9_]*)\b(.*)$", line)
         if m:
-            out[cur].append(m.group(1))
+            if operands:
+                out[cur].append((m.group(1), m.group(2).split("//")[0].strip()))
+            else:
+                out[cur].append(m.group(1))
     return out

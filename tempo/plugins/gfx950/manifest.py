@@ -173,13 +173,72 @@ def gate_numbers(op, jobs=8):
         return list(ex.map(_compile_body, gate_bodies(op)))
 
 
-def build_numbers(op):
-    """Compile each ladder row's kernel alone (rendered by the plugin) and read our numbers."""
+# Ladder-row kinds whose operand copies are global->LDS DMA (a build of one of them with no LDS-DMA
+# instruction has fallen back to register-staged loads)
+DMA_KINDS = ("ilv", "ilv8", "dma", "line")
+# Shipped rows allowed to keep a spill, with the reason and the measured cost of removing it
+# (none today: the gate below refuses every spill)
+SPILL_WAIVERS = {}
+
+
+def gate_build(numbers: dict, waivers: dict = None) -> list:
+    """The build gate of the verify stage: every shipped row compiles with no spilled VGPR or
+    SGPR, no scratch and no scratch instruction (reference: the spill and stack numbers read
+    per build, tempo/plugins/sm70/toolchain.py:102-112, and the loop-spill field of the
+    contract's BuildResult, tempo/plugins/base.py:534), and every LDS-DMA kind copies through
+    LDS-DMA.  Returns the failures as "row: reason" lines; a waived row is listed as waived."""
+    waivers = SPILL_WAIVERS if waivers is None else waivers
+    bad = []
+    for key, b in numbers.items():
+        why = []
+        if b.get("vgpr_spill") or b.get("sgpr_spill"):
+            why.append("spills %d VGPRs, %d SGPRs" % (b.get("vgpr_spill", 0), b.get("sgpr_spill", 0)))
+        if b.get("scratch_bytes_per_lane") or b.get("scratch_insts"):
+            why.append("scratch %d B/lane, %d scratch instructions"
+                       % (b.get("scratch_bytes_per_lane", 0), b.get("scratch_insts", 0)))
+        if b.get("kind") in DMA_KINDS and not b.get("lds_dma"):
+            why.append("kind %s without an LDS-DMA copy" % b.get("kind"))
+        if why and key not in waivers and b.get("tag") not in waivers:
+            bad.append("%s: %s" % (key, "; ".join(why)))
+    return bad
+
+
+def source_numbers(plug, src, kind, tag):
+    """Compile one kernel source alone (device code object) and read the build's numbers and
+    its instruction mix."""
+    from tempo.plugins.gfx950.classifier import parse_disasm
+    from tempo.plugins.gfx950.toolchain import isa_summary
+
+    with tempfile.TemporaryDirectory() as td:
+        obj = os.path.join(td, "k.o")
+        b = plug.toolchain.compile(src, obj, mode="device")
+        if not b.ok:
+            raise RuntimeError("row %s does not compile:\n%s" % (tag, b.log[-3000:]))
+        isa = isa_summary(sum(parse_disasm(plug.toolchain.disasm(obj), operands=True).values(),
+                              []))
+    return dict(tag=tag, kind=kind, regs=b.regs, vgpr_spill=b.spill_st, sgpr_spill=b.spill_ld,
+                scratch_bytes_per_lane=b.stack_frame, lds_static=b.smem_static, mfma=isa["mfma"],
+                lds_dma=isa["lds_dma"], lds_dma_buffer=isa["lds_dma_buffer"],
+                buffer_load=isa["buffer_load"], ds_read_b128=isa["ds_read_b128"],
+                scratch_insts=isa["scratch"])
+
+
+def row_numbers(plug, spec, h, kind, tag):
+    """A ladder row rendered by the plugin, compiled alone: source_numbers()."""
+    r = plug.skeletons.render(spec, h)
+    with tempfile.TemporaryDirectory() as td:
+        src = os.path.join(td, r.filename)
+        with open(src, "w") as f:
+            f.write(r.source)
+        return source_numbers(plug, src, kind, tag)
+
+
+def build_numbers(op, gate: bool = True):
+    """Compile each ladder row's kernel alone (rendered by the plugin) and read our numbers; with
+    gate=True a row that fails gate_build() stops the manifest."""
     sys.path.insert(0, ROOT)
     from tempo.plugins.base import Hyperform, OpSpec
     from tempo.plugins.gfx950 import load
-    from tempo.plugins.gfx950.toolchain import isa_summary
-    from tempo.plugins.gfx950.classifier import parse_disasm
 
     plug = load()
     sel = _select(op)
@@ -194,21 +253,25 @@ def build_numbers(op):
                 continue
             params = hyper_params(kind, p, fmt, epi)
             h = Hyperform(plugin="gfx950", params=params, key="%s_f%d" % (tag, fmt))
-            r = plug.skeletons.render(spec, h)
-            with tempfile.TemporaryDirectory() as td:
-                src = os.path.join(td, r.filename)
-                with open(src, "w") as f:
-                    f.write(r.source)
-                obj = os.path.join(td, "k.o")
-                b = plug.toolchain.compile(src, obj, mode="device")
-                if not b.ok:
-                    raise RuntimeError("row %s does not compile:\n%s" % (tag, b.log[-3000:]))
-                isa = isa_summary(sum(parse_disasm(plug.toolchain.disasm(obj)).values(), []))
             key = tag if len(OPS[op]["fmts"]) == 1 else "%s/fmt%d" % (tag, fmt)
-            out[key] = dict(tag=tag, kind=kind, regs=b.regs, vgpr_spill=b.spill_st,
-                            sgpr_spill=b.spill_ld, scratch_bytes_per_lane=b.stack_frame,
-                            lds_static=b.smem_static, mfma=isa["mfma"], lds_dma=isa["lds_dma"],
-                            ds_read_b128=isa["ds_read_b128"], scratch_insts=isa["scratch"])
+            out[key] = row_numbers(plug, spec, h, kind, tag)
+    if gate:
+        bad = gate_build(out)
+        if bad:
+            raise RuntimeError("build gate failed for %s:\n  %s" % (op, "\n  ".join(bad)))
+    return out
+
+
+def card_passport(before, after):
+    """The manifest's card block from the measure stage's card states (card.snapshot() taken
+    before and after the run): the reference's passport keys (manifest.json:107-113) with the
+    clocks observed instead of locked."""
+    from tempo.plugins.gfx950 import card
+
+    before, after = before or {}, after or {}
+    out = card.passport(before, after, name=before.get("name", ""))
+    out["gcn_arch"] = before.get("gcn_arch")
+    out["clean"] = card.clean(before, after)
     return out
 
 
@@ -314,7 +377,7 @@ def make(op, rows_files=(), counter_files=()):
         if got.get("op") != op:
             continue
         man["rows"] = got["rows"]
-        man["card"] = {"before": got.get("card_before"), "after": got.get("card_after")}
+        man["card"] = card_passport(got.get("card_before"), got.get("card_after"))
         man["rows_source_md5"] = md5_of(op)
     fold_counters(man["rows"], counter_files, op)
     with open(path, "w") as f:

@@ -113,6 +113,13 @@ __device__ __forceinline__ f16x8 dequant8_u8(uint32_t w0, uint32_t w1, uint8_t z
   return dequant8(w0, w1, (_Float16)(1024.0f + (float)z), s);
 }
 
+// The lane index recomputed from the exec-mask bit count (mbcnt), for epilogues: a value derived
+// from threadIdx.x and kept across a register-full main loop gets spilled; this one is rebuilt
+// where it is needed.
+__device__ __forceinline__ int lane_id() {
+  return (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+}
+
 __device__ __forceinline__ f16x8 as_f16x8(const u32x4& u) { return __builtin_bit_cast(f16x8, u); }
 __device__ __forceinline__ u32x4 as_u32x4(const f16x8& h) { return __builtin_bit_cast(u32x4, h); }
 

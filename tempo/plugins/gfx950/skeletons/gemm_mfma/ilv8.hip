@@ -305,16 +305,21 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv8(
   }
 
   // ---- epilogue: C tile through LDS, as k_gemm_ilv ---------------------------------------------
+  // The lane and thread indices are rebuilt here (lane_id) rather than kept from the prologue:
+  // with 256 accumulators and the fragment buffers live, a value held across the loop spills.
   constexpr int RB = BN * 2, CPRW = RB / 16, RPP = NW * 64 / CPRW;
   static_assert(BM * BN * 2 <= STAGES * SBYTES && CPRW >= 16 && (CPRW & (CPRW - 1)) == 0, "C tile in LDS");
   const bool c16 = ((reinterpret_cast<uintptr_t>(C) | (uintptr_t)ldc * 2) & 15) == 0;
   __syncthreads();
+  const int elane = lane_id();
+  const int efr = elane % 16, efk = elane / 16;
+  const int etid = wave * 64 + elane;
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
-    const int r = wm * WTM + i * 16 + fr;
+    const int r = wm * WTM + i * 16 + efr;
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
-      const int cb = (wn * WTN + j * 16 + 4 * fk) * 2;
+      const int cb = (wn * WTN + j * 16 + 4 * efk) * 2;
       f16x4 o;
       o[0] = (_Float16)acc[i][j][0];
       o[1] = (_Float16)acc[i][j][1];
@@ -329,7 +334,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv8(
     constexpr int CPO = CPRW / 2, RPO = NW * 64 / CPO;
 #pragma unroll 4
     for (int p = 0; p < BM / RPO; ++p) {
-      const int r = p * RPO + tid / CPO, c = tid % CPO;
+      const int r = p * RPO + etid / CPO, c = etid % CPO;
       const f16x8 g = as_f16x8(*reinterpret_cast<const u32x4*>(smem + r * RB + ((c ^ (r & 15)) << 4)));
       const f16x8 u =
           as_f16x8(*reinterpret_cast<const u32x4*>(smem + r * RB + (((c + CPO) ^ (r & 15)) << 4)));
@@ -351,7 +356,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_ilv8(
   }
 #pragma unroll 4
   for (int p = 0; p < BM / RPP; ++p) {
-    const int r = p * RPP + tid / CPRW, c = tid % CPRW;
+    const int r = p * RPP + etid / CPRW, c = etid % CPRW;
     const u32x4 v = *reinterpret_cast<const u32x4*>(smem + r * RB + ((c ^ (r & 15)) << 4));
     if (m0 + r < M) {
       _Float16* dst = C + (long)(m0 + r) * ldc + n0 + c * 8;

@@ -63,15 +63,32 @@ def parse_resource_remarks(text: str) -> dict:
     return out
 
 
-def isa_summary(mnemonics: list) -> dict:
+def _is_lds_dma(mn: str, ops: str) -> bool:
+    """A global->LDS copy: the FLAT form global_load_lds_*, or a MUBUF load carrying the lds
+    modifier (buffer_load_dword* ... lds), which writes LDS instead of VGPRs."""
+    if mn.startswith("global_load_lds"):
+        return True
+    return mn.startswith("buffer_load") and re.search(r"(^|[\s,])lds($|\s)", ops) is not None
+
+
+def isa_summary(instrs: list) -> dict:
+    """Instruction mix of a disassembled kernel.  `instrs` holds mnemonics, or (mnemonic, operand
+    text) pairs (parse_disasm(..., operands=True)); the LDS-DMA and buffer-load counts need the
+    operands, since the MUBUF LDS copy differs from a register load only by its lds modifier."""
+    pairs = [(x, "") if isinstance(x, str) else (x[0], x[1]) for x in instrs]
+    dma = [_is_lds_dma(mn, ops) for mn, ops in pairs]
     return {
-        "mfma": sum(1 for x in mnemonics if x.startswith("v_mfma")),
-        "ds_read_b128": sum(1 for x in mnemonics if x in ("ds_read_b128", "ds_load_b128")),
-        "lds_dma": sum(1 for x in mnemonics if x.startswith("global_load_lds")),
-        "global_load_dwordx4": sum(1 for x in mnemonics if x == "global_load_dwordx4"),
-        "scratch": sum(1 for x in mnemonics if x.startswith("scratch_")),
-        "barrier": sum(1 for x in mnemonics if x == "s_barrier"),
-        "total": len(mnemonics),
+        "mfma": sum(1 for mn, _ in pairs if mn.startswith("v_mfma")),
+        "ds_read_b128": sum(1 for mn, _ in pairs if mn in ("ds_read_b128", "ds_load_b128")),
+        "lds_dma": sum(dma),
+        "lds_dma_buffer": sum(1 for (mn, _), d in zip(pairs, dma)
+                              if d and mn.startswith("buffer_load")),
+        "buffer_load": sum(1 for (mn, _), d in zip(pairs, dma)
+                           if not d and mn.startswith("buffer_load")),
+        "global_load_dwordx4": sum(1 for mn, _ in pairs if mn == "global_load_dwordx4"),
+        "scratch": sum(1 for mn, _ in pairs if mn.startswith("scratch_")),
+        "barrier": sum(1 for mn, _ in pairs if mn == "s_barrier"),
+        "total": len(pairs),
     }
 
 
@@ -117,7 +134,8 @@ class Gfx950Toolchain:
         lds = max((k.get("LDS Size [bytes/block]", 0) for k in res.values()), default=0)
         scratch_in_code = None
         if mode == "device":
-            scratch_in_code = isa_summary(sum(parse_disasm(self.disasm(out)).values(), []))["scratch"]
+            scratch_in_code = isa_summary(
+                sum(parse_disasm(self.disasm(out), operands=True).values(), []))["scratch"]
         return BuildResult(ok=True, binary=out, regs=int(vg + ag), spill_st=int(sp),
                            spill_ld=int(ssp), stack_frame=int(scr), smem_static=int(lds),
                            smem_dynamic=0, ldl_stl_in_loops=scratch_in_code, log=log)
