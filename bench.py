@@ -26,6 +26,23 @@ Extra fields of the one JSON line:
                 gemm_fp16 on the two C2 shapes, weights rotated through > 512 MiB so no launch
                 finds its weights in the 256 MiB Infinity Cache.
   fmha          the causal FMHA forward at configuration C5, TFLOP/s.
+  card          the card passport before and after the run (tempo/plugins/gfx950/card.py):
+                engine and memory clocks, socket power, temperature, clock lock, and the
+                processes seen on the card other than this one (the reference's
+                kernels/shipped/gemm_fp16/sm_70/manifest.json:107-113).
+  roofline.sclk_mhz / peak_at_sclk / frac_at_sclk
+                the engine clock the C1 kernel runs at -- GRBM_GUI_ACTIVE per dispatch over its
+                duration, from the committed counter summary (the clock follows the matrix
+                cores' load within microseconds, so only a counter read during the dispatch
+                gives it) -- and the matrix-core peak at that clock (256 CUs x 4096 flop/clk x
+                sclk), the reference's peak_tflops_1530 at its locked clock (manifest.json:119).
+  decode[].hbm_frac_measured
+                GB/s against the MEASURED pure-read HBM rate of the plugin's rate table
+                (HBM.READ_PURE, taken by tempo.plugins.gfx950.calibrate on a clean card), next
+                to hbm_frac against the 8 TB/s spec.
+  cpu_baseline.w8a16_arm
+                the W8A16 CPU path: the oracle's dequantisation followed by its fp32 GEMM, on a
+                row sample of the (34816, 5120) decode shape, both weight formats.
 """
 from __future__ import annotations
 
@@ -134,15 +151,26 @@ def settle_clocks(fn, stream, batch=20, tol=0.02, max_s=3.0, min_s=0.0):
 
 
 def cpu_model():
-    """The host CPU's model name (lscpu's field, read from /proc/cpuinfo)."""
+    """The host CPU as /proc/cpuinfo names it: model name, family / model / stepping, and the
+    vector extensions the oracle's code paths use."""
+    info = {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                if ":" not in line:
+                    if info:
+                        break  # the first processor's block is enough
+                    continue
+                k, v = (x.strip() for x in line.split(":", 1))
+                info.setdefault(k, v)
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    flags = set(info.get("flags", "").split())
+    ext = [f for f in ("avx2", "f16c", "fma", "avx512f", "avx512_bf16") if f in flags]
+    return "%s (family %s model %s stepping %s; %s; %d logical CPUs on the host, %d usable)" % (
+        info.get("model name", "unknown"), info.get("cpu family", "?"), info.get("model", "?"),
+        info.get("stepping", "?"), " ".join(ext), os.cpu_count() or 0,
+        len(os.sched_getaffinity(0)))
 
 
 def cpu_library_arm(A, B, threads, budget_s=5.0):
@@ -195,12 +223,94 @@ def cpu_baseline(A, B, budget_s=12.0):
         out["library_arm"] = cpu_library_arm(A, B, threads)
     except Exception as e:  # a missing BLAS is reported, not fatal
         out["library_arm"] = {"error": str(e)}
+    out["w8a16_arm"] = cpu_w8a16_arm(threads)
     return out
+
+
+def cpu_w8a16_arm(threads, budget_s=4.0):
+    """The W8A16 CPU path (dequantise, then the fp32 sequential-k GEMM: oracle_gemm_w8a16) on a
+    row sample of the (34816, 5120) decode shape, M = 16, both weight formats; reported as weight
+    bytes streamed per second (the decode metric's unit) and TFLOP/s."""
+    from oracle import oracle as O
+
+    g = np.random.Generator(np.random.PCG64(5))
+    K, M, G = 5120, 16, 128
+    A = randn_f16((M, K), 6, 1.0 / np.sqrt(K))
+    out = []
+    for fmt in (1, 2):
+        def make(n):
+            if fmt == 1:
+                q = g.integers(-127, 128, (n, K), dtype=np.int8)
+                sc = (g.uniform(0.5, 1.5, n) / 127).astype(np.float16)
+                return q, sc, None
+            q = g.integers(0, 256, (n, K), dtype=np.uint8)
+            sc = (g.uniform(0.5, 1.5, (n, K // G)) / 255).astype(np.float16)
+            z = g.integers(100, 157, (n, K // G), dtype=np.uint8)
+            return q, sc, z
+
+        q, sc, z = make(1024)
+        O.gemm_w8a16(A, q[:64], sc[:64], None if z is None else z[:64], G if fmt == 2 else 0,
+                     fmt, threads)  # thread pool and page warm-up, not timed
+        t = time.perf_counter()
+        O.gemm_w8a16(A, q, sc, z, G if fmt == 2 else 0, fmt, threads)
+        rate = 1024 / max(time.perf_counter() - t, 1e-6)
+        n = int(min(34816, max(512, budget_s * rate)))
+        n -= n % 64
+        q, sc, z = make(n)
+        t = time.perf_counter()
+        O.gemm_w8a16(A, q, sc, z, G if fmt == 2 else 0, fmt, threads)
+        dt = time.perf_counter() - t
+        wbytes = n * K + (2 * n if fmt == 1 else 3 * n * K // G)
+        out.append({"fmt": "sym_i8" if fmt == 1 else "asym_u8_g128", "M": M, "N": n, "K": K,
+                    "s": round(dt, 2), "GBps": round(wbytes / dt / 1e9, 3),
+                    "TFLOPs": round(2 * M * n * K / dt / 1e12, 5), "threads": threads,
+                    "kind": "port", "what": "oracle_gemm_w8a16: dequantise (fp16_rn((q-z)*s)) "
+                    "then fp32 sequential-k FMA per output"})
+    return out
+
+
+def measured_rate(kind):
+    """A MEASURED rate of the plugin's table (GB/s or TFLOP/s) with its card date, or None."""
+    try:
+        from tempo.plugins.gfx950.machine import Gfx950Machine
+
+        r = Gfx950Machine().peak(kind)
+    except Exception:
+        return None
+    if r.status != "MEASURED":
+        return None
+    return {"value": r.value, "units": r.units, "symbol": r.symbol,
+            "date": r.prov.card.date if r.prov and r.prov.card else None}
+
+
+def read_sclk():
+    """The engine clock the C1 kernel ran at, from the committed rocprofv3 --pmc summary
+    (GRBM_GUI_ACTIVE / 8 XCDs / the dispatch's duration, its C1 row's "sclk GHz" column), or
+    None.  The clock follows the matrix cores' load within microseconds -- a probe kernel queued
+    right after a C1 launch already reads ~2.4 GHz, and amd-smi's per-XCD clock is not sampled
+    fast enough -- so only a counter read during the dispatch itself gives it."""
+    if not os.path.exists(TRAFFIC_FILE):
+        return None
+    with open(TRAFFIC_FILE, encoding="utf-8") as f:
+        for line in f:
+            c = [x.strip() for x in line.split("|")]
+            if len(c) > 13 and c[1:5] == [str(C1["M"]), str(C1["N"]), str(C1["K"]), "0"]:
+                try:
+                    ghz = float(c[12])
+                except ValueError:
+                    return None
+                return {"median_mhz": round(ghz * 1e3, 1),
+                        "source": "profiles/counters_gemm_fp16_configs.md (C1 row): "
+                                  "GRBM_GUI_ACTIVE / 8 XCDs / dispatch duration under "
+                                  "rocprofv3 --pmc"}
+    return None
 
 
 def decode_lines(steps):
     import torch
     from cuda_tempiler_amd import capi
+
+    hbm = measured_rate("hbm_read_pure")
 
     out = []
     stream = torch.cuda.current_stream()
@@ -237,6 +347,7 @@ def decode_lines(steps):
                 out.append({"op": "gemm_w8a16", "fmt": "sym_i8" if fmt == 1 else "asym_u8_g128",
                             "M": M, "N": N, "K": K, "us": round(ms * 1e3, 2),
                             "GBps": round(gbps, 1), "hbm_frac": round(gbps / PEAK_HBM_GBPS, 4),
+                            "hbm_frac_measured": round(gbps / hbm["value"], 4) if hbm else None,
                             "route": capi.route(1 if fmt == 1 else 2, M, N, K)})
             del W, S, Z
     # fp16 decode (C2 shapes)
@@ -254,8 +365,12 @@ def decode_lines(steps):
             gbps = byts / (ms * 1e-3) / 1e9
             out.append({"op": "gemm_fp16", "M": M, "N": N, "K": K, "us": round(ms * 1e3, 2),
                         "GBps": round(gbps, 1), "hbm_frac": round(gbps / PEAK_HBM_GBPS, 4),
+                        "hbm_frac_measured": round(gbps / hbm["value"], 4) if hbm else None,
                         "route": capi.route(0, M, N, K)})
         del Bs
+    if hbm:
+        out.append({"hbm_measured": hbm, "mode": "HBM.READ_PURE: nontemporal 16-byte loads, "
+                    "4 GiB buffer (tempo.plugins.gfx950.calibrate)"})
     return out
 
 
@@ -394,6 +509,9 @@ def main():
               "Run with --gpus 1.", file=sys.stderr)
         return 2
 
+    from tempo.plugins.gfx950 import card
+
+    card_before = card.wait_idle(0)  # before this process touches the GPU
     import torch
     from cuda_tempiler_amd import capi
 
@@ -422,6 +540,8 @@ def main():
     flops = 2 * M * N * K
     tflops = flops / (ms * 1e-3) / 1e12
     traffic = read_traffic()
+    sclk = read_sclk()
+    peak_sclk = 256 * 4096 * sclk["median_mhz"] * 1e6 / 1e12 if sclk else None
     line = {
         "metric": METRIC, "value": round(tflops, 1), "unit": "TFLOP/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "settle": settle,
@@ -434,7 +554,10 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": PEAK_FP16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / PEAK_FP16_TFLOPS, 4),
                      "traffic": traffic,
-                     "algorithmic_bytes": 2 * (M * K + N * K + M * N)},
+                     "algorithmic_bytes": 2 * (M * K + N * K + M * N),
+                     "sclk_mhz": sclk, "peak_at_sclk": round(peak_sclk, 1) if sclk else None,
+                     "frac_at_sclk": round(tflops / peak_sclk, 4) if sclk else None,
+                     "mfma_measured": measured_rate("tensor_measured")},
     }
     del C
     if args.copy_calibration:
@@ -454,6 +577,10 @@ def main():
         line["gptq_repack"] = gptq_lines(max(20, args.steps // 4))
         torch.cuda.empty_cache()
         line["gate_up"] = gate_up_lines(max(50, args.steps // 2))
+    torch.cuda.synchronize()
+    card_after = card.snapshot(0)
+    line["card"] = {"before": card_before, "after": card_after,
+                    "clean": card.clean(card_before, card_after)}
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(Ah, Bh)
     else:

@@ -136,11 +136,27 @@ def build_probes(ex) -> list:
     return out
 
 
+# The measure stage's machine calibration probes (tempo/plugins/gfx950/calibrate.py): a library of
+# their own, outside the product path.
+CALIB_SRC = os.path.join(ROOT, "tempo", "plugins", "gfx950", "calib", "calib.hip")
+CALIB_OUT = os.path.join(ROOT, "tempo", "plugins", "gfx950", "calib", "libgfx950_calib.so")
+
+
+def build_calib() -> str:
+    cmd = [HIPCC] + FLAGS + ["-shared", "-o", CALIB_OUT + ".tmp", CALIB_SRC]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("hipcc failed on %s:\n%s" % (CALIB_SRC, r.stderr[-4000:]))
+    os.replace(CALIB_OUT + ".tmp", CALIB_OUT)
+    return CALIB_OUT
+
+
 def build(verbose: bool = False, probes: bool = True) -> str:
     os.makedirs(BUILD, exist_ok=True)
     regenerate()
     with cf.ThreadPoolExecutor(max_workers=8) as ex:
         fut_probes = ex.submit(build_probes, ex) if probes else None
+        fut_calib = ex.submit(build_calib)
         objs = list(ex.map(_compile, UNITS))
         cmd = [HIPCC, "--offload-arch=%s" % ARCH, "-shared", "-fPIC", "-o", OUT + ".tmp"] + objs
         r = subprocess.run(cmd, capture_output=True, text=True)
@@ -149,6 +165,7 @@ def build(verbose: bool = False, probes: bool = True) -> str:
         os.replace(OUT + ".tmp", OUT)
         if fut_probes is not None:
             fut_probes.result()
+        fut_calib.result()
     if verbose:
         print(OUT)
     return OUT

@@ -45,9 +45,10 @@ class Gfx950Plugin:
 
     def declared_stubs(self):
         return (
-            "HBM.STREAM_READ is NOT_MEASURED in the rate table until a clean-card run records it "
-            "with its CardState; the bound's HBM channel uses each CU's share of the spec peak "
-            "(CAP.HBM_SHARE), so it is loose for decode",
+            "the bound's HBM channel uses each CU's share of the spec peak (CAP.HBM_SHARE, an "
+            "upper bound); the MEASURED modes (HBM.READ_PURE / READ / COPY) are reported next "
+            "to it, not used inside it, because a measured streaming rate is not an upper bound "
+            "on what a kernel may reach",
             "clock locking (Meters.clock_lock) is not offered: clocks are recorded, not set",
             "classifier.control_fields: the AMD ISA has no scheduling control words",
             "FMHA is a fixed skeleton (skeletons/fmha_fwd), outside the searched space",
@@ -63,6 +64,28 @@ class Gfx950Plugin:
         bad = [s.symbol for s in syms.values() if s.status == "MEASURED" and
                (s.prov is None or s.prov.card is None or s.prov.card.foreign_procs != 0)]
         r.check("every MEASURED rate carries a clean card", not bad, ", ".join(bad[:3]))
+        # bandwidth as three named modes, not one number (reference sm70/__init__.py:110-131)
+        modes = ("hbm_read_pure", "hbm_read", "hbm_copy")
+        rates = [M.peak(k) for k in modes]
+        r.check("HBM bandwidth is declared as three MEASURED modes",
+                all(x.status == "MEASURED" for x in rates),
+                ", ".join("%s %s" % (x.symbol, x.status) for x in rates))
+        vals = [x.value for x in rates]
+        r.check("the three modes differ (else the symbols are redundant)", len(set(vals)) == 3,
+                "%s" % vals)
+        r.check("every mode names its access pattern", all("MODE:" in x.note for x in rates))
+        r.check("the spec HBM peak is declared and differs from every mode",
+                M.peak("hbm_spec").status == "SPEC" and M.peak("hbm_spec").value not in vals)
+        # a measured rate above the declared ceiling of the same resource falsifies the ceiling
+        lds = M.rate("LDS.READ")
+        r.check("measured LDS rate within its UPPER_BOUND",
+                lds.value <= M.rate("CAP.LDS").value,
+                "%.1f vs %.1f B/clk/CU" % (lds.value, M.rate("CAP.LDS").value))
+        mf = M.rate("MFMA.F16")
+        sclk = M.rate("CLOCK.SCLK_MFMA_PROBE").value
+        cap_tf = M.rate("GEOM.SMS").value * sclk * 1e6 * M.rate("CAP.MFMA_F16").value / 1e12
+        r.check("measured MFMA rate within the issue ceiling at its own clock",
+                mf.value <= cap_tf, "%.1f vs %.1f TFLOP/s at %d MHz" % (mf.value, cap_tf, sclk))
         try:
             M.rate("CAP.NONEXISTENT")
             r.check("closed table refuses an unknown symbol", False)

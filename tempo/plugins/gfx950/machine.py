@@ -16,7 +16,7 @@ import json
 import os
 from typing import Mapping
 
-from ..base import Channel, Rate, closed_table_get, not_measured, rate
+from ..base import CardState, Channel, Provenance, Rate, closed_table_get, not_measured, rate
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 _TABLE = None
@@ -32,9 +32,22 @@ def _load_table() -> Mapping[str, Rate]:
             if r["status"] == "NOT_MEASURED" or r["value"] is None:
                 t[sym] = not_measured(sym, r["units"], r.get("note", ""))
             else:
-                t[sym] = rate(sym, r["value"], r["units"], r["status"], r.get("note", ""))
+                t[sym] = rate(sym, r["value"], r["units"], r["status"], r.get("note", ""),
+                              prov=_prov(r.get("prov")))
         _TABLE = t
     return _TABLE
+
+
+def _prov(p):
+    """Provenance of a rate as the table stores it (calibrate.py writes it for MEASURED rates)."""
+    if not p:
+        return None
+    c = p.get("card")
+    cs = None if c is None else CardState(index=int(c["index"]), clock_mhz=int(c["clock_mhz"]),
+                                          foreign_procs=c["foreign_procs"], date=str(c["date"]))
+    return Provenance(tool=p["tool"], counter=p.get("counter"), version=str(p["version"]),
+                      date=str(p["date"]), who=p["who"], observability=p["observability"],
+                      card=cs)
 
 
 class Gfx950Machine:
@@ -92,7 +105,10 @@ class Gfx950Machine:
             "tensor_dense": "PEAK.TENSOR_FP16_DENSE",
             "tensor_fp8_dense": "PEAK.TENSOR_FP8_DENSE",
             "hbm_spec": "PEAK.HBM",
-            "hbm_read": "HBM.STREAM_READ",
+            "hbm_read_pure": "HBM.READ_PURE",
+            "hbm_read": "HBM.READ",
+            "hbm_copy": "HBM.COPY",
+            "tensor_measured": "MFMA.F16",
             "l2": "CAP.VMEM_L2",
         }
         if kind not in table:

@@ -84,6 +84,13 @@ def _rel_l2(got, ref):
     return float(torch.sqrt(torch.sum((g - r) ** 2) / den).item()) if den > 0 else 0.0
 
 
+ONLY = []  # --only: restrict the configuration shapes to these (M, N, K[, fmt]) tuples
+
+
+def _only_ok(case) -> bool:
+    return not ONLY or any(tuple(case[:len(o)]) == o for o in ONLY)
+
+
 def cases_of(op: str, quick: bool = False):
     if op == "gemm_fp16":
         cases = [(M, N, K, 0) for (M, N, K) in SHAPES_FP16]
@@ -91,7 +98,8 @@ def cases_of(op: str, quick: bool = False):
         cases = [(M, N, K, f) for f in (1, 2) for (M, N, K) in SHAPES_W8]
     else:  # fmha: configuration C5 (B, H, Hkv, S, D) carried as (S, H, D, Hkv)
         cases = [(4096, 16, 256, 8)]
-    return cases[::4] if quick else cases
+    cases = cases[::4] if quick else cases
+    return [c for c in cases if _only_ok(c)]
 
 
 def label_of(M, N, K, fmt):
@@ -198,6 +206,8 @@ def counters(op: str, out: str, groups, quick: bool = False) -> str:
         os.makedirs(d, exist_ok=True)
         argv = [sys.executable, "-m", "tempo.plugins.gfx950.measure_shipped", op,
                 "--counter-pass", seg] + (["--quick"] if quick else [])
+        if ONLY:
+            argv += ["--only"] + [",".join(str(x) for x in o) for o in ONLY]
         _say("counter group %s: %s" % (g, " ".join(GROUPS[g])))
         disp = meters.run_pass(argv, GROUPS[g], d)
         with open(seg) as f:
@@ -393,9 +403,11 @@ def measure(op: str, quick: bool = False):
 
 
 def card_state():
-    import subprocess
+    """The card passport (card.snapshot: clocks, power, foreign processes) plus the device's
+    name, architecture and CU count as torch reports them."""
+    from tempo.plugins.gfx950 import card
 
-    out = {"time": time.strftime("%Y-%m-%dT%H:%M:%S")}
+    out = card.snapshot(0)
     try:
         import torch
 
@@ -405,14 +417,6 @@ def card_state():
         out["cus"] = p.multi_processor_count
     except Exception as e:  # recorded, not fatal
         out["name_error"] = str(e)
-    for cmd in (["amd-smi", "metric", "--clock", "--json"], ["rocm-smi", "--showclocks", "--json"]):
-        try:
-            r = subprocess.run(cmd, capture_output=True, text=True, timeout=30)
-            if r.returncode == 0:
-                out[cmd[0]] = r.stdout[-4000:]
-                break
-        except Exception:
-            continue
     return out
 
 
@@ -427,9 +431,12 @@ def main():
     ap.add_argument("--groups", nargs="*", default=["hbm_read", "hbm_write", "mfma"])
     ap.add_argument("--counter-pass", metavar="SEGFILE",
                     help="(internal) the program a counter pass profiles")
+    ap.add_argument("--only", nargs="*", default=[], metavar="M,N,K[,fmt]",
+                    help="restrict the configuration shapes to these")
     ap.add_argument("--render", metavar="COUNTERS_JSON",
                     help="print a counter step's JSON as a markdown table (no GPU)")
     a = ap.parse_args()
+    ONLY[:] = [tuple(int(x) for x in o.split(",")) for o in a.only]
     if a.render:
         sys.stdout.write(render_counters(a.render))
         return 0
