@@ -84,6 +84,7 @@ W8 = {
         ("l0r1n2d2", 1, 5120, 6144),
         ("l0r1d2", 1, 1024, 5120),
         ("l0r1d4", 1, 7168, 5120),
+        ("l0r1d2w", 1, 34816, 5120),      # the C3/C4 decode point M = 1, N = 34816
         ("l1r1n4d2t", 16, 34816, 5120),
         ("l1r1n4d2t", 16, 16400, 256),    # one remaining slab
         ("l1r1n4d2t", 9, 16384, 384),     # whole rounds, no tail
@@ -139,6 +140,7 @@ W8 = {
         ("l0r1n2d2", 1, 5120, 5120),
         ("l0r1d2", 1, 1024, 5120),
         ("l0r1d4", 1, 7168, 5120),
+        ("l0r1d2w", 1, 34816, 5120),      # the C3/C4 decode point M = 1, N = 34816
         ("l1r1n4d2t", 16, 34816, 5120),
         ("l1r1n4d2t", 16, 16400, 256),    # one remaining slab
         ("l1r1n4d2t", 9, 16384, 384),     # whole rounds, no tail
