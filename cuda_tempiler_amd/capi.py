@@ -76,7 +76,10 @@ EXPORTS = {
     "tempo_gemm_fp16_workspace_bytes": ([ct.POINTER(TempoGemmParams)], ct.c_size_t),
     "tempo_gemm_w8a16_workspace_bytes": ([ct.POINTER(TempoW8A16Params)], ct.c_size_t),
     "tempo_gemm_w8a16_launch_noalloc": ([ct.POINTER(TempoW8A16Params), _p], _i),
+    "tempo_gemm_fp16_launch_ws": ([ct.POINTER(TempoGemmParams), _p, ct.c_size_t, _p], _i),
+    "tempo_gemm_w8a16_launch_ws": ([ct.POINTER(TempoW8A16Params), _p, ct.c_size_t, _p], _i),
 }
+HIP_ERROR_CAPTURE_UNSUPPORTED = 900  # hipErrorStreamCaptureUnsupported: the pool cannot grow
 NOALLOC_SCRATCH_BYTES = 32 << 20
 
 
@@ -138,8 +141,42 @@ def _ptr(t):
     return _p(t.data_ptr()) if t is not None else None
 
 
-def gemm_fp16(A, B, C=None, stream=None):
-    """C[M,N] = A[M,K] . B[N,K]^T on the shipped gfx950 ladder.  Raises NotCovered."""
+def _require_out(C, M, N, A, what):
+    """C must be fp16 [M, N] with unit inner stride on A's device: the kernels write it as raw
+    memory of that layout."""
+    import torch
+
+    if C.dtype != torch.float16 or C.dim() != 2 or tuple(C.shape) != (M, N) \
+            or C.stride(1) != 1 or C.device != A.device:
+        raise ValueError("%s: C must be fp16 [%d, %d] with unit inner stride on %s, got %s %s "
+                         "strides %s on %s" % (what, M, N, A.device, C.dtype, tuple(C.shape),
+                                               tuple(C.stride()), C.device))
+
+
+def _launch(name, name_ws, p, need_fn, workspace, device, stream):
+    """Run a GEMM entry point.  workspace=None: the library's pool (tempo_*_launch); "torch": a
+    workspace from torch's caching allocator when the row needs one (graph-capture safe: under
+    capture torch hands out memory of the graph's pool); a tensor: that device memory."""
+    L = lib()
+    if workspace is None:
+        _check(getattr(L, name)(p, _stream(stream)), name)
+        return
+    if isinstance(workspace, str):
+        if workspace != "torch":
+            raise ValueError("workspace must be None, 'torch' or a device tensor")
+        import torch
+
+        need = int(need_fn(p))
+        buf = torch.empty(need, dtype=torch.uint8, device=device) if need else None
+    else:
+        buf = workspace
+    nbytes = 0 if buf is None else buf.numel() * buf.element_size()
+    _check(getattr(L, name_ws)(p, _ptr(buf), nbytes, _stream(stream)), name_ws)
+
+
+def gemm_fp16(A, B, C=None, stream=None, workspace=None):
+    """C[M,N] = A[M,K] . B[N,K]^T on the shipped gfx950 ladder.  Raises NotCovered.  `workspace`
+    as for _launch (None = the library's pool)."""
     import torch
 
     M, K = A.shape
@@ -147,8 +184,8 @@ def gemm_fp16(A, B, C=None, stream=None):
     if C is None:
         C = torch.empty((M, N), dtype=torch.float16, device=A.device)
     p = TempoGemmParams(_ptr(A), _ptr(B), _ptr(C), M, N, K, A.stride(0), B.stride(0), C.stride(0))
-    _check(lib().tempo_gemm_fp16_launch(p, _stream(stream)),
-           "tempo_gemm_fp16_launch")
+    _launch("tempo_gemm_fp16_launch", "tempo_gemm_fp16_launch_ws", p,
+            lib().tempo_gemm_fp16_workspace_bytes, workspace, A.device, stream)
     return C
 
 
@@ -176,6 +213,7 @@ def gemm_w8a16_gate_up(A, Wq, scale, zero=None, fmt: int = W8_SYM_I8, group: int
     _require_w8(A, Wq, scale, zero, fmt, group)
     if C is None:
         C = torch.empty((M, N), dtype=torch.float16, device=A.device)
+    _require_out(C, M, N, A, "gemm_w8a16_gate_up")
     p = w8a16_params(A, Wq, scale, zero, C, fmt, group)
     p.N = N
     _check(lib().tempo_gemm_w8a16_gate_up_launch(p, _stream(stream)),
@@ -241,7 +279,8 @@ def w8a16_params(A, Wq, scale, zero, C, fmt: int, group: int = 128) -> TempoW8A1
 
 
 def gemm_w8a16(A, Wq, scale, zero=None, fmt: int = W8_SYM_I8, group: int = 128, C=None,
-               stream=None):
+               stream=None, workspace=None):
+    """C[M,N] = A . deq(Wq)^T on the shipped ladder; `workspace` as for gemm_fp16."""
     import torch
 
     M = A.shape[0]
@@ -249,8 +288,10 @@ def gemm_w8a16(A, Wq, scale, zero=None, fmt: int = W8_SYM_I8, group: int = 128, 
     _require_w8(A, Wq, scale, zero, fmt, group)
     if C is None:
         C = torch.empty((M, N), dtype=torch.float16, device=A.device)
+    _require_out(C, M, N, A, "gemm_w8a16")
     p = w8a16_params(A, Wq, scale, zero, C, fmt, group)
-    _check(lib().tempo_gemm_w8a16_launch(p, _stream(stream)), "tempo_gemm_w8a16_launch")
+    _launch("tempo_gemm_w8a16_launch", "tempo_gemm_w8a16_launch_ws", p,
+            lib().tempo_gemm_w8a16_workspace_bytes, workspace, A.device, stream)
     return C
 
 
@@ -261,6 +302,7 @@ def gemm_w8a16_noalloc(A, Wq, scale, zero=None, fmt: int = W8_SYM_I8, group: int
     if C is None:
         raise ValueError("gemm_w8a16_noalloc writes into a caller-provided C")
     _require_w8(A, Wq, scale, zero, fmt, group)
+    _require_out(C, A.shape[0], Wq.shape[0], A, "gemm_w8a16_noalloc")
     p = w8a16_params(A, Wq, scale, zero, C, fmt, group)
     _check(lib().tempo_gemm_w8a16_launch_noalloc(p, _stream(stream)),
            "tempo_gemm_w8a16_launch_noalloc")

@@ -128,6 +128,16 @@ int tempo_gemm_fp16_launch(const TempoGemmParams* p, tempo_stream_t stream) {
   return (int)tempo::gen::launch(to_pod(p), static_cast<hipStream_t>(stream));
 }
 
+int tempo_gemm_fp16_launch_ws(const TempoGemmParams* p, void* ws, size_t ws_bytes,
+                              tempo_stream_t stream) {
+  if (!p) return (int)hipErrorInvalidValue;
+  tempo::gen::Workspace w;
+  w.ptr = ws;
+  w.bytes = ws ? ws_bytes : 0;
+  w.pool = false;
+  return (int)tempo::gen::launch_with(to_pod(p), static_cast<hipStream_t>(stream), w);
+}
+
 size_t tempo_gemm_fp16_workspace_bytes(const TempoGemmParams* p) {
   if (!p) return 0;
   return tempo::gen::workspace_bytes(to_pod(p));
@@ -146,6 +156,16 @@ int tempo_gemm_w8a16_applicable(const TempoW8A16Params* p) {
 int tempo_gemm_w8a16_launch(const TempoW8A16Params* p, tempo_stream_t stream) {
   if (!p) return (int)hipErrorInvalidValue;
   return (int)tempo::gen8::launch(to_pod(p), static_cast<hipStream_t>(stream));
+}
+
+int tempo_gemm_w8a16_launch_ws(const TempoW8A16Params* p, void* ws, size_t ws_bytes,
+                               tempo_stream_t stream) {
+  if (!p) return (int)hipErrorInvalidValue;
+  tempo::gen8::Workspace w;
+  w.ptr = ws;
+  w.bytes = ws ? ws_bytes : 0;
+  w.pool = false;
+  return (int)tempo::gen8::launch_with(to_pod(p), static_cast<hipStream_t>(stream), w);
 }
 
 int tempo_gemm_w8a16_launch_noalloc(const TempoW8A16Params* p, tempo_stream_t stream) {

@@ -89,7 +89,9 @@ def _linear_fp16_impl(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     tag = capi.route(0, M, N, K)
     y = torch.empty((M, N), dtype=torch.float16, device=x.device)
     try:
-        capi.gemm_fp16(x2, w, y)
+        # the split-K workspace comes from torch's caching allocator (graph-capture safe), not
+        # from the library's pool
+        capi.gemm_fp16(x2, w, y, workspace="torch")
     except capi.NotCovered:
         _count("fallback")
         return F.linear(x, w)
@@ -135,7 +137,19 @@ def _w8_covered(x, wq, scale, zero, fmt, group) -> bool:
                                     zero, fmt, group) is None
 
 
+def _packed_meta(scale, zero):
+    """Scale and zero-points as the kernels read them: packed rows.  A strided view (a column
+    slice of a larger table, say) is copied once here rather than sent to the caller's path."""
+    if scale is not None and not scale.is_contiguous():
+        scale = scale.contiguous()
+    if zero is not None and not zero.is_contiguous():
+        zero = zero.contiguous()
+    return scale, zero
+
+
 def _linear_w8a16_impl(x, wq, scale, zero, fmt, group):
+    scale, zero = _packed_meta(scale, zero)
+
     def own_path():
         return F.linear(x, dequantize(wq, scale, zero, fmt, group).to(x.device))
 
@@ -151,7 +165,7 @@ def _linear_w8a16_impl(x, wq, scale, zero, fmt, group):
     tag = capi.route(fmt, M, N, K)
     y = torch.empty((M, N), dtype=torch.float16, device=x.device)
     try:
-        capi.gemm_w8a16(x2, wq, scale, zero, fmt=fmt, group=group, C=y)
+        capi.gemm_w8a16(x2, wq, scale, zero, fmt=fmt, group=group, C=y, workspace="torch")
     except capi.NotCovered:
         _count("fallback")
         return own_path()
@@ -224,6 +238,7 @@ def linear_gate_up_w8a16(x: torch.Tensor, wq: torch.Tensor, scale: torch.Tensor,
                          zero: Optional[torch.Tensor], fmt: int, group: int) -> torch.Tensor:
     """The fused gate/up projection on 8-bit weights wq [2N, K] (scale / zero rows follow)."""
     N, K = wq.shape[0] // 2, wq.shape[1]
+    scale, zero = _packed_meta(scale, zero)
 
     def own_path():
         return _silu_mul_own(F.linear(x, dequantize(wq, scale, zero, fmt, group).to(x.device)))

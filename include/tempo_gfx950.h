@@ -53,8 +53,22 @@ typedef struct TempoGemmParams {
 /* 1 = covered (launch will run a kernel), 0 = not covered (caller takes its own path).
  * Reference: launch.cuh:59-67 applicable() plus the ladder coverage of dispatch.inc. */
 int tempo_gemm_fp16_applicable(const TempoGemmParams* p);
-/* Reference: launch.cu:20-22 tempo::gen::launch(const GemmParams&, cudaStream_t). */
+/* Reference: launch.cu:20-22 tempo::gen::launch(const GemmParams&, cudaStream_t).  A split-K
+ * row takes its fp32 partial sums from the library's pool: one device buffer per (device,
+ * stream), allocated on first use and grown with hipMalloc when a larger shape needs it (a
+ * grown-out buffer is kept, not freed, until the process ends, so work already queued or a graph
+ * captured earlier never sees it freed).  On a stream under graph capture the pool cannot grow:
+ * such a call returns hipErrorStreamCaptureUnsupported (900) and launches nothing; use
+ * tempo_gemm_fp16_launch_ws there. */
 int tempo_gemm_fp16_launch(const TempoGemmParams* p, tempo_stream_t stream);
+/* tempo_gemm_fp16_launch with the caller's workspace (ws, ws_bytes device memory; may be NULL /
+ * 0 for shapes whose row needs none): never allocates, never synchronises.  A row needing more
+ * than ws_bytes (tempo_gemm_fp16_workspace_bytes) returns hipErrorOutOfMemory (2) without
+ * launching.  No reference counterpart (its launcher has no workspace, launch.cuh:20-26): this
+ * is for callers whose own allocator must own every buffer -- a framework capturing HIP graphs
+ * (torch's graph-aware caching allocator), arenas of a serving loop. */
+int tempo_gemm_fp16_launch_ws(const TempoGemmParams* p, void* ws, size_t ws_bytes,
+                              tempo_stream_t stream);
 /* Bytes of workspace the row tempo_gemm_fp16_launch runs for this shape needs (0: none, or not
  * covered).  Host-only.  No reference counterpart: the reference's ladder has no split-K row
  * (kernels/shipped/gemm_fp16/sm_70/dispatch.inc:15-26). */
@@ -87,7 +101,12 @@ typedef struct TempoW8A16Params {
 } TempoW8A16Params;
 
 int tempo_gemm_w8a16_applicable(const TempoW8A16Params* p);
+/* Split-K rows take the library's pool, as tempo_gemm_fp16_launch does (same growth, retirement
+ * and graph-capture rule). */
 int tempo_gemm_w8a16_launch(const TempoW8A16Params* p, tempo_stream_t stream);
+/* tempo_gemm_w8a16_launch with the caller's workspace, as tempo_gemm_fp16_launch_ws. */
+int tempo_gemm_w8a16_launch_ws(const TempoW8A16Params* p, void* ws, size_t ws_bytes,
+                               tempo_stream_t stream);
 /* Bytes of workspace the row tempo_gemm_w8a16_launch runs for this shape needs (0: none, or not
  * covered).  Host-only; no reference counterpart (as for tempo_gemm_fp16_workspace_bytes). */
 size_t tempo_gemm_w8a16_workspace_bytes(const TempoW8A16Params* p);

@@ -26,8 +26,9 @@ hipError_t launch_ilv(const GemmParams& p, hipStream_t s, const Workspace& w) {
                        p.ldc, static_cast<float*>(nullptr), 1, p.N);
     return hipGetLastError();
   }
-  float* ws = workspace_for(w, bytes, s);
-  if (!ws) return hipErrorOutOfMemory;
+  hipError_t werr = hipSuccess;
+  float* ws = workspace_for(w, bytes, s, &werr);
+  if (!ws) return werr;
   hipLaunchKernelGGL((k_gemm_ilv<BM, BN, BK, WM, WN, STAGES, GROUP, XCD, RSP, 1>),
                      dim3(nm * nn * splits), blk, 0, s, p.A, p.B, p.C, p.M, p.N, p.K, p.lda, p.ldb,
                      p.ldc, ws, splits, p.N);

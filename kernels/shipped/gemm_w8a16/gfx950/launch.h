@@ -248,8 +248,9 @@ inline hipError_t launch_line_fmt(const W8A16Params& p, hipStream_t s, const Wor
     return hipSuccess;
   }
   if (a.ks > 1) {
-    a.part = workspace_for(*w, bytes, s);
-    if (!a.part) return hipErrorOutOfMemory;
+    hipError_t werr = hipSuccess;
+    a.part = workspace_for(*w, bytes, s, &werr);
+    if (!a.part) return werr;
   }
   hipLaunchKernelGGL((k_stream_line<MB, R, D, BFMT, EPI, SN, TPB, TL>), dim3(wgs * a.ks),
                      dim3(64 * SN * a.S), lds, s, a, G);

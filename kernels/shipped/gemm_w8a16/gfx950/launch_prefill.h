@@ -34,8 +34,9 @@ hipError_t launch_ilv8(const W8A16Params& p, hipStream_t s, const Workspace& w) 
       run_ilv8<BM, BN, BK, WM, WN, STAGES, GROUP, XCD, RSP, 2, 0>(p, s, dim3(nm * nn), nullptr, 1);
     return hipGetLastError();
   }
-  float* ws = workspace_for(w, bytes, s);
-  if (!ws) return hipErrorOutOfMemory;
+  hipError_t werr = hipSuccess;
+  float* ws = workspace_for(w, bytes, s, &werr);
+  if (!ws) return werr;
   const dim3 grid(nm * nn * splits);
   if (p.fmt == 1)
     run_ilv8<BM, BN, BK, WM, WN, STAGES, GROUP, XCD, RSP, 1, 1>(p, s, grid, ws, splits);

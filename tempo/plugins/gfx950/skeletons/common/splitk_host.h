@@ -6,7 +6,7 @@
 // them with k_splitk_reduce on the same stream.  The workspace is either memory the caller hands
 // over, or the delivery's pool: one buffer per (device, stream), allocated on first use and grown
 // when a larger shape needs it, so calls on different streams stay independent and calls on one
-// stream are ordered by it.  (The frozen file's preamble includes <map>, <mutex> and <utility>.)
+// stream are ordered by it.
 
 // Workspace of a split-K row.  `ptr`/`bytes`: device memory the caller hands over (may be
 // null / 0); `pool`: the row may take the delivery's per-(device, stream) pool instead; `need`:
@@ -19,31 +19,48 @@ struct Workspace {
   size_t* need = nullptr;
 };
 
-// The pool: one buffer per (device, stream), grown on demand.  Work already queued on the stream
-// may still read the old buffer, so it is freed only after the stream has drained.
-inline void* pool_buffer(hipStream_t s, size_t bytes) {
+// The pool: one buffer per (device, stream), grown on demand.  A buffer that a larger shape
+// outgrows is retired, not freed: work already queued on the stream, a graph captured earlier
+// or another thread that took the pointer a moment ago may still use it, so it stays allocated
+// until the process ends (at most one retired buffer per growth step, each smaller than its
+// successor).  Growing needs hipMalloc, which a stream under graph capture cannot take: there
+// the pool returns hipErrorStreamCaptureUnsupported and the caller hands over its workspace
+// instead (launch_with, or the C ABI's *_launch_ws entry points).  (The frozen file's preamble
+// includes <map>, <mutex>, <utility> and <vector>.)
+inline void* pool_buffer(hipStream_t s, size_t bytes, hipError_t* err) {
   static std::mutex mu;
   static std::map<std::pair<int, hipStream_t>, std::pair<void*, size_t>> pool;
+  static std::vector<void*> retired;
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+  if ((*err = hipGetDevice(&dev)) != hipSuccess) return nullptr;
   std::lock_guard<std::mutex> lock(mu);
   std::pair<void*, size_t>& e = pool[std::make_pair(dev, s)];
   if (e.second < bytes) {
-    if (e.first) {
-      if (hipStreamSynchronize(s) != hipSuccess) return nullptr;
-      (void)hipFree(e.first);
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if ((*err = hipStreamIsCapturing(s, &cs)) != hipSuccess) return nullptr;
+    if (cs != hipStreamCaptureStatusNone) {
+      *err = hipErrorStreamCaptureUnsupported;
+      return nullptr;
     }
-    e = std::make_pair(nullptr, (size_t)0);
     void* q = nullptr;
-    if (hipMalloc(&q, bytes) != hipSuccess) return nullptr;
+    if (hipMalloc(&q, bytes) != hipSuccess) {
+      *err = hipErrorOutOfMemory;
+      return nullptr;
+    }
+    if (e.first) retired.push_back(e.first);
     e = std::make_pair(q, bytes);
   }
   return e.first;
 }
 
-inline float* workspace_for(const Workspace& w, size_t bytes, hipStream_t s) {
+// The workspace of a split-K launch: the caller's if it is large enough, else the pool's when the
+// row may take it.  nullptr with *err set otherwise (hipErrorOutOfMemory: the caller's buffer is
+// too small and no pool was allowed).
+inline float* workspace_for(const Workspace& w, size_t bytes, hipStream_t s, hipError_t* err) {
+  *err = hipSuccess;
   if (w.ptr && w.bytes >= bytes) return static_cast<float*>(w.ptr);
-  if (w.pool) return static_cast<float*>(pool_buffer(s, bytes));
+  if (w.pool) return static_cast<float*>(pool_buffer(s, bytes, err));
+  *err = hipErrorOutOfMemory;
   return nullptr;
 }
 

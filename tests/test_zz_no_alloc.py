@@ -33,11 +33,14 @@ def test_noalloc_matches_the_allocating_entry_point(gpu, fmt):
 
     # first a split-K shape with a large workspace, then a smaller split-K shape, then a shape
     # whose row uses no workspace at all
-    for M, N, K in [(128, 5120, 17408), (100, 2048, 5120), (16, 7168, 5120)]:
+    for i, (M, N, K) in enumerate([(128, 5120, 17408), (100, 2048, 5120), (16, 7168, 5120)]):
         need = capi.workspace_bytes(fmt, M, N, K)
         say("noalloc fmt", fmt, "M", M, "N", N, "K", K, "route", capi.route(fmt, M, N, K),
             "workspace", need)
         assert need <= capi.NOALLOC_SCRATCH_BYTES
+        # the first two shapes must exercise the scratch (a ladder change that stopped routing
+        # them to split-K rows would otherwise leave it untested), the third must not
+        assert (need > 0) == (i < 2), (M, N, K, need)
         A = O.randn_f16((M, K), 3 + M, K ** -0.5)
         q, s, z = _weights(N, K, fmt, 5 + N)
         dA, dq, ds = dev(A, gpu), dev(q, gpu), dev(s, gpu)
