@@ -24,7 +24,10 @@ Extra fields of the one JSON line:
                 the host's CPU model and a numpy fp32 BLAS arm over a row sample as a library bar.
   decode        HBM GB/s of the decode regime (M <= 32): gemm_w8a16 on both weight formats and
                 gemm_fp16 on the two C2 shapes, weights rotated through > 512 MiB so no launch
-                finds its weights in the 256 MiB Infinity Cache.
+                finds its weights in the 256 MiB Infinity Cache.  These launches (and the
+                gate/up ones) go straight to the C entry points on parameter blocks built once
+                per weight copy: a Python wrapper's checks per call take longer than a 20-40 us
+                kernel and would time the host instead.
   fmha          the causal FMHA forward at configuration C5, TFLOP/s.
   card          the card passport before and after the run (tempo/plugins/gfx950/card.py):
                 engine and memory clocks, socket power, temperature, clock lock, and the
@@ -63,6 +66,10 @@ PEAK_HBM_GBPS = 8000.0      # MI355X HBM3E
 TRAFFIC_FILE = os.path.join(HERE, "profiles", "counters_gemm_fp16_configs.md")
 
 C1 = dict(M=4096, N=15360, K=3840)
+# Each decode and gate/up line first runs its own launches for at least this long: the engine
+# clock and power state take a few hundred ms of steady load to settle (measured on the M = 1
+# W8A16 line at (34816, 5120): 31.5 us per launch after ~150 launches, 29.7 us after 0.3 s)
+DECODE_SETTLE_S = 0.3
 SEED_A, SEED_B = 11, 77
 
 
@@ -91,6 +98,23 @@ def time_launches(fn, steps, warmup, stream):
     e1.record(stream)
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / steps
+
+
+def direct(entry, params, stream):
+    """fn(i) launching the C entry point `entry` on prebuilt parameter blocks params[i % len]:
+    a launch then costs the C-ABI call alone (a few microseconds), so a timed loop of kernels of
+    ~20-40 us is not bound by the host.  The operands were checked once, when the blocks were
+    built (capi's wrappers)."""
+    from cuda_tempiler_amd import capi
+
+    sp = capi._stream(stream)
+    n = len(params)
+
+    def fn(i):
+        rc = entry(params[i % n], sp)
+        if rc != 0:
+            raise capi.TempoError(rc, entry.__name__)
+    return fn
 
 
 def gate_c1(A, B, C):
@@ -338,9 +362,10 @@ def decode_lines(steps):
             for M in (1, 16, 32):
                 A = to_dev((g.standard_normal((M, K), dtype=np.float32) / np.sqrt(K)).astype(np.float16))
                 C = torch.empty((M, N), dtype=torch.float16, device="cuda:0")
-                fn = lambda i: capi.gemm_w8a16(A, W[i % copies], S[i % copies], Z[i % copies],
-                                               fmt=fmt, group=G, C=C, stream=stream)
-                settle_clocks(fn, stream, batch=50)
+                capi.gemm_w8a16(A, W[0], S[0], Z[0], fmt=fmt, group=G, C=C, stream=stream)
+                ps = [capi.w8a16_params(A, W[c], S[c], Z[c], C, fmt, G) for c in range(copies)]
+                fn = direct(capi.lib().tempo_gemm_w8a16_launch, ps, stream)
+                settle_clocks(fn, stream, batch=50, min_s=DECODE_SETTLE_S)
                 ms = time_launches(fn, steps, max(10, steps // 5), stream)
                 byts = nb + 2 * M * K + 2 * M * N
                 gbps = byts / (ms * 1e-3) / 1e9
@@ -358,8 +383,11 @@ def decode_lines(steps):
         for M in (1, 8, 16, 32):
             A = torch.randn((M, K), dtype=torch.float16, device="cuda:0")
             C = torch.empty((M, N), dtype=torch.float16, device="cuda:0")
-            fn = lambda i: capi.gemm_fp16(A, Bs[i % copies], C, stream=stream)
-            settle_clocks(fn, stream, batch=50)
+            capi.gemm_fp16(A, Bs[0], C, stream=stream)
+            ps = [capi.TempoGemmParams(capi._ptr(A), capi._ptr(Bs[c]), capi._ptr(C), M, N, K,
+                                       K, K, N) for c in range(copies)]
+            fn = direct(capi.lib().tempo_gemm_fp16_launch, ps, stream)
+            settle_clocks(fn, stream, batch=50, min_s=DECODE_SETTLE_S)
             ms = time_launches(fn, steps, max(10, steps // 5), stream)
             byts = nb + 2 * M * K + 2 * M * N
             gbps = byts / (ms * 1e-3) / 1e9
@@ -408,22 +436,36 @@ def gate_up_lines(steps):
             A = torch.randn((M, K), dtype=torch.float16, device="cuda:0") / K ** 0.5
             C = torch.empty((M, N), dtype=torch.float16, device="cuda:0")
             T = torch.empty((M, 2 * N), dtype=torch.float16, device="cuda:0")
+            L = capi.lib()
             if fmt == 0:
-                fused = lambda i: capi.gemm_fp16_gate_up(A, W[i % copies], C, stream=stream)
-                plain = lambda i: capi.gemm_fp16(A, W[i % copies], T, stream=stream)
+                capi.gemm_fp16_gate_up(A, W[0], C, stream=stream)  # operand checks, once
+                capi.gemm_fp16(A, W[0], T, stream=stream)
+                pf = [capi.TempoGemmParams(capi._ptr(A), capi._ptr(W[c]), capi._ptr(C), M, N, K,
+                                           K, K, N) for c in range(copies)]
+                pp = [capi.TempoGemmParams(capi._ptr(A), capi._ptr(W[c]), capi._ptr(T), M, 2 * N,
+                                           K, K, K, 2 * N) for c in range(copies)]
+                fused = direct(L.tempo_gemm_fp16_gate_up_launch, pf, stream)
+                plain = direct(L.tempo_gemm_fp16_launch, pp, stream)
             else:
-                fused = lambda i: capi.gemm_w8a16_gate_up(A, W[i % copies], S[i % copies],
-                                                          Z[i % copies], fmt=fmt, group=G, C=C,
-                                                          stream=stream)
-                plain = lambda i: capi.gemm_w8a16(A, W[i % copies], S[i % copies], Z[i % copies],
-                                                  fmt=fmt, group=G, C=T, stream=stream)
+                capi.gemm_w8a16_gate_up(A, W[0], S[0], Z[0], fmt=fmt, group=G, C=C, stream=stream)
+                capi.gemm_w8a16(A, W[0], S[0], Z[0], fmt=fmt, group=G, C=T, stream=stream)
+                pf = []
+                for c in range(copies):
+                    q = capi.w8a16_params(A, W[c], S[c], Z[c], C, fmt, G)
+                    q.N = N  # the output width; the weights hold 2N rows
+                    pf.append(q)
+                pp = [capi.w8a16_params(A, W[c], S[c], Z[c], T, fmt, G) for c in range(copies)]
+                fused = direct(L.tempo_gemm_w8a16_gate_up_launch, pf, stream)
+                plain = direct(L.tempo_gemm_w8a16_launch, pp, stream)
 
             def unfused(i):
                 plain(i)
                 g, u = T.chunk(2, dim=-1)
                 return F.silu(g) * u
 
+            settle_clocks(fused, stream, batch=20, min_s=DECODE_SETTLE_S)
             ms_f = time_launches(fused, steps, max(10, steps // 5), stream)
+            settle_clocks(unfused, stream, batch=20, min_s=DECODE_SETTLE_S)
             ms_u = time_launches(unfused, steps, max(10, steps // 5), stream)
             byts = nb + 2 * M * K + 2 * M * N
             gbps = byts / (ms_f * 1e-3) / 1e9

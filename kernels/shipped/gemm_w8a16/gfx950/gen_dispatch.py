@@ -75,8 +75,9 @@ def instantiation(kind, p, epi=0):
 
 def condition(sel, kind, p, m_max, n_min=0, gate_up=False):
     if kind == "line" and p.get("TL"):
-        fit = "(p.N %% %d) == 0 && (p.K %% %d) == 0 && (line_tail_fits<%d,%d,%d,%d>(p))" % (
-            sel.STREAM_N_ROWS * p["R"], sel.LINE_K_STEP, p["MB"], p["R"], p["D"], p["SN"])
+        fit = "(p.N %% %d) == 0 && (p.K %% %d) == 0 && (line_tail_fits<%d,%d,%d,%d,%d>(p))" % (
+            sel.STREAM_N_ROWS * p["R"], sel.LINE_K_STEP, p["MB"], p["R"], p["D"], p["SN"],
+            1 if gate_up else 0)
     elif kind == "line":
         sno = p.get("SN", 1) // 2 if gate_up and p.get("SN", 1) >= 2 else p.get("SN", 1)
         fit = "(p.N %% %d) == 0 && (p.K %% %d) == 0 && p.K <= %d" % (

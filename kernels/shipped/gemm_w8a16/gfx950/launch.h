@@ -165,34 +165,39 @@ inline bool line_split(int wgs, int SN, int K, int waves, int* S_out, int* chunk
   }
 }
 
-// Tail grid of the line kernel (TL = 1): q whole rounds of SN-slab workgroups, kLineCus per
-// round, then one single-wave workgroup per remaining slab.  It applies when q >= 1, at most one
-// slab per CU remains, and a CU holds its q workgroups and one tail at once (LDS: the launch's
-// size is the larger of the two bodies'; waves: 16).  The ladder's fit predicate calls
-// line_tail_fits, so a row that fits always launches.
+// Tail grid of the line kernel (TL = 1): q whole rounds of SN-slab-wave workgroups, kLineCus per
+// round, then one single-wave workgroup per remaining output slab.  It applies when q >= 1, at
+// most one slab per CU remains, and a CU holds its q workgroups and one tail at once (LDS: the
+// launch's size is the larger of the two bodies'; waves: 16).  EPI = 1 (fused gate/up): the
+// workgroups' slab waves pair up (SN/2 output slabs each) and a tail wave carries its output
+// slab's gate and up row groups.  The ladder's fit predicate calls line_tail_fits, so a row
+// that fits always launches.
 constexpr int kLineCus = 256;  // CUs of the part (MI355X, MI350X)
-template <int MB, int R, int D, int SN>
+template <int MB, int R, int D, int SN, int EPI = 0>
 inline bool line_tail_grid(const W8A16Params& p, int* nbig, int* grid, size_t* lds) {
   if (p.N % (16 * R) || p.K % 128 || p.K > 65536) return false;
-  const int slabs = p.N / (16 * R);
-  const int q = slabs / (kLineCus * SN);
-  const int tail = slabs - q * kLineCus * SN;
+  constexpr int SNO = EPI ? SN / 2 : SN;
+  const int slabs = p.N / (16 * R);  // output slabs
+  const int q = slabs / (kLineCus * SNO);
+  const int tail = slabs - q * kLineCus * SNO;
   if (q < 1 || tail > kLineCus) return false;
   const int G = p.K / 128;
   const size_t L =
-      p.fmt == 1 ? std::max(StreamLine<MB, R, D, 1, 0, SN>::lds(1, G), StreamLine<MB, R, D, 1, 0, 1>::lds(1, G))
-                 : std::max(StreamLine<MB, R, D, 2, 0, SN>::lds(1, G), StreamLine<MB, R, D, 2, 0, 1>::lds(1, G));
+      p.fmt == 1 ? std::max(StreamLine<MB, R, D, 1, EPI, SN>::lds(1, G),
+                            StreamLine<MB, R, D, 1, EPI, 1>::lds(1, G))
+                 : std::max(StreamLine<MB, R, D, 2, EPI, SN>::lds(1, G),
+                            StreamLine<MB, R, D, 2, EPI, 1>::lds(1, G));
   if ((size_t)(q + 1) * L > 160 * 1024 || (q + 1) * SN > 16) return false;
   *nbig = q * kLineCus;
   *grid = q * kLineCus + tail;
   *lds = L;
   return true;
 }
-template <int MB, int R, int D, int SN>
+template <int MB, int R, int D, int SN, int EPI = 0>
 inline bool line_tail_fits(const W8A16Params& p) {
   int nbig = 0, grid = 0;
   size_t lds = 0;
-  return line_tail_grid<MB, R, D, SN>(p, &nbig, &grid, &lds);
+  return line_tail_grid<MB, R, D, SN, EPI>(p, &nbig, &grid, &lds);
 }
 
 // k slices of the line kernel across workgroups (KS = the most a row allows): the count that
@@ -230,8 +235,9 @@ inline hipError_t launch_line_fmt(const W8A16Params& p, hipStream_t s, const Wor
   int wgs = p.N / (16 * R * SL::SNO);  // output slabs / per workgroup
   constexpr int TPB = MB >= 4 ? 512 : 1024;  // many activation blocks: 256 VGPRs per lane
   if constexpr (TL) {
-    static_assert(SN > 1 && EPI == 0, "tail grid: shared activation ring, plain epilogue");
-    if (!line_tail_grid<MB, R, D, SN>(p, &a.nbig, &wgs, &lds)) return hipErrorInvalidConfiguration;
+    static_assert(SN > 1 && (EPI == 0 || SN % 2 == 0), "tail grid: shared activation ring");
+    if (!line_tail_grid<MB, R, D, SN, EPI>(p, &a.nbig, &wgs, &lds))
+      return hipErrorInvalidConfiguration;
     G = p.K / 128;
   } else {
     if constexpr (KS > 1) {

@@ -131,8 +131,14 @@ LADDER = [
 LADDER_GATE_UP = [
     # two ring steps at M = 1 and M = 32 (1.05-1.08x / 1.02-1.06x four, both formats)
     (1, 0, "gl0r1n2d2", "line", dict(MB=0, R=1, D=2, SN=2, W=2048)),
+    # M <= 16 / 32, wide N: the tail grid -- whole rounds of paired workgroups (SN/2 output
+    # slabs each), then one wave per remaining output slab carrying its gate and up row groups;
+    # at (17408 x 2, 5120) M = 32 1.14x / 1.05x the paired row below (41.2 / 47.0 us against
+    # 46.8 / 49.5, int8 / uint8, one process), M = 16 int8 1.04x (uint8: 0.97x, kept off)
+    (16, 12288, "gl1r1n4d2t", "line", dict(MB=1, R=1, D=2, SN=4, W=2048, TL=1, fmts=(1,))),
     (16, 12288, "gl1r1n4d3", "line", dict(MB=1, R=1, D=3, SN=4, W=2048)),
     (16, 0, "gl1r1n2d4", "line", dict(MB=1, R=1, D=4, SN=2, W=2048)),
+    (32, 12288, "gl2r1n8d2t", "line", dict(MB=2, R=1, D=2, SN=8, W=2048, TL=1)),
     (32, 12288, "gl2r1n4d2", "line", dict(MB=2, R=1, D=2, SN=4, W=2048)),
     (32, 0, "gl2r1n2d4", "line", dict(MB=2, R=1, D=4, SN=2, W=2048)),
     (1, 0, "g1a_r1u2", "stream", dict(MB=1, R=1, U=2, A=1, fmts=(1,))),
@@ -177,32 +183,40 @@ LINE_CUS = 256      # CUs of the part: one round of workgroups of the line kerne
 LINE_LDS = 160 * 1024
 
 
-def _line_lds(p, fmt, K, sn):
+def _line_lds(p, fmt, K, sn, rr=None):
     """LDS of one workgroup of the line kernel with one k chunk, as StreamLine::lds(1, K/128)
-    declares it: sn weight rings (their own activation slots too when sn = 1), the fmt 2
-    metadata of K/128 groups per wave, and (sn > 1) the shared activation ring of D + 1 slots."""
-    wslot, aslot = p["R"] * 2048, (p["MB"] * 16 * 256 if p["MB"] else 256)
-    meta = -(-(p["R"] * 16 * (K // LINE_K_STEP) * 3) // 16) * 16 if fmt == 2 else 0
+    declares it: sn weight rings of rr row groups each (their own activation slots too when
+    sn = 1), the fmt 2 metadata of K/128 groups per wave, and (sn > 1) the shared activation
+    ring of D + 1 slots.  rr defaults to R (2R: a fused gate/up wave carrying both halves)."""
+    rr = p["R"] if rr is None else rr
+    wslot, aslot = rr * 2048, (p["MB"] * 16 * 256 if p["MB"] else 256)
+    meta = -(-(rr * 16 * (K // LINE_K_STEP) * 3) // 16) * 16 if fmt == 2 else 0
     wave = -(-(p["D"] * (wslot + (aslot if sn == 1 else 0)) + meta) // 1024) * 1024
     act = -(-((p["D"] + 1) * aslot) // 1024) * 1024 if sn > 1 else 0
     return sn * wave + act
 
 
-def line_tail_fits(p, N, K, fmt):
+def line_tail_fits(p, N, K, fmt, epi=0):
     """The tail grid (TL = 1) of the line kernel (launch.h line_tail_grid): q >= 1 whole rounds of
-    SN-slab workgroups, at most one remaining slab per CU, and a CU's q workgroups plus one tail
-    resident together (LDS and 16 waves)."""
-    slabs, rnd = N // (STREAM_N_ROWS * p["R"]), LINE_CUS * p["SN"]
+    SN-slab-wave workgroups, at most one remaining output slab per CU, and a CU's q workgroups
+    plus one tail resident together (LDS and 16 waves).  epi = 1 (fused gate/up): SN/2 output
+    slabs per workgroup, and a tail wave carries 2R row groups (gate and up)."""
+    sno = p["SN"] // 2 if epi else p["SN"]
+    slabs, rnd = N // (STREAM_N_ROWS * p["R"]), LINE_CUS * sno
     q = slabs // rnd
     if q < 1 or slabs - q * rnd > LINE_CUS or K > LINE_K_MAX:
         return False
-    lds = max(_line_lds(p, fmt, K, p["SN"]), _line_lds(p, fmt, K, 1))
+    lds = max(_line_lds(p, fmt, K, p["SN"]),
+              _line_lds(p, fmt, K, 1, rr=2 * p["R"] if epi else p["R"]))
     return (q + 1) * lds <= LINE_LDS and (q + 1) * p["SN"] <= 16
 
 
 def _fits_gate_up(kind, p, M, N, K, fmt=1):
     # N is the output width; the slab waves of the shared kernel and of the line kernel with
     # SN >= 2 pair up (SN/2 output slabs per workgroup)
+    if kind == "line" and p.get("TL"):  # tail grid of paired workgroups
+        return (N % (STREAM_N_ROWS * p["R"]) == 0 and K % LINE_K_STEP == 0
+                and line_tail_fits(p, N, K, fmt, epi=1))
     if kind == "line" and p.get("SN", 1) >= 2:
         return (N % (STREAM_N_ROWS * p["R"] * p["SN"] // 2) == 0 and K % LINE_K_STEP == 0
                 and K <= LINE_K_MAX)

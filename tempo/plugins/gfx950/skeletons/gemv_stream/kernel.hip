@@ -1233,21 +1233,23 @@ __device__ __forceinline__ void line_body(const StreamArgs& p, int G, int wgi, i
   }
 }
 
-// TL = 1 (SN > 1, EPI = 0, one k chunk): the grid is p.nbig workgroups of SN slabs -- a whole
-// number of them per CU -- followed by one workgroup per remaining slab, in which wave 0 streams
-// that slab over the whole K with its own activation ring (the body with SN = 1) and the other
-// waves leave at once.  A grid of whole rounds plus at most one such tail per CU keeps the slabs
-// per CU within one of each other; with workgroups of SN slabs alone, a partial last round puts
+// TL = 1 (SN > 1, one k chunk): the grid is p.nbig workgroups of SN slab waves -- a whole number
+// of them per CU -- followed by one workgroup per remaining output slab, in which wave 0 streams
+// that slab over the whole K with its own activation ring (the body with SN = 1; for the fused
+// gate/up, EPI = 1, that wave carries the slab's gate and up row groups) and the other waves
+// leave at once.  A grid of whole rounds plus at most one such tail per CU keeps the slabs per
+// CU within one of each other; with workgroups of SN slabs alone, a partial last round puts
 // 2 SN slabs on some CUs and SN on others (N = 34816, SN = 4: 8 or 12).
 template <int MB, int R, int D, int BFMT, int EPI = 0, int SN = 1, int TPB = 1024, int TL = 0>
 __global__ __launch_bounds__(TPB) void k_stream_line(StreamArgs p, int G) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t dsm[];
   if constexpr (TL) {
-    static_assert(SN > 1 && EPI == 0, "tail workgroups: shared activation ring, plain epilogue");
+    static_assert(SN > 1, "tail workgroups: a shared activation ring in the whole rounds");
+    constexpr int SNO = StreamLine<MB, R, D, BFMT, EPI, SN>::SNO;  // output slabs per workgroup
     const int wgi = blockIdx.x;
     if (wgi >= p.nbig) {
       if (threadIdx.x >= 64) return;
-      line_body<MB, R, D, BFMT, 0, 1>(p, G, p.nbig * SN + (wgi - p.nbig), 0, dsm);
+      line_body<MB, R, D, BFMT, EPI, 1>(p, G, p.nbig * SNO + (wgi - p.nbig), 0, dsm);
       return;
     }
   }

@@ -196,9 +196,12 @@ W8 = {
 W8_GATE_UP = {
     1: [
         ("gl0r1n2d2", 1, 17408, 5120),
-        ("gl1r1n4d3", 16, 17408, 5120),
+        ("gl1r1n4d2t", 16, 17408, 5120),   # tail grid: 2 rounds of paired workgroups, 64 tails
+        ("gl1r1n4d2t", 9, 12288, 5120),    # ragged M; whole rounds and a full tail round
+        ("gl1r1n4d3", 16, 13312, 5120),    # 320 remaining slabs: past the tail grid
         ("gl1r1n2d4", 8, 7680, 3840),
-        ("gl2r1n4d2", 32, 17408, 5120),
+        ("gl2r1n8d2t", 32, 17408, 5120),
+        ("gl2r1n4d2", 32, 12288, 5120),    # fewer slabs than one round of 8-wave workgroups
         ("gl2r1n2d4", 32, 7680, 3840),
         ("g1a_r1u2", 1, 512, 65664),
         ("gh16r1u2n2", 16, 512, 65664),
@@ -213,7 +216,9 @@ W8_GATE_UP = {
         ("gl0r1n2d2", 1, 17408, 5120),
         ("gl1r1n4d3", 16, 17408, 5120),
         ("gl1r1n2d4", 8, 7680, 3840),
-        ("gl2r1n4d2", 32, 17408, 5120),
+        ("gl2r1n8d2t", 32, 17408, 5120),
+        ("gl2r1n8d2t", 20, 17408, 5120),   # ragged M
+        ("gl2r1n4d2", 32, 12288, 5120),
         ("gl2r1n2d4", 32, 7680, 3840),
         ("g1a_r1u8", 1, 512, 66048),
         ("g1a_r1u4", 1, 512, 65792),
