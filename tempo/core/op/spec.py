@@ -36,7 +36,9 @@ def flops(op: OpSpec) -> float:
 
 
 def describe(op: OpSpec) -> str:
-    s = op.shapes
-    return "%s %sx%sx%s  %s*%s->%s (acc %s), layouts %s/%s/%s" % (
-        op.kind, s.get("M"), s.get("N"), s.get("K"), op.dtype_a, op.dtype_b, op.dtype_c,
-        op.dtype_acc, op.layout_a, op.layout_b, op.layout_c)
+    """One line for logs and reports, e.g.
+    "gemm[M=4096 N=15360 K=3840] A:fp16/k B:fp16/k -> C:fp16/n, fp32 accumulation"."""
+    dims = " ".join("%s=%s" % (k, op.shapes[k]) for k in ("M", "N", "K") if k in op.shapes)
+    return "%s[%s] A:%s/%s B:%s/%s -> C:%s/%s, %s accumulation" % (
+        op.kind, dims, op.dtype_a, op.layout_a, op.dtype_b, op.layout_b, op.dtype_c, op.layout_c,
+        op.dtype_acc)

@@ -77,6 +77,39 @@ def test_g4_spec_refused_in_time_bound():
         base.spec_forbidden_in_time_bound(r)
 
 
+# ---- the loader's refusals (reference tempo/plugins/registry.py:41-76) -------------------------
+def test_loader_refuses_what_breaks_the_contract():
+    import types
+
+    with pytest.raises(base.ContractError):
+        registry.load("no_such_plugin")
+
+    def plugin(contract="tempo/arch/1", rates=None, raises=False):
+        def symbols():
+            if raises:
+                raise RuntimeError("table unavailable")
+            return rates or {}
+        return types.SimpleNamespace(contract=contract,
+                                     machine=types.SimpleNamespace(symbols=symbols))
+
+    card = base.CardState(index=0, clock_mhz=2400, foreign_procs=0, date="d")
+    prov = base.Provenance("t", None, "1", "d", "w", "clean", card)
+    busy = base.Provenance("t", None, "1", "d", "w", "clean",
+                           base.CardState(index=0, clock_mhz=2400, foreign_procs=2, date="d"))
+    ok = {"HBM.X": base.Rate("HBM.X", 1.0, "GB/s", "MEASURED", prov)}
+    for check in registry.GATE:
+        check(plugin(rates=ok), "p")  # a clean plugin passes every check
+    bad = [plugin(contract=None), plugin(contract="tempo/arch2/1"), plugin(raises=True),
+           plugin(rates={"X": 1.0}),                                                 # not a Rate
+           plugin(rates={"X": base.Rate("X", 1.0, "u", "MEASURED")}),                # no card
+           plugin(rates={"X": base.Rate("X", 1.0, "u", "MEASURED", busy)})]          # neighbours
+    for p in bad:
+        with pytest.raises(base.ContractError):
+            for check in registry.GATE:
+                check(p, "p")
+    assert registry._contract_major("tempo/arch/7") == base.CONTRACT_MAJOR
+
+
 # ---- G5: self-test -----------------------------------------------------------------------------
 def test_g5_selftest_green(plug):
     rep = plug.selftest()
