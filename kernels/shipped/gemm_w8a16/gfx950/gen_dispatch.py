@@ -36,6 +36,10 @@ HEAD = """// GENERATED from select.py -- do not edit.  Regenerate with:
 
 def instantiation(kind, p, epi=0):
     tail = ",%d" % epi if epi else ""
+    if kind == "line" and p.get("MT"):  # row tiles x slab groups
+        if epi or p.get("TL") or p.get("KS", 1) > 1:
+            raise ValueError("row tiles take the plain epilogue, whole k and no tail grid")
+        return "launch_line_mt<%d,%d,%d,%d>" % (p["MB"], p["R"], p["D"], p["S"])
     if kind == "line" and p.get("KS", 1) > 1:  # k slices across workgroups: a workspace row
         if epi or p.get("TL"):
             raise ValueError("k slices take the plain epilogue and no tail grid")
@@ -78,6 +82,12 @@ def condition(sel, kind, p, m_max, n_min=0, gate_up=False):
         fit = "(p.N %% %d) == 0 && (p.K %% %d) == 0 && (line_tail_fits<%d,%d,%d,%d,%d>(p))" % (
             sel.STREAM_N_ROWS * p["R"], sel.LINE_K_STEP, p["MB"], p["R"], p["D"], p["SN"],
             1 if gate_up else 0)
+    elif kind == "line" and p.get("MT"):
+        fit = "(p.N %% %d) == 0 && (p.K %% %d) == 0 && p.K <= %d" % (
+            sel.STREAM_N_ROWS * p["R"], sel.LINE_K_STEP, sel.LINE_K_MAX)
+        if "NMAX" in p:
+            fit += " && p.N < %d" % p["NMAX"]
+        fit += " && (line_mt_fits<%d,%d,%d,%d>(p))" % (p["MB"], p["R"], p["D"], p["S"])
     elif kind == "line":
         sno = p.get("SN", 1) // 2 if gate_up and p.get("SN", 1) >= 2 else p.get("SN", 1)
         fit = "(p.N %% %d) == 0 && (p.K %% %d) == 0 && p.K <= %d" % (

@@ -271,6 +271,58 @@ inline hipError_t launch_line(const W8A16Params& p, hipStream_t s) {
   return launch_line_fmt<2, MB, R, D, SN, WAVES, EPI, TL>(p, s);
 }
 
+// Row-tiled line kernel (64 < M <= 128): the rows of A in tiles of 16 MB across workgroups, each
+// workgroup one row tile x one slab group of 16 R weight rows over the whole K, its S waves
+// splitting K (partial sums added through LDS in chunk order) -- no split-K partials in HBM, and
+// the activations streamed from L2 per tile instead of per 128-column tile.  Workgroups = row
+// tiles x slab groups (the rows' bands choose R so that this makes whole rounds of the part).
+// S is the most waves, at most SMAX, whose rings (+ fmt 2 metadata) fit the LDS.
+template <int BFMT, int MB, int R, int D, int SMAX>
+inline bool line_mt_config(const W8A16Params& p, int* S_out, int* per_out, size_t* lds_out) {
+  using SL = StreamLine<MB, R, D, BFMT, 0, 1>;
+  if (p.N % (16 * R) || p.K % 128 || p.K > 65536 || p.M <= 0) return false;
+  const int steps = p.K / 128;
+  for (int S = std::min(SMAX, steps); S >= 1; --S) {
+    const int per = (steps + S - 1) / S;  // steps per wave
+    const int s2 = (steps + per - 1) / per;
+    const size_t lds = SL::lds(s2, per);
+    if (lds <= 160 * 1024) {
+      *S_out = s2;
+      *per_out = per;
+      *lds_out = lds;
+      return true;
+    }
+  }
+  return false;
+}
+template <int MB, int R, int D, int SMAX>
+inline bool line_mt_fits(const W8A16Params& p) {
+  int S = 0, per = 0;
+  size_t lds = 0;
+  return p.fmt == 1 ? line_mt_config<1, MB, R, D, SMAX>(p, &S, &per, &lds)
+                    : line_mt_config<2, MB, R, D, SMAX>(p, &S, &per, &lds);
+}
+template <int BFMT, int MB, int R, int D, int SMAX>
+inline hipError_t launch_line_mt_fmt(const W8A16Params& p, hipStream_t s) {
+  int S = 0, per = 0;
+  size_t lds = 0;
+  if (!line_mt_config<BFMT, MB, R, D, SMAX>(p, &S, &per, &lds)) return hipErrorInvalidConfiguration;
+  StreamArgs a = stream_args(p);
+  a.S = S;
+  a.chunk = per * 128;
+  a.mrows = 16 * MB;
+  a.mtiles = (p.M + a.mrows - 1) / a.mrows;
+  const int groups = p.N / (16 * R);
+  hipLaunchKernelGGL((k_stream_line<MB, R, D, BFMT, 0, 1, 64 * SMAX, 0>),
+                     dim3(a.mtiles * groups), dim3(64 * S), lds, s, a, per);
+  return hipGetLastError();
+}
+template <int MB, int R, int D, int SMAX>
+inline hipError_t launch_line_mt(const W8A16Params& p, hipStream_t s) {
+  if (p.fmt == 1) return launch_line_mt_fmt<1, MB, R, D, SMAX>(p, s);
+  return launch_line_mt_fmt<2, MB, R, D, SMAX>(p, s);
+}
+
 // The line kernel with up to KS k slices across workgroups (a workspace row).
 template <int MB, int R, int D, int SN, int WAVES, int KS>
 inline hipError_t launch_line_ks(const W8A16Params& p, hipStream_t s, const Workspace& w) {

@@ -74,9 +74,12 @@ LADDER = [
      dict(BM=128, BN=128, BK=128, WM=1, WN=4, STAGES=2, GROUP=8, XCD=1, RSP=8, SW=256, MINKT=8,
           NMAX=12288)),
     (64, 0, "l4r1n2d3", "line", dict(MB=4, R=1, D=3, SN=2, W=2048)),
-    # 64 < M <= 128, narrow N (< 2048): the line kernel with eight activation blocks, two slab
-    # waves per ring and k slices (1.09x the 128 x 128 tile row below at (128, 1024, 5120))
-    (128, 0, "l8r1n2d2k8", "line", dict(MB=8, R=1, D=2, SN=2, W=2048, KS=8, NMAX=2048)),
+    # 64 < M <= 128, narrow N (< 2048): the line kernel on row tiles of 32 rows, each workgroup
+    # one row tile x 16 weight rows over the whole K on four waves (k chunks summed through LDS);
+    # the weight rows of one slab group are read by the row tiles on one XCD, from its L2 after
+    # the first (1.50x / 1.41x the line row with eight activation blocks and k slices across
+    # workgroups it replaced, at (128, 1024, 5120), int8 / uint8)
+    (128, 0, "l2r1d2m4", "line", dict(MB=2, R=1, D=2, MT=1, S=4, NMAX=2048)),
     # 64 < M <= 128, N < 12288, uint8 and long K: 128 x 256 tiles of 128 k, split-K (1.11x the
     # 64-k row at (128, 5120, 17408))
     (128, 0, "i8x128x256k128s2w256", "ilv8",
@@ -196,6 +199,21 @@ def _line_lds(p, fmt, K, sn, rr=None):
     return sn * wave + act
 
 
+def line_mt_fits(p, K, fmt):
+    """A row-tiled line row (MT = 1, launch.h line_mt_config): some count of waves, at most S,
+    each taking an equal count of whole 128-k steps, whose rings (+ fmt 2 metadata of those
+    steps) fit the LDS; with more than one wave the k chunks' partial sums ([S][R][MB] x 1 KiB)
+    reuse the rings' bytes."""
+    steps = K // LINE_K_STEP
+    for s in range(min(p["S"], steps), 0, -1):
+        per = -(-steps // s)
+        s2 = -(-steps // per)
+        rings = s2 * _line_lds(p, fmt, per * LINE_K_STEP, 1)
+        if (max(rings, s2 * p["R"] * p["MB"] * 1024) if s2 > 1 else rings) <= LINE_LDS:
+            return True
+    return False
+
+
 def line_tail_fits(p, N, K, fmt, epi=0):
     """The tail grid (TL = 1) of the line kernel (launch.h line_tail_grid): q >= 1 whole rounds of
     SN-slab-wave workgroups, at most one remaining output slab per CU, and a CU's q workgroups
@@ -243,6 +261,9 @@ def _fits(kind, p, M, N, K, fmt=1):
     if kind == "line" and p.get("TL"):  # tail grid: whole slabs, one k chunk
         return (N % (STREAM_N_ROWS * p["R"]) == 0 and K % LINE_K_STEP == 0
                 and line_tail_fits(p, N, K, fmt))
+    if kind == "line" and p.get("MT"):  # row tiles: whole slabs, whole k per workgroup
+        return (N % (STREAM_N_ROWS * p["R"]) == 0 and K % LINE_K_STEP == 0 and K <= LINE_K_MAX
+                and N < p.get("NMAX", 1 << 30) and line_mt_fits(p, K, fmt))
     if kind == "line":  # NMAX / KMIN (optional): the row holds narrower N / longer K only
         return (N % (STREAM_N_ROWS * p["R"] * p.get("SN", 1)) == 0 and K % LINE_K_STEP == 0
                 and K <= LINE_K_MAX and N < p.get("NMAX", 1 << 30) and K >= p.get("KMIN", 0))

@@ -217,6 +217,11 @@ class Gfx950Skeletons:
             grid = N // (16 * p["R"] * p["SN"])
             threads = 64 * p["SN"] * S
             bound = p["TPB"]  # __launch_bounds__(TPB)
+        elif kind == "line" and p.get("MT"):  # row tiles x slab groups
+            sp = space.line_split(N, int(op.shapes["K"]), p)
+            grid = -(-M // (16 * p["MB"])) * (N // (16 * p["R"]))
+            threads = 64 * (sp[0] if sp else 1)
+            bound = p["TPB"]
         elif kind == "line":
             sp = space.line_split(N, int(op.shapes["K"]), p)
             grid = (N // (16 * p["R"] * (p["SN"] // 2 if space.line_paired(p) else p.get("SN", 1)))
@@ -245,6 +250,9 @@ class Gfx950Skeletons:
                                                             lau.bound_threads)), lds, lau.threads)
         per_cu = max(1, occ.ctas_per_sm)
         rounds = -(-lau.grid_ctas // (int(_M.rate("GEOM.SMS").value) * per_cu))
+        # a grid smaller than one residency round leaves slots empty: a CU then holds only
+        # ceil(grid / CUs) workgroups, and its per-wave load counts that many times, not per_cu
+        fill = min(per_cu, -(-lau.grid_ctas // int(_M.rate("GEOM.SMS").value))) / per_cu
         atoms = []
         if kind in ("dma", "reg", "ilv", "ilv8"):
             ms = p.get("MS", 32) if kind not in ("ilv", "ilv8") else 16
@@ -273,6 +281,7 @@ class Gfx950Skeletons:
             flops = 2 * p["R"] * p["MB"] * space.MFMA_FLOPS[16]
             vmem = (p["R"] * wb + 2 * p["MB"]) * 1024
             lds_rd = vmem if kind == "ring" else 0
+        reps *= fill
         atoms.append(Atom(uid=0, kind=AtomKind.COMPUTE, op_id="v_mfma x%d" % (flops // 16384),
                           footprint={"MFMA": float(flops * reps)},
                           latency=_M.rate("LATENCY.MFMA32").value))

@@ -78,7 +78,9 @@ def hyper_params(kind, p, fmt, epi=0):
     params["kind"] = pk
     if pk == "shared":
         params.setdefault("TPB", 1024)
-    if pk == "line" and params["MB"] >= 4:  # the shipped launchers bound these at 512 threads
+    if pk == "line" and params.get("MT"):  # row tiles: the launcher bounds at 64 S threads
+        params["TPB"] = 64 * params["S"]
+    elif pk == "line" and params["MB"] >= 4:  # the shipped launchers bound these at 512 threads
         params.setdefault("SN", 1)
         params["TPB"] = 512
     if pk not in ("dma", "ilv"):

@@ -47,6 +47,8 @@ struct StreamArgs {
   int ks = 1;          // k_stream_line: k slices across workgroups (grid = workgroups x ks)
   int kspan = 0;       // ks > 1: k per slice (whole 128-k steps)
   float* part = nullptr;  // ks > 1: fp32 partial sums [ks][M][N], summed by k_splitk_reduce
+  int mtiles = 1;      // k_stream_line: row tiles of mrows rows each across workgroups
+  int mrows = 0;       // (mtiles > 1) rows per tile, 16 MB
 };
 
 // Group-wise metadata of one stage for one lane's row (fmt 2, group 128): GPS = 64*U/128 groups.
@@ -938,9 +940,14 @@ struct StreamLine {
             (BFMT == 2 ? ((size_t)RR * 16 * G * 3 + 15) / 16 * 16 : 0) + 1023) / 1024 * 1024;
   }
   static constexpr size_t act_bytes() { return SN > 1 ? ((size_t)DA * ASLOT + 1023) / 1024 * 1024 : 0; }
+  // S > 1: the k chunks' partial sums ([S][SN][RR][MBE] x 1 KiB) are reduced through LDS; they
+  // reuse the rings (all waves are past their loops then) except in the paired epilogue, whose
+  // up-to-gate exchange uses the start of the LDS after the reduction
+  static constexpr size_t red_bytes(int S) { return (size_t)S * SN * RR * MBE * 1024; }
   static constexpr size_t lds(int S, int G) {
-    return (size_t)S * (SN * wave_bytes(G) + act_bytes()) +
-           (S > 1 ? (size_t)S * SN * RR * MBE * 1024 : 0);
+    const size_t rings = (size_t)S * (SN * wave_bytes(G) + act_bytes());
+    if (S <= 1) return rings;
+    return PAIRED ? rings + red_bytes(S) : (rings > red_bytes(S) ? rings : red_bytes(S));
   }
 };
 
@@ -966,7 +973,8 @@ __device__ __forceinline__ void line_body(const StreamArgs& p, int G, int wgi, i
   uint8_t* meta_z = ring + D * WSTRIDE;                                  // fmt 2: [RR*16][G]
   _Float16* meta_s = reinterpret_cast<_Float16*>(meta_z + (RR * 16 * G + 1) / 2 * 2);
   const int S = p.S;  // k chunks
-  f32x4* red = reinterpret_cast<f32x4*>(dsm + S * (SN * wbytes + SL::act_bytes()));
+  f32x4* red = reinterpret_cast<f32x4*>(SL::PAIRED ? dsm + S * (SN * wbytes + SL::act_bytes())
+                                                   : dsm);
 
   const int k0 = ksi * p.kspan, k1 = ksi * p.kspan + (p.ks > 1 ? p.kspan : p.K);  // k slice
   const int kbeg = min(k1, k0 + kc * p.chunk);
@@ -1015,10 +1023,16 @@ __device__ __forceinline__ void line_body(const StreamArgs& p, int G, int wgi, i
 #pragma unroll
       for (int h = 0; h < EB; ++h)
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
-          __builtin_amdgcn_global_load_lds((void*)(wsrc[r][i] + (long)jj * 128 * EB + 128 * h),
-                                           (lds_void_stream_t*)(slot + (r * EB + h) * 2048 + i * 1024),
-                                           16, 0, 2 /* nt */);
+        for (int i = 0; i < 2; ++i) {
+          void* src = (void*)(wsrc[r][i] + (long)jj * 128 * EB + 128 * h);
+          lds_void_stream_t* dst = (lds_void_stream_t*)(slot + (r * EB + h) * 2048 + i * 1024);
+          // the weights stream through once (nontemporal: not kept in the caches), except with
+          // row tiles, whose workgroups on one XCD read the same weight rows from its L2
+          if (p.mtiles > 1)
+            __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
+          else
+            __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 2 /* nt */);
+        }
   };
   auto dma_a = [&](int j) {
     const int jj = min(j, n - 1);
@@ -1045,13 +1059,31 @@ __device__ __forceinline__ void line_body(const StreamArgs& p, int G, int wgi, i
     dma_a(j);
   }
   if constexpr (BFMT == 2) {  // this wave's zero-points and scales, one group per step
+    // batches of 8 entries per lane: the loads of a batch are in flight together before the
+    // LDS stores wait on them (one latency per batch, not per entry)
     const long gstride = p.K / 128;
     const int g0 = kbeg / 128;
-    for (int i = lane; i < RR * 16 * n; i += 64) {
-      const int row = i / n, g = i - row * n;
-      const long gi = (row_of(row / 16) + row % 16) * gstride + g0 + g;
-      meta_z[row * G + g] = p.zero[gi];
-      meta_s[row * G + g] = p.scale[gi];
+    const int tot = RR * 16 * n;
+    for (int i0 = lane; i0 < tot; i0 += 64 * 8) {
+      uint8_t zz[8];
+      _Float16 ss[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int i = min(i0 + 64 * u, tot - 1);
+        const int row = i / n, g = i - row * n;
+        const long gi = (row_of(row / 16) + row % 16) * gstride + g0 + g;
+        zz[u] = p.zero[gi];
+        ss[u] = p.scale[gi];
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int i = i0 + 64 * u;
+        if (i < tot) {
+          const int row = i / n, g = i - row * n;
+          meta_z[row * G + g] = zz[u];
+          meta_s[row * G + g] = ss[u];
+        }
+      }
     }
   }
   __builtin_amdgcn_s_waitcnt(0);  // prologue copies landed, scales and metadata loaded
@@ -1117,7 +1149,7 @@ __device__ __forceinline__ void line_body(const StreamArgs& p, int G, int wgi, i
         sc[r] = meta_s[(16 * r + r16) * G + j];
       }
     }
-    if constexpr (MB <= 2) {
+    if constexpr (MB <= 2 && RR <= 2) {
       // early reads: every fragment of the step into registers, then the slot is refilled while
       // the MFMAs run
       u32x4 w[RR][2][2], a[MBE][2][2];
@@ -1151,8 +1183,8 @@ __device__ __forceinline__ void line_body(const StreamArgs& p, int G, int wgi, i
           }
         }
     } else {
-      // late reads (many activation blocks): half by half, fragments read just before their
-      // MFMAs; the slot is refilled once both halves are done
+      // late reads (many activation blocks or row groups): half by half, fragments read just
+      // before their MFMAs; the slot is refilled once both halves are done
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         u32x4 w[RR][2];
@@ -1186,6 +1218,7 @@ __device__ __forceinline__ void line_body(const StreamArgs& p, int G, int wgi, i
     for (int b = 0; b < MBE; ++b) acc[r][b] += acc2[r][b];
 
   if (S > 1) {  // partial sums of the S k chunks of each slab, added in chunk order
+    if constexpr (!PAIRED) __syncthreads();  // every wave is past its ring reads: reuse them
 #pragma unroll
     for (int r = 0; r < RR; ++r)
 #pragma unroll
@@ -1252,6 +1285,27 @@ __global__ __launch_bounds__(TPB) void k_stream_line(StreamArgs p, int G) {
       line_body<MB, R, D, BFMT, EPI, 1>(p, G, p.nbig * SNO + (wgi - p.nbig), 0, dsm);
       return;
     }
+  }
+  if (p.mtiles > 1) {
+    // row tiles (one k slice): workgroup b takes row tile mi of slab group sgi, the row tiles of
+    // one slab group on one XCD (workgroups go to the 8 XCDs round robin) so their weight rows
+    // stream from HBM into that XCD's L2 once
+    const int b = blockIdx.x, groups = (int)gridDim.x / p.mtiles;
+    int mi, sgi;
+    if (groups % 8 == 0) {
+      const int j = b / 8;
+      mi = j % p.mtiles;
+      sgi = (j / p.mtiles) * 8 + b % 8;
+    } else {
+      mi = b % p.mtiles;
+      sgi = b / p.mtiles;
+    }
+    StreamArgs q = p;
+    q.A = p.A + (long)mi * p.mrows * p.lda;
+    q.C = p.C + (long)mi * p.mrows * p.ldc;
+    q.M = min(p.mrows, p.M - mi * p.mrows);
+    line_body<MB, R, D, BFMT, EPI, SN>(q, G, sgi, 0, dsm);
+    return;
   }
   const int wgi = p.ks > 1 ? (int)blockIdx.x / p.ks : (int)blockIdx.x;
   line_body<MB, R, D, BFMT, EPI, SN>(p, G, wgi, (int)blockIdx.x - wgi * p.ks, dsm);

@@ -9,7 +9,8 @@ The skeleton kinds, each a kernel family of tempo/plugins/gfx950/skeletons:
   reg     gemm_mfma/k_gemm          any weight format, register-staged copy that can dequantise
                                     on the way into LDS (W8A16 prefill, fp16 fallback)
   line    gemv_stream/k_stream_line decode (M <= 32): whole 128-byte weight lines by nontemporal
-                                    LDS-DMA into per-wave rings, fragments read back swizzled
+                                    LDS-DMA into per-wave rings, fragments read back swizzled;
+                                    with row tiles (MT = 1) also 32 < M <= 128, 8-bit weights
   ring    gemv_stream/k_stream_dma  decode (M <= 32): per-wave LDS-DMA ring of k-steps
   stream  gemv_stream/k_stream      decode, register-staged prefetch (kept as a measured arm)
 
@@ -55,6 +56,8 @@ DOMAINS = {
                 XCD=(1,)),
     "line": dict(R=(1, 2, 4), D=(2, 3, 4, 5, 6), W=(1024, 2048, 4096), SN=(1, 2, 4, 8), TL=(0, 1),
                  KS=(1, 4, 8, 16)),
+    # row tiles (MT = 1): 16 MB rows of A per workgroup, S waves splitting K (64 < M <= 128)
+    "line_mt": dict(MB=(1, 2, 4), R=(1, 2), D=(2, 3, 4), S=(2, 4, 8)),
     "ring": dict(R=(1, 2, 4), D=(4, 5, 6, 8, 10, 12, 14, 16)),
     "stream": dict(R=(1, 2, 4), U=(2, 4, 8), ALDS=(0, 1)),
     "shared": dict(R=(1, 2), U=(2, 4), SN=(2, 4, 8)),
@@ -130,6 +133,33 @@ def line_kslices(wgs: int, K: int, KS: int) -> int:
     return best if even(best) >= even(1) + 0.08 else 1
 
 
+def _line_lds(rings: int, red: int, S: int, paired: bool) -> int:
+    """StreamLine::lds: with S > 1 k chunks the partial sums (red bytes) are added through LDS,
+    in the rings' own bytes once every wave is past its loop, except in the paired epilogue,
+    which keeps them apart."""
+    if S <= 1:
+        return rings
+    return rings + red if paired else max(rings, red)
+
+
+def line_mt_split(K: int, p: dict):
+    """(S, steps per wave, LDS bytes, 1) of a row-tiled line hyperform (MT = 1), as
+    kernels/shipped/gemm_w8a16/gfx950/launch.h line_mt_config chooses them: the most waves, at
+    most p["S"], each taking an equal count of whole 128-k steps, whose rings (+ fmt 2 metadata of
+    those steps) fit the LDS; None if none does."""
+    steps = K // 128
+    _, wslot, aslot = line_geometry(p)
+    for S in range(min(p["S"], steps), 0, -1):
+        per = -(-steps // S)
+        s2 = -(-steps // per)
+        meta = -(-(p["R"] * 16 * per * 3) // 16) * 16 if p["BFMT"] == 2 else 0
+        wave = -(-(p["D"] * (wslot + aslot) + meta) // 1024) * 1024
+        lds = _line_lds(s2 * wave, s2 * p["R"] * p["MB"] * 1024, s2, False)
+        if lds <= LDS_MAX:
+            return s2, per, lds, 1
+    return None
+
+
 def line_tail_grid(N: int, K: int, p: dict):
     """(workgroups of SN slabs, grid) of the line kernel's tail grid (TL = 1), or None: q >= 1
     whole rounds of LINE_CUS workgroups, then one single-wave workgroup per remaining slab (at
@@ -151,6 +181,8 @@ def line_split(N: int, K: int, p: dict):
     compute them; None if none fits."""
     rr = 2 * p["R"] if p.get("EPI") and not line_paired(p) else p["R"]
     sn = p.get("SN", 1)
+    if p.get("MT"):  # row tiles: the most waves, at most S, whose rings fit (line_mt_config)
+        return line_mt_split(K, p)
     if p.get("TL"):  # one k chunk; LDS of the shared-ring body or the tail body, the larger
         steps = K // 128
         _, wslot, aslot = line_geometry(p)
@@ -171,7 +203,8 @@ def line_split(N: int, K: int, p: dict):
         meta = -(-(rr * 16 * per * 3) // 16) * 16 if p["BFMT"] == 2 else 0
         wave = -(-(p["D"] * (wslot + (aslot if sn == 1 else 0)) + meta) // 1024) * 1024
         act = -(-((p["D"] + 1) * aslot) // 1024) * 1024 if sn > 1 else 0  # D+1 shared slots
-        return s_ * (sn * wave + act) + (s_ * sn * rr * max(1, p["MB"]) * 1024 if s_ > 1 else 0)
+        return _line_lds(s_ * (sn * wave + act), s_ * sn * rr * max(1, p["MB"]) * 1024, s_,
+                         line_paired(p))
 
     while True:
         per = -(-steps // S)
@@ -256,6 +289,8 @@ def tag(kind: str, p: dict) -> str:
     if kind == "reg":
         return "reg_m%dn%dk%d_w%dx%d_f%d_z%d_b%d" % (p["BM"], p["BN"], p["BK"], p["WM"], p["WN"],
                                                    p["MS"], p["SWZ"], p["BFMT"])
+    if kind == "line" and p.get("MT"):
+        return "line_mb%d_r%d_d%d_mt%d_b%d" % (p["MB"], p["R"], p["D"], p["S"], p["BFMT"])
     if kind == "line":
         return "line_mb%d_r%d_n%d_d%d_w%d_b%d%s%s%s" % (
             p["MB"], p["R"], p.get("SN", 1), p["D"], p["W"], p["BFMT"],
@@ -336,6 +371,19 @@ def legal(kind: str, p: dict, M: int, N: int, K: int):
     R = p["R"]
     if N % (16 * R):
         return "N %% %d" % (16 * R)
+    if kind == "line" and p.get("MT"):
+        if p["MB"] < 1 or p.get("SN", 1) != 1 or p.get("EPI") or p.get("TL") or p.get("KS", 1) > 1:
+            return "row tiles: MB >= 1, one slab wave, plain epilogue, whole k"
+        if K % 128 or K > 65536:
+            return "K % 128 / K > 65536"
+        L, _, _ = line_geometry(p)
+        if (p["D"] - 1) * L >= 64:
+            return "vmcnt depth"
+        if p.get("TPB") != 64 * p["S"]:
+            return "row tiles: the launch bound is 64 S threads"
+        if line_mt_split(K, p) is None:
+            return "LDS"
+        return None
     if kind == "line":
         sn = p.get("SN", 1)
         if M > max(1, 16 * p["MB"]):
@@ -425,6 +473,14 @@ def variants(op: OpSpec) -> Iterator[Hyperform]:
                             q["SN"] = SN
                             q["TPB"] = 512
                         out.append(("line", q))
+        if b and M > 16:  # row tiles of 16 MB rows, at least two of them (8-bit weights)
+            d = DOMAINS["line_mt"]
+            for MBT in (m for m in d["MB"] if 16 * m < M):
+                for R in d["R"]:
+                    for D in d["D"]:
+                        for S in d["S"]:
+                            out.append(("line", dict(MB=MBT, R=R, D=D, MT=1, S=S, BFMT=b,
+                                                     TPB=64 * S)))
     if M <= 32:
         MB = 1 if M <= 16 else 2
         for R in DOMAINS["ring"]["R"]:

@@ -84,6 +84,8 @@ def row_of(params: dict):
             return None
     if kind == "stream":
         p["A"] = p.pop("ALDS", 0)
+    if kind == "line" and p.get("MT"):
+        return ("line", p) if p.pop("TPB", 0) == 64 * p["S"] else None
     if kind == "line":
         tpb = p.pop("TPB", 1024)
         if tpb != (512 if p["MB"] >= 4 else 1024):

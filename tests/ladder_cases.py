@@ -122,8 +122,9 @@ W8 = {
         ("i8x128x128w1x4k128s2w256", 100, 7168, 5120),
         ("i8x128x128w1x4k128s2w256", 128, 5120, 5120),
         ("i8x128x128w1x4k128s2w256", 100, 2048, 5120),
-        ("l8r1n2d2k8", 128, 1024, 5120),
-        ("l8r1n2d2k8", 100, 1024, 5120),
+        ("l2r1d2m4", 128, 1024, 5120),
+        ("l2r1d2m4", 100, 1024, 5120),    # last row tile of 4 rows
+        ("l2r1d2m4", 72, 1040, 1536),     # 3 row tiles, 65 slab groups (not whole XCD rounds)
         ("l8r1n2d3", 128, 5152, 5120),
         ("m128x128k64", 256, 5120, 5120),
         ("i8x128x128w1x4k128s2w256", 2048, 1024, 5120),
@@ -180,8 +181,9 @@ W8 = {
         ("i8x128x128w1x4k128s2w256", 100, 7168, 5120),
         ("i8x128x128w1x4k128s2w256", 128, 5120, 5120),
         ("i8x128x128w1x4k128s2w256", 100, 2048, 5120),
-        ("l8r1n2d2k8", 128, 1024, 5120),
-        ("l8r1n2d2k8", 100, 1024, 5120),
+        ("l2r1d2m4", 128, 1024, 5120),
+        ("l2r1d2m4", 100, 1024, 5120),    # last row tile of 4 rows
+        ("l2r1d2m4", 72, 1040, 1536),     # 3 row tiles, 65 slab groups (not whole XCD rounds)
         ("l8r1n2d3", 128, 5152, 5120),
         ("m128x128k64", 256, 5120, 5120),
         ("i8x128x128w1x4k128s2w256", 2048, 1024, 5120),
