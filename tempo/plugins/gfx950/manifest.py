@@ -277,15 +277,19 @@ def card_passport(before, after):
     return out
 
 
-def fold_counters(rows, counter_files, op):
+def fold_counters(rows, counter_files, op, md5=None):
     """Attach the counter step's per-launch figures (measure_shipped --counters) to the measured
-    rows of the same shape and format; returns how many rows got them."""
+    rows of the same shape and format; returns how many rows got them.  A counter file taken on
+    other sources than md5 (the rows') is refused."""
     n = 0
     for cf_ in counter_files:
         with open(cf_) as f:
             got = json.load(f)
         if got.get("op") != op:
             continue
+        if md5 is not None and got.get("source_md5") != md5:
+            raise ValueError("%s was taken on other sources than the rows (%s vs %s)"
+                             % (cf_, got.get("source_md5"), md5))
         by = {(r["M"], r["N"], r["K"], r["fmt"]): r for r in got["rows"]}
         for row in rows:
             c = by.get((row["M"], row["N"], row["K"], row["fmt"]))
@@ -380,8 +384,8 @@ def make(op, rows_files=(), counter_files=()):
             continue
         man["rows"] = got["rows"]
         man["card"] = card_passport(got.get("card_before"), got.get("card_after"))
-        man["rows_source_md5"] = md5_of(op)
-    fold_counters(man["rows"], counter_files, op)
+        man["rows_source_md5"] = got.get("source_md5")  # the sources the rows were timed on
+    fold_counters(man["rows"], counter_files, op, man.get("rows_source_md5"))
     with open(path, "w") as f:
         json.dump(man, f, indent=1)
         f.write("\n")

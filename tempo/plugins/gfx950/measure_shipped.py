@@ -48,6 +48,16 @@ NK_W8 = [(7168, 5120), (5120, 6144), (34816, 5120), (5120, 17408), (1024, 5120),
 SHAPES_W8 = [(M, N, K) for (N, K) in NK_W8 for M in (1, 16, 32, 128, 2048)]
 
 
+def _source_md5(op):
+    """md5 over the delivery's signed files as they were when these figures were taken (the
+    manifest keeps it beside the md5 of the files it ships; a mismatch means stale figures)."""
+    if op not in ("gemm_fp16", "gemm_w8a16"):
+        return None
+    from .manifest import md5_of
+
+    return md5_of(op)
+
+
 def _say(*a):
     print(*a, flush=True)
 
@@ -235,7 +245,7 @@ def counters(op: str, out: str, groups, quick: bool = False) -> str:
     path = os.path.join(out, "counters_%s.json" % op)
     with open(path, "w") as f:
         json.dump({"op": op, "groups": list(groups), "scales": scales, "reps": REPS,
-                   "rows": rows}, f, indent=1)
+                   "source_md5": _source_md5(op), "rows": rows}, f, indent=1)
     _say("wrote %s: %d shapes" % (path, len(rows)))
     return path
 
@@ -453,8 +463,8 @@ def main():
     after = card_state()
     path = os.path.join(a.out, "rows_%s.json" % a.op)
     with open(path, "w") as f:
-        json.dump({"op": a.op, "card_before": before, "card_after": after, "rows": rows}, f,
-                  indent=1)
+        json.dump({"op": a.op, "card_before": before, "card_after": after,
+                   "source_md5": _source_md5(a.op), "rows": rows}, f, indent=1)
     bad = [r for r in rows if r.get("gate") == "FAIL"]
     _say("wrote %s: %d rows, %d gate failures" % (path, len(rows), len(bad)))
     return 1 if bad else 0

@@ -1059,31 +1059,52 @@ __device__ __forceinline__ void line_body(const StreamArgs& p, int G, int wgi, i
     dma_a(j);
   }
   if constexpr (BFMT == 2) {  // this wave's zero-points and scales, one group per step
-    // batches of 8 entries per lane: the loads of a batch are in flight together before the
-    // LDS stores wait on them (one latency per batch, not per entry)
+    // entry i of [RR*16 rows][n groups] is lane i % 64's, batches of 8 per lane: the loads of a
+    // batch are in flight together before the LDS stores wait on them.  Each lane steps its
+    // (row, group) by 64 entries with the wave-uniform quotient and remainder of 64 / n (one
+    // division per wave, not one per entry: per-entry divisions cost 10-20% of a fmt 2 decode
+    // launch)
     const long gstride = p.K / 128;
     const int g0 = kbeg / 128;
+    const int nn = max(n, 1);
     const int tot = RR * 16 * n;
+    const int q64 = 64 / nn, r64 = 64 - q64 * nn;
+    int row0 = lane / nn, col0 = lane - row0 * nn;
     for (int i0 = lane; i0 < tot; i0 += 64 * 8) {
       uint8_t zz[8];
       _Float16 ss[8];
+      int row = row0, g = col0;
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        const int i = min(i0 + 64 * u, tot - 1);
-        const int row = i / n, g = i - row * n;
-        const long gi = (row_of(row / 16) + row % 16) * gstride + g0 + g;
-        zz[u] = p.zero[gi];
-        ss[u] = p.scale[gi];
+        if (i0 + 64 * u < tot) {
+          const long gi = (row_of(row / 16) + row % 16) * gstride + g0 + g;
+          zz[u] = p.zero[gi];
+          ss[u] = p.scale[gi];
+        }
+        g += r64;
+        row += q64;
+        if (g >= nn) {
+          g -= nn;
+          ++row;
+        }
       }
+      row = row0;
+      g = col0;
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        const int i = i0 + 64 * u;
-        if (i < tot) {
-          const int row = i / n, g = i - row * n;
+        if (i0 + 64 * u < tot) {
           meta_z[row * G + g] = zz[u];
           meta_s[row * G + g] = ss[u];
         }
+        g += r64;
+        row += q64;
+        if (g >= nn) {
+          g -= nn;
+          ++row;
+        }
       }
+      row0 = row;
+      col0 = g;
     }
   }
   __builtin_amdgcn_s_waitcnt(0);  // prologue copies landed, scales and metadata loaded
@@ -1149,7 +1170,9 @@ __device__ __forceinline__ void line_body(const StreamArgs& p, int G, int wgi, i
         sc[r] = meta_s[(16 * r + r16) * G + j];
       }
     }
-    if constexpr (MB <= 2 && RR <= 2) {
+    // early reads hold a whole step's fragments (16 RR + 16 MBE VGPRs) beside the accumulators
+    // (8 RR MBE): within 64 of them they fit the 128 VGPRs of a 1024-thread workgroup
+    if constexpr (MB <= 2 && 16 * RR + 16 * MBE + 8 * RR * MBE <= 64) {
       // early reads: every fragment of the step into registers, then the slot is refilled while
       // the MFMAs run
       u32x4 w[RR][2][2], a[MBE][2][2];
