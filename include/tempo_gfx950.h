@@ -116,8 +116,11 @@ size_t tempo_gemm_w8a16_workspace_bytes(const TempoW8A16Params* p);
  * the reference.  Same rows, kernels and results as tempo_gemm_w8a16_launch (bit for bit); a
  * split-K row takes its workspace from a static device array of TEMPO_NOALLOC_SCRATCH_BYTES per
  * GPU instead of the allocating pool, and a row that would need more returns
- * hipErrorOutOfMemory (2) without launching.  The current ladder never needs more: a split-K row
- * keeps tiles x splits <= 256, so its workspace is at most 256 x 128 x 256 x 4 bytes = 32 MiB.
+ * hipErrorOutOfMemory (2) without launching.  The current ladder never needs more: an
+ * interleaved split-K row keeps tiles x splits <= 256, so its workspace is at most
+ * 256 x 128 x 256 x 4 bytes = 32 MiB; a line row with k slices needs ks x M x N x 4 bytes with
+ * ks <= 8 and M <= 32, and slices only grids short of whole rounds of the part (3.75 MiB at most
+ * today, at (32, 5120, 12288)).
  * Every call on one GPU shares that GPU's array (the first call on a device looks its address
  * up): calls that overlap on one GPU -- on different streams, or from different threads without
  * ordering -- race on it.  Nothing in it needs clearing: a split-K launch writes every partial

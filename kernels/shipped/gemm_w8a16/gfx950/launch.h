@@ -182,11 +182,12 @@ inline bool line_tail_grid(const W8A16Params& p, int* nbig, int* grid, size_t* l
   const int tail = slabs - q * kLineCus * SNO;
   if (q < 1 || tail > kLineCus) return false;
   const int G = p.K / 128;
+  constexpr int TSN = EPI ? 2 : 1;  // waves of a tail workgroup (gate/up: a gate, up pair)
   const size_t L =
       p.fmt == 1 ? std::max(StreamLine<MB, R, D, 1, EPI, SN>::lds(1, G),
-                            StreamLine<MB, R, D, 1, EPI, 1>::lds(1, G))
+                            StreamLine<MB, R, D, 1, EPI, TSN>::lds(1, G))
                  : std::max(StreamLine<MB, R, D, 2, EPI, SN>::lds(1, G),
-                            StreamLine<MB, R, D, 2, EPI, 1>::lds(1, G));
+                            StreamLine<MB, R, D, 2, EPI, TSN>::lds(1, G));
   if ((size_t)(q + 1) * L > 160 * 1024 || (q + 1) * SN > 16) return false;
   *nbig = q * kLineCus;
   *grid = q * kLineCus + tail;

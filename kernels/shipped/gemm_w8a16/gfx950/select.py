@@ -135,10 +135,11 @@ LADDER_GATE_UP = [
     # two ring steps at M = 1 and M = 32 (1.05-1.08x / 1.02-1.06x four, both formats)
     (1, 0, "gl0r1n2d2", "line", dict(MB=0, R=1, D=2, SN=2, W=2048)),
     # M <= 16 / 32, wide N: the tail grid -- whole rounds of paired workgroups (SN/2 output
-    # slabs each), then one wave per remaining output slab carrying its gate and up row groups;
-    # at (17408 x 2, 5120) M = 32 1.14x / 1.05x the paired row below (41.2 / 47.0 us against
-    # 46.8 / 49.5, int8 / uint8, one process), M = 16 int8 1.04x (uint8: 0.97x, kept off)
-    (16, 12288, "gl1r1n4d2t", "line", dict(MB=1, R=1, D=2, SN=4, W=2048, TL=1, fmts=(1,))),
+    # slabs each), then one gate, up pair of waves per remaining output slab; at
+    # (17408 x 2, 5120), one process: M = 32 39.5 / 41.6 us (int8 / uint8) against 46.9 / 48.8
+    # for the paired row below, and 1.18x / 1.13x the tail grid with one wave carrying both
+    # halves of a tail slab; M = 16 36.9 / 38.9 us against 38.4 / 40.3 for the row below
+    (16, 12288, "gl1r1n4d2t", "line", dict(MB=1, R=1, D=2, SN=4, W=2048, TL=1)),
     (16, 12288, "gl1r1n4d3", "line", dict(MB=1, R=1, D=3, SN=4, W=2048)),
     (16, 0, "gl1r1n2d4", "line", dict(MB=1, R=1, D=4, SN=2, W=2048)),
     (32, 12288, "gl2r1n8d2t", "line", dict(MB=2, R=1, D=2, SN=8, W=2048, TL=1)),
@@ -218,14 +219,14 @@ def line_tail_fits(p, N, K, fmt, epi=0):
     """The tail grid (TL = 1) of the line kernel (launch.h line_tail_grid): q >= 1 whole rounds of
     SN-slab-wave workgroups, at most one remaining output slab per CU, and a CU's q workgroups
     plus one tail resident together (LDS and 16 waves).  epi = 1 (fused gate/up): SN/2 output
-    slabs per workgroup, and a tail wave carries 2R row groups (gate and up)."""
+    slabs per workgroup, and a tail workgroup is a gate, up pair of waves sharing an activation
+    ring (one wave otherwise)."""
     sno = p["SN"] // 2 if epi else p["SN"]
     slabs, rnd = N // (STREAM_N_ROWS * p["R"]), LINE_CUS * sno
     q = slabs // rnd
     if q < 1 or slabs - q * rnd > LINE_CUS or K > LINE_K_MAX:
         return False
-    lds = max(_line_lds(p, fmt, K, p["SN"]),
-              _line_lds(p, fmt, K, 1, rr=2 * p["R"] if epi else p["R"]))
+    lds = max(_line_lds(p, fmt, K, p["SN"]), _line_lds(p, fmt, K, 2 if epi else 1))
     return (q + 1) * lds <= LINE_LDS and (q + 1) * p["SN"] <= 16
 
 

@@ -57,6 +57,13 @@ GROUPS = {
     "stall": ["SQ_WAIT_ANY", "SQ_WAIT_INST_LDS", "SQ_ACTIVE_INST_ANY", "SQ_ACTIVE_INST_LDS",
               "SQ_ACTIVE_INST_VALU", "SQ_ACTIVE_INST_VMEM", "SQ_ACTIVE_INST_SCA", "SQ_INSTS_VALU",
               "GRBM_GUI_ACTIVE"],
+    # issue mix: matrix cores busy and VALU work co-issued with them, scalar and memory issue
+    "issue": ["SQ_VALU_MFMA_BUSY_CYCLES", "SQ_VALU_MFMA_COEXEC_CYCLES", "SQ_INST_CYCLES_SALU",
+              "SQ_INST_CYCLES_VMEM_RD", "SQ_ACTIVE_INST_MISC", "SQ_ACTIVE_INST_FLAT",
+              "SQ_WAVE_CYCLES", "GRBM_GUI_ACTIVE"],
+    # the CU's memory intake: cycles the texture-address and LDS queues were full
+    "fifo": ["SQ_VMEM_TA_ADDR_FIFO_FULL", "SQ_VMEM_TA_CMD_FIFO_FULL", "SQ_LDS_DATA_FIFO_FULL",
+             "SQ_LDS_CMD_FIFO_FULL", "SQ_INSTS_VMEM", "SQ_WAVE_CYCLES", "GRBM_GUI_ACTIVE"],
 }
 
 COPY_KERNEL = "__amd_rocclr_copyBuffer"

@@ -294,6 +294,60 @@ def render_counters(path: str) -> str:
     return "\n".join(lines) + "\n"
 
 
+STALL_FRACTIONS = (  # (label, counter): wave-cycle counters as fractions of SQ_WAVE_CYCLES
+    ("waiting on anything (waitcnt, barrier)", "SQ_WAIT_ANY"),
+    ("waiting to issue (dependencies, issue ports)", "SQ_WAIT_INST_ANY"),
+    ("issuing any instruction", "SQ_ACTIVE_INST_ANY"),
+    ("issuing VALU (MFMA included)", "SQ_ACTIVE_INST_VALU"),
+    ("issuing LDS", "SQ_ACTIVE_INST_LDS"),
+    ("waiting to issue LDS", "SQ_WAIT_INST_LDS"),
+    ("issuing VMEM", "SQ_ACTIVE_INST_VMEM"),
+    ("issuing FLAT", "SQ_ACTIVE_INST_FLAT"),
+    ("issuing scalar", "SQ_ACTIVE_INST_SCA"),
+    ("issuing misc (s_waitcnt, s_barrier, branches)", "SQ_ACTIVE_INST_MISC"),
+)
+
+
+def render_stalls(path: str) -> str:
+    """The stall groups of a counter step (waves, stall, issue, fifo) per shape: where the
+    wave-cycles go (each SQ wave-cycle counter over SQ_WAVE_CYCLES, both in quad-cycles summed
+    over the waves), the matrix cores' busy cycles and the VALU work co-issued with them (over
+    the busy cycles), and the cycles the CU's address / LDS queues were full per engine cycle
+    (GRBM_GUI_ACTIVE / XCDs), summed over the units that report them."""
+    from tempo.plugins.gfx950.counters import XCDS
+
+    with open(path) as f:
+        got = json.load(f)
+    out = []
+    for r in got["rows"]:
+        c = r["counters"]
+        out.append("### M=%d N=%d K=%d fmt %d, row %s (%s dispatch(es) per launch, %.1f us under "
+                   "counters)" % (r["M"], r["N"], r["K"], r["fmt"], r.get("route") or "-",
+                                  r.get("dispatches_per_launch", 1),
+                                  c.get("pmc_duration_us", float("nan"))))
+        out += ["", "| wave-cycles | fraction |", "|---|---|"]
+        wc = c.get("SQ_WAVE_CYCLES")
+        for label, name in STALL_FRACTIONS:
+            if wc and name in c:
+                out.append("| %s (%s) | %.3f |" % (label, name, c[name] / wc))
+        if "SQ_WAVES" in c:
+            out.append("| waves per dispatch | %d |" % c["SQ_WAVES"])
+        busy, coex = c.get("SQ_VALU_MFMA_BUSY_CYCLES"), c.get("SQ_VALU_MFMA_COEXEC_CYCLES")
+        if busy and coex is not None:
+            out.append("| VALU cycles co-issued with MFMA / MFMA busy cycles | %.3f |" % (coex / busy))
+        gui = c.get("GRBM_GUI_ACTIVE")
+        if gui:
+            cyc = gui / XCDS
+            for name in ("SQ_VMEM_TA_ADDR_FIFO_FULL", "SQ_VMEM_TA_CMD_FIFO_FULL",
+                         "SQ_LDS_DATA_FIFO_FULL", "SQ_LDS_CMD_FIFO_FULL", "SQ_INST_CYCLES_SALU",
+                         "SQ_INST_CYCLES_VMEM_RD"):
+                if name in c:
+                    out.append("| %s per engine cycle (summed over reporting units) | %.3f |"
+                               % (name, c[name] / cyc))
+        out.append("")
+    return "\n".join(out) + "\n"
+
+
 def measure(op: str, quick: bool = False):
     import torch
 
@@ -445,10 +499,15 @@ def main():
                     help="restrict the configuration shapes to these")
     ap.add_argument("--render", metavar="COUNTERS_JSON",
                     help="print a counter step's JSON as a markdown table (no GPU)")
+    ap.add_argument("--render-stalls", metavar="COUNTERS_JSON",
+                    help="print the stall groups of a counter step's JSON (no GPU)")
     a = ap.parse_args()
     ONLY[:] = [tuple(int(x) for x in o.split(",")) for o in a.only]
     if a.render:
         sys.stdout.write(render_counters(a.render))
+        return 0
+    if a.render_stalls:
+        sys.stdout.write(render_stalls(a.render_stalls))
         return 0
     os.makedirs(a.out, exist_ok=True)
     if a.counter_pass:

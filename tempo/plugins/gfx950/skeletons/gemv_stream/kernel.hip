@@ -1170,9 +1170,10 @@ __device__ __forceinline__ void line_body(const StreamArgs& p, int G, int wgi, i
         sc[r] = meta_s[(16 * r + r16) * G + j];
       }
     }
-    // early reads hold a whole step's fragments (16 RR + 16 MBE VGPRs) beside the accumulators
-    // (8 RR MBE): within 64 of them they fit the 128 VGPRs of a 1024-thread workgroup
-    if constexpr (MB <= 2 && 16 * RR + 16 * MBE + 8 * RR * MBE <= 64) {
+    // early reads hold a whole step's fragments (8 RR EB + 16 MBE VGPRs) beside the
+    // accumulators (8 RR MBE): within 80 of them the kernel stays inside its register budget
+    // (the fp16 form with two row groups and two activation blocks, 96, spilled)
+    if constexpr (MB <= 2 && 8 * RR * EB + 16 * MBE + 8 * RR * MBE <= 80) {
       // early reads: every fragment of the step into registers, then the slot is refilled while
       // the MFMAs run
       u32x4 w[RR][2][2], a[MBE][2][2];
@@ -1292,8 +1293,11 @@ __device__ __forceinline__ void line_body(const StreamArgs& p, int G, int wgi, i
 // TL = 1 (SN > 1, one k chunk): the grid is p.nbig workgroups of SN slab waves -- a whole number
 // of them per CU -- followed by one workgroup per remaining output slab, in which wave 0 streams
 // that slab over the whole K with its own activation ring (the body with SN = 1; for the fused
-// gate/up, EPI = 1, that wave carries the slab's gate and up row groups) and the other waves
-// leave at once.  A grid of whole rounds plus at most one such tail per CU keeps the slabs per
+// gate/up, EPI = 1, waves 0 and 1 stream its gate and up rows as a pair on a shared activation
+// ring, the body with SN = 2) and the other waves leave at once.  (A single tail wave carrying
+// both gate and up streamed twice the bytes of the other waves and set the launch's end: the
+// M = 32 gate/up row lost 4-7 % to the unfused chain with it.)  A grid of whole rounds plus at
+// most one such tail per CU keeps the slabs per
 // CU within one of each other; with workgroups of SN slabs alone, a partial last round puts
 // 2 SN slabs on some CUs and SN on others (N = 34816, SN = 4: 8 or 12).
 template <int MB, int R, int D, int BFMT, int EPI = 0, int SN = 1, int TPB = 1024, int TL = 0>
@@ -1302,10 +1306,15 @@ __global__ __launch_bounds__(TPB) void k_stream_line(StreamArgs p, int G) {
   if constexpr (TL) {
     static_assert(SN > 1, "tail workgroups: a shared activation ring in the whole rounds");
     constexpr int SNO = StreamLine<MB, R, D, BFMT, EPI, SN>::SNO;  // output slabs per workgroup
+    // tail workgroups: one output slab each, on one wave, or (gate/up) on a pair of waves, gate
+    // and up, so that a tail wave streams as many weight rows as a wave of the whole rounds.
+    // The other waves of the block leave at once; the pair's barriers wait only for the waves
+    // still running.
+    constexpr int TSN = EPI ? 2 : 1;
     const int wgi = blockIdx.x;
     if (wgi >= p.nbig) {
-      if (threadIdx.x >= 64) return;
-      line_body<MB, R, D, BFMT, EPI, 1>(p, G, p.nbig * SNO + (wgi - p.nbig), 0, dsm);
+      if (threadIdx.x >= 64 * TSN) return;
+      line_body<MB, R, D, BFMT, EPI, TSN>(p, G, p.nbig * SNO + (wgi - p.nbig), 0, dsm);
       return;
     }
   }

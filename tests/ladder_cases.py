@@ -198,7 +198,7 @@ W8 = {
 W8_GATE_UP = {
     1: [
         ("gl0r1n2d2", 1, 17408, 5120),
-        ("gl1r1n4d2t", 16, 17408, 5120),   # tail grid: 2 rounds of paired workgroups, 64 tails
+        ("gl1r1n4d2t", 16, 17408, 5120),   # tail grid: 2 rounds of paired workgroups, 64 tail pairs
         ("gl1r1n4d2t", 9, 12288, 5120),    # ragged M; whole rounds and a full tail round
         ("gl1r1n4d3", 16, 13312, 5120),    # 320 remaining slabs: past the tail grid
         ("gl1r1n2d4", 8, 7680, 3840),
@@ -216,7 +216,9 @@ W8_GATE_UP = {
     ],
     2: [
         ("gl0r1n2d2", 1, 17408, 5120),
-        ("gl1r1n4d3", 16, 17408, 5120),
+        ("gl1r1n4d2t", 16, 17408, 5120),   # tail grid: 2 rounds of paired workgroups, 64 tail pairs
+        ("gl1r1n4d2t", 9, 12288, 5120),    # ragged M; whole rounds and a full tail round
+        ("gl1r1n4d3", 16, 13312, 5120),    # 320 remaining slabs: past the tail grid
         ("gl1r1n2d4", 8, 7680, 3840),
         ("gl2r1n8d2t", 32, 17408, 5120),
         ("gl2r1n8d2t", 20, 17408, 5120),   # ragged M
