@@ -72,6 +72,7 @@ EXPORTS = {
     "tempo_gemm_fp16_gate_up_launch": ([ct.POINTER(TempoGemmParams), _p], _i),
     "tempo_gemm_w8a16_gate_up_launch": ([ct.POINTER(TempoW8A16Params), _p], _i),
     "tempo_naive_gemm_w8a16_launch": ([ct.POINTER(TempoW8A16Params), _p], _i),
+    "tempo_naive_fmha_fwd_launch": ([_p, _p, _p, _p, _p] + [_i] * 6 + [ct.c_float, _i, _p], _i),
     "tempo_gptq_repack_u8": ([_p, _p, _p, _i, _i, _i, _p, _p, _p, _p], _i),
     "tempo_gemm_fp16_workspace_bytes": ([ct.POINTER(TempoGemmParams)], ct.c_size_t),
     "tempo_gemm_w8a16_workspace_bytes": ([ct.POINTER(TempoW8A16Params)], ct.c_size_t),
@@ -357,6 +358,26 @@ def naive_gemm_fp16(A, B, C=None, stream=None):
     _check(lib().tempo_naive_gemm_fp16_launch(_ptr(A), _ptr(B), _ptr(C), M, N, K,
                                                _stream(stream)), "tempo_naive_gemm_fp16_launch")
     return C
+
+
+def naive_fmha_fwd(Q, K, V, scale: float, causal: bool = True, stream=None):
+    """The naive attention input kernel on dense BSHD tensors: Q [B,Sq,H,D], K/V [B,Sk,Hkv,D]
+    -> (O [B,Sq,H,D] fp16, LSE [B,H,Sq] fp32)."""
+    import torch
+
+    for t in (Q, K, V):
+        if t.dtype != torch.float16 or not t.is_contiguous() or t.dim() != 4:
+            raise ValueError("naive_fmha_fwd takes contiguous fp16 [B, S, heads, D] tensors")
+    B, Sq, H, D = Q.shape
+    Sk, Hkv = K.shape[1], K.shape[2]
+    if tuple(K.shape) != (B, Sk, Hkv, D) or tuple(V.shape) != tuple(K.shape):
+        raise ValueError("K and V must be [B, Sk, Hkv, D] with Q's B and D")
+    O = torch.empty_like(Q)
+    LSE = torch.empty((B, H, Sq), dtype=torch.float32, device=Q.device)
+    _check(lib().tempo_naive_fmha_fwd_launch(_ptr(Q), _ptr(K), _ptr(V), _ptr(O), _ptr(LSE), B, H,
+                                             Hkv, Sq, Sk, D, float(scale), int(bool(causal)),
+                                             _stream(stream)), "tempo_naive_fmha_fwd_launch")
+    return O, LSE
 
 
 def naive_gemm_w8a16(A, Wq, scale, zero=None, fmt: int = W8_SYM_I8, group: int = 128, C=None,

@@ -13,6 +13,7 @@
 #include "gemm_w8a16/gfx950/launch.h"
 #include "naive/gemm_fp16.hip"
 #include "naive/gemm_w8a16.hip"
+#include "naive/fmha_fwd.hip"
 #include "fmha_api.h"
 
 namespace {
@@ -228,6 +229,16 @@ int tempo_naive_gemm_w8a16_launch(const TempoW8A16Params* p, tempo_stream_t stre
       static_cast<const _Float16*>(p->A), p->Wq, static_cast<const _Float16*>(p->scale),
       static_cast<const uint8_t*>(p->zero), static_cast<_Float16*>(p->C), p->M, p->N, p->K,
       p->fmt == TEMPO_W8_ASYM_U8 ? p->group : 0, p->fmt, static_cast<hipStream_t>(stream));
+}
+
+int tempo_naive_fmha_fwd_launch(const void* Q, const void* K, const void* V, void* O, float* LSE,
+                                int B, int H, int Hkv, int Sq, int Sk, int D, float scale,
+                                int causal, tempo_stream_t stream) {
+  if (!Q || !K || !V || !O) return (int)hipErrorInvalidValue;
+  return (int)naive_fmha_fwd_launch(static_cast<const _Float16*>(Q), static_cast<const _Float16*>(K),
+                                    static_cast<const _Float16*>(V), static_cast<_Float16*>(O), LSE,
+                                    B, H, Hkv, Sq, Sk, D, scale, causal,
+                                    static_cast<hipStream_t>(stream));
 }
 
 int tempo_probe_mfma_layout(int ms, float* out, tempo_stream_t stream) {

@@ -203,6 +203,15 @@ int tempo_naive_gemm_fp16_launch(const void* A, const void* B, void* C, int M, i
  * bench/gemm_baseline.py:229. */
 int tempo_naive_gemm_w8a16_launch(const TempoW8A16Params* p, tempo_stream_t stream);
 
+/* The naive attention input kernel (kernels/naive/fmha_fwd.hip): one thread per (batch, head,
+ * query row), two fp32 passes over the visible keys; dense BSHD storage (Q, O [B][Sq][H][D];
+ * K, V [B][Sk][Hkv][D]), D <= 256, LSE optional (NULL: not written).  The "vs input" bar of
+ * tempo_fmha_fwd_launch, with the semantics it replaces (profiled/fwd_ws/fa2_sm70/csrc/
+ * attn_fwd_cutlass.cu:137,193; volta_fwd_ws.cuh:432,863,1063). */
+int tempo_naive_fmha_fwd_launch(const void* Q, const void* K, const void* V, void* O, float* LSE,
+                                int B, int H, int Hkv, int Sq, int Sk, int D, float scale,
+                                int causal, tempo_stream_t stream);
+
 /* ------------------------------------------------------------------------------------------
  * Plugin support (no reference counterpart in the C ABI; the sm70 plugin does these checks
  * from Python, tempo/plugins/sm70/tensor.py:72-86).

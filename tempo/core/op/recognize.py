@@ -31,7 +31,7 @@ from __future__ import annotations
 import re
 from dataclasses import dataclass, field
 
-from .spec import OpSpec, validate
+from .spec import DIMS, OpSpec, validate
 
 BLOCK_MAX_LINES = 40          # a declaration block longer than this is not read past its end
 _HEADER = re.compile(r"TEMPO-OP\s*:\s*([A-Za-z_]\w*)")
@@ -157,7 +157,10 @@ def build_spec(decl: Declaration, shapes: dict = None) -> OpSpec:
     given = dict(shapes or {})
     declared = {k.upper(): v for k, v in decl.get("shape", {}).items()}
     resolved = {}
-    for dim in ("M", "N", "K"):
+    if decl.kind not in DIMS:
+        raise NotRecognised("operation %r is not declared; known: %s"
+                            % (decl.kind, ", ".join(sorted(DIMS))))
+    for dim in DIMS[decl.kind]:
         value = given.get(dim, declared.get(dim))
         if value is None or str(value).strip() == "*":
             raise NotRecognised("shape %s is declared '*' (set at run time) but was not given"

@@ -51,7 +51,8 @@ class Gfx950Plugin:
             "on what a kernel may reach",
             "clock locking (Meters.clock_lock) is not offered: clocks are recorded, not set",
             "classifier.control_fields: the AMD ISA has no scheduling control words",
-            "FMHA is a fixed skeleton (skeletons/fmha_fwd), outside the searched space",
+            "the attention skeleton (skeletons/fmha_fwd) has one tile: its space holds one "
+            "hyperform per head dimension (128 or 256) and mask",
             "the fused silu(gate)*up epilogue of the interleaved prefill kernels has no split-K "
             "form: mid-M gate/up shapes with few column tiles leave CUs idle",
         )

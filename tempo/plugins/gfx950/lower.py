@@ -27,7 +27,7 @@ CAPABILITIES = frozenset({
     "lds_dma_pipeline",       # global_load_lds_dwordx4 multi-stage copies
     "xcd_aware_raster",       # block ids remapped so each XCD owns a contiguous tile run
     "decode_lds_ring",        # per-wave LDS-DMA ring for the weight-streaming regime
-    "fmha_fwd_causal_gqa",    # fixed skeleton skeletons/fmha_fwd (not searched)
+    "fmha_fwd_causal_gqa",    # attention forward: skeletons/fmha_fwd, op kind 'attention'
 })
 
 # kernel symbol, template-parameter order, and argument list, per kind: the emitter's only data
@@ -58,6 +58,12 @@ _ENTRY = {
     "shared": ("k_stream_sh", ("MB", "R", "U", "BFMT", "SN", "TPB", "EPI"), "StreamArgs",
                ("common/cdna4.h", "gemv_stream/kernel.hip")),
 }
+_ENTRY["fmha"] = ("fmha::k_fmha_fwd", ("D", "CAUSAL"),
+                  "const _Float16*, const _Float16*, const _Float16*, _Float16*, float*, int, int, "
+                  "int, int, int, float, long, long, long, long, long, long, long, long, long, long, "
+                  "long, long",
+                  ("common/cdna4.h", "fmha_fwd/kernel.hip"))
+_BOOL = {("fmha", "CAUSAL")}  # template parameters of type bool (written true / false)
 NAMESPACE = "tempo::gen"
 # compiler flags a kind needs beyond the toolchain's own; render() writes them into the source as
 # a "// tempo:flags ..." line, which the toolchain (and the library build) read back.  The
@@ -80,6 +86,13 @@ def _order(kind: str, p: dict) -> tuple:
     return tuple(names[:last + 1])
 
 
+def _targ(kind: str, name: str, value) -> str:
+    """A template argument as C++ text: bool parameters as true / false, the rest as integers."""
+    if (kind, name) in _BOOL or isinstance(value, bool):
+        return "true" if value else "false"
+    return str(int(value))
+
+
 def _p(h: Hyperform) -> dict:
     return dict(h.params)
 
@@ -89,7 +102,7 @@ class Gfx950Skeletons:
     _ACC_V1 = "fp32"
 
     def ops(self):
-        return ("gemm",)
+        return ("gemm", "attention")
 
     def axes(self):
         return space.axes()
@@ -98,6 +111,19 @@ class Gfx950Skeletons:
         return CAPABILITIES
 
     def _require_form_v1(self, op: OpSpec) -> None:
+        if op.kind == "attention":
+            # Q, K, V and O rows d-contiguous (any batch / sequence / head strides), fp16 in and
+            # out, fp32 scores and accumulation
+            if (op.dtype_a, op.dtype_b, op.dtype_c, op.dtype_acc) != ("fp16", "fp16", "fp16",
+                                                                       "fp32"):
+                raise PluginCapabilityError("gfx950 attention skeleton: fp16 Q/K/V/O, fp32 "
+                                            "accumulation; declared %s/%s/%s/%s"
+                                            % (op.dtype_a, op.dtype_b, op.dtype_c, op.dtype_acc))
+            if (op.layout_a, op.layout_b, op.layout_c) != ("d", "d", "d"):
+                raise PluginCapabilityError("gfx950 attention skeleton reads d-contiguous rows; "
+                                            "declared layouts %s/%s/%s"
+                                            % (op.layout_a, op.layout_b, op.layout_c))
+            return
         got = (op.layout_a, op.layout_b, op.layout_c)
         if got != self._LAYOUT_V1:
             raise PluginCapabilityError(
@@ -131,6 +157,13 @@ class Gfx950Skeletons:
         are the optimistic and pessimistic edges of one estimate."""
         p = _p(h)
         kind = p["kind"]
+        if kind == "fmha":
+            # O accumulators (D/2), Q fragments (D/4), one block's K and V fragments (D/4 each:
+            # the chain's reads run ahead), two score sets (32), two probability sets (16),
+            # addresses and the softmax state (~32); pessimistic edge D/8 + 16 more
+            D = p["D"]
+            regs = D // 2 + 3 * (D // 4) + 32 + 16 + 32
+            return regs, regs + D // 8 + 16, space.fmha_lds(D)
         if kind == "stream" and p.get("EPI"):
             p = dict(p, R=2 * p["R"])  # each wave carries the gate and the up row groups
         if kind in ("ilv", "ilv8"):
@@ -204,9 +237,17 @@ class Gfx950Skeletons:
 
     def launch_of(self, op: OpSpec, h: Hyperform) -> Launch:
         p = _p(h)
-        M, N = int(op.shapes["M"]), int(op.shapes["N"])
         kind = p["kind"]
         minb, bound = 1, 0
+        if kind != "fmha":
+            M, N = int(op.shapes["M"]), int(op.shapes["N"])
+        if kind == "fmha":  # one workgroup per (128 query rows, head, batch)
+            s = op.shapes
+            grid = -(-int(s["SQ"]) // p["BQ"]) * int(s["H"]) * int(s["B"])
+            _, _, lds = self.resources_of(op, h)
+            return Launch(grid_ctas=grid, threads=64 * p["WAVES"], smem_bytes=lds,
+                          entry=self.entry_probe(h), min_ctas_per_sm=1,
+                          bound_threads=64 * p["WAVES"])
         if kind in ("dma", "reg", "ilv", "ilv8"):
             grid = (-(-M // p["BM"]) * (N // p["BN"])
                     * space.splits_of(kind, p, M, N, int(op.shapes["K"])))
@@ -243,7 +284,8 @@ class Gfx950Skeletons:
         CU replays it (k-tiles x rounds of resident workgroups)."""
         p = _p(h)
         kind = p["kind"]
-        M, N, K = int(op.shapes["M"]), int(op.shapes["N"]), int(op.shapes["K"])
+        if kind != "fmha":
+            M, N, K = int(op.shapes["M"]), int(op.shapes["N"]), int(op.shapes["K"])
         regs, _, lds = self.resources_of(op, h)
         lau = self.launch_of(op, h)
         occ = _RES.occupancy(min(regs, _RES.declared_budget(lau.threads, lau.min_ctas_per_sm,
@@ -254,6 +296,8 @@ class Gfx950Skeletons:
         # ceil(grid / CUs) workgroups, and its per-wave load counts that many times, not per_cu
         fill = min(per_cu, -(-lau.grid_ctas // int(_M.rate("GEOM.SMS").value))) / per_cu
         atoms = []
+        if kind == "fmha":
+            return self._fmha_atoms(op, p, lau, occ, rounds, fill)
         if kind in ("dma", "reg", "ilv", "ilv8"):
             ms = p.get("MS", 32) if kind not in ("ilv", "ilv8") else 16
             tm, tn = p["BM"] // p["WM"] // ms, p["BN"] // p["WN"] // ms
@@ -315,6 +359,42 @@ class Gfx950Skeletons:
                           latency=_M.rate("LATENCY.VMEM").value))
         return atoms
 
+    def _fmha_atoms(self, op: OpSpec, p: dict, lau, occ, rounds, fill):
+        """Per-wave load of the attention skeleton: per 32-key block a wave runs the scores
+        (32 x 32 x D) and P.V (32 x D x 32) on the matrix cores, reads that block's K and V from
+        LDS (32 x D x 2 bytes each), and issues a quarter of the block's K and V copies; a
+        workgroup walks the key blocks its 128 query rows see (with the causal mask, about the
+        mean visible keys of a row plus the half block of its diagonal)."""
+        from tempo.core.op.spec import visible_pairs
+
+        s = op.shapes
+        D, BKV = p["D"], p["BKV"]
+        sq, sk = int(s["SQ"]), int(s["SK"])
+        mean_keys = visible_pairs(sq, sk, int(s["CAUSAL"])) / sq
+        blocks = min(-(-sk // BKV), -(-int(mean_keys + p["BQ"] / 2) // BKV))
+        reps = blocks * rounds * fill
+        flops = 4 * BKV * 32 * D  # scores + P.V of one block for the wave's 32 query rows
+        lds_rd = 2 * BKV * D * 2
+        vmem = 2 * BKV * D * 2 // p["WAVES"]
+        hbm = (2 * int(s["B"]) * sq * int(s["H"]) * D * 2
+               + 2 * int(s["B"]) * sk * int(s["HKV"]) * D * 2)
+        cus = int(_M.rate("GEOM.SMS").value)
+        return [
+            Atom(uid=0, kind=AtomKind.COMPUTE, op_id="v_mfma x%d" % (flops // 32768),
+                 footprint={"MFMA": float(flops * reps)}, latency=_M.rate("LATENCY.MFMA32").value),
+            Atom(uid=1, kind=AtomKind.MEM_READ, op_id="ds_read_b128 / ds_read_b64_tr_b16",
+                 footprint={"LDS": float(lds_rd * reps)}, latency=_M.rate("LATENCY.LDS").value),
+            Atom(uid=2, kind=AtomKind.XFER_ISSUE, op_id="buffer_load_dwordx4 lds",
+                 footprint={"VMEM": float(vmem * reps)}, latency=_M.rate("LATENCY.VMEM").value,
+                 token="copy"),
+            Atom(uid=3, kind=AtomKind.XFER_WAIT, op_id="s_waitcnt vmcnt", footprint={},
+                 token="copy"),
+            Atom(uid=4, kind=AtomKind.BARRIER, op_id="s_barrier", footprint={}),
+            Atom(uid=5, kind=AtomKind.MEM_READ, op_id="HBM (device share)",
+                 footprint={"HBM": float(hbm) / (cus * max(1, occ.warps_per_sm))},
+                 latency=_M.rate("LATENCY.VMEM").value),
+        ]
+
     # -- emission ------------------------------------------------------------------------------
     def render(self, op: OpSpec, h: Hyperform) -> Rendered:
         self._require_form_v1(op)
@@ -328,15 +408,16 @@ class Gfx950Skeletons:
         for f in files:
             with open(os.path.join(SKEL, f), encoding="utf-8") as fh:
                 body.append("// ===== %s =====\n%s\n" % (f, fh.read()))
-        head = ("// GENERATED by tempo: plugin gfx950, hyperform %s, operation %s %sx%sx%s.\n"
-                % (h.key, op.kind, op.shapes.get("M"), op.shapes.get("N"), op.shapes.get("K")))
+        head = ("// GENERATED by tempo: plugin gfx950, hyperform %s, operation %s %s.\n"
+                % (h.key, op.kind, " ".join("%s=%s" % kv for kv in sorted(op.shapes.items()))))
         if kind in KIND_FLAGS:
             head += "// tempo:flags %s\n" % " ".join(KIND_FLAGS[kind])
         head += ("#include <hip/hip_runtime.h>\n#include <stdint.h>\n\nnamespace tempo {\n"
                  "namespace gen {\n\n")
         inst = ("\n// explicit instantiation: the one kernel this file exists to contain\n"
                 "template __global__ void %s<%s>(%s);\n"
-                % (sym, ", ".join(str(int(p.get(k, _DEFAULT.get(k, 0)))) for k in order), args))
+                % (sym, ", ".join(_targ(kind, k, p.get(k, _DEFAULT.get(k, 0))) for k in order),
+                   args))
         src = head + "".join(body) + inst + "\n}  // namespace gen\n}  // namespace tempo\n"
         return Rendered(source=src, launch=self.launch_of(op, h), includes=(),
                         notes="namespace wrap + one explicit instantiation; logic lives in the skeleton",
@@ -347,8 +428,5 @@ class Gfx950Skeletons:
         p = _p(h)
         sym = _ENTRY[p["kind"]][0]
         order = _order(p["kind"], p)
-        vals = []
-        for k in order:
-            v = p.get(k, _DEFAULT.get(k, 0))
-            vals.append("true" if v is True else "false" if v is False else str(int(v)))
+        vals = [_targ(p["kind"], k, p.get(k, _DEFAULT.get(k, 0))) for k in order]
         return "%s::%s<%s>" % (NAMESPACE, sym, ", ".join(vals))

@@ -12,6 +12,8 @@ The skeleton kinds, each a kernel family of tempo/plugins/gfx950/skeletons:
                                     LDS-DMA into per-wave rings, fragments read back swizzled;
                                     with row tiles (MT = 1) also 32 < M <= 128, 8-bit weights
   ring    gemv_stream/k_stream_dma  decode (M <= 32): per-wave LDS-DMA ring of k-steps
+  fmha    fmha_fwd/k_fmha_fwd       attention forward (op kind 'attention'), one hyperform per
+                                    head dimension and mask (fixed 128-row / 32-key tile)
   stream  gemv_stream/k_stream      decode, register-staged prefetch (kept as a measured arm)
 
 Legality here means "compiles and launches": LDS within 160 KiB, tiles divide the shape, the
@@ -289,6 +291,8 @@ def tag(kind: str, p: dict) -> str:
     if kind == "reg":
         return "reg_m%dn%dk%d_w%dx%d_f%d_z%d_b%d" % (p["BM"], p["BN"], p["BK"], p["WM"], p["WN"],
                                                    p["MS"], p["SWZ"], p["BFMT"])
+    if kind == "fmha":
+        return "fmha_d%d_c%d_q%d_kv%d_w%d" % (p["D"], p["CAUSAL"], p["BQ"], p["BKV"], p["WAVES"])
     if kind == "line" and p.get("MT"):
         return "line_mb%d_r%d_d%d_mt%d_b%d" % (p["MB"], p["R"], p["D"], p["S"], p["BFMT"])
     if kind == "line":
@@ -443,10 +447,37 @@ def _with_split(p: dict, sw: int) -> dict:
     return p
 
 
+# The attention skeleton (fmha_fwd/k_fmha_fwd): its tile is fixed by its design -- 4 waves of 32
+# query rows (128 per workgroup), 32-key blocks, four LDS slots per operand -- so one hyperform
+# per (head dimension, mask) is what the space holds; D 128 or 256 (the skeleton's two forms).
+FMHA_TILE = dict(BQ=128, BKV=32, WAVES=4)
+FMHA_D = (128, 256)
+
+
+def attention_variants(op: OpSpec) -> Iterator[Hyperform]:
+    D, causal = int(op.shapes["D"]), int(op.shapes["CAUSAL"])
+    if D not in FMHA_D:
+        raise PluginCapabilityError("gfx950 attention skeleton takes head dimension %s; declared "
+                                    "D = %d" % (" or ".join(map(str, FMHA_D)), D))
+    p = dict(kind="fmha", D=D, CAUSAL=causal, **FMHA_TILE)
+    yield Hyperform(plugin="gfx950", params=p, key=tag("fmha", p))
+
+
+def fmha_lds(D: int) -> int:
+    """LDS of one workgroup of the attention skeleton: four K and four V slots of 32 keys x D."""
+    return 8 * FMHA_TILE["BKV"] * D * 2
+
+
 def variants(op: OpSpec) -> Iterator[Hyperform]:
+    if op.kind == "attention":
+        return attention_variants(op)
     if op.kind != "gemm":
-        raise PluginCapabilityError("gfx950 skeletons take 'gemm' in the pipeline; FMHA is a "
-                                    "fixed skeleton (skeletons/fmha_fwd), not a searched one")
+        raise PluginCapabilityError("gfx950 skeletons take 'gemm' and 'attention'; declared %r"
+                                    % op.kind)
+    return _gemm_variants(op)
+
+
+def _gemm_variants(op: OpSpec) -> Iterator[Hyperform]:
     M, N, K = int(op.shapes["M"]), int(op.shapes["N"]), int(op.shapes["K"])
     b = bfmt(op)
     out = []

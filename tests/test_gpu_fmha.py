@@ -143,3 +143,34 @@ def test_fmha_refuses_uncovered_head_dim(gpu):
     Q, K, V = _inputs(1, 64, 64, 2, 2, 64, seed=3)
     with pytest.raises(capi.NotCovered):
         _run(Q, K, V, 0.125, True, gpu)
+
+
+NAIVE_CASES = [c for c in CASES if c[1] * c[3] <= 1200]  # the naive kernel is one thread per row
+
+
+@pytest.mark.parametrize("case", NAIVE_CASES, ids=lambda c: "b%d_q%d_k%d_h%d_kv%d_d%d_%s" % (
+    c[0], c[1], c[2], c[3], c[4], c[5], "causal" if c[6] else "full"))
+def test_naive_attention_input_against_oracle_and_shipped(gpu, case):
+    """The naive attention input (kernels/naive/fmha_fwd.hip, the operation's declaration and
+    "vs input" bar) against the oracle, and the shipped kernel against it."""
+    import torch
+    from cuda_tempiler_amd import capi
+
+    B, Sq, Sk, H, Hkv, D, causal = case
+    say("naive fmha case", case)
+    Q, K, V = _inputs(B, Sq, Sk, H, Hkv, D, seed=2000 + Sq + Sk + D)
+    scale = 1.0 / np.sqrt(D)
+    On, Ln = capi.naive_fmha_fwd(dev(Q, gpu), dev(K, gpu), dev(V, gpu), scale, causal)
+    torch.cuda.synchronize()
+    naive, lnaive = host(On), host(Ln)
+    ref, lref = O.fmha_fwd(Q, K, V, scale, causal)
+    r = O.rel_l2(naive, ref)
+    say("  naive relL2 vs oracle %.3e" % r)
+    assert r <= TOL
+    inf = ~np.isfinite(lref)
+    assert np.array_equal(inf, ~np.isfinite(lnaive))
+    assert np.max(np.abs(lnaive[~inf] - lref[~inf]), initial=0.0) <= LSE_TOL
+    got, _ = _run(Q, K, V, scale, causal, gpu)
+    r2 = O.rel_l2(got, naive)
+    say("  shipped relL2 vs naive %.3e" % r2)
+    assert r2 <= TOL
