@@ -146,6 +146,17 @@ class Gfx950Plugin:
             r.check("layout b=n is refused structurally", type(e).__name__ == "PluginCapabilityError")
         src = self.skeletons.render(op, hs[0]).source
         r.check("render emits one explicit instantiation", src.count("template __global__") == 1)
+        # the attention skeleton: one hyperform per head dimension and mask, rendered as the
+        # shipped kernel's instantiation
+        att = OpSpec(kind="attention", dtype_a="fp16", dtype_b="fp16", dtype_c="fp16",
+                     dtype_acc="fp32", layout_a="d", layout_b="d", layout_c="d",
+                     shapes={"B": 1, "H": 16, "HKV": 8, "SQ": 4096, "SK": 4096, "D": 256,
+                             "CAUSAL": 1}, tol_rel_l2=3e-3)
+        ah = list(self.skeletons.variants(att))
+        r.check("attention (C5) has one hyperform", len(ah) == 1, ",".join(h.key for h in ah))
+        asrc = self.skeletons.render(att, ah[0]).source
+        r.check("attention renders fmha::k_fmha_fwd<256, true>",
+                "template __global__ void fmha::k_fmha_fwd<256, true>(" in asrc)
         return r
 
 
