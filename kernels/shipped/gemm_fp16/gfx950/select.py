@@ -27,9 +27,11 @@ ARCH = "gfx950"
 LADDER = [
     # M = 1, long K: a two-step ring (1.05x three steps at (1, 3840, 15360))
     (1, 0, "l0r1d2", "line", dict(MB=0, R=1, D=2, W=1024, KMIN=12288)),
-    (1, 0, "l0r1d3", "line", dict(MB=0, R=1, D=3, W=2048)),
+    # two ring steps (1.03x three at (1, 15360, 3840))
+    (1, 0, "l0r1d2w", "line", dict(MB=0, R=1, D=2, W=2048)),
     (1, 0, "s1a_r1u4", "stream", dict(MB=1, R=1, U=4, A=1)),
-    (16, 12288, "l1r1n4d3", "line", dict(MB=1, R=1, D=3, SN=4, W=2048)),
+    # four ring steps (1.07x three at M = 8 and 16, (15360, 3840))
+    (16, 12288, "l1r1n4d4", "line", dict(MB=1, R=1, D=4, SN=4, W=2048)),
     # narrow N, long K: k slices across workgroups (KS, fp32 partials reduced in slice order)
     # spread the 60 four-slab workgroups of N = 3840 over the part (1.10x the row below at
     # (16, 3840, 15360); 0.99x at M = 8)
@@ -38,8 +40,9 @@ LADDER = [
     (16, 0, "s16r1u4", "stream", dict(MB=1, R=1, U=4, A=0)),
     # four ring stages (1.08-1.12x three at M = 24-32, N = 12288-15360)
     (32, 12288, "l2r1n4d4", "line", dict(MB=2, R=1, D=4, SN=4, W=2048)),
-    # k slices as above (1.28x the row below at (32, 3840, 15360))
-    (32, 0, "l2r1n4d3k8", "line", dict(MB=2, R=1, D=3, SN=4, W=2048, KS=8, KMIN=12288)),
+    # k slices as above (1.28x the row below at (32, 3840, 15360)), four ring steps (1.07x /
+    # 1.07x / 1.09x three at M = 24 / 32 (K = 15360) and M = 32 (K = 12288), N = 3840)
+    (32, 0, "l2r1n4d4k8", "line", dict(MB=2, R=1, D=4, SN=4, W=2048, KS=8, KMIN=12288)),
     (32, 0, "l2r1d4", "line", dict(MB=2, R=1, D=4, W=2048)),
     (32, 0, "s32r1u4", "stream", dict(MB=2, R=1, U=4, A=0)),
     (64, 12288, "l4r1n4d3", "line", dict(MB=4, R=1, D=3, SN=4, W=2048)),

@@ -25,11 +25,10 @@ LADDER = [
     (1, 4096, "l0r1n2d2", "line", dict(MB=0, R=1, D=2, SN=2, W=2048, NMAX=6145)),
     # M = 1, narrow N: two ring steps (1.24x four at (1, 1024, 5120))
     (1, 0, "l0r1d2", "line", dict(MB=0, R=1, D=2, W=2048, NMAX=4096)),
-    # M = 1, wide N: two ring steps where a CU holds 4+ slab waves (8.5 at N = 34816), so two
-    # steps per wave already keep ~35 KiB per CU in flight; 1.06x / 1.02x the four-step row at
-    # (1, 34816, 5120), int8 / uint8 (29.5 / 33.2 us against 31.3 / 33.9, one process, settled)
-    (1, 16384, "l0r1d2w", "line", dict(MB=0, R=1, D=2, W=2048)),
-    (1, 0, "l0r1d4", "line", dict(MB=0, R=1, D=4, W=2048)),
+    # M = 1, wider N: two ring steps; where a CU holds 4+ slab waves (8.5 at N = 34816) two steps
+    # per wave already keep ~35 KiB per CU in flight.  1.06x / 1.02x the four-step row it
+    # replaced at (1, 34816, 5120) and 1.10x / 1.05x at (1, 7168, 5120), int8 / uint8
+    (1, 0, "l0r1d2w", "line", dict(MB=0, R=1, D=2, W=2048)),
     # M <= 16 / 32, wide N: the tail grid -- whole rounds of 4- / 8-slab workgroups (one ring of
     # activations each) and one single-wave workgroup per remaining slab, so the slabs per CU
     # differ by at most one (1.10-1.19x / 1.29-1.31x the rows after them at (34816, 5120))

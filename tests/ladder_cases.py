@@ -15,10 +15,10 @@ The pattern is the reference's dispatch consistency gate
 
 FP16 = [
     ("l0r1d2", 1, 3840, 15360),
-    ("l0r1d3", 1, 15360, 3840),
+    ("l0r1d2w", 1, 15360, 3840),
     ("s1a_r1u4", 1, 512, 65792),
-    ("l1r1n4d3", 8, 15360, 3840),
-    ("l1r1n4d3", 16, 15360, 3840),          # the C2 point M = 16: the row's whole 16-row M tile
+    ("l1r1n4d4", 8, 15360, 3840),
+    ("l1r1n4d4", 16, 15360, 3840),          # the C2 point M = 16: the row's whole 16-row M tile
     ("l1r1n4d4k8", 16, 3840, 15360),        # 60 workgroups x 8 k slices
     ("l1r1n4d4k8", 8, 3840, 15360),         # the C2 point M = 8, N = 3840
     ("l1r1n4d4k8", 5, 3840, 12288),         # ragged M, 12 steps per slice
@@ -26,8 +26,8 @@ FP16 = [
     ("l1r1d4", 16, 3840, 3840),
     ("s16r1u4", 16, 512, 65792),
     ("l2r1n4d4", 24, 15360, 3840),
-    ("l2r1n4d3k8", 32, 3840, 15360),
-    ("l2r1n4d3k8", 20, 3840, 12288),
+    ("l2r1n4d4k8", 32, 3840, 15360),
+    ("l2r1n4d4k8", 20, 3840, 12288),
     ("l2r1d4", 32, 3840, 3840),
     ("s32r1u4", 32, 512, 65792),
     ("l4r1n4d3", 64, 15360, 3840),
@@ -83,7 +83,7 @@ W8 = {
         ("l0r1d2k8", 1, 4096, 16384),     # 256 slabs: no slices (no workspace)
         ("l0r1n2d2", 1, 5120, 6144),
         ("l0r1d2", 1, 1024, 5120),
-        ("l0r1d4", 1, 7168, 5120),
+        ("l0r1d2w", 1, 7168, 5120),
         ("l0r1d2w", 1, 34816, 5120),      # the C3/C4 decode point M = 1, N = 34816
         ("l1r1n4d2t", 16, 34816, 5120),
         ("l1r1n4d2t", 16, 16400, 256),    # one remaining slab
@@ -140,7 +140,7 @@ W8 = {
         ("l0r1d2k8", 1, 4096, 16384),
         ("l0r1n2d2", 1, 5120, 5120),
         ("l0r1d2", 1, 1024, 5120),
-        ("l0r1d4", 1, 7168, 5120),
+        ("l0r1d2w", 1, 7168, 5120),
         ("l0r1d2w", 1, 34816, 5120),      # the C3/C4 decode point M = 1, N = 34816
         ("l1r1n4d2t", 16, 34816, 5120),
         ("l1r1n4d2t", 16, 16400, 256),    # one remaining slab

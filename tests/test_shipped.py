@@ -165,7 +165,7 @@ def test_route_unknown_op_is_empty():
 def test_rows_fall_through_when_the_first_row_does_not_fit():
     from cuda_tempiler_amd import capi
 
-    assert capi.route(0, 8, 15360, 3840) == "l1r1n4d3"
+    assert capi.route(0, 8, 15360, 3840) == "l1r1n4d4"
     assert capi.route(0, 8, 12304, 3840) == "l1r1d4"      # N % 64 != 0: the unshared line row
     assert capi.route(0, 8, 15360, 65792) == "s16r1u4"    # K > 65536: past the line rows
     assert capi.route(1, 16, 34816, 5120) == "l1r1n4d2t"
@@ -178,12 +178,12 @@ def test_rows_fall_through_when_the_first_row_does_not_fit():
     assert capi.route(1, 32, 34816, 5120) == "l2r1n8d2t"
     assert capi.route(2, 32, 34816, 16384) == "l2r1n4d4"  # fmt 2 metadata: not co-resident
     assert capi.route(2, 32, 34816, 65536 + 256) == "h32r1u4n2"
-    assert capi.route(0, 1, 15360, 3840) == "l0r1d3"
+    assert capi.route(0, 1, 15360, 3840) == "l0r1d2w"
     assert capi.route(0, 1, 3840, 15360) == "l0r1d2"    # long K
     assert capi.route(1, 1, 5120, 5120) == "l0r1n2d2"
     assert capi.route(2, 1, 5120, 5120) == "l0r1n2d2"
     assert capi.route(1, 1, 5120, 17408) == "l0r1d2k8"  # long K: k slices
-    assert capi.route(1, 1, 7168, 5120) == "l0r1d4"     # past its N band
+    assert capi.route(1, 1, 7168, 5120) == "l0r1d2w"    # past the narrow row's N band
     assert capi.route(1, 1, 1024, 5120) == "l0r1d2"     # narrow N
     assert capi.route(1, 1, 5120, 65536 + 512) == "s1a_r1u8"
     assert capi.route(1, 1, 5120, 65536 + 256) == "s1a_r1u4"   # K % 512 != 0, K % 256 == 0
