@@ -114,6 +114,8 @@ def condition(sel, kind, p, m_max, n_min=0, gate_up=False):
             fit += " && p.K < %d" % p["KMAX"]
         if p.get("TAIL") == 2:  # fits only where N splits in two
             fit += " && (ilv8_tail_cols<%d,%d>(p) > 0)" % (p["BM"], p["BN"])
+        if p.get("FILL"):  # one round of its tiles, more of them than 256-row tiles give
+            fit += " && (ilv8_fill_fits<%d,%d>(p))" % (p["BM"], p["BN"])
     else:
         fit = "(p.N %% %d) == 0 && (p.K %% %d) == 0" % (p["BN"], p["BK"])
         if "NMAX" in p:

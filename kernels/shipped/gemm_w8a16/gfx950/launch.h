@@ -351,6 +351,14 @@ inline int ilv8_tail_cols(const W8A16Params& p) {
   if (whole == 0 || whole % nm || whole / nm == nn || 4 * (tiles - whole) > CUS) return 0;
   return whole / nm * BN;
 }
+// A FILL row: its BM x BN grid is one round of the part and holds more tiles than 256-row tiles
+// would (select.py fill_fits).
+template <int BM, int BN>
+inline bool ilv8_fill_fits(const W8A16Params& p) {
+  constexpr int CUS = 256;
+  const int nm = (p.M + BM - 1) / BM;
+  return nm * (p.N / BN) <= CUS && nm > (p.M + 255) / 256;
+}
 // The same kernel with the fused gate/up epilogue (p.N the output width, 2N weight rows), and
 // that row with the output columns in two parts.
 template <int BM, int BN, int BK, int WM, int WN, int STAGES, int GROUP, int XCD, int RSP>

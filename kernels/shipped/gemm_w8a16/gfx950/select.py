@@ -115,6 +115,13 @@ LADDER = [
     # 128-k)
     (1 << 30, 0, "m128x128k64s16", "mfma",
      dict(BM=128, BN=128, BK=64, WM=2, WN=2, MS=16, SWZ=1, GROUP=8, XCD=1, NMAX=2048, fmts=(1,))),
+    # FILL: where one round of 192 x 256 tiles holds the whole grid and has more tiles than the
+    # 256 x 256 grid (220 against 160 tiles at (2048, 5120)), the 192-row tiles fill more of the
+    # part: 1.05-1.10x the row below at (2048, 5120, 5120 | 6144 | 17408) in both formats,
+    # 1.07-1.26x at M = 512-1536 (variant driver, paired rounds); a 192-row tile's M past the
+    # last row is predicated like any other
+    (1 << 30, 0, "i8x192x256w1x4k64s3f", "ilv8",
+     dict(BM=192, BN=256, BK=64, WM=1, WN=4, STAGES=3, GROUP=8, XCD=1, RSP=8, FILL=1)),
     # TAIL: where the last round of 256 x 256 tiles is at most a quarter full (four rounds and
     # 64 tiles at (2048, 34816)), the columns of the whole rounds run on these tiles and the rest
     # of N on ILV8_TAIL_TILE tiles, one round of their own; any other grid runs this row plain
@@ -246,6 +253,13 @@ def _fits_gate_up(kind, p, M, N, K, fmt=1):
     return _fits(kind, p, M, N, K, fmt)
 
 
+def fill_fits(M, N, BM, BN, cus=LINE_CUS):
+    """A FILL row: its BM x BN grid is one round of the part and holds more tiles than the grid
+    of 256 x BN tiles would -- ilv8_fill_fits of launch.h."""
+    nm = -(-M // BM)
+    return nm * (N // BN) <= cus and nm > -(-M // 256)
+
+
 def ilv_ld_max(p):
     """Largest leading dimension the interleaved int8 kernel takes: its copies address a 256-row
     panel with 31-bit byte offsets (A rows are fp16)."""
@@ -257,7 +271,8 @@ def _fits(kind, p, M, N, K, fmt=1):
         return (N % p["BN"] == 0 and K % 128 == 0 and K <= ilv_ld_max(p)
                 and N < p.get("NMAX", 1 << 30) and K >= p.get("KMIN", 0)
                 and K < p.get("KMAX", 1 << 30)
-                and (p.get("TAIL") != 2 or tail_split(M, N, p["BM"], p["BN"]) > 0))
+                and (p.get("TAIL") != 2 or tail_split(M, N, p["BM"], p["BN"]) > 0)
+                and (not p.get("FILL") or fill_fits(M, N, p["BM"], p["BN"])))
     if kind == "line" and p.get("TL"):  # tail grid: whole slabs, one k chunk
         return (N % (STREAM_N_ROWS * p["R"]) == 0 and K % LINE_K_STEP == 0
                 and line_tail_fits(p, N, K, fmt))

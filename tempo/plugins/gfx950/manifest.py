@@ -74,7 +74,8 @@ def hyper_params(kind, p, fmt, epi=0):
     same kernel, named the way space.variants() names it."""
     pk = {"stream": "stream", "mfma": "reg", "dma": "dma", "shared": "shared", "ilv": "ilv",
           "ilv8": "ilv8", "line": "line"}[kind]
-    params = {k: v for k, v in p.items() if k not in ("fmts", "NMAX", "KMIN", "KMAX")}
+    # NMAX / KMIN / KMAX / FILL are the row's dispatch conditions, not kernel parameters
+    params = {k: v for k, v in p.items() if k not in ("fmts", "NMAX", "KMIN", "KMAX", "FILL")}
     params["kind"] = pk
     if pk == "shared":
         params.setdefault("TPB", 1024)

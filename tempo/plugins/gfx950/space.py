@@ -47,8 +47,8 @@ DOMAINS = {
     "ilv": dict(BM=(64, 128, 256), BN=(128, 192, 256), BK=(32, 64), STAGES=(2, 3, 4),
                 GROUP=(4, 8, 16), XCD=(0, 1), WAVES=((2, 2), (2, 4), (4, 2), (1, 4)),
                 RSP=(0, 8, 12), SW=(0, 128, 256, 512)),
-    "ilv8": dict(TILES=((256, 256, 2, 2), (256, 256, 1, 4), (128, 256, 1, 4), (128, 128, 2, 2),
-                        (128, 128, 1, 4)),
+    "ilv8": dict(TILES=((256, 256, 2, 2), (256, 256, 1, 4), (192, 256, 1, 4), (128, 256, 1, 4),
+                        (128, 128, 2, 2), (128, 128, 1, 4)),
                  BK=(64, 128),
                  STAGES=(2, 3, 4),
                  GROUP=(4, 8, 16), XCD=(0, 1), RSP=(4, 8, 12), SW=(0, 128, 256, 512)),
@@ -333,12 +333,13 @@ def legal(kind: str, p: dict, M: int, N: int, K: int):
         return None
     if kind == "ilv8":
         BM, BN, BK, WM, WN = p["BM"], p["BN"], p["BK"], p["WM"], p["WN"]
-        if (BM, BN, BK, WM, WN) not in ((256, 256, 64, 2, 2), (256, 256, 64, 1, 4), (128, 256, 64, 1, 4),
-                                        (128, 128, 64, 2, 2), (128, 256, 128, 1, 4),
-                                        (128, 128, 128, 2, 2), (128, 128, 128, 1, 4)):
-            return ("the int8 interleaved kernel takes 256 x 256 (2 x 2 waves), 128 x 256 "
-                    "(1 x 4 waves) or 128 x 128 (2 x 2 waves) tiles of 64 k, and the last two "
-                    "also of 128 k")
+        if (BM, BN, BK, WM, WN) not in ((256, 256, 64, 2, 2), (256, 256, 64, 1, 4), (192, 256, 64, 1, 4),
+                                        (128, 256, 64, 1, 4), (128, 128, 64, 2, 2),
+                                        (128, 256, 128, 1, 4), (128, 128, 128, 2, 2),
+                                        (128, 128, 128, 1, 4)):
+            return ("the int8 interleaved kernel takes 256 x 256 (2 x 2 waves), 192 x 256 and "
+                    "128 x 256 (1 x 4 waves) or 128 x 128 (2 x 2 waves) tiles of 64 k, and the "
+                    "last two also of 128 k")
         if p["BFMT"] not in (1, 2):
             return "weights must be int8 (fmt 1) or uint8 group-128 (fmt 2)"
         if N % BN or K % 128:

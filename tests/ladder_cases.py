@@ -130,6 +130,8 @@ W8 = {
         ("i8x128x128w1x4k128s2w256", 2048, 1024, 5120),
         ("i8x128x128w1x4k128s2w256", 2049, 1024, 5120),
         ("m128x128k64s16", 2048, 1152, 5184),
+        ("i8x192x256w1x4k64s3f", 2048, 5120, 1024),   # 11 x 20 tiles, the last tile row 128 rows
+        ("i8x192x256w1x4k64s3f", 500, 5120, 640),     # 3 tile rows, the last 116 rows
         ("i8x256w1x4k64s3t", 2048, 7168, 5120),
         ("i8x256w1x4k64s3t", 512, 34816, 1024),   # N in two parts: 256 tiles, then 16 in 128 x 128
         ("i8x256w1x4k64s3t", 500, 34816, 1024),
@@ -189,6 +191,8 @@ W8 = {
         ("i8x128x128w1x4k128s2w256", 2048, 1024, 5120),
         ("i8x128x128w1x4k128s2w256", 2049, 1024, 5120),
         ("i8x128x128w1x4k128s2w256", 2048, 1152, 5120),
+        ("i8x192x256w1x4k64s3f", 2048, 5120, 1024),
+        ("i8x192x256w1x4k64s3f", 700, 5120, 1024),    # 4 tile rows, the last 124 rows
         ("i8x256w1x4k64s3t", 2048, 7168, 5120),
         ("i8x256w1x4k64s3t", 512, 34816, 1024),   # N in two parts
         ("i8x256w1x4k64s3t", 300, 34816, 1024),

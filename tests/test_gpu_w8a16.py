@@ -137,13 +137,23 @@ def test_w8a16_parity_prefill(gpu, fmt, NK):
 
 @pytest.mark.parametrize("fmt", [1, 2])
 @pytest.mark.parametrize("M, N, K", [(2049, 2048, 5120), (512, 5120, 17408), (2048, 2048, 5184),
-                                     (2049, 1024, 5120), (300, 1792, 5120)])
+                                     (2049, 1024, 5120), (300, 1792, 5120), (2049, 7168, 1024)])
 def test_w8a16_parity_interleaved_prefill_rows(gpu, fmt, M, N, K):
     """The interleaved int8 prefill kernel: a ragged last tile row (M = 2049), a long k loop
     (K = 17408), and K % 128 != 0, which it does not take (fmt 1: the register-staged row runs;
     fmt 2 needs whole 128-k groups, so the shape is not covered at all).  Narrow N (< 2048)
     takes the 128 x 128 split-K row of the same kernel on 128-k tiles instead, ragged M
-    included."""
+    included.  Wider N takes 192 x 256 tiles where one round of them holds the grid with more
+    tiles than 256 x 256 ones (the FILL row: (2049, 2048), (512, 5120)), else 256 x 256 tiles
+    ((2049, 7168): 308 tiles of 192 rows would need a second round)."""
+    import importlib.util
+    import os
+
+    path = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "kernels",
+                        "shipped", "gemm_w8a16", "gfx950", "select.py")
+    spec = importlib.util.spec_from_file_location("select_w8_prefill_rows", path)
+    sel = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(sel)
     route = _route(fmt, M, N, K)
     say("w8a16 fmt", fmt, "M", M, "N", N, "K", K, "route", route)
     if K % 128:
@@ -153,7 +163,8 @@ def test_w8a16_parity_interleaved_prefill_rows(gpu, fmt, M, N, K):
     elif N < 2048:
         assert route == "i8x128x128w1x4k128s2w256"
     else:
-        assert route == "i8x256w1x4k64s3t"
+        assert route == ("i8x192x256w1x4k64s3f" if sel.fill_fits(M, N, 192, 256)
+                         else "i8x256w1x4k64s3t")
     A = O.randn_f16((M, K), 13, K ** -0.5)
     q, s, z = make_weights(N, K, fmt, 79)
     C = _run(A, q, s, z, fmt, gpu)
