@@ -248,3 +248,20 @@ def test_tail_rule_of_the_two_part_row():
     assert sel.tail_split(2048, 7168) == 0        # 224 tiles
     assert sel.tail_split(4096, 34816) == 0       # 2176 tiles: the last round half full
     assert sel.tail_split(2048, 32768) == 0       # 1024 tiles: whole rounds only
+
+
+def test_fill_rule_of_the_192_row_tiles():
+    """The W8A16 FILL row (192 x 256 tiles) takes a grid only where one round of its tiles holds
+    it and it has more tiles than 256 x 256 tiles would (select.fill_fits mirrors
+    ilv8_fill_fits of launch.h; the compiled-route sweep above checks the two agree)."""
+    sel = _select("gemm_w8a16")
+    assert sel.fill_fits(2048, 5120, 192, 256)       # 220 tiles against 160
+    assert sel.fill_fits(1536, 7168, 192, 256)       # 224 against 168
+    assert sel.fill_fits(512, 17408, 192, 256)       # 204 against 136
+    assert not sel.fill_fits(2048, 7168, 192, 256)   # 308 tiles: a second round
+    assert not sel.fill_fits(4096, 5120, 192, 256)   # 440 tiles
+    assert not sel.fill_fits(192, 5120, 192, 256)    # one tile row either way
+    assert not sel.fill_fits(384, 5120, 192, 256)    # two tile rows either way
+    assert not sel.fill_fits(257, 5120, 192, 256)
+    assert sel.select("gemm_w8a16", 2048, 5120, 5120, fmt=1)["tag"] == "i8x192x256w1x4k64s3f"
+    assert sel.select("gemm_w8a16", 2048, 7168, 5120, fmt=2)["tag"] == "i8x256w1x4k64s3t"
