@@ -8,11 +8,13 @@ Rows are tried in order; the first row whose band holds (M, N) -- M <= M_max and
 AND whose kernel fits the shape (divisibility) is taken.  No such row: None, the caller's own
 path.  (The reference stops at the first band that holds M; here a row that does not fit falls
 through to the next one, so a narrower row can sit in front of a general one.)
-  * M <= 32   line / stream: the weight-streaming decode kernels (HBM-bound; one pass over B).
+  * M <= 32   line / stream: the weight-streaming decode kernels (HBM-bound; one pass over B);
+              16 < M <= 32 at wide N: dma tiles of 64 weight rows and 256 k per stage.
               line = whole 128-byte weight lines by nontemporal LDS-DMA into per-wave rings
               (needs K % 128 and K <= 65536); stream (register-pipelined) takes the rest.  A = 1
               stages the activations in LDS once per workgroup (M = 1).
-  * 32 < M <= 64  line rows with more activation blocks; narrow N (< 6144) takes the interleaved
+  * 32 < M <= 64  dma tiles of 128 k at wide N, then line rows with more activation blocks;
+              narrow N (< 6144) takes the interleaved
               kernel with split-K (64 x 192 tiles).
   * 64 < M <= 256  narrow N (< 6144 for M <= 128): the interleaved kernel with split-K (128 x 128
               or 128 x 256 tiles); otherwise dma: k_gemm_dma tiles (64x64 to 128x128, 4-stage
@@ -38,6 +40,12 @@ LADDER = [
     (16, 0, "l1r1n4d4k8", "line", dict(MB=1, R=1, D=4, SN=4, W=2048, KS=8, KMIN=12288)),
     (16, 0, "l1r1d4", "line", dict(MB=1, R=1, D=4, W=2048)),
     (16, 0, "s16r1u4", "stream", dict(MB=1, R=1, U=4, A=0)),
+    # 16 < M <= 32, wide N: LDS-DMA tiles of 64 weight rows that take 256 k per stage (512
+    # contiguous bytes of each weight row per copy), one workgroup per 64 rows: 1.01 / 1.03 /
+    # 1.08x the ring row below at M = 24, 32 (15360, 3840) and 32 (12288, 4096); at M <= 16
+    # the ring rows above stay ahead (0.96-0.97x)
+    (32, 12288, "d32x64k256s3", "dma",
+     dict(BM=32, BN=64, BK=256, WM=2, WN=4, STAGES=3, SWZ=1, GROUP=8, XCD=1, MS=16)),
     # four ring stages (1.08-1.12x three at M = 24-32, N = 12288-15360)
     (32, 12288, "l2r1n4d4", "line", dict(MB=2, R=1, D=4, SN=4, W=2048)),
     # k slices as above (1.28x the row below at (32, 3840, 15360)), four ring steps (1.07x /
@@ -45,7 +53,11 @@ LADDER = [
     (32, 0, "l2r1n4d4k8", "line", dict(MB=2, R=1, D=4, SN=4, W=2048, KS=8, KMIN=12288)),
     (32, 0, "l2r1d4", "line", dict(MB=2, R=1, D=4, W=2048)),
     (32, 0, "s32r1u4", "stream", dict(MB=2, R=1, U=4, A=0)),
-    (64, 12288, "l4r1n4d3", "line", dict(MB=4, R=1, D=3, SN=4, W=2048)),
+    # 32 < M <= 64, wide N: 64 x 64 LDS-DMA tiles of 128 k (1.04x the four-slab ring row
+    # l4r1n4d3 they replace, at M = 48 and 64, (15360, 3840); that row needed the same N % 64
+    # and K % 128)
+    (64, 12288, "d64x64k128s3", "dma",
+     dict(BM=64, BN=64, BK=128, WM=2, WN=2, STAGES=3, SWZ=1, GROUP=8, XCD=1, MS=16)),
     # narrow N, long K: split-K over the interleaved kernel's tiles (fp32 partials in the
     # workspace, reduced in order) gives the 20 column tiles of N = 3840 enough workgroups;
     # measured by the variant driver (tempo/plugins/gfx950/tune.py) at (64|128|256, 3840, 15360);
@@ -57,6 +69,11 @@ LADDER = [
     # 64 < M <= 256: LDS-DMA tiles with a 4-stage ring.  Per CU they keep more operand bytes in
     # flight than the line kernel (which re-reads the activations per slab wave) or the
     # register-staged tiles.  Narrow N gives few workgroups (N = 3840: 60 column tiles)
+    # 128-k stages (256 contiguous bytes of each weight row per copy): 1.01-1.06x the 64-k
+    # four-stage row at M = 100, 128 (15360, 3840) and 128 (12288, 4096); at M = 200-256 the
+    # 128 x 128 tiles of 128 k lose (0.92-0.97x), so the M <= 256 rows keep 64 k
+    (128, 12288, "d128x64k128s3", "dma",
+     dict(BM=128, BN=64, BK=128, WM=2, WN=2, STAGES=3, SWZ=1, GROUP=8, XCD=1, MS=16)),
     (128, 12288, "d128x64k64s4", "dma",
      dict(BM=128, BN=64, BK=64, WM=2, WN=2, STAGES=4, SWZ=1, GROUP=8, XCD=1, MS=16)),
     (128, 0, "i128x128k64s3w256", "ilv",

@@ -188,6 +188,11 @@ class Gfx950Skeletons:
             tm, tn = p["BM"] // p["WM"] // ms, p["BN"] // p["WN"] // ms
             acc = tm * tn * nacc
             frags = 2 * (tm + tn) * 4 if kind == "dma" else (tm + tn) * 4
+            if kind == "dma":
+                # stages of more than four MFMA k-steps (128 k at MS = 16, 256 k at MS = 16 or
+                # 32): the compiler runs the fragment reads of a stage further ahead; measured
+                # 64 registers at 32 x 64 x 256 where the double-buffer count gives 48
+                frags *= max(1, (p["BK"] // (32 if ms == 16 else 16)) // 4)
             nw = p["WM"] * p["WN"]
             if kind == "dma":
                 rpb = 1024 // (p["BK"] * 2)

@@ -52,7 +52,7 @@ DOMAINS = {
                  BK=(64, 128),
                  STAGES=(2, 3, 4),
                  GROUP=(4, 8, 16), XCD=(0, 1), RSP=(4, 8, 12), SW=(0, 128, 256, 512)),
-    "dma": dict(BM=(64, 128, 256), BN=(64, 128, 192, 256), BK=(32, 64), STAGES=(2, 3, 4), SWZ=(0, 1, 2),
+    "dma": dict(BM=(32, 64, 128, 256), BN=(64, 128, 192, 256), BK=(32, 64, 128, 256), STAGES=(2, 3, 4), SWZ=(0, 1, 2),
                 GROUP=(4, 8, 16), XCD=(0, 1), WAVES=((2, 2), (2, 4), (4, 2), (4, 4)), MS=(16, 32)),
     "reg": dict(BM=(64, 128, 256), BN=(64, 128, 256), BK=(64,), MS=(16, 32), SWZ=(1, 2), GROUP=(8,),
                 XCD=(1,)),

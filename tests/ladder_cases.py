@@ -25,16 +25,22 @@ FP16 = [
     ("l1r1n4d4k8", 16, 3840, 12416),        # 97 steps (prime): no slices (no workspace)
     ("l1r1d4", 16, 3840, 3840),
     ("s16r1u4", 16, 512, 65792),
-    ("l2r1n4d4", 24, 15360, 3840),
+    ("d32x64k256s3", 24, 15360, 3840),
+    ("d32x64k256s3", 32, 12288, 4096),
+    ("d32x64k256s3", 17, 12352, 512),       # ragged M, N = 193 x 64, two k-stages
+    ("l2r1n4d4", 24, 15360, 3968),          # K % 256 != 0: past the 256-k tiles
     ("l2r1n4d4k8", 32, 3840, 15360),
     ("l2r1n4d4k8", 20, 3840, 12288),
     ("l2r1d4", 32, 3840, 3840),
     ("s32r1u4", 32, 512, 65792),
-    ("l4r1n4d3", 64, 15360, 3840),
+    ("d64x64k128s3", 64, 15360, 3840),
+    ("d64x64k128s3", 40, 12352, 640),
     ("i64x128k64s4w256", 64, 3840, 15360),  # the C2 decode-sweep point M = 64, N = 3840
     ("i64x128k64s4w256", 40, 1920, 4096),   # ragged M, few k-tiles per split
     ("l4r1d3", 64, 6144, 3840),             # N at the interleaved row's NMAX
-    ("d128x64k64s4", 128, 15360, 3840),
+    ("d128x64k128s3", 128, 15360, 3840),
+    ("d128x64k128s3", 100, 12288, 4096),
+    ("d128x64k64s4", 128, 15360, 3904),     # K % 128 == 64: past the 128-k tiles
     ("d128x64k64s4", 200, 8192, 3840),
     ("i128x128k64s3w256", 128, 3840, 15360),
     ("i128x128k64s3w256", 100, 3840, 3840),
