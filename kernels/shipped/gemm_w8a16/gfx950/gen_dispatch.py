@@ -36,6 +36,10 @@ HEAD = """// GENERATED from select.py -- do not edit.  Regenerate with:
 
 def instantiation(kind, p, epi=0):
     tail = ",%d" % epi if epi else ""
+    if kind == "phase":
+        if epi:
+            raise ValueError("the phase-ordered kernel takes the plain epilogue")
+        return "launch_phase<%d,%d,%d>" % (p["MB"], p["NS"], p["D"])
     if kind == "line" and p.get("MT"):  # row tiles x slab groups
         if epi or p.get("TL") or p.get("KS", 1) > 1:
             raise ValueError("row tiles take the plain epilogue, whole k and no tail grid")
@@ -78,7 +82,11 @@ def instantiation(kind, p, epi=0):
 
 
 def condition(sel, kind, p, m_max, n_min=0, gate_up=False):
-    if kind == "line" and p.get("TL"):
+    if kind == "phase":
+        fit = "(phase_fits<%d,%d,%d>(p))" % (p["MB"], p["NS"], p["D"])
+        if "KMAX" in p:
+            fit += " && p.K < %d" % p["KMAX"]
+    elif kind == "line" and p.get("TL"):
         fit = "(p.N %% %d) == 0 && (p.K %% %d) == 0 && (line_tail_fits<%d,%d,%d,%d,%d>(p))" % (
             sel.STREAM_N_ROWS * p["R"], sel.LINE_K_STEP, p["MB"], p["R"], p["D"], p["SN"],
             1 if gate_up else 0)

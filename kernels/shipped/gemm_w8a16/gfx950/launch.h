@@ -272,6 +272,65 @@ inline hipError_t launch_line(const W8A16Params& p, hipStream_t s) {
   return launch_line_fmt<2, MB, R, D, SN, WAVES, EPI, TL>(p, s);
 }
 
+// The phase-ordered decode kernel (k_stream_phase; wide N, M <= 16 MB, MB = 0: M = 1): one
+// workgroup per CU, its 8 waves the k chunks; rwg = N / 256 rows per workgroup (a multiple of 8:
+// NS - 1 slabs of 16 and a last one of 8 or 16), K a multiple of 1024.  The fit predicate and the
+// launcher share phase_layout, so a row that fits always launches.
+template <int MB, int NS, int D, int BFMT>
+inline bool phase_layout(const W8A16Params& p, PhaseArgs* a, int* lds) {
+  using SP = StreamPhase<MB, NS, D, BFMT>;
+  if (p.M > 16 * SP::MBE || (MB == 0 && p.M != 1)) return false;
+  if (p.N % SP::CUS || p.K % 1024) return false;
+  const int rwg = p.N / SP::CUS;
+  if (rwg % 8 || (rwg + 15) / 16 != NS) return false;
+  const int G = p.K / 128;
+  // the workgroups' metadata blocks are copied in 16-byte pieces
+  if (BFMT == 2 && (p.group != 128 || (rwg * G) % 16)) return false;
+  if (((reinterpret_cast<uintptr_t>(p.scale) | reinterpret_cast<uintptr_t>(p.zero)) % 16) != 0)
+    return false;
+  if (SP::lds(G) > 160 * 1024) return false;
+  a->A = p.A;
+  a->B = reinterpret_cast<const uint8_t*>(p.Wq);
+  a->scale = p.scale;
+  a->zero = p.zero;
+  a->C = p.C;
+  a->M = p.M;
+  a->K = p.K;
+  a->lda = p.lda;
+  a->ldb = p.ldw;
+  a->ldc = p.ldc;
+  a->rwg = rwg;
+  a->G = G;
+  a->spc = p.K / 1024;
+  a->stg_off = SP::ring_bytes();
+  a->out_off = a->stg_off + SP::stg_bytes();
+  a->meta_off = a->out_off + SP::out_bytes();
+  a->meta_s_off = a->meta_off + SP::meta_z_bytes(G);
+  *lds = SP::lds(G);
+  return true;
+}
+template <int MB, int NS, int D>
+inline bool phase_fits(const W8A16Params& p) {
+  PhaseArgs a;
+  int lds = 0;
+  return p.fmt == 1 ? phase_layout<MB, NS, D, 1>(p, &a, &lds) : phase_layout<MB, NS, D, 2>(p, &a, &lds);
+}
+template <int MB, int NS, int D>
+inline hipError_t launch_phase(const W8A16Params& p, hipStream_t s) {
+  PhaseArgs a;
+  int lds = 0;
+  if (p.fmt == 1) {
+    if (!phase_layout<MB, NS, D, 1>(p, &a, &lds)) return hipErrorInvalidConfiguration;
+    hipLaunchKernelGGL((k_stream_phase<MB, NS, D, 1>), dim3(StreamPhase<MB, NS, D, 1>::CUS),
+                       dim3(64 * StreamPhase<MB, NS, D, 1>::NWV), lds, s, a);
+  } else {
+    if (!phase_layout<MB, NS, D, 2>(p, &a, &lds)) return hipErrorInvalidConfiguration;
+    hipLaunchKernelGGL((k_stream_phase<MB, NS, D, 2>), dim3(StreamPhase<MB, NS, D, 2>::CUS),
+                       dim3(64 * StreamPhase<MB, NS, D, 2>::NWV), lds, s, a);
+  }
+  return hipGetLastError();
+}
+
 // Row-tiled line kernel (64 < M <= 128): the rows of A in tiles of 16 MB across workgroups, each
 // workgroup one row tile x one slab group of 16 R weight rows over the whole K, its S waves
 // splitting K (partial sums added through LDS in chunk order) -- no split-K partials in HBM, and

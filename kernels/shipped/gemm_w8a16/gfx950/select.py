@@ -28,10 +28,18 @@ LADDER = [
     # M = 1, wider N: two ring steps; where a CU holds 4+ slab waves (8.5 at N = 34816) two steps
     # per wave already keep ~35 KiB per CU in flight.  1.06x / 1.02x the four-step row it
     # replaced at (1, 34816, 5120) and 1.10x / 1.05x at (1, 7168, 5120), int8 / uint8
+    # M = 1, uint8, wide N: the phase-ordered kernel (k loop outside the slab loop, one
+    # workgroup per CU, the workgroup's metadata staged once by LDS-DMA): 1.06x the row below at
+    # (1, 34816, 5120) (int8: 1.01x, the row below stays)
+    (1, 12288, "p0n9d3", "phase", dict(MB=0, NS=9, D=3, KMAX=12288, fmts=(2,))),
     (1, 0, "l0r1d2w", "line", dict(MB=0, R=1, D=2, W=2048)),
     # M <= 16 / 32, wide N: the tail grid -- whole rounds of 4- / 8-slab workgroups (one ring of
     # activations each) and one single-wave workgroup per remaining slab, so the slabs per CU
     # differ by at most one (1.10-1.19x / 1.29-1.31x the rows after them at (34816, 5120))
+    # M <= 16, wide N: the phase-ordered kernel -- each CU reads the activations once, a phase
+    # (128 k) ahead of their use, and its ring carries weights only: 1.11x / 1.17x the tail grid
+    # below at (16, 34816, 5120), int8 / uint8
+    (16, 12288, "p1n9d4", "phase", dict(MB=1, NS=9, D=4, KMAX=12288)),
     (16, 12288, "l1r1n4d2t", "line", dict(MB=1, R=1, D=2, SN=4, W=2048, TL=1)),
     (16, 12288, "l1r1n4d3", "line", dict(MB=1, R=1, D=3, SN=4, W=2048)),
     # long K: k slices (1.17x / 1.25x the row below at (16, 5120, 17408))
@@ -41,6 +49,8 @@ LADDER = [
     (16, 0, "l1r1d2k8", "line", dict(MB=1, R=1, D=2, W=2048, KS=8, NMAX=2048)),
     # two ring steps (1.10-1.11x four at (16, 5120 | 7168, 5120))
     (16, 0, "l1r1n2d2", "line", dict(MB=1, R=1, D=2, SN=2, W=2048)),
+    # M <= 32, uint8: 1.05x the tail grid below at (32, 34816, 5120) (int8: 1.00x, it stays)
+    (32, 12288, "p2n9d4", "phase", dict(MB=2, NS=9, D=4, KMAX=12288, fmts=(2,))),
     (32, 12288, "l2r1n8d2t", "line", dict(MB=2, R=1, D=2, SN=8, W=2048, TL=1)),
     (32, 12288, "l2r1n4d4", "line", dict(MB=2, R=1, D=4, SN=4, W=2048)),
     # long K: k slices, eight slab waves per activation ring (1.37x / 1.46x the row below at
@@ -253,6 +263,39 @@ def _fits_gate_up(kind, p, M, N, K, fmt=1):
     return _fits(kind, p, M, N, K, fmt)
 
 
+PHASE_WAVES = 8  # k_stream_phase: waves (k chunks) per workgroup
+
+
+def phase_lds(p, K, fmt):
+    """LDS of k_stream_phase (StreamPhase::lds of the kernel): the weight rings, the activation
+    staging (after the loop: the chunk partial sums), the output image, the metadata."""
+    mb, ns, d = p["MB"], p["NS"], p["D"]
+    mbe = max(1, mb)
+    stg = 4 * mb * 1024 if mb else 256
+    G = K // 128
+    kib = lambda b: -(-b // 1024) * 1024  # noqa: E731
+    return (PHASE_WAVES * d * 2048 + max(PHASE_WAVES * stg, 2 * PHASE_WAVES * mbe * 1024)
+            + kib(mbe * 16 * ns * 16 * 2) + (kib(ns * 16 * G) if fmt == 2 else 0)
+            + kib(ns * 32 * G if fmt == 2 else ns * 32))
+
+
+def phase_fits(p, M, N, K, fmt):
+    """k_stream_phase's fit -- phase_layout of launch.h (pointer alignment aside): one workgroup
+    per CU over N / 256 rows (a multiple of 8; NS slabs of 16, the last 8 or 16), K / 8 k per
+    wave in steps of 128, and the LDS."""
+    mb = p["MB"]
+    if M > 16 * max(1, mb) or (mb == 0 and M != 1):
+        return False
+    if N % LINE_CUS or K % (PHASE_WAVES * LINE_K_STEP):
+        return False
+    rwg = N // LINE_CUS
+    if rwg % 8 or -(-rwg // 16) != p["NS"] or p["NS"] < p["D"]:
+        return False
+    if fmt == 2 and (rwg * (K // 128)) % 16:
+        return False
+    return phase_lds(p, K, fmt) <= LINE_LDS
+
+
 def fill_fits(M, N, BM, BN, cus=LINE_CUS):
     """A FILL row: its BM x BN grid is one round of the part and holds more tiles than the grid
     of 256 x BN tiles would -- ilv8_fill_fits of launch.h."""
@@ -276,6 +319,8 @@ def _fits(kind, p, M, N, K, fmt=1):
     if kind == "line" and p.get("TL"):  # tail grid: whole slabs, one k chunk
         return (N % (STREAM_N_ROWS * p["R"]) == 0 and K % LINE_K_STEP == 0
                 and line_tail_fits(p, N, K, fmt))
+    if kind == "phase":  # KMAX (optional): shorter K only
+        return phase_fits(p, M, N, K, fmt) and K < p.get("KMAX", 1 << 30)
     if kind == "line" and p.get("MT"):  # row tiles: whole slabs, whole k per workgroup
         return (N % (STREAM_N_ROWS * p["R"]) == 0 and K % LINE_K_STEP == 0 and K <= LINE_K_MAX
                 and N < p.get("NMAX", 1 << 30) and line_mt_fits(p, K, fmt))

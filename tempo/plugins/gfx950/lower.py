@@ -57,6 +57,8 @@ _ENTRY = {
                ("common/cdna4.h", "gemv_stream/kernel.hip")),
     "shared": ("k_stream_sh", ("MB", "R", "U", "BFMT", "SN", "TPB", "EPI"), "StreamArgs",
                ("common/cdna4.h", "gemv_stream/kernel.hip")),
+    "phase": ("k_stream_phase", ("MB", "NS", "D", "BFMT"), "PhaseArgs",
+              ("common/cdna4.h", "gemv_stream/kernel.hip", "gemv_stream/phase.hip")),
 }
 _ENTRY["fmha"] = ("fmha::k_fmha_fwd", ("D", "CAUSAL"),
                   "const _Float16*, const _Float16*, const _Float16*, _Float16*, float*, int, int, "
@@ -166,6 +168,15 @@ class Gfx950Skeletons:
             return regs, regs + D // 8 + 16, space.fmha_lds(D)
         if kind == "stream" and p.get("EPI"):
             p = dict(p, R=2 * p["R"])  # each wave carries the gate and the up row groups
+        if kind == "phase":
+            # one accumulator per slab and block for the whole chunk (4 NS MBE), one phase's
+            # activation fragments (16 MBE), a step's weight bytes and their fp16 expansion (16),
+            # fmt 2 zero-points and scales and their LDS addresses per slab (2 NS + 8), copy
+            # sources and loop state (48); pessimistic edge x1.25 (measured: 132-199 registers)
+            mbe = max(1, p["MB"])
+            regs = (4 * p["NS"] * mbe + 16 * mbe + 16 + (2 * p["NS"] + 8 if p["BFMT"] == 2 else 0)
+                    + 48)
+            return regs, int(regs * 1.25), space.phase_lds(int(op.shapes["K"]), p)
         if kind in ("ilv", "ilv8"):
             tm, tn = p["BM"] // p["WM"] // 16, p["BN"] // p["WN"] // 16
             acc = tm * tn * 4
@@ -263,6 +274,8 @@ class Gfx950Skeletons:
             grid = N // (16 * p["R"] * p["SN"])
             threads = 64 * p["SN"] * S
             bound = p["TPB"]  # __launch_bounds__(TPB)
+        elif kind == "phase":  # one workgroup of 8 waves per CU
+            grid, threads, bound = space.PHASE_CUS, 64 * space.PHASE_WAVES, 512
         elif kind == "line" and p.get("MT"):  # row tiles x slab groups
             sp = space.line_split(N, int(op.shapes["K"]), p)
             grid = -(-M // (16 * p["MB"])) * (N // (16 * p["R"]))
@@ -315,6 +328,16 @@ class Gfx950Skeletons:
             vmem = (p["BM"] + p["BN"]) * p["BK"] * 2 // nw
             if p.get("BFMT", 0):
                 vmem = p["BM"] * p["BK"] * 2 // nw + p["BN"] * p["BK"] // nw
+        elif kind == "phase":
+            # a wave's step: 16 rows x 128 k of weights (two 1 KiB copies, two 16-byte reads a
+            # lane) against 4 MBE MFMAs; a phase's activations (4 MBE KiB, or 256 B at M = 1)
+            # copied and read once per NS steps
+            mbe = max(1, p["MB"])
+            act = 4 * p["MB"] * 1024 if p["MB"] else 256
+            reps = p["NS"] * (K // (128 * space.PHASE_WAVES)) * rounds
+            flops = 4 * mbe * space.MFMA_FLOPS[16]
+            vmem = 2048 + act // p["NS"]
+            lds_rd = 2048 + act // p["NS"]
         elif kind == "line":
             wb = 2 if p["BFMT"] == 0 else 1
             sp = space.line_split(N, K, p)
@@ -340,7 +363,7 @@ class Gfx950Skeletons:
                               latency=_M.rate("LATENCY.LDS").value))
         atoms.append(Atom(uid=2, kind=AtomKind.XFER_ISSUE,
                           op_id=("buffer_load_dwordx4 lds" if kind in ("ilv", "ilv8") else
-                                 "global_load_lds_dwordx4" if kind in ("dma", "ring", "line")
+                                 "global_load_lds_dwordx4" if kind in ("dma", "ring", "line", "phase")
                                  else "global_load_dwordx4"),
                           footprint={"VMEM": float(vmem * reps)},
                           latency=_M.rate("LATENCY.VMEM").value, token="copy"))

@@ -73,7 +73,7 @@ def hyper_params(kind, p, fmt, epi=0):
     """A ladder row of select.py (kind, template params) -> the plugin's hyperform params: the
     same kernel, named the way space.variants() names it."""
     pk = {"stream": "stream", "mfma": "reg", "dma": "dma", "shared": "shared", "ilv": "ilv",
-          "ilv8": "ilv8", "line": "line"}[kind]
+          "ilv8": "ilv8", "line": "line", "phase": "phase"}[kind]
     # NMAX / KMIN / KMAX / FILL are the row's dispatch conditions, not kernel parameters
     params = {k: v for k, v in p.items() if k not in ("fmts", "NMAX", "KMIN", "KMAX", "FILL")}
     params["kind"] = pk
@@ -178,7 +178,7 @@ def gate_numbers(op, jobs=8):
 
 # Ladder-row kinds whose operand copies are global->LDS DMA (a build of one of them with no LDS-DMA
 # instruction has fallen back to register-staged loads)
-DMA_KINDS = ("ilv", "ilv8", "dma", "line")
+DMA_KINDS = ("ilv", "ilv8", "dma", "line", "phase")
 # Shipped rows allowed to keep a spill, with the reason and the measured cost of removing it
 # (none today: the gate below refuses every spill)
 SPILL_WAIVERS = {}
@@ -347,6 +347,11 @@ def make(op, rows_files=(), counter_files=()):
                                                                  sel.ilv_ld_max(p))
         elif kind == "ilv8":
             fit = "N %% %d == 0 and K %% 128 == 0 and K <= %d" % (p["BN"], sel.ilv_ld_max(p))
+        elif kind == "phase":
+            fit = ("N %% 256 == 0, N / 256 %% 8 == 0 and ceil(N / 256 / 16) == %d, K %% 1024 == 0, "
+                   "LDS <= 160 KiB" % p["NS"])
+            if "KMAX" in p:
+                fit += " and K < %d" % p["KMAX"]
         elif kind == "line" and p.get("TL"):
             fit = ("N %% %d == 0 and K %% %d == 0 and K <= %d; tail grid: q = (N / %d) // %d >= 1 "
                    "whole rounds, at most %d slabs left, q + 1 workgroups resident per CU" % (

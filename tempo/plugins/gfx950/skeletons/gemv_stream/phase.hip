@@ -1,0 +1,301 @@
+// gemv_stream/phase.hip -- the phase-ordered decode kernel of the W8A16 delivery.  Uses the
+// copy vocabulary of gemv_stream/kernel.hip (lds_void_stream_t, s_wait_vm_stream, line_key) and
+// the dequantisation of common/cdna4.h.
+// ============================================================================================
+// k_stream_phase -- the decode kernel with the k loop outside the slab loop (wide N, M <= 32).
+//
+// One workgroup per CU (256 of them), 8 waves; workgroup b owns the weight rows [b rwg, (b+1) rwg)
+// with rwg = N / 256 (a multiple of 8): NS - 1 slabs of 16 rows and a last slab of 8 or 16.  Wave w
+// owns the k chunk [1024 w / 8 ... ) = K / 8 (a multiple of 128: SPC steps of 128 k).  The wave
+// walks its chunk phase by phase (a phase = one 128-k step) and, inside a phase, the NS slabs:
+// step (s, sl) is 16 rows x 128 bytes of slab sl at k step s, copied HBM -> LDS by two whole-line
+// LDS-DMA copies (the line kernel's copy map and chunk swizzle) into a private ring of D slots.
+// The point of the order: a phase needs the activations of ONE 128-k step (16 MB registers per
+// lane), which travel by LDS-DMA into a per-wave staging slot during the phase before and are
+// read into registers at the phase's first step -- so the activations ride the weight stream a
+// phase ahead instead of being fetched up front, the ring carries weights only, and the
+// activation registers do not grow with K.  Each slab keeps its own accumulators for the whole
+// chunk (NS x MB f32x4 per lane).  At the end the 8 chunk partial sums of each slab are added
+// through LDS in chunk order (one slab per round, one wave per slab), written as fp16 into an
+// LDS image of the workgroup's output columns, and stored row by row.
+// Activations: MB = 1 / 2 (M <= 16 / 32): lane l's 16 bytes of row 16 mb + l % 16 (rows past M
+// re-read row M-1) per copy, four copies per 16 rows; MB = 0 (M = 1): the phase's 256-byte slice
+// of row 0 by one dword copy, read by broadcast.  Metadata (fmt 1 row scales; fmt 2 zero-points
+// and scales of the workgroup's rows, all groups) are staged in LDS once, by LDS-DMA of their
+// contiguous blocks, before the first step.
+// Waits: every step issues its two weight copies, so "step u has landed" is vmcnt((D-1) * 2),
+// plus the phase's activation copies (4 MB, or 1) when they were issued after step u's copies
+// (the steps 1 .. D-1 of every phase but the last).  The slab loop is unrolled (the waits are
+// compile-time per step) and the phase loop is not: all phases but the last issue the same
+// instructions; the last one (no next activations, its copies past the end fetch a dummy line
+// of A from L2 into slots nobody reads) is peeled.  Requirements (launcher): N % 256 == 0,
+// N / 256 % 8 == 0 with NS = ceil(N / 256 / 16) >= D, K % 1024 == 0, 16-byte aligned A, Wq,
+// scale and zero, and (fmt 2) group 128 with the workgroup's metadata blocks 16-byte aligned.
+// ============================================================================================
+struct PhaseArgs {
+  const _Float16* A;
+  const uint8_t* B;
+  const _Float16* scale;
+  const uint8_t* zero;
+  _Float16* C;
+  int M, K, lda, ldb, ldc;
+  int rwg;   // weight rows per workgroup (N / 256)
+  int G;     // groups of 128 k per row (K / 128)
+  int spc;   // 128-k steps per wave (K / 1024)
+  int stg_off, out_off, meta_off, meta_s_off;  // LDS byte offsets
+};
+
+template <int B, int E, class F>
+__device__ __forceinline__ void unroll_for(F&& f) {
+  if constexpr (B < E) {
+    f(IC<B>{});
+    unroll_for<B + 1, E>(f);
+  }
+}
+
+template <int MB, int NS, int D, int BFMT>
+struct StreamPhase {
+  static constexpr int NWV = 8;                  // waves = k chunks per workgroup
+  static constexpr int L = 2;                    // weight copies per step
+  static constexpr int MBE = MB > 0 ? MB : 1;    // 16-column blocks of the result
+  static constexpr int LA = MB > 0 ? 4 * MB : 1; // activation copies per phase
+  static constexpr int SLOT = 2048;              // one ring slot: 16 rows x 128 bytes
+  static constexpr int STG = MB > 0 ? LA * 1024 : 256;  // activation staging per wave
+  static constexpr int CUS = 256;                // workgroups: one per CU of the part
+  static_assert(NS >= D && D >= 2 && (D - 1) * L + LA < 64, "ring depth / vmcnt range");
+  // vmcnt of "step (s, sl) landed": LAST = the phase issues no next activations
+  static constexpr int wait_of(int sl, bool last) {
+    return (D - 1) * L + (!last && sl > 0 && sl < D ? LA : 0);
+  }
+  // LDS layout (bytes): rings, activation staging (after the loop: the chunk partial sums), the
+  // output image, metadata; -1 if it exceeds 160 KiB
+  static constexpr int ring_bytes() { return NWV * D * SLOT; }
+  static constexpr int stg_bytes() {
+    return NWV * STG > 2 * NWV * MBE * 1024 ? NWV * STG : 2 * NWV * MBE * 1024;
+  }
+  static constexpr int out_bytes() { return (MBE * 16 * NS * 16 * 2 + 1023) / 1024 * 1024; }
+  static constexpr int meta_z_bytes(int G) { return BFMT == 2 ? (NS * 16 * G + 1023) / 1024 * 1024 : 0; }
+  static constexpr int meta_s_bytes(int G) {
+    return ((BFMT == 2 ? NS * 32 * G : NS * 32) + 1023) / 1024 * 1024;
+  }
+  static constexpr int lds(int G) {
+    return ring_bytes() + stg_bytes() + out_bytes() + meta_z_bytes(G) + meta_s_bytes(G);
+  }
+};
+
+template <int MB, int NS, int D, int BFMT>
+__global__ __launch_bounds__(512, 1) void k_stream_phase(PhaseArgs p) {
+  using SP = StreamPhase<MB, NS, D, BFMT>;
+  constexpr int NWV = SP::NWV, L = SP::L, LA = SP::LA, SLOT = SP::SLOT, MBE = SP::MBE;
+  constexpr int NSX = NS * 16;  // output image row length (columns)
+  extern __shared__ __attribute__((aligned(1024))) uint8_t dsm[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r16 = lane & 15, kg = lane >> 4;
+  const int rwg = p.rwg, spc = p.spc;
+  const long row0 = (long)blockIdx.x * rwg;
+  const int kbeg = wave * spc * 128;
+  uint8_t* ring = dsm + wave * D * SLOT;
+  uint8_t* stg = dsm + p.stg_off + wave * SP::STG;
+  f32x4* red = reinterpret_cast<f32x4*>(dsm + p.stg_off);  // after the loop: [2][NWV][MBE][64]
+  _Float16* outl = reinterpret_cast<_Float16*>(dsm + p.out_off);
+  const uint8_t* meta_z = dsm + p.meta_off;
+  const _Float16* meta_s = reinterpret_cast<const _Float16*>(dsm + p.meta_s_off);
+  const uint8_t* dummy = reinterpret_cast<const uint8_t*>(p.A) + 16 * lane;  // 1 KiB of A (L2)
+
+  // metadata blocks of the workgroup's rows, 1 KiB pieces over the waves
+  auto copy_block = [&](uint8_t* dst, const uint8_t* src, int bytes) {
+    for (int pc = wave; pc * 1024 < bytes; pc += NWV) {
+      const int off = pc * 1024 + 16 * lane;
+      if (off < bytes)
+        __builtin_amdgcn_global_load_lds((void*)(src + off), (lds_void_stream_t*)(dst + pc * 1024),
+                                         16, 0, 0);
+    }
+  };
+  if constexpr (BFMT == 1) {
+    copy_block(dsm + p.meta_s_off, reinterpret_cast<const uint8_t*>(p.scale + row0), rwg * 2);
+  } else {
+    copy_block(dsm + p.meta_off, p.zero + row0 * p.G, rwg * p.G);
+    copy_block(dsm + p.meta_s_off, reinterpret_cast<const uint8_t*>(p.scale + row0 * p.G),
+               rwg * 2 * p.G);
+  }
+  // activation copies of phase s: copy (mb, h, q) carries lane l's 16 bytes -- row 16 mb + l % 16,
+  // k kbeg + 128 s + 64 h + 16 (l / 16) + 8 q -- read back by the same lane; MB = 0: one dword per
+  // lane of row 0's 256-byte slice
+  const _Float16* arow[MBE];
+#pragma unroll
+  for (int mb = 0; mb < MBE; ++mb)
+    arow[mb] = MB == 0 ? p.A + kbeg + 2 * lane
+                       : p.A + (long)min(16 * mb + r16, p.M - 1) * p.lda + kbeg + 16 * kg;
+  auto dma_act = [&](int s) {
+    if constexpr (MB == 0) {
+      __builtin_amdgcn_global_load_lds((void*)(arow[0] + 128 * s), (lds_void_stream_t*)stg, 4, 0, 0);
+    } else {
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int q = 0; q < 2; ++q)
+            __builtin_amdgcn_global_load_lds(
+                (void*)(arow[mb] + 128 * s + 64 * h + 8 * q),
+                (lds_void_stream_t*)(stg + ((mb * 2 + h) * 2 + q) * 1024), 16, 0, 0);
+    }
+  };
+  // weight copy i of a step fills rows 8i .. 8i+7: lane l row 8i + l/8, physical chunk l%8 =
+  // logical chunk (l%8) ^ key(row); the last slab's second half past the workgroup's rows
+  // fetches the dummy line instead
+  const uint8_t* wsrc[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int rr = 8 * i + lane / 8;
+    const int c = (lane % 8) ^ line_key(rr);
+    wsrc[i] = p.B + (row0 + rr) * p.ldb + kbeg + c * 16;
+  }
+  const long slab_stride = 16L * p.ldb;
+  // copies of step (s, sl) into ring slot `slot`; past = beyond the chunk's last step.  One copy
+  // instruction per half whatever its source (a selected address, no branch: copies in a branch
+  // make the compiler wait for every copy in flight where the paths merge)
+  auto dma_w = [&](int s, int sl, int slot, bool past) {
+    uint8_t* dst = ring + slot * SLOT;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const bool real = !past && (sl < NS - 1 || 16 * sl + 8 * i < rwg);
+      const uint8_t* src = real ? wsrc[i] + sl * slab_stride + s * 128 : dummy;
+      __builtin_amdgcn_global_load_lds((void*)src, (lds_void_stream_t*)(dst + i * 1024), 16, 0,
+                                       2 /* nt */);
+    }
+  };
+
+  dma_act(0);
+  unroll_for<0, D>([&](auto uc) {  // NS >= D: the first D steps are slabs 0 .. D-1 of phase 0
+    constexpr int u = decltype(uc)::value;
+    dma_w(0, u, u, false);
+  });
+  asm volatile("" ::: "memory");
+  s_wait_vm_stream<(D - 1) * L>();  // metadata, phase 0's activations and step 0 have landed
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();     // ... in every wave: the metadata pieces are all in
+  asm volatile("" ::: "memory");
+
+  const int key = line_key(r16);
+  const int g0 = kbeg / 128;
+  f32x4 acc[NS][MBE];
+#pragma unroll
+  for (int sl = 0; sl < NS; ++sl)
+#pragma unroll
+    for (int mb = 0; mb < MBE; ++mb) acc[sl][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  u32x4 a[MBE][2][2];
+
+  // one phase: the NS steps of k step s (ring slot of step (s, sl) = (s NS + sl) % D)
+  auto phase = [&](int s, auto lastc) {
+    constexpr bool LAST = decltype(lastc)::value;
+    const int ub = s * NS;
+    unroll_for<0, NS>([&](auto slc) {
+      constexpr int sl = decltype(slc)::value;
+      asm volatile("" ::: "memory");
+      s_wait_vm_stream<SP::wait_of(sl, LAST)>();  // step (s, sl) landed (sl = 0: and phase s's
+      asm volatile("" ::: "memory");              // activations)
+      if constexpr (sl == 0) {
+#pragma unroll
+        for (int mb = 0; mb < MBE; ++mb)
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int q = 0; q < 2; ++q)
+              a[mb][h][q] = MB == 0
+                  ? *reinterpret_cast<const u32x4*>(stg + (64 * h + 16 * kg + 8 * q) * 2)
+                  : *reinterpret_cast<const u32x4*>(stg + ((mb * 2 + h) * 2 + q) * 1024 + 16 * lane);
+      }
+      const uint8_t* slot = ring + ((ub + sl) % D) * SLOT;
+      u32x4 w[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        w[h] = *reinterpret_cast<const u32x4*>(slot + r16 * 128 + (((4 * h + kg) ^ key) * 16));
+      uint8_t z = 0;
+      _Float16 scl;
+      if constexpr (BFMT == 2) {
+        z = meta_z[(sl * 16 + r16) * p.G + g0 + s];
+        scl = meta_s[(sl * 16 + r16) * p.G + g0 + s];
+      } else {
+        scl = meta_s[sl * 16 + r16];
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the slot (and the staging) are read
+      asm volatile("" ::: "memory");
+      if constexpr (sl == 0 && !LAST) dma_act(s + 1);
+      {
+        constexpr int nx = sl + D;  // step D ahead: (s + nx / NS, nx % NS)
+        dma_w(s + nx / NS, nx % NS, (ub + nx) % D, LAST && nx >= NS);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        f16x8 w0, w1;
+        if constexpr (BFMT == 1) {
+          w0 = dequant8_i8(w[h][0], w[h][1], scl);
+          w1 = dequant8_i8(w[h][2], w[h][3], scl);
+        } else {
+          w0 = dequant8_u8(w[h][0], w[h][1], z, scl);
+          w1 = dequant8_u8(w[h][2], w[h][3], z, scl);
+        }
+#pragma unroll
+        for (int mb = 0; mb < MBE; ++mb) {
+          acc[sl][mb] = Mfma<16>::run(w0, as_f16x8(a[mb][h][0]), acc[sl][mb]);
+          acc[sl][mb] = Mfma<16>::run(w1, as_f16x8(a[mb][h][1]), acc[sl][mb]);
+        }
+      }
+    });
+  };
+  for (int s = 0; s < spc - 1; ++s) phase(s, IC<0>{});
+  phase(spc - 1, IC<1>{});
+
+  s_wait_vm_stream<0>();  // the copies past the end have landed
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  __builtin_amdgcn_s_barrier();  // every wave is past its staging reads: the partial sums reuse it
+  asm volatile("" ::: "memory");
+  // the 8 chunk partial sums of slab sl, added in chunk order by wave sl % 8 (double-buffered)
+  unroll_for<0, NS>([&](auto slc) {
+    constexpr int sl = decltype(slc)::value;
+    constexpr int rb = sl & 1;
+#pragma unroll
+    for (int mb = 0; mb < MBE; ++mb) red[((rb * NWV + wave) * MBE + mb) * 64 + lane] = acc[sl][mb];
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (wave == sl % NWV) {
+#pragma unroll
+      for (int mb = 0; mb < MBE; ++mb) {
+        f32x4 t = red[((rb * NWV + 0) * MBE + mb) * 64 + lane];
+#pragma unroll
+        for (int c = 1; c < NWV; ++c) {
+          const f32x4 v = red[((rb * NWV + c) * MBE + mb) * 64 + lane];
+          t[0] += v[0];
+          t[1] += v[1];
+          t[2] += v[2];
+          t[3] += v[3];
+        }
+        f16x4 o;
+        o[0] = (_Float16)t[0];
+        o[1] = (_Float16)t[1];
+        o[2] = (_Float16)t[2];
+        o[3] = (_Float16)t[3];
+        *reinterpret_cast<f16x4*>(outl + (16 * mb + r16) * NSX + sl * 16 + 4 * kg) = o;
+      }
+    }
+  });
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  // rows m < M of the workgroup's rwg output columns, 8 bytes per thread and pass
+  const int cpr = rwg / 4;
+  for (int i = threadIdx.x; i < p.M * cpr; i += 64 * NWV) {
+    const int m = i / cpr, c = i - m * cpr;
+    const u32x2 v = *reinterpret_cast<const u32x2*>(outl + m * NSX + 4 * c);
+    *reinterpret_cast<u32x2*>(p.C + (long)m * p.ldc + row0 + 4 * c) = v;
+  }
+}

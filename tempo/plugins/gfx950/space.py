@@ -63,7 +63,11 @@ DOMAINS = {
     "ring": dict(R=(1, 2, 4), D=(4, 5, 6, 8, 10, 12, 14, 16)),
     "stream": dict(R=(1, 2, 4), U=(2, 4, 8), ALDS=(0, 1)),
     "shared": dict(R=(1, 2), U=(2, 4), SN=(2, 4, 8)),
+    # phase-ordered decode kernel (8-bit weights, wide N): ring depth; NS follows from N
+    "phase": dict(D=(2, 3, 4)),
 }
+PHASE_WAVES = 8  # k_stream_phase: waves (k chunks) per workgroup, one workgroup per CU
+PHASE_CUS = 256
 
 BFMT_OF = {("fp16", "fp16"): 0, ("fp16", "int8"): 1, ("fp16", "uint8"): 2}
 SPLIT_MINKT = 8  # split-K rows keep at least this many k-tiles per split
@@ -218,6 +222,29 @@ def line_split(N: int, K: int, p: dict):
         S -= 1
 
 
+def phase_lds(K: int, p: dict) -> int:
+    """LDS of k_stream_phase (StreamPhase::lds of the skeleton): D-slot weight rings of the 8
+    waves, the activation staging (after the loop: the chunk partial sums), the output image of
+    NS slabs, the metadata of 16 NS rows (fmt 1: row scales; fmt 2: zero-points and scales of
+    every group)."""
+    mb, ns, d = p["MB"], p["NS"], p["D"]
+    mbe = max(1, mb)
+    stg = 4 * mb * 1024 if mb else 256
+    G = K // 128
+    kib = lambda b: -(-b // 1024) * 1024  # noqa: E731
+    return (PHASE_WAVES * d * 2048 + max(PHASE_WAVES * stg, 2 * PHASE_WAVES * mbe * 1024)
+            + kib(mbe * 16 * ns * 16 * 2) + (kib(ns * 16 * G) if p["BFMT"] == 2 else 0)
+            + kib(ns * 32 * G if p["BFMT"] == 2 else ns * 32))
+
+
+def phase_ns(N: int):
+    """Slabs per workgroup of k_stream_phase for width N (None: N does not split into 256
+    workgroups of a multiple of 8 rows)."""
+    if N % PHASE_CUS or (N // PHASE_CUS) % 8:
+        return None
+    return -(-(N // PHASE_CUS) // 16)
+
+
 def lds_bytes(kind: str, p: dict) -> int:
     if kind in ("dma", "ilv"):
         return p["STAGES"] * (p["BM"] + p["BN"]) * p["BK"] * 2
@@ -302,6 +329,8 @@ def tag(kind: str, p: dict) -> str:
             "_ks%d" % p["KS"] if p.get("KS", 1) > 1 else "")
     if kind == "ring":
         return "ring_mb%d_r%d_d%d_b%d" % (p["MB"], p["R"], p["D"], p["BFMT"])
+    if kind == "phase":
+        return "phase_mb%d_n%d_d%d_b%d" % (p["MB"], p["NS"], p["D"], p["BFMT"])
     if kind == "shared":
         return "shared_mb%d_r%d_u%d_b%d_n%d" % (p["MB"], p["R"], p["U"], p["BFMT"], p["SN"])
     return "stream_mb%d_r%d_u%d_b%d_a%d" % (p["MB"], p["R"], p["U"], p["BFMT"], p.get("ALDS", 0))
@@ -351,6 +380,23 @@ def legal(kind: str, p: dict, M: int, N: int, K: int):
             return "the C tile does not fit the stages"
         if lds_bytes(kind, p) > LDS_MAX:
             return "LDS %d B > 160 KiB" % lds_bytes(kind, p)
+        return None
+    if kind == "phase":
+        mb, ns, d = p["MB"], p["NS"], p["D"]
+        if p["BFMT"] not in (1, 2):
+            return "weights must be int8 (fmt 1) or uint8 group-128 (fmt 2)"
+        if M > 16 * max(1, mb) or (mb == 0 and M != 1):
+            return "M > 16*MB (MB = 0: M = 1)"
+        if phase_ns(N) != ns:
+            return "N is not 256 workgroups of a multiple of 8 rows in %d slabs" % ns
+        if K % (PHASE_WAVES * 128):
+            return "K %% %d" % (PHASE_WAVES * 128)
+        if ns < d or d < 2 or (d - 1) * 2 + (4 * mb if mb else 1) >= 64:
+            return "ring depth: 2 <= D <= NS, vmcnt range"
+        if p["BFMT"] == 2 and ((N // PHASE_CUS) * (K // 128)) % 16:
+            return "the workgroups' metadata blocks are not 16-byte aligned"
+        if phase_lds(K, p) > LDS_MAX:
+            return "LDS %d B > 160 KiB" % phase_lds(K, p)
         return None
     if kind in ("dma", "reg"):
         BM, BN, BK = p["BM"], p["BN"], p["BK"]
@@ -526,6 +572,9 @@ def _gemm_variants(op: OpSpec) -> Iterator[Hyperform]:
             for U in DOMAINS["shared"]["U"]:
                 for SN in DOMAINS["shared"]["SN"]:
                     out.append(("shared", dict(MB=MB, R=R, U=U, BFMT=b, SN=SN, TPB=1024)))
+        if b and phase_ns(N):  # the phase-ordered kernel: 8-bit weights, N in 256 row blocks
+            for D in DOMAINS["phase"]["D"]:
+                out.append(("phase", dict(MB=0 if M == 1 else MB, NS=phase_ns(N), D=D, BFMT=b)))
     if b == 0:
         d = DOMAINS["ilv"]
         for BM in d["BM"]:

@@ -91,7 +91,10 @@ W8 = {
         ("l0r1d2", 1, 1024, 5120),
         ("l0r1d2w", 1, 7168, 5120),
         ("l0r1d2w", 1, 34816, 5120),      # the C3/C4 decode point M = 1, N = 34816
-        ("l1r1n4d2t", 16, 34816, 5120),
+        ("p1n9d4", 16, 34816, 5120),      # the C3/C4 decode point M = 16: 136 rows per CU
+        ("p1n9d4", 9, 36864, 1024),       # ragged M; 144 rows per CU (a whole last slab), one phase
+        ("p1n9d4", 2, 34816, 3072),
+        ("l1r1n4d2t", 16, 34816, 3840),   # K % 1024 != 0: past the phase-ordered row
         ("l1r1n4d2t", 16, 16400, 256),    # one remaining slab
         ("l1r1n4d2t", 9, 16384, 384),     # whole rounds, no tail
         ("l1r1n4d3", 16, 15360, 5120),    # too few slabs for a round of the tail grid
@@ -149,8 +152,12 @@ W8 = {
         ("l0r1n2d2", 1, 5120, 5120),
         ("l0r1d2", 1, 1024, 5120),
         ("l0r1d2w", 1, 7168, 5120),
-        ("l0r1d2w", 1, 34816, 5120),      # the C3/C4 decode point M = 1, N = 34816
-        ("l1r1n4d2t", 16, 34816, 5120),
+        ("p0n9d3", 1, 34816, 5120),       # the C3/C4 decode point M = 1, N = 34816
+        ("p0n9d3", 1, 36864, 1024),       # a whole last slab, one phase
+        ("l0r1d2w", 1, 34816, 3840),      # K % 1024 != 0: past the phase-ordered row
+        ("p1n9d4", 16, 34816, 5120),      # the C3/C4 decode point M = 16
+        ("p1n9d4", 11, 36864, 2048),
+        ("l1r1n4d2t", 16, 34816, 3840),
         ("l1r1n4d2t", 16, 16400, 256),    # one remaining slab
         ("l1r1n4d2t", 9, 16384, 384),     # whole rounds, no tail
         ("l1r1n4d3", 16, 15360, 5120),    # too few slabs for a round of the tail grid
@@ -160,7 +167,9 @@ W8 = {
         ("l1r1d2k8", 7, 1024, 1024),      # 8 steps: no slices (no workspace)
         ("l1r1n2d2", 16, 5120, 6144),
         ("l1r1n2d2", 16, 7168, 5120),
-        ("l2r1n8d2t", 32, 34816, 5120),
+        ("p2n9d4", 32, 34816, 5120),      # the C3/C4 decode point M = 32
+        ("p2n9d4", 20, 36864, 3072),
+        ("l2r1n8d2t", 32, 34816, 3840),
         ("l2r1n8d2t", 17, 32784, 256),    # one remaining slab
         ("l2r1n8d2t", 32, 36864, 128),    # one slab per CU remaining, a single k step
         ("l2r1n4d4", 32, 15360, 5120),

@@ -168,7 +168,12 @@ def test_rows_fall_through_when_the_first_row_does_not_fit():
     assert capi.route(0, 8, 15360, 3840) == "l1r1n4d4"
     assert capi.route(0, 8, 12304, 3840) == "l1r1d4"      # N % 64 != 0: the unshared line row
     assert capi.route(0, 8, 15360, 65792) == "s16r1u4"    # K > 65536: past the line rows
-    assert capi.route(1, 16, 34816, 5120) == "l1r1n4d2t"
+    assert capi.route(1, 16, 34816, 5120) == "p1n9d4"    # 256 workgroups of 136 rows
+    assert capi.route(1, 16, 34816, 3840) == "l1r1n4d2t"  # K % 1024 != 0
+    assert capi.route(1, 16, 34816, 12288) == "l1r1n4d2t"  # long K: past the phase rows
+    assert capi.route(2, 32, 34816, 5120) == "p2n9d4"
+    assert capi.route(2, 1, 34816, 5120) == "p0n9d3"
+    assert capi.route(1, 1, 34816, 5120) == "l0r1d2w"     # int8 at M = 1: the line row
     assert capi.route(1, 16, 15360, 5120) == "l1r1n4d3"  # too few slabs for the tail grid
     assert capi.route(1, 16, 69632, 5120) == "l1r1n4d3"  # 5 workgroups of 4 waves per CU
     assert capi.route(2, 16, 5120, 17408) == "l1r1n4d2k8"   # long K: the k-slice row
