@@ -84,6 +84,8 @@ def instantiation(kind, p, epi=0):
 def condition(sel, kind, p, m_max, n_min=0, gate_up=False):
     if kind == "phase":
         fit = "(phase_fits<%d,%d,%d>(p))" % (p["MB"], p["NS"], p["D"])
+        if "NMAX" in p:
+            fit += " && p.N < %d" % p["NMAX"]
         if "KMAX" in p:
             fit += " && p.K < %d" % p["KMAX"]
     elif kind == "line" and p.get("TL"):

@@ -272,9 +272,9 @@ inline hipError_t launch_line(const W8A16Params& p, hipStream_t s) {
   return launch_line_fmt<2, MB, R, D, SN, WAVES, EPI, TL>(p, s);
 }
 
-// The phase-ordered decode kernel (k_stream_phase; wide N, M <= 16 MB, MB = 0: M = 1): one
-// workgroup per CU, its 8 waves the k chunks; rwg = N / 256 rows per workgroup (a multiple of 8:
-// NS - 1 slabs of 16 and a last one of 8 or 16), K a multiple of 1024.  The fit predicate and the
+// The phase-ordered decode kernel (k_stream_phase; M <= 16 MB, MB = 0: M = 1): one workgroup
+// per CU, its 8 waves the k chunks; rwg = N / 256 rows per workgroup (a multiple of 4: NS - 1
+// slabs of 16 and a last one of 4 .. 16), K a multiple of 1024.  The fit predicate and the
 // launcher share phase_layout, so a row that fits always launches.
 template <int MB, int NS, int D, int BFMT>
 inline bool phase_layout(const W8A16Params& p, PhaseArgs* a, int* lds) {
@@ -282,11 +282,11 @@ inline bool phase_layout(const W8A16Params& p, PhaseArgs* a, int* lds) {
   if (p.M > 16 * SP::MBE || (MB == 0 && p.M != 1)) return false;
   if (p.N % SP::CUS || p.K % 1024) return false;
   const int rwg = p.N / SP::CUS;
-  if (rwg % 8 || (rwg + 15) / 16 != NS) return false;
+  if (rwg % 4 || (rwg + 15) / 16 != NS) return false;
   const int G = p.K / 128;
-  // the workgroups' metadata blocks are copied in 16-byte pieces
-  if (BFMT == 2 && (p.group != 128 || (rwg * G) % 16)) return false;
-  if (((reinterpret_cast<uintptr_t>(p.scale) | reinterpret_cast<uintptr_t>(p.zero)) % 16) != 0)
+  if (BFMT == 2 && p.group != 128) return false;
+  // the workgroups' metadata blocks are copied in 4-byte pieces (rwg % 4 keeps them aligned)
+  if (((reinterpret_cast<uintptr_t>(p.scale) | reinterpret_cast<uintptr_t>(p.zero)) % 4) != 0)
     return false;
   if (SP::lds(G) > 160 * 1024) return false;
   a->A = p.A;
@@ -303,7 +303,7 @@ inline bool phase_layout(const W8A16Params& p, PhaseArgs* a, int* lds) {
   a->G = G;
   a->spc = p.K / 1024;
   a->stg_off = SP::ring_bytes();
-  a->out_off = a->stg_off + SP::stg_bytes();
+  a->out_off = a->stg_off + SP::stg_bytes(G);
   a->meta_off = a->out_off + SP::out_bytes();
   a->meta_s_off = a->meta_off + SP::meta_z_bytes(G);
   *lds = SP::lds(G);

@@ -20,6 +20,10 @@ LADDER = [
     # the 320 slabs of N = 5120 evenly over the part; two ring steps (1.04x / 1.12x the rows
     # below at (1, 5120, 17408), int8 / uint8)
     (1, 0, "l0r1d2k8", "line", dict(MB=0, R=1, D=2, W=2048, KS=8, KMIN=12288)),
+    # M = 1 on N = 4096..7168, K < 12288, K % 1024 == 0: the phase-ordered kernel, 20-24 rows
+    # per CU (a slab of 16 and one of 4-8), no tail: 1.08x / 1.10x the row below at (1, 5120,
+    # 5120), 1.00x / 1.03x at (1, 5120, 6144), int8 / uint8 (at N = 7168: 0.95x, not taken)
+    (1, 4096, "p0n2d2", "phase", dict(MB=0, NS=2, D=2, NMAX=7168, KMAX=12288)),
     # M = 1 on N = 4096..6144: two slab waves per activation ring, two ring steps (1.10-1.14x
     # the five-step row it replaced at N = 5120, K = 5120-6144)
     (1, 4096, "l0r1n2d2", "line", dict(MB=0, R=1, D=2, SN=2, W=2048, NMAX=6145)),
@@ -271,8 +275,8 @@ def phase_lds(p, K, fmt):
     staging (after the loop: the chunk partial sums), the output image, the metadata."""
     mb, ns, d = p["MB"], p["NS"], p["D"]
     mbe = max(1, mb)
-    stg = 4 * mb * 1024 if mb else 256
     G = K // 128
+    stg = 4 * mb * 1024 if mb else G // PHASE_WAVES * 256  # M = 1: every phase's slice
     kib = lambda b: -(-b // 1024) * 1024  # noqa: E731
     return (PHASE_WAVES * d * 2048 + max(PHASE_WAVES * stg, 2 * PHASE_WAVES * mbe * 1024)
             + kib(mbe * 16 * ns * 16 * 2) + (kib(ns * 16 * G) if fmt == 2 else 0)
@@ -281,17 +285,16 @@ def phase_lds(p, K, fmt):
 
 def phase_fits(p, M, N, K, fmt):
     """k_stream_phase's fit -- phase_layout of launch.h (pointer alignment aside): one workgroup
-    per CU over N / 256 rows (a multiple of 8; NS slabs of 16, the last 8 or 16), K / 8 k per
-    wave in steps of 128, and the LDS."""
+    per CU over N / 256 rows (a multiple of 4; NS slabs of 16, the last 4 .. 16), K / 8 k per
+    wave in steps of 128, a ring no deeper than a phase where activations ride it (M > 1), and
+    the LDS."""
     mb = p["MB"]
     if M > 16 * max(1, mb) or (mb == 0 and M != 1):
         return False
     if N % LINE_CUS or K % (PHASE_WAVES * LINE_K_STEP):
         return False
     rwg = N // LINE_CUS
-    if rwg % 8 or -(-rwg // 16) != p["NS"] or p["NS"] < p["D"]:
-        return False
-    if fmt == 2 and (rwg * (K // 128)) % 16:
+    if rwg % 4 or -(-rwg // 16) != p["NS"] or (mb > 0 and p["NS"] < p["D"]):
         return False
     return phase_lds(p, K, fmt) <= LINE_LDS
 
@@ -319,8 +322,9 @@ def _fits(kind, p, M, N, K, fmt=1):
     if kind == "line" and p.get("TL"):  # tail grid: whole slabs, one k chunk
         return (N % (STREAM_N_ROWS * p["R"]) == 0 and K % LINE_K_STEP == 0
                 and line_tail_fits(p, N, K, fmt))
-    if kind == "phase":  # KMAX (optional): shorter K only
-        return phase_fits(p, M, N, K, fmt) and K < p.get("KMAX", 1 << 30)
+    if kind == "phase":  # NMAX / KMAX (optional): narrower N / shorter K only
+        return (phase_fits(p, M, N, K, fmt) and N < p.get("NMAX", 1 << 30)
+                and K < p.get("KMAX", 1 << 30))
     if kind == "line" and p.get("MT"):  # row tiles: whole slabs, whole k per workgroup
         return (N % (STREAM_N_ROWS * p["R"]) == 0 and K % LINE_K_STEP == 0 and K <= LINE_K_MAX
                 and N < p.get("NMAX", 1 << 30) and line_mt_fits(p, K, fmt))

@@ -348,8 +348,10 @@ def make(op, rows_files=(), counter_files=()):
         elif kind == "ilv8":
             fit = "N %% %d == 0 and K %% 128 == 0 and K <= %d" % (p["BN"], sel.ilv_ld_max(p))
         elif kind == "phase":
-            fit = ("N %% 256 == 0, N / 256 %% 8 == 0 and ceil(N / 256 / 16) == %d, K %% 1024 == 0, "
+            fit = ("N %% 256 == 0, N / 256 %% 4 == 0 and ceil(N / 256 / 16) == %d, K %% 1024 == 0, "
                    "LDS <= 160 KiB" % p["NS"])
+            if "NMAX" in p:
+                fit += " and N < %d" % p["NMAX"]
             if "KMAX" in p:
                 fit += " and K < %d" % p["KMAX"]
         elif kind == "line" and p.get("TL"):

@@ -5,7 +5,7 @@
 // k_stream_phase -- the decode kernel with the k loop outside the slab loop (wide N, M <= 32).
 //
 // One workgroup per CU (256 of them), 8 waves; workgroup b owns the weight rows [b rwg, (b+1) rwg)
-// with rwg = N / 256 (a multiple of 8): NS - 1 slabs of 16 rows and a last slab of 8 or 16.  Wave w
+// with rwg = N / 256 (a multiple of 4): NS - 1 slabs of 16 rows and a last slab of 4 .. 16.  Wave w
 // owns the k chunk [1024 w / 8 ... ) = K / 8 (a multiple of 128: SPC steps of 128 k).  The wave
 // walks its chunk phase by phase (a phase = one 128-k step) and, inside a phase, the NS slabs:
 // step (s, sl) is 16 rows x 128 bytes of slab sl at k step s, copied HBM -> LDS by two whole-line
@@ -19,18 +19,19 @@
 // through LDS in chunk order (one slab per round, one wave per slab), written as fp16 into an
 // LDS image of the workgroup's output columns, and stored row by row.
 // Activations: MB = 1 / 2 (M <= 16 / 32): lane l's 16 bytes of row 16 mb + l % 16 (rows past M
-// re-read row M-1) per copy, four copies per 16 rows; MB = 0 (M = 1): the phase's 256-byte slice
-// of row 0 by one dword copy, read by broadcast.  Metadata (fmt 1 row scales; fmt 2 zero-points
-// and scales of the workgroup's rows, all groups) are staged in LDS once, by LDS-DMA of their
-// contiguous blocks, before the first step.
+// re-read row M-1) per copy, four copies per 16 rows, a phase ahead; MB = 0 (M = 1): every
+// phase's 256-byte slice of row 0 (one dword copy each) staged before the first step, read by
+// broadcast.  Metadata (fmt 1 row scales; fmt 2 zero-points and scales of the workgroup's rows,
+// all groups) are staged in LDS once, by 4-byte LDS-DMA pieces of their contiguous blocks,
+// before the first step.  Rows of the last slab past the workgroup's rows (and copies past the
+// chunk's end) fetch a dummy line of A, an L2 hit, into slots whose results nobody stores.
 // Waits: every step issues its two weight copies, so "step u has landed" is vmcnt((D-1) * 2),
-// plus the phase's activation copies (4 MB, or 1) when they were issued after step u's copies
+// plus (MB > 0) the phase's activation copies (4 MB) when they were issued after step u's copies
 // (the steps 1 .. D-1 of every phase but the last).  The slab loop is unrolled (the waits are
-// compile-time per step) and the phase loop is not: all phases but the last issue the same
-// instructions; the last one (no next activations, its copies past the end fetch a dummy line
-// of A from L2 into slots nobody reads) is peeled.  Requirements (launcher): N % 256 == 0,
-// N / 256 % 8 == 0 with NS = ceil(N / 256 / 16) >= D, K % 1024 == 0, 16-byte aligned A, Wq,
-// scale and zero, and (fmt 2) group 128 with the workgroup's metadata blocks 16-byte aligned.
+// compile-time per step) and the phase loop is not; with MB > 0 the last phase (no next
+// activations) is peeled.  Requirements (launcher): N % 256 == 0, N / 256 % 4 == 0 with
+// NS = ceil(N / 256 / 16) (>= D when MB > 0), K % 1024 == 0, 16-byte aligned A and Wq, 4-byte
+// aligned scale and zero, and (fmt 2) group 128.
 // ============================================================================================
 struct PhaseArgs {
   const _Float16* A;
@@ -60,18 +61,20 @@ struct StreamPhase {
   static constexpr int MBE = MB > 0 ? MB : 1;    // 16-column blocks of the result
   static constexpr int LA = MB > 0 ? 4 * MB : 1; // activation copies per phase
   static constexpr int SLOT = 2048;              // one ring slot: 16 rows x 128 bytes
-  static constexpr int STG = MB > 0 ? LA * 1024 : 256;  // activation staging per wave
   static constexpr int CUS = 256;                // workgroups: one per CU of the part
-  static_assert(NS >= D && D >= 2 && (D - 1) * L + LA < 64, "ring depth / vmcnt range");
+  static_assert((MB == 0 || NS >= D) && D >= 2 && (D - 1) * L + LA < 64,
+                "ring depth / vmcnt range");
+  // activation staging per wave: one phase's copies (MB > 0), every phase's slice (MB = 0)
+  static constexpr int stg_wave(int G) { return MB > 0 ? LA * 1024 : G / NWV * 256; }
   // vmcnt of "step (s, sl) landed": LAST = the phase issues no next activations
   static constexpr int wait_of(int sl, bool last) {
-    return (D - 1) * L + (!last && sl > 0 && sl < D ? LA : 0);
+    return (D - 1) * L + (MB > 0 && !last && sl > 0 && sl < D ? LA : 0);
   }
   // LDS layout (bytes): rings, activation staging (after the loop: the chunk partial sums), the
   // output image, metadata; -1 if it exceeds 160 KiB
   static constexpr int ring_bytes() { return NWV * D * SLOT; }
-  static constexpr int stg_bytes() {
-    return NWV * STG > 2 * NWV * MBE * 1024 ? NWV * STG : 2 * NWV * MBE * 1024;
+  static constexpr int stg_bytes(int G) {
+    return NWV * stg_wave(G) > 2 * NWV * MBE * 1024 ? NWV * stg_wave(G) : 2 * NWV * MBE * 1024;
   }
   static constexpr int out_bytes() { return (MBE * 16 * NS * 16 * 2 + 1023) / 1024 * 1024; }
   static constexpr int meta_z_bytes(int G) { return BFMT == 2 ? (NS * 16 * G + 1023) / 1024 * 1024 : 0; }
@@ -79,7 +82,7 @@ struct StreamPhase {
     return ((BFMT == 2 ? NS * 32 * G : NS * 32) + 1023) / 1024 * 1024;
   }
   static constexpr int lds(int G) {
-    return ring_bytes() + stg_bytes() + out_bytes() + meta_z_bytes(G) + meta_s_bytes(G);
+    return ring_bytes() + stg_bytes(G) + out_bytes() + meta_z_bytes(G) + meta_s_bytes(G);
   }
 };
 
@@ -96,20 +99,20 @@ __global__ __launch_bounds__(512, 1) void k_stream_phase(PhaseArgs p) {
   const long row0 = (long)blockIdx.x * rwg;
   const int kbeg = wave * spc * 128;
   uint8_t* ring = dsm + wave * D * SLOT;
-  uint8_t* stg = dsm + p.stg_off + wave * SP::STG;
+  uint8_t* stg = dsm + p.stg_off + wave * SP::stg_wave(p.G);
   f32x4* red = reinterpret_cast<f32x4*>(dsm + p.stg_off);  // after the loop: [2][NWV][MBE][64]
   _Float16* outl = reinterpret_cast<_Float16*>(dsm + p.out_off);
   const uint8_t* meta_z = dsm + p.meta_off;
   const _Float16* meta_s = reinterpret_cast<const _Float16*>(dsm + p.meta_s_off);
   const uint8_t* dummy = reinterpret_cast<const uint8_t*>(p.A) + 16 * lane;  // 1 KiB of A (L2)
 
-  // metadata blocks of the workgroup's rows, 1 KiB pieces over the waves
+  // metadata blocks of the workgroup's rows, 256-byte pieces (a dword per lane) over the waves
   auto copy_block = [&](uint8_t* dst, const uint8_t* src, int bytes) {
-    for (int pc = wave; pc * 1024 < bytes; pc += NWV) {
-      const int off = pc * 1024 + 16 * lane;
+    for (int pc = wave; pc * 256 < bytes; pc += NWV) {
+      const int off = pc * 256 + 4 * lane;
       if (off < bytes)
-        __builtin_amdgcn_global_load_lds((void*)(src + off), (lds_void_stream_t*)(dst + pc * 1024),
-                                         16, 0, 0);
+        __builtin_amdgcn_global_load_lds((void*)(src + off), (lds_void_stream_t*)(dst + pc * 256),
+                                         4, 0, 0);
     }
   };
   if constexpr (BFMT == 1) {
@@ -128,8 +131,9 @@ __global__ __launch_bounds__(512, 1) void k_stream_phase(PhaseArgs p) {
     arow[mb] = MB == 0 ? p.A + kbeg + 2 * lane
                        : p.A + (long)min(16 * mb + r16, p.M - 1) * p.lda + kbeg + 16 * kg;
   auto dma_act = [&](int s) {
-    if constexpr (MB == 0) {
-      __builtin_amdgcn_global_load_lds((void*)(arow[0] + 128 * s), (lds_void_stream_t*)stg, 4, 0, 0);
+    if constexpr (MB == 0) {  // phase s's slice into its own staging slot
+      __builtin_amdgcn_global_load_lds((void*)(arow[0] + 128 * s), (lds_void_stream_t*)(stg + 256 * s),
+                                       4, 0, 0);
     } else {
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb)
@@ -143,14 +147,15 @@ __global__ __launch_bounds__(512, 1) void k_stream_phase(PhaseArgs p) {
     }
   };
   // weight copy i of a step fills rows 8i .. 8i+7: lane l row 8i + l/8, physical chunk l%8 =
-  // logical chunk (l%8) ^ key(row); the last slab's second half past the workgroup's rows
-  // fetches the dummy line instead
+  // logical chunk (l%8) ^ key(row); a lane whose row of the last slab lies past the workgroup's
+  // rows fetches the dummy line instead
   const uint8_t* wsrc[2];
+  int wrow[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    const int rr = 8 * i + lane / 8;
-    const int c = (lane % 8) ^ line_key(rr);
-    wsrc[i] = p.B + (row0 + rr) * p.ldb + kbeg + c * 16;
+    wrow[i] = 8 * i + lane / 8;
+    const int c = (lane % 8) ^ line_key(wrow[i]);
+    wsrc[i] = p.B + (row0 + wrow[i]) * p.ldb + kbeg + c * 16;
   }
   const long slab_stride = 16L * p.ldb;
   // copies of step (s, sl) into ring slot `slot`; past = beyond the chunk's last step.  One copy
@@ -160,20 +165,24 @@ __global__ __launch_bounds__(512, 1) void k_stream_phase(PhaseArgs p) {
     uint8_t* dst = ring + slot * SLOT;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const bool real = !past && (sl < NS - 1 || 16 * sl + 8 * i < rwg);
+      const bool real = !past && (sl < NS - 1 || 16 * sl + wrow[i] < rwg);
       const uint8_t* src = real ? wsrc[i] + sl * slab_stride + s * 128 : dummy;
       __builtin_amdgcn_global_load_lds((void*)src, (lds_void_stream_t*)(dst + i * 1024), 16, 0,
                                        2 /* nt */);
     }
   };
 
-  dma_act(0);
-  unroll_for<0, D>([&](auto uc) {  // NS >= D: the first D steps are slabs 0 .. D-1 of phase 0
+  if constexpr (MB == 0) {
+    for (int s = 0; s < spc; ++s) dma_act(s);
+  } else {
+    dma_act(0);
+  }
+  unroll_for<0, D>([&](auto uc) {  // the first D steps (MB > 0: NS >= D, all of phase 0)
     constexpr int u = decltype(uc)::value;
-    dma_w(0, u, u, false);
+    dma_w(u / NS, u % NS, u % D, u / NS >= spc);
   });
   asm volatile("" ::: "memory");
-  s_wait_vm_stream<(D - 1) * L>();  // metadata, phase 0's activations and step 0 have landed
+  s_wait_vm_stream<(D - 1) * L>();  // metadata, the first activations and step 0 have landed
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_barrier();     // ... in every wave: the metadata pieces are all in
   asm volatile("" ::: "memory");
@@ -204,7 +213,7 @@ __global__ __launch_bounds__(512, 1) void k_stream_phase(PhaseArgs p) {
 #pragma unroll
             for (int q = 0; q < 2; ++q)
               a[mb][h][q] = MB == 0
-                  ? *reinterpret_cast<const u32x4*>(stg + (64 * h + 16 * kg + 8 * q) * 2)
+                  ? *reinterpret_cast<const u32x4*>(stg + 256 * s + (64 * h + 16 * kg + 8 * q) * 2)
                   : *reinterpret_cast<const u32x4*>(stg + ((mb * 2 + h) * 2 + q) * 1024 + 16 * lane);
       }
       const uint8_t* slot = ring + ((ub + sl) % D) * SLOT;
@@ -224,10 +233,10 @@ __global__ __launch_bounds__(512, 1) void k_stream_phase(PhaseArgs p) {
       asm volatile("" ::: "memory");
       __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the slot (and the staging) are read
       asm volatile("" ::: "memory");
-      if constexpr (sl == 0 && !LAST) dma_act(s + 1);
+      if constexpr (MB > 0 && sl == 0 && !LAST) dma_act(s + 1);
       {
         constexpr int nx = sl + D;  // step D ahead: (s + nx / NS, nx % NS)
-        dma_w(s + nx / NS, nx % NS, (ub + nx) % D, LAST && nx >= NS);
+        dma_w(s + nx / NS, nx % NS, (ub + nx) % D, s + nx / NS >= spc);
       }
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -248,8 +257,12 @@ __global__ __launch_bounds__(512, 1) void k_stream_phase(PhaseArgs p) {
       }
     });
   };
-  for (int s = 0; s < spc - 1; ++s) phase(s, IC<0>{});
-  phase(spc - 1, IC<1>{});
+  if constexpr (MB == 0) {  // every phase alike: no activation copies in the loop
+    for (int s = 0; s < spc; ++s) phase(s, IC<1>{});
+  } else {
+    for (int s = 0; s < spc - 1; ++s) phase(s, IC<0>{});
+    phase(spc - 1, IC<1>{});
+  }
 
   s_wait_vm_stream<0>();  // the copies past the end have landed
   asm volatile("" ::: "memory");

@@ -229,8 +229,8 @@ def phase_lds(K: int, p: dict) -> int:
     every group)."""
     mb, ns, d = p["MB"], p["NS"], p["D"]
     mbe = max(1, mb)
-    stg = 4 * mb * 1024 if mb else 256
     G = K // 128
+    stg = 4 * mb * 1024 if mb else G // PHASE_WAVES * 256  # M = 1: every phase's slice
     kib = lambda b: -(-b // 1024) * 1024  # noqa: E731
     return (PHASE_WAVES * d * 2048 + max(PHASE_WAVES * stg, 2 * PHASE_WAVES * mbe * 1024)
             + kib(mbe * 16 * ns * 16 * 2) + (kib(ns * 16 * G) if p["BFMT"] == 2 else 0)
@@ -239,8 +239,8 @@ def phase_lds(K: int, p: dict) -> int:
 
 def phase_ns(N: int):
     """Slabs per workgroup of k_stream_phase for width N (None: N does not split into 256
-    workgroups of a multiple of 8 rows)."""
-    if N % PHASE_CUS or (N // PHASE_CUS) % 8:
+    workgroups of a multiple of 4 rows)."""
+    if N % PHASE_CUS or (N // PHASE_CUS) % 4:
         return None
     return -(-(N // PHASE_CUS) // 16)
 
@@ -388,13 +388,11 @@ def legal(kind: str, p: dict, M: int, N: int, K: int):
         if M > 16 * max(1, mb) or (mb == 0 and M != 1):
             return "M > 16*MB (MB = 0: M = 1)"
         if phase_ns(N) != ns:
-            return "N is not 256 workgroups of a multiple of 8 rows in %d slabs" % ns
+            return "N is not 256 workgroups of a multiple of 4 rows in %d slabs" % ns
         if K % (PHASE_WAVES * 128):
             return "K %% %d" % (PHASE_WAVES * 128)
-        if ns < d or d < 2 or (d - 1) * 2 + (4 * mb if mb else 1) >= 64:
-            return "ring depth: 2 <= D <= NS, vmcnt range"
-        if p["BFMT"] == 2 and ((N // PHASE_CUS) * (K // 128)) % 16:
-            return "the workgroups' metadata blocks are not 16-byte aligned"
+        if (mb > 0 and ns < d) or d < 2 or (d - 1) * 2 + (4 * mb if mb else 1) >= 64:
+            return "ring depth: 2 <= D (<= NS where activations ride the ring), vmcnt range"
         if phase_lds(K, p) > LDS_MAX:
             return "LDS %d B > 160 KiB" % phase_lds(K, p)
         return None

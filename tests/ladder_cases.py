@@ -87,7 +87,9 @@ W8 = {
     1: [
         ("l0r1d2k8", 1, 5120, 17408),     # 320 slabs x 4 k slices
         ("l0r1d2k8", 1, 4096, 16384),     # 256 slabs: no slices (no workspace)
-        ("l0r1n2d2", 1, 5120, 6144),
+        ("p0n2d2", 1, 5120, 6144),        # 20 rows per CU: a slab of 16 and one of 4
+        ("p0n2d2", 1, 6144, 2048),        # 24 rows per CU
+        ("l0r1n2d2", 1, 5120, 3840),      # K % 1024 != 0: past the phase-ordered row
         ("l0r1d2", 1, 1024, 5120),
         ("l0r1d2w", 1, 7168, 5120),
         ("l0r1d2w", 1, 34816, 5120),      # the C3/C4 decode point M = 1, N = 34816
@@ -149,7 +151,9 @@ W8 = {
     2: [
         ("l0r1d2k8", 1, 5120, 17408),
         ("l0r1d2k8", 1, 4096, 16384),
-        ("l0r1n2d2", 1, 5120, 5120),
+        ("p0n2d2", 1, 5120, 5120),
+        ("p0n2d2", 1, 6144, 1024),        # 24 rows per CU, one phase
+        ("l0r1n2d2", 1, 5120, 3840),
         ("l0r1d2", 1, 1024, 5120),
         ("l0r1d2w", 1, 7168, 5120),
         ("p0n9d3", 1, 34816, 5120),       # the C3/C4 decode point M = 1, N = 34816

@@ -185,8 +185,10 @@ def test_rows_fall_through_when_the_first_row_does_not_fit():
     assert capi.route(2, 32, 34816, 65536 + 256) == "h32r1u4n2"
     assert capi.route(0, 1, 15360, 3840) == "l0r1d2w"
     assert capi.route(0, 1, 3840, 15360) == "l0r1d2"    # long K
-    assert capi.route(1, 1, 5120, 5120) == "l0r1n2d2"
-    assert capi.route(2, 1, 5120, 5120) == "l0r1n2d2"
+    assert capi.route(1, 1, 5120, 5120) == "p0n2d2"      # 20 rows per CU, K % 1024 == 0
+    assert capi.route(2, 1, 5120, 5120) == "p0n2d2"
+    assert capi.route(1, 1, 5120, 3840) == "l0r1n2d2"    # K % 1024 != 0
+    assert capi.route(1, 1, 7168, 5120) == "l0r1d2w"     # N = 7168: past the narrow phase row
     assert capi.route(1, 1, 5120, 17408) == "l0r1d2k8"  # long K: k slices
     assert capi.route(1, 1, 7168, 5120) == "l0r1d2w"    # past the narrow row's N band
     assert capi.route(1, 1, 1024, 5120) == "l0r1d2"     # narrow N
