@@ -37,9 +37,7 @@ HEAD = """// GENERATED from select.py -- do not edit.  Regenerate with:
 def instantiation(kind, p, epi=0):
     tail = ",%d" % epi if epi else ""
     if kind == "phase":
-        if epi:
-            raise ValueError("the phase-ordered kernel takes the plain epilogue")
-        return "launch_phase<%d,%d,%d>" % (p["MB"], p["NS"], p["D"])
+        return "launch_phase%s<%d,%d,%d>" % ("_gu" if epi else "", p["MB"], p["NS"], p["D"])
     if kind == "line" and p.get("MT"):  # row tiles x slab groups
         if epi or p.get("TL") or p.get("KS", 1) > 1:
             raise ValueError("row tiles take the plain epilogue, whole k and no tail grid")
@@ -83,7 +81,7 @@ def instantiation(kind, p, epi=0):
 
 def condition(sel, kind, p, m_max, n_min=0, gate_up=False):
     if kind == "phase":
-        fit = "(phase_fits<%d,%d,%d>(p))" % (p["MB"], p["NS"], p["D"])
+        fit = "(phase%s_fits<%d,%d,%d>(p))" % ("_gu" if gate_up else "", p["MB"], p["NS"], p["D"])
         if "NMAX" in p:
             fit += " && p.N < %d" % p["NMAX"]
         if "KMAX" in p:

@@ -276,13 +276,15 @@ inline hipError_t launch_line(const W8A16Params& p, hipStream_t s) {
 // per CU, its 8 waves the k chunks; rwg = N / 256 rows per workgroup (a multiple of 4: NS - 1
 // slabs of 16 and a last one of 4 .. 16), K a multiple of 1024.  The fit predicate and the
 // launcher share phase_layout, so a row that fits always launches.
-template <int MB, int NS, int D, int BFMT>
+// EPI = 1 (fused gate/up): p.N is the output width; a workgroup's cwg = N / 256 output columns
+// (a multiple of 4) take its 2 cwg rows, the gate rows and the matching up rows.
+template <int MB, int NS, int D, int BFMT, int EPI = 0>
 inline bool phase_layout(const W8A16Params& p, PhaseArgs* a, int* lds) {
-  using SP = StreamPhase<MB, NS, D, BFMT>;
+  using SP = StreamPhase<MB, NS, D, BFMT, EPI>;
   if (p.M > 16 * SP::MBE || (MB == 0 && p.M != 1)) return false;
   if (p.N % SP::CUS || p.K % 1024) return false;
-  const int rwg = p.N / SP::CUS;
-  if (rwg % 4 || (rwg + 15) / 16 != NS) return false;
+  const int cwg = p.N / SP::CUS, rwg = EPI ? 2 * cwg : cwg;
+  if (cwg % 4 || (rwg + 15) / 16 != NS) return false;
   const int G = p.K / 128;
   if (BFMT == 2 && p.group != 128) return false;
   // the workgroups' metadata blocks are copied in 4-byte pieces (rwg % 4 keeps them aligned)
@@ -300,6 +302,8 @@ inline bool phase_layout(const W8A16Params& p, PhaseArgs* a, int* lds) {
   a->ldb = p.ldw;
   a->ldc = p.ldc;
   a->rwg = rwg;
+  a->cwg = cwg;
+  a->up = EPI ? p.N : 0;
   a->G = G;
   a->spc = p.K / 1024;
   a->stg_off = SP::ring_bytes();
@@ -315,20 +319,31 @@ inline bool phase_fits(const W8A16Params& p) {
   int lds = 0;
   return p.fmt == 1 ? phase_layout<MB, NS, D, 1>(p, &a, &lds) : phase_layout<MB, NS, D, 2>(p, &a, &lds);
 }
-template <int MB, int NS, int D>
+template <int MB, int NS, int D, int EPI = 0>
 inline hipError_t launch_phase(const W8A16Params& p, hipStream_t s) {
   PhaseArgs a;
   int lds = 0;
   if (p.fmt == 1) {
-    if (!phase_layout<MB, NS, D, 1>(p, &a, &lds)) return hipErrorInvalidConfiguration;
-    hipLaunchKernelGGL((k_stream_phase<MB, NS, D, 1>), dim3(StreamPhase<MB, NS, D, 1>::CUS),
+    if (!phase_layout<MB, NS, D, 1, EPI>(p, &a, &lds)) return hipErrorInvalidConfiguration;
+    hipLaunchKernelGGL((k_stream_phase<MB, NS, D, 1, EPI>), dim3(StreamPhase<MB, NS, D, 1>::CUS),
                        dim3(64 * StreamPhase<MB, NS, D, 1>::NWV), lds, s, a);
   } else {
-    if (!phase_layout<MB, NS, D, 2>(p, &a, &lds)) return hipErrorInvalidConfiguration;
-    hipLaunchKernelGGL((k_stream_phase<MB, NS, D, 2>), dim3(StreamPhase<MB, NS, D, 2>::CUS),
+    if (!phase_layout<MB, NS, D, 2, EPI>(p, &a, &lds)) return hipErrorInvalidConfiguration;
+    hipLaunchKernelGGL((k_stream_phase<MB, NS, D, 2, EPI>), dim3(StreamPhase<MB, NS, D, 2>::CUS),
                        dim3(64 * StreamPhase<MB, NS, D, 2>::NWV), lds, s, a);
   }
   return hipGetLastError();
+}
+template <int MB, int NS, int D>
+inline bool phase_gu_fits(const W8A16Params& p) {
+  PhaseArgs a;
+  int lds = 0;
+  return p.fmt == 1 ? phase_layout<MB, NS, D, 1, 1>(p, &a, &lds)
+                    : phase_layout<MB, NS, D, 2, 1>(p, &a, &lds);
+}
+template <int MB, int NS, int D>
+inline hipError_t launch_phase_gu(const W8A16Params& p, hipStream_t s) {
+  return launch_phase<MB, NS, D, 1>(p, s);
 }
 
 // Row-tiled line kernel (64 < M <= 128): the rows of A in tiles of 16 MB across workgroups, each

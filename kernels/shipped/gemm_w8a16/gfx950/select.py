@@ -152,6 +152,10 @@ LADDER = [
 # production gate_up shape (N, K) = (17408, 5120), both formats; then the interleaved int8
 # kernel with EPI = 1 for every M.
 LADDER_GATE_UP = [
+    # the phase-ordered kernel with the gate/up epilogue (a workgroup's 68 output columns take
+    # its 136 rows: the gate rows and the matching up rows), wide N: at (17408 x 2, 5120) uint8
+    # 1.04x the paired line row at M = 1 (int8 1.01x: not taken)
+    (1, 12288, "gp0n9d4", "phase", dict(MB=0, NS=9, D=4, KMAX=12288, fmts=(2,))),
     # two ring steps at M = 1 and M = 32 (1.05-1.08x / 1.02-1.06x four, both formats)
     (1, 0, "gl0r1n2d2", "line", dict(MB=0, R=1, D=2, SN=2, W=2048)),
     # M <= 16 / 32, wide N: the tail grid -- whole rounds of paired workgroups (SN/2 output
@@ -159,9 +163,13 @@ LADDER_GATE_UP = [
     # (17408 x 2, 5120), one process: M = 32 39.5 / 41.6 us (int8 / uint8) against 46.9 / 48.8
     # for the paired row below, and 1.18x / 1.13x the tail grid with one wave carrying both
     # halves of a tail slab; M = 16 36.9 / 38.9 us against 38.4 / 40.3 for the row below
+    # M <= 16: 1.11x / 1.15x the tail grid below at (17408 x 2, 5120), int8 / uint8
+    (16, 12288, "gp1n9d4", "phase", dict(MB=1, NS=9, D=4, KMAX=12288)),
     (16, 12288, "gl1r1n4d2t", "line", dict(MB=1, R=1, D=2, SN=4, W=2048, TL=1)),
     (16, 12288, "gl1r1n4d3", "line", dict(MB=1, R=1, D=3, SN=4, W=2048)),
     (16, 0, "gl1r1n2d4", "line", dict(MB=1, R=1, D=4, SN=2, W=2048)),
+    # M <= 32, uint8: 1.04x the tail grid below (int8 1.01x: not taken)
+    (32, 12288, "gp2n9d4", "phase", dict(MB=2, NS=9, D=4, KMAX=12288, fmts=(2,))),
     (32, 12288, "gl2r1n8d2t", "line", dict(MB=2, R=1, D=2, SN=8, W=2048, TL=1)),
     (32, 12288, "gl2r1n4d2", "line", dict(MB=2, R=1, D=2, SN=4, W=2048)),
     (32, 0, "gl2r1n2d4", "line", dict(MB=2, R=1, D=4, SN=2, W=2048)),
@@ -253,6 +261,10 @@ def line_tail_fits(p, N, K, fmt, epi=0):
 def _fits_gate_up(kind, p, M, N, K, fmt=1):
     # N is the output width; the slab waves of the shared kernel and of the line kernel with
     # SN >= 2 pair up (SN/2 output slabs per workgroup)
+    if kind == "phase":  # a workgroup's N / 256 output columns (a multiple of 4) take 2 N / 256
+        # rows -- phase_gu_fits of launch.h
+        return (N % LINE_CUS == 0 and (N // LINE_CUS) % 4 == 0
+                and phase_fits(p, M, 2 * N, K, fmt) and K < p.get("KMAX", 1 << 30))
     if kind == "line" and p.get("TL"):  # tail grid of paired workgroups
         return (N % (STREAM_N_ROWS * p["R"]) == 0 and K % LINE_K_STEP == 0
                 and line_tail_fits(p, N, K, fmt, epi=1))

@@ -57,7 +57,7 @@ _ENTRY = {
                ("common/cdna4.h", "gemv_stream/kernel.hip")),
     "shared": ("k_stream_sh", ("MB", "R", "U", "BFMT", "SN", "TPB", "EPI"), "StreamArgs",
                ("common/cdna4.h", "gemv_stream/kernel.hip")),
-    "phase": ("k_stream_phase", ("MB", "NS", "D", "BFMT"), "PhaseArgs",
+    "phase": ("k_stream_phase", ("MB", "NS", "D", "BFMT", "EPI"), "PhaseArgs",
               ("common/cdna4.h", "gemv_stream/kernel.hip", "gemv_stream/phase.hip")),
 }
 _ENTRY["fmha"] = ("fmha::k_fmha_fwd", ("D", "CAUSAL"),
@@ -172,10 +172,11 @@ class Gfx950Skeletons:
             # one accumulator per slab and block for the whole chunk (4 NS MBE), one phase's
             # activation fragments (16 MBE), a step's weight bytes and their fp16 expansion (16),
             # fmt 2 zero-points and scales and their LDS addresses per slab (2 NS + 8), copy
-            # sources and loop state (48); pessimistic edge x1.25 (measured: 132-199 registers)
+            # sources and loop state (48), the gate/up epilogue's up-row copy sources and half
+            # selects (8); pessimistic edge x1.25 (measured: 120-245 registers)
             mbe = max(1, p["MB"])
             regs = (4 * p["NS"] * mbe + 16 * mbe + 16 + (2 * p["NS"] + 8 if p["BFMT"] == 2 else 0)
-                    + 48)
+                    + 48 + (8 if p.get("EPI") else 0))
             return regs, int(regs * 1.25), space.phase_lds(int(op.shapes["K"]), p)
         if kind in ("ilv", "ilv8"):
             tm, tn = p["BM"] // p["WM"] // 16, p["BN"] // p["WN"] // 16

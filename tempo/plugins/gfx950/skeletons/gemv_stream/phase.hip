@@ -32,6 +32,11 @@
 // activations) is peeled.  Requirements (launcher): N % 256 == 0, N / 256 % 4 == 0 with
 // NS = ceil(N / 256 / 16) (>= D when MB > 0), K % 1024 == 0, 16-byte aligned A and Wq, 4-byte
 // aligned scale and zero, and (fmt 2) group 128.
+// EPI = 1 (fused gate/up; p.N below is the output width, W holds the gate rows then, from row
+// `up`, the up rows): workgroup b owns the output columns [b cwg, (b+1) cwg) with cwg = N / 256
+// (a multiple of 4), and its rwg = 2 cwg rows are cwg gate rows followed by the cwg matching up
+// rows -- a lane picks its row's source by which half it falls in.  The output image then holds
+// the fp16 gate and up results side by side, and the store writes fp16_rn(silu(g) * u).
 // ============================================================================================
 struct PhaseArgs {
   const _Float16* A;
@@ -40,7 +45,9 @@ struct PhaseArgs {
   const uint8_t* zero;
   _Float16* C;
   int M, K, lda, ldb, ldc;
-  int rwg;   // weight rows per workgroup (N / 256)
+  int rwg;   // weight rows per workgroup (N / 256; EPI: 2 cwg)
+  int cwg;   // output columns per workgroup (rwg; EPI: N / 256)
+  long up;   // EPI: first row of the up half of W (the output width N)
   int G;     // groups of 128 k per row (K / 128)
   int spc;   // 128-k steps per wave (K / 1024)
   int stg_off, out_off, meta_off, meta_s_off;  // LDS byte offsets
@@ -54,7 +61,7 @@ __device__ __forceinline__ void unroll_for(F&& f) {
   }
 }
 
-template <int MB, int NS, int D, int BFMT>
+template <int MB, int NS, int D, int BFMT, int EPI = 0>
 struct StreamPhase {
   static constexpr int NWV = 8;                  // waves = k chunks per workgroup
   static constexpr int L = 2;                    // weight copies per step
@@ -86,17 +93,17 @@ struct StreamPhase {
   }
 };
 
-template <int MB, int NS, int D, int BFMT>
+template <int MB, int NS, int D, int BFMT, int EPI = 0>
 __global__ __launch_bounds__(512, 1) void k_stream_phase(PhaseArgs p) {
-  using SP = StreamPhase<MB, NS, D, BFMT>;
+  using SP = StreamPhase<MB, NS, D, BFMT, EPI>;
   constexpr int NWV = SP::NWV, L = SP::L, LA = SP::LA, SLOT = SP::SLOT, MBE = SP::MBE;
   constexpr int NSX = NS * 16;  // output image row length (columns)
   extern __shared__ __attribute__((aligned(1024))) uint8_t dsm[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r16 = lane & 15, kg = lane >> 4;
-  const int rwg = p.rwg, spc = p.spc;
-  const long row0 = (long)blockIdx.x * rwg;
+  const int rwg = p.rwg, cwg = p.cwg, spc = p.spc;
+  const long row0 = (long)blockIdx.x * cwg;  // first row (EPI: of the gate half)
   const int kbeg = wave * spc * 128;
   uint8_t* ring = dsm + wave * D * SLOT;
   uint8_t* stg = dsm + p.stg_off + wave * SP::stg_wave(p.G);
@@ -115,12 +122,18 @@ __global__ __launch_bounds__(512, 1) void k_stream_phase(PhaseArgs p) {
                                          4, 0, 0);
     }
   };
-  if constexpr (BFMT == 1) {
-    copy_block(dsm + p.meta_s_off, reinterpret_cast<const uint8_t*>(p.scale + row0), rwg * 2);
-  } else {
-    copy_block(dsm + p.meta_off, p.zero + row0 * p.G, rwg * p.G);
-    copy_block(dsm + p.meta_s_off, reinterpret_cast<const uint8_t*>(p.scale + row0 * p.G),
-               rwg * 2 * p.G);
+  // (EPI: the gate block, then the up block behind it, in the rows' workgroup order)
+#pragma unroll
+  for (int half = 0; half < 1 + EPI; ++half) {
+    const long r = row0 + half * p.up;
+    if constexpr (BFMT == 1) {
+      copy_block(dsm + p.meta_s_off + half * cwg * 2, reinterpret_cast<const uint8_t*>(p.scale + r),
+                 cwg * 2);
+    } else {
+      copy_block(dsm + p.meta_off + half * cwg * p.G, p.zero + r * p.G, cwg * p.G);
+      copy_block(dsm + p.meta_s_off + half * cwg * 2 * p.G,
+                 reinterpret_cast<const uint8_t*>(p.scale + r * p.G), cwg * 2 * p.G);
+    }
   }
   // activation copies of phase s: copy (mb, h, q) carries lane l's 16 bytes -- row 16 mb + l % 16,
   // k kbeg + 128 s + 64 h + 16 (l / 16) + 8 q -- read back by the same lane; MB = 0: one dword per
@@ -150,12 +163,14 @@ __global__ __launch_bounds__(512, 1) void k_stream_phase(PhaseArgs p) {
   // logical chunk (l%8) ^ key(row); a lane whose row of the last slab lies past the workgroup's
   // rows fetches the dummy line instead
   const uint8_t* wsrc[2];
+  const uint8_t* wsrc_up[2];  // EPI: rows of the up half (workgroup row v >= cwg)
   int wrow[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     wrow[i] = 8 * i + lane / 8;
     const int c = (lane % 8) ^ line_key(wrow[i]);
     wsrc[i] = p.B + (row0 + wrow[i]) * p.ldb + kbeg + c * 16;
+    wsrc_up[i] = EPI ? p.B + (p.up + row0 + wrow[i] - cwg) * p.ldb + kbeg + c * 16 : wsrc[i];
   }
   const long slab_stride = 16L * p.ldb;
   // copies of step (s, sl) into ring slot `slot`; past = beyond the chunk's last step.  One copy
@@ -166,7 +181,8 @@ __global__ __launch_bounds__(512, 1) void k_stream_phase(PhaseArgs p) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const bool real = !past && (sl < NS - 1 || 16 * sl + wrow[i] < rwg);
-      const uint8_t* src = real ? wsrc[i] + sl * slab_stride + s * 128 : dummy;
+      const uint8_t* base = EPI && 16 * sl + wrow[i] >= cwg ? wsrc_up[i] : wsrc[i];
+      const uint8_t* src = real ? base + sl * slab_stride + s * 128 : dummy;
       __builtin_amdgcn_global_load_lds((void*)src, (lds_void_stream_t*)(dst + i * 1024), 16, 0,
                                        2 /* nt */);
     }
@@ -304,11 +320,20 @@ __global__ __launch_bounds__(512, 1) void k_stream_phase(PhaseArgs p) {
   __builtin_amdgcn_s_waitcnt(0xC07F);
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
-  // rows m < M of the workgroup's rwg output columns, 8 bytes per thread and pass
-  const int cpr = rwg / 4;
+  // rows m < M of the workgroup's cwg output columns, 8 bytes per thread and pass (EPI: the
+  // gate result of column c and the up result cwg columns further in the image)
+  const int cpr = cwg / 4;
   for (int i = threadIdx.x; i < p.M * cpr; i += 64 * NWV) {
     const int m = i / cpr, c = i - m * cpr;
-    const u32x2 v = *reinterpret_cast<const u32x2*>(outl + m * NSX + 4 * c);
+    u32x2 v = *reinterpret_cast<const u32x2*>(outl + m * NSX + 4 * c);
+    if constexpr (EPI) {
+      const f16x4 g = __builtin_bit_cast(f16x4, v);
+      const f16x4 u = *reinterpret_cast<const f16x4*>(outl + m * NSX + cwg + 4 * c);
+      f16x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = silu_mul_f16((float)g[e], (float)u[e]);
+      v = __builtin_bit_cast(u32x2, o);
+    }
     *reinterpret_cast<u32x2*>(p.C + (long)m * p.ldc + row0 + 4 * c) = v;
   }
 }

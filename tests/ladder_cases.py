@@ -221,7 +221,9 @@ W8 = {
 W8_GATE_UP = {
     1: [
         ("gl0r1n2d2", 1, 17408, 5120),
-        ("gl1r1n4d2t", 16, 17408, 5120),   # tail grid: 2 rounds of paired workgroups, 64 tail pairs
+        ("gp1n9d4", 16, 17408, 5120),      # 68 output columns (136 rows) per CU
+        ("gp1n9d4", 7, 18432, 1024),       # 72 columns per CU, one phase
+        ("gl1r1n4d2t", 16, 17408, 3840),   # tail grid: 2 rounds of paired workgroups, 64 tail pairs
         ("gl1r1n4d2t", 9, 12288, 5120),    # ragged M; whole rounds and a full tail round
         ("gl1r1n4d3", 16, 13312, 5120),    # 320 remaining slabs: past the tail grid
         ("gl1r1n2d4", 8, 7680, 3840),
@@ -238,13 +240,17 @@ W8_GATE_UP = {
         ("gi8x256w1x4k64s3t", 512, 17408, 1024),   # output columns in two parts
     ],
     2: [
-        ("gl0r1n2d2", 1, 17408, 5120),
-        ("gl1r1n4d2t", 16, 17408, 5120),   # tail grid: 2 rounds of paired workgroups, 64 tail pairs
+        ("gp0n9d4", 1, 17408, 5120),
+        ("gl0r1n2d2", 1, 17408, 3840),
+        ("gp1n9d4", 16, 17408, 5120),
+        ("gp1n9d4", 12, 17408, 2048),
+        ("gl1r1n4d2t", 16, 17408, 3840),   # tail grid: 2 rounds of paired workgroups, 64 tail pairs
         ("gl1r1n4d2t", 9, 12288, 5120),    # ragged M; whole rounds and a full tail round
         ("gl1r1n4d3", 16, 13312, 5120),    # 320 remaining slabs: past the tail grid
         ("gl1r1n2d4", 8, 7680, 3840),
-        ("gl2r1n8d2t", 32, 17408, 5120),
-        ("gl2r1n8d2t", 20, 17408, 5120),   # ragged M
+        ("gp2n9d4", 32, 17408, 5120),
+        ("gp2n9d4", 20, 17408, 5120),      # ragged M
+        ("gl2r1n8d2t", 32, 17408, 3840),
         ("gl2r1n4d2", 32, 12288, 5120),
         ("gl2r1n2d4", 32, 7680, 3840),
         ("g1a_r1u8", 1, 512, 66048),
