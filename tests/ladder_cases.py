@@ -56,6 +56,27 @@ FP16 = [
 
 # Strided operands and an 8-byte-aligned C (its rows take the 8-byte store path): (row, M, N, K,
 # extra elements per row of A, B, C)
+# W8A16 rows on views into wider buffers: (tag, M, N, K, lda - K, ldw - K, ldc - N); ldw keeps
+# 16-byte weight rows, ldc = N + 4 leaves C rows 8-byte aligned only
+W8_STRIDED = {
+    1: [
+        ("p1n9d4", 16, 34816, 5120, 8, 16, 4),
+        ("p0n2d2", 1, 5120, 5120, 8, 16, 4),
+        ("l0r1d2w", 1, 34816, 5120, 8, 16, 4),
+        ("i8x128x128w1x4k128s2w256", 128, 7168, 5120, 8, 16, 4),
+    ],
+    2: [
+        ("p0n9d3", 1, 34816, 5120, 8, 16, 4),
+        ("p1n9d4", 9, 34816, 5120, 16, 32, 8),
+        ("p2n9d4", 32, 34816, 5120, 8, 16, 4),
+        ("l2r1n8d2t", 32, 34816, 3840, 8, 16, 4),
+    ],
+}
+W8_GATE_UP_STRIDED = {
+    1: [("gp1n9d4", 16, 17408, 5120, 8, 16, 4)],
+    2: [("gp0n9d4", 1, 17408, 5120, 8, 16, 4), ("gp2n9d4", 32, 17408, 5120, 8, 16, 4)],
+}
+
 FP16_STRIDED = [
     ("l1r1d4", 16, 3840, 3840, 8, 16, 4),
     ("i64x128k64s4w256", 64, 3840, 3840, 8, 8, 4),

@@ -136,3 +136,57 @@ def test_w8a16_gate_up_row(gpu, fmt, case):
                                 C=poisoned((M, N), gpu))
     torch.cuda.synchronize()
     _check(host(C), O.gemm_gate_up_w8a16(A, q, s, z, 128, fmt), tag)
+
+
+def _strided_w8(gpu, A, q, s, z, M, N, K, pa, pb, pc):
+    """A, q as views into buffers pa / pb wider, C a view pc columns narrower than its buffer."""
+    Aw = np.zeros((M, K + pa), np.float16)
+    Aw[:, :K] = A
+    qw = np.zeros((q.shape[0], K + pb), q.dtype)
+    qw[:, :K] = q
+    dA, dq = dev(Aw, gpu)[:, :K], dev(qw, gpu)[:, :K]
+    Cw = poisoned((M, N + pc), gpu)
+    dC = Cw[:, :N]
+    assert dA.stride(0) == K + pa and dq.stride(0) == K + pb and dC.stride(0) == N + pc
+    return dA, dq, dev(s, gpu), (dev(z, gpu) if z is not None else None), Cw, dC
+
+
+@pytest.mark.parametrize("fmt,case", [(f, c) for f in (1, 2) for c in LC.W8_STRIDED[f]],
+                         ids=lambda v: v if isinstance(v, int) else LC.case_id(v))
+def test_w8a16_row_strided(gpu, fmt, case):
+    """lda > K, ldw > K, ldc > N; the padding columns of C must stay untouched."""
+    import torch
+    from cuda_tempiler_amd import capi
+
+    tag, M, N, K, pa, pb, pc = case
+    say("w8a16 fmt", fmt, "strided row", tag, "M", M, "N", N, "K", K, "pads", pa, pb, pc)
+    assert capi.route(fmt, M, N, K) == tag
+    A = O.randn_f16((M, K), 5 + M, K ** -0.5)
+    q, s, z = _weights(N, K, fmt, 31 + N)
+    dA, dq, ds, dz, Cw, dC = _strided_w8(gpu, A, q, s, z, M, N, K, pa, pb, pc)
+    capi.gemm_w8a16(dA, dq, ds, dz, fmt=fmt, group=128, C=dC)
+    torch.cuda.synchronize()
+    full = host(Cw)
+    assert O.count_poison(full[:, N:]) == full[:, N:].size, "padding columns written"
+    _check(np.ascontiguousarray(full[:, :N]), O.gemm_w8a16(A, q, s, z, 128, fmt), tag)
+
+
+@pytest.mark.parametrize("fmt,case", [(f, c) for f in (1, 2) for c in LC.W8_GATE_UP_STRIDED[f]],
+                         ids=lambda v: v if isinstance(v, int) else LC.case_id(v))
+def test_w8a16_gate_up_row_strided(gpu, fmt, case):
+    """The fused gate/up on views into wider buffers (2N weight rows of ldw > K)."""
+    import torch
+    from cuda_tempiler_amd import capi
+
+    tag, M, N, K, pa, pb, pc = case
+    say("w8a16 gate_up fmt", fmt, "strided row", tag, "M", M, "N", N, "K", K, "pads", pa, pb, pc)
+    assert capi.route(3 + fmt, M, N, K) == tag
+    A = O.randn_f16((M, K), 7 + M, 3 * K ** -0.5)
+    q, s, z = _weights(2 * N, K, fmt, 13 + N)
+    s = O.f2h(O.h2f(s) * 2)
+    dA, dq, ds, dz, Cw, dC = _strided_w8(gpu, A, q, s, z, M, N, K, pa, pb, pc)
+    capi.gemm_w8a16_gate_up(dA, dq, ds, dz, fmt=fmt, group=128, C=dC)
+    torch.cuda.synchronize()
+    full = host(Cw)
+    assert O.count_poison(full[:, N:]) == full[:, N:].size, "padding columns written"
+    _check(np.ascontiguousarray(full[:, :N]), O.gemm_gate_up_w8a16(A, q, s, z, 128, fmt), tag)
