@@ -39,6 +39,10 @@ Extra fields of the one JSON line:
                 cores' load within microseconds, so only a counter read during the dispatch
                 gives it) -- and the matrix-core peak at that clock (256 CUs x 4096 flop/clk x
                 sclk), the reference's peak_tflops_1530 at its locked clock (manifest.json:119).
+  roofline.sclk_live_mhz / peak_at_sclk_live / frac_at_sclk_live
+                the same clock read on this box during the run: amd-smi's gfx clocks sampled
+                while C1 runs back to back after the timed steps (a short-window average, so the
+                load lasts across the reads), the median of the reads.
   decode[].hbm_frac_measured
                 GB/s against the MEASURED pure-read HBM rate of the plugin's rate table
                 (HBM.READ_PURE, taken by tempo.plugins.gfx950.calibrate on a clean card), next
@@ -330,6 +334,45 @@ def read_sclk():
     return None
 
 
+def live_sclk(fn, stream, samples=5, settle_s=0.3, gap_s=0.1, budget_s=8.0):
+    """The engine clock of this box under a sustained C1 load: C1 launched back to back while a
+    second thread reads amd-smi's gfx clocks (`samples` reads, each the mean over the XCDs, after
+    `settle_s` of load); the median read, or None when amd-smi gives nothing.  amd-smi's clock is
+    a short-window average, so it is read under a load that lasts across the reads -- the timed
+    run itself is too short for that -- and it complements the counter-derived clock of
+    read_sclk, which is the dispatch's own but comes from the committed profile's box."""
+    import threading
+
+    from tempo.plugins.gfx950 import card
+
+    vals = []
+
+    def sampler():
+        time.sleep(settle_s)
+        for j in range(samples + 1):
+            txt = card._run([card.AMD_SMI, "metric", "-g", "0", "--clock", "--json"], timeout=5)
+            m = card.parse_metric(txt or "", 0)
+            # the first read after the load starts still reports the idle clock: dropped
+            if j > 0 and "gfx_clock_mhz" in m:
+                vals.append(round(m["gfx_clock_mhz"], 1))
+            time.sleep(gap_s)
+
+    t = threading.Thread(target=sampler, daemon=True)
+    t.start()
+    t0 = time.time()
+    i = 0
+    while t.is_alive() and time.time() - t0 < budget_s:
+        for _ in range(16):  # ~6 ms of C1 per batch; the host never runs far ahead
+            fn(i)
+            i += 1
+        stream.synchronize()
+    t.join(timeout=1.0)
+    if not vals:
+        return None
+    return {"median_mhz": float(np.median(vals)), "samples_mhz": vals, "launches": i,
+            "source": "amd-smi metric --clock (mean over XCDs) under back-to-back C1 launches"}
+
+
 def decode_lines(steps):
     import torch
     from cuda_tempiler_amd import capi
@@ -584,6 +627,8 @@ def main():
     traffic = read_traffic()
     sclk = read_sclk()
     peak_sclk = 256 * 4096 * sclk["median_mhz"] * 1e6 / 1e12 if sclk else None
+    live = live_sclk(fn, stream)
+    peak_live = 256 * 4096 * live["median_mhz"] * 1e6 / 1e12 if live else None
     line = {
         "metric": METRIC, "value": round(tflops, 1), "unit": "TFLOP/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "settle": settle,
@@ -599,6 +644,9 @@ def main():
                      "algorithmic_bytes": 2 * (M * K + N * K + M * N),
                      "sclk_mhz": sclk, "peak_at_sclk": round(peak_sclk, 1) if sclk else None,
                      "frac_at_sclk": round(tflops / peak_sclk, 4) if sclk else None,
+                     "sclk_live_mhz": live,
+                     "peak_at_sclk_live": round(peak_live, 1) if live else None,
+                     "frac_at_sclk_live": round(tflops / peak_live, 4) if live else None,
                      "mfma_measured": measured_rate("tensor_measured")},
     }
     del C
