@@ -115,7 +115,10 @@ SWEEP_NK = ((15360, 3840), (3840, 15360), (7168, 5120), (5120, 6144), (34816, 51
             # the line kernel's tail grid: one slab left, none left, one per CU left, too many
             # waves per CU, fmt 2 metadata past the LDS, more rounds
             (16400, 256), (16384, 384), (36864, 128), (69632, 5120), (34816, 16384),
-            (32784, 256), (49152, 5120))
+            (32784, 256), (49152, 5120),
+            # the phase-ordered rows: 136 / 144 / 24 / 20 rows per CU, K % 1024, the gate/up width
+            (36864, 2048), (6144, 1024), (5120, 3072), (34816, 3840), (17408, 5120),
+            (18432, 1024), (17408, 3840))
 
 
 def test_compiled_route_agrees_with_select_fp16():
