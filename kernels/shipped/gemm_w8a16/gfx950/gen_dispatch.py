@@ -36,6 +36,10 @@ HEAD = """// GENERATED from select.py -- do not edit.  Regenerate with:
 
 def instantiation(kind, p, epi=0):
     tail = ",%d" % epi if epi else ""
+    if kind == "phase" and p.get("KS", 1) > 1:  # k slices across workgroups: a workspace row
+        if epi:
+            raise ValueError("k slices take the plain epilogue")
+        return "launch_phase_ks<%d,%d,%d,%d>" % (p["MB"], p["NS"], p["D"], p["KS"])
     if kind == "phase":
         return "launch_phase%s<%d,%d,%d>" % ("_gu" if epi else "", p["MB"], p["NS"], p["D"])
     if kind == "line" and p.get("MT"):  # row tiles x slab groups
@@ -81,7 +85,13 @@ def instantiation(kind, p, epi=0):
 
 def condition(sel, kind, p, m_max, n_min=0, gate_up=False):
     if kind == "phase":
-        fit = "(phase%s_fits<%d,%d,%d>(p))" % ("_gu" if gate_up else "", p["MB"], p["NS"], p["D"])
+        if p.get("KS", 1) > 1:
+            fit = "(phase_ks_fits<%d,%d,%d,%d>(p))" % (p["MB"], p["NS"], p["D"], p["KS"])
+        else:
+            fit = "(phase%s_fits<%d,%d,%d>(p))" % ("_gu" if gate_up else "", p["MB"], p["NS"],
+                                                    p["D"])
+        if "KMIN" in p:
+            fit += " && p.K >= %d" % p["KMIN"]
         if "NMAX" in p:
             fit += " && p.N < %d" % p["NMAX"]
         if "KMAX" in p:

@@ -290,7 +290,7 @@ inline bool phase_layout(const W8A16Params& p, PhaseArgs* a, int* lds) {
   // the workgroups' metadata blocks are copied in 4-byte pieces (rwg % 4 keeps them aligned)
   if (((reinterpret_cast<uintptr_t>(p.scale) | reinterpret_cast<uintptr_t>(p.zero)) % 4) != 0)
     return false;
-  if (SP::lds(G) > 160 * 1024) return false;
+  if (SP::lds(G, G) > 160 * 1024) return false;
   a->A = p.A;
   a->B = reinterpret_cast<const uint8_t*>(p.Wq);
   a->scale = p.scale;
@@ -305,12 +305,15 @@ inline bool phase_layout(const W8A16Params& p, PhaseArgs* a, int* lds) {
   a->cwg = cwg;
   a->up = EPI ? p.N : 0;
   a->G = G;
-  a->spc = p.K / 1024;
+  a->steps = G;
+  a->ks = 1;
+  a->N = p.N;
+  a->part = nullptr;
   a->stg_off = SP::ring_bytes();
   a->out_off = a->stg_off + SP::stg_bytes(G);
   a->meta_off = a->out_off + SP::out_bytes();
-  a->meta_s_off = a->meta_off + SP::meta_z_bytes(G);
-  *lds = SP::lds(G);
+  a->meta_s_off = a->meta_off + SP::meta_z_bytes(G, G);
+  *lds = SP::lds(G, G);
   return true;
 }
 template <int MB, int NS, int D>
@@ -334,6 +337,78 @@ inline hipError_t launch_phase(const W8A16Params& p, hipStream_t s) {
   }
   return hipGetLastError();
 }
+// KS k slices across the workgroups (KSL instantiation): 256 / KS row groups of N / (256 / KS)
+// rows (a multiple of 4, NS slabs), K / KS k each in at least 8 steps of 128 (a step or more per
+// wave); the slices' fp32 sums in the workspace, added in slice order by k_splitk_reduce.
+template <int MB, int NS, int D, int BFMT, int KS>
+inline bool phase_ks_layout(const W8A16Params& p, PhaseArgs* a, int* lds) {
+  using SP = StreamPhase<MB, NS, D, BFMT, 0, 1>;
+  static_assert(SP::CUS % KS == 0, "row groups");
+  constexpr int groups = SP::CUS / KS;
+  if (p.M > 16 * SP::MBE || (MB == 0 && p.M != 1)) return false;
+  if (p.N % groups || p.K % (128 * KS)) return false;
+  const int rwg = p.N / groups, S = p.K / (128 * KS), G = p.K / 128;
+  if (rwg % 4 || (rwg + 15) / 16 != NS || S < SP::NWV) return false;
+  if (BFMT == 2 && p.group != 128) return false;
+  if ((reinterpret_cast<uintptr_t>(p.scale) % 4) != 0) return false;  // fmt 1: row-scale block
+  if (SP::lds(G, S) > 160 * 1024) return false;
+  a->A = p.A;
+  a->B = reinterpret_cast<const uint8_t*>(p.Wq);
+  a->scale = p.scale;
+  a->zero = p.zero;
+  a->C = p.C;
+  a->M = p.M;
+  a->K = p.K;
+  a->lda = p.lda;
+  a->ldb = p.ldw;
+  a->ldc = p.ldc;
+  a->rwg = rwg;
+  a->cwg = rwg;
+  a->up = 0;
+  a->G = G;
+  a->steps = S;
+  a->ks = KS;
+  a->N = p.N;
+  a->part = nullptr;
+  a->stg_off = SP::ring_bytes();
+  a->out_off = a->stg_off + SP::stg_bytes(S);
+  a->meta_off = a->out_off + SP::out_bytes();
+  a->meta_s_off = a->meta_off + SP::meta_z_bytes(G, S);
+  *lds = SP::lds(G, S);
+  return true;
+}
+template <int MB, int NS, int D, int KS>
+inline bool phase_ks_fits(const W8A16Params& p) {
+  PhaseArgs a;
+  int lds = 0;
+  return p.fmt == 1 ? phase_ks_layout<MB, NS, D, 1, KS>(p, &a, &lds)
+                    : phase_ks_layout<MB, NS, D, 2, KS>(p, &a, &lds);
+}
+template <int MB, int NS, int D, int KS>
+inline hipError_t launch_phase_ks(const W8A16Params& p, hipStream_t s, const Workspace& w) {
+  PhaseArgs a;
+  int lds = 0;
+  const bool ok = p.fmt == 1 ? phase_ks_layout<MB, NS, D, 1, KS>(p, &a, &lds)
+                             : phase_ks_layout<MB, NS, D, 2, KS>(p, &a, &lds);
+  if (!ok) return hipErrorInvalidConfiguration;
+  const size_t bytes = (size_t)KS * p.M * p.N * sizeof(float);
+  if (w.need) {
+    *w.need = bytes;
+    return hipSuccess;
+  }
+  hipError_t werr = hipSuccess;
+  a.part = workspace_for(w, bytes, s, &werr);
+  if (!a.part) return werr;
+  constexpr int CUS = StreamPhase<MB, NS, D, 1, 0, 1>::CUS, NWV = StreamPhase<MB, NS, D, 1, 0, 1>::NWV;
+  if (p.fmt == 1)
+    hipLaunchKernelGGL((k_stream_phase<MB, NS, D, 1, 0, 1>), dim3(CUS), dim3(64 * NWV), lds, s, a);
+  else
+    hipLaunchKernelGGL((k_stream_phase<MB, NS, D, 2, 0, 1>), dim3(CUS), dim3(64 * NWV), lds, s, a);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  return launch_reduce(a.part, KS, p.M, p.N, p.C, p.ldc, s);
+}
+
 template <int MB, int NS, int D>
 inline bool phase_gu_fits(const W8A16Params& p) {
   PhaseArgs a;

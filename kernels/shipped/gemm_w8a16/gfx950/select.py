@@ -46,6 +46,9 @@ LADDER = [
     (16, 12288, "p1n9d4", "phase", dict(MB=1, NS=9, D=4, KMAX=12288)),
     (16, 12288, "l1r1n4d2t", "line", dict(MB=1, R=1, D=2, SN=4, W=2048, TL=1)),
     (16, 12288, "l1r1n4d3", "line", dict(MB=1, R=1, D=3, SN=4, W=2048)),
+    # uint8, long K: the phase-ordered kernel with 8 k slices over all 256 CUs (32 row groups of
+    # 160 rows, 17 steps of 128 k each): 1.05x the row below at (16, 5120, 17408) (int8 1.00x)
+    (16, 0, "p1n10d4k8", "phase", dict(MB=1, NS=10, D=4, KS=8, KMIN=12288, fmts=(2,))),
     # long K: k slices (1.17x / 1.25x the row below at (16, 5120, 17408))
     (16, 0, "l1r1n4d2k8", "line", dict(MB=1, R=1, D=2, SN=4, W=2048, KS=8, KMIN=12288)),
     # narrow N: one slab wave per ring, k slices over the part (1.43-1.47x the two-slab
@@ -60,6 +63,8 @@ LADDER = [
     # long K: k slices, eight slab waves per activation ring (1.37x / 1.46x the row below at
     # (32, 5120, 17408), int8 / uint8)
     (32, 0, "l2r1n8d3k8", "line", dict(MB=2, R=1, D=3, SN=8, W=1024, KS=8, KMIN=12288, fmts=(1,))),
+    # uint8: the phase-ordered kernel with 8 k slices, 1.07x the row below at (32, 5120, 17408)
+    (32, 0, "p2n10d4k8", "phase", dict(MB=2, NS=10, D=4, KS=8, KMIN=12288, fmts=(2,))),
     (32, 0, "l2r1n8d2k8", "line", dict(MB=2, R=1, D=2, SN=8, W=2048, KS=8, KMIN=12288, fmts=(2,))),
     # narrow N: one slab wave per ring, k slices (1.53-1.62x at (32, 1024, 5120))
     (32, 0, "l2r1d2k8", "line", dict(MB=2, R=1, D=2, W=2048, KS=8, NMAX=2048)),
@@ -284,15 +289,17 @@ PHASE_WAVES = 8  # k_stream_phase: waves (k chunks) per workgroup
 
 def phase_lds(p, K, fmt):
     """LDS of k_stream_phase (StreamPhase::lds of the kernel): the weight rings, the activation
-    staging (after the loop: the chunk partial sums), the output image, the metadata."""
-    mb, ns, d = p["MB"], p["NS"], p["D"]
+    staging (after the loop: the chunk partial sums), the output image (whole K only), the
+    metadata (k slices: the slice's groups, 4 bytes apart)."""
+    mb, ns, d, ks = p["MB"], p["NS"], p["D"], p.get("KS", 1)
     mbe = max(1, mb)
-    G = K // 128
-    stg = 4 * mb * 1024 if mb else G // PHASE_WAVES * 256  # M = 1: every phase's slice
+    G, S = K // 128, K // (128 * ks)
+    stg = 4 * mb * 1024 if mb else -(-S // PHASE_WAVES) * 256  # M = 1: every phase's slice
     kib = lambda b: -(-b // 1024) * 1024  # noqa: E731
+    meta = ((kib(ns * 16 * 4 * S) * 2 if ks > 1 else kib(ns * 16 * G) + kib(ns * 32 * G))
+            if fmt == 2 else kib(ns * 32))
     return (PHASE_WAVES * d * 2048 + max(PHASE_WAVES * stg, 2 * PHASE_WAVES * mbe * 1024)
-            + kib(mbe * 16 * ns * 16 * 2) + (kib(ns * 16 * G) if fmt == 2 else 0)
-            + kib(ns * 32 * G if fmt == 2 else ns * 32))
+            + (0 if ks > 1 else kib(mbe * 16 * ns * 16 * 2)) + meta)
 
 
 def phase_fits(p, M, N, K, fmt):
@@ -300,12 +307,15 @@ def phase_fits(p, M, N, K, fmt):
     per CU over N / 256 rows (a multiple of 4; NS slabs of 16, the last 4 .. 16), K / 8 k per
     wave in steps of 128, a ring no deeper than a phase where activations ride it (M > 1), and
     the LDS."""
-    mb = p["MB"]
+    mb, ks = p["MB"], p.get("KS", 1)
     if M > 16 * max(1, mb) or (mb == 0 and M != 1):
         return False
-    if N % LINE_CUS or K % (PHASE_WAVES * LINE_K_STEP):
+    groups = LINE_CUS // ks  # KS > 1: k slices across the workgroups (phase_ks_layout)
+    if N % groups or K % (ks * LINE_K_STEP) or K // (ks * LINE_K_STEP) < PHASE_WAVES:
         return False
-    rwg = N // LINE_CUS
+    if ks == 1 and K % (PHASE_WAVES * LINE_K_STEP):
+        return False
+    rwg = N // groups
     if rwg % 4 or -(-rwg // 16) != p["NS"] or (mb > 0 and p["NS"] < p["D"]):
         return False
     return phase_lds(p, K, fmt) <= LINE_LDS
@@ -334,9 +344,9 @@ def _fits(kind, p, M, N, K, fmt=1):
     if kind == "line" and p.get("TL"):  # tail grid: whole slabs, one k chunk
         return (N % (STREAM_N_ROWS * p["R"]) == 0 and K % LINE_K_STEP == 0
                 and line_tail_fits(p, N, K, fmt))
-    if kind == "phase":  # NMAX / KMAX (optional): narrower N / shorter K only
+    if kind == "phase":  # NMAX / KMIN / KMAX (optional): narrower N / longer / shorter K only
         return (phase_fits(p, M, N, K, fmt) and N < p.get("NMAX", 1 << 30)
-                and K < p.get("KMAX", 1 << 30))
+                and K >= p.get("KMIN", 0) and K < p.get("KMAX", 1 << 30))
     if kind == "line" and p.get("MT"):  # row tiles: whole slabs, whole k per workgroup
         return (N % (STREAM_N_ROWS * p["R"]) == 0 and K % LINE_K_STEP == 0 and K <= LINE_K_MAX
                 and N < p.get("NMAX", 1 << 30) and line_mt_fits(p, K, fmt))

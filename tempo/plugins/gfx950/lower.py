@@ -57,7 +57,7 @@ _ENTRY = {
                ("common/cdna4.h", "gemv_stream/kernel.hip")),
     "shared": ("k_stream_sh", ("MB", "R", "U", "BFMT", "SN", "TPB", "EPI"), "StreamArgs",
                ("common/cdna4.h", "gemv_stream/kernel.hip")),
-    "phase": ("k_stream_phase", ("MB", "NS", "D", "BFMT", "EPI"), "PhaseArgs",
+    "phase": ("k_stream_phase", ("MB", "NS", "D", "BFMT", "EPI", "KSL"), "PhaseArgs",
               ("common/cdna4.h", "gemv_stream/kernel.hip", "gemv_stream/phase.hip")),
 }
 _ENTRY["fmha"] = ("fmha::k_fmha_fwd", ("D", "CAUSAL"),
@@ -75,9 +75,9 @@ KIND_FLAGS = {"ilv": ("-mllvm", "-amdgpu-sched-strategy=iterative-minreg"),
               "ilv8": ("-mllvm", "-amdgpu-sched-strategy=iterative-minreg")}
 # trailing template parameters with a default in the skeleton: named only when the hyperform
 # sets them (EPI = 1 is the fused gate/up epilogue of the decode kernels)
-_OPTIONAL = frozenset({"EPI", "SN", "TPB", "SPLIT"})
+_OPTIONAL = frozenset({"EPI", "SN", "TPB", "SPLIT", "KSL"})
 # default of an optional parameter left out in front of one that is named
-_DEFAULT = {"EPI": 0, "SN": 1, "TPB": 1024, "SPLIT": 0}
+_DEFAULT = {"EPI": 0, "SN": 1, "TPB": 1024, "SPLIT": 0, "KSL": 0}
 
 
 def _order(kind: str, p: dict) -> tuple:
@@ -173,10 +173,11 @@ class Gfx950Skeletons:
             # activation fragments (16 MBE), a step's weight bytes and their fp16 expansion (16),
             # fmt 2 zero-points and scales and their LDS addresses per slab (2 NS + 8), copy
             # sources and loop state (48), the gate/up epilogue's up-row copy sources and half
-            # selects (8); pessimistic edge x1.25 (measured: 120-245 registers)
+            # selects (8), the k-slice's partial-row addresses and slice offsets (16);
+            # pessimistic edge x1.25 (measured: 120-256 registers)
             mbe = max(1, p["MB"])
             regs = (4 * p["NS"] * mbe + 16 * mbe + 16 + (2 * p["NS"] + 8 if p["BFMT"] == 2 else 0)
-                    + 48 + (8 if p.get("EPI") else 0))
+                    + 48 + (8 if p.get("EPI") else 0) + (16 if p.get("KSL") else 0))
             return regs, int(regs * 1.25), space.phase_lds(int(op.shapes["K"]), p)
         if kind in ("ilv", "ilv8"):
             tm, tn = p["BM"] // p["WM"] // 16, p["BN"] // p["WN"] // 16
@@ -335,7 +336,7 @@ class Gfx950Skeletons:
             # copied and read once per NS steps
             mbe = max(1, p["MB"])
             act = 4 * p["MB"] * 1024 if p["MB"] else 256
-            reps = p["NS"] * (K // (128 * space.PHASE_WAVES)) * rounds
+            reps = p["NS"] * -(-K // (128 * p.get("KS", 1) * space.PHASE_WAVES)) * rounds
             flops = 4 * mbe * space.MFMA_FLOPS[16]
             vmem = 2048 + act // p["NS"]
             lds_rd = 2048 + act // p["NS"]
@@ -382,6 +383,8 @@ class Gfx950Skeletons:
         elif kind == "line":
             sp = space.line_split(N, K, p)
             hbm += 2 * 4 * M * N * sp[3] if sp and sp[3] > 1 else 0
+        elif kind == "phase" and p.get("KS", 1) > 1:
+            hbm += 2 * 4 * M * N * p["KS"]
         cus = int(_M.rate("GEOM.SMS").value)
         atoms.append(Atom(uid=5, kind=AtomKind.MEM_READ, op_id="HBM (device share)",
                           footprint={"HBM": float(hbm) / (cus * max(1, occ.warps_per_sm))},

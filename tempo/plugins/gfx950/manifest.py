@@ -94,6 +94,8 @@ def hyper_params(kind, p, fmt, epi=0):
         params.setdefault("MS", 32)
     if pk in ("ilv", "ilv8") and params.get("SW", 0):
         params["SPLIT"] = 1  # the split-K instantiation of the kernel
+    if pk == "phase" and params.get("KS", 1) > 1:
+        params["KSL"] = 1  # the k-sliced instantiation of the kernel
     if epi:
         params["EPI"] = 1
     return params
@@ -350,6 +352,13 @@ def make(op, rows_files=(), counter_files=()):
         elif kind == "phase":
             fit = ("N %% 256 == 0, N / 256 %% 4 == 0 and ceil(N / 256 / 16) == %d, K %% 1024 == 0, "
                    "LDS <= 160 KiB" % p["NS"])
+            if p.get("KS", 1) > 1:
+                fit = ("N %% (256 / %d) == 0 with N / (256 / %d) rows per workgroup (%% 4 == 0, "
+                       "ceil(rows / 16) == %d), K %% %d == 0 with >= 8 steps per slice, LDS <= "
+                       "160 KiB; %d k slices, fp32 partials added in order"
+                       % (p["KS"], p["KS"], p["NS"], 128 * p["KS"], p["KS"]))
+            if "KMIN" in p:
+                fit += " and K >= %d" % p["KMIN"]
             if "NMAX" in p:
                 fit += " and N < %d" % p["NMAX"]
             if "KMAX" in p:

@@ -37,6 +37,13 @@
 // (a multiple of 4), and its rwg = 2 cwg rows are cwg gate rows followed by the cwg matching up
 // rows -- a lane picks its row's source by which half it falls in.  The output image then holds
 // the fp16 gate and up results side by side, and the store writes fp16_rn(silu(g) * u).
+// KSL = 1 (k slices across workgroups, plain epilogue): the 256 workgroups are ks slices of K
+// times 256 / ks row groups (N / (256 / ks) rows each); a workgroup's K / ks k (its `steps`
+// 128-k steps) split over the 8 waves as evenly as whole steps allow (the waves run their phases
+// independently; only the final reduction syncs them).  fmt 2 metadata: the slice's groups of the
+// workgroup's rows, one byte / one half per (row, group), 4 bytes apart (sub-dword LDS-DMA).  The
+// slice's fp32 sum of each output goes to part[slice][m][n]; a second kernel adds the slices in
+// order (k_splitk_reduce).
 // ============================================================================================
 struct PhaseArgs {
   const _Float16* A;
@@ -49,7 +56,10 @@ struct PhaseArgs {
   int cwg;   // output columns per workgroup (rwg; EPI: N / 256)
   long up;   // EPI: first row of the up half of W (the output width N)
   int G;     // groups of 128 k per row (K / 128)
-  int spc;   // 128-k steps per wave (K / 1024)
+  int steps; // 128-k steps of a workgroup's k range (K / 128 / ks)
+  int ks;    // KSL: k slices across workgroups
+  int N;     // KSL: row pitch of the partial sums
+  float* part;  // KSL: fp32 partial sums [ks][M][N]
   int stg_off, out_off, meta_off, meta_s_off;  // LDS byte offsets
 };
 
@@ -61,7 +71,7 @@ __device__ __forceinline__ void unroll_for(F&& f) {
   }
 }
 
-template <int MB, int NS, int D, int BFMT, int EPI = 0>
+template <int MB, int NS, int D, int BFMT, int EPI = 0, int KSL = 0>
 struct StreamPhase {
   static constexpr int NWV = 8;                  // waves = k chunks per workgroup
   static constexpr int L = 2;                    // weight copies per step
@@ -71,8 +81,10 @@ struct StreamPhase {
   static constexpr int CUS = 256;                // workgroups: one per CU of the part
   static_assert((MB == 0 || NS >= D) && D >= 2 && (D - 1) * L + LA < 64,
                 "ring depth / vmcnt range");
-  // activation staging per wave: one phase's copies (MB > 0), every phase's slice (MB = 0)
-  static constexpr int stg_wave(int G) { return MB > 0 ? LA * 1024 : G / NWV * 256; }
+  static_assert(!(EPI && KSL), "k slices take the plain epilogue");
+  // activation staging per wave: one phase's copies (MB > 0), every phase's slice (MB = 0) --
+  // S = the workgroup's 128-k steps, at most ceil(S / NWV) per wave
+  static constexpr int stg_wave(int S) { return MB > 0 ? LA * 1024 : (S + NWV - 1) / NWV * 256; }
   // vmcnt of "step (s, sl) landed": LAST = the phase issues no next activations
   static constexpr int wait_of(int sl, bool last) {
     return (D - 1) * L + (MB > 0 && !last && sl > 0 && sl < D ? LA : 0);
@@ -80,33 +92,45 @@ struct StreamPhase {
   // LDS layout (bytes): rings, activation staging (after the loop: the chunk partial sums), the
   // output image, metadata; -1 if it exceeds 160 KiB
   static constexpr int ring_bytes() { return NWV * D * SLOT; }
-  static constexpr int stg_bytes(int G) {
-    return NWV * stg_wave(G) > 2 * NWV * MBE * 1024 ? NWV * stg_wave(G) : 2 * NWV * MBE * 1024;
+  static constexpr int stg_bytes(int S) {
+    return NWV * stg_wave(S) > 2 * NWV * MBE * 1024 ? NWV * stg_wave(S) : 2 * NWV * MBE * 1024;
   }
-  static constexpr int out_bytes() { return (MBE * 16 * NS * 16 * 2 + 1023) / 1024 * 1024; }
-  static constexpr int meta_z_bytes(int G) { return BFMT == 2 ? (NS * 16 * G + 1023) / 1024 * 1024 : 0; }
-  static constexpr int meta_s_bytes(int G) {
-    return ((BFMT == 2 ? NS * 32 * G : NS * 32) + 1023) / 1024 * 1024;
+  static constexpr int out_bytes() {
+    return KSL ? 0 : (MBE * 16 * NS * 16 * 2 + 1023) / 1024 * 1024;
   }
-  static constexpr int lds(int G) {
-    return ring_bytes() + stg_bytes(G) + out_bytes() + meta_z_bytes(G) + meta_s_bytes(G);
+  // metadata per row: whole K, packed (G bytes of z, G halves of s), or the slice's S groups,
+  // 4 bytes apart each (KSL)
+  static constexpr int meta_z_bytes(int G, int S) {
+    return BFMT == 2 ? (NS * 16 * (KSL ? 4 * S : G) + 1023) / 1024 * 1024 : 0;
+  }
+  static constexpr int meta_s_bytes(int G, int S) {
+    return ((BFMT == 2 ? NS * 16 * (KSL ? 4 * S : 2 * G) : NS * 32) + 1023) / 1024 * 1024;
+  }
+  static constexpr int lds(int G, int S) {
+    return ring_bytes() + stg_bytes(S) + out_bytes() + meta_z_bytes(G, S) + meta_s_bytes(G, S);
   }
 };
 
-template <int MB, int NS, int D, int BFMT, int EPI = 0>
+template <int MB, int NS, int D, int BFMT, int EPI = 0, int KSL = 0>
 __global__ __launch_bounds__(512, 1) void k_stream_phase(PhaseArgs p) {
-  using SP = StreamPhase<MB, NS, D, BFMT, EPI>;
+  using SP = StreamPhase<MB, NS, D, BFMT, EPI, KSL>;
   constexpr int NWV = SP::NWV, L = SP::L, LA = SP::LA, SLOT = SP::SLOT, MBE = SP::MBE;
   constexpr int NSX = NS * 16;  // output image row length (columns)
   extern __shared__ __attribute__((aligned(1024))) uint8_t dsm[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r16 = lane & 15, kg = lane >> 4;
-  const int rwg = p.rwg, cwg = p.cwg, spc = p.spc;
-  const long row0 = (long)blockIdx.x * cwg;  // first row (EPI: of the gate half)
-  const int kbeg = wave * spc * 128;
+  const int rwg = p.rwg, cwg = p.cwg, S = p.steps;
+  const int groups = KSL ? SP::CUS / p.ks : SP::CUS;       // row groups
+  const int rg = (int)blockIdx.x % groups, slice = (int)blockIdx.x / groups;
+  const long row0 = (long)rg * cwg;  // first row (EPI: of the gate half)
+  // this wave's steps of the workgroup's S: as even as whole steps allow
+  const int sbase = S / NWV, sextra = S - sbase * NWV;
+  const int spc = sbase + (wave < sextra ? 1 : 0);
+  const int first = wave * sbase + (wave < sextra ? wave : sextra);
+  const int kbeg = (slice * S + first) * 128;
   uint8_t* ring = dsm + wave * D * SLOT;
-  uint8_t* stg = dsm + p.stg_off + wave * SP::stg_wave(p.G);
+  uint8_t* stg = dsm + p.stg_off + wave * SP::stg_wave(S);
   f32x4* red = reinterpret_cast<f32x4*>(dsm + p.stg_off);  // after the loop: [2][NWV][MBE][64]
   _Float16* outl = reinterpret_cast<_Float16*>(dsm + p.out_off);
   const uint8_t* meta_z = dsm + p.meta_off;
@@ -123,16 +147,32 @@ __global__ __launch_bounds__(512, 1) void k_stream_phase(PhaseArgs p) {
     }
   };
   // (EPI: the gate block, then the up block behind it, in the rows' workgroup order)
+  if constexpr (KSL && BFMT == 2) {
+    // the slice's groups of each row: (row r, group j) at 4 (r S + j), byte / half copies
+    const int tot = rwg * S;
+    for (int pc = wave; pc * 64 < tot; pc += NWV) {
+      const int i = pc * 64 + lane;
+      if (i < tot) {
+        const int r = i / S, j = i - r * S;
+        const long gi = (row0 + r) * p.G + slice * S + j;
+        __builtin_amdgcn_global_load_lds((void*)(p.zero + gi), (lds_void_stream_t*)(dsm + p.meta_off + pc * 256),
+                                         1, 0, 0);
+        __builtin_amdgcn_global_load_lds((void*)(p.scale + gi),
+                                         (lds_void_stream_t*)(dsm + p.meta_s_off + pc * 256), 2, 0, 0);
+      }
+    }
+  } else {
 #pragma unroll
-  for (int half = 0; half < 1 + EPI; ++half) {
-    const long r = row0 + half * p.up;
-    if constexpr (BFMT == 1) {
-      copy_block(dsm + p.meta_s_off + half * cwg * 2, reinterpret_cast<const uint8_t*>(p.scale + r),
-                 cwg * 2);
-    } else {
-      copy_block(dsm + p.meta_off + half * cwg * p.G, p.zero + r * p.G, cwg * p.G);
-      copy_block(dsm + p.meta_s_off + half * cwg * 2 * p.G,
-                 reinterpret_cast<const uint8_t*>(p.scale + r * p.G), cwg * 2 * p.G);
+    for (int half = 0; half < 1 + EPI; ++half) {
+      const long r = row0 + half * p.up;
+      if constexpr (BFMT == 1) {
+        copy_block(dsm + p.meta_s_off + half * cwg * 2,
+                   reinterpret_cast<const uint8_t*>(p.scale + r), cwg * 2);
+      } else {
+        copy_block(dsm + p.meta_off + half * cwg * p.G, p.zero + r * p.G, cwg * p.G);
+        copy_block(dsm + p.meta_s_off + half * cwg * 2 * p.G,
+                   reinterpret_cast<const uint8_t*>(p.scale + r * p.G), cwg * 2 * p.G);
+      }
     }
   }
   // activation copies of phase s: copy (mb, h, q) carries lane l's 16 bytes -- row 16 mb + l % 16,
@@ -204,7 +244,7 @@ __global__ __launch_bounds__(512, 1) void k_stream_phase(PhaseArgs p) {
   asm volatile("" ::: "memory");
 
   const int key = line_key(r16);
-  const int g0 = kbeg / 128;
+  const int g0 = KSL ? first : kbeg / 128;  // the wave's first group in the staged metadata
   f32x4 acc[NS][MBE];
 #pragma unroll
   for (int sl = 0; sl < NS; ++sl)
@@ -239,7 +279,10 @@ __global__ __launch_bounds__(512, 1) void k_stream_phase(PhaseArgs p) {
         w[h] = *reinterpret_cast<const u32x4*>(slot + r16 * 128 + (((4 * h + kg) ^ key) * 16));
       uint8_t z = 0;
       _Float16 scl;
-      if constexpr (BFMT == 2) {
+      if constexpr (BFMT == 2 && KSL) {
+        z = meta_z[4 * ((sl * 16 + r16) * S + g0 + s)];
+        scl = meta_s[2 * ((sl * 16 + r16) * S + g0 + s)];
+      } else if constexpr (BFMT == 2) {
         z = meta_z[(sl * 16 + r16) * p.G + g0 + s];
         scl = meta_s[(sl * 16 + r16) * p.G + g0 + s];
       } else {
@@ -307,15 +350,22 @@ __global__ __launch_bounds__(512, 1) void k_stream_phase(PhaseArgs p) {
           t[2] += v[2];
           t[3] += v[3];
         }
-        f16x4 o;
-        o[0] = (_Float16)t[0];
-        o[1] = (_Float16)t[1];
-        o[2] = (_Float16)t[2];
-        o[3] = (_Float16)t[3];
-        *reinterpret_cast<f16x4*>(outl + (16 * mb + r16) * NSX + sl * 16 + 4 * kg) = o;
+        if constexpr (KSL) {  // the slice's fp32 sums, straight to the partials
+          const int m = 16 * mb + r16, c = sl * 16 + 4 * kg;
+          if (m < p.M && c < rwg)
+            *reinterpret_cast<f32x4*>(p.part + ((long)slice * p.M + m) * p.N + row0 + c) = t;
+        } else {
+          f16x4 o;
+          o[0] = (_Float16)t[0];
+          o[1] = (_Float16)t[1];
+          o[2] = (_Float16)t[2];
+          o[3] = (_Float16)t[3];
+          *reinterpret_cast<f16x4*>(outl + (16 * mb + r16) * NSX + sl * 16 + 4 * kg) = o;
+        }
       }
     }
   });
+  if constexpr (KSL) return;
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_waitcnt(0xC07F);
   __builtin_amdgcn_s_barrier();

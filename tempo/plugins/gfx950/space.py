@@ -64,7 +64,7 @@ DOMAINS = {
     "stream": dict(R=(1, 2, 4), U=(2, 4, 8), ALDS=(0, 1)),
     "shared": dict(R=(1, 2), U=(2, 4), SN=(2, 4, 8)),
     # phase-ordered decode kernel (8-bit weights, wide N): ring depth; NS follows from N
-    "phase": dict(D=(2, 3, 4)),
+    "phase": dict(D=(2, 3, 4), KS=(1, 8)),
 }
 PHASE_WAVES = 8  # k_stream_phase: waves (k chunks) per workgroup, one workgroup per CU
 PHASE_CUS = 256
@@ -227,22 +227,24 @@ def phase_lds(K: int, p: dict) -> int:
     waves, the activation staging (after the loop: the chunk partial sums), the output image of
     NS slabs, the metadata of 16 NS rows (fmt 1: row scales; fmt 2: zero-points and scales of
     every group)."""
-    mb, ns, d = p["MB"], p["NS"], p["D"]
+    mb, ns, d, ks = p["MB"], p["NS"], p["D"], p.get("KS", 1)
     mbe = max(1, mb)
-    G = K // 128
-    stg = 4 * mb * 1024 if mb else G // PHASE_WAVES * 256  # M = 1: every phase's slice
+    G, S = K // 128, K // (128 * ks)
+    stg = 4 * mb * 1024 if mb else -(-S // PHASE_WAVES) * 256  # M = 1: every phase's slice
     kib = lambda b: -(-b // 1024) * 1024  # noqa: E731
+    meta = ((kib(ns * 16 * 4 * S) * 2 if ks > 1 else kib(ns * 16 * G) + kib(ns * 32 * G))
+            if p["BFMT"] == 2 else kib(ns * 32))
     return (PHASE_WAVES * d * 2048 + max(PHASE_WAVES * stg, 2 * PHASE_WAVES * mbe * 1024)
-            + kib(mbe * 16 * ns * 16 * 2) + (kib(ns * 16 * G) if p["BFMT"] == 2 else 0)
-            + kib(ns * 32 * G if p["BFMT"] == 2 else ns * 32))
+            + (0 if ks > 1 else kib(mbe * 16 * ns * 16 * 2)) + meta)
 
 
-def phase_ns(N: int):
-    """Slabs per workgroup of k_stream_phase for width N (None: N does not split into 256
-    workgroups of a multiple of 4 rows)."""
-    if N % PHASE_CUS or (N // PHASE_CUS) % 4:
+def phase_ns(N: int, ks: int = 1):
+    """Slabs per workgroup of k_stream_phase for width N and ks k slices (None: N does not split
+    into 256 / ks row groups of a multiple of 4 rows)."""
+    groups = PHASE_CUS // ks
+    if N % groups or (N // groups) % 4:
         return None
-    return -(-(N // PHASE_CUS) // 16)
+    return -(-(N // groups) // 16)
 
 
 def lds_bytes(kind: str, p: dict) -> int:
@@ -330,7 +332,9 @@ def tag(kind: str, p: dict) -> str:
     if kind == "ring":
         return "ring_mb%d_r%d_d%d_b%d" % (p["MB"], p["R"], p["D"], p["BFMT"])
     if kind == "phase":
-        return "phase_mb%d_n%d_d%d_b%d" % (p["MB"], p["NS"], p["D"], p["BFMT"])
+        return "phase_mb%d_n%d_d%d_b%d%s%s" % (p["MB"], p["NS"], p["D"], p["BFMT"],
+                                              "_e1" if p.get("EPI") else "",
+                                              "_ks%d" % p["KS"] if p.get("KS", 1) > 1 else "")
     if kind == "shared":
         return "shared_mb%d_r%d_u%d_b%d_n%d" % (p["MB"], p["R"], p["U"], p["BFMT"], p["SN"])
     return "stream_mb%d_r%d_u%d_b%d_a%d" % (p["MB"], p["R"], p["U"], p["BFMT"], p.get("ALDS", 0))
@@ -387,10 +391,13 @@ def legal(kind: str, p: dict, M: int, N: int, K: int):
             return "weights must be int8 (fmt 1) or uint8 group-128 (fmt 2)"
         if M > 16 * max(1, mb) or (mb == 0 and M != 1):
             return "M > 16*MB (MB = 0: M = 1)"
-        if phase_ns(N) != ns:
-            return "N is not 256 workgroups of a multiple of 4 rows in %d slabs" % ns
-        if K % (PHASE_WAVES * 128):
-            return "K %% %d" % (PHASE_WAVES * 128)
+        ks = p.get("KS", 1)
+        if ks > 1 and (p.get("EPI") or not p.get("KSL")):
+            return "k slices: the KSL instantiation, plain epilogue"
+        if phase_ns(N, ks) != ns:
+            return "N is not 256 / %d row groups of a multiple of 4 rows in %d slabs" % (ks, ns)
+        if K % (128 * ks) or K // (128 * ks) < PHASE_WAVES or (ks == 1 and K % (PHASE_WAVES * 128)):
+            return "K: whole 128-k steps per slice, at least one per wave"
         if (mb > 0 and ns < d) or d < 2 or (d - 1) * 2 + (4 * mb if mb else 1) >= 64:
             return "ring depth: 2 <= D (<= NS where activations ride the ring), vmcnt range"
         if phase_lds(K, p) > LDS_MAX:
@@ -570,9 +577,15 @@ def _gemm_variants(op: OpSpec) -> Iterator[Hyperform]:
             for U in DOMAINS["shared"]["U"]:
                 for SN in DOMAINS["shared"]["SN"]:
                     out.append(("shared", dict(MB=MB, R=R, U=U, BFMT=b, SN=SN, TPB=1024)))
-        if b and phase_ns(N):  # the phase-ordered kernel: 8-bit weights, N in 256 row blocks
-            for D in DOMAINS["phase"]["D"]:
-                out.append(("phase", dict(MB=0 if M == 1 else MB, NS=phase_ns(N), D=D, BFMT=b)))
+        if b:  # the phase-ordered kernel: 8-bit weights, N in 256 / KS row groups
+            for ks in DOMAINS["phase"]["KS"]:
+                if not phase_ns(N, ks):
+                    continue
+                for D in DOMAINS["phase"]["D"]:
+                    q = dict(MB=0 if M == 1 else MB, NS=phase_ns(N, ks), D=D, BFMT=b)
+                    if ks > 1:
+                        q.update(KS=ks, KSL=1)
+                    out.append(("phase", q))
     if b == 0:
         d = DOMAINS["ilv"]
         for BM in d["BM"]:

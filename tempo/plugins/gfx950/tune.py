@@ -77,6 +77,7 @@ def row_of(params: dict):
     kind = p.pop("kind")
     p.pop("BFMT", None)
     p.pop("SPLIT", None)
+    p.pop("KSL", None)  # the phase kernel's k-sliced instantiation follows from KS
     if kind == "ring":
         return None
     if kind == "dma":

@@ -186,8 +186,9 @@ W8 = {
         ("l1r1n4d2t", 16, 16400, 256),    # one remaining slab
         ("l1r1n4d2t", 9, 16384, 384),     # whole rounds, no tail
         ("l1r1n4d3", 16, 15360, 5120),    # too few slabs for a round of the tail grid
-        ("l1r1n4d2k8", 16, 5120, 17408),
-        ("l1r1n4d2k8", 3, 5120, 12288),   # ragged M
+        ("p1n10d4k8", 16, 5120, 17408),   # 8 k slices x 32 row groups of 160 rows
+        ("p1n10d4k8", 3, 5120, 12288),    # ragged M; 12 steps per slice
+        ("l1r1n4d2k8", 16, 5120, 12416),  # K % 1024 != 0: past the phase-ordered row
         ("l1r1d2k8", 16, 1024, 5120),
         ("l1r1d2k8", 7, 1024, 1024),      # 8 steps: no slices (no workspace)
         ("l1r1n2d2", 16, 5120, 6144),
@@ -198,8 +199,9 @@ W8 = {
         ("l2r1n8d2t", 17, 32784, 256),    # one remaining slab
         ("l2r1n8d2t", 32, 36864, 128),    # one slab per CU remaining, a single k step
         ("l2r1n4d4", 32, 15360, 5120),
-        ("l2r1n8d2k8", 32, 5120, 17408),
-        ("l2r1n8d2k8", 25, 5120, 12288),
+        ("p2n10d4k8", 32, 5120, 17408),
+        ("p2n10d4k8", 25, 5120, 12288),
+        ("l2r1n8d2k8", 32, 5120, 12416),
         ("l2r1d2k8", 32, 1024, 5120),
         ("l2r1n4d2k8", 32, 5120, 6144),
         ("l2r1n4d2k8", 30, 7168, 6144),

@@ -50,11 +50,12 @@ for _f in (1, 2):
 # the search grid: band edges of M, every multiple of 8 below 4200 for N plus the neighbourhoods
 # of the N thresholds (32768: one round of 8-slab workgroups of the line kernel's tail grid;
 # 34816: whole rounds of 128 x 128 tiles and a quarter round more; 17408: the gate/up output
-# width, 68 columns per CU for the phase-ordered rows), and K over the divisibility
+# width, 68 columns per CU for the phase-ordered rows; 5120: 160 rows per row group of the
+# k-sliced phase rows), and K over the divisibility
 # classes the rows test (K > 65536 is past the line rows; 12288: the long-K rows; 5120: a
 # multiple of 1024 below 12288, the phase-ordered rows' class)
 _M = (1, 2, 8, 9, 16, 17, 32, 33, 64, 65, 128, 129, 256, 257, 2048)
-_N = sorted(set(range(8, 4200, 8)) | {n + d for n in (6144, 8192, 12288, 16384, 17408, 32768, 34816)
+_N = sorted(set(range(8, 4200, 8)) | {n + d for n in (5120, 6144, 8192, 12288, 16384, 17408, 32768, 34816)
                                         for d in range(-64, 72, 8)})
 _K = (64, 128, 192, 256, 384, 512, 3840, 5120, 5184, 12288) + tuple(65536 + 64 * j for j in range(1, 9))
 

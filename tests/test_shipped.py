@@ -179,7 +179,11 @@ def test_rows_fall_through_when_the_first_row_does_not_fit():
     assert capi.route(1, 1, 34816, 5120) == "l0r1d2w"     # int8 at M = 1: the line row
     assert capi.route(1, 16, 15360, 5120) == "l1r1n4d3"  # too few slabs for the tail grid
     assert capi.route(1, 16, 69632, 5120) == "l1r1n4d3"  # 5 workgroups of 4 waves per CU
-    assert capi.route(2, 16, 5120, 17408) == "l1r1n4d2k8"   # long K: the k-slice row
+    assert capi.route(2, 16, 5120, 17408) == "p1n10d4k8"    # long K: the k-sliced phase row
+    assert capi.route(2, 32, 5120, 17408) == "p2n10d4k8"
+    assert capi.route(2, 16, 5120, 12416) == "l1r1n4d2k8"   # K % 1024 != 0: the k-slice row
+    assert capi.route(1, 16, 5120, 17408) == "l1r1n4d2k8"   # int8: the k-sliced phase row is uint8 only
+    assert capi.route(2, 16, 5120, 8192) != "p1n10d4k8"     # K < 12288: under the row's band
     assert capi.route(2, 16, 5120, 6144) == "l1r1n2d2"
     assert capi.route(2, 16, 1024, 5120) == "l1r1d2k8"     # narrow N
     assert capi.route(1, 32, 5120, 5120) == "l2r1n2d4"     # K < 6144: past the k-slice row
