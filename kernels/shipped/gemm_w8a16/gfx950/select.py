@@ -19,6 +19,11 @@ LADDER = [
     # M = 1, long K: k slices across workgroups (KS, fp32 partials reduced in slice order) spread
     # the 320 slabs of N = 5120 evenly over the part; two ring steps (1.04x / 1.12x the rows
     # below at (1, 5120, 17408), int8 / uint8)
+    # M = 1, uint8, long K on N = 4096..7168: the phase-ordered kernel over the whole K (17
+    # phases dealt 3 or 2 per wave at K = 17408), three ring steps: 1.06x the k-slice row below
+    # at (1, 5120, 17408) (int8 1.02x, not taken)
+    (1, 4096, "p0n2d3", "phase", dict(MB=0, NS=2, D=3, NMAX=7168, KMIN=13312, KMAX=20480,
+                                      fmts=(2,))),
     (1, 0, "l0r1d2k8", "line", dict(MB=0, R=1, D=2, W=2048, KS=8, KMIN=12288)),
     # M = 1 on N = 4096..7168, K < 12288, K % 1024 == 0: the phase-ordered kernel, 20-24 rows
     # per CU (a slab of 16 and one of 4-8), no tail: 1.08x / 1.10x the row below at (1, 5120,

@@ -170,8 +170,10 @@ W8 = {
         ("m256x256k64", 512, 2048, 5184),
     ],
     2: [
-        ("l0r1d2k8", 1, 5120, 17408),
-        ("l0r1d2k8", 1, 4096, 16384),
+        ("p0n2d3", 1, 5120, 17408),       # 17 phases: 3 or 2 per wave
+        ("p0n2d3", 1, 6144, 13312),       # 24 rows per CU, 13 phases
+        ("l0r1d2k8", 1, 3840, 17408),     # N < 4096: past the whole-K phase row
+        ("l0r1d2k8", 1, 4096, 12288),     # K < 13312
         ("p0n2d2", 1, 5120, 5120),
         ("p0n2d2", 1, 6144, 1024),        # 24 rows per CU, one phase
         ("l0r1n2d2", 1, 5120, 3840),

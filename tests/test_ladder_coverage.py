@@ -57,7 +57,7 @@ for _f in (1, 2):
 _M = (1, 2, 8, 9, 16, 17, 32, 33, 64, 65, 128, 129, 256, 257, 2048)
 _N = sorted(set(range(8, 4200, 8)) | {n + d for n in (5120, 6144, 8192, 12288, 16384, 17408, 32768, 34816)
                                         for d in range(-64, 72, 8)})
-_K = (64, 128, 192, 256, 384, 512, 3840, 5120, 5184, 12288) + tuple(65536 + 64 * j for j in range(1, 9))
+_K = (64, 128, 192, 256, 384, 512, 3840, 5120, 5184, 12288, 17408) + tuple(65536 + 64 * j for j in range(1, 9))
 
 
 def _tag(route, M, N, K):

@@ -176,6 +176,8 @@ def test_rows_fall_through_when_the_first_row_does_not_fit():
     assert capi.route(1, 16, 34816, 12288) == "l1r1n4d2t"  # long K: past the phase rows
     assert capi.route(2, 32, 34816, 5120) == "p2n9d4"
     assert capi.route(2, 1, 34816, 5120) == "p0n9d3"
+    assert capi.route(2, 1, 5120, 17408) == "p0n2d3"      # uint8, long K: the whole-K phase row
+    assert capi.route(2, 1, 5120, 24576) == "l0r1d2k8"    # past the row's K band
     assert capi.route(1, 1, 34816, 5120) == "l0r1d2w"     # int8 at M = 1: the line row
     assert capi.route(1, 16, 15360, 5120) == "l1r1n4d3"  # too few slabs for the tail grid
     assert capi.route(1, 16, 69632, 5120) == "l1r1n4d3"  # 5 workgroups of 4 waves per CU
